@@ -1,0 +1,211 @@
+"""Benchmark of the MI355X QLoRA kernel set (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME,...]
+
+Per kernel: K timed launches after W warm-up launches. The launches are
+captured once in a HIP graph of `--reps` back-to-back launches and the graph is replayed, with
+HIP events recorded on the launch stream around the replays, so the average duration is the
+kernel's, not Python's launch overhead. Achieved throughput divides the ALGORITHMIC bytes (or
+FLOPs) of one launch, stated next to each kernel below, by that average duration.
+
+The last line printed is one JSON object (the driver's contract); per-kernel results ride in
+its "kernels" list.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+
+METRIC = "QLoRA step ms (Qwen2.5-1.5B shape, B4xS512); kernel HBM GB/s & MFMA %"
+
+
+def graph_time_ms(fn, steps, warmup, reps):
+    """Average duration (ms) of one fn() launch: `reps` launches captured in one graph,
+    replayed until `steps` launches are timed."""
+    for _ in range(max(1, warmup)):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()  # first launch outside capture on the side stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(reps):
+                fn()
+    torch.cuda.synchronize()
+    replays = max(1, steps // reps)
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / (replays * reps), replays * reps
+
+
+def kernel_suite(args, only):
+    from talm_amd import qgroup, rmsnorm, rope, swiglu, workloads
+
+    dev = "cuda"
+    results = []
+
+    def record(name, ms, count, bytes_=None, flops=None, config=""):
+        entry = {"kernel": name, "config": config, "us": round(ms * 1e3, 3), "launches": count}
+        if bytes_ is not None:
+            gbs = bytes_ / (ms * 1e-3) / 1e9
+            entry.update(bytes=int(bytes_), gbs=round(gbs, 1),
+                         hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+        if flops is not None:
+            tf = flops / (ms * 1e-3) / 1e12
+            entry.update(flops=int(flops), tflops=round(tf, 1),
+                         mfma_frac=round(tf / FP16_PEAK_TFLOPS, 4))
+        results.append(entry)
+        print(f"[bench] {json.dumps(entry)}", flush=True)
+
+    def want(name):
+        return not only or name in only
+
+    if want("nf4_group"):
+        d = workloads.nf4_layer()
+        t = {k: d[k].to(dev) for k in ("packed", "absmax8", "code", "absmax2", "offset2")}
+        out = torch.empty(d["n"], dtype=torch.float16, device=dev)
+        n_rows = d["absmax8"].numel()
+
+        def fn():
+            qgroup.launch(t["packed"], t["absmax8"], t["code"], t["absmax2"], t["offset2"],
+                          None, out, n_rows, 64, 256)
+
+        ms, cnt = graph_time_ms(fn, args.steps, args.warmup, args.reps)
+        # packed + absmax8 + absmax2 + offsets(7 x 4) + code + fp16 out
+        algo = d["n"] // 2 + n_rows + 4 * t["absmax2"].numel() + 28 + 1024 + 2 * d["n"]
+        record("nf4_group_dequant", ms, cnt, bytes_=algo, config="1: Qwen2.5-1.5B layer")
+
+    d2 = workloads.norm_rope() if (want("addnorm_fwd") or want("addnorm_bwd")
+                                   or want("rope")) else None
+    if d2 is not None and (want("addnorm_fwd") or want("addnorm_bwd")):
+        n, hdim = d2["n"], 1536
+        x, br, w = d2["residual"].to(dev), d2["x"].to(dev), d2["weight"].to(dev)
+        total = torch.empty_like(x)
+        y = torch.empty_like(x)
+        xhat = torch.empty_like(x)
+        rstd = torch.empty(n, dtype=torch.float32, device=dev)
+        dy, ds = d2["dy"].to(dev), d2["ds"].to(dev)
+        dx = torch.empty_like(x)
+        db = torch.empty_like(x)
+
+        def fwd():
+            rmsnorm.launch(x, w, y, xhat, rstd, 1e-6, 0, p=br, q=total)
+
+        def bwd():
+            rmsnorm.launch(dx, w, dy, xhat, rstd, 1e-6, 1, p=db, q=ds)
+
+        fwd()
+        if want("addnorm_fwd"):
+            ms, cnt = graph_time_ms(fwd, args.steps, args.warmup, args.reps)
+            record("add_rmsnorm_fwd", ms, cnt, bytes_=10 * n * hdim + 4 * n + 4 * hdim,
+                   config=f"2: N={n}")
+        if want("addnorm_bwd"):
+            ms, cnt = graph_time_ms(bwd, args.steps, args.warmup, args.reps)
+            record("add_rmsnorm_bwd", ms, cnt, bytes_=10 * n * hdim + 4 * n + 4 * hdim,
+                   config=f"2: N={n}")
+
+    if d2 is not None and want("rope"):
+        n = d2["n"]
+        qkv = torch.randn(n, 2048, device=dev).half()
+        q = qkv[:, :1536].view(n, 12, 128)
+        k = qkv[:, 1536:1792].view(n, 2, 128)
+        cos, sin = d2["cos"].to(dev), d2["sin"].to(dev)
+
+        def fn():
+            rope.rope_(q, k, cos, sin, backward=False)
+
+        ms, cnt = graph_time_ms(fn, args.steps, args.warmup, args.reps)
+        record("rope_inplace", ms, cnt, bytes_=8192 * n, config=f"2: N={n}")
+
+    if want("swiglu_fwd") or want("swiglu_bwd"):
+        d3 = workloads.swiglu_inputs()
+        gate, up, grad = (d3[k].to(dev) for k in ("gate", "up", "grad"))
+        out = torch.empty_like(gate)
+        dgate, dup = torch.empty_like(gate), torch.empty_like(up)
+        n = gate.numel()
+        if want("swiglu_fwd"):
+            ms, cnt = graph_time_ms(lambda: swiglu.swiglu_fwd(gate, up, out), args.steps,
+                                    args.warmup, args.reps)
+            record("swiglu_fwd", ms, cnt, bytes_=6 * n, config="3: [2048, 8960]")
+        if want("swiglu_bwd"):
+            ms, cnt = graph_time_ms(lambda: swiglu.swiglu_bwd(grad, gate, up, dgate, dup),
+                                    args.steps, args.warmup, args.reps)
+            record("swiglu_bwd", ms, cnt, bytes_=10 * n, config="3: [2048, 8960]")
+    return results
+
+
+def cpu_baseline_nf4(seconds):
+    """The C oracle of the grouped NF4 dequant (one thread) on the config-1 layer, repeated for
+    about `seconds`; weights per second."""
+    from oracle import nf4 as nf4_oracle
+    from talm_amd import workloads
+
+    d = workloads.nf4_layer()
+    args = [d[k].numpy() for k in ("packed", "absmax8", "code", "absmax2", "offset2")]
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        nf4_oracle.group_dequant(*args)
+        reps += 1
+        if time.perf_counter() - t0 > seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(reps * d["n"] / dt / 1e9, 4), "unit": "Gweights/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{reps} x config-1 layer ({d['n']} weights), C oracle, 1 thread, {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--only", default="")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every box of this build has a single MI355X and "
+              "the kernel set runs unsharded (see DESIGN.md for how it would shard).",
+              file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    only = {s for s in args.only.split(",") if s}
+    kernels = kernel_suite(args, only)
+    dominant = max(kernels, key=lambda e: e["us"]) if kernels else None
+    line = {"metric": METRIC, "value": None, "unit": "ms", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+            "config": {"workload": "kernel suite (configs 1-4)"}, "kernels": kernels}
+    if dominant is not None:
+        line["roofline"] = {"kernel": dominant["kernel"], "bound": "hbm",
+                            "achieved": dominant["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": dominant["hbm_frac"], "traffic": None}
+    if args.cpu_seconds > 0:
+        line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,120 @@
+/*
+ * talm.h — the C-ABI of libtalm.so, the MI355X (gfx950) QLoRA kernel set.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, sizes and an explicit stream (a hipStream_t passed as void*;
+ *     NULL is the legacy default stream);
+ *   - only enqueues work on that stream: it never synchronizes and never allocates device
+ *     memory (every buffer, workspaces included, is owned by the caller);
+ *   - returns TALM_OK (0) or a nonzero status, with a message for the calling thread in
+ *     talm_last_error(). TALM_EINVAL means the arguments were rejected before anything was
+ *     launched (the Python layer raises ValueError), TALM_EHIP a HIP launch error (RuntimeError).
+ *   - is reentrant: no state is kept between calls (forward launches come from the Python main
+ *     thread, backward launches from the autograd device thread).
+ *
+ * fp16 tensors are passed as uint16_t* / void* holding IEEE binary16 bit patterns.
+ * Reference citations are paths inside otarernazar-eng/Talm.
+ */
+#ifndef TALM_H
+#define TALM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TALM_OK 0
+#define TALM_EINVAL 1
+#define TALM_EHIP 2
+
+/* Element types of the tensors whose dtype is a runtime argument. */
+#define TALM_F32 0
+#define TALM_F16 1
+
+/* Message of the last failed call on this thread ("" after a success). */
+const char* talm_last_error(void);
+
+/* ABI version: bumped whenever a signature below changes. */
+int talm_abi_version(void);
+
+/*
+ * Grouped NF4 dequantization of the seven projections of one decoder layer in one launch.
+ * Replaces qgroup.launch / nf4_group_dequant_kernel (solution/qgroup.py:72-99).
+ *   packed   u8  [n_rows * qblock / 2]   two NF4 codes per byte, the high nibble is the even element
+ *   absmax8  u8  [n_rows]                index into `code` of each block's absmax
+ *   code     f32 [256]                   second-level code table (bitsandbytes state2.code)
+ *   absmax2  f32 [n_rows / qblock2]      second-level scale of every qblock2 blocks
+ *   offset2  f32 [n_rows / qblock2]      the offset of the projection each block belongs to
+ *   out      f16 [n_rows * qblock]
+ * Per element e of block r: scale = fl32(fl32(code[absmax8[r]] * absmax2[r/qblock2]) +
+ * offset2[r/qblock2]); out[e] = f16_rne(fl32(NF4[nibble] * scale)) (no fused multiply-add).
+ * qblock: even power of two >= 8; qblock2 >= 1. Pointers 4-byte (packed) / 16-byte (out) aligned.
+ */
+int talm_nf4_group_dequant(const uint8_t* packed, const uint8_t* absmax8, const float* code,
+                           const float* absmax2, const float* offset2, uint16_t* out,
+                           int64_t n_rows, int32_t qblock, int32_t qblock2, void* stream);
+
+/*
+ * Per-projection NF4 dequantization with an fp32 absmax per block (bitsandbytes'
+ * dequantize_blockwise + offset already applied).
+ * Replaces nf4_dequant.nf4_dequantize / nf4_dequant_pairs_kernel (solution/nf4_dequant.py:38-91).
+ *   packed u8 [n / 2], absmax f32 [ceil(n / blocksize)], out f16 [n]; n even, blocksize even.
+ */
+int talm_nf4_dequant(const uint8_t* packed, const float* absmax, uint16_t* out, int64_t n,
+                     int32_t blocksize, void* stream);
+
+/*
+ * Fused (residual-add +) RMSNorm, forward or backward, one launch.
+ * Replaces rmsnorm.launch / rmsnorm_kernel (solution/rmsnorm.py:58-118).
+ * Every [n_rows, n_cols] operand is contiguous (row stride n_cols).
+ *   a, q: x_dtype;  h, xhat, p: out_dtype;  weight: w_dtype [n_cols];  rstd: f32 [n_rows].
+ * backward == 0: x = a (+ p when add); writes q = x (when add), h = w * xhat, xhat = x * rstd,
+ *                rstd = rsqrt(mean(x^2) + eps).
+ * backward != 0: reads dy = h, xhat, rstd; dx = rstd * (g - xhat * mean(g * xhat)), g = dy * w;
+ *                with add, dx += q and dx is also written to p; dx is written to a.
+ * p and q are ignored (may be NULL) when add == 0.
+ */
+int talm_rmsnorm(void* a, void* q, void* h, void* xhat, void* p, const void* weight, float* rstd,
+                 int64_t n_rows, int64_t n_cols, int32_t x_dtype, int32_t out_dtype,
+                 int32_t w_dtype, float eps, int32_t backward, int32_t add, void* stream);
+
+/*
+ * Rotary position embedding of q and k, forward or backward, fp16 with fp32 math.
+ * Replaces rope._launch / rope_kernel (solution/rope.py:64-134). In place when the output
+ * pointers equal the input pointers (every thread reads its elements before writing them).
+ * Element (token t, head h, column d) of q is at q[t * q_stride_tok + h * q_stride_head + d];
+ * k, out_q, out_k alike; cos/sin f32 at [t * cs_stride_tok + d], d < head_dim.
+ *   forward:  y1 = x1 c1 - x2 s1,  y2 = x2 c2 + x1 s2
+ *   backward: y1 = x1 c1 + x2 s2,  y2 = x2 c2 - x1 s1      (x1/x2: first/second half of d)
+ * head_dim even, <= 512; strides in elements.
+ */
+int talm_rope(const uint16_t* q, const uint16_t* k, const float* cos, const float* sin,
+              uint16_t* out_q, uint16_t* out_k, int64_t n_tokens, int32_t n_q_heads,
+              int32_t n_k_heads, int32_t head_dim, int64_t q_stride_tok, int64_t q_stride_head,
+              int64_t k_stride_tok, int64_t k_stride_head, int64_t out_q_stride_tok,
+              int64_t out_q_stride_head, int64_t out_k_stride_tok, int64_t out_k_stride_head,
+              int64_t cs_stride_tok, int32_t backward, void* stream);
+
+/*
+ * SwiGLU forward: out = silu(gate) * up in fp32, written as fp16. n elements, contiguous.
+ * Replaces example_swiglu_fwd_kernel (solution/swiglu.py:23-30); `out` may alias `gate`
+ * (the save-up node, solution/mlp_save_up.py:63).
+ */
+int talm_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                    void* stream);
+
+/*
+ * SwiGLU backward: sig = sigmoid(gate); dup = grad * gate * sig;
+ * dgate = grad * up * sig * (1 + gate * (1 - sig)), fp16 in and out, fp32 math.
+ * Replaces example_swiglu_bwd_kernel (solution/swiglu.py:33-45); dgate may alias gate and dup
+ * may alias up (the in-place backward, solution/swiglu_inplace.py:40).
+ */
+int talm_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up,
+                    uint16_t* dgate, uint16_t* dup, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TALM_H */

@@ -1,0 +1,145 @@
+"""`torch.ops.talm.*`: the PyTorch custom ops over the C-ABI of libtalm.so.
+
+Each op validates device, dtype and layout, passes raw data pointers and the current HIP stream
+of the tensors' device to one `extern "C"` entry point, and returns nothing (outputs are the
+caller's tensors, annotated as mutated). Registered for the CUDA (= HIP on ROCm) dispatch key
+only: a CPU tensor raises NotImplementedError from the dispatcher, never a CPU fallback.
+"""
+
+import torch
+
+from . import _lib
+
+_DEF = torch.library.Library("talm", "DEF")
+
+
+def _stream(t):
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _require(cond, message):
+    if not cond:
+        raise ValueError(message)
+
+
+def _fp16(t, name):
+    _require(t.is_cuda and t.dtype == torch.float16, f"{name} must be a CUDA float16 tensor")
+
+
+def _op(schema):
+    """Define `talm::<schema>` and register the decorated function as its CUDA kernel."""
+    name = schema.split("(", 1)[0]
+    _DEF.define(schema)
+
+    def register(fn):
+        _DEF.impl(name, fn, "CUDA")
+        return fn
+
+    return register
+
+
+@_op("nf4_group_dequant(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
+     "Tensor offset2, Tensor(a!) out, int qblock, int qblock2) -> ()")
+def nf4_group_dequant(packed, absmax8, code, absmax2, offset2, out, qblock, qblock2):
+    _require(packed.dtype == torch.uint8 and absmax8.dtype == torch.uint8, "packed/absmax8: uint8")
+    _require(code.dtype == absmax2.dtype == offset2.dtype == torch.float32,
+             "code/absmax2/offset2: float32")
+    _fp16(out, "out")
+    for t in (packed, absmax8, code, absmax2, offset2, out):
+        _require(t.is_contiguous() and t.device == out.device, "operands: contiguous, one device")
+    n_rows = absmax8.numel()
+    _require(code.numel() >= 256, "code: 256 entries")
+    _require(packed.numel() * 2 == n_rows * qblock and out.numel() == n_rows * qblock,
+             "packed / out sizes do not match n_rows * qblock")
+    _require(absmax2.numel() * qblock2 >= n_rows and offset2.numel() == absmax2.numel(),
+             "absmax2 / offset2 do not cover every block")
+    lib = _lib.lib()
+    _lib.check(lib.talm_nf4_group_dequant(packed.data_ptr(), absmax8.data_ptr(), code.data_ptr(),
+                                          absmax2.data_ptr(), offset2.data_ptr(), out.data_ptr(),
+                                          n_rows, qblock, qblock2, _stream(out)),
+               "nf4_group_dequant")
+
+
+@_op("nf4_dequant(Tensor packed, Tensor absmax, Tensor(a!) out, int blocksize) -> ()")
+def nf4_dequant(packed, absmax, out, blocksize):
+    _require(packed.dtype == torch.uint8 and absmax.dtype == torch.float32,
+             "packed: uint8, absmax: float32")
+    _fp16(out, "out")
+    _require(packed.is_contiguous() and absmax.is_contiguous() and out.is_contiguous(),
+             "operands must be contiguous")
+    n = out.numel()
+    _require(packed.numel() * 2 >= n and absmax.numel() * blocksize >= n,
+             "packed / absmax do not cover out")
+    lib = _lib.lib()
+    _lib.check(lib.talm_nf4_dequant(packed.data_ptr(), absmax.data_ptr(), out.data_ptr(), n,
+                                    blocksize, _stream(out)), "nf4_dequant")
+
+
+@_op("rmsnorm(Tensor(a!) a, Tensor(b!)? q, Tensor(c!) h, Tensor(d!) xhat, Tensor(e!)? p, "
+     "Tensor weight, Tensor(f!) rstd, float eps, int backward) -> ()")
+def rmsnorm(a, q, h, xhat, p, weight, rstd, eps, backward):
+    n_rows, n_cols = xhat.shape
+    add = p is not None
+    _require(not add or q is not None, "rmsnorm: p and q go together")
+    for t in (a, h, xhat) + ((p, q) if add else ()):
+        _require(t.is_cuda and t.is_contiguous() and tuple(t.shape) == (n_rows, n_cols),
+                 "rmsnorm: [N, H] operands must be contiguous CUDA tensors of one shape")
+    _require(a.dtype == (q.dtype if add else a.dtype), "rmsnorm: q has a's dtype")
+    _require(h.dtype == xhat.dtype and (not add or p.dtype == h.dtype),
+             "rmsnorm: h, xhat and p share the output dtype")
+    _require(weight.is_contiguous() and weight.numel() == n_cols, "rmsnorm: weight [H]")
+    _require(rstd.dtype == torch.float32 and rstd.numel() == n_rows, "rmsnorm: rstd float32 [N]")
+    lib = _lib.lib()
+    _lib.check(lib.talm_rmsnorm(a.data_ptr(), _ptr(q), h.data_ptr(), xhat.data_ptr(), _ptr(p),
+                                weight.data_ptr(), rstd.data_ptr(), n_rows, n_cols,
+                                _lib.dtype_code(a.dtype), _lib.dtype_code(h.dtype),
+                                _lib.dtype_code(weight.dtype), float(eps), int(backward), int(add),
+                                _stream(xhat)), "rmsnorm")
+
+
+@_op("rope(Tensor q, Tensor k, Tensor cos, Tensor sin, Tensor(a!) out_q, Tensor(b!) out_k, "
+     "int backward) -> ()")
+def rope(q, k, cos, sin, out_q, out_k, backward):
+    """q, out_q [T, Hq, D] and k, out_k [T, Hk, D] fp16 views (any token / head strides, unit
+    column stride); cos, sin float32 [T, D] with unit column stride. out_* may be q / k."""
+    n_tokens, hq, dim = q.shape
+    hk = k.shape[1]
+    for t, heads in ((q, hq), (k, hk), (out_q, hq), (out_k, hk)):
+        _fp16(t, "q/k")
+        _require(tuple(t.shape) == (n_tokens, heads, dim) and t.stride(2) == 1,
+                 "rope: q/k must be [T, H, D] views with unit column stride")
+    for t in (cos, sin):
+        _require(t.is_cuda and t.dtype == torch.float32 and tuple(t.shape) == (n_tokens, dim)
+                 and t.stride(1) == 1, "rope: cos/sin float32 [T, D]")
+    _require(cos.stride(0) == sin.stride(0), "rope: cos and sin share their token stride")
+    lib = _lib.lib()
+    _lib.check(lib.talm_rope(q.data_ptr(), k.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                             out_q.data_ptr(), out_k.data_ptr(), n_tokens, hq, hk, dim,
+                             q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+                             out_q.stride(0), out_q.stride(1), out_k.stride(0), out_k.stride(1),
+                             cos.stride(0), int(backward), _stream(q)), "rope")
+
+
+@_op("swiglu_fwd(Tensor gate, Tensor up, Tensor(a!) out) -> ()")
+def swiglu_fwd(gate, up, out):
+    for t in (gate, up, out):
+        _fp16(t, "swiglu operand")
+        _require(t.is_contiguous() and t.numel() == gate.numel(), "swiglu: contiguous, one size")
+    lib = _lib.lib()
+    _lib.check(lib.talm_swiglu_fwd(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+                                   _stream(gate)), "swiglu_fwd")
+
+
+@_op("swiglu_bwd(Tensor grad, Tensor gate, Tensor up, Tensor(a!) dgate, Tensor(b!) dup) -> ()")
+def swiglu_bwd(grad, gate, up, dgate, dup):
+    for t in (grad, gate, up, dgate, dup):
+        _fp16(t, "swiglu operand")
+        _require(t.is_contiguous() and t.numel() == gate.numel(), "swiglu: contiguous, one size")
+    lib = _lib.lib()
+    _lib.check(lib.talm_swiglu_bwd(grad.data_ptr(), gate.data_ptr(), up.data_ptr(),
+                                   dgate.data_ptr(), dup.data_ptr(), gate.numel(), _stream(gate)),
+               "swiglu_bwd")

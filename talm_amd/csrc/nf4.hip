@@ -1,0 +1,165 @@
+// NF4 -> fp16 dequantization for gfx950: the grouped seven-projection launch of a decoder layer
+// (double-quantized absmax rebuilt in the kernel) and the per-projection launch with an fp32
+// absmax. HBM-bound: per 8 weights the kernel reads one 32-bit word of packed codes and writes
+// one 128-bit word of fp16, so a wavefront reads 256 contiguous bytes and writes 1 KiB per step.
+//
+// Both NF4 tables live in LDS: the 16 levels occupy 16 distinct banks, so the per-nibble gather
+// is conflict-free (lanes reading the same level broadcast). The 256-entry second-level code
+// table is gathered once per 64 weights (one absmax block).
+//
+// Arithmetic is the reference's bit for bit: the scale is rounded after the product and after
+// the offset (no fused multiply-add: __fmul_rn / __fadd_rn are never contracted), the level
+// times the scale is one fp32 product and one round-to-nearest-even to fp16.
+#include "common.h"
+
+namespace talm {
+namespace {
+
+// The 16 NormalFloat levels (QLoRA, Dettmers et al. 2023), as in solution/qgroup.py:60-63.
+__constant__ float kNF4Levels[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+constexpr int kThreads = 256;
+constexpr int kWordsPerThread = 4;  // 32 weights per thread, four independent 128-bit stores
+
+// Eight weights of one packed word (4 bytes, high nibble first) scaled and packed to 4 x 2 fp16.
+__device__ __forceinline__ uint4 dequant_word(uint32_t word, float scale, const float* levels) {
+  uint32_t out[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (word >> (8 * b)) & 0xffu;
+    const float first = __fmul_rn(levels[byte >> 4], scale);
+    const float second = __fmul_rn(levels[byte & 15u], scale);
+    out[b] = pack2(first, second);
+  }
+  return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// Grouped kernel: word w covers weights [8w, 8w + 8) of absmax block w >> word_shift.
+__global__ __launch_bounds__(kThreads) void nf4_group_kernel(
+    const uint32_t* __restrict__ packed, const uint8_t* __restrict__ absmax8,
+    const float* __restrict__ code, const float* __restrict__ absmax2,
+    const float* __restrict__ offset2, uint4* __restrict__ out, int64_t n_words, int word_shift,
+    uint32_t qblock2, int qblock2_shift) {
+  __shared__ float s_code[256];
+  __shared__ float s_levels[16];
+  s_code[threadIdx.x] = code[threadIdx.x];
+  if (threadIdx.x < 16) s_levels[threadIdx.x] = kNF4Levels[threadIdx.x];
+  __syncthreads();
+
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kWordsPerThread) + threadIdx.x;
+  uint32_t words[kWordsPerThread];
+  float scales[kWordsPerThread];
+#pragma unroll
+  for (int j = 0; j < kWordsPerThread; ++j) {
+    const int64_t w = base + j * kThreads;
+    words[j] = 0u;
+    scales[j] = 0.f;
+    if (w < n_words) {
+      words[j] = __builtin_nontemporal_load(packed + w);
+      const int64_t row = w >> word_shift;
+      const int64_t blk2 = qblock2_shift >= 0 ? (row >> qblock2_shift)
+                                              : static_cast<int64_t>(static_cast<uint64_t>(row) / qblock2);
+      const float prod = __fmul_rn(s_code[absmax8[row]], absmax2[blk2]);
+      scales[j] = __fadd_rn(prod, offset2[blk2]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kWordsPerThread; ++j) {
+    const int64_t w = base + j * kThreads;
+    if (w < n_words) out[w] = dequant_word(words[j], scales[j], s_levels);
+  }
+}
+
+// Per-projection kernel, word path: blocksize a multiple of 8.
+__global__ __launch_bounds__(kThreads) void nf4_words_kernel(const uint32_t* __restrict__ packed,
+                                                             const float* __restrict__ absmax,
+                                                             uint4* __restrict__ out,
+                                                             int64_t n_words, int64_t words_per_block) {
+  __shared__ float s_levels[16];
+  if (threadIdx.x < 16) s_levels[threadIdx.x] = kNF4Levels[threadIdx.x];
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kWordsPerThread) + threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < kWordsPerThread; ++j) {
+    const int64_t w = base + j * kThreads;
+    if (w < n_words) {
+      const uint32_t word = __builtin_nontemporal_load(packed + w);
+      out[w] = dequant_word(word, absmax[w / words_per_block], s_levels);
+    }
+  }
+}
+
+// Per-projection kernel, byte path: any even blocksize / element count (one byte -> 2 fp16).
+__global__ __launch_bounds__(kThreads) void nf4_bytes_kernel(const uint8_t* __restrict__ packed,
+                                                             const float* __restrict__ absmax,
+                                                             uint32_t* __restrict__ out,
+                                                             int64_t n_bytes, int64_t blocksize) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n_bytes) return;
+  const uint32_t byte = packed[i];
+  const float scale = absmax[(2 * i) / blocksize];
+  out[i] = pack2(__fmul_rn(kNF4Levels[byte >> 4], scale), __fmul_rn(kNF4Levels[byte & 15u], scale));
+}
+
+int log2_exact(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((int64_t{1} << s) < v) ++s;
+  return s;
+}
+
+}  // namespace
+}  // namespace talm
+
+using namespace talm;
+
+TALM_API int talm_nf4_group_dequant(const uint8_t* packed, const uint8_t* absmax8,
+                                    const float* code, const float* absmax2,
+                                    const float* offset2, uint16_t* out, int64_t n_rows,
+                                    int32_t qblock, int32_t qblock2, void* stream) {
+  const int qshift = log2_exact(qblock);
+  if (n_rows < 0) return fail(TALM_EINVAL, "nf4_group_dequant: n_rows %lld < 0", (long long)n_rows);
+  if (qshift < 3) return fail(TALM_EINVAL, "nf4_group_dequant: qblock %d is not a power of two >= 8", qblock);
+  if (qblock2 < 1) return fail(TALM_EINVAL, "nf4_group_dequant: qblock2 %d < 1", qblock2);
+  if (!aligned(packed, 4) || !aligned(out, 16))
+    return fail(TALM_EINVAL, "nf4_group_dequant: packed must be 4-byte and out 16-byte aligned");
+  if (n_rows == 0) return ok();
+  if (!packed || !absmax8 || !code || !absmax2 || !offset2 || !out)
+    return fail(TALM_EINVAL, "nf4_group_dequant: null pointer");
+  const int64_t n_words = n_rows * (qblock / 8);
+  const int64_t per_block = kThreads * kWordsPerThread;
+  const int64_t blocks = (n_words + per_block - 1) / per_block;
+  if (blocks > 0x7fffffff) return fail(TALM_EINVAL, "nf4_group_dequant: too many weights");
+  hipLaunchKernelGGL(nf4_group_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                     as_stream(stream), reinterpret_cast<const uint32_t*>(packed), absmax8, code,
+                     absmax2, offset2, reinterpret_cast<uint4*>(out), n_words, qshift - 3,
+                     static_cast<uint32_t>(qblock2), log2_exact(qblock2));
+  return check_launch("nf4_group_dequant");
+}
+
+TALM_API int talm_nf4_dequant(const uint8_t* packed, const float* absmax, uint16_t* out, int64_t n,
+                              int32_t blocksize, void* stream) {
+  if (n < 0 || (n & 1)) return fail(TALM_EINVAL, "nf4_dequant: element count %lld is not even", (long long)n);
+  if (blocksize < 2 || (blocksize & 1)) return fail(TALM_EINVAL, "nf4_dequant: blocksize %d is not even", blocksize);
+  if (n == 0) return ok();
+  if (!packed || !absmax || !out) return fail(TALM_EINVAL, "nf4_dequant: null pointer");
+  if (!aligned(out, 4)) return fail(TALM_EINVAL, "nf4_dequant: out must be 4-byte aligned");
+  const hipStream_t s = as_stream(stream);
+  if (blocksize % 8 == 0 && n % 8 == 0 && aligned(packed, 4) && aligned(out, 16)) {
+    const int64_t n_words = n / 8;
+    const int64_t per_block = kThreads * kWordsPerThread;
+    hipLaunchKernelGGL(nf4_words_kernel, dim3(static_cast<unsigned>((n_words + per_block - 1) / per_block)),
+                       dim3(kThreads), 0, s, reinterpret_cast<const uint32_t*>(packed), absmax,
+                       reinterpret_cast<uint4*>(out), n_words, static_cast<int64_t>(blocksize / 8));
+  } else {
+    const int64_t n_bytes = n / 2;
+    hipLaunchKernelGGL(nf4_bytes_kernel, dim3(static_cast<unsigned>((n_bytes + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, s, packed, absmax, reinterpret_cast<uint32_t*>(out), n_bytes,
+                       static_cast<int64_t>(blocksize));
+  }
+  return check_launch("nf4_dequant");
+}

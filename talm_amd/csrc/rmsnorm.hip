@@ -1,0 +1,294 @@
+// Fused (residual-add +) RMSNorm for gfx950, forward and backward.
+//
+// One wavefront owns one row: lane l holds the 8-column chunks l, l + 64, ... of the row in
+// registers (16-byte loads of fp16, 32-byte of fp32), so every operand is read once and written
+// once, and the two row reductions (sum of squares forward, sum of g * xhat backward) are wave64
+// butterfly sums with no LDS and no barrier. Rows whose width is not a multiple of 8 or wider
+// than kMaxChunks * 8 * 64 columns take a generic path that reads the row twice.
+#include "common.h"
+
+namespace talm {
+namespace {
+
+constexpr int kThreads = 256;            // four rows per workgroup
+constexpr int kRowsPerBlock = kThreads / kWave;
+constexpr int kMaxChunks = 8;            // vector path: rows up to 8 * 8 * 64 = 4096 columns
+
+template <typename T>
+struct IO;
+
+template <>
+struct IO<float> {
+  static __device__ __forceinline__ void load8(const float* p, float* v) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store8(float* p, const float* v) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  static __device__ __forceinline__ float load1(const float* p) { return *p; }
+  static __device__ __forceinline__ void store1(float* p, float v) { *p = v; }
+};
+
+template <>
+struct IO<uint16_t> {
+  static __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    v[0] = lo_f(a.x); v[1] = hi_f(a.x); v[2] = lo_f(a.y); v[3] = hi_f(a.y);
+    v[4] = lo_f(a.z); v[5] = hi_f(a.z); v[6] = lo_f(a.w); v[7] = hi_f(a.w);
+  }
+  static __device__ __forceinline__ void store8(uint16_t* p, const float* v) {
+    *reinterpret_cast<uint4*>(p) =
+        make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+  }
+  static __device__ __forceinline__ float load1(const uint16_t* p) { return h2f(*p); }
+  static __device__ __forceinline__ void store1(uint16_t* p, float v) { *p = f2h(v); }
+};
+
+// Forward, vector path. x = a (+ p); q = x; h = w * xhat; xhat = x * rstd.
+template <typename XT, typename OT, typename WT, bool ADD>
+__global__ __launch_bounds__(kThreads) void rms_fwd_vec(const XT* __restrict__ a,
+                                                        const OT* __restrict__ p, XT* __restrict__ q,
+                                                        OT* __restrict__ h, OT* __restrict__ xhat,
+                                                        const WT* __restrict__ w,
+                                                        float* __restrict__ rstd, int64_t n_rows,
+                                                        int n_cols, float eps) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int n_chunks = n_cols / 8;
+  const int64_t at = row * n_cols;
+  float x[kMaxChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int c = lane + kWave * i;
+    if (c < n_chunks) {
+      IO<XT>::load8(a + at + 8 * c, x[i]);
+      if constexpr (ADD) {
+        float pv[8];
+        IO<OT>::load8(p + at + 8 * c, pv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[i][e] += pv[e];
+        IO<XT>::store8(q + at + 8 * c, x[i]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(n_cols) + eps);
+  if (lane == 0) rstd[row] = r;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int c = lane + kWave * i;
+    if (c < n_chunks) {
+      float wv[8], xh[8], y[8];
+      IO<WT>::load8(w + 8 * c, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xh[e] = x[i][e] * r;
+        y[e] = wv[e] * xh[e];
+      }
+      IO<OT>::store8(h + at + 8 * c, y);
+      IO<OT>::store8(xhat + at + 8 * c, xh);
+    }
+  }
+}
+
+// Backward, vector path. g = dy * w; dx = rstd * (g - xhat * mean(g * xhat)) (+ ds -> p).
+template <typename XT, typename OT, typename WT, bool ADD>
+__global__ __launch_bounds__(kThreads) void rms_bwd_vec(XT* __restrict__ a, OT* __restrict__ p,
+                                                        const XT* __restrict__ q,
+                                                        const OT* __restrict__ h,
+                                                        const OT* __restrict__ xhat,
+                                                        const WT* __restrict__ w,
+                                                        const float* __restrict__ rstd,
+                                                        int64_t n_rows, int n_cols) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int n_chunks = n_cols / 8;
+  const int64_t at = row * n_cols;
+  float g[kMaxChunks][8], xh[kMaxChunks][8];
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int c = lane + kWave * i;
+    if (c < n_chunks) {
+      float wv[8];
+      IO<OT>::load8(h + at + 8 * c, g[i]);
+      IO<OT>::load8(xhat + at + 8 * c, xh[i]);
+      IO<WT>::load8(w + 8 * c, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        g[i][e] *= wv[e];
+        dot += g[i][e] * xh[i][e];
+      }
+    }
+  }
+  const float cmean = wave_sum(dot) / static_cast<float>(n_cols);
+  const float r = rstd[row];
+#pragma unroll
+  for (int i = 0; i < kMaxChunks; ++i) {
+    const int c = lane + kWave * i;
+    if (c < n_chunks) {
+      float dx[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dx[e] = r * (g[i][e] - xh[i][e] * cmean);
+      if constexpr (ADD) {
+        float ds[8];
+        IO<XT>::load8(q + at + 8 * c, ds);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dx[e] += ds[e];
+        IO<OT>::store8(p + at + 8 * c, dx);
+      }
+      IO<XT>::store8(a + at + 8 * c, dx);
+    }
+  }
+}
+
+// Generic path (any width): the row is read twice, one element per lane per step.
+template <typename XT, typename OT, typename WT, bool ADD>
+__global__ __launch_bounds__(kThreads) void rms_fwd_any(const XT* __restrict__ a,
+                                                        const OT* __restrict__ p, XT* __restrict__ q,
+                                                        OT* __restrict__ h, OT* __restrict__ xhat,
+                                                        const WT* __restrict__ w,
+                                                        float* __restrict__ rstd, int64_t n_rows,
+                                                        int n_cols, float eps) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int64_t at = row * n_cols;
+  float ss = 0.f;
+  for (int j = lane; j < n_cols; j += kWave) {
+    float x = IO<XT>::load1(a + at + j);
+    if constexpr (ADD) {
+      x += IO<OT>::load1(p + at + j);
+      IO<XT>::store1(q + at + j, x);
+    }
+    ss += x * x;
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(n_cols) + eps);
+  if (lane == 0) rstd[row] = r;
+  for (int j = lane; j < n_cols; j += kWave) {
+    float x = IO<XT>::load1(a + at + j);
+    if constexpr (ADD) x += IO<OT>::load1(p + at + j);
+    const float xh = x * r;
+    IO<OT>::store1(h + at + j, IO<WT>::load1(w + j) * xh);
+    IO<OT>::store1(xhat + at + j, xh);
+  }
+}
+
+template <typename XT, typename OT, typename WT, bool ADD>
+__global__ __launch_bounds__(kThreads) void rms_bwd_any(XT* __restrict__ a, OT* __restrict__ p,
+                                                        const XT* __restrict__ q,
+                                                        const OT* __restrict__ h,
+                                                        const OT* __restrict__ xhat,
+                                                        const WT* __restrict__ w,
+                                                        const float* __restrict__ rstd,
+                                                        int64_t n_rows, int n_cols) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+  if (row >= n_rows) return;
+  const int64_t at = row * n_cols;
+  float dot = 0.f;
+  for (int j = lane; j < n_cols; j += kWave)
+    dot += IO<OT>::load1(h + at + j) * IO<WT>::load1(w + j) * IO<OT>::load1(xhat + at + j);
+  const float cmean = wave_sum(dot) / static_cast<float>(n_cols);
+  const float r = rstd[row];
+  for (int j = lane; j < n_cols; j += kWave) {
+    const float g = IO<OT>::load1(h + at + j) * IO<WT>::load1(w + j);
+    float dx = r * (g - IO<OT>::load1(xhat + at + j) * cmean);
+    if constexpr (ADD) {
+      dx += IO<XT>::load1(q + at + j);
+      IO<OT>::store1(p + at + j, dx);
+    }
+    IO<XT>::store1(a + at + j, dx);
+  }
+}
+
+template <typename XT, typename OT, typename WT, bool ADD>
+void launch(void* a, void* q, void* h, void* xhat, void* p, const void* weight, float* rstd,
+            int64_t n_rows, int n_cols, float eps, bool backward, bool vec, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((n_rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  const dim3 block(kThreads);
+  XT* ax = static_cast<XT*>(a);
+  XT* qx = static_cast<XT*>(q);
+  OT* ho = static_cast<OT*>(h);
+  OT* xo = static_cast<OT*>(xhat);
+  OT* po = static_cast<OT*>(p);
+  const WT* wv = static_cast<const WT*>(weight);
+  if (!backward) {
+    if (vec)
+      hipLaunchKernelGGL((rms_fwd_vec<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
+                         rstd, n_rows, n_cols, eps);
+    else
+      hipLaunchKernelGGL((rms_fwd_any<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
+                         rstd, n_rows, n_cols, eps);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((rms_bwd_vec<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
+                         rstd, n_rows, n_cols);
+    else
+      hipLaunchKernelGGL((rms_bwd_any<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
+                         rstd, n_rows, n_cols);
+  }
+}
+
+template <typename XT, typename OT, typename WT>
+void dispatch_add(bool add, void* a, void* q, void* h, void* xhat, void* p, const void* weight,
+                  float* rstd, int64_t n_rows, int n_cols, float eps, bool backward, bool vec,
+                  hipStream_t s) {
+  if (add)
+    launch<XT, OT, WT, true>(a, q, h, xhat, p, weight, rstd, n_rows, n_cols, eps, backward, vec, s);
+  else
+    launch<XT, OT, WT, false>(a, q, h, xhat, p, weight, rstd, n_rows, n_cols, eps, backward, vec, s);
+}
+
+template <typename XT, typename OT>
+void dispatch_w(int w_dtype, bool add, void* a, void* q, void* h, void* xhat, void* p,
+                const void* weight, float* rstd, int64_t n_rows, int n_cols, float eps,
+                bool backward, bool vec, hipStream_t s) {
+  if (w_dtype == TALM_F32)
+    dispatch_add<XT, OT, float>(add, a, q, h, xhat, p, weight, rstd, n_rows, n_cols, eps, backward, vec, s);
+  else
+    dispatch_add<XT, OT, uint16_t>(add, a, q, h, xhat, p, weight, rstd, n_rows, n_cols, eps, backward, vec, s);
+}
+
+}  // namespace
+}  // namespace talm
+
+using namespace talm;
+
+TALM_API int talm_rmsnorm(void* a, void* q, void* h, void* xhat, void* p, const void* weight,
+                          float* rstd, int64_t n_rows, int64_t n_cols, int32_t x_dtype,
+                          int32_t out_dtype, int32_t w_dtype, float eps, int32_t backward,
+                          int32_t add, void* stream) {
+  for (int32_t dt : {x_dtype, out_dtype, w_dtype})
+    if (dt != TALM_F32 && dt != TALM_F16) return fail(TALM_EINVAL, "rmsnorm: unsupported dtype code %d", dt);
+  if (n_rows < 0 || n_cols < 1 || n_cols > (1 << 24))
+    return fail(TALM_EINVAL, "rmsnorm: bad shape [%lld, %lld]", (long long)n_rows, (long long)n_cols);
+  if (n_rows == 0) return ok();
+  if (!a || !h || !xhat || !weight || !rstd || (add && (!p || !q)))
+    return fail(TALM_EINVAL, "rmsnorm: null pointer");
+  const bool vec = n_cols % 8 == 0 && n_cols <= kMaxChunks * 8 * kWave && aligned(a, 16) &&
+                   aligned(h, 16) && aligned(xhat, 16) && aligned(weight, 16) &&
+                   (!add || (aligned(p, 16) && aligned(q, 16)));
+  const hipStream_t s = as_stream(stream);
+  const int cols = static_cast<int>(n_cols);
+  const bool bwd = backward != 0, ad = add != 0;
+  if (x_dtype == TALM_F32 && out_dtype == TALM_F16)
+    dispatch_w<float, uint16_t>(w_dtype, ad, a, q, h, xhat, p, weight, rstd, n_rows, cols, eps, bwd, vec, s);
+  else if (x_dtype == TALM_F32 && out_dtype == TALM_F32)
+    dispatch_w<float, float>(w_dtype, ad, a, q, h, xhat, p, weight, rstd, n_rows, cols, eps, bwd, vec, s);
+  else if (x_dtype == TALM_F16 && out_dtype == TALM_F16)
+    dispatch_w<uint16_t, uint16_t>(w_dtype, ad, a, q, h, xhat, p, weight, rstd, n_rows, cols, eps, bwd, vec, s);
+  else
+    dispatch_w<uint16_t, float>(w_dtype, ad, a, q, h, xhat, p, weight, rstd, n_rows, cols, eps, bwd, vec, s);
+  return check_launch("rmsnorm");
+}

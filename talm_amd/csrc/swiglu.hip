@@ -1,0 +1,167 @@
+// SwiGLU for gfx950: forward silu(gate) * up and its backward, fp16 storage with fp32 math.
+// Flat, contiguous operands; each thread moves 8 elements per 16-byte access, two accesses in
+// flight per operand. Aliasing the outputs onto the inputs is allowed (the in-place backward and
+// the save-up forward): a thread loads all its operands before storing at the same offsets.
+#include "common.h"
+
+namespace talm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kVecPerThread = 2;  // 16 elements per thread per grid step
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ void unpack8(const uint4& a, float* v) {
+  v[0] = lo_f(a.x); v[1] = hi_f(a.x); v[2] = lo_f(a.y); v[3] = hi_f(a.y);
+  v[4] = lo_f(a.z); v[5] = hi_f(a.z); v[6] = lo_f(a.w); v[7] = hi_f(a.w);
+}
+
+__device__ __forceinline__ uint4 pack8(const float* v) {
+  return make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(const uint4* gate, const uint4* up,
+                                                           uint4* out, int64_t n_vec) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVecPerThread;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kVecPerThread + threadIdx.x;
+       base < n_vec; base += stride) {
+    uint4 gv[kVecPerThread], uv[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      const int64_t i = base + j * kThreads;
+      if (i < n_vec) {
+        gv[j] = gate[i];
+        uv[j] = up[i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      const int64_t i = base + j * kThreads;
+      if (i < n_vec) {
+        float g[8], u[8], o[8];
+        unpack8(gv[j], g);
+        unpack8(uv[j], u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = g[e] * sigmoid(g[e]) * u[e];
+        out[i] = pack8(o);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(const uint4* grad, const uint4* gate,
+                                                           const uint4* up, uint4* dgate,
+                                                           uint4* dup, int64_t n_vec) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVecPerThread;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads * kVecPerThread + threadIdx.x;
+       base < n_vec; base += stride) {
+    uint4 dv[kVecPerThread], gv[kVecPerThread], uv[kVecPerThread];
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      const int64_t i = base + j * kThreads;
+      if (i < n_vec) {
+        dv[j] = grad[i];
+        gv[j] = gate[i];
+        uv[j] = up[i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kVecPerThread; ++j) {
+      const int64_t i = base + j * kThreads;
+      if (i < n_vec) {
+        float d[8], g[8], u[8], dg[8], du[8];
+        unpack8(dv[j], d);
+        unpack8(gv[j], g);
+        unpack8(uv[j], u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float sig = sigmoid(g[e]);
+          du[e] = d[e] * g[e] * sig;
+          dg[e] = d[e] * u[e] * sig * (1.0f + g[e] * (1.0f - sig));
+        }
+        dgate[i] = pack8(dg);
+        dup[i] = pack8(du);
+      }
+    }
+  }
+}
+
+// Scalar tail / unaligned path.
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_any(const uint16_t* gate, const uint16_t* up,
+                                                           uint16_t* out, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const float g = h2f(gate[i]);
+  out[i] = f2h(g * sigmoid(g) * h2f(up[i]));
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_any(const uint16_t* grad, const uint16_t* gate,
+                                                           const uint16_t* up, uint16_t* dgate,
+                                                           uint16_t* dup, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const float d = h2f(grad[i]), g = h2f(gate[i]), u = h2f(up[i]);
+  const float sig = sigmoid(g);
+  dgate[i] = f2h(d * u * sig * (1.0f + g * (1.0f - sig)));
+  dup[i] = f2h(d * g * sig);
+}
+
+unsigned vec_blocks(int64_t n_vec) {
+  // Enough workgroups to cover every CU several times over; the grid-stride loop takes the rest.
+  const int64_t per_block = static_cast<int64_t>(kThreads) * kVecPerThread;
+  const int64_t need = (n_vec + per_block - 1) / per_block;
+  return static_cast<unsigned>(need < 65536 ? need : 65536);
+}
+
+}  // namespace
+}  // namespace talm
+
+using namespace talm;
+
+TALM_API int talm_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                             void* stream) {
+  if (n < 0) return fail(TALM_EINVAL, "swiglu_fwd: n %lld < 0", (long long)n);
+  if (n == 0) return ok();
+  if (!gate || !up || !out) return fail(TALM_EINVAL, "swiglu_fwd: null pointer");
+  const hipStream_t s = as_stream(stream);
+  int64_t head = 0;
+  if (aligned(gate, 16) && aligned(up, 16) && aligned(out, 16)) {
+    const int64_t n_vec = n / 8;
+    head = n_vec * 8;
+    if (n_vec)
+      hipLaunchKernelGGL(swiglu_fwd_vec, dim3(vec_blocks(n_vec)), dim3(kThreads), 0, s,
+                         reinterpret_cast<const uint4*>(gate), reinterpret_cast<const uint4*>(up),
+                         reinterpret_cast<uint4*>(out), n_vec);
+  }
+  const int64_t tail = n - head;
+  if (tail)
+    hipLaunchKernelGGL(swiglu_fwd_any, dim3(static_cast<unsigned>((tail + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, s, gate + head, up + head, out + head, tail);
+  return check_launch("swiglu_fwd");
+}
+
+TALM_API int talm_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up,
+                             uint16_t* dgate, uint16_t* dup, int64_t n, void* stream) {
+  if (n < 0) return fail(TALM_EINVAL, "swiglu_bwd: n %lld < 0", (long long)n);
+  if (n == 0) return ok();
+  if (!grad || !gate || !up || !dgate || !dup) return fail(TALM_EINVAL, "swiglu_bwd: null pointer");
+  const hipStream_t s = as_stream(stream);
+  int64_t head = 0;
+  if (aligned(grad, 16) && aligned(gate, 16) && aligned(up, 16) && aligned(dgate, 16) &&
+      aligned(dup, 16)) {
+    const int64_t n_vec = n / 8;
+    head = n_vec * 8;
+    if (n_vec)
+      hipLaunchKernelGGL(swiglu_bwd_vec, dim3(vec_blocks(n_vec)), dim3(kThreads), 0, s,
+                         reinterpret_cast<const uint4*>(grad), reinterpret_cast<const uint4*>(gate),
+                         reinterpret_cast<const uint4*>(up), reinterpret_cast<uint4*>(dgate),
+                         reinterpret_cast<uint4*>(dup), n_vec);
+  }
+  const int64_t tail = n - head;
+  if (tail)
+    hipLaunchKernelGGL(swiglu_bwd_any, dim3(static_cast<unsigned>((tail + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, s, grad + head, gate + head, up + head, dgate + head,
+                       dup + head, tail);
+  return check_launch("swiglu_bwd");
+}

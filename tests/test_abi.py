@@ -1,0 +1,66 @@
+"""The C-ABI library: it loads, it exports every entry point include/talm.h declares with the
+arity the Python binding uses, and argument rejection returns TALM_EINVAL with a message before
+anything touches a GPU (no compute call runs here)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from talm_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "talm.h"
+
+
+def declared():
+    """{name: number of parameters} of every function declared in include/talm.h."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(talm_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+def test_library_builds_loads_and_reports_abi():
+    lib = _lib.lib()
+    assert lib.talm_abi_version() == _lib.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported_with_the_bound_arity():
+    lib = _lib.lib()
+    decl = declared()
+    assert {"talm_last_error", "talm_abi_version", "talm_nf4_group_dequant"} <= set(decl)
+    for name, arity in decl.items():
+        assert hasattr(lib, name), f"{name} declared in talm.h but not exported"
+        if name in _lib.SIGNATURES:
+            assert len(_lib.SIGNATURES[name]) == arity, name
+    assert set(_lib.SIGNATURES) <= set(decl)
+
+
+def test_argument_rejection_needs_no_gpu():
+    lib = _lib.lib()
+    status = lib.talm_nf4_group_dequant(None, None, None, None, None, None, 4, 3, 256, None)
+    assert status == _lib.TALM_EINVAL
+    assert b"qblock" in lib.talm_last_error()
+    status = lib.talm_rmsnorm(None, None, None, None, None, None, None, 1, 8, 7, 1, 0,
+                              ctypes.c_float(1e-6), 0, 0, None)
+    assert status == _lib.TALM_EINVAL and b"dtype" in lib.talm_last_error()
+    with pytest.raises(ValueError, match="even"):
+        _lib.check(lib.talm_nf4_dequant(None, None, None, 3, 64, None), "nf4_dequant")
+    assert lib.talm_swiglu_fwd(None, None, None, 0, None) == _lib.TALM_OK  # empty: no launch
+    assert lib.talm_last_error() == b""
+
+
+def test_custom_ops_are_registered_for_the_gpu_only():
+    import torch
+
+    import talm_amd._ops  # noqa: F401
+
+    for name in ("nf4_group_dequant", "nf4_dequant", "rmsnorm", "rope", "swiglu_fwd",
+                 "swiglu_bwd"):
+        assert hasattr(torch.ops.talm, name)
+    x = torch.zeros(8, dtype=torch.float16)
+    with pytest.raises(NotImplementedError):
+        torch.ops.talm.swiglu_fwd(x, x, x)  # CPU tensors: no kernel, no fallback
