@@ -152,6 +152,35 @@ def kernel_suite(args, only):
             ms, cnt = graph_time_ms(lambda: swiglu.swiglu_bwd(grad, gate, up, dgate, dup),
                                     args.steps, args.warmup, args.reps)
             record("swiglu_bwd", ms, cnt, bytes_=10 * n, config="3: [2048, 8960]")
+    if want("head"):
+        from talm_amd import _ops, fused_head
+
+        d4 = workloads.head_inputs()
+        targets = d4["targets"]
+        labelled = targets >= 0
+        n_lab = int(labelled.sum())
+        order = torch.cat([torch.nonzero(labelled)[:, 0], torch.nonzero(~labelled)[:, 0]])
+        h16 = d4["hidden"][order].contiguous().to(dev)
+        w16 = d4["weight"].to(dev)
+        tt = targets[order].contiguous().to(dev)
+        n, hdim = h16.shape
+        vocab = w16.shape[0]
+        vchunk, group = fused_head.VOCAB_CHUNK, fused_head.GROUP
+        outs = [torch.empty(n, dtype=torch.float32, device=dev),
+                torch.empty(n, dtype=torch.float32, device=dev),
+                torch.empty(n, dtype=torch.int32, device=dev),
+                torch.empty(n, dtype=torch.int32, device=dev),
+                torch.empty(n, hdim, dtype=torch.float16, device=dev)]
+        ws = torch.empty(_ops.head_ce_workspace_bytes(n, hdim, vocab, vchunk, n_lab, group),
+                         dtype=torch.uint8, device=dev)
+
+        def fn():
+            torch.ops.talm.head_ce(h16, w16, tt, vchunk, n_lab, group, *outs, ws)
+
+        ms, cnt = graph_time_ms(fn, max(10, args.steps // 20), args.warmup, 4)
+        flops = 2.0 * vocab * hdim * (n + n_lab)
+        record("head_ce_fwd_bwd", ms, cnt, flops=flops,
+               config=f"4: N={n} H={hdim} V={vocab} N_lab={n_lab} vchunk={vchunk}")
     return results
 
 
@@ -194,14 +223,20 @@ def main():
     only = {s for s in args.only.split(",") if s}
     kernels = kernel_suite(args, only)
     dominant = max(kernels, key=lambda e: e["us"]) if kernels else None
+    if dominant is not None and "tflops" in dominant:
+        line_roofline = {"kernel": dominant["kernel"], "bound": "mfma",
+                         "achieved": dominant["tflops"], "peak": FP16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": dominant["mfma_frac"], "traffic": None}
+    elif dominant is not None:
+        line_roofline = {"kernel": dominant["kernel"], "bound": "hbm",
+                         "achieved": dominant["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": dominant["hbm_frac"], "traffic": None}
     line = {"metric": METRIC, "value": None, "unit": "ms", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": None, "higher_is_better": False,
             "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
             "config": {"workload": "kernel suite (configs 1-4)"}, "kernels": kernels}
     if dominant is not None:
-        line["roofline"] = {"kernel": dominant["kernel"], "bound": "hbm",
-                            "achieved": dominant["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": dominant["hbm_frac"], "traffic": None}
+        line["roofline"] = line_roofline
     if args.cpu_seconds > 0:
         line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -113,6 +113,36 @@ int talm_swiglu_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int
 int talm_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* up,
                     uint16_t* dgate, uint16_t* dup, int64_t n, void* stream);
 
+/*
+ * Bytes of workspace talm_head_ce needs (-1 for arguments it would reject). `group` vocabulary
+ * slices are processed per step: the workspace holds their fp16 logits [n_rows, group * vchunk],
+ * the per-tile statistics and the fp32 gradient partials [group, n_grad, hidden].
+ */
+int64_t talm_head_ce_workspace(int64_t n_rows, int64_t hidden, int64_t vocab, int64_t vchunk,
+                               int64_t n_grad, int32_t group);
+
+/*
+ * Fused LM head + cross-entropy over the vocabulary in slices of `vchunk` columns (a multiple of
+ * 128), forward and gradient in one call; the [n_rows, vocab] logits never exist.
+ * Replaces FusedHeadLossVocab.forward's slice loop with torch.mm, launch_vocab /
+ * fused_head_vocab_kernel and the accumulator addmm (solution/fused_head.py:88-182, :236-251,
+ * :356-383).
+ *   hidden_states f16 [n_rows, hidden] (row stride ldh), weight f16 [vocab, hidden] (row
+ *   stride ldw), targets i64 [n_rows] (-100 = ignore). Rows [0, n_grad) must be exactly the
+ *   labelled rows (the caller orders rows labelled-first, solution/fused_head.py:290-299).
+ * Writes per row: token_loss f32 (log s + m - z_target, 0 unlabelled), entropy f32
+ * (lse - t / s), best_idx i32 (first argmax of the fp16 logits), correct i32 (labelled and
+ * best_idx == target); and, when grad_hidden is not NULL, grad_hidden f16 [n_rows, hidden]
+ * (row stride hidden): dH = acc / s - W[target] for labelled rows, 0 for the others, with
+ * acc = sum over slices of the reference's rescaled fp16(e^{z - m}) W products.
+ * `workspace` (256-byte aligned) holds talm_head_ce_workspace(...) bytes.
+ */
+int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* weight, int64_t ldw,
+                 const int64_t* targets, int64_t n_rows, int64_t hidden, int64_t vocab,
+                 int64_t vchunk, int64_t n_grad, int32_t group, float* token_loss,
+                 float* entropy, int32_t* best_idx, int32_t* correct, uint16_t* grad_hidden,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,6 +30,13 @@ SIGNATURES = {
                   _I64, _I64, _I64, _I64, _I32, _P],
     "talm_swiglu_fwd": [_P, _P, _P, _I64, _P],
     "talm_swiglu_bwd": [_P, _P, _P, _P, _P, _I64, _P],
+    "talm_head_ce": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P,
+                     _P, _P, _I64, _P],
+}
+
+# Entry points that return a size instead of a status.
+SIZE_FUNCTIONS = {
+    "talm_head_ce_workspace": [_I64, _I64, _I64, _I64, _I64, _I32],
 }
 
 _lock = threading.Lock()
@@ -65,6 +72,10 @@ def lib():
                 fn = getattr(handle, name)
                 fn.argtypes = argtypes
                 fn.restype = ctypes.c_int
+            for name, argtypes in SIZE_FUNCTIONS.items():
+                fn = getattr(handle, name)
+                fn.argtypes = argtypes
+                fn.restype = ctypes.c_int64
             _lib = handle
     return _lib
 

@@ -143,3 +143,45 @@ def swiglu_bwd(grad, gate, up, dgate, dup):
     _lib.check(lib.talm_swiglu_bwd(grad.data_ptr(), gate.data_ptr(), up.data_ptr(),
                                    dgate.data_ptr(), dup.data_ptr(), gate.numel(), _stream(gate)),
                "swiglu_bwd")
+
+
+def head_ce_workspace_bytes(n_rows, hidden, vocab, vchunk, n_grad, group):
+    size = _lib.lib().talm_head_ce_workspace(n_rows, hidden, vocab, vchunk, n_grad, group)
+    if size < 0:
+        raise ValueError(f"head_ce: unsupported shape rows={n_rows} hidden={hidden} "
+                         f"vocab={vocab} vchunk={vchunk} n_grad={n_grad} group={group}")
+    return int(size)
+
+
+@_op("head_ce(Tensor hidden, Tensor weight, Tensor targets, int vchunk, int n_grad, int group, "
+     "Tensor(a!) token_loss, Tensor(b!) entropy, Tensor(c!) best_idx, Tensor(d!) correct, "
+     "Tensor(e!)? grad_hidden, Tensor(f!) workspace) -> ()")
+def head_ce(hidden, weight, targets, vchunk, n_grad, group, token_loss, entropy, best_idx,
+            correct, grad_hidden, workspace):
+    """hidden fp16 [N, H] (unit column stride), weight fp16 [V, H] (unit column stride),
+    targets int64 [N] with rows [0, n_grad) exactly the labelled ones."""
+    n_rows, size = hidden.shape
+    vocab = weight.shape[0]
+    _fp16(hidden, "hidden")
+    _fp16(weight, "weight")
+    _require(hidden.stride(1) == 1 and weight.stride(1) == 1 and weight.shape[1] == size,
+             "head_ce: hidden [N, H] and weight [V, H] with unit column stride")
+    _require(targets.dtype == torch.int64 and targets.is_contiguous() and
+             targets.numel() == n_rows, "head_ce: targets int64 [N]")
+    for t, dt in ((token_loss, torch.float32), (entropy, torch.float32), (best_idx, torch.int32),
+                  (correct, torch.int32)):
+        _require(t.dtype == dt and t.is_contiguous() and t.numel() == n_rows,
+                 "head_ce: per-row outputs of N elements")
+    if grad_hidden is not None:
+        _fp16(grad_hidden, "grad_hidden")
+        _require(grad_hidden.is_contiguous() and tuple(grad_hidden.shape) == (n_rows, size),
+                 "head_ce: grad_hidden contiguous [N, H]")
+    _require(workspace.is_cuda and workspace.is_contiguous(), "head_ce: workspace")
+    lib = _lib.lib()
+    _lib.check(lib.talm_head_ce(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
+                                weight.stride(0), targets.data_ptr(), n_rows, size, vocab,
+                                int(vchunk), int(n_grad), int(group), token_loss.data_ptr(),
+                                entropy.data_ptr(), best_idx.data_ptr(), correct.data_ptr(),
+                                _ptr(grad_hidden), workspace.data_ptr(),
+                                workspace.numel() * workspace.element_size(), _stream(hidden)),
+               "head_ce")

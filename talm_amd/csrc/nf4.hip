@@ -8,9 +8,14 @@
 // table is gathered once per 64 weights (one absmax block).
 //
 // Arithmetic is the reference's bit for bit: the scale is rounded after the product and after
-// the offset (no fused multiply-add: __fmul_rn / __fadd_rn are never contracted), the level
-// times the scale is one fp32 product and one round-to-nearest-even to fp16.
+// the offset (no fused multiply-add anywhere in this file), the level times the scale is one
+// fp32 product and one round-to-nearest-even to fp16.
 #include "common.h"
+
+// hipcc contracts a * b + c into v_fma_f32 by default (also through HIP's rounding-mode helpers,
+// whose header definitions carry the contraction flag): contraction is switched off for this
+// whole file and the products and sums below are plain operators, each rounded on its own.
+#pragma clang fp contract(off)
 
 namespace talm {
 namespace {
@@ -25,14 +30,22 @@ __constant__ float kNF4Levels[16] = {
 constexpr int kThreads = 256;
 constexpr int kWordsPerThread = 4;  // 32 weights per thread, four independent 128-bit stores
 
+// The fp32 product, materialized: the empty asm keeps the backend from folding "multiply, then
+// convert to fp16" into one v_fma_mix (a single rounding of the exact product).
+__device__ __forceinline__ float mul_f32(float a, float b) {
+  float p = a * b;
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
 // Eight weights of one packed word (4 bytes, high nibble first) scaled and packed to 4 x 2 fp16.
 __device__ __forceinline__ uint4 dequant_word(uint32_t word, float scale, const float* levels) {
   uint32_t out[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const uint32_t byte = (word >> (8 * b)) & 0xffu;
-    const float first = __fmul_rn(levels[byte >> 4], scale);
-    const float second = __fmul_rn(levels[byte & 15u], scale);
+    const float first = mul_f32(levels[byte >> 4], scale);
+    const float second = mul_f32(levels[byte & 15u], scale);
     out[b] = pack2(first, second);
   }
   return make_uint4(out[0], out[1], out[2], out[3]);
@@ -62,9 +75,9 @@ __global__ __launch_bounds__(kThreads) void nf4_group_kernel(
       words[j] = __builtin_nontemporal_load(packed + w);
       const int64_t row = w >> word_shift;
       const int64_t blk2 = qblock2_shift >= 0 ? (row >> qblock2_shift)
-                                              : static_cast<int64_t>(static_cast<uint64_t>(row) / qblock2);
-      const float prod = __fmul_rn(s_code[absmax8[row]], absmax2[blk2]);
-      scales[j] = __fadd_rn(prod, offset2[blk2]);
+                                              : static_cast<int64_t>(static_cast<uint32_t>(row) / qblock2);
+      const float prod = mul_f32(s_code[absmax8[row]], absmax2[blk2]);
+      scales[j] = prod + offset2[blk2];
     }
   }
 #pragma unroll
@@ -78,7 +91,7 @@ __global__ __launch_bounds__(kThreads) void nf4_group_kernel(
 __global__ __launch_bounds__(kThreads) void nf4_words_kernel(const uint32_t* __restrict__ packed,
                                                              const float* __restrict__ absmax,
                                                              uint4* __restrict__ out,
-                                                             int64_t n_words, int64_t words_per_block) {
+                                                             int64_t n_words, uint32_t words_per_block) {
   __shared__ float s_levels[16];
   if (threadIdx.x < 16) s_levels[threadIdx.x] = kNF4Levels[threadIdx.x];
   __syncthreads();
@@ -88,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void nf4_words_kernel(const uint32_t* __r
     const int64_t w = base + j * kThreads;
     if (w < n_words) {
       const uint32_t word = __builtin_nontemporal_load(packed + w);
-      out[w] = dequant_word(word, absmax[w / words_per_block], s_levels);
+      out[w] = dequant_word(word, absmax[static_cast<uint32_t>(w) / words_per_block], s_levels);
     }
   }
 }
@@ -97,12 +110,12 @@ __global__ __launch_bounds__(kThreads) void nf4_words_kernel(const uint32_t* __r
 __global__ __launch_bounds__(kThreads) void nf4_bytes_kernel(const uint8_t* __restrict__ packed,
                                                              const float* __restrict__ absmax,
                                                              uint32_t* __restrict__ out,
-                                                             int64_t n_bytes, int64_t blocksize) {
+                                                             int64_t n_bytes, uint32_t blocksize) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i >= n_bytes) return;
   const uint32_t byte = packed[i];
-  const float scale = absmax[(2 * i) / blocksize];
-  out[i] = pack2(__fmul_rn(kNF4Levels[byte >> 4], scale), __fmul_rn(kNF4Levels[byte & 15u], scale));
+  const float scale = absmax[static_cast<uint32_t>(2 * i) / blocksize];
+  out[i] = pack2(mul_f32(kNF4Levels[byte >> 4], scale), mul_f32(kNF4Levels[byte & 15u], scale));
 }
 
 int log2_exact(int64_t v) {
@@ -133,7 +146,8 @@ TALM_API int talm_nf4_group_dequant(const uint8_t* packed, const uint8_t* absmax
   const int64_t n_words = n_rows * (qblock / 8);
   const int64_t per_block = kThreads * kWordsPerThread;
   const int64_t blocks = (n_words + per_block - 1) / per_block;
-  if (blocks > 0x7fffffff) return fail(TALM_EINVAL, "nf4_group_dequant: too many weights");
+  if (blocks > 0x7fffffff || n_rows > 0xffffffffLL)
+    return fail(TALM_EINVAL, "nf4_group_dequant: too many weights");
   hipLaunchKernelGGL(nf4_group_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
                      as_stream(stream), reinterpret_cast<const uint32_t*>(packed), absmax8, code,
                      absmax2, offset2, reinterpret_cast<uint4*>(out), n_words, qshift - 3,
@@ -148,18 +162,19 @@ TALM_API int talm_nf4_dequant(const uint8_t* packed, const float* absmax, uint16
   if (n == 0) return ok();
   if (!packed || !absmax || !out) return fail(TALM_EINVAL, "nf4_dequant: null pointer");
   if (!aligned(out, 4)) return fail(TALM_EINVAL, "nf4_dequant: out must be 4-byte aligned");
+  if (n > 0xffffffffLL) return fail(TALM_EINVAL, "nf4_dequant: more than 2^32 weights");
   const hipStream_t s = as_stream(stream);
   if (blocksize % 8 == 0 && n % 8 == 0 && aligned(packed, 4) && aligned(out, 16)) {
     const int64_t n_words = n / 8;
     const int64_t per_block = kThreads * kWordsPerThread;
     hipLaunchKernelGGL(nf4_words_kernel, dim3(static_cast<unsigned>((n_words + per_block - 1) / per_block)),
                        dim3(kThreads), 0, s, reinterpret_cast<const uint32_t*>(packed), absmax,
-                       reinterpret_cast<uint4*>(out), n_words, static_cast<int64_t>(blocksize / 8));
+                       reinterpret_cast<uint4*>(out), n_words, static_cast<uint32_t>(blocksize / 8));
   } else {
     const int64_t n_bytes = n / 2;
     hipLaunchKernelGGL(nf4_bytes_kernel, dim3(static_cast<unsigned>((n_bytes + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, s, packed, absmax, reinterpret_cast<uint32_t*>(out), n_bytes,
-                       static_cast<int64_t>(blocksize));
+                       static_cast<uint32_t>(blocksize));
   }
   return check_launch("nf4_dequant");
 }

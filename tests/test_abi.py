@@ -34,9 +34,10 @@ def test_every_declared_symbol_is_exported_with_the_bound_arity():
     assert {"talm_last_error", "talm_abi_version", "talm_nf4_group_dequant"} <= set(decl)
     for name, arity in decl.items():
         assert hasattr(lib, name), f"{name} declared in talm.h but not exported"
-        if name in _lib.SIGNATURES:
-            assert len(_lib.SIGNATURES[name]) == arity, name
-    assert set(_lib.SIGNATURES) <= set(decl)
+        bound = {**_lib.SIGNATURES, **_lib.SIZE_FUNCTIONS}
+        if name in bound:
+            assert len(bound[name]) == arity, name
+    assert set(_lib.SIGNATURES) | set(_lib.SIZE_FUNCTIONS) <= set(decl)
 
 
 def test_argument_rejection_needs_no_gpu():
@@ -64,3 +65,28 @@ def test_custom_ops_are_registered_for_the_gpu_only():
     x = torch.zeros(8, dtype=torch.float16)
     with pytest.raises(NotImplementedError):
         torch.ops.talm.swiglu_fwd(x, x, x)  # CPU tensors: no kernel, no fallback
+
+
+def test_nf4_kernels_have_no_fused_multiply_add():
+    """The grouped NF4 kernel must round code * absmax2 before adding the offset (the reference
+    compiles without FMA, solution/qgroup.py:99): the gfx950 assembly of the NF4 kernels holds no
+    fused multiply-add instruction."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    src = Path(__file__).resolve().parents[1] / "talm_amd" / "csrc" / "nf4.hip"
+    with tempfile.TemporaryDirectory() as tmp:
+        asm = Path(tmp) / "nf4.s"
+        subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "--cuda-device-only",
+                        "-S", str(src), "-o", str(asm)], check=True, capture_output=True)
+        text = asm.read_text()
+    bodies = re.findall(r"^(_Z\w*nf4_\w+_kernel\w*):[^\n]*\n(.*?)^\.Lfunc_end", text,
+                        flags=re.S | re.M)
+    assert len(bodies) == 3
+    for name, body in bodies:
+        assert "v_cvt_pk_f16_f32" in body or "v_cvt_f16_f32" in body, name
+        assert not re.search(r"\bv_(pk_)?fma", body), f"{name} contains a fused multiply-add"
