@@ -184,6 +184,102 @@ def kernel_suite(args, only):
     return results
 
 
+def run_steps(model, trainer, n_steps, seed, timed_from):
+    """Run n_steps optimizer steps; time steps [timed_from, n_steps) between two device syncs.
+    Returns (losses, ms_per_timed_step, peak_bytes)."""
+    from talm_amd import qlora_model
+
+    vocab = model.config.vocab_size
+    batches = [qlora_model.make_batch(seed, i, vocab) for i in range(n_steps)]
+    losses = []
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    t0 = None
+    for i in range(n_steps):
+        if i == timed_from:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+        losses.append(trainer.step(batches[i]))
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / max(1, n_steps - timed_from)
+    return [float(x) for x in losses], ms, torch.cuda.max_memory_allocated()
+
+
+def step_workload(args):
+    """Configuration 5: the full QLoRA step of the Qwen2.5-1.5B-shaped model, patched
+    (every kernel of the package), and the unpatched eager path for the loss curve."""
+    from talm_amd import engaged, patches, qlora_model
+
+    n_steps = args.warmup + args.steps
+    out = {}
+    for mode in ("patched", "eager") if not args.no_eager else ("patched",):
+        torch.cuda.empty_cache()
+        model = qlora_model.build_model(seed=1)
+        trainer = qlora_model.Trainer(model, steps=n_steps)
+        if mode == "patched":
+            patches.apply()
+            engaged.reset()
+        try:
+            losses, ms, peak = run_steps(model, trainer, n_steps, seed=7, timed_from=args.warmup)
+        finally:
+            if mode == "patched":
+                ran = dict(engaged.RAN)
+                patches.unapply()
+        out[mode] = {"losses": losses, "ms_per_step": ms, "peak_bytes": peak}
+        if mode == "patched":
+            out[mode]["engaged"] = ran
+        print(f"[bench] step {mode}: {ms:.2f} ms/step, peak {peak / 2**30:.2f} GiB, "
+              f"loss {losses[0]:.4f} -> {losses[-1]:.4f}", flush=True)
+        del model, trainer
+    return out
+
+
+def cpu_baseline_step(seconds):
+    """The reference's eager path on the host cores, bounded: one decoder layer of the QLoRA
+    model (fp32, forward + backward) on a config-5 token count, timed and scaled to 28 layers,
+    plus the head + cross-entropy oracle on a row sample scaled to the token count."""
+    import numpy as np
+
+    from oracle import head as head_oracle
+    from talm_amd import qlora_model
+
+    torch.manual_seed(0)
+    n_tok = 1280  # 4 rows of 128-512 tokens: the mean of config 5
+    cfg = qlora_model.qwen2_config(num_hidden_layers=1)
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2DecoderLayer, Qwen2RotaryEmbedding
+
+    layer = Qwen2DecoderLayer(cfg, 0).float()
+    rot = Qwen2RotaryEmbedding(cfg)
+    x = torch.randn(1, n_tok, cfg.hidden_size, requires_grad=True)
+    pos = torch.arange(n_tok)[None]
+    pe = rot(x, pos)
+    mask = torch.full((n_tok, n_tok), float("-inf")).triu(1)[None, None]
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        y = layer(x, attention_mask=mask, position_embeddings=pe, position_ids=pos)
+        y.float().sum().backward()
+        reps += 1
+        if time.perf_counter() - t0 > seconds / 2:
+            break
+    layer_ms = (time.perf_counter() - t0) * 1e3 / reps
+    rows = 16
+    rng = np.random.default_rng(0)
+    h = rng.standard_normal((rows, cfg.hidden_size)).astype(np.float16)
+    w = (rng.standard_normal((cfg.vocab_size, cfg.hidden_size)) * 0.02).astype(np.float16)
+    t = rng.integers(0, cfg.vocab_size, rows)
+    t1 = time.perf_counter()
+    head_oracle.head_ce(h, w, t, vchunk=8192)
+    head_ms = (time.perf_counter() - t1) * 1e3 * n_tok / rows
+    threads = torch.get_num_threads()
+    return {"value": round(28 * layer_ms + head_ms, 1), "unit": "ms/step (estimated)",
+            "cores": threads, "kind": "port",
+            "sample": f"1 Qwen2.5-1.5B decoder layer fwd+bwd in fp32 PyTorch CPU eager on "
+                      f"{n_tok} tokens ({reps} reps, {layer_ms:.0f} ms) x 28 layers + the head/CE "
+                      f"oracle on {rows} rows x full vocabulary scaled to {n_tok} rows "
+                      f"({head_ms:.0f} ms); {threads} threads, {os.cpu_count()} CPUs visible"}
+
+
 def cpu_baseline_nf4(seconds):
     """The C oracle of the grouped NF4 dequant (one thread) on the config-1 layer, repeated for
     about `seconds`; weights per second."""
@@ -212,7 +308,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--only", default="")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--workload", choices=("step", "kernels"), default="step")
+    ap.add_argument("--no-eager", action="store_true", help="skip the eager loss-curve run")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every box of this build has a single MI355X and "
@@ -221,8 +319,17 @@ def main():
         sys.exit(2)
     torch.cuda.set_device(0)
     only = {s for s in args.only.split(",") if s}
-    kernels = kernel_suite(args, only)
+    if args.workload == "step":
+        # defaults: 64 steps, the first 2 untimed (the reference times steps 3-64)
+        if "--steps" not in sys.argv:
+            args.steps = 62
+        if "--warmup" not in sys.argv:
+            args.warmup = 2
+    step = step_workload(args) if args.workload == "step" else None
+    kernel_args = argparse.Namespace(**{**vars(args), "steps": 200, "warmup": 10})
+    kernels = kernel_suite(kernel_args, only)
     dominant = max(kernels, key=lambda e: e["us"]) if kernels else None
+    line_roofline = None
     if dominant is not None and "tflops" in dominant:
         line_roofline = {"kernel": dominant["kernel"], "bound": "mfma",
                          "achieved": dominant["tflops"], "peak": FP16_PEAK_TFLOPS,
@@ -234,11 +341,30 @@ def main():
     line = {"metric": METRIC, "value": None, "unit": "ms", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": None, "higher_is_better": False,
             "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
-            "config": {"workload": "kernel suite (configs 1-4)"}, "kernels": kernels}
-    if dominant is not None:
+            "config": {"workload": "kernel suite (configs 1-4)"}}
+    if step is not None:
+        p = step["patched"]
+        line.update(value=round(p["ms_per_step"], 3), ms_per_step=round(p["ms_per_step"], 3))
+        line["config"] = {"workload": "config 5: QLoRA step, Qwen2.5-1.5B shape (28 layers, "
+                                      "NF4 double-quant base, LoRA r16/a32 on q,v), B4 x S512 "
+                                      "varlen (lengths U[128,512]), fp16 autocast, AdamW",
+                          "global_batch": 4, "seq_len": 512, "parallelism": "none (1 GPU)"}
+        line["peak_hbm_gib"] = round(p["peak_bytes"] / 2**30, 3)
+        line["loss_first_last"] = [round(p["losses"][0], 5), round(p["losses"][-1], 5)]
+        if "eager" in step:
+            e = step["eager"]
+            rel = [abs(a - b) / abs(b) for a, b in zip(p["losses"], e["losses"])]
+            line["eager_ms_per_step"] = round(e["ms_per_step"], 3)
+            line["eager_peak_hbm_gib"] = round(e["peak_bytes"] / 2**30, 3)
+            line["loss_curve_max_rel_diff"] = round(max(rel), 6)
+            line["loss_curve_mean_rel_diff"] = round(sum(rel) / len(rel), 6)
+        line["engaged"] = {k: v for k, v in sorted(p["engaged"].items()) if v}
+    line["kernels"] = kernels
+    if line_roofline is not None:
         line["roofline"] = line_roofline
     if args.cpu_seconds > 0:
-        line["cpu_baseline"] = cpu_baseline_nf4(args.cpu_seconds)
+        line["cpu_baseline"] = (cpu_baseline_step(args.cpu_seconds) if step is not None
+                                else cpu_baseline_nf4(args.cpu_seconds))
     print(json.dumps(line), flush=True)
 
 

@@ -1,0 +1,295 @@
+"""q|k|v of a decoder layer as one projection node on the packed 4-bit weights (qgroup.py).
+
+Mirrors solution/fused_proj.py:88-218: the layer group dequantizes q, k, v, o, gate, up, down
+into one buffer per pass, so [Wq; Wk; Wv] ([1536 + 256 + 256, 1536]) is one row-major matrix:
+[q|k|v] = x [Wq; Wk; Wv]^T + [bq|bk|bv] is ONE GEMM, the LoRA adapters of q_proj and v_proj are
+added with PEFT's ops in PEFT's order (lora.py), v is returned as a fresh tensor and q, k as column
+views. Backward: dX = [dq|dk|dv] [Wq; Wk; Wv] in one GEMM (K = 2048) plus the adapters' input
+gradients, and the adapters' weight gradients.
+
+MI355X addition: with `rope=(cos, sin)` the node also applies the rotary embedding to q and k IN
+PLACE on its own output (the rope kernel reads each rotation pair before writing it), and in the
+backward rotates dq and dk back in place inside the concatenated gradient it builds for the dX
+GEMM anyway: no RoPE node, no new q/k tensors, no strided gradient copies. This is safe because
+the node keeps only x for its backward (the reference notes this: q and k are views of the
+node's output that nothing else reads before the attention).
+"""
+
+import torch
+import torch.nn.functional as F
+
+from .engaged import FELL_BACK, ON, RAN
+from .lora import _power_of_two, _to_half, lora_plan
+from .rope import rope_
+from .state import DISABLED, fallback
+
+Q, K, V, O, GATE, UP, DOWN = range(7)
+COUNTS = {"attn": 0, "attn_fallback": 0}
+
+
+class FusedProjections(torch.autograd.Function):
+    """y_i = x W_i^T + b_i (+ scaling_i * B_i(A_i(dropout_i(x)))) for the adjacent packed
+    projections first .. last - 1 of a LayerGroup, the base part as one GEMM; optionally the
+    rotary embedding of the first two outputs (q, k) in place."""
+
+    @staticmethod
+    def forward(ctx, x, group, first, last, adapters, compact, rope, head_dim, *lora_weights):
+        ctx.fetched, states = False, []
+        try:
+            return FusedProjections._forward(ctx, x, group, first, last, adapters, compact, rope,
+                                             head_dim, lora_weights, states)
+        except Exception:
+            if ctx.fetched:
+                group.refund("fwd", last - first)
+            drawn = [state for state in states if state is not None]
+            if drawn:
+                torch.cuda.set_rng_state(drawn[0], x.device)
+            raise
+
+    @staticmethod
+    def _forward(ctx, x, group, first, last, adapters, compact, rope, head_dim, lora_weights,
+                 states):
+        x2 = x.reshape(-1, x.shape[-1])
+        n_tok = x2.shape[0]
+        sizes = [group.shapes[i][0] for i in range(first, last)]
+        bounds = [0]
+        for size in sizes:
+            bounds.append(bounds[-1] + size)
+        weight = group.span("fwd", first, last)
+        ctx.fetched = weight is not None
+        out = F.linear(x2, weight, group.span_bias(first, last))
+        del weight
+        results = [None] * len(sizes)
+        saved = [x2]
+        for k, (seg, scaling, p) in enumerate(adapters):
+            a16, b16 = _to_half(lora_weights[2 * k], lora_weights[2 * k + 1])
+            state = None
+            if p > 0:
+                state = torch.cuda.get_rng_state(x.device)
+                xd = torch.native_dropout(x2, p, True)[0]
+            else:
+                xd = x2
+            t = torch.mm(xd, a16.t())
+            del xd
+            branch = torch.mm(t, b16.t())
+            base = out[:, bounds[seg]:bounds[seg + 1]]
+            alpha = scaling
+            if not _power_of_two(scaling):
+                branch.mul_(scaling)
+                alpha = 1
+            base.add_(branch, alpha=alpha)
+            states.append(state)
+            saved += [t, a16, b16]
+        if rope is not None:
+            cos, sin = rope
+            q = out[:, bounds[0]:bounds[1]].view(n_tok, -1, head_dim)
+            k = out[:, bounds[1]:bounds[2]].view(n_tok, -1, head_dim)
+            rope_(q, k, cos, sin, backward=False)
+            RAN["rope"] += 1
+            saved += [cos, sin]
+        for seg in range(len(sizes)):
+            base = out[:, bounds[seg]:bounds[seg + 1]]
+            results[seg] = base.contiguous() if seg in compact else base
+        ctx.save_for_backward(*saved)
+        ctx.group, ctx.first, ctx.last = group, first, last
+        ctx.adapters, ctx.states, ctx.sizes = adapters, states, sizes
+        ctx.has_rope, ctx.head_dim = rope is not None, head_dim
+        ctx.x_shape = x.shape
+        lead = x.shape[:-1]
+        return tuple(r.view(*lead, r.shape[1]) for r in results)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        x2, *rest = ctx.saved_tensors
+        n_tok = x2.shape[0]
+        group = ctx.group
+        if ctx.has_rope:
+            cos, sin = rest[-2:]
+            rest = rest[:-2]
+        bounds = [0]
+        for size in ctx.sizes:
+            bounds.append(bounds[-1] + size)
+        # one [N, sum of out] fp16 gradient: the dX GEMM's operand and the adapters' dy
+        dcat = torch.empty(n_tok, bounds[-1], dtype=torch.float16, device=x2.device)
+        for i, grad in enumerate(grads):
+            part = dcat[:, bounds[i]:bounds[i + 1]]
+            if grad is None:
+                part.zero_()
+            else:
+                part.copy_(grad.reshape(n_tok, -1))
+        if ctx.has_rope:
+            dq = dcat[:, bounds[0]:bounds[1]].view(n_tok, -1, ctx.head_dim)
+            dk = dcat[:, bounds[1]:bounds[2]].view(n_tok, -1, ctx.head_dim)
+            rope_(dq, dk, cos, sin, backward=True)
+            RAN["rope"] += 1
+        dys = [dcat[:, bounds[i]:bounds[i + 1]] for i in range(len(ctx.sizes))]
+        dx = None
+        if ctx.needs_input_grad[0]:
+            weight = group.span("bwd", ctx.first, ctx.last)
+            if weight is not None:
+                dx = torch.mm(dcat, weight)
+                del weight
+            else:
+                for i, dy in enumerate(dys):
+                    weight = group.weight("bwd", ctx.first + i)
+                    if dx is None:
+                        dx = torch.mm(dy, weight)
+                    else:
+                        dx.addmm_(dy, weight)
+                    del weight
+        lora_grads = []
+        for k, (seg, scaling, p) in enumerate(ctx.adapters):
+            t, a16, b16 = rest[3 * k:3 * k + 3]
+            dy = dys[seg]
+            state = ctx.states[k]
+            mask = None
+            xd = x2
+            if state is not None:
+                device = x2.device
+                current = torch.cuda.get_rng_state(device)
+                torch.cuda.set_rng_state(state, device)
+                xd, mask = torch.native_dropout(x2, p, True)
+                torch.cuda.set_rng_state(current, device)
+            g = dy * scaling
+            u = torch.mm(g, b16)
+            if dx is not None:
+                dx_lora = torch.mm(u, a16)
+                if mask is not None:
+                    dx_lora = torch.ops.aten.native_dropout_backward(dx_lora, mask, 1.0 / (1.0 - p))
+                dx.add_(dx_lora)
+                del dx_lora
+            index = 8 + 2 * k
+            lora_grads.append(torch.mm(u.t(), xd).float() if ctx.needs_input_grad[index] else None)
+            lora_grads.append(torch.mm(g.t(), t).float() if ctx.needs_input_grad[index + 1]
+                              else None)
+            del xd, mask
+        dx = None if dx is None else dx.view(ctx.x_shape)
+        return (dx, None, None, None, None, None, None, None, *lora_grads)
+
+
+_HOOK_DICTS = ("_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks")
+
+
+def _no_hooks(modules):
+    from torch.nn.modules import module as nn_module
+
+    for name in ("_global_forward_hooks", "_global_forward_pre_hooks", "_global_backward_hooks",
+                 "_global_backward_pre_hooks"):
+        if getattr(nn_module, name, None):
+            return False
+    return all(not getattr(m, attr, None) for m in modules for attr in _HOOK_DICTS)
+
+
+def _packed(module):
+    return getattr(module, "_solution_group", None)
+
+
+def qkv_plan(attn, x):
+    """(group, adapters, lora weights) when q_proj, k_proj and v_proj are projections 0, 1, 2 of
+    one packed layer group, each plain or a LoRA layer `lora_plan` takes, and this forward pass
+    dequantizes the whole layer; else None (solution/fused_proj.py:318-353)."""
+    from .lora import LoraLinear
+
+    if not (x.is_cuda and x.dtype == torch.float16 and x.dim() >= 2) \
+            or "fused_proj" in DISABLED or "qgroup" in DISABLED:
+        return None
+    group, adapters, weights, modules = None, [], [], []
+    for seg, name in enumerate(("q_proj", "k_proj", "v_proj")):
+        module = getattr(attn, name, None)
+        if module is None:
+            return None
+        tag = _packed(module)
+        modules.append(module)
+        if tag is None:
+            if not isinstance(module, LoraLinear) or "lora" in DISABLED:
+                return None
+            plan = lora_plan(module, x)
+            if plan is None:
+                return None
+            tag = plan[:2]
+            name_ = module.active_adapters[0]
+            modules += [module.base_layer, module.lora_A[name_], module.lora_B[name_],
+                        module.lora_dropout[name_]]
+            adapters.append((seg, plan[4], plan[5]))
+            weights += [plan[2], plan[3]]
+        if group is None:
+            group = tag[0]
+        if tag[0] is not group or tag[1] != seg:
+            return None
+    if any(group.shapes[i][1] != x.shape[-1] for i in (Q, K, V)):
+        return None
+    if not _no_hooks(modules) or group.split_now("fwd"):
+        return None
+    return group, tuple(adapters), weights
+
+
+def _rope_ok(cos, sin, n_tok, head_dim):
+    return (cos is not None and cos.dim() == 3 and cos.shape[0] == 1 and cos.shape[1] == n_tok
+            and cos.shape[2] == head_dim and cos.dtype == torch.float32 and cos.shape == sin.shape
+            and cos.stride(-1) == 1 and sin.stride(-1) == 1 and "rope" not in DISABLED)
+
+
+def patch_qwen2_attention():
+    """`Qwen2Attention.forward` with q|k|v (+ LoRA, + RoPE in place) as one FusedProjections
+    node when `qkv_plan` takes the layer; transformers' own forward otherwise
+    (solution/fused_proj.py:382-445)."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    from transformers.models.qwen2 import modeling_qwen2
+
+    cls = modeling_qwen2.Qwen2Attention
+    original = cls.forward
+    ON.add("fused_proj")
+    if getattr(original, "_solution_fused", False):
+        return
+
+    def forward(self, hidden_states, position_embeddings=None, attention_mask=None,
+                past_key_values=None, **kwargs):
+        plan = None
+        if position_embeddings is not None and past_key_values is None:
+            plan = qkv_plan(self, hidden_states)
+        if plan is None:
+            COUNTS["attn_fallback"] += 1
+            FELL_BACK["fused_proj"] += 1
+            return original(self, hidden_states, position_embeddings, attention_mask,
+                            past_key_values=past_key_values, **kwargs)
+        group, adapters, weights = plan
+        cos, sin = position_embeddings
+        input_shape = hidden_states.shape[:-1]
+        n_tok = hidden_states.numel() // hidden_states.shape[-1]
+        rope = (cos[0] if cos.dim() == 3 else cos, sin[0] if sin.dim() == 3 else sin) \
+            if hidden_states.shape[0] == 1 and _rope_ok(cos, sin, n_tok, self.head_dim) else None
+        try:
+            q, k, v = FusedProjections.apply(hidden_states, group, Q, V + 1, adapters, (V - Q,),
+                                             rope, self.head_dim, *weights)
+        except Exception as exc:  # noqa: BLE001 - state.py convention
+            if not fallback("fused_proj", exc):
+                raise
+            COUNTS["attn_fallback"] += 1
+            FELL_BACK["fused_proj"] += 1
+            return original(self, hidden_states, position_embeddings, attention_mask,
+                            past_key_values=past_key_values, **kwargs)
+        COUNTS["attn"] += 1
+        RAN["fused_proj"] += 1
+        if torch.is_grad_enabled() and hidden_states.requires_grad:
+            group.expected_bwd += 3
+        hidden_shape = (*input_shape, -1, self.head_dim)
+        query_states = q.view(hidden_shape).transpose(1, 2)
+        key_states = k.view(hidden_shape).transpose(1, 2)
+        value_states = v.view(hidden_shape).transpose(1, 2)
+        del q, k, v
+        if rope is None:
+            query_states, key_states = modeling_qwen2.apply_rotary_pos_emb(
+                query_states, key_states, cos, sin)
+        attention_interface = ALL_ATTENTION_FUNCTIONS.get_interface(
+            self.config._attn_implementation, modeling_qwen2.eager_attention_forward)
+        attn_output, attn_weights = attention_interface(
+            self, query_states, key_states, value_states, attention_mask,
+            dropout=0.0 if not self.training else self.attention_dropout,
+            scaling=self.scaling, sliding_window=self.sliding_window, **kwargs)
+        attn_output = attn_output.reshape(*input_shape, -1).contiguous()
+        attn_output = self.o_proj(attn_output)
+        return attn_output, attn_weights
+
+    forward._solution_fused = True
+    forward._original = original
+    cls.forward = forward

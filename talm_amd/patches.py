@@ -8,17 +8,19 @@ the original code outside the exact situation it was written for. Installed here
 - RoPE (rope.py);
 - SwiGLU with the in-place backward (swiglu.py, swiglu_inplace.py), or the save-up MLP
   (mlp_save_up.py, opt-in SOLUTION_MLP_SAVE_UP=1);
-- grouped NF4 dequantization of the 4-bit projections (qgroup.py);
-- the fused LM head + cross-entropy of the causal LM (fused_head.py, below).
+- grouped NF4 dequantization of the 4-bit projections (qgroup.py), the LoRA node (lora.py) and
+  q|k|v as one projection node with the rotary embedding in place (fused_proj.py);
+- padding removal with per-row attention (unpad.py) and the fused LM head + cross-entropy of
+  the causal LM (fused_head.py, `patch_qwen2_causal_lm` below).
 
 Switches: SOLUTION_DISABLE_<PART>=1 leaves a part out (RMSNORM, ADDNORM, ROPE, SWIGLU_INPLACE,
-GROUP, FUSED_HEAD), as in the reference (solution/__init__.py:51-84).
+GROUP, LORA, FUSED_PROJ, FUSED_HEAD, UNPAD), as in the reference (solution/__init__.py:51-84).
 """
 
 import os
 
 from .engaged import ON
-from .state import installing
+from .state import DISABLED, fallback, installing
 
 
 def _in_chain(fn, marker):
@@ -35,6 +37,170 @@ def _in_chain(fn, marker):
 
 def _off(name):
     return os.environ.get(f"SOLUTION_DISABLE_{name}") == "1"
+
+
+# ------------------------------------------------------------------ the fused causal LM -----
+
+_unpad = {"enabled": os.environ.get("SOLUTION_DISABLE_UNPAD") != "1", "checked": 0}
+ORIGINAL_FORWARD = {}
+LAST_STEP = []  # the per-token outputs of the last fused forward (Soup's ChunkedStep fields)
+
+
+def _restart(device, rng_state):
+    """Before a forward that failed part-way runs again: the generator back to `rng_state` and
+    the layer groups' pass bookkeeping reset (solution/patches.py:55-63)."""
+    import torch
+
+    from . import qgroup
+
+    torch.cuda.set_rng_state(rng_state, device)
+    qgroup.reset_passes()
+
+
+def _head_is_fusable(lm):
+    import torch
+
+    head = getattr(lm, "lm_head", None)
+    weight = getattr(head, "weight", None)
+    return (isinstance(weight, torch.Tensor) and weight.is_cuda and not weight.requires_grad
+            and getattr(head, "bias", None) is None and weight.dim() == 2
+            and "forward" not in lm.__dict__)
+
+
+def _fused_forward_applies(lm, labels, logits_to_keep, kwargs):
+    import torch
+
+    model = getattr(lm, "model", None)
+    return (labels is not None and isinstance(labels, torch.Tensor) and labels.dim() == 2
+            and getattr(lm, "training", False) and isinstance(logits_to_keep, int)
+            and logits_to_keep == 0 and "shift_labels" not in kwargs and _head_is_fusable(lm)
+            and not getattr(model, "gradient_checkpointing", False))
+
+
+def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_values,
+                   inputs_embeds, labels, use_cache, kwargs, output_cls, stage):
+    """The fused training forward of Qwen2ForCausalLM (solution/patches.py:173-260): shift the
+    labels, pack the real tokens of a right-padded batch into one flat sequence (one host sync),
+    run the decoder, the fused head + cross-entropy, and scatter the per-token outputs back."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from .engaged import FELL_BACK, RAN
+    from .fused_head import fused_head_loss
+    from .rmsnorm import link_next_norms
+    from .unpad import is_right_padded, rows_context, unpad_batch
+
+    stage.clear()
+    kwargs.pop("return_dict", None)
+    num_items = kwargs.pop("num_items_in_batch", None)
+    batch, seq = labels.shape
+    shift = torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:].reshape(-1)
+    unpad = ("unpad" not in DISABLED and _unpad["enabled"] and input_ids is not None
+             and inputs_embeds is None and position_ids is None and past_key_values is None
+             and isinstance(attention_mask, torch.Tensor) and attention_mask.dim() == 2
+             and tuple(attention_mask.shape) == (batch, seq)
+             and tuple(input_ids.shape) == (batch, seq)
+             and not getattr(self.model, "has_sliding_layers", True))
+    counts = None
+    if unpad:
+        try:
+            idx, positions, bounds, lengths, counts = unpad_batch(
+                attention_mask, shift.to(attention_mask.device))
+            if _unpad["checked"] < 3:
+                _unpad["checked"] += 1
+                if not is_right_padded(attention_mask, lengths):
+                    _unpad["enabled"] = False
+                    unpad = False
+        except Exception as exc:  # noqa: BLE001 - state.py convention
+            if not fallback("unpad", exc):
+                raise
+            unpad, counts = False, None
+    RAN["fused_head"] += 1
+    if unpad:
+        RAN["unpad"] += 1
+    else:
+        FELL_BACK["unpad"] += 1
+    link_next_norms(self.model)
+    n_labelled = None if counts is None else counts[0 if unpad else 1]
+    if unpad:
+        stage.append("unpadded")
+        shift = shift.to(idx.device)[idx]
+        with rows_context(bounds, device=input_ids.device):
+            outputs = self.model(input_ids=input_ids.reshape(-1)[idx][None],
+                                 attention_mask={"full_attention": None},
+                                 position_ids=positions, past_key_values=None,
+                                 inputs_embeds=None, use_cache=False, **kwargs)
+    else:
+        stage.append("padded")
+        outputs = self.model(input_ids=input_ids, attention_mask=attention_mask,
+                             position_ids=position_ids, past_key_values=past_key_values,
+                             inputs_embeds=inputs_embeds, use_cache=use_cache, **kwargs)
+    stage.append("head")
+    hidden = outputs.last_hidden_state
+    size = hidden.shape[-1]
+    shift = shift.to(hidden.device)
+    loss, token_loss, token_entropy, correct, argmax = fused_head_loss(
+        hidden.reshape(-1, size), self.lm_head.weight, shift, num_items, n_labelled=n_labelled,
+        return_argmax=True)
+    if unpad:
+        full_loss = token_loss.new_zeros(batch * seq)
+        full_entropy = token_entropy.new_zeros(batch * seq)
+        full_loss[idx] = token_loss
+        full_entropy[idx] = token_entropy
+        token_loss, token_entropy = full_loss, full_entropy
+    LAST_STEP.clear()
+    LAST_STEP.append(SimpleNamespace(
+        token_entropy=token_entropy.view(batch, seq), token_loss=token_loss.view(batch, seq),
+        correct=correct.sum(), labelled=(shift >= 0).sum(), argmax=argmax))
+    return output_cls(loss=loss, logits=None, past_key_values=None,
+                      hidden_states=outputs.hidden_states, attentions=outputs.attentions)
+
+
+def patch_qwen2_causal_lm():
+    """`Qwen2ForCausalLM.forward` through `_fused_forward` in training with labels; the original
+    forward otherwise (solution/patches.py:116-159)."""
+    import torch
+    from transformers.modeling_outputs import CausalLMOutputWithPast
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from .engaged import FELL_BACK
+
+    cls = modeling_qwen2.Qwen2ForCausalLM
+    if _in_chain(cls.forward, "_solution_fused_lm"):
+        return
+    original = ORIGINAL_FORWARD.setdefault(cls, cls.forward)
+
+    def forward(self, input_ids=None, attention_mask=None, position_ids=None,
+                past_key_values=None, inputs_embeds=None, labels=None, use_cache=None,
+                logits_to_keep=0, **kwargs):
+        if "fused_head" not in DISABLED \
+                and _fused_forward_applies(self, labels, logits_to_keep, kwargs):
+            device = self.lm_head.weight.device
+            rng_state = torch.cuda.get_rng_state(device)
+            stage = []
+            for _ in range(2):
+                try:
+                    return _fused_forward(self, input_ids, attention_mask, position_ids,
+                                          past_key_values, inputs_embeds, labels, use_cache,
+                                          dict(kwargs), CausalLMOutputWithPast, stage)
+                except Exception as exc:  # noqa: BLE001 - state.py convention
+                    component = "unpad" if stage[-1:] == ["unpadded"] else "fused_head"
+                    if not fallback(component, exc):
+                        raise
+                _restart(device, rng_state)
+                if "fused_head" in DISABLED:
+                    break
+        FELL_BACK["head"] += 1
+        return original(self, input_ids=input_ids, attention_mask=attention_mask,
+                        position_ids=position_ids, past_key_values=past_key_values,
+                        inputs_embeds=inputs_embeds, labels=labels, use_cache=use_cache,
+                        logits_to_keep=logits_to_keep, **kwargs)
+
+    forward._solution_fused_lm = True
+    forward._original = original
+    cls.forward = forward
+    ON.add("head")
 
 
 def apply():
@@ -70,4 +236,53 @@ def apply():
             from .qgroup import patch_group_dequant
 
             patch_group_dequant()
+        if not _off("LORA"):
+            with installing("lora"):
+                from .lora import patch_lora
+
+                patch_lora()
+        if not (_off("FUSED_PROJ") or _off("FUSED_QKV")):
+            with installing("fused_proj"):
+                from .fused_proj import patch_qwen2_attention
+
+                patch_qwen2_attention()
+    if not _off("FUSED_HEAD"):
+        with installing("fused_head"):
+            from .unpad import patch_sdpa_rows
+
+            patch_sdpa_rows()
+            patch_qwen2_causal_lm()
     return sorted(ON)
+
+
+def _root(fn):
+    seen = set()
+    while fn is not None and id(fn) not in seen:
+        seen.add(id(fn))
+        nxt = getattr(fn, "_previous", None) or getattr(fn, "_original", None)
+        if nxt is None:
+            return fn
+        fn = nxt
+    return fn
+
+
+def unapply():
+    """Restore every original method this package patched (for A/B runs in one process)."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from . import rmsnorm
+    from .lora import LoraLinear
+    from .nf4_linear import Linear4bit
+
+    for cls in (modeling_qwen2.Qwen2RMSNorm, modeling_qwen2.Qwen2DecoderLayer,
+                modeling_qwen2.Qwen2MLP, modeling_qwen2.Qwen2Attention,
+                modeling_qwen2.Qwen2ForCausalLM, Linear4bit, LoraLinear):
+        cls.forward = _root(cls.forward)
+    forward = modeling_qwen2.Qwen2Model.forward
+    if getattr(forward, "_solution_link_norms", False):
+        modeling_qwen2.Qwen2Model.forward = forward.__wrapped__
+    modeling_qwen2.apply_rotary_pos_emb = _root(modeling_qwen2.apply_rotary_pos_emb)
+    ALL_ATTENTION_FUNCTIONS["sdpa"] = _root(ALL_ATTENTION_FUNCTIONS["sdpa"])
+    rmsnorm.LAYER_FORWARDS.clear()
+    ON.clear()
