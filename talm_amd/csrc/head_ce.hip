@@ -37,7 +37,6 @@ constexpr int kBK = 32;              // reduction step: two 32x32x16 MFMAs deep
 constexpr int kWM = 4, kWN = 2;      // 32x32 MFMA blocks per wavefront (128 x 64)
 constexpr int kTile = 128;           // statistics granule (columns) == kBN
 constexpr int kZS = kBN + 8;         // LDS row stride (halfs) of the staged logits tile
-constexpr int kBS = kBN + 8;         // LDS row stride (halfs) of the [k][n] weight tile (GEMM2)
 constexpr int kXcds = 8;
 
 // Row-major [rows][kBK] fp16 tile as 16-byte chunks (4 per row), XOR-swizzled so that the 8
@@ -91,7 +90,8 @@ __device__ __forceinline__ Stat shfl_stat(Stat v, int off) {
 __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
     const uint16_t* __restrict__ H, int64_t ldh, const uint16_t* __restrict__ W, int64_t ldw,
     int n_rows, int K, int group_cols, int first_col, uint16_t* __restrict__ Z, int64_t ldz,
-    float4* __restrict__ part, int parts_per_row, int n_mtiles, int n_ntiles) {
+    float4* __restrict__ part, int parts_per_row, int n_mtiles, int n_ntiles,
+    const int64_t* __restrict__ targets, float* __restrict__ ztarget) {
   constexpr int kLdsMain = 2 * (kBM + kBN) * kBK * 2;   // double-buffered A and B tiles
   constexpr int kLdsEpi = kBM * kZS * 2;                 // staged logits tile
   constexpr int kLds = kLdsMain > kLdsEpi ? kLdsMain : kLdsEpi;
@@ -232,6 +232,9 @@ __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
       }
       part[static_cast<int64_t>(gr) * parts_per_row + ntile] =
           make_float4(m, s, t, __int_as_float(first_col + n0 + idx));
+      // the logit at the target, when the target column is in this tile (one tile per row)
+      const int64_t rel = targets[gr] - (first_col + n0);
+      if (rel >= 0 && rel < valid) ztarget[gr] = h2f(Zs[row * kZS + static_cast<int>(rel)]);
     }
   }
 
@@ -252,10 +255,12 @@ __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
 struct MergeArgs {
   const float4* part;
   int parts_per_row;
-  const uint16_t* Z;
+  uint16_t* Z;             // the group's logits; rows < n_grad become P = fp16(e^{z - m_c})
   int64_t ldz;
   const int64_t* targets;
+  const float* ztarget;    // [n_rows] the logit at the target (written by head_logits)
   int n_rows;
+  int n_grad;
   int n_slices;            // slices in this group
   int slice_cols[8];       // columns of each slice (the last may be narrower)
   int slice_col0[8];       // first vocabulary column of each slice
@@ -263,7 +268,6 @@ struct MergeArgs {
   int first_slice;         // this group holds the first slice of the vocabulary
   int last_slice;          // this group holds the last slice
   float* run;              // [6][n_rows]: m, s, t, best, zt, best_idx (as int bits)
-  float* mslice;           // [n_slices][n_rows]: running max after each slice
   float* alpha;            // [n_slices][n_rows]: e^{m_old - m} of each slice (0 for the first)
   float* token_loss;
   float* entropy;
@@ -310,10 +314,20 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
       bidx = acc.idx;
     }
     const int64_t rel = target - a.slice_col0[c];
-    if (labelled && rel >= 0 && rel < a.slice_cols[c])
-      zt = h2f(a.Z[static_cast<int64_t>(row) * a.ldz + (a.slice_col0[c] - a.slice_col0[0]) + rel]);
+    if (labelled && rel >= 0 && rel < a.slice_cols[c]) zt = a.ztarget[row];
+    if (row < a.n_grad) {
+      // the slice's logits of a labelled row become fp16(e^{z - m_c}) in place
+      // (solution/fused_head.py:178-182), the A operand of head_grad
+      uint16_t* zrow = a.Z + static_cast<int64_t>(row) * a.ldz + (a.slice_col0[c] - a.slice_col0[0]);
+      for (int e0 = lane * 8; e0 < a.slice_cols[c]; e0 += kWave * 8) {
+        uint4 v = *reinterpret_cast<const uint4*>(zrow + e0);
+        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = pack2(__expf(lo_f(w[q]) - m), __expf(hi_f(w[q]) - m));
+        *reinterpret_cast<uint4*>(zrow + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
     if (lane == 0) {
-      a.mslice[static_cast<int64_t>(c) * n + row] = m;
       a.alpha[static_cast<int64_t>(c) * n + row] =
           (a.first_slice && c == 0) || m_old == -INFINITY ? 0.f : __expf(m_old - m);
     }
@@ -340,7 +354,6 @@ struct GradArgs {
   int64_t ldz;
   const uint16_t* W;      // weight row of the group's first vocabulary column
   int64_t ldw;
-  const float* mslice;    // [n_slices][n_rows]
   int n_rows;
   int n_grad;
   int hidden;
@@ -352,10 +365,10 @@ struct GradArgs {
 
 __global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
   constexpr int kLdsA = 2 * kBM * kBK * 2;   // P tiles, swizzled chunks
-  constexpr int kLdsB = 2 * kBK * kBS * 2;   // weight tiles, [k][n] rows
+  constexpr int kLdsB = 2 * kBN * kBK * 2;   // weight tiles transposed to [n][k], swizzled chunks
   __shared__ __attribute__((aligned(16))) unsigned char smem[kLdsA + kLdsB];
   uint4* As = reinterpret_cast<uint4*>(smem);
-  uint16_t* Bs = reinterpret_cast<uint16_t*>(smem + kLdsA);
+  uint4* Bs = reinterpret_cast<uint4*>(smem + kLdsA);
 
   const uint32_t per_slice = static_cast<uint32_t>(a.n_mtiles * a.n_ntiles);
   const int slice = static_cast<int>(blockIdx.x / per_slice);
@@ -366,16 +379,10 @@ __global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
   const int cols = a.slice_cols[slice];
   const int zcol0 = slice * a.vchunk;  // slice's first column inside the group's logits
   const uint16_t* Wc = a.W + static_cast<int64_t>(zcol0) * a.ldw;
-  const float* mrow = a.mslice + static_cast<int64_t>(slice) * a.n_rows;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-
-  float rowmax[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int gr = m0 + ((tid + kThreads * r) >> 2);
-    rowmax[r] = gr < a.n_grad ? mrow[gr] : 0.f;
-  }
+  // B staging: thread = (k pair kp, 8-column group ng): rows k, k+1 of 8 weight columns
+  const int kp = tid & 15, ng = tid >> 4;
 
   uint4 ra[4], rb[2];
   auto load = [&](int k0) {
@@ -383,24 +390,24 @@ __global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
     for (int r = 0; r < 4; ++r) {
       const int c = tid + kThreads * r, row = c >> 2, kc = c & 3;
       const int gr = m0 + row, gk = k0 + kc * 8;
-      uint32_t out[4] = {0u, 0u, 0u, 0u};
+      uint4 v = make_uint4(0, 0, 0, 0);
       if (gr < a.n_grad && gk < cols) {
-        const uint4 z = *reinterpret_cast<const uint4*>(a.Z + static_cast<int64_t>(gr) * a.ldz + zcol0 + gk);
-        const uint32_t zw[4] = {z.x, z.y, z.z, z.w};
+        v = *reinterpret_cast<const uint4*>(a.Z + static_cast<int64_t>(gr) * a.ldz + zcol0 + gk);
+        if (gk + 8 > cols) {  // the last slice's tail: columns past `cols` hold no P
+          uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool ok0 = gk + 2 * e < cols, ok1 = gk + 2 * e + 1 < cols;
-          const float p0 = ok0 ? __expf(lo_f(zw[e]) - rowmax[r]) : 0.f;
-          const float p1 = ok1 ? __expf(hi_f(zw[e]) - rowmax[r]) : 0.f;
-          out[e] = pack2(p0, p1);
+          for (int e = 0; e < 4; ++e) {
+            if (gk + 2 * e >= cols) w[e] = 0u;
+            else if (gk + 2 * e + 1 >= cols) w[e] &= 0xffffu;
+          }
+          v = make_uint4(w[0], w[1], w[2], w[3]);
         }
       }
-      ra[r] = make_uint4(out[0], out[1], out[2], out[3]);
+      ra[r] = v;
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int c = tid + kThreads * r, k = c >> 4, nc = c & 15;
-      const int gk = k0 + k, gn = n0 + nc * 8;
+      const int gk = k0 + 2 * kp + r, gn = n0 + 8 * ng;
       rb[r] = (gk < cols && gn < a.hidden)
                   ? *reinterpret_cast<const uint4*>(Wc + static_cast<int64_t>(gk) * a.ldw + gn)
                   : make_uint4(0, 0, 0, 0);
@@ -412,10 +419,16 @@ __global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
       const int c = tid + kThreads * r;
       As[buf * kBM * 4 + swz(c >> 2, c & 3)] = ra[r];
     }
+    // transpose 2 (k) x 8 (n) into 8 rows of [n][k]: one 32-bit (k, k+1) pair per row
+    uint32_t* Bw = reinterpret_cast<uint32_t*>(Bs + buf * kBN * 4);
+    const uint32_t lo[4] = {rb[0].x, rb[0].y, rb[0].z, rb[0].w};
+    const uint32_t hi[4] = {rb[1].x, rb[1].y, rb[1].z, rb[1].w};
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int c = tid + kThreads * r, k = c >> 4, nc = c & 15;
-      *reinterpret_cast<uint4*>(Bs + buf * kBK * kBS + k * kBS + nc * 8) = rb[r];
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t even = (lo[q] & 0xffffu) | (hi[q] << 16);
+      const uint32_t odd = (lo[q] >> 16) | (hi[q] & 0xffff0000u);
+      Bw[swz(8 * ng + 2 * q, kp >> 2) * 4 + (kp & 3)] = even;
+      Bw[swz(8 * ng + 2 * q + 1, kp >> 2) * 4 + (kp & 3)] = odd;
     }
   };
 
@@ -445,10 +458,8 @@ __global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
       }
 #pragma unroll
       for (int j = 0; j < kWN; ++j) {
-        const uint16_t* col = Bs + buf * kBK * kBS + (ks * 16 + 8 * (lane >> 5)) * kBS +
-                              wn * 64 + j * 32 + (lane & 31);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bv[j][e] = __builtin_bit_cast(_Float16, col[e * kBS]);
+        const uint4 v = Bs[buf * kBN * 4 + swz(wn * 64 + j * 32 + (lane & 31), kc)];
+        bv[j] = __builtin_bit_cast(half8_t, v);
       }
 #pragma unroll
       for (int i = 0; i < kWM; ++i)
@@ -529,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Layout {
-  size_t z, part, run, mslice, alpha, y, acc, total;
+  size_t z, part, run, ztarget, alpha, y, acc, total;
   int64_t ldz;
   int parts_per_row;
 };
@@ -542,7 +553,7 @@ Layout layout(int64_t n_rows, int64_t hidden, int64_t vchunk, int64_t n_grad, in
   l.z = off;      off = align_up(off + static_cast<size_t>(n_rows) * l.ldz * 2, 256);
   l.part = off;   off = align_up(off + static_cast<size_t>(n_rows) * l.parts_per_row * 16, 256);
   l.run = off;    off = align_up(off + static_cast<size_t>(n_rows) * 6 * 4, 256);
-  l.mslice = off; off = align_up(off + static_cast<size_t>(group) * n_rows * 4, 256);
+  l.ztarget = off; off = align_up(off + static_cast<size_t>(n_rows) * 4, 256);
   l.alpha = off;  off = align_up(off + static_cast<size_t>(group) * n_rows * 4, 256);
   l.y = off;      off = align_up(off + static_cast<size_t>(group) * n_grad * hidden * 4, 256);
   l.acc = off;    off = align_up(off + static_cast<size_t>(n_grad) * hidden * 4, 256);
@@ -600,7 +611,7 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
   uint16_t* Z = reinterpret_cast<uint16_t*>(ws + l.z);
   float4* part = reinterpret_cast<float4*>(ws + l.part);
   float* run = reinterpret_cast<float*>(ws + l.run);
-  float* mslice = reinterpret_cast<float*>(ws + l.mslice);
+  float* ztarget = reinterpret_cast<float*>(ws + l.ztarget);
   float* alpha = reinterpret_cast<float*>(ws + l.alpha);
   float* Y = reinterpret_cast<float*>(ws + l.y);
   float* accbuf = reinterpret_cast<float*>(ws + l.acc);
@@ -616,10 +627,12 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
     hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>(mt * nt)), dim3(kThreads), 0, s,
                        hidden_states, ldh, weight + col0 * ldw, ldw, rows, static_cast<int>(hidden),
                        static_cast<int>(gcols), static_cast<int>(col0), Z, l.ldz, part,
-                       l.parts_per_row, mt, nt);
+                       l.parts_per_row, mt, nt, targets, ztarget);
     MergeArgs ma{};
     ma.part = part; ma.parts_per_row = l.parts_per_row; ma.Z = Z; ma.ldz = l.ldz;
-    ma.targets = targets; ma.n_rows = rows; ma.n_slices = ns; ma.vchunk = static_cast<int>(vchunk);
+    ma.targets = targets; ma.ztarget = ztarget; ma.n_rows = rows;
+    ma.n_grad = grad_hidden ? static_cast<int>(n_grad) : 0;
+    ma.n_slices = ns; ma.vchunk = static_cast<int>(vchunk);
     for (int c = 0; c < ns; ++c) {
       const int64_t c0 = col0 + c * vchunk;
       ma.slice_col0[c] = static_cast<int>(c0);
@@ -627,13 +640,13 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
     }
     ma.first_slice = s0 == 0;
     ma.last_slice = s0 + ns == slices;
-    ma.run = run; ma.mslice = mslice; ma.alpha = alpha;
+    ma.run = run; ma.alpha = alpha;
     ma.token_loss = token_loss; ma.entropy = entropy; ma.best_idx = best_idx; ma.correct = correct;
     hipLaunchKernelGGL(head_merge_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(kThreads),
                        0, s, ma);
     if (n_grad > 0 && grad_hidden) {
       GradArgs ga{};
-      ga.Z = Z; ga.ldz = l.ldz; ga.W = weight + col0 * ldw; ga.ldw = ldw; ga.mslice = mslice;
+      ga.Z = Z; ga.ldz = l.ldz; ga.W = weight + col0 * ldw; ga.ldw = ldw;
       ga.n_rows = rows; ga.n_grad = static_cast<int>(n_grad); ga.hidden = static_cast<int>(hidden);
       ga.vchunk = static_cast<int>(vchunk);
       for (int c = 0; c < ns; ++c) ga.slice_cols[c] = ma.slice_cols[c];

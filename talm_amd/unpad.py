@@ -3,9 +3,12 @@
 The causal-LM patch (patches.py) gathers the real tokens of a right-padded [B, T] batch into one
 flat sequence [1, N] with per-row positions, runs the decoder on it and scatters per-token
 outputs back. Attention must not cross rows: while the flat forward runs (`rows_context`), the
-registered "sdpa" attention interface runs causal attention per row (`rows_sdpa`), GQA heads
-shared by stride, not repeated. Attention itself is not one of this package's kernels (it is
-PyTorch's SDPA); its row bounds and `cu_seqlens` are the packing contract the other kernels use.
+registered "sdpa" attention interface runs causal attention that never crosses rows
+(`rows_sdpa`): all rows in one variable-length flash-attention launch per direction with the
+row offsets `cu_seqlens` and GQA heads shared, not repeated (`VarlenAttention`; the reference
+does the same with one memory-efficient launch per KV head, solution/unpad.py:199-294), else one
+SDPA call per row. Attention itself is not one of this package's kernels (it is PyTorch's);
+its `cu_seqlens` are the packing contract the other kernels use.
 """
 
 import contextlib
@@ -14,6 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from .engaged import FELL_BACK, ON, RAN
+from .state import DISABLED, fallback
 
 _rows = []
 _cu = []
@@ -22,11 +26,13 @@ _cu = []
 @contextlib.contextmanager
 def rows_context(bounds, device=None):
     """Row bounds [(start, end)] of the flat sequence for the attention of this forward; with
-    `device`, also cu_seqlens (int32) on it (solution/unpad.py:46-63)."""
+    `device`, also (cu_seqlens int32 on it, longest row, total tokens) (solution/unpad.py:46-63)."""
     cu = None
     if device is not None:
         ends = [e for s, e in bounds if e > s]
-        cu = torch.tensor([0] + ends, dtype=torch.int32, device=device)
+        if ends:
+            cu = (torch.tensor([0] + ends, dtype=torch.int32, device=device),
+                  max(e - s for s, e in bounds if e > s), ends[-1])
     _rows.append(bounds)
     _cu.append(cu)
     try:
@@ -70,6 +76,45 @@ def is_right_padded(attention_mask, lengths):
     return bool((attention_mask.bool() == prefix).all().item())
 
 
+class VarlenAttention(torch.autograd.Function):
+    """Causal attention of every row of the flat sequence in ONE launch each way: PyTorch's
+    variable-length flash attention with the row offsets `cu_seqlens` and the KV heads shared by
+    the query heads of their group (GQA, no repeated K/V). Inputs are the [1, H, N, D] views the
+    attention interface receives; the output is [1, N, Hq, D] as SDPA's transposed output is.
+    Bit-identical to per-row `scaled_dot_product_attention(..., is_causal=True)` on this
+    backend (the same kernel family, one launch instead of one per row)."""
+
+    @staticmethod
+    def forward(ctx, query, key, value, cu, max_len, scale):
+        q, k, v = (t[0].transpose(0, 1) for t in (query, key, value))  # [N, H, D] views
+        out, lse, rng, unused, _ = torch.ops.aten._flash_attention_forward(
+            q, k, v, cu, cu, max_len, max_len, 0.0, True, False, scale=scale)
+        ctx.save_for_backward(q, k, v, out, lse, rng, unused, cu)
+        ctx.max_len, ctx.scale = max_len, scale
+        return out[None]
+
+    @staticmethod
+    def backward(ctx, grad):
+        q, k, v, out, lse, rng, unused, cu = ctx.saved_tensors
+        g = grad[0]
+        if not g.is_contiguous():
+            g = g.contiguous()
+        dq, dk, dv = torch.ops.aten._flash_attention_backward(
+            g, q, k, v, out, lse, cu, cu, ctx.max_len, ctx.max_len, 0.0, True, rng, unused,
+            scale=ctx.scale)
+        return (dq.transpose(0, 1)[None], dk.transpose(0, 1)[None], dv.transpose(0, 1)[None],
+                None, None, None)
+
+
+def _varlen_applies(query, key, value, dropout, cu):
+    return (cu is not None and dropout == 0.0 and query.is_cuda and query.dim() == 4
+            and query.shape[0] == 1 and query.dtype in (torch.float16, torch.bfloat16)
+            and key.dtype == query.dtype and value.dtype == query.dtype
+            and key.shape == value.shape and query.shape[1] % key.shape[1] == 0
+            and query.shape[2] == key.shape[2] and query.shape[3] == key.shape[3]
+            and query.stride(-1) == 1 and key.stride(-1) == 1 and value.stride(-1) == 1)
+
+
 def _autocast_half(query):
     if query.dtype != torch.float32 or not query.is_cuda or not torch.is_autocast_enabled("cuda"):
         return None
@@ -97,6 +142,19 @@ def patch_sdpa_rows():
         half = _autocast_half(query)
         if half is not None:
             query, key, value = query.to(half), key.to(half), value.to(half)
+        cu = _cu[-1] if _cu else None
+        if "varlen_attention" not in DISABLED and cu is not None \
+                and _varlen_applies(query, key, value, dropout, cu[0]) \
+                and cu[2] == query.shape[2]:
+            try:
+                scale = scaling if scaling is not None else query.shape[-1] ** -0.5
+                out = VarlenAttention.apply(query, key, value, cu[0], cu[1], scale)
+            except Exception as exc:  # noqa: BLE001 - state.py convention
+                if not fallback("varlen_attention", exc):
+                    raise
+            else:
+                RAN["varlen_attn"] += 1
+                return out, None
         gqa = query.shape[1] != key.shape[1]
         outs = [F.scaled_dot_product_attention(query[:, :, s:e], key[:, :, s:e], value[:, :, s:e],
                                                dropout_p=dropout, is_causal=True, scale=scaling,

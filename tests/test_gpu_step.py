@@ -46,8 +46,43 @@ def test_patched_step_matches_eager_loss_curve(monkeypatch):
     assert engaged.RAN["fused_head"] == 0
     fused = _run(True, 6, monkeypatch)
     for name in ("fused_head", "unpad", "group", "fused_proj", "rope", "addnorm",
-                 "swiglu_inplace", "head", "rows_attn"):
+                 "swiglu_inplace", "head", "varlen_attn"):
         assert engaged.RAN[name] > 0, f"{name} did not run"
     assert abs(fused[0] - eager[0]) <= 1e-3 * abs(eager[0]), (fused[0], eager[0])
     for a, b in zip(fused, eager):
         assert abs(a - b) <= 5e-3 * abs(b), (fused, eager)
+
+
+def test_varlen_attention_matches_per_row_sdpa():
+    """The one-launch variable-length attention (unpad.VarlenAttention) against causal SDPA per
+    row with GQA (the reference's per-row semantics, solution/unpad.py:121-134) on the config-5
+    row lengths: outputs and q/k/v gradients to one fp16 rounding."""
+    import torch.nn.functional as F
+
+    from talm_amd import unpad, workloads
+
+    print("[case] varlen attention vs per-row sdpa", flush=True)
+    lengths, cu = workloads.varlen_lengths(1005)
+    n = int(cu[-1])
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(n, 2048, generator=g).half().cuda()
+    gout = torch.randn(1, n, 12, 128, generator=g).half().cuda()
+    bounds = [(int(cu[i]), int(cu[i + 1])) for i in range(len(lengths))]
+
+    def views(x):
+        return (x[:, :1536].view(1, n, 12, 128).transpose(1, 2),
+                x[:, 1536:1792].view(1, n, 2, 128).transpose(1, 2),
+                x[:, 1792:].view(1, n, 2, 128).transpose(1, 2))
+
+    x1 = qkv.clone().requires_grad_()
+    out1 = unpad.VarlenAttention.apply(*views(x1), cu.cuda(), int(lengths.max()), 128 ** -0.5)
+    out1.backward(gout)
+    x2 = qkv.clone().requires_grad_()
+    q, k, v = views(x2)
+    outs = [F.scaled_dot_product_attention(q[:, :, s:e], k[:, :, s:e], v[:, :, s:e],
+                                           is_causal=True, enable_gqa=True) for s, e in bounds]
+    out2 = torch.cat(outs, 2).transpose(1, 2)
+    out2.backward(gout)
+    for a, b in ((out1, out2), (x1.grad, x2.grad)):
+        torch.testing.assert_close(a.float(), b.float(), rtol=2 ** -10,
+                                   atol=2 ** -10 * float(b.abs().max()))
