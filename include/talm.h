@@ -122,6 +122,17 @@ int64_t talm_head_ce_workspace(int64_t n_rows, int64_t hidden, int64_t vocab, in
                                int64_t n_grad, int32_t group);
 
 /*
+ * The transposed head weight the gradient GEMM of talm_head_ce reads:
+ * weight_t[h][v] = weight[v][h] for v < vocab, 0 for vocab <= v < ldwt (row stride ldwt >= vocab,
+ * a multiple of 8). The reference has no counterpart: its accumulator GEMM hands cuBLAS the
+ * weight slice as is (solution/fused_head.py:178-182); here both GEMM operands are streamed
+ * k-contiguous, so the frozen weight's transpose is built once per weight version by the caller
+ * (talm_amd.fused_head keeps it) and reused by every call.
+ */
+int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t vocab, int64_t hidden,
+                       uint16_t* weight_t, int64_t ldwt, void* stream);
+
+/*
  * Fused LM head + cross-entropy over the vocabulary in slices of `vchunk` columns (a multiple of
  * 128), forward and gradient in one call; the [n_rows, vocab] logits never exist.
  * Replaces FusedHeadLossVocab.forward's slice loop with torch.mm, launch_vocab /
@@ -130,6 +141,8 @@ int64_t talm_head_ce_workspace(int64_t n_rows, int64_t hidden, int64_t vocab, in
  *   hidden_states f16 [n_rows, hidden] (row stride ldh), weight f16 [vocab, hidden] (row
  *   stride ldw), targets i64 [n_rows] (-100 = ignore). Rows [0, n_grad) must be exactly the
  *   labelled rows (the caller orders rows labelled-first, solution/fused_head.py:290-299).
+ *   weight_t: talm_head_weight_t of the same weight (row stride ldwt); required when the
+ *   gradient is requested (n_grad > 0 and grad_hidden not NULL), ignored otherwise.
  * Writes per row: token_loss f32 (log s + m - z_target, 0 unlabelled), entropy f32
  * (lse - t / s), best_idx i32 (first argmax of the fp16 logits), correct i32 (labelled and
  * best_idx == target); and, when grad_hidden is not NULL, grad_hidden f16 [n_rows, hidden]
@@ -138,10 +151,10 @@ int64_t talm_head_ce_workspace(int64_t n_rows, int64_t hidden, int64_t vocab, in
  * `workspace` (256-byte aligned) holds talm_head_ce_workspace(...) bytes.
  */
 int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* weight, int64_t ldw,
-                 const int64_t* targets, int64_t n_rows, int64_t hidden, int64_t vocab,
-                 int64_t vchunk, int64_t n_grad, int32_t group, float* token_loss,
-                 float* entropy, int32_t* best_idx, int32_t* correct, uint16_t* grad_hidden,
-                 void* workspace, int64_t workspace_bytes, void* stream);
+                 const uint16_t* weight_t, int64_t ldwt, const int64_t* targets, int64_t n_rows,
+                 int64_t hidden, int64_t vocab, int64_t vchunk, int64_t n_grad, int32_t group,
+                 float* token_loss, float* entropy, int32_t* best_idx, int32_t* correct,
+                 uint16_t* grad_hidden, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

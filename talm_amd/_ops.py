@@ -153,19 +153,40 @@ def head_ce_workspace_bytes(n_rows, hidden, vocab, vchunk, n_grad, group):
     return int(size)
 
 
-@_op("head_ce(Tensor hidden, Tensor weight, Tensor targets, int vchunk, int n_grad, int group, "
-     "Tensor(a!) token_loss, Tensor(b!) entropy, Tensor(c!) best_idx, Tensor(d!) correct, "
-     "Tensor(e!)? grad_hidden, Tensor(f!) workspace) -> ()")
-def head_ce(hidden, weight, targets, vchunk, n_grad, group, token_loss, entropy, best_idx,
-            correct, grad_hidden, workspace):
+@_op("head_weight_t(Tensor weight, Tensor(a!) weight_t) -> ()")
+def head_weight_t(weight, weight_t):
+    """weight fp16 [V, H] (unit column stride) -> weight_t fp16 [H, ldwt] (unit column stride,
+    ldwt >= V): the transpose, with columns [V, ldwt) zero."""
+    vocab, size = weight.shape
+    _fp16(weight, "weight")
+    _fp16(weight_t, "weight_t")
+    _require(weight.stride(1) == 1 and weight_t.stride(1) == 1 and weight_t.shape[0] == size
+             and weight_t.stride(0) >= vocab and weight_t.shape[1] >= vocab,
+             "head_weight_t: weight [V, H] and weight_t [H, >= V] with unit column stride")
+    lib = _lib.lib()
+    _lib.check(lib.talm_head_weight_t(weight.data_ptr(), weight.stride(0), vocab, size,
+                                      weight_t.data_ptr(), weight_t.stride(0), _stream(weight)),
+               "head_weight_t")
+
+
+@_op("head_ce(Tensor hidden, Tensor weight, Tensor? weight_t, Tensor targets, int vchunk, "
+     "int n_grad, int group, Tensor(a!) token_loss, Tensor(b!) entropy, Tensor(c!) best_idx, "
+     "Tensor(d!) correct, Tensor(e!)? grad_hidden, Tensor(f!) workspace) -> ()")
+def head_ce(hidden, weight, weight_t, targets, vchunk, n_grad, group, token_loss, entropy,
+            best_idx, correct, grad_hidden, workspace):
     """hidden fp16 [N, H] (unit column stride), weight fp16 [V, H] (unit column stride),
-    targets int64 [N] with rows [0, n_grad) exactly the labelled ones."""
+    weight_t its head_weight_t transpose (needed with the gradient), targets int64 [N] with rows
+    [0, n_grad) exactly the labelled ones."""
     n_rows, size = hidden.shape
     vocab = weight.shape[0]
     _fp16(hidden, "hidden")
     _fp16(weight, "weight")
     _require(hidden.stride(1) == 1 and weight.stride(1) == 1 and weight.shape[1] == size,
              "head_ce: hidden [N, H] and weight [V, H] with unit column stride")
+    if weight_t is not None:
+        _fp16(weight_t, "weight_t")
+        _require(weight_t.stride(1) == 1 and weight_t.shape[0] == size
+                 and weight_t.shape[1] >= vocab, "head_ce: weight_t [H, >= V], unit column stride")
     _require(targets.dtype == torch.int64 and targets.is_contiguous() and
              targets.numel() == n_rows, "head_ce: targets int64 [N]")
     for t, dt in ((token_loss, torch.float32), (entropy, torch.float32), (best_idx, torch.int32),
@@ -179,9 +200,10 @@ def head_ce(hidden, weight, targets, vchunk, n_grad, group, token_loss, entropy,
     _require(workspace.is_cuda and workspace.is_contiguous(), "head_ce: workspace")
     lib = _lib.lib()
     _lib.check(lib.talm_head_ce(hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
-                                weight.stride(0), targets.data_ptr(), n_rows, size, vocab,
-                                int(vchunk), int(n_grad), int(group), token_loss.data_ptr(),
-                                entropy.data_ptr(), best_idx.data_ptr(), correct.data_ptr(),
-                                _ptr(grad_hidden), workspace.data_ptr(),
+                                weight.stride(0), _ptr(weight_t),
+                                0 if weight_t is None else weight_t.stride(0), targets.data_ptr(),
+                                n_rows, size, vocab, int(vchunk), int(n_grad), int(group),
+                                token_loss.data_ptr(), entropy.data_ptr(), best_idx.data_ptr(),
+                                correct.data_ptr(), _ptr(grad_hidden), workspace.data_ptr(),
                                 workspace.numel() * workspace.element_size(), _stream(hidden)),
                "head_ce")

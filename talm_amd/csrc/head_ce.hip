@@ -7,21 +7,26 @@
 // with m the running maximum after slice c; at the end dH = acc / s - W[target].
 //
 // The same recurrence here, shaped for MI355X. Slices are processed `group` at a time:
-//   head_logits   Z = H W^T over the group's columns (v_mfma_f32_32x32x16_f16, 256x128 tiles,
-//                 LDS double buffer, XOR-swizzled 16-byte chunks); the epilogue rounds to fp16,
-//                 stages the tile in LDS, writes it to the group's logits buffer and emits, per
-//                 (row, 128-column tile), the tile's max, first argmax, sum e^{z-max} and
+//   head_logits   Z = H W^T over the group's columns; the epilogue rounds to fp16, stages the
+//                 tile in LDS, writes it to the group's logits buffer and emits, per (row,
+//                 128-column tile), the tile's max, first argmax, sum e^{z-max} and
 //                 sum e^{z-max} z.
 //   head_merge    one wavefront per row folds the tiles of each slice, in column order, into the
 //                 running statistics exactly as the reference's per-slice update, recording the
-//                 slice's running max m_c and rescale e^{m_old - m_c}; after the last slice it
-//                 writes token loss, entropy, argmax and correctness.
-//   head_grad     Y_c = P_c W_c with P_c = fp16(e^{z - m_c}) formed while the logits tile is
-//                 staged into LDS (never stored); one workgroup per (slice, 256-row, 128-col)
-//                 tile, so the small [n_lab, H] output of each slice still fills the chip.
+//                 slice's running max m_c and rescale e^{m_old - m_c}; labelled rows' logits
+//                 become P = fp16(e^{z - m_c}) in place; after the last slice it writes token
+//                 loss, entropy, argmax and correctness.
+//   head_grad     Y_c = P_c W_c for every slice of the group side by side, against the
+//                 transposed weight W^T [hidden, vocab] so that both operands are k-contiguous.
 //   head_combine  acc = e^{m_old - m_c} acc + Y_c in slice order (the reference's rescale then
 //                 add), and after the last slice dH = acc / s - W16[target] in fp16.
 // The full [N, V] logits never exist: one group of slices (group * vchunk columns) at a time.
+//
+// Both GEMMs run the same tile core: 256 x 128 output tiles, four wavefronts of 128 x 64
+// (v_mfma_f32_32x32x16_f16), operands streamed by buffer_load_dwordx4 ... lds straight into a
+// three-stage LDS ring (two steps of 32 in flight while the third is multiplied), 16-byte chunks
+// XOR-swizzled so that fragment reads are free of bank conflicts, tiles mapped to XCDs so the
+// tiles that share an operand panel share an L2. Two workgroups per CU.
 #include "common.h"
 
 namespace talm {
@@ -29,25 +34,149 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int kThreads = 256;        // 4 wavefronts, 2 x 2 over the tile
-constexpr int kBM = 256;             // tile rows (hidden-state rows)
+constexpr int kBM = 256;             // tile rows
 constexpr int kBN = 128;             // tile columns
 constexpr int kBK = 32;              // reduction step: two 32x32x16 MFMAs deep
 constexpr int kWM = 4, kWN = 2;      // 32x32 MFMA blocks per wavefront (128 x 64)
+constexpr int kStages = 3;           // LDS ring depth
+constexpr int kAChunks = kBM * kBK / 8;                    // 16-byte chunks per A stage
+constexpr int kBChunks = kBN * kBK / 8;                    // 16-byte chunks per B stage
+constexpr int kStageBytes = (kAChunks + kBChunks) * 16;    // 24 KiB
+constexpr int kLdsMain = kStages * kStageBytes;            // 72 KiB
 constexpr int kTile = 128;           // statistics granule (columns) == kBN
 constexpr int kZS = kBN + 8;         // LDS row stride (halfs) of the staged logits tile
 constexpr int kXcds = 8;
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every range: the load returns 0
 
-// Row-major [rows][kBK] fp16 tile as 16-byte chunks (4 per row), XOR-swizzled so that the 8
-// lanes of a ds_read_b128 phase (8 consecutive rows, one chunk column) hit 8 distinct bank groups.
-__device__ __forceinline__ int swz(int row, int kc) { return row * 4 + (kc ^ ((row >> 1) & 3)); }
+static_assert(kBM * kZS * 2 <= kLdsMain, "the staged logits tile reuses the LDS ring");
 
+// [rows][kBK] fp16 tile as 16-byte chunks (4 per row). The chunk column is XOR-ed with
+// ((row >> 1) ^ (row >> 2)) & 3: the rows read by one ds_read_b128 phase (8 consecutive rows on
+// 32 banks, 16 on 64 banks, one chunk column) then land on distinct banks.
+__device__ __forceinline__ int swz_key(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+__device__ __forceinline__ int swz(int row, int kc) { return row * 4 + (kc ^ swz_key(row)); }
+
+// Wait until at most N vector-memory operations of this wavefront are outstanding (vmcnt only).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that orders LDS accesses only: the LDS reads issued before it have returned
+// (lgkmcnt 0), and the compiler moves no memory access across it. Unlike __syncthreads() it does
+// not drain the wavefront's outstanding buffer ... lds transfers, which the ring keeps in flight
+// and waits for with wait_vmcnt.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on XCD b % 8). Give
+// each XCD one contiguous range of tile indices (a bijection for any tile count), so tiles that
+// are neighbours in the caller's order share that XCD's L2.
 __device__ __forceinline__ uint32_t xcd_tile(uint32_t bid, uint32_t n_tiles) {
-  // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a contiguous range of
-  // tiles (tiles that share weight columns share that XCD's L2).
-  if (n_tiles % kXcds) return bid;
-  return (bid % kXcds) * (n_tiles / kXcds) + bid / kXcds;
+  const uint32_t x = bid % kXcds, i = bid / kXcds;
+  const uint32_t q = n_tiles / kXcds, r = n_tiles % kXcds;
+  return x * q + min(x, r) + i;
+}
+
+// One operand of the tile core: kRows rows of fp16 with k contiguous, from `base` (the tile's
+// first row, k = 0) with row stride `ld` halfs. Each step, every wavefront moves its 1 KiB blocks
+// (16 rows x 4 chunks) of the stage with buffer_load_dwordx4 ... lds: lane l fills the block's
+// l-th chunk, so the lane loads the global chunk that the swizzle puts there. Chunks of rows past
+// `rows_valid`, or starting at k >= `k_valid`, get an out-of-range offset and read as zeros.
+template <int kRows>
+struct Loader {
+  static constexpr int kPer = kRows * kBK / 8 / kThreads;  // DMA instructions per thread per step
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[kPer];
+  int kc8[kPer];
+  int k_valid;
+
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int rows_valid,
+                                       int k_valid_, int wave, int lane) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, 0x7fffffff,
+                                             0x00020000);
+    k_valid = k_valid_;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int row = 16 * (p * 4 + wave) + (lane >> 2);
+      const int kc = (lane & 3) ^ swz_key(row);
+      kc8[p] = kc * 8;
+      off[p] = row < rows_valid ? static_cast<uint32_t>((row * ld + kc * 8) * 2) : kOob;
+    }
+  }
+  // operands of step k0 into the stage block at `dst`
+  __device__ __forceinline__ void issue(unsigned char* dst, int k0, int wave) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const uint32_t v = k0 + kc8[p] < k_valid ? off[p] + static_cast<uint32_t>(k0 * 2) : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (lds_ptr_t)(dst + (p * 4 + wave) * 1024), 16, v, 0, 0, 0);
+    }
+  }
+};
+
+// One 32-deep step of the wavefront's 128 x 64 block: 2 x (4 A + 2 B fragments, 8 MFMAs).
+__device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uint4* __restrict__ Bs,
+                                         f32x16 (&acc)[kWM][kWN], int lane, int wm, int wn) {
+  half8_t a[2][kWM], b[2][kWN];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int kc = ks * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < kWM; ++i)
+      a[ks][i] = __builtin_bit_cast(half8_t, As[swz(wm * 128 + i * 32 + (lane & 31), kc)]);
+#pragma unroll
+    for (int j = 0; j < kWN; ++j)
+      b[ks][j] = __builtin_bit_cast(half8_t, Bs[swz(wn * 64 + j * 32 + (lane & 31), kc)]);
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < kWM; ++i)
+#pragma unroll
+      for (int j = 0; j < kWN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+}
+
+// acc = A B^T over nk steps of 32: A is the 256-row operand, B the 128-row one. Step kt waits for
+// its own DMA group (the next one stays in flight), one barrier makes every wavefront's data
+// visible and retires the stage read in step kt - 1, which then receives step kt + 2.
+__device__ __forceinline__ void tile_gemm(Loader<kBM>& la, Loader<kBN>& lb, unsigned char* smem,
+                                          int nk, f32x16 (&acc)[kWM][kWN], int lane, int wave) {
+  constexpr int kGroup = Loader<kBM>::kPer + Loader<kBN>::kPer;
+  const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+  for (int i = 0; i < kWM; ++i)
+#pragma unroll
+    for (int j = 0; j < kWN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  la.issue(smem, 0, wave);
+  lb.issue(smem + kAChunks * 16, 0, wave);
+  if (nk > 1) {
+    la.issue(smem + kStageBytes, kBK, wave);
+    lb.issue(smem + kStageBytes + kAChunks * 16, kBK, wave);
+  }
+  int s = 0;  // stage of step kt
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) wait_vmcnt<kGroup>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (kt + 2 < nk) {
+      unsigned char* st = smem + (s == 0 ? 2 : s - 1) * kStageBytes;  // stage (kt + 2) % 3
+      la.issue(st, (kt + 2) * kBK, wave);
+      lb.issue(st + kAChunks * 16, (kt + 2) * kBK, wave);
+    }
+    const uint4* As = reinterpret_cast<const uint4*>(smem + s * kStageBytes);
+    mma_step(As, As + kAChunks, acc, lane, wm, wn);
+    s = s == 2 ? 0 : s + 1;
+  }
+  __syncthreads();  // every wavefront is done with the ring before the caller reuses the LDS
 }
 
 struct Stat {
@@ -84,99 +213,31 @@ __device__ __forceinline__ Stat shfl_stat(Stat v, int off) {
 }
 
 // ------------------------------------------------------------------------------------------
-// GEMM1: Z[r][j] = fp16(sum_k H[r][k] W[col0 + j][k]) for the group's columns j < group_cols,
-// plus the per-(row, 128-column tile) partial statistics.
+// GEMM1: Z[r][j] = fp16(sum_k H[r][k] W[j][k]) for the group's columns j < group_cols (W starts
+// at the group's first vocabulary row), plus the per-(row, 128-column tile) partial statistics.
 // ------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
     const uint16_t* __restrict__ H, int64_t ldh, const uint16_t* __restrict__ W, int64_t ldw,
     int n_rows, int K, int group_cols, int first_col, uint16_t* __restrict__ Z, int64_t ldz,
     float4* __restrict__ part, int parts_per_row, int n_mtiles, int n_ntiles,
     const int64_t* __restrict__ targets, float* __restrict__ ztarget) {
-  constexpr int kLdsMain = 2 * (kBM + kBN) * kBK * 2;   // double-buffered A and B tiles
-  constexpr int kLdsEpi = kBM * kZS * 2;                 // staged logits tile
-  constexpr int kLds = kLdsMain > kLdsEpi ? kLdsMain : kLdsEpi;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kLds];
-  uint4* As = reinterpret_cast<uint4*>(smem);            // [2][kBM * 4] chunks
-  uint4* Bs = As + 2 * kBM * 4;                          // [2][kBN * 4] chunks
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kLdsMain];
 
+  // row tiles vary fastest inside an XCD's range: the tiles in flight on one XCD share weight rows
   const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(n_mtiles * n_ntiles));
   const int ntile = static_cast<int>(tile / n_mtiles);
   const int mtile = static_cast<int>(tile % n_mtiles);
   const int m0 = mtile * kBM, n0 = ntile * kBN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Global -> register staging: A 256 rows x 4 chunks (4 per thread), B 128 x 4 (2 per thread).
-  uint4 ra[4], rb[2];
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + kThreads * r, row = c >> 2, kc = c & 3;
-      const int gr = m0 + row, gk = k0 + kc * 8;
-      ra[r] = (gr < n_rows && gk < K)
-                  ? *reinterpret_cast<const uint4*>(H + static_cast<int64_t>(gr) * ldh + gk)
-                  : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int c = tid + kThreads * r, row = c >> 2, kc = c & 3;
-      const int gc = n0 + row, gk = k0 + kc * 8;
-      rb[r] = (gc < group_cols && gk < K)
-                  ? *reinterpret_cast<const uint4*>(W + static_cast<int64_t>(gc) * ldw + gk)
-                  : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + kThreads * r;
-      As[buf * kBM * 4 + swz(c >> 2, c & 3)] = ra[r];
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int c = tid + kThreads * r;
-      Bs[buf * kBN * 4 + swz(c >> 2, c & 3)] = rb[r];
-    }
-  };
-
+  Loader<kBM> la;
+  Loader<kBN> lb;
+  la.init(H + static_cast<int64_t>(m0) * ldh, ldh, n_rows - m0, K, wave, lane);
+  lb.init(W + static_cast<int64_t>(n0) * ldw, ldw, group_cols - n0, K, wave, lane);
   f32x16 acc[kWM][kWN];
-#pragma unroll
-  for (int i = 0; i < kWM; ++i)
-#pragma unroll
-    for (int j = 0; j < kWN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  const int nk = (K + kBK - 1) / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load((kt + 1) * kBK);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int kc = ks * 2 + (lane >> 5);
-      half8_t a[kWM], b[kWN];
-#pragma unroll
-      for (int i = 0; i < kWM; ++i) {
-        const uint4 v = As[buf * kBM * 4 + swz(wm * 128 + i * 32 + (lane & 31), kc)];
-        a[i] = __builtin_bit_cast(half8_t, v);
-      }
-#pragma unroll
-      for (int j = 0; j < kWN; ++j) {
-        const uint4 v = Bs[buf * kBN * 4 + swz(wn * 64 + j * 32 + (lane & 31), kc)];
-        b[j] = __builtin_bit_cast(half8_t, v);
-      }
-#pragma unroll
-      for (int i = 0; i < kWM; ++i)
-#pragma unroll
-        for (int j = 0; j < kWN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) store(buf ^ 1);
-    __syncthreads();
-  }
+  tile_gemm(la, lb, smem, (K + kBK - 1) / kBK, acc, lane, wave);
 
   // Epilogue 1: fp16 logits tile into LDS ([kBM][kZS] halfs).
   uint16_t* Zs = reinterpret_cast<uint16_t*>(smem);
@@ -317,13 +378,19 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
     if (labelled && rel >= 0 && rel < a.slice_cols[c]) zt = a.ztarget[row];
     if (row < a.n_grad) {
       // the slice's logits of a labelled row become fp16(e^{z - m_c}) in place
-      // (solution/fused_head.py:178-182), the A operand of head_grad
+      // (solution/fused_head.py:178-182), the A operand of head_grad; in the chunk that holds
+      // the vocabulary's last column, the columns past it become 0 (head_grad reads whole chunks)
       uint16_t* zrow = a.Z + static_cast<int64_t>(row) * a.ldz + (a.slice_col0[c] - a.slice_col0[0]);
-      for (int e0 = lane * 8; e0 < a.slice_cols[c]; e0 += kWave * 8) {
+      const int cols = a.slice_cols[c];
+      for (int e0 = lane * 8; e0 < cols; e0 += kWave * 8) {
         uint4 v = *reinterpret_cast<const uint4*>(zrow + e0);
         uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) w[q] = pack2(__expf(lo_f(w[q]) - m), __expf(hi_f(w[q]) - m));
+        for (int q = 0; q < 4; ++q) {
+          const float p0 = e0 + 2 * q < cols ? __expf(lo_f(w[q]) - m) : 0.f;
+          const float p1 = e0 + 2 * q + 1 < cols ? __expf(hi_f(w[q]) - m) : 0.f;
+          w[q] = pack2(p0, p1);
+        }
         *reinterpret_cast<uint4*>(zrow + e0) = make_uint4(w[0], w[1], w[2], w[3]);
       }
     }
@@ -346,130 +413,46 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// GEMM2: Y_c[r][h] = sum_j fp16(e^{Z[r][j] - m_c[r]}) W[col0_c + j][h] over slice c's columns,
-// for the first n_grad rows (the labelled rows, put first by the caller).
+// GEMM2: Y_c[r][h] = sum_j P[r][zc + j] W^T[h][col0 + zc + j] over slice c's columns (zc = c *
+// vchunk inside the group), for the first n_grad rows (the labelled rows, put first by the
+// caller); P = fp16(e^{z - m_c}) is what head_merge left in the logits buffer.
 // ------------------------------------------------------------------------------------------
 struct GradArgs {
   const uint16_t* Z;
   int64_t ldz;
-  const uint16_t* W;      // weight row of the group's first vocabulary column
-  int64_t ldw;
-  int n_rows;
+  const uint16_t* WT;     // transposed weight [hidden][ldwt], columns past the vocabulary zero
+  int64_t ldwt;
+  int col0;               // the group's first vocabulary column
   int n_grad;
   int hidden;
   int vchunk;
   int slice_cols[8];
   float* Y;               // [n_slices][n_grad][hidden] fp32
-  int n_mtiles, n_ntiles;
+  int n_mtiles, n_ntiles, n_tiles;
 };
 
 __global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
-  constexpr int kLdsA = 2 * kBM * kBK * 2;   // P tiles, swizzled chunks
-  constexpr int kLdsB = 2 * kBN * kBK * 2;   // weight tiles transposed to [n][k], swizzled chunks
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kLdsA + kLdsB];
-  uint4* As = reinterpret_cast<uint4*>(smem);
-  uint4* Bs = reinterpret_cast<uint4*>(smem + kLdsA);
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kLdsMain];
 
-  const uint32_t per_slice = static_cast<uint32_t>(a.n_mtiles * a.n_ntiles);
-  const int slice = static_cast<int>(blockIdx.x / per_slice);
-  const uint32_t tile = xcd_tile(blockIdx.x % per_slice, per_slice);
-  const int ntile = static_cast<int>(tile / a.n_mtiles);
-  const int mtile = static_cast<int>(tile % a.n_mtiles);
+  // hidden tiles vary fastest inside an XCD's range: the tiles in flight on one XCD share P rows
+  const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_tiles));
+  const int ntile = static_cast<int>(tile % a.n_ntiles);
+  const int rest = static_cast<int>(tile / a.n_ntiles);
+  const int mtile = rest % a.n_mtiles, slice = rest / a.n_mtiles;
   const int m0 = mtile * kBM, n0 = ntile * kBN;
   const int cols = a.slice_cols[slice];
-  const int zcol0 = slice * a.vchunk;  // slice's first column inside the group's logits
-  const uint16_t* Wc = a.W + static_cast<int64_t>(zcol0) * a.ldw;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int zc = slice * a.vchunk;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  // B staging: thread = (k pair kp, 8-column group ng): rows k, k+1 of 8 weight columns
-  const int kp = tid & 15, ng = tid >> 4;
 
-  uint4 ra[4], rb[2];
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + kThreads * r, row = c >> 2, kc = c & 3;
-      const int gr = m0 + row, gk = k0 + kc * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (gr < a.n_grad && gk < cols) {
-        v = *reinterpret_cast<const uint4*>(a.Z + static_cast<int64_t>(gr) * a.ldz + zcol0 + gk);
-        if (gk + 8 > cols) {  // the last slice's tail: columns past `cols` hold no P
-          uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (gk + 2 * e >= cols) w[e] = 0u;
-            else if (gk + 2 * e + 1 >= cols) w[e] &= 0xffffu;
-          }
-          v = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-      }
-      ra[r] = v;
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int gk = k0 + 2 * kp + r, gn = n0 + 8 * ng;
-      rb[r] = (gk < cols && gn < a.hidden)
-                  ? *reinterpret_cast<const uint4*>(Wc + static_cast<int64_t>(gk) * a.ldw + gn)
-                  : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int c = tid + kThreads * r;
-      As[buf * kBM * 4 + swz(c >> 2, c & 3)] = ra[r];
-    }
-    // transpose 2 (k) x 8 (n) into 8 rows of [n][k]: one 32-bit (k, k+1) pair per row
-    uint32_t* Bw = reinterpret_cast<uint32_t*>(Bs + buf * kBN * 4);
-    const uint32_t lo[4] = {rb[0].x, rb[0].y, rb[0].z, rb[0].w};
-    const uint32_t hi[4] = {rb[1].x, rb[1].y, rb[1].z, rb[1].w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t even = (lo[q] & 0xffffu) | (hi[q] << 16);
-      const uint32_t odd = (lo[q] >> 16) | (hi[q] & 0xffff0000u);
-      Bw[swz(8 * ng + 2 * q, kp >> 2) * 4 + (kp & 3)] = even;
-      Bw[swz(8 * ng + 2 * q + 1, kp >> 2) * 4 + (kp & 3)] = odd;
-    }
-  };
-
+  Loader<kBM> la;
+  Loader<kBN> lb;
+  la.init(a.Z + static_cast<int64_t>(m0) * a.ldz + zc, a.ldz, a.n_grad - m0, cols, wave, lane);
+  lb.init(a.WT + static_cast<int64_t>(n0) * a.ldwt + a.col0 + zc, a.ldwt, a.hidden - n0, cols,
+          wave, lane);
   f32x16 acc[kWM][kWN];
-#pragma unroll
-  for (int i = 0; i < kWM; ++i)
-#pragma unroll
-    for (int j = 0; j < kWN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  const int nk = (cols + kBK - 1) / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load((kt + 1) * kBK);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int kc = ks * 2 + (lane >> 5);
-      half8_t av[kWM], bv[kWN];
-#pragma unroll
-      for (int i = 0; i < kWM; ++i) {
-        const uint4 v = As[buf * kBM * 4 + swz(wm * 128 + i * 32 + (lane & 31), kc)];
-        av[i] = __builtin_bit_cast(half8_t, v);
-      }
-#pragma unroll
-      for (int j = 0; j < kWN; ++j) {
-        const uint4 v = Bs[buf * kBN * 4 + swz(wn * 64 + j * 32 + (lane & 31), kc)];
-        bv[j] = __builtin_bit_cast(half8_t, v);
-      }
-#pragma unroll
-      for (int i = 0; i < kWM; ++i)
-#pragma unroll
-        for (int j = 0; j < kWN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) store(buf ^ 1);
-    __syncthreads();
-  }
+  tile_gemm(la, lb, smem, (cols + kBK - 1) / kBK, acc, lane, wave);
 
   float* Y = a.Y + static_cast<int64_t>(slice) * a.n_grad * a.hidden;
 #pragma unroll
@@ -537,6 +520,44 @@ __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
   *reinterpret_cast<uint2*>(a.grad + at) = make_uint2(pack2(g0, g1), pack2(g2, g3));
 }
 
+// ------------------------------------------------------------------------------------------
+// WT[h][v] = W[v][h] for v < vocab, 0 for vocab <= v < ldwt: the k-contiguous B operand of
+// head_grad. 64 x 64 blocks through LDS, 16-byte loads and stores.
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void weight_t_kernel(const uint16_t* __restrict__ W,
+                                                            int64_t ldw, int vocab, int hidden,
+                                                            uint16_t* __restrict__ WT,
+                                                            int64_t ldwt) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int v0 = blockIdx.x * 64, h0 = blockIdx.y * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {  // 64 vocabulary rows x 8 chunks of 8 hidden columns
+    const int c = it * kThreads + tid, r = c >> 3, hc = (c & 7) * 8;
+    const int v = v0 + r, h = h0 + hc;
+    uint4 x = make_uint4(0, 0, 0, 0);
+    if (v < vocab && h < hidden) x = *reinterpret_cast<const uint4*>(W + static_cast<int64_t>(v) * ldw + h);
+    const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[hc + 2 * e][r] = static_cast<uint16_t>(w4[e] & 0xffffu);
+      tile[hc + 2 * e + 1][r] = static_cast<uint16_t>(w4[e] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {  // 64 hidden rows x 8 chunks of 8 vocabulary columns
+    const int c = it * kThreads + tid, r = c >> 3, vc = (c & 7) * 8;
+    const int h = h0 + r, v = v0 + vc;
+    if (h >= hidden || v >= ldwt) continue;
+    uint32_t w4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w4[e] = static_cast<uint32_t>(tile[r][vc + 2 * e]) | (static_cast<uint32_t>(tile[r][vc + 2 * e + 1]) << 16);
+    *reinterpret_cast<uint4*>(WT + static_cast<int64_t>(h) * ldwt + v) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  }
+}
+
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Layout {
@@ -576,8 +597,26 @@ TALM_API int64_t talm_head_ce_workspace(int64_t n_rows, int64_t hidden, int64_t 
   return static_cast<int64_t>(layout(n_rows, hidden, vchunk, n_grad, g).total);
 }
 
+TALM_API int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t vocab,
+                                int64_t hidden, uint16_t* weight_t, int64_t ldwt, void* stream) {
+  if (vocab < 1 || hidden < 8 || hidden % 8 || ldw < hidden || ldw % 8 || ldwt < vocab ||
+      ldwt % 8 || vocab > (1 << 30) || hidden > (1 << 20))
+    return fail(TALM_EINVAL,
+                "head_weight_t: bad shape (vocab %lld, hidden %lld, ldw %lld, ldwt %lld): hidden "
+                "and both strides multiples of 8, ldw >= hidden, ldwt >= vocab",
+                (long long)vocab, (long long)hidden, (long long)ldw, (long long)ldwt);
+  if (!weight || !weight_t) return fail(TALM_EINVAL, "head_weight_t: null pointer");
+  if (!aligned(weight, 16) || !aligned(weight_t, 16))
+    return fail(TALM_EINVAL, "head_weight_t: weight and weight_t must be 16-byte aligned");
+  const dim3 grid(static_cast<unsigned>((ldwt + 63) / 64), static_cast<unsigned>((hidden + 63) / 64));
+  hipLaunchKernelGGL(weight_t_kernel, grid, dim3(kThreads), 0, as_stream(stream), weight, ldw,
+                     static_cast<int>(vocab), static_cast<int>(hidden), weight_t, ldwt);
+  return check_launch("head_weight_t");
+}
+
 TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* weight,
-                          int64_t ldw, const int64_t* targets, int64_t n_rows, int64_t hidden,
+                          int64_t ldw, const uint16_t* weight_t, int64_t ldwt,
+                          const int64_t* targets, int64_t n_rows, int64_t hidden,
                           int64_t vocab, int64_t vchunk, int64_t n_grad, int32_t group,
                           float* token_loss, float* entropy, int32_t* best_idx, int32_t* correct,
                           uint16_t* grad_hidden, void* workspace, int64_t workspace_bytes,
@@ -591,19 +630,27 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
                 "a multiple of %d, 1 <= group <= 8",
                 (long long)n_rows, (long long)hidden, (long long)vocab, (long long)vchunk,
                 (long long)n_grad, group, (long long)ldh, (long long)ldw, kTile);
-  if (n_rows > (1 << 30) || vocab > (1 << 30) || hidden > (1 << 20))
-    return fail(TALM_EINVAL, "head_ce: sizes beyond 32-bit indexing");
+  if (n_rows > (1 << 30) || vocab > (1 << 30) || hidden > (1 << 20) || ldh >= (1 << 22) ||
+      ldw >= (1 << 22))
+    return fail(TALM_EINVAL, "head_ce: sizes beyond 32-bit indexing (row strides below 2^22)");
+  const bool with_grad = n_grad > 0 && grad_hidden;
+  if (with_grad && (ldwt < vocab || ldwt % 8 || ldwt >= (1 << 22)))
+    return fail(TALM_EINVAL, "head_ce: weight_t row stride %lld: at least vocab (%lld), a "
+                             "multiple of 8", (long long)ldwt, (long long)vocab);
   if (n_rows == 0) return ok();
   if (!hidden_states || !weight || !targets || !token_loss || !entropy || !best_idx || !correct ||
-      !workspace || (n_grad > 0 && !grad_hidden))
+      !workspace || (n_grad > 0 && !grad_hidden) || (with_grad && !weight_t))
     return fail(TALM_EINVAL, "head_ce: null pointer");
   if (!aligned(hidden_states, 16) || !aligned(weight, 16) || !aligned(workspace, 256) ||
-      (grad_hidden && !aligned(grad_hidden, 16)))
-    return fail(TALM_EINVAL, "head_ce: hidden states, weight and dH must be 16-byte aligned, the "
-                             "workspace 256-byte aligned");
+      (grad_hidden && !aligned(grad_hidden, 16)) || (with_grad && !aligned(weight_t, 16)))
+    return fail(TALM_EINVAL, "head_ce: hidden states, weight, weight_t and dH must be 16-byte "
+                             "aligned, the workspace 256-byte aligned");
   const int64_t slices = (vocab + vchunk - 1) / vchunk;
   const int g = static_cast<int>(slices < group ? slices : group);
   const Layout l = layout(n_rows, hidden, vchunk, n_grad, g);
+  if (l.ldz >= (1 << 22))
+    return fail(TALM_EINVAL, "head_ce: group * vchunk = %lld columns per step, below 2^22 needed",
+                (long long)l.ldz);
   if (workspace_bytes < static_cast<int64_t>(l.total))
     return fail(TALM_EINVAL, "head_ce: workspace of %lld bytes, %zu needed",
                 (long long)workspace_bytes, l.total);
@@ -646,15 +693,16 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
                        0, s, ma);
     if (n_grad > 0 && grad_hidden) {
       GradArgs ga{};
-      ga.Z = Z; ga.ldz = l.ldz; ga.W = weight + col0 * ldw; ga.ldw = ldw;
-      ga.n_rows = rows; ga.n_grad = static_cast<int>(n_grad); ga.hidden = static_cast<int>(hidden);
+      ga.Z = Z; ga.ldz = l.ldz; ga.WT = weight_t; ga.ldwt = ldwt; ga.col0 = static_cast<int>(col0);
+      ga.n_grad = static_cast<int>(n_grad); ga.hidden = static_cast<int>(hidden);
       ga.vchunk = static_cast<int>(vchunk);
       for (int c = 0; c < ns; ++c) ga.slice_cols[c] = ma.slice_cols[c];
       ga.Y = Y;
       ga.n_mtiles = static_cast<int>((n_grad + kBM - 1) / kBM);
       ga.n_ntiles = static_cast<int>((hidden + kBN - 1) / kBN);
-      hipLaunchKernelGGL(head_grad_kernel, dim3(static_cast<unsigned>(ga.n_mtiles * ga.n_ntiles * ns)),
-                         dim3(kThreads), 0, s, ga);
+      ga.n_tiles = ga.n_mtiles * ga.n_ntiles * ns;
+      hipLaunchKernelGGL(head_grad_kernel, dim3(static_cast<unsigned>(ga.n_tiles)), dim3(kThreads),
+                         0, s, ga);
       CombineArgs ca{};
       ca.acc = accbuf; ca.Y = Y; ca.alpha = alpha; ca.run = run; ca.targets = targets;
       ca.W = weight; ca.ldw = ldw; ca.vocab = vocab; ca.grad = grad_hidden; ca.n_rows = rows;

@@ -23,6 +23,7 @@ the fp16 logits (`fused_head_loss(..., return_argmax=True)`).
 """
 
 import os
+import weakref
 
 import torch
 
@@ -43,11 +44,12 @@ def _slice_width(vocab_chunk, vocab):
 
 
 def head_ce(h16, w16, targets, vocab_chunk=VOCAB_CHUNK, n_grad=None, need_grad=True,
-            group=GROUP):
+            group=GROUP, weight_t=None):
     """One talm_head_ce call. h16 fp16 [N, H], w16 fp16 [V, H] (unit column strides), targets
     int64 [N]. With `need_grad`, rows [0, n_grad) must be the labelled rows (labelled-first order;
-    n_grad defaults to counting them, one host sync). Returns per-row token_loss, entropy,
-    best_idx (int32), correct (int32) and grad (fp16 [N, H] or None)."""
+    n_grad defaults to counting them, one host sync) and `weight_t` is w16's transpose from
+    `head_weights` (built here when not given). Returns per-row token_loss, entropy, best_idx
+    (int32), correct (int32) and grad (fp16 [N, H] or None)."""
     n, size = h16.shape
     vocab = w16.shape[0]
     device = h16.device
@@ -64,12 +66,47 @@ def head_ce(h16, w16, targets, vocab_chunk=VOCAB_CHUNK, n_grad=None, need_grad=T
     }
     if n == 0:
         return out
+    if need_grad and n_grad > 0 and weight_t is None:
+        weight_t = transpose_weight(w16)
     nbytes = _ops.head_ce_workspace_bytes(n, size, vocab, vchunk, n_grad, group)
     workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    torch.ops.talm.head_ce(h16, w16, targets, vchunk, n_grad, group, out["token_loss"],
-                           out["entropy"], out["best_idx"], out["correct"], out["grad"],
-                           workspace)
+    torch.ops.talm.head_ce(h16, w16, weight_t if need_grad else None, targets, vchunk, n_grad,
+                           group, out["token_loss"], out["entropy"], out["best_idx"],
+                           out["correct"], out["grad"], workspace)
     return out
+
+
+def transpose_weight(w16):
+    """w16 fp16 [V, H] -> [H, ldwt] with ldwt = V rounded up to 64 and columns [V, ldwt) zero:
+    the k-contiguous operand of the head's gradient GEMM."""
+    vocab, size = w16.shape
+    ldwt = -(-vocab // 64) * 64
+    wt = torch.empty(size, ldwt, dtype=torch.float16, device=w16.device)
+    torch.ops.talm.head_weight_t(w16, wt)
+    return wt
+
+
+_HEAD_WEIGHTS = {}
+
+
+def head_weights(weight, need_transpose=True):
+    """(w16, w16^T) of the frozen output weight: w16 its fp16 [V, H] view (or one converted copy)
+    and, with `need_transpose`, the transposed copy the gradient GEMM reads (else None). Both are
+    kept for the weight object at its current version (data pointer, version counter, layout) and
+    rebuilt when any of these changes: the tied embedding of the QLoRA model is frozen, so they
+    are built once (the transpose is 2 bytes per weight element of extra HBM)."""
+    w = weight.detach()
+    key = (w.data_ptr(), w._version, w.dtype, tuple(w.shape), tuple(w.stride()), str(w.device))
+    hit = _HEAD_WEIGHTS.get("head")
+    if hit is not None and hit[0]() is weight and hit[1] == key:
+        if hit[3] is not None or not need_transpose:
+            return hit[2], hit[3]
+        w16 = hit[2]
+    else:
+        w16 = _fp16_weight(weight)
+    wt = transpose_weight(w16) if need_transpose else None
+    _HEAD_WEIGHTS["head"] = (weakref.ref(weight), key, w16, wt)
+    return w16, wt
 
 
 def _denominator(num_items, labelled_count):
@@ -118,7 +155,7 @@ class FusedHeadLossVocab(torch.autograd.Function):
         h16 = hidden.detach().to(torch.float16)
         if h16.stride(1) != 1 or h16.stride(0) % 8 or h16.data_ptr() % 16:
             h16 = h16.contiguous()
-        w16 = _fp16_weight(weight)
+        w16, wt = head_weights(weight, need_transpose=bool(need_grad))
         targets = targets.to(device=hidden.device, dtype=torch.int64).contiguous()
         labelled = targets >= 0
         n_grad, dest, rows_targets = 0, None, targets
@@ -133,7 +170,7 @@ class FusedHeadLossVocab(torch.autograd.Function):
                 h16 = h16.index_select(0, src)
                 rows_targets = targets.index_select(0, src)
                 RAN["compact"] += 1
-        out = head_ce(h16, w16, rows_targets, vocab_chunk, n_grad, need_grad)
+        out = head_ce(h16, w16, rows_targets, vocab_chunk, n_grad, need_grad, weight_t=wt)
         RAN["head"] += 1
         token_loss, entropy = out["token_loss"], out["entropy"]
         correct, best_idx, grad_hidden = out["correct"], out["best_idx"], out["grad"]

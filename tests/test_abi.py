@@ -52,6 +52,15 @@ def test_argument_rejection_needs_no_gpu():
         _lib.check(lib.talm_nf4_dequant(None, None, None, 3, 64, None), "nf4_dequant")
     assert lib.talm_swiglu_fwd(None, None, None, 0, None) == _lib.TALM_OK  # empty: no launch
     assert lib.talm_last_error() == b""
+    # the transposed head weight: ldwt below the vocabulary, then a stride that is not 16-byte
+    assert lib.talm_head_weight_t(None, 64, 100, 64, None, 96, None) == _lib.TALM_EINVAL
+    assert b"ldwt" in lib.talm_last_error()
+    assert lib.talm_head_weight_t(None, 64, 100, 64, None, 100, None) == _lib.TALM_EINVAL
+    # the gradient needs the transposed weight: a NULL weight_t is rejected before any launch
+    ws, out = 1 << 8, 1 << 12  # fake, aligned addresses: never dereferenced on rejection
+    status = lib.talm_head_ce(out, 64, out, 64, None, 0, out, 4, 64, 1000, 256, 2, 1, out, out,
+                              out, out, out, ws, 1 << 30, None)
+    assert status == _lib.TALM_EINVAL and b"weight_t" in lib.talm_last_error()
 
 
 def test_custom_ops_are_registered_for_the_gpu_only():
@@ -60,7 +69,7 @@ def test_custom_ops_are_registered_for_the_gpu_only():
     import talm_amd._ops  # noqa: F401
 
     for name in ("nf4_group_dequant", "nf4_dequant", "rmsnorm", "rope", "swiglu_fwd",
-                 "swiglu_bwd"):
+                 "swiglu_bwd", "head_weight_t", "head_ce"):
         assert hasattr(torch.ops.talm, name)
     x = torch.zeros(8, dtype=torch.float16)
     with pytest.raises(NotImplementedError):

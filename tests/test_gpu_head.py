@@ -158,3 +158,20 @@ def test_head_config4_full_size_sampled_rows():
     assert np.all(np.abs(sub["grad"] - g_ref) <= 2e-3 * np.abs(g_ref) + 2.0 ** -7 * scale)
     total = res["token_loss"].astype(np.float64).sum() / n_lab
     assert abs(res["loss"] - total) <= 1e-5 * total
+
+
+def test_head_weight_transpose_and_cache():
+    """talm_head_weight_t: exact transpose with zero columns past the vocabulary; the cached
+    transpose is reused for the same weight version and rebuilt after an in-place update."""
+    _case("head weight_t + cache")
+    w = torch.randn(1003, 136, device=DEV).half()
+    wt = fused_head.transpose_weight(w)
+    assert tuple(wt.shape) == (136, 1024)
+    assert torch.equal(wt[:, :1003], w.t())
+    assert bool(torch.all(wt[:, 1003:] == 0))
+    _, wt_a = fused_head.head_weights(w)
+    _, wt_b = fused_head.head_weights(w)
+    assert wt_a is wt_b
+    w.mul_(2)
+    _, wt_c = fused_head.head_weights(w)
+    assert wt_c is not wt_a and torch.equal(wt_c[:, :1003], w.t())
