@@ -29,6 +29,8 @@
 // tiles that share an operand panel share an L2. Two workgroups per CU.
 #include "common.h"
 
+#include <algorithm>
+
 namespace talm {
 namespace {
 
@@ -36,28 +38,45 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int kThreads = 256;        // 4 wavefronts, 2 x 2 over the tile
-constexpr int kBM = 256;             // tile rows
-constexpr int kBN = 128;             // tile columns
-constexpr int kBK = 32;              // reduction step: two 32x32x16 MFMAs deep
+constexpr int kThreads = 256;        // block size of the merge, combine and transpose kernels
+constexpr int kBM = 256;             // GEMM tile rows
 constexpr int kWM = 4, kWN = 2;      // 32x32 MFMA blocks per wavefront (128 x 64)
-constexpr int kStages = 3;           // LDS ring depth
-constexpr int kAChunks = kBM * kBK / 8;                    // 16-byte chunks per A stage
-constexpr int kBChunks = kBN * kBK / 8;                    // 16-byte chunks per B stage
-constexpr int kStageBytes = (kAChunks + kBChunks) * 16;    // 24 KiB
-constexpr int kLdsMain = kStages * kStageBytes;            // 72 KiB
-constexpr int kTile = 128;           // statistics granule (columns) == kBN
-constexpr int kZS = kBN + 8;         // LDS row stride (halfs) of the staged logits tile
+constexpr int kTile = 128;           // statistics granule (columns)
 constexpr int kXcds = 8;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every range: the load returns 0
 
-static_assert(kBM * kZS * 2 <= kLdsMain, "the staged logits tile reuses the LDS ring");
+// GEMM tile shapes: 256 x BN outputs, BK-deep steps, a STAGES-slot LDS ring. Every wavefront owns
+// 128 x 64 of the tile, so both shapes run two wavefronts per SIMD: Narrow as two 256-thread
+// workgroups per CU, Wide as one 512-thread workgroup that moves a third fewer bytes per FLOP.
+template <int BN, int BK, int STAGES>
+struct TileShape {
+  static constexpr int kBN = BN, kBK = BK, kStages = STAGES;
+  static constexpr int kWaves = 2 * (BN / 64);
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kCpr = BK / 8;                       // 16-byte chunks per row of a stage
+  static constexpr int kAChunks = kBM * kCpr, kBChunks = BN * kCpr;
+  static constexpr int kStageBytes = (kAChunks + kBChunks) * 16;
+  static constexpr int kRing = STAGES * kStageBytes;
+  static constexpr int kZS = BN + 8;                        // staged logits row stride (halfs)
+  static constexpr int kLds = kRing > kBM * kZS * 2 ? kRing : kBM * kZS * 2;
+  static constexpr int kPerCu = 512 / kThreads;             // workgroups per CU
+  static_assert(STAGES == 2 || STAGES == 3, "ring depth");
+  static_assert(kLds <= 160 * 1024, "LDS per CU");
+};
+using Narrow = TileShape<128, 32, 3>;  // 72 KiB ring
+using Wide = TileShape<256, 64, 2>;    // 128 KiB ring, 135 KiB with the staged logits tile
 
-// [rows][kBK] fp16 tile as 16-byte chunks (4 per row). The chunk column is XOR-ed with
-// ((row >> 1) ^ (row >> 2)) & 3: the rows read by one ds_read_b128 phase (8 consecutive rows on
-// 32 banks, 16 on 64 banks, one chunk column) then land on distinct banks.
-__device__ __forceinline__ int swz_key(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
-__device__ __forceinline__ int swz(int row, int kc) { return row * 4 + (kc ^ swz_key(row)); }
+// [rows][BK] fp16 stage as 16-byte chunks, CPR per row. The chunk column is XOR-ed with a key of
+// the row so that the rows read by one ds_read_b128 phase (8 consecutive rows on 32 banks, 16 on
+// 64 banks, one chunk column) land on distinct banks: ((row >> 1) ^ (row >> 2)) & 3 for 64-byte
+// rows, (row ^ (row >> 3)) & 7 for 128-byte rows.
+template <int CPR>
+__device__ __forceinline__ int swz_key(int row) {
+  if constexpr (CPR == 4) return ((row >> 1) ^ (row >> 2)) & 3;
+  else return (row ^ (row >> 3)) & 7;
+}
+template <int CPR>
+__device__ __forceinline__ int swz(int row, int kc) { return row * CPR + (kc ^ swz_key<CPR>(row)); }
 
 // Wait until at most N vector-memory operations of this wavefront are outstanding (vmcnt only).
 template <int N>
@@ -83,14 +102,23 @@ __device__ __forceinline__ uint32_t xcd_tile(uint32_t bid, uint32_t n_tiles) {
   return x * q + min(x, r) + i;
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const uint16_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)dst, 16, off, 0, 0, 0);
+}
+
 // One operand of the tile core: kRows rows of fp16 with k contiguous, from `base` (the tile's
 // first row, k = 0) with row stride `ld` halfs. Each step, every wavefront moves its 1 KiB blocks
-// (16 rows x 4 chunks) of the stage with buffer_load_dwordx4 ... lds: lane l fills the block's
-// l-th chunk, so the lane loads the global chunk that the swizzle puts there. Chunks of rows past
-// `rows_valid`, or starting at k >= `k_valid`, get an out-of-range offset and read as zeros.
-template <int kRows>
+// of the stage with buffer_load_dwordx4 ... lds: lane l fills the block's l-th chunk, so the lane
+// loads the global chunk that the swizzle puts there. Chunks of rows past `rows_valid`, or
+// starting at k >= `k_valid`, get an out-of-range offset and read as zeros.
+template <class S, int kRows>
 struct Loader {
-  static constexpr int kPer = kRows * kBK / 8 / kThreads;  // DMA instructions per thread per step
+  static constexpr int kPer = kRows * S::kCpr / S::kThreads;  // DMA instructions per step
+  static constexpr int kRowsPerBlock = 64 / S::kCpr;
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t off[kPer];
   int kc8[kPer];
@@ -98,13 +126,12 @@ struct Loader {
 
   __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int rows_valid,
                                        int k_valid_, int wave, int lane) {
-    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, 0x7fffffff,
-                                             0x00020000);
+    rsrc = buffer_rsrc(base);
     k_valid = k_valid_;
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
-      const int row = 16 * (p * 4 + wave) + (lane >> 2);
-      const int kc = (lane & 3) ^ swz_key(row);
+      const int row = kRowsPerBlock * (p * S::kWaves + wave) + lane / S::kCpr;
+      const int kc = (lane % S::kCpr) ^ swz_key<S::kCpr>(row);
       kc8[p] = kc * 8;
       off[p] = row < rows_valid ? static_cast<uint32_t>((row * ld + kc * 8) * 2) : kOob;
     }
@@ -114,28 +141,29 @@ struct Loader {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const uint32_t v = k0 + kc8[p] < k_valid ? off[p] + static_cast<uint32_t>(k0 * 2) : kOob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, (lds_ptr_t)(dst + (p * 4 + wave) * 1024), 16, v, 0, 0, 0);
+      dma16(rsrc, dst + (p * S::kWaves + wave) * 1024, v);
     }
   }
 };
 
-// One 32-deep step of the wavefront's 128 x 64 block: 2 x (4 A + 2 B fragments, 8 MFMAs).
+// One step of the wavefront's 128 x 64 block: BK / 16 x (4 A + 2 B fragments, 8 MFMAs).
+template <class S>
 __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uint4* __restrict__ Bs,
                                          f32x16 (&acc)[kWM][kWN], int lane, int wm, int wn) {
-  half8_t a[2][kWM], b[2][kWN];
+  constexpr int kSteps = S::kBK / 16;
+  half8_t a[kSteps][kWM], b[kSteps][kWN];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < kSteps; ++ks) {
     const int kc = ks * 2 + (lane >> 5);
 #pragma unroll
     for (int i = 0; i < kWM; ++i)
-      a[ks][i] = __builtin_bit_cast(half8_t, As[swz(wm * 128 + i * 32 + (lane & 31), kc)]);
+      a[ks][i] = __builtin_bit_cast(half8_t, As[swz<S::kCpr>(wm * 128 + i * 32 + (lane & 31), kc)]);
 #pragma unroll
     for (int j = 0; j < kWN; ++j)
-      b[ks][j] = __builtin_bit_cast(half8_t, Bs[swz(wn * 64 + j * 32 + (lane & 31), kc)]);
+      b[ks][j] = __builtin_bit_cast(half8_t, Bs[swz<S::kCpr>(wn * 64 + j * 32 + (lane & 31), kc)]);
   }
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
+  for (int ks = 0; ks < kSteps; ++ks)
 #pragma unroll
     for (int i = 0; i < kWM; ++i)
 #pragma unroll
@@ -143,38 +171,43 @@ __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uin
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
 }
 
-// acc = A B^T over nk steps of 32: A is the 256-row operand, B the 128-row one. Step kt waits for
-// its own DMA group (the next one stays in flight), one barrier makes every wavefront's data
-// visible and retires the stage read in step kt - 1, which then receives step kt + 2.
-__device__ __forceinline__ void tile_gemm(Loader<kBM>& la, Loader<kBN>& lb, unsigned char* smem,
-                                          int nk, f32x16 (&acc)[kWM][kWN], int lane, int wave) {
-  constexpr int kGroup = Loader<kBM>::kPer + Loader<kBN>::kPer;
-  const int wm = wave >> 1, wn = wave & 1;
+// acc = A B^T over nk steps: A is the 256-row operand, B the BN-row one. Step kt waits for its
+// own DMA group (with three stages the next group stays in flight), one barrier makes every
+// wavefront's data visible and retires the slot read in step kt - 1, which then receives step
+// kt + STAGES - 1.
+template <class S>
+__device__ __forceinline__ void tile_gemm(Loader<S, kBM>& la, Loader<S, S::kBN>& lb,
+                                          unsigned char* smem, int nk, f32x16 (&acc)[kWM][kWN],
+                                          int lane, int wave) {
+  constexpr int kGroup = Loader<S, kBM>::kPer + Loader<S, S::kBN>::kPer;
+  constexpr int kB = S::kAChunks * 16;  // B block offset inside a stage
+  const int wm = wave / (S::kWaves / 2), wn = wave % (S::kWaves / 2);
 #pragma unroll
   for (int i = 0; i < kWM; ++i)
 #pragma unroll
     for (int j = 0; j < kWN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-  la.issue(smem, 0, wave);
-  lb.issue(smem + kAChunks * 16, 0, wave);
-  if (nk > 1) {
-    la.issue(smem + kStageBytes, kBK, wave);
-    lb.issue(smem + kStageBytes + kAChunks * 16, kBK, wave);
-  }
-  int s = 0;  // stage of step kt
+#pragma unroll
+  for (int st = 0; st < S::kStages - 1; ++st)
+    if (st < nk) {
+      la.issue(smem + st * S::kStageBytes, st * S::kBK, wave);
+      lb.issue(smem + st * S::kStageBytes + kB, st * S::kBK, wave);
+    }
+  int s = 0;  // slot of step kt
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) wait_vmcnt<kGroup>();
+    if (S::kStages == 3 && kt + 1 < nk) wait_vmcnt<kGroup>();
     else wait_vmcnt<0>();
     lds_barrier();
-    if (kt + 2 < nk) {
-      unsigned char* st = smem + (s == 0 ? 2 : s - 1) * kStageBytes;  // stage (kt + 2) % 3
-      la.issue(st, (kt + 2) * kBK, wave);
-      lb.issue(st + kAChunks * 16, (kt + 2) * kBK, wave);
+    if (kt + S::kStages - 1 < nk) {
+      const int s2 = s == 0 ? S::kStages - 1 : s - 1;  // slot (kt + STAGES - 1) % STAGES
+      la.issue(smem + s2 * S::kStageBytes, (kt + S::kStages - 1) * S::kBK, wave);
+      lb.issue(smem + s2 * S::kStageBytes + kB, (kt + S::kStages - 1) * S::kBK, wave);
     }
-    const uint4* As = reinterpret_cast<const uint4*>(smem + s * kStageBytes);
-    mma_step(As, As + kAChunks, acc, lane, wm, wn);
-    s = s == 2 ? 0 : s + 1;
+    const unsigned char* st = smem + s * S::kStageBytes;
+    mma_step<S>(reinterpret_cast<const uint4*>(st), reinterpret_cast<const uint4*>(st + kB), acc,
+                lane, wm, wn);
+    s = s + 1 == S::kStages ? 0 : s + 1;
   }
   __syncthreads();  // every wavefront is done with the ring before the caller reuses the LDS
 }
@@ -216,12 +249,14 @@ __device__ __forceinline__ Stat shfl_stat(Stat v, int off) {
 // GEMM1: Z[r][j] = fp16(sum_k H[r][k] W[j][k]) for the group's columns j < group_cols (W starts
 // at the group's first vocabulary row), plus the per-(row, 128-column tile) partial statistics.
 // ------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
+template <class S>
+__global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_logits_kernel(
     const uint16_t* __restrict__ H, int64_t ldh, const uint16_t* __restrict__ W, int64_t ldw,
     int n_rows, int K, int group_cols, int first_col, uint16_t* __restrict__ Z, int64_t ldz,
     float4* __restrict__ part, int parts_per_row, int n_mtiles, int n_ntiles,
     const int64_t* __restrict__ targets, float* __restrict__ ztarget) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kLdsMain];
+  constexpr int kBN = S::kBN, kZS = S::kZS;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kLds];
 
   // row tiles vary fastest inside an XCD's range: the tiles in flight on one XCD share weight rows
   const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(n_mtiles * n_ntiles));
@@ -230,14 +265,14 @@ __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
   const int m0 = mtile * kBM, n0 = ntile * kBN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (S::kWaves / 2), wn = wave % (S::kWaves / 2);
 
-  Loader<kBM> la;
-  Loader<kBN> lb;
+  Loader<S, kBM> la;
+  Loader<S, kBN> lb;
   la.init(H + static_cast<int64_t>(m0) * ldh, ldh, n_rows - m0, K, wave, lane);
   lb.init(W + static_cast<int64_t>(n0) * ldw, ldw, group_cols - n0, K, wave, lane);
   f32x16 acc[kWM][kWN];
-  tile_gemm(la, lb, smem, (K + kBK - 1) / kBK, acc, lane, wave);
+  tile_gemm<S>(la, lb, smem, (K + S::kBK - 1) / S::kBK, acc, lane, wave);
 
   // Epilogue 1: fp16 logits tile into LDS ([kBM][kZS] halfs).
   uint16_t* Zs = reinterpret_cast<uint16_t*>(smem);
@@ -253,18 +288,20 @@ __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
       }
   __syncthreads();
 
-  // Epilogue 2: partial statistics of row `tid` over this tile's valid columns.
+  // Epilogue 2: partial statistics of one (row, 128-column statistics tile) per thread.
   {
-    const int row = tid, gr = m0 + row;
-    const int valid = min(kBN, group_cols - n0);
-    if (gr < n_rows) {
-      uint4 zv[kBN / 8];
+    const int row = tid % kBM, st = tid / kBM, gr = m0 + row;
+    const int c0 = n0 + st * kTile;  // the statistics tile's first column in the group
+    const int valid = min(kTile, group_cols - c0);
+    if (gr < n_rows && valid > 0) {
+      const uint16_t* zr = Zs + row * kZS + st * kTile;
+      uint4 zv[kTile / 8];
 #pragma unroll
-      for (int c = 0; c < kBN / 8; ++c) zv[c] = *reinterpret_cast<const uint4*>(Zs + row * kZS + 8 * c);
+      for (int c = 0; c < kTile / 8; ++c) zv[c] = *reinterpret_cast<const uint4*>(zr + 8 * c);
       float m = -INFINITY;
       int idx = 0;
 #pragma unroll
-      for (int c = 0; c < kBN / 8; ++c) {
+      for (int c = 0; c < kTile / 8; ++c) {
         const uint32_t w4[4] = {zv[c].x, zv[c].y, zv[c].z, zv[c].w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -276,9 +313,9 @@ __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
           }
         }
       }
-      float s = 0.f, t = 0.f;
+      float sum = 0.f, t = 0.f;
 #pragma unroll
-      for (int c = 0; c < kBN / 8; ++c) {
+      for (int c = 0; c < kTile / 8; ++c) {
         const uint32_t w4[4] = {zv[c].x, zv[c].y, zv[c].z, zv[c].w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -286,23 +323,23 @@ __global__ __launch_bounds__(kThreads, 2) void head_logits_kernel(
           const float z = (e & 1) ? hi_f(w4[e >> 1]) : lo_f(w4[e >> 1]);
           if (col < valid) {
             const float ez = __expf(z - m);
-            s += ez;
+            sum += ez;
             t += ez * z;
           }
         }
       }
-      part[static_cast<int64_t>(gr) * parts_per_row + ntile] =
-          make_float4(m, s, t, __int_as_float(first_col + n0 + idx));
+      part[static_cast<int64_t>(gr) * parts_per_row + c0 / kTile] =
+          make_float4(m, sum, t, __int_as_float(first_col + c0 + idx));
       // the logit at the target, when the target column is in this tile (one tile per row)
-      const int64_t rel = targets[gr] - (first_col + n0);
-      if (rel >= 0 && rel < valid) ztarget[gr] = h2f(Zs[row * kZS + static_cast<int>(rel)]);
+      const int64_t rel = targets[gr] - (first_col + c0);
+      if (rel >= 0 && rel < valid) ztarget[gr] = h2f(zr[static_cast<int>(rel)]);
     }
   }
 
-  // Epilogue 3: the logits tile to global memory in 16-byte chunks (16 per row).
+  // Epilogue 3: the logits tile to global memory in 16-byte chunks (kBN / 8 per row).
 #pragma unroll
-  for (int it = 0; it < (kBM * kBN / 8) / kThreads; ++it) {
-    const int c = it * kThreads + tid, row = c >> 4, kc = c & 15;
+  for (int it = 0; it < (kBM * kBN / 8) / S::kThreads; ++it) {
+    const int c = it * S::kThreads + tid, row = c / (kBN / 8), kc = c % (kBN / 8);
     const int gr = m0 + row, gc = n0 + kc * 8;
     if (gr < n_rows && gc < group_cols)
       *reinterpret_cast<uint4*>(Z + static_cast<int64_t>(gr) * ldz + gc) =
@@ -427,34 +464,42 @@ struct GradArgs {
   int hidden;
   int vchunk;
   int slice_cols[8];
-  float* Y;               // [n_slices][n_grad][hidden] fp32
+  int ksplit;             // parts of each slice's columns, each with its own partial
+  float* Y;               // [n_slices * ksplit][n_grad][hidden] fp32
   int n_mtiles, n_ntiles, n_tiles;
 };
 
-__global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kLdsMain];
+template <class S>
+__global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradArgs a) {
+  constexpr int kBN = S::kBN;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing];
 
   // hidden tiles vary fastest inside an XCD's range: the tiles in flight on one XCD share P rows
   const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_tiles));
   const int ntile = static_cast<int>(tile % a.n_ntiles);
   const int rest = static_cast<int>(tile / a.n_ntiles);
-  const int mtile = rest % a.n_mtiles, slice = rest / a.n_mtiles;
+  const int mtile = rest % a.n_mtiles, piece = rest / a.n_mtiles;
+  const int slice = piece / a.ksplit, kpart = piece % a.ksplit;
   const int m0 = mtile * kBM, n0 = ntile * kBN;
   const int cols = a.slice_cols[slice];
-  const int zc = slice * a.vchunk;
+  // this part's columns of the slice, in whole steps
+  const int span = (cols + a.ksplit - 1) / a.ksplit;
+  const int per = (span + S::kBK - 1) / S::kBK * S::kBK;
+  const int k0 = min(kpart * per, cols), kn = min(cols - k0, per);
+  const int zc = slice * a.vchunk + k0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (S::kWaves / 2), wn = wave % (S::kWaves / 2);
 
-  Loader<kBM> la;
-  Loader<kBN> lb;
-  la.init(a.Z + static_cast<int64_t>(m0) * a.ldz + zc, a.ldz, a.n_grad - m0, cols, wave, lane);
-  lb.init(a.WT + static_cast<int64_t>(n0) * a.ldwt + a.col0 + zc, a.ldwt, a.hidden - n0, cols,
+  Loader<S, kBM> la;
+  Loader<S, kBN> lb;
+  la.init(a.Z + static_cast<int64_t>(m0) * a.ldz + zc, a.ldz, a.n_grad - m0, kn, wave, lane);
+  lb.init(a.WT + static_cast<int64_t>(n0) * a.ldwt + a.col0 + zc, a.ldwt, a.hidden - n0, kn,
           wave, lane);
   f32x16 acc[kWM][kWN];
-  tile_gemm(la, lb, smem, (cols + kBK - 1) / kBK, acc, lane, wave);
+  tile_gemm<S>(la, lb, smem, (kn + S::kBK - 1) / S::kBK, acc, lane, wave);
 
-  float* Y = a.Y + static_cast<int64_t>(slice) * a.n_grad * a.hidden;
+  float* Y = a.Y + static_cast<int64_t>(piece) * a.n_grad * a.hidden;
 #pragma unroll
   for (int i = 0; i < kWM; ++i)
 #pragma unroll
@@ -473,7 +518,7 @@ __global__ __launch_bounds__(kThreads, 2) void head_grad_kernel(GradArgs a) {
 // ------------------------------------------------------------------------------------------
 struct CombineArgs {
   float* acc;              // [n_grad][hidden]
-  const float* Y;          // [n_slices][n_grad][hidden]
+  const float* Y;          // [n_slices * ksplit][n_grad][hidden]: ksplit partials per slice
   const float* alpha;      // [n_slices][n_rows]
   const float* run;        // running statistics (s at [n_rows + row])
   const int64_t* targets;
@@ -481,7 +526,7 @@ struct CombineArgs {
   int64_t ldw;
   int64_t vocab;
   uint16_t* grad;          // [n_rows][hidden] fp16 (written after the last slice)
-  int n_rows, n_grad, hidden, n_slices, first_slice, last_slice;
+  int n_rows, n_grad, hidden, n_slices, ksplit, first_slice, last_slice;
 };
 
 __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
@@ -498,7 +543,12 @@ __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
   float4 v = a.first_slice ? make_float4(0.f, 0.f, 0.f, 0.f) : *reinterpret_cast<const float4*>(a.acc + at);
   for (int c = 0; c < a.n_slices; ++c) {
     const float al = a.alpha[static_cast<int64_t>(c) * a.n_rows + row];
-    const float4 y = *reinterpret_cast<const float4*>(a.Y + static_cast<int64_t>(c) * a.n_grad * a.hidden + at);
+    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int p = 0; p < a.ksplit; ++p) {
+      const float4 yp = *reinterpret_cast<const float4*>(
+          a.Y + static_cast<int64_t>(c * a.ksplit + p) * a.n_grad * a.hidden + at);
+      y.x += yp.x; y.y += yp.y; y.z += yp.z; y.w += yp.w;
+    }
     if (a.first_slice && c == 0) {
       v = y;
     } else {
@@ -560,23 +610,76 @@ __global__ __launch_bounds__(kThreads) void weight_t_kernel(const uint16_t* __re
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+constexpr int kCus = 256;  // MI355X compute units
+
+// Fraction of the launch's workgroup slots that hold work, over the rounds it takes.
+double fill(int64_t blocks, int per_cu) {
+  const int64_t slots = static_cast<int64_t>(kCus) * per_cu;
+  const int64_t rounds = (blocks + slots - 1) / slots;
+  return rounds ? static_cast<double>(blocks) / static_cast<double>(rounds * slots) : 0.0;
+}
+
+// The Wide shape moves a third fewer bytes per FLOP (~20% faster per tile); pick it unless the
+// launch fills the chip clearly worse with it.
+constexpr double kWideGain = 1.2;
+
+bool logits_wide(int64_t n_rows, int64_t gcols) {
+  const int64_t mt = (n_rows + kBM - 1) / kBM;
+  return kWideGain * fill(mt * ((gcols + Wide::kBN - 1) / Wide::kBN), Wide::kPerCu) >=
+         fill(mt * ((gcols + Narrow::kBN - 1) / Narrow::kBN), Narrow::kPerCu);
+}
+
+// The gradient GEMM's output [n_grad, hidden] per slice is small: besides the shape, each slice's
+// columns may be split into `ksplit` parts (each its own fp32 partial, summed by head_combine) so
+// the launch fills the chip. Each extra part costs a little partial traffic.
+struct GradPlan {
+  bool wide;
+  int ksplit;
+};
+
+GradPlan plan_grad(int64_t n_grad, int64_t hidden, int ns) {
+  const int64_t mt = (n_grad + kBM - 1) / kBM;
+  GradPlan best{true, 1};
+  double best_score = -1.0;
+  for (int wide = 1; wide >= 0; --wide) {
+    const int bn = wide ? Wide::kBN : Narrow::kBN;
+    for (int ks = 1; ks <= 4; ++ks) {
+      const int64_t blocks = mt * ((hidden + bn - 1) / bn) * ns * ks;
+      const double score = (wide ? kWideGain : 1.0) * (1.0 - 0.03 * (ks - 1)) *
+                           fill(blocks, wide ? Wide::kPerCu : Narrow::kPerCu);
+      if (score > best_score + 1e-9) {
+        best_score = score;
+        best = GradPlan{wide != 0, ks};
+      }
+    }
+  }
+  return best;
+}
+
 struct Layout {
   size_t z, part, run, ztarget, alpha, y, acc, total;
   int64_t ldz;
   int parts_per_row;
 };
 
-Layout layout(int64_t n_rows, int64_t hidden, int64_t vchunk, int64_t n_grad, int group) {
+Layout layout(int64_t n_rows, int64_t hidden, int64_t vocab, int64_t vchunk, int64_t n_grad,
+              int group) {
   Layout l{};
   l.ldz = align_up(static_cast<size_t>(group * vchunk), 8);
   l.parts_per_row = static_cast<int>(group * vchunk / kTile);
+  // fp32 partials for the largest group: a full one, or the last (narrower) one
+  const int64_t slices = (vocab + vchunk - 1) / vchunk;
+  const int last = static_cast<int>(slices - (slices - 1) / group * group);
+  const int64_t pieces = n_grad > 0 ? std::max<int64_t>(group * plan_grad(n_grad, hidden, group).ksplit,
+                                                        last * plan_grad(n_grad, hidden, last).ksplit)
+                                    : 0;
   size_t off = 0;
   l.z = off;      off = align_up(off + static_cast<size_t>(n_rows) * l.ldz * 2, 256);
   l.part = off;   off = align_up(off + static_cast<size_t>(n_rows) * l.parts_per_row * 16, 256);
   l.run = off;    off = align_up(off + static_cast<size_t>(n_rows) * 6 * 4, 256);
   l.ztarget = off; off = align_up(off + static_cast<size_t>(n_rows) * 4, 256);
   l.alpha = off;  off = align_up(off + static_cast<size_t>(group) * n_rows * 4, 256);
-  l.y = off;      off = align_up(off + static_cast<size_t>(group) * n_grad * hidden * 4, 256);
+  l.y = off;      off = align_up(off + static_cast<size_t>(pieces) * n_grad * hidden * 4, 256);
   l.acc = off;    off = align_up(off + static_cast<size_t>(n_grad) * hidden * 4, 256);
   l.total = off;
   return l;
@@ -594,7 +697,7 @@ TALM_API int64_t talm_head_ce_workspace(int64_t n_rows, int64_t hidden, int64_t 
     return -1;
   const int64_t slices = (vocab + vchunk - 1) / vchunk;
   const int g = static_cast<int>(slices < group ? slices : group);
-  return static_cast<int64_t>(layout(n_rows, hidden, vchunk, n_grad, g).total);
+  return static_cast<int64_t>(layout(n_rows, hidden, vocab, vchunk, n_grad, g).total);
 }
 
 TALM_API int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t vocab,
@@ -647,7 +750,7 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
                              "aligned, the workspace 256-byte aligned");
   const int64_t slices = (vocab + vchunk - 1) / vchunk;
   const int g = static_cast<int>(slices < group ? slices : group);
-  const Layout l = layout(n_rows, hidden, vchunk, n_grad, g);
+  const Layout l = layout(n_rows, hidden, vocab, vchunk, n_grad, g);
   if (l.ldz >= (1 << 22))
     return fail(TALM_EINVAL, "head_ce: group * vchunk = %lld columns per step, below 2^22 needed",
                 (long long)l.ldz);
@@ -670,11 +773,21 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
     const int ns = static_cast<int>(slices - s0 < g ? slices - s0 : g);
     const int64_t col0 = s0 * vchunk;
     const int64_t gcols = (s0 + ns == slices) ? vocab - col0 : ns * vchunk;
-    const int nt = static_cast<int>((gcols + kBN - 1) / kBN);
-    hipLaunchKernelGGL(head_logits_kernel, dim3(static_cast<unsigned>(mt * nt)), dim3(kThreads), 0, s,
-                       hidden_states, ldh, weight + col0 * ldw, ldw, rows, static_cast<int>(hidden),
-                       static_cast<int>(gcols), static_cast<int>(col0), Z, l.ldz, part,
-                       l.parts_per_row, mt, nt, targets, ztarget);
+    if (logits_wide(rows, gcols)) {
+      const int nt = static_cast<int>((gcols + Wide::kBN - 1) / Wide::kBN);
+      hipLaunchKernelGGL((head_logits_kernel<Wide>), dim3(static_cast<unsigned>(mt * nt)),
+                         dim3(Wide::kThreads), 0, s, hidden_states, ldh, weight + col0 * ldw, ldw,
+                         rows, static_cast<int>(hidden), static_cast<int>(gcols),
+                         static_cast<int>(col0), Z, l.ldz, part, l.parts_per_row, mt, nt, targets,
+                         ztarget);
+    } else {
+      const int nt = static_cast<int>((gcols + Narrow::kBN - 1) / Narrow::kBN);
+      hipLaunchKernelGGL((head_logits_kernel<Narrow>), dim3(static_cast<unsigned>(mt * nt)),
+                         dim3(Narrow::kThreads), 0, s, hidden_states, ldh, weight + col0 * ldw,
+                         ldw, rows, static_cast<int>(hidden), static_cast<int>(gcols),
+                         static_cast<int>(col0), Z, l.ldz, part, l.parts_per_row, mt, nt, targets,
+                         ztarget);
+    }
     MergeArgs ma{};
     ma.part = part; ma.parts_per_row = l.parts_per_row; ma.Z = Z; ma.ldz = l.ldz;
     ma.targets = targets; ma.ztarget = ztarget; ma.n_rows = rows;
@@ -698,16 +811,24 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
       ga.vchunk = static_cast<int>(vchunk);
       for (int c = 0; c < ns; ++c) ga.slice_cols[c] = ma.slice_cols[c];
       ga.Y = Y;
+      const GradPlan gp = plan_grad(n_grad, hidden, ns);
+      const int bn = gp.wide ? Wide::kBN : Narrow::kBN;
+      ga.ksplit = gp.ksplit;
       ga.n_mtiles = static_cast<int>((n_grad + kBM - 1) / kBM);
-      ga.n_ntiles = static_cast<int>((hidden + kBN - 1) / kBN);
-      ga.n_tiles = ga.n_mtiles * ga.n_ntiles * ns;
-      hipLaunchKernelGGL(head_grad_kernel, dim3(static_cast<unsigned>(ga.n_tiles)), dim3(kThreads),
-                         0, s, ga);
+      ga.n_ntiles = static_cast<int>((hidden + bn - 1) / bn);
+      ga.n_tiles = ga.n_mtiles * ga.n_ntiles * ns * gp.ksplit;
+      if (gp.wide)
+        hipLaunchKernelGGL((head_grad_kernel<Wide>), dim3(static_cast<unsigned>(ga.n_tiles)),
+                           dim3(Wide::kThreads), 0, s, ga);
+      else
+        hipLaunchKernelGGL((head_grad_kernel<Narrow>), dim3(static_cast<unsigned>(ga.n_tiles)),
+                           dim3(Narrow::kThreads), 0, s, ga);
       CombineArgs ca{};
       ca.acc = accbuf; ca.Y = Y; ca.alpha = alpha; ca.run = run; ca.targets = targets;
       ca.W = weight; ca.ldw = ldw; ca.vocab = vocab; ca.grad = grad_hidden; ca.n_rows = rows;
       ca.n_grad = static_cast<int>(n_grad); ca.hidden = static_cast<int>(hidden);
-      ca.n_slices = ns; ca.first_slice = ma.first_slice; ca.last_slice = ma.last_slice;
+      ca.n_slices = ns; ca.ksplit = gp.ksplit;
+      ca.first_slice = ma.first_slice; ca.last_slice = ma.last_slice;
       const int64_t work = (ca.last_slice ? n_rows : n_grad) * (hidden / 4);
       hipLaunchKernelGGL(head_combine_kernel, dim3(static_cast<unsigned>((work + kThreads - 1) / kThreads)),
                          dim3(kThreads), 0, s, ca);
