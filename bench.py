@@ -29,6 +29,21 @@ FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
 
 METRIC = "QLoRA step ms (Qwen2.5-1.5B shape, B4xS512); kernel HBM GB/s & MFMA %"
 
+# HBM-side bytes per launch of each suite kernel, measured offline: two rocprofv3 --pmc runs of
+# this file's kernel suite (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the
+# counter reads for the 512 MiB calibration copy (--only copy): FETCH x 2.000, WRITE x 1.000.
+# Commands and per-dispatch tables: profiles/kernel_suite_config1-4_hbm_traffic.md. The head is
+# one talm_head_ce call (all its dispatches). Re-measured whenever a kernel changes.
+MEASURED_TRAFFIC = {
+    "nf4_group_dequant": 118.0e6,
+    "add_rmsnorm_fwd": 18.1e6,
+    "add_rmsnorm_bwd": 18.1e6,
+    "rope_inplace": 10.1e6,
+    "swiglu_fwd": 110.1e6,
+    "swiglu_bwd": 183.6e6,
+    "head_ce_fwd_bwd": 5719e6,
+}
+
 
 def graph_time_ms(fn, steps, warmup, reps):
     """Average duration (ms) of one fn() launch: `reps` launches captured in one graph,
@@ -341,14 +356,15 @@ def main():
     kernels = kernel_suite(kernel_args, only)
     dominant = max(kernels, key=lambda e: e["us"]) if kernels else None
     line_roofline = None
+    traffic = MEASURED_TRAFFIC.get(dominant["kernel"]) if dominant is not None else None
     if dominant is not None and "tflops" in dominant:
         line_roofline = {"kernel": dominant["kernel"], "bound": "mfma",
                          "achieved": dominant["tflops"], "peak": FP16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": dominant["mfma_frac"], "traffic": None}
+                         "unit": "TFLOP/s", "frac": dominant["mfma_frac"], "traffic": traffic}
     elif dominant is not None:
         line_roofline = {"kernel": dominant["kernel"], "bound": "hbm",
                          "achieved": dominant["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": dominant["hbm_frac"], "traffic": None}
+                         "frac": dominant["hbm_frac"], "traffic": traffic}
     line = {"metric": METRIC, "value": None, "unit": "ms", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": None, "higher_is_better": False,
             "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
