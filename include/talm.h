@@ -156,6 +156,38 @@ int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* wei
                  float* token_loss, float* entropy, int32_t* best_idx, int32_t* correct,
                  uint16_t* grad_hidden, void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * LoRA down-projection of the q|k|v node: for adapter g < n_adapters (1 or 2, rank 16 each),
+ * t[:, 16g:16g+16] = fp16(x A_g^T) and ts[:, 16g:16g+16] = fp16(scaling_g * x A_g^T)
+ * (fp32 accumulation). x f16 [n_tokens, hidden] (row stride ldx, hidden a multiple of 32),
+ * A_g f16 [16, hidden] contiguous, t and ts f16 [n_tokens, ldt]. Replaces the adapters'
+ * t = drop(x) A^T GEMMs without dropout (solution/fused_proj.py:139-153, solution/lora.py:
+ * 183-186); t is what the backward keeps.
+ */
+int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
+                   const uint16_t* a0, const uint16_t* a1, int32_t n_adapters, float scaling0,
+                   float scaling1, uint16_t* t, uint16_t* ts, int64_t ldt, void* stream);
+
+/*
+ * The fused q|k|v projection forward: out = x W^T + bias + sum_g (ts_g B_g^T on adapter g's
+ * columns), then the rotary embedding on the heads of 128 columns in [0, rope_cols), in one MFMA
+ * GEMM (the adapter term is one more reduction step: rounded once with the base product).
+ *   x f16 [n_tokens, hidden] (ldx); weight f16 [n_out, hidden] (ldw; the layer group's q|k|v
+ *   rows); bias f16 [n_out] or NULL; ts from talm_lora_down (ldt); adapter g: B_g f16
+ *   [seg_end - seg_begin, 16] contiguous on output columns [seg_begin, seg_end) (whole
+ *   128-column tiles); cos/sin f32 [n_tokens, cs_stride >= 128] or NULL (no rotation);
+ *   out f16 [n_tokens, ldo].
+ * Replaces FusedProjections.forward's base GEMM, the adapters' branch GEMMs and adds, and the
+ * RoPE launch on q and k (solution/fused_proj.py:88-218, solution/rope.py:64-134).
+ */
+int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
+                      const uint16_t* weight, int64_t ldw, int64_t n_out, const uint16_t* bias,
+                      const uint16_t* ts, int64_t ldt, int32_t n_adapters, const uint16_t* b0,
+                      int64_t seg0_begin, int64_t seg0_end, const uint16_t* b1,
+                      int64_t seg1_begin, int64_t seg1_end, const float* cos, const float* sin,
+                      int64_t cs_stride, int64_t rope_cols, uint16_t* out, int64_t ldo,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -207,3 +207,65 @@ def head_ce(hidden, weight, weight_t, targets, vchunk, n_grad, group, token_loss
                                 correct.data_ptr(), _ptr(grad_hidden), workspace.data_ptr(),
                                 workspace.numel() * workspace.element_size(), _stream(hidden)),
                "head_ce")
+
+
+@_op("lora_down(Tensor x, Tensor a0, Tensor? a1, float scaling0, float scaling1, Tensor(a!) t, "
+     "Tensor(b!) ts) -> ()")
+def lora_down(x, a0, a1, scaling0, scaling1, t, ts):
+    """x fp16 [N, H] (unit column stride); a0 (a1) fp16 [16, H] contiguous; t, ts fp16 [N, >= 16
+    per adapter] with a common row stride: t = x A^T per adapter, ts = scaling * that."""
+    for name, v in (("x", x), ("a0", a0), ("t", t), ("ts", ts)):
+        _fp16(v, name)
+    n, size = x.shape
+    adapters = [a0] + ([a1] if a1 is not None else [])
+    for a in adapters:
+        _fp16(a, "lora A")
+        _require(a.is_contiguous() and tuple(a.shape) == (16, size), "lora_down: A [16, H]")
+    _require(x.stride(1) == 1 and t.stride(1) == 1 and ts.stride(1) == 1
+             and t.stride(0) == ts.stride(0) and t.shape[0] == n and ts.shape[0] == n
+             and t.shape[1] >= 16 * len(adapters) and ts.shape[1] >= 16 * len(adapters),
+             "lora_down: x [N, H], t/ts [N, 16 * adapters] with one row stride")
+    lib = _lib.lib()
+    _lib.check(lib.talm_lora_down(x.data_ptr(), x.stride(0), n, size, a0.data_ptr(), _ptr(a1),
+                                  len(adapters), float(scaling0), float(scaling1), t.data_ptr(),
+                                  ts.data_ptr(), t.stride(0), _stream(x)), "lora_down")
+
+
+@_op("qkv_lora_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? ts, Tensor? b0, int seg0_begin, "
+     "int seg0_end, Tensor? b1, int seg1_begin, int seg1_end, Tensor? cos, Tensor? sin, "
+     "int rope_cols, Tensor(a!) out) -> ()")
+def qkv_lora_fwd(x, weight, bias, ts, b0, seg0_begin, seg0_end, b1, seg1_begin, seg1_end, cos,
+                 sin, rope_cols, out):
+    """out [N, n_out] = x W^T + bias + the adapters' ts B^T on their columns, then the rotary
+    embedding (cos/sin fp32 [N, >= 128]) on the 128-column heads below rope_cols."""
+    _fp16(x, "x")
+    _fp16(weight, "weight")
+    _fp16(out, "out")
+    n, size = x.shape
+    n_out = weight.shape[0]
+    _require(x.stride(1) == 1 and weight.stride(1) == 1 and out.stride(1) == 1
+             and weight.shape[1] == size and tuple(out.shape) == (n, n_out),
+             "qkv_lora_fwd: x [N, H], weight [n_out, H], out [N, n_out], unit column strides")
+    if bias is not None:
+        _fp16(bias, "bias")
+        _require(bias.is_contiguous() and bias.numel() == n_out, "qkv_lora_fwd: bias [n_out]")
+    bs = [b for b in (b0, b1) if b is not None]
+    for b in bs:
+        _fp16(b, "lora B")
+        _require(b.is_contiguous() and b.shape[1] == 16, "qkv_lora_fwd: B [segment, 16]")
+    if bs:
+        _fp16(ts, "ts")
+        _require(ts.stride(1) == 1 and ts.shape[0] == n and ts.shape[1] >= 16 * len(bs),
+                 "qkv_lora_fwd: ts [N, 16 * adapters]")
+    if cos is not None:
+        for v in (cos, sin):
+            _require(v is not None and v.is_cuda and v.dtype == torch.float32 and v.stride(1) == 1
+                     and v.shape[0] == n and v.shape[1] >= 128 and v.stride(0) == cos.stride(0),
+                     "qkv_lora_fwd: cos/sin fp32 [N, >= 128] with one row stride")
+    lib = _lib.lib()
+    _lib.check(lib.talm_qkv_lora_fwd(
+        x.data_ptr(), x.stride(0), n, size, weight.data_ptr(), weight.stride(0), n_out,
+        _ptr(bias), _ptr(ts), 0 if ts is None else ts.stride(0), len(bs), _ptr(b0), seg0_begin,
+        seg0_end, _ptr(b1), seg1_begin, seg1_end, _ptr(cos), _ptr(sin),
+        0 if cos is None else cos.stride(0), rope_cols, out.data_ptr(), out.stride(0),
+        _stream(x)), "qkv_lora_fwd")

@@ -27,190 +27,29 @@
 // three-stage LDS ring (two steps of 32 in flight while the third is multiplied), 16-byte chunks
 // XOR-swizzled so that fragment reads are free of bank conflicts, tiles mapped to XCDs so the
 // tiles that share an operand panel share an L2. Two workgroups per CU.
-#include "common.h"
+#include "mfma_tile.h"
 
 #include <algorithm>
 
 namespace talm {
 namespace {
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
 constexpr int kThreads = 256;        // block size of the merge, combine and transpose kernels
-constexpr int kBM = 256;             // GEMM tile rows
-constexpr int kWM = 4, kWN = 2;      // 32x32 MFMA blocks per wavefront (128 x 64)
 constexpr int kTile = 128;           // statistics granule (columns)
-constexpr int kXcds = 8;
-constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every range: the load returns 0
 
-// GEMM tile shapes: 256 x BN outputs, BK-deep steps, a STAGES-slot LDS ring. Every wavefront owns
-// 128 x 64 of the tile, so both shapes run two wavefronts per SIMD: Narrow as two 256-thread
-// workgroups per CU, Wide as one 512-thread workgroup that moves a third fewer bytes per FLOP.
+// GEMM tile shapes of the head: 256 x BN, every wavefront 128 x 64, two wavefronts per SIMD.
+// Narrow runs two 256-thread workgroups per CU; Wide one 512-thread workgroup that moves a third
+// fewer bytes per FLOP. The logits epilogue stages the fp16 tile in LDS ([256][BN + 8] halfs).
 template <int BN, int BK, int STAGES>
-struct TileShape {
-  static constexpr int kBN = BN, kBK = BK, kStages = STAGES;
-  static constexpr int kWaves = 2 * (BN / 64);
-  static constexpr int kThreads = 64 * kWaves;
-  static constexpr int kCpr = BK / 8;                       // 16-byte chunks per row of a stage
-  static constexpr int kAChunks = kBM * kCpr, kBChunks = BN * kCpr;
-  static constexpr int kStageBytes = (kAChunks + kBChunks) * 16;
-  static constexpr int kRing = STAGES * kStageBytes;
-  static constexpr int kZS = BN + 8;                        // staged logits row stride (halfs)
-  static constexpr int kLds = kRing > kBM * kZS * 2 ? kRing : kBM * kZS * 2;
-  static constexpr int kPerCu = 512 / kThreads;             // workgroups per CU
-  static_assert(STAGES == 2 || STAGES == 3, "ring depth");
+struct HeadShape : TileShape<256, BN, BK, STAGES, 2, BN / 64> {
+  static constexpr int kZS = BN + 8;
+  static constexpr int kRingBytes = TileShape<256, BN, BK, STAGES, 2, BN / 64>::kRing;
+  static constexpr int kLds = kRingBytes > 256 * kZS * 2 ? kRingBytes : 256 * kZS * 2;
   static_assert(kLds <= 160 * 1024, "LDS per CU");
 };
-using Narrow = TileShape<128, 32, 3>;  // 72 KiB ring
-using Wide = TileShape<256, 64, 2>;    // 128 KiB ring, 135 KiB with the staged logits tile
-
-// [rows][BK] fp16 stage as 16-byte chunks, CPR per row. The chunk column is XOR-ed with a key of
-// the row so that the rows read by one ds_read_b128 phase (8 consecutive rows on 32 banks, 16 on
-// 64 banks, one chunk column) land on distinct banks: ((row >> 1) ^ (row >> 2)) & 3 for 64-byte
-// rows, (row ^ (row >> 3)) & 7 for 128-byte rows.
-template <int CPR>
-__device__ __forceinline__ int swz_key(int row) {
-  if constexpr (CPR == 4) return ((row >> 1) ^ (row >> 2)) & 3;
-  else return (row ^ (row >> 3)) & 7;
-}
-template <int CPR>
-__device__ __forceinline__ int swz(int row, int kc) { return row * CPR + (kc ^ swz_key<CPR>(row)); }
-
-// Wait until at most N vector-memory operations of this wavefront are outstanding (vmcnt only).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier that orders LDS accesses only: the LDS reads issued before it have returned
-// (lgkmcnt 0), and the compiler moves no memory access across it. Unlike __syncthreads() it does
-// not drain the wavefront's outstanding buffer ... lds transfers, which the ring keeps in flight
-// and waits for with wait_vmcnt.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on XCD b % 8). Give
-// each XCD one contiguous range of tile indices (a bijection for any tile count), so tiles that
-// are neighbours in the caller's order share that XCD's L2.
-__device__ __forceinline__ uint32_t xcd_tile(uint32_t bid, uint32_t n_tiles) {
-  const uint32_t x = bid % kXcds, i = bid / kXcds;
-  const uint32_t q = n_tiles / kXcds, r = n_tiles % kXcds;
-  return x * q + min(x, r) + i;
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const uint16_t* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, 0x7fffffff, 0x00020000);
-}
-
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* dst, uint32_t off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)dst, 16, off, 0, 0, 0);
-}
-
-// One operand of the tile core: kRows rows of fp16 with k contiguous, from `base` (the tile's
-// first row, k = 0) with row stride `ld` halfs. Each step, every wavefront moves its 1 KiB blocks
-// of the stage with buffer_load_dwordx4 ... lds: lane l fills the block's l-th chunk, so the lane
-// loads the global chunk that the swizzle puts there. Chunks of rows past `rows_valid`, or
-// starting at k >= `k_valid`, get an out-of-range offset and read as zeros.
-template <class S, int kRows>
-struct Loader {
-  static constexpr int kPer = kRows * S::kCpr / S::kThreads;  // DMA instructions per step
-  static constexpr int kRowsPerBlock = 64 / S::kCpr;
-  __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t off[kPer];
-  int kc8[kPer];
-  int k_valid;
-
-  __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int rows_valid,
-                                       int k_valid_, int wave, int lane) {
-    rsrc = buffer_rsrc(base);
-    k_valid = k_valid_;
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int row = kRowsPerBlock * (p * S::kWaves + wave) + lane / S::kCpr;
-      const int kc = (lane % S::kCpr) ^ swz_key<S::kCpr>(row);
-      kc8[p] = kc * 8;
-      off[p] = row < rows_valid ? static_cast<uint32_t>((row * ld + kc * 8) * 2) : kOob;
-    }
-  }
-  // operands of step k0 into the stage block at `dst`
-  __device__ __forceinline__ void issue(unsigned char* dst, int k0, int wave) {
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const uint32_t v = k0 + kc8[p] < k_valid ? off[p] + static_cast<uint32_t>(k0 * 2) : kOob;
-      dma16(rsrc, dst + (p * S::kWaves + wave) * 1024, v);
-    }
-  }
-};
-
-// One step of the wavefront's 128 x 64 block: BK / 16 x (4 A + 2 B fragments, 8 MFMAs).
-template <class S>
-__device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uint4* __restrict__ Bs,
-                                         f32x16 (&acc)[kWM][kWN], int lane, int wm, int wn) {
-  constexpr int kSteps = S::kBK / 16;
-  half8_t a[kSteps][kWM], b[kSteps][kWN];
-#pragma unroll
-  for (int ks = 0; ks < kSteps; ++ks) {
-    const int kc = ks * 2 + (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < kWM; ++i)
-      a[ks][i] = __builtin_bit_cast(half8_t, As[swz<S::kCpr>(wm * 128 + i * 32 + (lane & 31), kc)]);
-#pragma unroll
-    for (int j = 0; j < kWN; ++j)
-      b[ks][j] = __builtin_bit_cast(half8_t, Bs[swz<S::kCpr>(wn * 64 + j * 32 + (lane & 31), kc)]);
-  }
-#pragma unroll
-  for (int ks = 0; ks < kSteps; ++ks)
-#pragma unroll
-    for (int i = 0; i < kWM; ++i)
-#pragma unroll
-      for (int j = 0; j < kWN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
-}
-
-// acc = A B^T over nk steps: A is the 256-row operand, B the BN-row one. Step kt waits for its
-// own DMA group (with three stages the next group stays in flight), one barrier makes every
-// wavefront's data visible and retires the slot read in step kt - 1, which then receives step
-// kt + STAGES - 1.
-template <class S>
-__device__ __forceinline__ void tile_gemm(Loader<S, kBM>& la, Loader<S, S::kBN>& lb,
-                                          unsigned char* smem, int nk, f32x16 (&acc)[kWM][kWN],
-                                          int lane, int wave) {
-  constexpr int kGroup = Loader<S, kBM>::kPer + Loader<S, S::kBN>::kPer;
-  constexpr int kB = S::kAChunks * 16;  // B block offset inside a stage
-  const int wm = wave / (S::kWaves / 2), wn = wave % (S::kWaves / 2);
-#pragma unroll
-  for (int i = 0; i < kWM; ++i)
-#pragma unroll
-    for (int j = 0; j < kWN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-#pragma unroll
-  for (int st = 0; st < S::kStages - 1; ++st)
-    if (st < nk) {
-      la.issue(smem + st * S::kStageBytes, st * S::kBK, wave);
-      lb.issue(smem + st * S::kStageBytes + kB, st * S::kBK, wave);
-    }
-  int s = 0;  // slot of step kt
-  for (int kt = 0; kt < nk; ++kt) {
-    if (S::kStages == 3 && kt + 1 < nk) wait_vmcnt<kGroup>();
-    else wait_vmcnt<0>();
-    lds_barrier();
-    if (kt + S::kStages - 1 < nk) {
-      const int s2 = s == 0 ? S::kStages - 1 : s - 1;  // slot (kt + STAGES - 1) % STAGES
-      la.issue(smem + s2 * S::kStageBytes, (kt + S::kStages - 1) * S::kBK, wave);
-      lb.issue(smem + s2 * S::kStageBytes + kB, (kt + S::kStages - 1) * S::kBK, wave);
-    }
-    const unsigned char* st = smem + s * S::kStageBytes;
-    mma_step<S>(reinterpret_cast<const uint4*>(st), reinterpret_cast<const uint4*>(st + kB), acc,
-                lane, wm, wn);
-    s = s + 1 == S::kStages ? 0 : s + 1;
-  }
-  __syncthreads();  // every wavefront is done with the ring before the caller reuses the LDS
-}
+using Narrow = HeadShape<128, 32, 3>;  // 72 KiB ring
+using Wide = HeadShape<256, 64, 2>;    // 128 KiB ring, 135 KiB with the staged logits tile
+constexpr int kBM = 256;
 
 struct Stat {
   float m, s, t;
@@ -265,21 +104,27 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_logits_kernel(
   const int m0 = mtile * kBM, n0 = ntile * kBN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / (S::kWaves / 2), wn = wave % (S::kWaves / 2);
+  const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 
   Loader<S, kBM> la;
   Loader<S, kBN> lb;
   la.init(H + static_cast<int64_t>(m0) * ldh, ldh, n_rows - m0, K, wave, lane);
   lb.init(W + static_cast<int64_t>(n0) * ldw, ldw, group_cols - n0, K, wave, lane);
-  f32x16 acc[kWM][kWN];
-  tile_gemm<S>(la, lb, smem, (K + S::kBK - 1) / S::kBK, acc, lane, wave);
+  Acc<S> acc;
+  ring_gemm<S>(
+      smem, (K + S::kBK - 1) / S::kBK,
+      [&](unsigned char* slot, int kt) {
+        la.issue(slot, kt * S::kBK, wave);
+        lb.issue(slot + S::kAChunks * 16, kt * S::kBK, wave);
+      },
+      acc, lane, wave);
 
   // Epilogue 1: fp16 logits tile into LDS ([kBM][kZS] halfs).
   uint16_t* Zs = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
-  for (int i = 0; i < kWM; ++i)
+  for (int i = 0; i < S::kFragM; ++i)
 #pragma unroll
-    for (int j = 0; j < kWN; ++j)
+    for (int j = 0; j < S::kFragN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
@@ -472,7 +317,7 @@ struct GradArgs {
 template <class S>
 __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradArgs a) {
   constexpr int kBN = S::kBN;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRingBytes];
 
   // hidden tiles vary fastest inside an XCD's range: the tiles in flight on one XCD share P rows
   const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_tiles));
@@ -489,21 +334,27 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
   const int zc = slice * a.vchunk + k0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / (S::kWaves / 2), wn = wave % (S::kWaves / 2);
+  const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 
   Loader<S, kBM> la;
   Loader<S, kBN> lb;
   la.init(a.Z + static_cast<int64_t>(m0) * a.ldz + zc, a.ldz, a.n_grad - m0, kn, wave, lane);
   lb.init(a.WT + static_cast<int64_t>(n0) * a.ldwt + a.col0 + zc, a.ldwt, a.hidden - n0, kn,
           wave, lane);
-  f32x16 acc[kWM][kWN];
-  tile_gemm<S>(la, lb, smem, (kn + S::kBK - 1) / S::kBK, acc, lane, wave);
+  Acc<S> acc;
+  ring_gemm<S>(
+      smem, (kn + S::kBK - 1) / S::kBK,
+      [&](unsigned char* slot, int kt) {
+        la.issue(slot, kt * S::kBK, wave);
+        lb.issue(slot + S::kAChunks * 16, kt * S::kBK, wave);
+      },
+      acc, lane, wave);
 
   float* Y = a.Y + static_cast<int64_t>(piece) * a.n_grad * a.hidden;
 #pragma unroll
-  for (int i = 0; i < kWM; ++i)
+  for (int i = 0; i < S::kFragM; ++i)
 #pragma unroll
-    for (int j = 0; j < kWN; ++j)
+    for (int j = 0; j < S::kFragN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int gr = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);

@@ -1,0 +1,205 @@
+// The fp16 MFMA tile core shared by the head (head_ce.hip) and the q|k|v projection (qkv.hip):
+// C[BM x BN] = A B^T with both operands k-contiguous, on gfx950.
+//
+// Operands stream from global memory straight into an LDS ring with buffer_load_dwordx4 ... lds
+// (no register staging: lane l of a 1 KiB wavefront block fills the block's l-th 16-byte chunk).
+// Chunks are XOR-swizzled so that the ds_read_b128 fragment reads of v_mfma_f32_32x32x16_f16 are
+// free of bank conflicts. Out-of-range rows / k-chunks get a buffer offset past the descriptor's
+// range and read as zeros, so tails need no branches. One barrier per step; the ring keeps
+// STAGES - 1 steps in flight. Every wavefront owns (BM / WM) x (BN / WN) of the tile.
+#pragma once
+
+#include "common.h"
+
+namespace talm {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int kXcds = 8;
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every range: the load returns 0
+
+// A BM x BN output tile in BK-deep steps through a STAGES-slot LDS ring, WM x WN wavefronts.
+// `kPerCu` workgroups share a CU so that two wavefronts run per SIMD.
+template <int BM, int BN, int BK, int STAGES, int WM, int WN>
+struct TileShape {
+  static constexpr int kBM = BM, kBN = BN, kBK = BK, kStages = STAGES;
+  static constexpr int kWaves = WM * WN, kWavesN = WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kWaveM = BM / WM, kWaveN = BN / WN;  // the wavefront's share of the tile
+  static constexpr int kFragM = kWaveM / 32, kFragN = kWaveN / 32;  // 32x32 MFMA blocks
+  static constexpr int kCpr = BK / 8;                         // 16-byte chunks per row of a stage
+  static constexpr int kAChunks = BM * kCpr, kBChunks = BN * kCpr;
+  static constexpr int kStageBytes = (kAChunks + kBChunks) * 16;
+  static constexpr int kRing = STAGES * kStageBytes;
+  static constexpr int kPerCu = 512 / kThreads;
+  static_assert(STAGES == 2 || STAGES == 3, "ring depth");
+  static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "32x32 MFMA blocks");
+  static_assert(BK == 32 || BK == 64, "swizzle keys exist for 4 and 8 chunks per row");
+  static_assert(kRing <= 160 * 1024, "LDS per CU");
+};
+
+// [rows][BK] fp16 stage as 16-byte chunks, CPR per row. The chunk column is XOR-ed with a key of
+// the row so that the rows read by one ds_read_b128 phase (8 consecutive rows on 32 banks, 16 on
+// 64 banks, one chunk column) land on distinct banks: ((row >> 1) ^ (row >> 2)) & 3 for 64-byte
+// rows, (row ^ (row >> 3)) & 7 for 128-byte rows.
+template <int CPR>
+__device__ __forceinline__ int swz_key(int row) {
+  if constexpr (CPR == 4) return ((row >> 1) ^ (row >> 2)) & 3;
+  else return (row ^ (row >> 3)) & 7;
+}
+template <int CPR>
+__device__ __forceinline__ int swz(int row, int kc) { return row * CPR + (kc ^ swz_key<CPR>(row)); }
+
+// Wait until at most N vector-memory operations of this wavefront are outstanding (vmcnt only).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that orders LDS accesses only: the LDS reads issued before it have returned
+// (lgkmcnt 0), and the compiler moves no memory access across it. Unlike __syncthreads() it does
+// not drain the wavefront's outstanding buffer ... lds transfers, which the ring keeps in flight
+// and waits for with wait_vmcnt.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on XCD b % 8). Give
+// each XCD one contiguous range of tile indices (a bijection for any tile count), so tiles that
+// are neighbours in the caller's order share that XCD's L2.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t bid, uint32_t n_tiles) {
+  const uint32_t x = bid % kXcds, i = bid / kXcds;
+  const uint32_t q = n_tiles / kXcds, r = n_tiles % kXcds;
+  return x * q + min(x, r) + i;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const uint16_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)dst, 16, off, 0, 0, 0);
+}
+
+// One operand of the tile: kRows rows of fp16 with k contiguous, from `base` (the tile's first
+// row, k = 0) with row stride `ld` halfs (row * ld * 2 below 2^31). Each step every wavefront
+// moves its 1 KiB blocks of the stage: lane l loads the global chunk that the swizzle puts at
+// the block's l-th chunk. Chunks of rows past `rows_valid`, or starting outside
+// [k_lo, k_valid), get an out-of-range offset and read as zeros (only in-window chunks are read,
+// so `base` may point before the operand when k_lo > 0).
+template <class S, int kRows>
+struct Loader {
+  static constexpr int kPer = kRows * S::kCpr / S::kThreads;  // DMA instructions per step
+  static constexpr int kRowsPerBlock = 64 / S::kCpr;
+  static_assert(kPer * S::kThreads == kRows * S::kCpr, "whole 1 KiB blocks per wavefront");
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[kPer];
+  int kc8[kPer];
+  int k_lo, k_valid;
+
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int rows_valid,
+                                       int k_valid_, int wave, int lane, int k_lo_ = 0) {
+    rsrc = buffer_rsrc(base);
+    k_lo = k_lo_;
+    k_valid = k_valid_;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int row = kRowsPerBlock * (p * S::kWaves + wave) + lane / S::kCpr;
+      const int kc = (lane % S::kCpr) ^ swz_key<S::kCpr>(row);
+      kc8[p] = kc * 8;
+      off[p] = row < rows_valid ? static_cast<uint32_t>((row * ld + kc * 8) * 2) : kOob;
+    }
+  }
+  // operands of step k0 into the stage block at `dst`
+  __device__ __forceinline__ void issue(unsigned char* dst, int k0, int wave) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int k = k0 + kc8[p];
+      const uint32_t v = k >= k_lo && k < k_valid ? off[p] + static_cast<uint32_t>(k0 * 2) : kOob;
+      dma16(rsrc, dst + (p * S::kWaves + wave) * 1024, v);
+    }
+  }
+};
+
+template <class S>
+using Acc = f32x16[S::kFragM][S::kFragN];
+
+// One step of the wavefront's block: BK / 16 x (kFragM A + kFragN B fragments, their MFMAs).
+template <class S>
+__device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uint4* __restrict__ Bs,
+                                         Acc<S>& acc, int lane, int wm, int wn) {
+  constexpr int kSteps = S::kBK / 16;
+  half8_t a[kSteps][S::kFragM], b[kSteps][S::kFragN];
+#pragma unroll
+  for (int ks = 0; ks < kSteps; ++ks) {
+    const int kc = ks * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < S::kFragM; ++i)
+      a[ks][i] = __builtin_bit_cast(
+          half8_t, As[swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), kc)]);
+#pragma unroll
+    for (int j = 0; j < S::kFragN; ++j)
+      b[ks][j] = __builtin_bit_cast(
+          half8_t, Bs[swz<S::kCpr>(wn * S::kWaveN + j * 32 + (lane & 31), kc)]);
+  }
+#pragma unroll
+  for (int ks = 0; ks < kSteps; ++ks)
+#pragma unroll
+    for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < S::kFragN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
+}
+
+// acc = sum over nk steps. issue(slot, kt) enqueues step kt's A block at `slot` and its B block
+// at slot + A bytes, exactly Loader<S, BM>::kPer + Loader<S, BN>::kPer DMA instructions per
+// thread. Step kt waits for its own group (with three slots the next group stays in flight); one
+// barrier makes every wavefront's data visible and retires the slot read in step kt - 1, which
+// then receives step kt + STAGES - 1.
+template <class S, class Issue>
+__device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& issue, Acc<S>& acc,
+                                          int lane, int wave) {
+  constexpr int kGroup = Loader<S, S::kBM>::kPer + Loader<S, S::kBN>::kPer;
+  const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
+#pragma unroll
+  for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+    for (int j = 0; j < S::kFragN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+#pragma unroll
+  for (int st = 0; st < S::kStages - 1; ++st)
+    if (st < nk) issue(smem + st * S::kStageBytes, st);
+  int s = 0;  // slot of step kt
+  for (int kt = 0; kt < nk; ++kt) {
+    if (S::kStages == 3 && kt + 1 < nk) wait_vmcnt<kGroup>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (kt + S::kStages - 1 < nk) {
+      const int s2 = s == 0 ? S::kStages - 1 : s - 1;  // slot (kt + STAGES - 1) % STAGES
+      issue(smem + s2 * S::kStageBytes, kt + S::kStages - 1);
+    }
+    const unsigned char* st = smem + s * S::kStageBytes;
+    mma_step<S>(reinterpret_cast<const uint4*>(st),
+                reinterpret_cast<const uint4*>(st + S::kAChunks * 16), acc, lane, wm, wn);
+    s = s + 1 == S::kStages ? 0 : s + 1;
+  }
+  __syncthreads();  // every wavefront is done with the ring before the caller reuses the LDS
+}
+
+// Row and column, inside the tile, of accumulator element v of 32x32 block (i, j) on `lane`.
+template <class S>
+__device__ __forceinline__ int acc_row(int wm, int i, int v, int lane) {
+  return wm * S::kWaveM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+}
+template <class S>
+__device__ __forceinline__ int acc_col(int wn, int j, int lane) {
+  return wn * S::kWaveN + j * 32 + (lane & 31);
+}
+
+}  // namespace
+}  // namespace talm

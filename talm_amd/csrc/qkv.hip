@@ -1,0 +1,306 @@
+// The q|k|v projection of a decoder layer with its LoRA adapters, on gfx950 fp16 MFMA.
+//
+// The reference (solution/fused_proj.py:88-218 with PEFT's LoRA arithmetic, solution/lora.py:
+// 151-231) computes [q|k|v] = x W^T + b as one GEMM, then per adapter t = x A^T,
+// branch = t B^T and out[:, seg] += scaling * branch, and the rotary embedding on q and k.
+// Here that is two launches:
+//   lora_down   t = x A_g^T for every adapter g (rank 16 each) and ts = scaling_g * t: a
+//               register-only v_mfma_f32_16x16x32_f16 kernel, the reduction split over the four
+//               wavefronts of a workgroup (t is what the backward keeps, as in the reference).
+//   qkv_fwd     out = [x | ts] [W | B]^T + b with the rotary embedding applied in the epilogue:
+//               the LoRA up-projection is one more 64-deep step of the tile GEMM (the adapter's
+//               16 columns of ts against its 16 columns of B, zeros elsewhere), so the adapter
+//               term is accumulated in fp32 with the base product and rounded once. Tiles of
+//               128 columns are whole heads, so the epilogue rotates each (j, j + 64) pair of
+//               the staged fp16 tile in LDS before the coalesced store.
+#include "mfma_tile.h"
+
+namespace talm {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRank = 16;         // LoRA rank of the MFMA path (one 16x16x32 column block)
+constexpr int kMaxAdapters = 2;
+
+// ------------------------------------------------------------------------------------------
+// t[r][16 g + i] = fp16(sum_k x[r][k] A_g[i][k]); ts = fp16(scaling_g * the same fp32 sum).
+// One workgroup per 16 tokens, wavefront w takes the 32-deep k-steps w, w + 4, ...
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void lora_down_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int n_tokens, int hidden,
+    const uint16_t* __restrict__ a0, const uint16_t* __restrict__ a1, int n_adapters, float s0,
+    float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts, int64_t ldt) {
+  __shared__ float red[4][kMaxAdapters][16][16 + 1];
+  const int m0 = blockIdx.x * 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = lane & 15, kq = 8 * (lane >> 4);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x + static_cast<int64_t>(m0) * ldx);
+  const __amdgpu_buffer_rsrc_t ra0 = buffer_rsrc(a0);
+  const __amdgpu_buffer_rsrc_t ra1 = buffer_rsrc(n_adapters > 1 ? a1 : a0);
+  const uint32_t xoff = m0 + row < n_tokens ? static_cast<uint32_t>((row * ldx + kq) * 2) : kOob;
+  const uint32_t aoff = static_cast<uint32_t>((row * hidden + kq) * 2);
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = wave * 32; k0 < hidden; k0 += 128) {
+    const uint32_t kb = static_cast<uint32_t>(k0 * 2);
+    const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff + kb, 0, 0));
+    const half8_t b0 = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra0, aoff + kb, 0, 0));
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b0, acc0, 0, 0, 0);
+    if (n_adapters > 1) {
+      const half8_t b1 = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra1, aoff + kb, 0, 0));
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b1, acc1, 0, 0, 0);
+    }
+  }
+  // accumulator element v of lane l: token 4 * (l / 16) + v, rank l % 16
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    red[wave][0][4 * (lane >> 4) + v][lane & 15] = acc0[v];
+    red[wave][1][4 * (lane >> 4) + v][lane & 15] = acc1[v];
+  }
+  __syncthreads();
+  const int tid = threadIdx.x;
+  for (int e = tid; e < n_adapters * 256; e += 256) {
+    const int g = e >> 8, r = (e >> 4) & 15, i = e & 15;
+    if (m0 + r >= n_tokens) continue;
+    const float sum = red[0][g][r][i] + red[1][g][r][i] + red[2][g][r][i] + red[3][g][r][i];
+    const int64_t at = static_cast<int64_t>(m0 + r) * ldt + g * kRank + i;
+    t[at] = f2h(sum);
+    ts[at] = f2h((g == 0 ? s0 : s1) * sum);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// out = [x | ts] [W | B]^T + bias, rotary embedding on the columns below rope_cols.
+// ------------------------------------------------------------------------------------------
+using QkvShape = TileShape<128, 128, 64, 2, 2, 2>;  // 4 wavefronts of 64 x 64, 64 KiB ring
+constexpr int kQZS = 128 + 8;                       // staged tile row stride (halfs)
+static_assert(128 * kQZS * 2 <= QkvShape::kRing, "the staged tile reuses the ring");
+
+// An operand whose k range has two parts: steps [0, nk1) read `base1` (k < k1), one more step
+// reads `base2` (k in [lo2, hi2)). The per-lane row and chunk do not depend on the part; the
+// part's base, stride and bounds are chosen by value each step (scalar selects), so nothing is
+// indexed through a selected address and the loader stays in registers.
+template <class S, int kRows>
+struct TwoPartLoader {
+  static constexpr int kPer = Loader<S, kRows>::kPer;
+  static constexpr int kRowsPerBlock = Loader<S, kRows>::kRowsPerBlock;
+  __amdgpu_buffer_rsrc_t r1, r2;
+  int row[kPer], kc8[kPer];
+  int ld1, ld2, rows1, rows2, k1, lo2, hi2, nk1;
+
+  __device__ __forceinline__ void init(const uint16_t* base1, int64_t ld1_, int rows1_, int k1_,
+                                       const uint16_t* base2, int64_t ld2_, int rows2_, int lo2_,
+                                       int hi2_, int wave, int lane) {
+    r1 = buffer_rsrc(base1);
+    r2 = buffer_rsrc(base2);
+    ld1 = static_cast<int>(ld1_);
+    ld2 = static_cast<int>(ld2_);
+    rows1 = rows1_;
+    rows2 = rows2_;
+    k1 = k1_;
+    lo2 = lo2_;
+    hi2 = hi2_;
+    nk1 = (k1_ + S::kBK - 1) / S::kBK;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      row[p] = kRowsPerBlock * (p * S::kWaves + wave) + lane / S::kCpr;
+      kc8[p] = ((lane % S::kCpr) ^ swz_key<S::kCpr>(row[p])) * 8;
+    }
+  }
+  __device__ __forceinline__ void issue(unsigned char* dst, int kt, int wave) {
+    const bool second = kt >= nk1;
+    const int k0 = second ? 0 : kt * S::kBK;
+    const __amdgpu_buffer_rsrc_t r = second ? r2 : r1;
+    const int ld = second ? ld2 : ld1, rows = second ? rows2 : rows1;
+    const int lo = second ? lo2 : 0, hi = second ? hi2 : k1;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int k = k0 + kc8[p];
+      const uint32_t v = row[p] < rows && k >= lo && k < hi
+                             ? static_cast<uint32_t>((row[p] * ld + k) * 2)
+                             : kOob;
+      dma16(r, dst + (p * S::kWaves + wave) * 1024, v);
+    }
+  }
+};
+
+struct QkvArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  int n_tokens, hidden;
+  const uint16_t* w;      // [n_out][ldw], the layer group's q|k|v rows
+  int64_t ldw;
+  int n_out;
+  const uint16_t* bias;   // [n_out] or null
+  const uint16_t* ts;     // [n_tokens][ldt]: scaling_g * x A_g^T in columns [16 g, 16 g + 16)
+  int64_t ldt;
+  int n_adapters;
+  const uint16_t* b[kMaxAdapters];  // B_g [seg_end - seg_begin][16]
+  int seg_begin[kMaxAdapters], seg_end[kMaxAdapters];
+  const float* cos;       // [n_tokens][cs_stride] or null (no rotary embedding)
+  const float* sin;
+  int64_t cs_stride;
+  int rope_cols;          // columns [0, rope_cols) are heads of 128 to rotate
+  uint16_t* out;          // [n_tokens][ldo]
+  int64_t ldo;
+  int n_mtiles, n_ntiles;
+};
+
+__global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void qkv_fwd_kernel(QkvArgs a) {
+  using S = QkvShape;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing];
+  const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_mtiles * a.n_ntiles));
+  const int ntile = static_cast<int>(tile / a.n_mtiles), mtile = static_cast<int>(tile % a.n_mtiles);
+  const int m0 = mtile * S::kBM, n0 = ntile * S::kBN;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
+
+  // the adapter whose output columns hold this tile (segments are whole tiles); selected with
+  // conditionals, not by indexing the argument arrays (which would copy them to scratch)
+  const bool in0 = a.n_adapters > 0 && n0 >= a.seg_begin[0] && n0 < a.seg_end[0];
+  const bool in1 = a.n_adapters > 1 && n0 >= a.seg_begin[1] && n0 < a.seg_end[1];
+  const int g = in1 ? 1 : (in0 ? 0 : -1);
+  const int gc = g > 0 ? g : 0;
+  const uint16_t* bg = gc ? a.b[1] : a.b[0];
+  const int sb = gc ? a.seg_begin[1] : a.seg_begin[0], se = gc ? a.seg_end[1] : a.seg_end[0];
+  // A: x, then columns [16 g, 16 g + 16) of ts; B: W's rows, then B_g's (indexed from k = 16 g)
+  TwoPartLoader<S, S::kBM> la;
+  TwoPartLoader<S, S::kBN> lb;
+  la.init(a.x + static_cast<int64_t>(m0) * a.ldx, a.ldx, a.n_tokens - m0, a.hidden,
+          a.ts + static_cast<int64_t>(m0) * a.ldt, a.ldt, a.n_tokens - m0, kRank * gc,
+          kRank * (gc + 1), wave, lane);
+  lb.init(a.w + static_cast<int64_t>(n0) * a.ldw, a.ldw, a.n_out - n0, a.hidden,
+          bg + static_cast<int64_t>(n0 - sb) * kRank - kRank * gc, kRank, se - n0, kRank * gc,
+          kRank * (gc + 1), wave, lane);
+  const int nk1 = (a.hidden + S::kBK - 1) / S::kBK;
+  Acc<S> acc;
+  ring_gemm<S>(
+      smem, nk1 + (g >= 0 ? 1 : 0),
+      [&](unsigned char* slot, int kt) {
+        la.issue(slot, kt, wave);
+        lb.issue(slot + S::kAChunks * 16, kt, wave);
+      },
+      acc, lane, wave);
+
+  // Epilogue: + bias, fp16, staged in LDS ([128][kQZS] halfs)
+  uint16_t* Zs = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+    for (int j = 0; j < S::kFragN; ++j) {
+      const int col = acc_col<S>(wn, j, lane);
+      const float bv = a.bias && n0 + col < a.n_out ? h2f(a.bias[n0 + col]) : 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) Zs[acc_row<S>(wm, i, v, lane) * kQZS + col] = f2h(acc[i][j][v] + bv);
+    }
+  __syncthreads();
+  if (a.cos && n0 < a.rope_cols) {
+    // one head: y1 = x1 c1 - x2 s1, y2 = x2 c2 + x1 s2 on the pairs (j, j + 64)
+    for (int e = tid; e < S::kBM * 64; e += S::kThreads) {
+      const int row = e >> 6, j = e & 63, gr = m0 + row;
+      if (gr >= a.n_tokens) continue;
+      const float* cr = a.cos + static_cast<int64_t>(gr) * a.cs_stride;
+      const float* sr = a.sin + static_cast<int64_t>(gr) * a.cs_stride;
+      const float x1 = h2f(Zs[row * kQZS + j]), x2 = h2f(Zs[row * kQZS + j + 64]);
+      Zs[row * kQZS + j] = f2h(x1 * cr[j] - x2 * sr[j]);
+      Zs[row * kQZS + j + 64] = f2h(x2 * cr[j + 64] + x1 * sr[j + 64]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int it = 0; it < (S::kBM * S::kBN / 8) / S::kThreads; ++it) {
+    const int c = it * S::kThreads + tid, row = c >> 4, kc = c & 15;
+    const int gr = m0 + row, gc = n0 + kc * 8;
+    if (gr < a.n_tokens && gc < a.n_out)
+      *reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(gr) * a.ldo + gc) =
+          *reinterpret_cast<const uint4*>(Zs + row * kQZS + kc * 8);
+  }
+}
+
+bool fits32(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t{1} << 31); }
+
+}  // namespace
+}  // namespace talm
+
+using namespace talm;
+
+TALM_API int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
+                            const uint16_t* a0, const uint16_t* a1, int32_t n_adapters,
+                            float scaling0, float scaling1, uint16_t* t, uint16_t* ts,
+                            int64_t ldt, void* stream) {
+  if (n_tokens < 0 || hidden < 32 || hidden % 32 || ldx < hidden || ldx % 8 || n_adapters < 1 ||
+      n_adapters > kMaxAdapters || ldt < kRank * n_adapters || !fits32(16, ldx) ||
+      !fits32(16, hidden) || n_tokens > (1 << 30))
+    return fail(TALM_EINVAL,
+                "lora_down: bad shape (tokens %lld, hidden %lld, ldx %lld, adapters %d, ldt "
+                "%lld): hidden a multiple of 32, 1-2 adapters of rank 16",
+                (long long)n_tokens, (long long)hidden, (long long)ldx, n_adapters, (long long)ldt);
+  if (n_tokens == 0) return ok();
+  if (!x || !a0 || (n_adapters > 1 && !a1) || !t || !ts)
+    return fail(TALM_EINVAL, "lora_down: null pointer");
+  if (!aligned(x, 16) || !aligned(a0, 16) || (a1 && !aligned(a1, 16)))
+    return fail(TALM_EINVAL, "lora_down: x and the A matrices must be 16-byte aligned");
+  hipLaunchKernelGGL(lora_down_kernel, dim3(static_cast<unsigned>((n_tokens + 15) / 16)), dim3(256),
+                     0, as_stream(stream), x, ldx, static_cast<int>(n_tokens),
+                     static_cast<int>(hidden), a0, a1, n_adapters, scaling0, scaling1, t, ts, ldt);
+  return check_launch("lora_down");
+}
+
+TALM_API int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
+                               const uint16_t* weight, int64_t ldw, int64_t n_out,
+                               const uint16_t* bias, const uint16_t* ts, int64_t ldt,
+                               int32_t n_adapters, const uint16_t* b0, int64_t seg0_begin,
+                               int64_t seg0_end, const uint16_t* b1, int64_t seg1_begin,
+                               int64_t seg1_end, const float* cos, const float* sin,
+                               int64_t cs_stride, int64_t rope_cols, uint16_t* out, int64_t ldo,
+                               void* stream) {
+  using S = QkvShape;
+  if (n_tokens < 0 || hidden < 8 || hidden % 8 || ldx < hidden || ldx % 8 || n_out < 1 ||
+      ldw < hidden || ldw % 8 || ldo < n_out || ldo % 8 || n_adapters < 0 ||
+      n_adapters > kMaxAdapters || n_tokens > (1 << 30) || n_out > (1 << 30) ||
+      !fits32(S::kBM, ldx) || !fits32(S::kBN, ldw))
+    return fail(TALM_EINVAL,
+                "qkv_lora_fwd: bad shape (tokens %lld, hidden %lld, n_out %lld, ldx %lld, ldw "
+                "%lld, ldo %lld, adapters %d)",
+                (long long)n_tokens, (long long)hidden, (long long)n_out, (long long)ldx,
+                (long long)ldw, (long long)ldo, n_adapters);
+  const int64_t begins[2] = {seg0_begin, seg1_begin}, ends[2] = {seg0_end, seg1_end};
+  for (int g = 0; g < n_adapters; ++g)
+    if (begins[g] < 0 || ends[g] <= begins[g] || ends[g] > n_out || begins[g] % S::kBN ||
+        (ends[g] % S::kBN && ends[g] != n_out))
+      return fail(TALM_EINVAL,
+                  "qkv_lora_fwd: adapter %d columns [%lld, %lld) must be whole %d-column tiles "
+                  "of [0, %lld)",
+                  g, (long long)begins[g], (long long)ends[g], S::kBN, (long long)n_out);
+  if (n_adapters > 0 && ldt < kRank * n_adapters)
+    return fail(TALM_EINVAL, "qkv_lora_fwd: ldt %lld < %d", (long long)ldt, kRank * n_adapters);
+  if (cos && (rope_cols < 0 || rope_cols % 128 || rope_cols > n_out || cs_stride < 128))
+    return fail(TALM_EINVAL,
+                "qkv_lora_fwd: rotary columns %lld must be whole 128-column heads of the output "
+                "(cos/sin row stride %lld >= 128)",
+                (long long)rope_cols, (long long)cs_stride);
+  if (n_tokens == 0) return ok();
+  if (!x || !weight || !out || (n_adapters > 0 && (!ts || !b0)) || (n_adapters > 1 && !b1) ||
+      (cos && !sin))
+    return fail(TALM_EINVAL, "qkv_lora_fwd: null pointer");
+  if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, 16) || (ts && !aligned(ts, 16)) ||
+      (b0 && !aligned(b0, 16)) || (b1 && !aligned(b1, 16)))
+    return fail(TALM_EINVAL, "qkv_lora_fwd: x, weight, out, ts and B must be 16-byte aligned");
+  QkvArgs a{};
+  a.x = x; a.ldx = ldx; a.n_tokens = static_cast<int>(n_tokens); a.hidden = static_cast<int>(hidden);
+  a.w = weight; a.ldw = ldw; a.n_out = static_cast<int>(n_out); a.bias = bias;
+  a.ts = ts; a.ldt = ldt; a.n_adapters = n_adapters;
+  a.b[0] = b0; a.b[1] = b1;
+  for (int g = 0; g < 2; ++g) {
+    a.seg_begin[g] = static_cast<int>(begins[g]);
+    a.seg_end[g] = static_cast<int>(ends[g]);
+  }
+  a.cos = cos; a.sin = sin; a.cs_stride = cs_stride; a.rope_cols = static_cast<int>(rope_cols);
+  a.out = out; a.ldo = ldo;
+  a.n_mtiles = static_cast<int>((n_tokens + S::kBM - 1) / S::kBM);
+  a.n_ntiles = static_cast<int>((n_out + S::kBN - 1) / S::kBN);
+  hipLaunchKernelGGL(qkv_fwd_kernel, dim3(static_cast<unsigned>(a.n_mtiles * a.n_ntiles)),
+                     dim3(S::kThreads), 0, as_stream(stream), a);
+  return check_launch("qkv_lora_fwd");
+}

@@ -7,6 +7,11 @@ added with PEFT's ops in PEFT's order (lora.py), v is returned as a fresh tensor
 views. Backward: dX = [dq|dk|dv] [Wq; Wk; Wv] in one GEMM (K = 2048) plus the adapters' input
 gradients, and the adapters' weight gradients.
 
+On MI355X the forward runs as two launches when it can (`_mfma_ok`): talm_lora_down (t = x A^T
+of both adapters) and talm_qkv_lora_fwd, one fp16 MFMA GEMM [x | s t] [W | B]^T + b that also
+rotates q and k in its epilogue (qkv.hip); otherwise the ops below. SOLUTION_DISABLE_QKV_MFMA=1
+keeps the ops.
+
 MI355X addition: with `rope=(cos, sin)` the node also applies the rotary embedding to q and k IN
 PLACE on its own output (the rope kernel reads each rotation pair before writing it), and in the
 backward rotates dq and dk back in place inside the concatenated gradient it builds for the dX
@@ -14,6 +19,8 @@ GEMM anyway: no RoPE node, no new q/k tensors, no strided gradient copies. This 
 the node keeps only x for its backward (the reference notes this: q and k are views of the
 node's output that nothing else reads before the attention).
 """
+
+import os
 
 import torch
 import torch.nn.functional as F
@@ -24,6 +31,7 @@ from .rope import rope_
 from .state import DISABLED, fallback
 
 Q, K, V, O, GATE, UP, DOWN = range(7)
+QKV_MFMA = os.environ.get("SOLUTION_DISABLE_QKV_MFMA") != "1"
 COUNTS = {"attn": 0, "attn_fallback": 0}
 
 
@@ -57,12 +65,34 @@ class FusedProjections(torch.autograd.Function):
             bounds.append(bounds[-1] + size)
         weight = group.span("fwd", first, last)
         ctx.fetched = weight is not None
-        out = F.linear(x2, weight, group.span_bias(first, last))
+        bias = group.span_bias(first, last)
+        halves = [_to_half(lora_weights[2 * k], lora_weights[2 * k + 1])
+                  for k in range(len(adapters))]
+        mfma = None
+        if _mfma_ok(x2, weight, bias, bounds, adapters, halves, rope, head_dim):
+            try:
+                mfma = _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope)
+            except Exception as exc:  # noqa: BLE001 - state.py convention
+                if not fallback("qkv_mfma", exc):
+                    raise
+        if mfma is not None:
+            out, t = mfma
+            del weight
+            saved = [x2]
+            for k in range(len(adapters)):
+                states.append(None)
+                saved += [t[:, 16 * k:16 * (k + 1)], halves[k][0], halves[k][1]]
+            if rope is not None:
+                saved += list(rope)
+                RAN["rope"] += 1
+            RAN["qkv_mfma"] += 1
+            return FusedProjections._finish(ctx, x, out, sizes, bounds, compact, saved, group,
+                                            first, last, adapters, states, rope, head_dim)
+        out = F.linear(x2, weight, bias)
         del weight
-        results = [None] * len(sizes)
         saved = [x2]
         for k, (seg, scaling, p) in enumerate(adapters):
-            a16, b16 = _to_half(lora_weights[2 * k], lora_weights[2 * k + 1])
+            a16, b16 = halves[k]
             state = None
             if p > 0:
                 state = torch.cuda.get_rng_state(x.device)
@@ -87,6 +117,13 @@ class FusedProjections(torch.autograd.Function):
             rope_(q, k, cos, sin, backward=False)
             RAN["rope"] += 1
             saved += [cos, sin]
+        return FusedProjections._finish(ctx, x, out, sizes, bounds, compact, saved, group, first,
+                                        last, adapters, states, rope, head_dim)
+
+    @staticmethod
+    def _finish(ctx, x, out, sizes, bounds, compact, saved, group, first, last, adapters, states,
+                rope, head_dim):
+        results = [None] * len(sizes)
         for seg in range(len(sizes)):
             base = out[:, bounds[seg]:bounds[seg + 1]]
             results[seg] = base.contiguous() if seg in compact else base
@@ -165,6 +202,54 @@ class FusedProjections(torch.autograd.Function):
             del xd, mask
         dx = None if dx is None else dx.view(ctx.x_shape)
         return (dx, None, None, None, None, None, None, None, *lora_grads)
+
+
+def _mfma_ok(x2, weight, bias, bounds, adapters, halves, rope, head_dim):
+    """Whether the q|k|v node's forward can run as talm_lora_down + talm_qkv_lora_fwd: fp16
+    operands with unit column strides and 16-byte rows, at most two adapters of rank 16 without
+    dropout on whole 128-column tiles, the rotary embedding (if any) on 128-wide heads."""
+    if not QKV_MFMA or "qkv_mfma" in DISABLED or weight is None or len(adapters) > 2:
+        return False
+    n_out, size = bounds[-1], x2.shape[1]
+    if not (x2.dtype == weight.dtype == torch.float16 and x2.stride(1) == 1
+            and weight.stride(1) == 1 and x2.stride(0) % 8 == 0 and weight.stride(0) % 8 == 0
+            and x2.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0
+            and tuple(weight.shape) == (n_out, size) and size % 8 == 0):
+        return False
+    if bias is not None and not (bias.dtype == torch.float16 and bias.is_contiguous()):
+        return False
+    if adapters and size % 32:
+        return False
+    for (seg, _scaling, p), (a16, b16) in zip(adapters, halves):
+        lo, hi = bounds[seg], bounds[seg + 1]
+        if p > 0 or tuple(a16.shape) != (16, size) or tuple(b16.shape) != (hi - lo, 16) \
+                or not (a16.is_contiguous() and b16.is_contiguous()) \
+                or lo % 128 or (hi % 128 and hi != n_out):
+            return False
+    if rope is not None and (head_dim != 128 or len(bounds) < 3 or bounds[2] % 128):
+        return False
+    return True
+
+
+def _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope):
+    """[q|k|v] (+ LoRA, + RoPE on q and k) on MFMA: returns the [N, n_out] output and the
+    adapters' t = x A^T ([N, 16 per adapter], what the backward keeps)."""
+    n, n_out = x2.shape[0], bounds[-1]
+    t = ts = None
+    if adapters:
+        t = torch.empty(n, 16 * len(adapters), dtype=torch.float16, device=x2.device)
+        ts = torch.empty_like(t)
+        a1 = halves[1][0] if len(adapters) > 1 else None
+        s1 = adapters[1][1] if len(adapters) > 1 else 0.0
+        torch.ops.talm.lora_down(x2, halves[0][0], a1, adapters[0][1], s1, t, ts)
+    segs = [(bounds[seg], bounds[seg + 1]) for seg, _s, _p in adapters] + [(0, 0)] * 2
+    bs = [b16 for _a, b16 in halves] + [None] * 2
+    cos, sin = rope if rope is not None else (None, None)
+    out = torch.empty(n, n_out, dtype=torch.float16, device=x2.device)
+    torch.ops.talm.qkv_lora_fwd(x2, weight, bias, ts, bs[0], segs[0][0], segs[0][1], bs[1],
+                                segs[1][0], segs[1][1], cos, sin,
+                                bounds[2] if rope is not None else 0, out)
+    return out, t
 
 
 _HOOK_DICTS = ("_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks")

@@ -35,6 +35,7 @@ COMPONENTS = {
     "qgroup": "grouped NF4 dequantization -> the 4-bit linear's own forward",
     "lora": "the LoRA projection node -> the LoRA linear's own forward",
     "fused_proj": "q|k|v as one GEMM node -> transformers' attention forward",
+    "qkv_mfma": "q|k|v + LoRA + RoPE forward on MFMA -> the node's hipBLASLt GEMMs",
     "nf4_dequant": "per-projection NF4 dequantization kernel",
     "mlp_save_up": "opt-in MLP keeping only up and its input -> the MLP forward before it",
 }

@@ -1,0 +1,117 @@
+"""Parity of the q|k|v projection on MFMA (talm_lora_down, talm_qkv_lora_fwd) with float32
+references of the same arithmetic: the reference's node is x W^T + b, per adapter
+t = x A^T, + scaling * t B^T on its columns, then the rotary embedding of q and k
+(solution/fused_proj.py:88-218, solution/lora.py:151-231, solution/rope.py:145-157).
+
+Bars: t within one fp16 rounding of fp16(x A^T) (fp32 sums in another order); the projection
+within 2e-3 relative + 2e-3 x the output's scale (fp16 operands, one rounding of an fp32 sum, the
+reference rounds the adapter branch separately: solution/test_fused_proj.py:27-31 compares to
+GEMM rounding); whole-model use is covered by tests/test_gpu_step.py."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _rope_tables(n, dim=128, theta=1e6, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.randint(0, 512, (n,), generator=g).double()
+    inv = 1.0 / theta ** (torch.arange(0, dim, 2).double() / dim)
+    ang = pos[:, None] * inv[None]
+    ang = torch.cat((ang, ang), -1)
+    return ang.cos().float().to(DEV), ang.sin().float().to(DEV)
+
+
+def _rotate(y, cos, sin, cols):
+    y = y.clone()
+    n = y.shape[0]
+    heads = y[:, :cols].view(n, -1, 128)
+    x1, x2 = heads[..., :64].clone(), heads[..., 64:].clone()
+    c, s = cos[:, None], sin[:, None]
+    heads[..., :64] = x1 * c[..., :64] - x2 * s[..., :64]
+    heads[..., 64:] = x2 * c[..., 64:] + x1 * s[..., 64:]
+    return y
+
+
+def _inputs(n, size, n_out, segs, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, size, generator=g).half().to(DEV)
+    w = (torch.randn(n_out, size, generator=g) * size ** -0.5).half().to(DEV)
+    bias = (torch.randn(n_out, generator=g) * 0.1).half().to(DEV)
+    a = [(torch.rand(16, size, generator=g) * 2 - 1).mul(size ** -0.5).half().to(DEV) for _ in segs]
+    b = [(torch.randn(hi - lo, 16, generator=g) * 0.05).half().to(DEV) for lo, hi in segs]
+    return x, w, bias, a, b
+
+
+@pytest.mark.parametrize("n,size,adapters", [(1130, 1536, 2), (37, 64, 1), (1, 32, 2),
+                                             (300, 1536, 1)])
+def test_lora_down_matches_fp32(n, size, adapters):
+    _case(f"lora_down n={n} H={size} adapters={adapters}")
+    segs = [(0, 128), (128, 256)][:adapters]
+    x, _w, _b, a, _bb = _inputs(n, size, 256, segs, seed=n + size)
+    t = torch.empty(n, 16 * adapters, dtype=torch.float16, device=DEV)
+    ts = torch.empty_like(t)
+    scalings = [2.0, 0.75][:adapters] + [0.0]
+    torch.ops.talm.lora_down(x, a[0], a[1] if adapters > 1 else None, scalings[0], scalings[1],
+                             t, ts)
+    for g in range(adapters):
+        ref = x.float() @ a[g].float().t()
+        got = t[:, 16 * g:16 * (g + 1)].float()
+        assert torch.all((got - ref).abs() <= 2.0 ** -10 * ref.abs() + 1e-6 * size), g
+        got_s = ts[:, 16 * g:16 * (g + 1)].float()
+        ref_s = ref * scalings[g]
+        assert torch.all((got_s - ref_s).abs() <= 2.0 ** -10 * ref_s.abs() + 1e-6 * size), g
+
+
+@pytest.mark.parametrize("n,size,n_out,segs,rope_cols,with_bias", [
+    (1130, 1536, 2048, [(0, 1536), (1792, 2048)], 1792, True),   # Qwen2.5-1.5B q|k|v
+    (1130, 1536, 2048, [], 1792, True),                          # no adapters
+    (257, 512, 1024, [(0, 512), (768, 1024)], 768, False),       # test_gpu_step's layer, no bias
+    (37, 256, 1000, [(0, 256), (896, 1000)], 0, True),           # ragged n_out, no rotation
+    (1, 64, 384, [(128, 256)], 256, True),                       # one token, one adapter
+])
+def test_qkv_lora_fwd_matches_fp32(n, size, n_out, segs, rope_cols, with_bias):
+    _case(f"qkv_lora_fwd n={n} H={size} n_out={n_out} segs={segs} rope={rope_cols}")
+    x, w, bias, a, b = _inputs(n, size, n_out, segs, seed=n + n_out)
+    bias = bias if with_bias else None
+    scalings = [2.0, 2.0]
+    ts = t = None
+    if segs:
+        t = torch.empty(n, 16 * len(segs), dtype=torch.float16, device=DEV)
+        ts = torch.empty_like(t)
+        torch.ops.talm.lora_down(x, a[0], a[1] if len(segs) > 1 else None, scalings[0],
+                                 scalings[1], t, ts)
+    cos, sin = _rope_tables(n) if rope_cols else (None, None)
+    out = torch.empty(n, n_out, dtype=torch.float16, device=DEV)
+    pad = segs + [(0, 0)] * 2
+    bs = b + [None] * 2
+    torch.ops.talm.qkv_lora_fwd(x, w, bias, ts, bs[0], pad[0][0], pad[0][1], bs[1], pad[1][0],
+                                pad[1][1], cos, sin, rope_cols, out)
+    ref = x.float() @ w.float().t()
+    if bias is not None:
+        ref += bias.float()
+    for g, (lo, hi) in enumerate(segs):
+        tg = t[:, 16 * g:16 * (g + 1)].float()
+        ref[:, lo:hi] += scalings[g] * (tg @ b[g].float().t())
+    ref = ref.half().float()
+    if rope_cols:
+        ref = _rotate(ref, cos, sin, rope_cols)
+    got = out.float()
+    scale = ref.abs().max()
+    err = (got - ref).abs()
+    assert torch.all(err <= 2e-3 * ref.abs() + 2e-3 * scale), float(err.max())
+
+
+def test_qkv_lora_fwd_rejects_misaligned_adapter_columns():
+    _case("qkv_lora_fwd rejects")
+    x, w, bias, a, b = _inputs(8, 64, 512, [(64, 192)], seed=1)
+    t = torch.empty(8, 16, dtype=torch.float16, device=DEV)
+    out = torch.empty(8, 512, dtype=torch.float16, device=DEV)
+    with pytest.raises(ValueError, match="whole 128-column tiles"):
+        torch.ops.talm.qkv_lora_fwd(x, w, bias, t, b[0], 64, 192, None, 0, 0, None, None, 0, out)
