@@ -157,16 +157,20 @@ int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* wei
                  uint16_t* grad_hidden, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
- * LoRA down-projection of the q|k|v node: for adapter g < n_adapters (1 or 2, rank 16 each),
- * t[:, 16g:16g+16] = fp16(x A_g^T) and ts[:, 16g:16g+16] = fp16(scaling_g * x A_g^T)
- * (fp32 accumulation). x f16 [n_tokens, hidden] (row stride ldx, hidden a multiple of 32),
- * A_g f16 [16, hidden] contiguous, t and ts f16 [n_tokens, ldt]. Replaces the adapters'
- * t = drop(x) A^T GEMMs without dropout (solution/fused_proj.py:139-153, solution/lora.py:
- * 183-186); t is what the backward keeps.
+ * LoRA down-projection of the q|k|v node, rank 16 per adapter (1 or 2 adapters): adapter g
+ * reduces x's columns [xcol_g, xcol_g + k_g) against A_g f16 [16, k_g] (contiguous):
+ * t[:, 16g:16g+16] = fp16(sum) and ts[:, 16g:16g+16] = fp16(scaling_g * sum), fp32 sums.
+ * x f16 [n_tokens, ldx], t and ts f16 [n_tokens, ldt], k_g multiples of 32.
+ * Forward (xcol 0, k = hidden): the adapters' t = drop(x) A^T without dropout
+ * (solution/fused_proj.py:139-153, solution/lora.py:183-186); t is what the backward keeps.
+ * Backward (x = the node's output gradient, A_g = B_g^T over the adapter's own output columns,
+ * scaling as in the forward): ts = u = (scaling dy) B (solution/fused_proj.py:200-201,
+ * solution/lora.py:218-219).
  */
-int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
-                   const uint16_t* a0, const uint16_t* a1, int32_t n_adapters, float scaling0,
-                   float scaling1, uint16_t* t, uint16_t* ts, int64_t ldt, void* stream);
+int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t k0, int64_t k1,
+                   int64_t xcol0, int64_t xcol1, const uint16_t* a0, const uint16_t* a1,
+                   int32_t n_adapters, float scaling0, float scaling1, uint16_t* t, uint16_t* ts,
+                   int64_t ldt, void* stream);
 
 /*
  * The fused q|k|v projection forward: out = x W^T + bias + sum_g (ts_g B_g^T on adapter g's
@@ -187,6 +191,32 @@ int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t 
                       int64_t seg1_begin, int64_t seg1_end, const float* cos, const float* sin,
                       int64_t cs_stride, int64_t rope_cols, uint16_t* out, int64_t ldo,
                       void* stream);
+
+/*
+ * The q|k|v node's backward operand: dcat f16 [n_tokens, q + k + v] (row stride ldc) =
+ * [rope_back(dq) | rope_back(dk) | dv] with dx1 = dy1 c1 + dy2 s2, dx2 = dy2 c2 - dy1 s1 on the
+ * (j, j + 64) pairs of each 128-column head (no rotation when cos is NULL). Replaces the
+ * backward's gradient concatenation and its RoPE launch (solution/fused_proj.py:165-175,
+ * solution/rope.py:145-157).
+ */
+int talm_qkv_bwd_prep(const uint16_t* dq, int64_t ldq, const uint16_t* dk, int64_t ldk,
+                      const uint16_t* dv, int64_t ldv, int64_t n_tokens, int64_t q_cols,
+                      int64_t k_cols, int64_t v_cols, const float* cos, const float* sin,
+                      int64_t cs_stride, uint16_t* dcat, int64_t ldc, void* stream);
+
+/*
+ * The q|k|v node's input gradient on MFMA: dx f16 [n_tokens, hidden] = dcat W + u A, with
+ * dcat f16 [n_tokens, n_out] (ldc), weight_t = W^T f16 [hidden, ldwt >= n_out] (W the layer
+ * group's q|k|v rows), u f16 [n_tokens, rank] (ldu; the adapters' u side by side) and
+ * a_t = A^T f16 [hidden, ldat] (the adapters' A side by side, transposed), rank <= 64 a
+ * multiple of 8 (0: no adapter term). One fp32 accumulation, one rounding. Replaces the
+ * backward's dX GEMM (K = n_out) and the adapters' u A GEMMs and adds
+ * (solution/fused_proj.py:172-184, :202-209, solution/lora.py:221-222).
+ */
+int talm_qkv_lora_bwd_dx(const uint16_t* dcat, int64_t ldc, int64_t n_tokens, int64_t n_out,
+                         const uint16_t* weight_t, int64_t ldwt, int64_t hidden, const uint16_t* u,
+                         int64_t ldu, int64_t rank, const uint16_t* a_t, int64_t ldat,
+                         uint16_t* dx, int64_t lddx, void* stream);
 
 #ifdef __cplusplus
 }

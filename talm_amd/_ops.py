@@ -209,26 +209,29 @@ def head_ce(hidden, weight, weight_t, targets, vchunk, n_grad, group, token_loss
                "head_ce")
 
 
-@_op("lora_down(Tensor x, Tensor a0, Tensor? a1, float scaling0, float scaling1, Tensor(a!) t, "
-     "Tensor(b!) ts) -> ()")
-def lora_down(x, a0, a1, scaling0, scaling1, t, ts):
-    """x fp16 [N, H] (unit column stride); a0 (a1) fp16 [16, H] contiguous; t, ts fp16 [N, >= 16
-    per adapter] with a common row stride: t = x A^T per adapter, ts = scaling * that."""
+@_op("lora_down(Tensor x, Tensor a0, Tensor? a1, int k0, int k1, int xcol0, int xcol1, "
+     "float scaling0, float scaling1, Tensor(a!) t, Tensor(b!) ts) -> ()")
+def lora_down(x, a0, a1, k0, k1, xcol0, xcol1, scaling0, scaling1, t, ts):
+    """Adapter g: t[:, 16g:16g+16] = x[:, xcol_g:xcol_g + k_g] A_g^T, ts = scaling_g * that;
+    x fp16 (unit column stride), A_g fp16 [16, k_g] contiguous, t / ts fp16 with one row
+    stride."""
     for name, v in (("x", x), ("a0", a0), ("t", t), ("ts", ts)):
         _fp16(v, name)
-    n, size = x.shape
-    adapters = [a0] + ([a1] if a1 is not None else [])
-    for a in adapters:
+    n = x.shape[0]
+    adapters = [(a0, k0, xcol0)] + ([(a1, k1, xcol1)] if a1 is not None else [])
+    for a, k, col in adapters:
         _fp16(a, "lora A")
-        _require(a.is_contiguous() and tuple(a.shape) == (16, size), "lora_down: A [16, H]")
+        _require(a.is_contiguous() and tuple(a.shape) == (16, k) and col + k <= x.shape[1],
+                 "lora_down: A [16, k] inside x's columns")
     _require(x.stride(1) == 1 and t.stride(1) == 1 and ts.stride(1) == 1
              and t.stride(0) == ts.stride(0) and t.shape[0] == n and ts.shape[0] == n
              and t.shape[1] >= 16 * len(adapters) and ts.shape[1] >= 16 * len(adapters),
-             "lora_down: x [N, H], t/ts [N, 16 * adapters] with one row stride")
+             "lora_down: x [N, *], t/ts [N, 16 * adapters] with one row stride")
     lib = _lib.lib()
-    _lib.check(lib.talm_lora_down(x.data_ptr(), x.stride(0), n, size, a0.data_ptr(), _ptr(a1),
-                                  len(adapters), float(scaling0), float(scaling1), t.data_ptr(),
-                                  ts.data_ptr(), t.stride(0), _stream(x)), "lora_down")
+    _lib.check(lib.talm_lora_down(x.data_ptr(), x.stride(0), n, int(k0), int(k1), int(xcol0),
+                                  int(xcol1), a0.data_ptr(), _ptr(a1), len(adapters),
+                                  float(scaling0), float(scaling1), t.data_ptr(), ts.data_ptr(),
+                                  t.stride(0), _stream(x)), "lora_down")
 
 
 @_op("qkv_lora_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? ts, Tensor? b0, int seg0_begin, "
@@ -269,3 +272,54 @@ def qkv_lora_fwd(x, weight, bias, ts, b0, seg0_begin, seg0_end, b1, seg1_begin, 
         seg0_end, _ptr(b1), seg1_begin, seg1_end, _ptr(cos), _ptr(sin),
         0 if cos is None else cos.stride(0), rope_cols, out.data_ptr(), out.stride(0),
         _stream(x)), "qkv_lora_fwd")
+
+
+@_op("qkv_bwd_prep(Tensor dq, Tensor dk, Tensor dv, Tensor? cos, Tensor? sin, "
+     "Tensor(a!) dcat) -> ()")
+def qkv_bwd_prep(dq, dk, dv, cos, sin, dcat):
+    """dcat [N, q + k + v] = [rope_back(dq) | rope_back(dk) | dv] (cos/sin fp32 [N, >= 128], or
+    None for no rotation); every operand fp16 with unit column stride."""
+    n = dcat.shape[0]
+    for name, v in (("dq", dq), ("dk", dk), ("dv", dv), ("dcat", dcat)):
+        _fp16(v, name)
+        _require(v.dim() == 2 and v.stride(1) == 1 and v.shape[0] == n,
+                 f"qkv_bwd_prep: {name} [N, columns] with unit column stride")
+    _require(dcat.shape[1] == dq.shape[1] + dk.shape[1] + dv.shape[1],
+             "qkv_bwd_prep: dcat holds q, k and v")
+    if cos is not None:
+        for v in (cos, sin):
+            _require(v is not None and v.is_cuda and v.dtype == torch.float32 and v.stride(1) == 1
+                     and v.shape[0] == n and v.shape[1] >= 128 and v.stride(0) == cos.stride(0),
+                     "qkv_bwd_prep: cos/sin fp32 [N, >= 128] with one row stride")
+    lib = _lib.lib()
+    _lib.check(lib.talm_qkv_bwd_prep(dq.data_ptr(), dq.stride(0), dk.data_ptr(), dk.stride(0),
+                                     dv.data_ptr(), dv.stride(0), n, dq.shape[1], dk.shape[1],
+                                     dv.shape[1], _ptr(cos), _ptr(sin),
+                                     0 if cos is None else cos.stride(0), dcat.data_ptr(),
+                                     dcat.stride(0), _stream(dcat)), "qkv_bwd_prep")
+
+
+@_op("qkv_lora_bwd_dx(Tensor dcat, Tensor weight_t, Tensor? u, Tensor? a_t, Tensor(a!) dx) -> ()")
+def qkv_lora_bwd_dx(dcat, weight_t, u, a_t, dx):
+    """dx [N, H] = dcat [N, n_out] W + u [N, r] A, from weight_t = W^T [H, >= n_out] and
+    a_t = A^T [H, r] (the adapters side by side); fp16, unit column strides."""
+    for name, v in (("dcat", dcat), ("weight_t", weight_t), ("dx", dx)):
+        _fp16(v, name)
+        _require(v.dim() == 2 and v.stride(1) == 1, f"qkv_lora_bwd_dx: {name} unit column stride")
+    n, n_out = dcat.shape
+    size = weight_t.shape[0]
+    _require(weight_t.shape[1] >= n_out and tuple(dx.shape) == (n, size),
+             "qkv_lora_bwd_dx: weight_t [H, >= n_out], dx [N, H]")
+    rank = 0
+    if u is not None:
+        _fp16(u, "u")
+        _fp16(a_t, "a_t")
+        rank = u.shape[1]
+        _require(u.stride(1) == 1 and a_t.stride(1) == 1 and u.shape[0] == n
+                 and tuple(a_t.shape) == (size, rank), "qkv_lora_bwd_dx: u [N, r], a_t [H, r]")
+    lib = _lib.lib()
+    _lib.check(lib.talm_qkv_lora_bwd_dx(
+        dcat.data_ptr(), dcat.stride(0), n, n_out, weight_t.data_ptr(), weight_t.stride(0), size,
+        _ptr(u), 0 if u is None else u.stride(0), rank, _ptr(a_t),
+        0 if a_t is None else a_t.stride(0), dx.data_ptr(), dx.stride(0), _stream(dcat)),
+        "qkv_lora_bwd_dx")

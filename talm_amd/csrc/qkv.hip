@@ -27,28 +27,37 @@ constexpr int kMaxAdapters = 2;
 // t[r][16 g + i] = fp16(sum_k x[r][k] A_g[i][k]); ts = fp16(scaling_g * the same fp32 sum).
 // One workgroup per 16 tokens, wavefront w takes the 32-deep k-steps w, w + 4, ...
 // ------------------------------------------------------------------------------------------
+// Adapter g reduces over x's columns [xcol_g, xcol_g + k_g) against A_g [16][k_g] (the forward:
+// both over all of x; the backward: u = dy_seg B_g over each adapter's own output columns).
 __global__ __launch_bounds__(256) void lora_down_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, int n_tokens, int hidden,
-    const uint16_t* __restrict__ a0, const uint16_t* __restrict__ a1, int n_adapters, float s0,
-    float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts, int64_t ldt) {
+    const uint16_t* __restrict__ x, int64_t ldx, int n_tokens, int k0len, int k1len, int xcol0,
+    int xcol1, const uint16_t* __restrict__ a0, const uint16_t* __restrict__ a1, int n_adapters,
+    float s0, float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts, int64_t ldt) {
   __shared__ float red[4][kMaxAdapters][16][16 + 1];
   const int m0 = blockIdx.x * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = lane & 15, kq = 8 * (lane >> 4);
-  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(x + static_cast<int64_t>(m0) * ldx);
+  const uint16_t* xr = x + static_cast<int64_t>(m0) * ldx;
+  const __amdgpu_buffer_rsrc_t rx0 = buffer_rsrc(xr + xcol0);
+  const __amdgpu_buffer_rsrc_t rx1 = buffer_rsrc(xr + (n_adapters > 1 ? xcol1 : xcol0));
   const __amdgpu_buffer_rsrc_t ra0 = buffer_rsrc(a0);
   const __amdgpu_buffer_rsrc_t ra1 = buffer_rsrc(n_adapters > 1 ? a1 : a0);
   const uint32_t xoff = m0 + row < n_tokens ? static_cast<uint32_t>((row * ldx + kq) * 2) : kOob;
-  const uint32_t aoff = static_cast<uint32_t>((row * hidden + kq) * 2);
+  const uint32_t aoff0 = static_cast<uint32_t>((row * k0len + kq) * 2);
+  const uint32_t aoff1 = static_cast<uint32_t>((row * k1len + kq) * 2);
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = wave * 32; k0 < hidden; k0 += 128) {
+  for (int k0 = wave * 32; k0 < k0len; k0 += 128) {
     const uint32_t kb = static_cast<uint32_t>(k0 * 2);
-    const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff + kb, 0, 0));
-    const half8_t b0 = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra0, aoff + kb, 0, 0));
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b0, acc0, 0, 0, 0);
-    if (n_adapters > 1) {
-      const half8_t b1 = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra1, aoff + kb, 0, 0));
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b1, acc1, 0, 0, 0);
+    const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx0, xoff + kb, 0, 0));
+    const half8_t b = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra0, aoff0 + kb, 0, 0));
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc0, 0, 0, 0);
+  }
+  if (n_adapters > 1) {
+    for (int k0 = wave * 32; k0 < k1len; k0 += 128) {
+      const uint32_t kb = static_cast<uint32_t>(k0 * 2);
+      const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx1, xoff + kb, 0, 0));
+      const half8_t b = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra1, aoff1 + kb, 0, 0));
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc1, 0, 0, 0);
     }
   }
   // accumulator element v of lane l: token 4 * (l / 16) + v, rank l % 16
@@ -76,8 +85,8 @@ using QkvShape = TileShape<128, 128, 64, 2, 2, 2>;  // 4 wavefronts of 64 x 64, 
 constexpr int kQZS = 128 + 8;                       // staged tile row stride (halfs)
 static_assert(128 * kQZS * 2 <= QkvShape::kRing, "the staged tile reuses the ring");
 
-// An operand whose k range has two parts: steps [0, nk1) read `base1` (k < k1), one more step
-// reads `base2` (k in [lo2, hi2)). The per-lane row and chunk do not depend on the part; the
+// An operand whose k range has two parts: steps [0, nk1) read `base1` (k < k1), the steps after
+// them read `base2` (k in [lo2, hi2), counted from 0 again). The per-lane row and chunk do not depend on the part; the
 // part's base, stride and bounds are chosen by value each step (scalar selects), so nothing is
 // indexed through a selected address and the loader stays in registers.
 template <class S, int kRows>
@@ -109,7 +118,7 @@ struct TwoPartLoader {
   }
   __device__ __forceinline__ void issue(unsigned char* dst, int kt, int wave) {
     const bool second = kt >= nk1;
-    const int k0 = second ? 0 : kt * S::kBK;
+    const int k0 = (second ? kt - nk1 : kt) * S::kBK;
     const __amdgpu_buffer_rsrc_t r = second ? r2 : r1;
     const int ld = second ? ld2 : ld1, rows = second ? rows2 : rows1;
     const int lo = second ? lo2 : 0, hi = second ? hi2 : k1;
@@ -128,15 +137,17 @@ struct QkvArgs {
   const uint16_t* x;
   int64_t ldx;
   int n_tokens, hidden;
-  const uint16_t* w;      // [n_out][ldw], the layer group's q|k|v rows
+  const uint16_t* w;      // [n_out][ldw]: B rows of the main product (k = hidden)
   int64_t ldw;
   int n_out;
   const uint16_t* bias;   // [n_out] or null
-  const uint16_t* ts;     // [n_tokens][ldt]: scaling_g * x A_g^T in columns [16 g, 16 g + 16)
+  const uint16_t* ts;     // [n_tokens][ldt]: A of the extra step (k in a segment's window)
   int64_t ldt;
-  int n_adapters;
-  const uint16_t* b[kMaxAdapters];  // B_g [seg_end - seg_begin][16]
+  int n_segs;             // output-column segments that get the extra step (at most 2)
+  const uint16_t* b[kMaxAdapters];  // B of the extra step for segment g, row = output column
+  int64_t ldb[kMaxAdapters];
   int seg_begin[kMaxAdapters], seg_end[kMaxAdapters];
+  int k_lo[kMaxAdapters], k_hi[kMaxAdapters];  // the segment's k window of the extra step
   const float* cos;       // [n_tokens][cs_stride] or null (no rotary embedding)
   const float* sin;
   int64_t cs_stride;
@@ -146,7 +157,9 @@ struct QkvArgs {
   int n_mtiles, n_ntiles;
 };
 
-__global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void qkv_fwd_kernel(QkvArgs a) {
+// out = x w^T (+ the extra step on the tile's segment) (+ bias), optionally rotated: the forward
+// (extra step = the adapter term) and the backward dX (extra step = u A over all columns).
+__global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void proj_ext_kernel(QkvArgs a) {
   using S = QkvShape;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing];
   const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_mtiles * a.n_ntiles));
@@ -156,27 +169,27 @@ __global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void qkv_fwd_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 
-  // the adapter whose output columns hold this tile (segments are whole tiles); selected with
+  // the segment whose output columns hold this tile (segments are whole tiles); selected with
   // conditionals, not by indexing the argument arrays (which would copy them to scratch)
-  const bool in0 = a.n_adapters > 0 && n0 >= a.seg_begin[0] && n0 < a.seg_end[0];
-  const bool in1 = a.n_adapters > 1 && n0 >= a.seg_begin[1] && n0 < a.seg_end[1];
+  const bool in0 = a.n_segs > 0 && n0 >= a.seg_begin[0] && n0 < a.seg_end[0];
+  const bool in1 = a.n_segs > 1 && n0 >= a.seg_begin[1] && n0 < a.seg_end[1];
   const int g = in1 ? 1 : (in0 ? 0 : -1);
-  const int gc = g > 0 ? g : 0;
-  const uint16_t* bg = gc ? a.b[1] : a.b[0];
-  const int sb = gc ? a.seg_begin[1] : a.seg_begin[0], se = gc ? a.seg_end[1] : a.seg_end[0];
-  // A: x, then columns [16 g, 16 g + 16) of ts; B: W's rows, then B_g's (indexed from k = 16 g)
+  const bool g1 = g > 0;
+  const uint16_t* bg = g1 ? a.b[1] : a.b[0];
+  const int64_t ldb = g1 ? a.ldb[1] : a.ldb[0];
+  const int sb = g1 ? a.seg_begin[1] : a.seg_begin[0], se = g1 ? a.seg_end[1] : a.seg_end[0];
+  const int lo = g1 ? a.k_lo[1] : a.k_lo[0], hi = g1 ? a.k_hi[1] : a.k_hi[0];
+  // A: x, then ts's k window; B: w's rows, then the segment's B (indexed from k = lo)
   TwoPartLoader<S, S::kBM> la;
   TwoPartLoader<S, S::kBN> lb;
   la.init(a.x + static_cast<int64_t>(m0) * a.ldx, a.ldx, a.n_tokens - m0, a.hidden,
-          a.ts + static_cast<int64_t>(m0) * a.ldt, a.ldt, a.n_tokens - m0, kRank * gc,
-          kRank * (gc + 1), wave, lane);
+          a.ts + static_cast<int64_t>(m0) * a.ldt, a.ldt, a.n_tokens - m0, lo, hi, wave, lane);
   lb.init(a.w + static_cast<int64_t>(n0) * a.ldw, a.ldw, a.n_out - n0, a.hidden,
-          bg + static_cast<int64_t>(n0 - sb) * kRank - kRank * gc, kRank, se - n0, kRank * gc,
-          kRank * (gc + 1), wave, lane);
+          bg + static_cast<int64_t>(n0 - sb) * ldb - lo, ldb, se - n0, lo, hi, wave, lane);
   const int nk1 = (a.hidden + S::kBK - 1) / S::kBK;
   Acc<S> acc;
   ring_gemm<S>(
-      smem, nk1 + (g >= 0 ? 1 : 0),
+      smem, nk1 + (g >= 0 ? (hi + S::kBK - 1) / S::kBK : 0),
       [&](unsigned char* slot, int kt) {
         la.issue(slot, kt, wave);
         lb.issue(slot + S::kAChunks * 16, kt, wave);
@@ -218,6 +231,52 @@ __global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void qkv_fwd_
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// The backward's operand: dcat = [rope_back(dq) | rope_back(dk) | dv] ([N, q + k + v] fp16).
+// dx1 = dy1 c1 + dy2 s2, dx2 = dy2 c2 - dy1 s1 on each (j, j + 64) pair of a 128-wide head
+// (solution/rope.py:145-157). One workgroup per token row, one thread per 8 columns.
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void qkv_bwd_prep_kernel(
+    const uint16_t* __restrict__ dq, int64_t ldq, const uint16_t* __restrict__ dk, int64_t ldk,
+    const uint16_t* __restrict__ dv, int64_t ldv, int q_cols, int k_cols, int v_cols,
+    const float* __restrict__ cos, const float* __restrict__ sin, int64_t cs_stride,
+    uint16_t* __restrict__ dcat, int64_t ldc) {
+  const int r = blockIdx.x;
+  const int rope_cols = q_cols + k_cols, total = rope_cols + v_cols;
+  for (int c = threadIdx.x * 8; c < total; c += 256 * 8) {
+    auto chunk = [&](int col) {
+      const uint16_t* p = col < q_cols ? dq + static_cast<int64_t>(r) * ldq + col
+                          : col < rope_cols ? dk + static_cast<int64_t>(r) * ldk + (col - q_cols)
+                                            : dv + static_cast<int64_t>(r) * ldv + (col - rope_cols);
+      return *reinterpret_cast<const uint4*>(p);
+    };
+    uint4 v = chunk(c);
+    if (c < rope_cols && cos) {
+      const int j = c & 127, first = j < 64;
+      const uint4 o = chunk(first ? c + 64 : c - 64);  // the partner half of the same head
+      const float* cr = cos + static_cast<int64_t>(r) * cs_stride;
+      const float* sr = sin + static_cast<int64_t>(r) * cs_stride;
+      const uint32_t mine[4] = {v.x, v.y, v.z, v.w}, other[4] = {o.x, o.y, o.z, o.w};
+      uint32_t res[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float y[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int jj = j + 2 * e + h, pj = first ? jj + 64 : jj - 64;
+          const float me = h ? hi_f(mine[e]) : lo_f(mine[e]);
+          const float ot = h ? hi_f(other[e]) : lo_f(other[e]);
+          // first half: dy1 c1 + dy2 s2; second half: dy2 c2 - dy1 s1
+          y[h] = first ? me * cr[jj] + ot * sr[pj] : me * cr[jj] - ot * sr[pj];
+        }
+        res[e] = pack2(y[0], y[1]);
+      }
+      v = make_uint4(res[0], res[1], res[2], res[3]);
+    }
+    *reinterpret_cast<uint4*>(dcat + static_cast<int64_t>(r) * ldc + c) = v;
+  }
+}
+
 bool fits32(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t{1} << 31); }
 
 }  // namespace
@@ -225,27 +284,61 @@ bool fits32(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t{1} << 31
 
 using namespace talm;
 
-TALM_API int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
-                            const uint16_t* a0, const uint16_t* a1, int32_t n_adapters,
-                            float scaling0, float scaling1, uint16_t* t, uint16_t* ts,
-                            int64_t ldt, void* stream) {
-  if (n_tokens < 0 || hidden < 32 || hidden % 32 || ldx < hidden || ldx % 8 || n_adapters < 1 ||
-      n_adapters > kMaxAdapters || ldt < kRank * n_adapters || !fits32(16, ldx) ||
-      !fits32(16, hidden) || n_tokens > (1 << 30))
+TALM_API int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t k0,
+                            int64_t k1, int64_t xcol0, int64_t xcol1, const uint16_t* a0,
+                            const uint16_t* a1, int32_t n_adapters, float scaling0, float scaling1,
+                            uint16_t* t, uint16_t* ts, int64_t ldt, void* stream) {
+  const bool two = n_adapters > 1;
+  if (n_tokens < 0 || n_adapters < 1 || n_adapters > kMaxAdapters || k0 < 32 || k0 % 32 ||
+      (two && (k1 < 32 || k1 % 32)) || xcol0 < 0 || xcol0 % 8 || xcol0 + k0 > ldx ||
+      (two && (xcol1 < 0 || xcol1 % 8 || xcol1 + k1 > ldx)) || ldx % 8 ||
+      ldt < kRank * n_adapters || !fits32(16, ldx) || !fits32(16, k0) || !fits32(16, k1) ||
+      n_tokens > (1 << 30))
     return fail(TALM_EINVAL,
-                "lora_down: bad shape (tokens %lld, hidden %lld, ldx %lld, adapters %d, ldt "
-                "%lld): hidden a multiple of 32, 1-2 adapters of rank 16",
-                (long long)n_tokens, (long long)hidden, (long long)ldx, n_adapters, (long long)ldt);
+                "lora_down: bad shape (tokens %lld, k %lld/%lld at columns %lld/%lld, ldx %lld, "
+                "adapters %d, ldt %lld): reductions of a multiple of 32 inside x's rows, 1-2 "
+                "adapters of rank 16",
+                (long long)n_tokens, (long long)k0, (long long)k1, (long long)xcol0,
+                (long long)xcol1, (long long)ldx, n_adapters, (long long)ldt);
   if (n_tokens == 0) return ok();
-  if (!x || !a0 || (n_adapters > 1 && !a1) || !t || !ts)
-    return fail(TALM_EINVAL, "lora_down: null pointer");
-  if (!aligned(x, 16) || !aligned(a0, 16) || (a1 && !aligned(a1, 16)))
+  if (!x || !a0 || (two && !a1) || !t || !ts) return fail(TALM_EINVAL, "lora_down: null pointer");
+  if (!aligned(x, 16) || !aligned(a0, 16) || (two && !aligned(a1, 16)))
     return fail(TALM_EINVAL, "lora_down: x and the A matrices must be 16-byte aligned");
   hipLaunchKernelGGL(lora_down_kernel, dim3(static_cast<unsigned>((n_tokens + 15) / 16)), dim3(256),
-                     0, as_stream(stream), x, ldx, static_cast<int>(n_tokens),
-                     static_cast<int>(hidden), a0, a1, n_adapters, scaling0, scaling1, t, ts, ldt);
+                     0, as_stream(stream), x, ldx, static_cast<int>(n_tokens), static_cast<int>(k0),
+                     static_cast<int>(two ? k1 : k0), static_cast<int>(xcol0),
+                     static_cast<int>(two ? xcol1 : xcol0), a0, a1, n_adapters, scaling0, scaling1,
+                     t, ts, ldt);
   return check_launch("lora_down");
 }
+
+namespace talm {
+namespace {
+
+int check_proj(const char* what, int64_t ldx, int64_t n_tokens, int64_t hidden, int64_t ldw,
+               int64_t n_out, int64_t ldo) {
+  using S = QkvShape;
+  if (n_tokens < 0 || hidden < 8 || hidden % 8 || ldx < hidden || ldx % 8 || n_out < 1 ||
+      ldw < hidden || ldw % 8 || ldo < n_out || ldo % 8 || n_tokens > (1 << 30) ||
+      n_out > (1 << 30) || !fits32(S::kBM, ldx) || !fits32(S::kBN, ldw))
+    return fail(TALM_EINVAL,
+                "%s: bad shape (tokens %lld, hidden %lld, n_out %lld, ldx %lld, ldw %lld, ldo "
+                "%lld): sizes and strides multiples of 8",
+                what, (long long)n_tokens, (long long)hidden, (long long)n_out, (long long)ldx,
+                (long long)ldw, (long long)ldo);
+  return TALM_OK;
+}
+
+void launch_proj(QkvArgs& a, hipStream_t stream) {
+  using S = QkvShape;
+  a.n_mtiles = (a.n_tokens + S::kBM - 1) / S::kBM;
+  a.n_ntiles = (a.n_out + S::kBN - 1) / S::kBN;
+  hipLaunchKernelGGL(proj_ext_kernel, dim3(static_cast<unsigned>(a.n_mtiles * a.n_ntiles)),
+                     dim3(S::kThreads), 0, stream, a);
+}
+
+}  // namespace
+}  // namespace talm
 
 TALM_API int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
                                const uint16_t* weight, int64_t ldw, int64_t n_out,
@@ -256,15 +349,9 @@ TALM_API int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens,
                                int64_t cs_stride, int64_t rope_cols, uint16_t* out, int64_t ldo,
                                void* stream) {
   using S = QkvShape;
-  if (n_tokens < 0 || hidden < 8 || hidden % 8 || ldx < hidden || ldx % 8 || n_out < 1 ||
-      ldw < hidden || ldw % 8 || ldo < n_out || ldo % 8 || n_adapters < 0 ||
-      n_adapters > kMaxAdapters || n_tokens > (1 << 30) || n_out > (1 << 30) ||
-      !fits32(S::kBM, ldx) || !fits32(S::kBN, ldw))
-    return fail(TALM_EINVAL,
-                "qkv_lora_fwd: bad shape (tokens %lld, hidden %lld, n_out %lld, ldx %lld, ldw "
-                "%lld, ldo %lld, adapters %d)",
-                (long long)n_tokens, (long long)hidden, (long long)n_out, (long long)ldx,
-                (long long)ldw, (long long)ldo, n_adapters);
+  if (check_proj("qkv_lora_fwd", ldx, n_tokens, hidden, ldw, n_out, ldo)) return TALM_EINVAL;
+  if (n_adapters < 0 || n_adapters > kMaxAdapters)
+    return fail(TALM_EINVAL, "qkv_lora_fwd: %d adapters (0-2)", n_adapters);
   const int64_t begins[2] = {seg0_begin, seg1_begin}, ends[2] = {seg0_end, seg1_end};
   for (int g = 0; g < n_adapters; ++g)
     if (begins[g] < 0 || ends[g] <= begins[g] || ends[g] > n_out || begins[g] % S::kBN ||
@@ -290,17 +377,76 @@ TALM_API int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens,
   QkvArgs a{};
   a.x = x; a.ldx = ldx; a.n_tokens = static_cast<int>(n_tokens); a.hidden = static_cast<int>(hidden);
   a.w = weight; a.ldw = ldw; a.n_out = static_cast<int>(n_out); a.bias = bias;
-  a.ts = ts; a.ldt = ldt; a.n_adapters = n_adapters;
+  a.ts = ts; a.ldt = ldt; a.n_segs = n_adapters;
   a.b[0] = b0; a.b[1] = b1;
   for (int g = 0; g < 2; ++g) {
+    a.ldb[g] = kRank;
     a.seg_begin[g] = static_cast<int>(begins[g]);
     a.seg_end[g] = static_cast<int>(ends[g]);
+    a.k_lo[g] = kRank * g;        // adapter g's 16 columns of ts
+    a.k_hi[g] = kRank * (g + 1);
   }
   a.cos = cos; a.sin = sin; a.cs_stride = cs_stride; a.rope_cols = static_cast<int>(rope_cols);
   a.out = out; a.ldo = ldo;
-  a.n_mtiles = static_cast<int>((n_tokens + S::kBM - 1) / S::kBM);
-  a.n_ntiles = static_cast<int>((n_out + S::kBN - 1) / S::kBN);
-  hipLaunchKernelGGL(qkv_fwd_kernel, dim3(static_cast<unsigned>(a.n_mtiles * a.n_ntiles)),
-                     dim3(S::kThreads), 0, as_stream(stream), a);
+  launch_proj(a, as_stream(stream));
   return check_launch("qkv_lora_fwd");
+}
+
+TALM_API int talm_qkv_bwd_prep(const uint16_t* dq, int64_t ldq, const uint16_t* dk, int64_t ldk,
+                               const uint16_t* dv, int64_t ldv, int64_t n_tokens, int64_t q_cols,
+                               int64_t k_cols, int64_t v_cols, const float* cos, const float* sin,
+                               int64_t cs_stride, uint16_t* dcat, int64_t ldc, void* stream) {
+  const int64_t total = q_cols + k_cols + v_cols;
+  if (n_tokens < 0 || q_cols < 0 || k_cols < 0 || v_cols < 0 || q_cols % 8 || k_cols % 8 ||
+      v_cols % 8 || total < 8 || ldc < total || ldc % 8 || (q_cols && (ldq < q_cols || ldq % 8)) ||
+      (k_cols && (ldk < k_cols || ldk % 8)) || (v_cols && (ldv < v_cols || ldv % 8)) ||
+      n_tokens > (1 << 30) || total > (1 << 30))
+    return fail(TALM_EINVAL,
+                "qkv_bwd_prep: bad shape (tokens %lld, columns %lld/%lld/%lld, ldc %lld): column "
+                "counts and row strides multiples of 8",
+                (long long)n_tokens, (long long)q_cols, (long long)k_cols, (long long)v_cols,
+                (long long)ldc);
+  if (cos && (q_cols % 128 || k_cols % 128 || cs_stride < 128))
+    return fail(TALM_EINVAL, "qkv_bwd_prep: the rotated q and k need whole 128-column heads");
+  if (n_tokens == 0) return ok();
+  if (!dcat || (q_cols && !dq) || (k_cols && !dk) || (v_cols && !dv) || (cos && !sin))
+    return fail(TALM_EINVAL, "qkv_bwd_prep: null pointer");
+  if (!aligned(dcat, 16) || (dq && !aligned(dq, 16)) || (dk && !aligned(dk, 16)) ||
+      (dv && !aligned(dv, 16)))
+    return fail(TALM_EINVAL, "qkv_bwd_prep: gradients must be 16-byte aligned");
+  hipLaunchKernelGGL(qkv_bwd_prep_kernel, dim3(static_cast<unsigned>(n_tokens)), dim3(256), 0,
+                     as_stream(stream), dq, ldq, dk, ldk, dv, ldv, static_cast<int>(q_cols),
+                     static_cast<int>(k_cols), static_cast<int>(v_cols), cos, sin, cs_stride, dcat,
+                     ldc);
+  return check_launch("qkv_bwd_prep");
+}
+
+TALM_API int talm_qkv_lora_bwd_dx(const uint16_t* dcat, int64_t ldc, int64_t n_tokens,
+                                  int64_t n_out, const uint16_t* weight_t, int64_t ldwt,
+                                  int64_t hidden, const uint16_t* u, int64_t ldu, int64_t rank,
+                                  const uint16_t* a_t, int64_t ldat, uint16_t* dx, int64_t lddx,
+                                  void* stream) {
+  // dx [N, hidden] = dcat [N, n_out] W [n_out, hidden] + u [N, rank] A [rank, hidden], as the
+  // NT product [dcat | u] [W^T | A^T]^T: the kernel's "x" is dcat, its "w" is W^T
+  if (check_proj("qkv_lora_bwd_dx", ldc, n_tokens, n_out, ldwt, hidden, lddx)) return TALM_EINVAL;
+  if (rank < 0 || rank > 64 || rank % 8 || (rank && (ldu < rank || ldu % 8 || ldat < rank ||
+                                                      ldat % 8)))
+    return fail(TALM_EINVAL, "qkv_lora_bwd_dx: rank %lld (a multiple of 8, at most 64)",
+                (long long)rank);
+  if (n_tokens == 0) return ok();
+  if (!dcat || !weight_t || !dx || (rank && (!u || !a_t)))
+    return fail(TALM_EINVAL, "qkv_lora_bwd_dx: null pointer");
+  if (!aligned(dcat, 16) || !aligned(weight_t, 16) || !aligned(dx, 16) ||
+      (rank && (!aligned(u, 16) || !aligned(a_t, 16))))
+    return fail(TALM_EINVAL, "qkv_lora_bwd_dx: operands must be 16-byte aligned");
+  QkvArgs a{};
+  a.x = dcat; a.ldx = ldc; a.n_tokens = static_cast<int>(n_tokens); a.hidden = static_cast<int>(n_out);
+  a.w = weight_t; a.ldw = ldwt; a.n_out = static_cast<int>(hidden); a.bias = nullptr;
+  a.ts = u; a.ldt = ldu; a.n_segs = rank ? 1 : 0;
+  a.b[0] = a.b[1] = a_t; a.ldb[0] = a.ldb[1] = ldat;
+  a.seg_begin[0] = 0; a.seg_end[0] = static_cast<int>(hidden);
+  a.k_lo[0] = 0; a.k_hi[0] = static_cast<int>(rank);
+  a.out = dx; a.ldo = lddx;
+  launch_proj(a, as_stream(stream));
+  return check_launch("qkv_lora_bwd_dx");
 }

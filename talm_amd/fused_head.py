@@ -86,6 +86,14 @@ def transpose_weight(w16):
     return wt
 
 
+def transpose_weight_exact(w):
+    """w fp16 [R, C] (unit column stride, rows a multiple of 8) -> w^T [C, R] contiguous."""
+    rows, cols = w.shape
+    wt = torch.empty(cols, rows, dtype=torch.float16, device=w.device)
+    torch.ops.talm.head_weight_t(w, wt)
+    return wt
+
+
 _HEAD_WEIGHTS = {}
 
 

@@ -86,8 +86,10 @@ class FusedProjections(torch.autograd.Function):
                 saved += list(rope)
                 RAN["rope"] += 1
             RAN["qkv_mfma"] += 1
+            ctx.mfma = True
             return FusedProjections._finish(ctx, x, out, sizes, bounds, compact, saved, group,
                                             first, last, adapters, states, rope, head_dim)
+        ctx.mfma = False
         out = F.linear(x2, weight, bias)
         del weight
         saved = [x2]
@@ -137,6 +139,16 @@ class FusedProjections(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads):
+        if ctx.mfma and _mfma_bwd_ok(ctx, grads):
+            try:
+                result = _mfma_backward(ctx, grads)
+            except Exception as exc:  # noqa: BLE001 - state.py convention
+                if not fallback("qkv_mfma", exc):
+                    raise
+            else:
+                if result is not None:
+                    RAN["qkv_mfma_bwd"] += 1
+                    return result
         x2, *rest = ctx.saved_tensors
         n_tok = x2.shape[0]
         group = ctx.group
@@ -241,7 +253,9 @@ def _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope):
         ts = torch.empty_like(t)
         a1 = halves[1][0] if len(adapters) > 1 else None
         s1 = adapters[1][1] if len(adapters) > 1 else 0.0
-        torch.ops.talm.lora_down(x2, halves[0][0], a1, adapters[0][1], s1, t, ts)
+        size = x2.shape[1]
+        torch.ops.talm.lora_down(x2, halves[0][0], a1, size, size, 0, 0, adapters[0][1], s1, t,
+                                 ts)
     segs = [(bounds[seg], bounds[seg + 1]) for seg, _s, _p in adapters] + [(0, 0)] * 2
     bs = [b16 for _a, b16 in halves] + [None] * 2
     cos, sin = rope if rope is not None else (None, None)
@@ -250,6 +264,92 @@ def _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope):
                                 segs[1][0], segs[1][1], cos, sin,
                                 bounds[2] if rope is not None else 0, out)
     return out, t
+
+
+def _mfma_bwd_ok(ctx, grads):
+    """The MFMA backward takes the q|k|v node whose forward ran on MFMA (its saved tensors have
+    that layout) when every output has an fp16 gradient with unit column stride."""
+    if not QKV_MFMA or "qkv_mfma" in DISABLED or len(grads) != len(ctx.sizes):
+        return False
+    for grad, size in zip(grads, ctx.sizes):
+        if grad is None or grad.dtype != torch.float16 or grad.shape[-1] != size \
+                or grad.stride(-1) != 1 or grad.data_ptr() % 16 or size % 8:
+            return False
+    if any(ctx.sizes[seg] % 32 for seg, _s, _p in ctx.adapters):
+        return False
+    return len(ctx.sizes) == 3
+
+
+def _mfma_backward(ctx, grads):
+    """dX = [dq|dk|dv] W + u A in one MFMA GEMM (talm_qkv_lora_bwd_dx) after talm_qkv_bwd_prep
+    (RoPE-back, concatenation) and talm_lora_down (u = (scaling dy) B per adapter); the
+    adapters' dA = u^T x and dB = g^T t as in the reference (solution/fused_proj.py:160-216).
+    Returns None (the caller runs the ops) when the layer's weight is not in the group's buffer."""
+    x2, *rest = ctx.saved_tensors
+    group = ctx.group
+    cos = sin = None
+    if ctx.has_rope:
+        cos, sin = rest[-2:]
+        rest = rest[:-2]
+    weight = group.span("bwd", ctx.first, ctx.last) if ctx.needs_input_grad[0] else None
+    if ctx.needs_input_grad[0] and weight is None:
+        return None
+    try:
+        return _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight)
+    except Exception:
+        if weight is not None:  # the ops path takes the weight again
+            group.refund("bwd", ctx.last - ctx.first)
+        raise
+
+
+def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
+    n_tok, size = x2.shape
+    bounds = [0]
+    for s_ in ctx.sizes:
+        bounds.append(bounds[-1] + s_)
+    dys = [g.reshape(n_tok, -1) for g in grads]
+    dcat = torch.empty(n_tok, bounds[-1], dtype=torch.float16, device=x2.device)
+    torch.ops.talm.qkv_bwd_prep(dys[0], dys[1], dys[2], cos, sin, dcat)
+    if ctx.has_rope:
+        RAN["rope"] += 1
+    adapters = ctx.adapters
+    halves = [rest[3 * k:3 * k + 3] for k in range(len(adapters))]  # (t, a16, b16)
+    u = None
+    if adapters:
+        bts = [b16.t().contiguous() for _t, _a, b16 in halves]
+        t_tmp = torch.empty(n_tok, 16 * len(adapters), dtype=torch.float16, device=x2.device)
+        u = torch.empty_like(t_tmp)
+        lo = [bounds[seg] for seg, _s, _p in adapters] + [0]
+        ks = [bounds[seg + 1] - bounds[seg] for seg, _s, _p in adapters] + [0]
+        scal = [s_ for _seg, s_, _p in adapters] + [0.0]
+        torch.ops.talm.lora_down(dcat, bts[0], bts[1] if len(bts) > 1 else None, ks[0], ks[1],
+                                 lo[0], lo[1], scal[0], scal[1], t_tmp, u)
+    dx = None
+    if weight is not None:
+        from .fused_head import transpose_weight_exact
+
+        weight_t = transpose_weight_exact(weight)
+        del weight
+        a_t = torch.cat([a16 for _t, a16, _b in halves], 0).t().contiguous() if adapters else None
+        dx = torch.empty(n_tok, size, dtype=torch.float16, device=x2.device)
+        torch.ops.talm.qkv_lora_bwd_dx(dcat, weight_t, u, a_t, dx)
+        del weight_t
+    lora_grads = []
+    for k, (seg, scaling, _p) in enumerate(adapters):
+        t, a16, _b16 = halves[k]
+        index = 8 + 2 * k
+        uk = u[:, 16 * k:16 * (k + 1)]
+        lora_grads.append(torch.mm(uk.t(), x2).float() if ctx.needs_input_grad[index] else None)
+        if ctx.needs_input_grad[index + 1]:
+            dy = dcat[:, bounds[seg]:bounds[seg + 1]]
+            if _power_of_two(scaling):
+                lora_grads.append(torch.mm(dy.t(), t).float().mul_(scaling))
+            else:
+                lora_grads.append(torch.mm((dy * scaling).t(), t).float())
+        else:
+            lora_grads.append(None)
+    dx = None if dx is None else dx.view(ctx.x_shape)
+    return (dx, None, None, None, None, None, None, None, *lora_grads)
 
 
 _HOOK_DICTS = ("_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks")

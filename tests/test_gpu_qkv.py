@@ -11,6 +11,8 @@ GEMM rounding); whole-model use is covered by tests/test_gpu_step.py."""
 import pytest
 import torch
 
+import talm_amd._ops  # noqa: F401  (registers torch.ops.talm.*)
+
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
@@ -58,8 +60,8 @@ def test_lora_down_matches_fp32(n, size, adapters):
     t = torch.empty(n, 16 * adapters, dtype=torch.float16, device=DEV)
     ts = torch.empty_like(t)
     scalings = [2.0, 0.75][:adapters] + [0.0]
-    torch.ops.talm.lora_down(x, a[0], a[1] if adapters > 1 else None, scalings[0], scalings[1],
-                             t, ts)
+    torch.ops.talm.lora_down(x, a[0], a[1] if adapters > 1 else None, size, size, 0, 0,
+                             scalings[0], scalings[1], t, ts)
     for g in range(adapters):
         ref = x.float() @ a[g].float().t()
         got = t[:, 16 * g:16 * (g + 1)].float()
@@ -85,8 +87,8 @@ def test_qkv_lora_fwd_matches_fp32(n, size, n_out, segs, rope_cols, with_bias):
     if segs:
         t = torch.empty(n, 16 * len(segs), dtype=torch.float16, device=DEV)
         ts = torch.empty_like(t)
-        torch.ops.talm.lora_down(x, a[0], a[1] if len(segs) > 1 else None, scalings[0],
-                                 scalings[1], t, ts)
+        torch.ops.talm.lora_down(x, a[0], a[1] if len(segs) > 1 else None, size, size, 0, 0,
+                                 scalings[0], scalings[1], t, ts)
     cos, sin = _rope_tables(n) if rope_cols else (None, None)
     out = torch.empty(n, n_out, dtype=torch.float16, device=DEV)
     pad = segs + [(0, 0)] * 2
@@ -115,3 +117,76 @@ def test_qkv_lora_fwd_rejects_misaligned_adapter_columns():
     out = torch.empty(8, 512, dtype=torch.float16, device=DEV)
     with pytest.raises(ValueError, match="whole 128-column tiles"):
         torch.ops.talm.qkv_lora_fwd(x, w, bias, t, b[0], 64, 192, None, 0, 0, None, None, 0, out)
+
+
+def _rotate_back(y, cos, sin, cols):
+    y = y.clone()
+    n = y.shape[0]
+    heads = y[:, :cols].view(n, -1, 128)
+    x1, x2 = heads[..., :64].clone(), heads[..., 64:].clone()
+    c, s = cos[:, None], sin[:, None]
+    heads[..., :64] = x1 * c[..., :64] + x2 * s[..., 64:]
+    heads[..., 64:] = x2 * c[..., 64:] - x1 * s[..., :64]
+    return y
+
+
+@pytest.mark.parametrize("n,q,k,v,rope", [(1130, 1536, 256, 256, True), (37, 512, 256, 256, True),
+                                          (5, 128, 0, 64, False)])
+def test_qkv_bwd_prep_matches_rope_backward(n, q, k, v, rope):
+    """dcat = [rope_back(dq) | rope_back(dk) | dv] from strided gradient views: one fp16
+    rounding of the fp32 rotation (solution/rope.py:145-157), dv copied bit for bit."""
+    _case(f"qkv_bwd_prep n={n} q={q} k={k} v={v} rope={rope}")
+    g = torch.Generator().manual_seed(n + q)
+    big = torch.randn(n, q + k + v + 24, generator=g).half().to(DEV)  # strided row views
+    dq, dk, dv = big[:, :q], big[:, q:q + k], big[:, q + k:q + k + v]
+    cos, sin = _rope_tables(n, seed=3) if rope else (None, None)
+    dcat = torch.empty(n, q + k + v, dtype=torch.float16, device=DEV)
+    torch.ops.talm.qkv_bwd_prep(dq, dk, dv, cos, sin, dcat)
+    ref = torch.cat([dq, dk, dv], 1).float()
+    if rope:
+        ref = _rotate_back(ref, cos, sin, q + k)
+    got = dcat.float()
+    assert torch.equal(got[:, q + k:], ref[:, q + k:])
+    err = (got - ref.half().float()).abs()
+    assert torch.all(err <= 2.0 ** -10 * ref.abs() + 2.0 ** -24), float(err.max())
+
+
+def test_lora_down_backward_form_matches_fp32():
+    """u = (scaling dy) B per adapter over its own output columns: adapter 0 reduces columns
+    [0, 1536), adapter 1 columns [1792, 2048) of one [N, 2048] gradient."""
+    _case("lora_down backward form")
+    n = 700
+    g = torch.Generator().manual_seed(11)
+    dcat = torch.randn(n, 2048, generator=g).half().to(DEV)
+    b = [(torch.randn(1536, 16, generator=g) * 0.05).half().to(DEV),
+         (torch.randn(256, 16, generator=g) * 0.05).half().to(DEV)]
+    t = torch.empty(n, 32, dtype=torch.float16, device=DEV)
+    u = torch.empty_like(t)
+    torch.ops.talm.lora_down(dcat, b[0].t().contiguous(), b[1].t().contiguous(), 1536, 256, 0,
+                             1792, 2.0, 2.0, t, u)
+    for k, (lo, hi) in enumerate([(0, 1536), (1792, 2048)]):
+        ref = 2.0 * (dcat[:, lo:hi].float() @ b[k].float())
+        got = u[:, 16 * k:16 * (k + 1)].float()
+        assert torch.all((got - ref).abs() <= 2.0 ** -10 * ref.abs() + 1e-5 * (hi - lo)), k
+
+
+@pytest.mark.parametrize("n,size,n_out,rank", [(1130, 1536, 2048, 32), (257, 512, 1024, 32),
+                                               (37, 256, 1024, 0), (1, 64, 384, 16)])
+def test_qkv_lora_bwd_dx_matches_fp32(n, size, n_out, rank):
+    _case(f"qkv_lora_bwd_dx n={n} H={size} n_out={n_out} r={rank}")
+    g = torch.Generator().manual_seed(n + rank)
+    dcat = torch.randn(n, n_out, generator=g).half().to(DEV)
+    w = (torch.randn(n_out, size, generator=g) * n_out ** -0.5).half().to(DEV)
+    u = a_t = None
+    ref = dcat.float() @ w.float()
+    if rank:
+        u = torch.randn(n, rank, generator=g).half().to(DEV)
+        a = (torch.rand(rank, size, generator=g) * 2 - 1).half().to(DEV) * 0.05
+        a_t = a.t().contiguous()
+        ref += u.float() @ a.float()
+    wt = torch.empty(size, n_out, dtype=torch.float16, device=DEV)
+    torch.ops.talm.head_weight_t(w, wt)
+    dx = torch.empty(n, size, dtype=torch.float16, device=DEV)
+    torch.ops.talm.qkv_lora_bwd_dx(dcat, wt, u, a_t, dx)
+    err = (dx.float() - ref).abs()
+    assert torch.all(err <= 2e-3 * ref.abs() + 2e-3 * ref.abs().max()), float(err.max())

@@ -45,8 +45,8 @@ def test_patched_step_matches_eager_loss_curve(monkeypatch):
     eager = _run(False, 6, monkeypatch)
     assert engaged.RAN["fused_head"] == 0
     fused = _run(True, 6, monkeypatch)
-    for name in ("fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "rope", "addnorm",
-                 "swiglu_inplace", "head", "varlen_attn"):
+    for name in ("fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "rope",
+                 "addnorm", "swiglu_inplace", "head", "varlen_attn"):
         assert engaged.RAN[name] > 0, f"{name} did not run"
     assert abs(fused[0] - eager[0]) <= 1e-3 * abs(eager[0]), (fused[0], eager[0])
     for a, b in zip(fused, eager):
