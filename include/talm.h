@@ -163,14 +163,14 @@ int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* wei
  * x f16 [n_tokens, ldx], t and ts f16 [n_tokens, ldt], k_g multiples of 32.
  * Forward (xcol 0, k = hidden): the adapters' t = drop(x) A^T without dropout
  * (solution/fused_proj.py:139-153, solution/lora.py:183-186); t is what the backward keeps.
- * Backward (x = the node's output gradient, A_g = B_g^T over the adapter's own output columns,
- * scaling as in the forward): ts = u = (scaling dy) B (solution/fused_proj.py:200-201,
- * solution/lora.py:218-219).
+ * Backward (x = the node's output gradient over the adapter's own output columns, A_g = B_g^T
+ * given as B_g [k_g, 16] with a_kmajor = 1, scaling as in the forward): ts = u = (scaling dy) B
+ * (solution/fused_proj.py:200-201, solution/lora.py:218-219).
  */
 int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t k0, int64_t k1,
                    int64_t xcol0, int64_t xcol1, const uint16_t* a0, const uint16_t* a1,
-                   int32_t n_adapters, float scaling0, float scaling1, uint16_t* t, uint16_t* ts,
-                   int64_t ldt, void* stream);
+                   int32_t n_adapters, int32_t a_kmajor, float scaling0, float scaling1,
+                   uint16_t* t, uint16_t* ts, int64_t ldt, void* stream);
 
 /*
  * The fused q|k|v projection forward: out = x W^T + bias + sum_g (ts_g B_g^T on adapter g's
@@ -217,6 +217,23 @@ int talm_qkv_lora_bwd_dx(const uint16_t* dcat, int64_t ldc, int64_t n_tokens, in
                          const uint16_t* weight_t, int64_t ldwt, int64_t hidden, const uint16_t* u,
                          int64_t ldu, int64_t rank, const uint16_t* a_t, int64_t ldat,
                          uint16_t* dx, int64_t lddx, void* stream);
+
+/*
+ * The adapters' weight gradients in fp32 (both adapters, one call, two launches):
+ * dA_g [16, hidden] = u[:, 16g:16g+16]^T x and dB_g [seg_g, 16] = scaling_g dy[:, lo_g:lo_g+seg_g]^T
+ * t[:, 16g:16g+16], summed over the tokens in fixed-size chunks and then over the chunks in
+ * order (deterministic). x f16 [n_tokens, ldx], dy f16 [n_tokens, ldy] (the node's output
+ * gradient after the RoPE backward), u and t f16 [n_tokens, 16 per adapter]. `workspace` holds
+ * talm_lora_wgrad_workspace(...) bytes. Replaces the adapters' dA / dB GEMMs, their fp32 casts
+ * and the scaling of g (solution/fused_proj.py:199-215, solution/lora.py:218, :229-230).
+ */
+int64_t talm_lora_wgrad_workspace(int64_t n_tokens, int64_t hidden, int64_t seg0, int64_t seg1);
+int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t ldy,
+                    const uint16_t* u, int64_t ldu, const uint16_t* t, int64_t ldt,
+                    int64_t n_tokens, int64_t hidden, int32_t n_adapters, int64_t lo0,
+                    int64_t seg0, float scaling0, float* da0, float* db0, int64_t lo1,
+                    int64_t seg1, float scaling1, float* da1, float* db1, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -31,8 +31,10 @@ SIGNATURES = {
     "talm_swiglu_fwd": [_P, _P, _P, _I64, _P],
     "talm_swiglu_bwd": [_P, _P, _P, _P, _P, _I64, _P],
     "talm_head_weight_t": [_P, _I64, _I64, _I64, _P, _I64, _P],
-    "talm_lora_down": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I32, _F32, _F32, _P, _P,
-                       _I64, _P],
+    "talm_lora_down": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I32, _I32, _F32, _F32, _P,
+                       _P, _I64, _P],
+    "talm_lora_wgrad": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _I64, _I64, _F32,
+                        _P, _P, _I64, _I64, _F32, _P, _P, _P, _I64, _P],
     "talm_qkv_bwd_prep": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P,
                           _I64, _P],
     "talm_qkv_lora_bwd_dx": [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P,
@@ -46,6 +48,7 @@ SIGNATURES = {
 # Entry points that return a size instead of a status.
 SIZE_FUNCTIONS = {
     "talm_head_ce_workspace": [_I64, _I64, _I64, _I64, _I64, _I32],
+    "talm_lora_wgrad_workspace": [_I64, _I64, _I64, _I64],
 }
 
 _lock = threading.Lock()

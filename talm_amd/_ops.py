@@ -210,19 +210,20 @@ def head_ce(hidden, weight, weight_t, targets, vchunk, n_grad, group, token_loss
 
 
 @_op("lora_down(Tensor x, Tensor a0, Tensor? a1, int k0, int k1, int xcol0, int xcol1, "
-     "float scaling0, float scaling1, Tensor(a!) t, Tensor(b!) ts) -> ()")
-def lora_down(x, a0, a1, k0, k1, xcol0, xcol1, scaling0, scaling1, t, ts):
+     "int a_kmajor, float scaling0, float scaling1, Tensor(a!) t, Tensor(b!) ts) -> ()")
+def lora_down(x, a0, a1, k0, k1, xcol0, xcol1, a_kmajor, scaling0, scaling1, t, ts):
     """Adapter g: t[:, 16g:16g+16] = x[:, xcol_g:xcol_g + k_g] A_g^T, ts = scaling_g * that;
-    x fp16 (unit column stride), A_g fp16 [16, k_g] contiguous, t / ts fp16 with one row
-    stride."""
+    x fp16 (unit column stride), A_g fp16 contiguous [16, k_g] (or [k_g, 16] with a_kmajor),
+    t / ts fp16 with one row stride."""
     for name, v in (("x", x), ("a0", a0), ("t", t), ("ts", ts)):
         _fp16(v, name)
     n = x.shape[0]
     adapters = [(a0, k0, xcol0)] + ([(a1, k1, xcol1)] if a1 is not None else [])
     for a, k, col in adapters:
         _fp16(a, "lora A")
-        _require(a.is_contiguous() and tuple(a.shape) == (16, k) and col + k <= x.shape[1],
-                 "lora_down: A [16, k] inside x's columns")
+        shape = (k, 16) if a_kmajor else (16, k)
+        _require(a.is_contiguous() and tuple(a.shape) == shape and col + k <= x.shape[1],
+                 "lora_down: A [16, k] ([k, 16] k-major) inside x's columns")
     _require(x.stride(1) == 1 and t.stride(1) == 1 and ts.stride(1) == 1
              and t.stride(0) == ts.stride(0) and t.shape[0] == n and ts.shape[0] == n
              and t.shape[1] >= 16 * len(adapters) and ts.shape[1] >= 16 * len(adapters),
@@ -230,8 +231,8 @@ def lora_down(x, a0, a1, k0, k1, xcol0, xcol1, scaling0, scaling1, t, ts):
     lib = _lib.lib()
     _lib.check(lib.talm_lora_down(x.data_ptr(), x.stride(0), n, int(k0), int(k1), int(xcol0),
                                   int(xcol1), a0.data_ptr(), _ptr(a1), len(adapters),
-                                  float(scaling0), float(scaling1), t.data_ptr(), ts.data_ptr(),
-                                  t.stride(0), _stream(x)), "lora_down")
+                                  int(a_kmajor), float(scaling0), float(scaling1), t.data_ptr(),
+                                  ts.data_ptr(), t.stride(0), _stream(x)), "lora_down")
 
 
 @_op("qkv_lora_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? ts, Tensor? b0, int seg0_begin, "
@@ -323,3 +324,40 @@ def qkv_lora_bwd_dx(dcat, weight_t, u, a_t, dx):
         _ptr(u), 0 if u is None else u.stride(0), rank, _ptr(a_t),
         0 if a_t is None else a_t.stride(0), dx.data_ptr(), dx.stride(0), _stream(dcat)),
         "qkv_lora_bwd_dx")
+
+
+def lora_wgrad_workspace_bytes(n_tokens, hidden, seg0, seg1):
+    size = _lib.lib().talm_lora_wgrad_workspace(n_tokens, hidden, seg0, seg1)
+    _require(size >= 0, "lora_wgrad: unsupported shape")
+    return int(size)
+
+
+@_op("lora_wgrad(Tensor x, Tensor dy, Tensor u, Tensor t, int lo0, int seg0, float scaling0, "
+     "Tensor(a!) da0, Tensor(b!) db0, int lo1, int seg1, float scaling1, Tensor(c!)? da1, "
+     "Tensor(d!)? db1, Tensor(e!) workspace) -> ()")
+def lora_wgrad(x, dy, u, t, lo0, seg0, scaling0, da0, db0, lo1, seg1, scaling1, da1, db1,
+               workspace):
+    """fp32 dA_g [16, H] = u_g^T x, dB_g [seg_g, 16] = scaling_g dy[:, lo_g:lo_g+seg_g]^T t_g."""
+    for name, v in (("x", x), ("dy", dy), ("u", u), ("t", t)):
+        _fp16(v, name)
+        _require(v.dim() == 2 and v.stride(1) == 1, f"lora_wgrad: {name} unit column stride")
+    n, size = x.shape
+    two = da1 is not None
+    for da, db, seg in ((da0, db0, seg0),) + (((da1, db1, seg1),) if two else ()):
+        _require(da.is_cuda and da.dtype == torch.float32 and da.is_contiguous()
+                 and tuple(da.shape) == (16, size), "lora_wgrad: dA fp32 [16, H]")
+        _require(db.is_cuda and db.dtype == torch.float32 and db.is_contiguous()
+                 and tuple(db.shape) == (seg, 16), "lora_wgrad: dB fp32 [segment, 16]")
+    _require(workspace.is_cuda and workspace.is_contiguous(), "lora_wgrad: workspace")
+    if n == 0:  # no tokens: zero gradients, no launch
+        for out in (da0, db0, da1, db1):
+            if out is not None:
+                out.zero_()
+        return
+    lib = _lib.lib()
+    _lib.check(lib.talm_lora_wgrad(
+        x.data_ptr(), x.stride(0), dy.data_ptr(), dy.stride(0), u.data_ptr(), u.stride(0),
+        t.data_ptr(), t.stride(0), n, size, 2 if two else 1, int(lo0), int(seg0), float(scaling0),
+        da0.data_ptr(), db0.data_ptr(), int(lo1), int(seg1), float(scaling1), _ptr(da1),
+        _ptr(db1), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        _stream(x)), "lora_wgrad")

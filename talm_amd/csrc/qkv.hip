@@ -29,10 +29,20 @@ constexpr int kMaxAdapters = 2;
 // ------------------------------------------------------------------------------------------
 // Adapter g reduces over x's columns [xcol_g, xcol_g + k_g) against A_g [16][k_g] (the forward:
 // both over all of x; the backward: u = dy_seg B_g over each adapter's own output columns).
+// With `a_kmajor` the A_g are given as [k_g][16] (the backward passes B_g as it is stored):
+// each lane then gathers its 8 k-consecutive values with 2-byte loads.
+__device__ __forceinline__ half8_t gather_kmajor(const uint16_t* a, int k, int n) {
+  half8_t v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = __builtin_bit_cast(_Float16, a[(k + e) * 16 + n]);
+  return v;
+}
+
 __global__ __launch_bounds__(256) void lora_down_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int n_tokens, int k0len, int k1len, int xcol0,
     int xcol1, const uint16_t* __restrict__ a0, const uint16_t* __restrict__ a1, int n_adapters,
-    float s0, float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts, int64_t ldt) {
+    int a_kmajor, float s0, float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts,
+    int64_t ldt) {
   __shared__ float red[4][kMaxAdapters][16][16 + 1];
   const int m0 = blockIdx.x * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -49,14 +59,16 @@ __global__ __launch_bounds__(256) void lora_down_kernel(
   for (int k0 = wave * 32; k0 < k0len; k0 += 128) {
     const uint32_t kb = static_cast<uint32_t>(k0 * 2);
     const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx0, xoff + kb, 0, 0));
-    const half8_t b = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra0, aoff0 + kb, 0, 0));
+    const half8_t b = a_kmajor ? gather_kmajor(a0, k0 + kq, row)
+                               : __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra0, aoff0 + kb, 0, 0));
     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc0, 0, 0, 0);
   }
   if (n_adapters > 1) {
     for (int k0 = wave * 32; k0 < k1len; k0 += 128) {
       const uint32_t kb = static_cast<uint32_t>(k0 * 2);
       const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx1, xoff + kb, 0, 0));
-      const half8_t b = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra1, aoff1 + kb, 0, 0));
+      const half8_t b = a_kmajor ? gather_kmajor(a1, k0 + kq, row)
+                                 : __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra1, aoff1 + kb, 0, 0));
       acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc1, 0, 0, 0);
     }
   }
@@ -277,6 +289,94 @@ __global__ __launch_bounds__(256) void qkv_bwd_prep_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// The adapters' weight gradients (reductions over tokens), fp32, in two passes:
+//   dA_g[i][h] = sum_r u[r][16 g + i] x[r][h]                 (i < 16, h < hidden)
+//   dB_g[j][i] = scaling_g sum_r dy[r][lo_g + j] t[r][16 g + i]  (j < seg_g)
+// (solution/fused_proj.py:211-215, solution/lora.py:229-230: dA = u^T xd, dB = g^T t with
+// g = scaling dy). Pass 1: workgroup (column block, token chunk) accumulates one column per
+// thread over its chunk's tokens, the chunk's u / t rows broadcast from LDS, and writes a
+// partial; pass 2 sums the chunks in order (deterministic) into the fp32 gradients.
+// ------------------------------------------------------------------------------------------
+constexpr int kWgChunk = 64;  // tokens per partial
+
+struct WgradArgs {
+  const uint16_t* x;      // [N][ldx]
+  int64_t ldx;
+  const uint16_t* dy;     // [N][ldy]: the node's output gradient (after the RoPE backward)
+  int64_t ldy;
+  const uint16_t* u;      // [N][ldu]: 16 columns per adapter
+  int64_t ldu;
+  const uint16_t* t;      // [N][ldt]
+  int64_t ldt;
+  int n_tokens, hidden, n_adapters;
+  int lo[kMaxAdapters], seg[kMaxAdapters];
+  float scaling[kMaxAdapters];
+  float* part;            // [chunks][cols][32] fp32, cols = hidden + seg_0 + seg_1
+  float* da[kMaxAdapters];  // [16][hidden]
+  float* db[kMaxAdapters];  // [seg_g][16]
+  int cols, chunks;
+};
+
+__global__ __launch_bounds__(256) void lora_wgrad_partial_kernel(WgradArgs a) {
+  // every lane reads the same row (a broadcast): rows of 32 floats, 16-byte aligned
+  __shared__ __attribute__((aligned(16))) float su[kWgChunk][32];
+  __shared__ __attribute__((aligned(16))) float st[kWgChunk][32];
+  const int chunk = blockIdx.y, r0 = chunk * kWgChunk;
+  const int rn = min(kWgChunk, a.n_tokens - r0);
+  const int rank = 16 * a.n_adapters;
+  for (int e = threadIdx.x; e < kWgChunk * 32; e += 256) {
+    const int r = e >> 5, i = e & 31;
+    const bool ok = r < rn && i < rank;
+    su[r][i] = ok ? h2f(a.u[static_cast<int64_t>(r0 + r) * a.ldu + i]) : 0.f;
+    st[r][i] = ok ? h2f(a.t[static_cast<int64_t>(r0 + r) * a.ldt + i]) : 0.f;
+  }
+  __syncthreads();
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= a.cols) return;
+  float acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  float* out = a.part + (static_cast<int64_t>(chunk) * a.cols + c) * 32;
+  if (c < a.hidden) {  // dA column h: both adapters' u
+    const uint16_t* xc = a.x + static_cast<int64_t>(r0) * a.ldx + c;
+    for (int r = 0; r < rn; ++r) {
+      const float xv = h2f(xc[static_cast<int64_t>(r) * a.ldx]);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] += su[r][i] * xv;
+    }
+  } else {  // dB row j of adapter g: its t
+    const int cb = c - a.hidden, g = cb >= a.seg[0] ? 1 : 0;
+    const int j = g ? cb - a.seg[0] : cb, col = (g ? a.lo[1] : a.lo[0]) + j;
+    const uint16_t* yc = a.dy + static_cast<int64_t>(r0) * a.ldy + col;
+    for (int r = 0; r < rn; ++r) {
+      const float yv = h2f(yc[static_cast<int64_t>(r) * a.ldy]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] += st[r][16 * g + i] * yv;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 32; i += 4)
+    *reinterpret_cast<float4*>(out + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+}
+
+__global__ __launch_bounds__(256) void lora_wgrad_reduce_kernel(WgradArgs a) {
+  // one thread per (column, i): the dA columns carry 32 values, the dB rows 16
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= static_cast<int64_t>(a.cols) * 32) return;
+  const int c = static_cast<int>(e >> 5), i = static_cast<int>(e & 31);
+  float sum = 0.f;
+  for (int k = 0; k < a.chunks; ++k) sum += a.part[(static_cast<int64_t>(k) * a.cols + c) * 32 + i];
+  if (c < a.hidden) {
+    const int g = i >> 4;
+    if (g < a.n_adapters) (g ? a.da[1] : a.da[0])[static_cast<int64_t>(i & 15) * a.hidden + c] = sum;
+  } else if (i < 16) {
+    const int cb = c - a.hidden, g = cb >= a.seg[0] ? 1 : 0;
+    const int j = g ? cb - a.seg[0] : cb;
+    (g ? a.db[1] : a.db[0])[static_cast<int64_t>(j) * 16 + i] = (g ? a.scaling[1] : a.scaling[0]) * sum;
+  }
+}
+
 bool fits32(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t{1} << 31); }
 
 }  // namespace
@@ -286,8 +386,9 @@ using namespace talm;
 
 TALM_API int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t k0,
                             int64_t k1, int64_t xcol0, int64_t xcol1, const uint16_t* a0,
-                            const uint16_t* a1, int32_t n_adapters, float scaling0, float scaling1,
-                            uint16_t* t, uint16_t* ts, int64_t ldt, void* stream) {
+                            const uint16_t* a1, int32_t n_adapters, int32_t a_kmajor,
+                            float scaling0, float scaling1, uint16_t* t, uint16_t* ts, int64_t ldt,
+                            void* stream) {
   const bool two = n_adapters > 1;
   if (n_tokens < 0 || n_adapters < 1 || n_adapters > kMaxAdapters || k0 < 32 || k0 % 32 ||
       (two && (k1 < 32 || k1 % 32)) || xcol0 < 0 || xcol0 % 8 || xcol0 + k0 > ldx ||
@@ -307,8 +408,8 @@ TALM_API int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, in
   hipLaunchKernelGGL(lora_down_kernel, dim3(static_cast<unsigned>((n_tokens + 15) / 16)), dim3(256),
                      0, as_stream(stream), x, ldx, static_cast<int>(n_tokens), static_cast<int>(k0),
                      static_cast<int>(two ? k1 : k0), static_cast<int>(xcol0),
-                     static_cast<int>(two ? xcol1 : xcol0), a0, a1, n_adapters, scaling0, scaling1,
-                     t, ts, ldt);
+                     static_cast<int>(two ? xcol1 : xcol0), a0, a1, n_adapters, a_kmajor ? 1 : 0,
+                     scaling0, scaling1, t, ts, ldt);
   return check_launch("lora_down");
 }
 
@@ -449,4 +550,55 @@ TALM_API int talm_qkv_lora_bwd_dx(const uint16_t* dcat, int64_t ldc, int64_t n_t
   a.out = dx; a.ldo = lddx;
   launch_proj(a, as_stream(stream));
   return check_launch("qkv_lora_bwd_dx");
+}
+
+TALM_API int64_t talm_lora_wgrad_workspace(int64_t n_tokens, int64_t hidden, int64_t seg0,
+                                          int64_t seg1) {
+  if (n_tokens < 0 || hidden < 1 || seg0 < 0 || seg1 < 0) return -1;
+  const int64_t chunks = (n_tokens + kWgChunk - 1) / kWgChunk;
+  return chunks * (hidden + seg0 + seg1) * 32 * 4;
+}
+
+TALM_API int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t ldy,
+                             const uint16_t* u, int64_t ldu, const uint16_t* t, int64_t ldt,
+                             int64_t n_tokens, int64_t hidden, int32_t n_adapters,
+                             int64_t lo0, int64_t seg0, float scaling0, float* da0, float* db0,
+                             int64_t lo1, int64_t seg1, float scaling1, float* da1, float* db1,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  const bool two = n_adapters > 1;
+  if (n_tokens < 0 || hidden < 1 || n_adapters < 1 || n_adapters > kMaxAdapters || seg0 < 1 ||
+      lo0 < 0 || (two && (seg1 < 1 || lo1 < 0)) || ldx < hidden || ldu < 16 * n_adapters ||
+      ldt < 16 * n_adapters || ldy < lo0 + seg0 || (two && ldy < lo1 + seg1) ||
+      n_tokens > (1 << 30) || hidden + seg0 + seg1 > (1 << 24))
+    return fail(TALM_EINVAL,
+                "lora_wgrad: bad shape (tokens %lld, hidden %lld, adapters %d, segments "
+                "%lld+%lld / %lld+%lld)",
+                (long long)n_tokens, (long long)hidden, n_adapters, (long long)lo0,
+                (long long)seg0, (long long)lo1, (long long)seg1);
+  const int64_t need = talm_lora_wgrad_workspace(n_tokens, hidden, seg0, two ? seg1 : 0);
+  if (workspace_bytes < need)
+    return fail(TALM_EINVAL, "lora_wgrad: workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)need);
+  if (n_tokens == 0) return ok();  // the caller zeroes the gradients of an empty batch
+  if (!x || !dy || !u || !t || !da0 || !db0 || (two && (!da1 || !db1)) || !workspace)
+    return fail(TALM_EINVAL, "lora_wgrad: null pointer");
+  WgradArgs a{};
+  a.x = x; a.ldx = ldx; a.dy = dy; a.ldy = ldy; a.u = u; a.ldu = ldu; a.t = t; a.ldt = ldt;
+  a.n_tokens = static_cast<int>(n_tokens); a.hidden = static_cast<int>(hidden);
+  a.n_adapters = n_adapters;
+  a.lo[0] = static_cast<int>(lo0); a.seg[0] = static_cast<int>(seg0); a.scaling[0] = scaling0;
+  a.da[0] = da0; a.db[0] = db0;
+  a.lo[1] = two ? static_cast<int>(lo1) : 0; a.seg[1] = two ? static_cast<int>(seg1) : 0;
+  a.scaling[1] = two ? scaling1 : 0.f; a.da[1] = two ? da1 : da0; a.db[1] = two ? db1 : db0;
+  a.part = static_cast<float*>(workspace);
+  a.cols = static_cast<int>(hidden + seg0 + (two ? seg1 : 0));
+  a.chunks = static_cast<int>((n_tokens + kWgChunk - 1) / kWgChunk);
+  const hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(lora_wgrad_partial_kernel,
+                     dim3(static_cast<unsigned>((a.cols + 255) / 256), static_cast<unsigned>(a.chunks)),
+                     dim3(256), 0, s, a);
+  hipLaunchKernelGGL(lora_wgrad_reduce_kernel,
+                     dim3(static_cast<unsigned>((static_cast<int64_t>(a.cols) * 32 + 255) / 256)),
+                     dim3(256), 0, s, a);
+  return check_launch("lora_wgrad");
 }

@@ -254,8 +254,8 @@ def _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope):
         a1 = halves[1][0] if len(adapters) > 1 else None
         s1 = adapters[1][1] if len(adapters) > 1 else 0.0
         size = x2.shape[1]
-        torch.ops.talm.lora_down(x2, halves[0][0], a1, size, size, 0, 0, adapters[0][1], s1, t,
-                                 ts)
+        torch.ops.talm.lora_down(x2, halves[0][0], a1, size, size, 0, 0, 0, adapters[0][1], s1,
+                                 t, ts)
     segs = [(bounds[seg], bounds[seg + 1]) for seg, _s, _p in adapters] + [(0, 0)] * 2
     bs = [b16 for _a, b16 in halves] + [None] * 2
     cos, sin = rope if rope is not None else (None, None)
@@ -316,14 +316,15 @@ def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
     halves = [rest[3 * k:3 * k + 3] for k in range(len(adapters))]  # (t, a16, b16)
     u = None
     if adapters:
-        bts = [b16.t().contiguous() for _t, _a, b16 in halves]
+        # u_g = (scaling_g dy_g) B_g, B_g read as stored ([segment, 16], k-major)
         t_tmp = torch.empty(n_tok, 16 * len(adapters), dtype=torch.float16, device=x2.device)
         u = torch.empty_like(t_tmp)
         lo = [bounds[seg] for seg, _s, _p in adapters] + [0]
         ks = [bounds[seg + 1] - bounds[seg] for seg, _s, _p in adapters] + [0]
         scal = [s_ for _seg, s_, _p in adapters] + [0.0]
-        torch.ops.talm.lora_down(dcat, bts[0], bts[1] if len(bts) > 1 else None, ks[0], ks[1],
-                                 lo[0], lo[1], scal[0], scal[1], t_tmp, u)
+        b1 = halves[1][2] if len(adapters) > 1 else None
+        torch.ops.talm.lora_down(dcat, halves[0][2], b1, ks[0], ks[1], lo[0], lo[1], 1, scal[0],
+                                 scal[1], t_tmp, u)
     dx = None
     if weight is not None:
         from .fused_head import transpose_weight_exact
@@ -334,20 +335,49 @@ def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
         dx = torch.empty(n_tok, size, dtype=torch.float16, device=x2.device)
         torch.ops.talm.qkv_lora_bwd_dx(dcat, weight_t, u, a_t, dx)
         del weight_t
+    lora_grads = [None] * (2 * len(adapters))
+    wanted = [ctx.needs_input_grad[8 + i] for i in range(2 * len(adapters))]
+    if adapters and any(wanted):
+        # all adapters' dA, dB in fp32 in one call (t of each adapter is a column view of one
+        # [N, 16 * adapters] buffer when the forward ran on MFMA)
+        t_all = halves[0][0]
+        if len(adapters) > 1 and (halves[1][0].data_ptr() != t_all.data_ptr() + 32
+                                  or halves[1][0].stride() != t_all.stride()):
+            return _weight_grads_ops(ctx, dcat, u, x2, halves, bounds, dx)
+        t_cat = torch.as_strided(t_all, (n_tok, 16 * len(adapters)), (t_all.stride(0), 1))
+        segs = [(bounds[seg], bounds[seg + 1] - bounds[seg], s_) for seg, s_, _p in adapters]
+        grads_ = [torch.empty(16, size, dtype=torch.float32, device=x2.device) if i % 2 == 0
+                  else torch.empty(segs[i // 2][1], 16, dtype=torch.float32, device=x2.device)
+                  for i in range(2 * len(adapters))]
+        pad = segs + [(0, 0, 0.0)]
+        ws = torch.empty(_ops_ws(n_tok, size, pad[0][1], pad[1][1]), dtype=torch.uint8,
+                         device=x2.device)
+        torch.ops.talm.lora_wgrad(x2, dcat, u, t_cat, pad[0][0], pad[0][1], pad[0][2], grads_[0],
+                                  grads_[1], pad[1][0], pad[1][1], pad[1][2],
+                                  grads_[2] if len(adapters) > 1 else None,
+                                  grads_[3] if len(adapters) > 1 else None, ws)
+        lora_grads = [g if w else None for g, w in zip(grads_, wanted)]
+    dx = None if dx is None else dx.view(ctx.x_shape)
+    return (dx, None, None, None, None, None, None, None, *lora_grads)
+
+
+def _ops_ws(n_tok, size, seg0, seg1):
+    from . import _ops
+
+    return _ops.lora_wgrad_workspace_bytes(n_tok, size, seg0, seg1)
+
+
+def _weight_grads_ops(ctx, dcat, u, x2, halves, bounds, dx):
+    """The adapters' dA / dB with the reference's ops (when their t are not one buffer)."""
     lora_grads = []
-    for k, (seg, scaling, _p) in enumerate(adapters):
-        t, a16, _b16 = halves[k]
+    for k, (seg, scaling, _p) in enumerate(ctx.adapters):
+        t, _a16, _b16 = halves[k]
         index = 8 + 2 * k
         uk = u[:, 16 * k:16 * (k + 1)]
         lora_grads.append(torch.mm(uk.t(), x2).float() if ctx.needs_input_grad[index] else None)
-        if ctx.needs_input_grad[index + 1]:
-            dy = dcat[:, bounds[seg]:bounds[seg + 1]]
-            if _power_of_two(scaling):
-                lora_grads.append(torch.mm(dy.t(), t).float().mul_(scaling))
-            else:
-                lora_grads.append(torch.mm((dy * scaling).t(), t).float())
-        else:
-            lora_grads.append(None)
+        dy = dcat[:, bounds[seg]:bounds[seg + 1]]
+        lora_grads.append(torch.mm((dy * scaling).t(), t).float()
+                          if ctx.needs_input_grad[index + 1] else None)
     dx = None if dx is None else dx.view(ctx.x_shape)
     return (dx, None, None, None, None, None, None, None, *lora_grads)
 

@@ -60,7 +60,7 @@ def test_lora_down_matches_fp32(n, size, adapters):
     t = torch.empty(n, 16 * adapters, dtype=torch.float16, device=DEV)
     ts = torch.empty_like(t)
     scalings = [2.0, 0.75][:adapters] + [0.0]
-    torch.ops.talm.lora_down(x, a[0], a[1] if adapters > 1 else None, size, size, 0, 0,
+    torch.ops.talm.lora_down(x, a[0], a[1] if adapters > 1 else None, size, size, 0, 0, 0,
                              scalings[0], scalings[1], t, ts)
     for g in range(adapters):
         ref = x.float() @ a[g].float().t()
@@ -87,7 +87,7 @@ def test_qkv_lora_fwd_matches_fp32(n, size, n_out, segs, rope_cols, with_bias):
     if segs:
         t = torch.empty(n, 16 * len(segs), dtype=torch.float16, device=DEV)
         ts = torch.empty_like(t)
-        torch.ops.talm.lora_down(x, a[0], a[1] if len(segs) > 1 else None, size, size, 0, 0,
+        torch.ops.talm.lora_down(x, a[0], a[1] if len(segs) > 1 else None, size, size, 0, 0, 0,
                                  scalings[0], scalings[1], t, ts)
     cos, sin = _rope_tables(n) if rope_cols else (None, None)
     out = torch.empty(n, n_out, dtype=torch.float16, device=DEV)
@@ -162,12 +162,13 @@ def test_lora_down_backward_form_matches_fp32():
          (torch.randn(256, 16, generator=g) * 0.05).half().to(DEV)]
     t = torch.empty(n, 32, dtype=torch.float16, device=DEV)
     u = torch.empty_like(t)
-    torch.ops.talm.lora_down(dcat, b[0].t().contiguous(), b[1].t().contiguous(), 1536, 256, 0,
-                             1792, 2.0, 2.0, t, u)
-    for k, (lo, hi) in enumerate([(0, 1536), (1792, 2048)]):
-        ref = 2.0 * (dcat[:, lo:hi].float() @ b[k].float())
-        got = u[:, 16 * k:16 * (k + 1)].float()
-        assert torch.all((got - ref).abs() <= 2.0 ** -10 * ref.abs() + 1e-5 * (hi - lo)), k
+    for kmajor in (0, 1):  # B_g transposed to [16, seg], or read as stored [seg, 16]
+        bs = [bb.t().contiguous() for bb in b] if not kmajor else b
+        torch.ops.talm.lora_down(dcat, bs[0], bs[1], 1536, 256, 0, 1792, kmajor, 2.0, 2.0, t, u)
+        for k, (lo, hi) in enumerate([(0, 1536), (1792, 2048)]):
+            ref = 2.0 * (dcat[:, lo:hi].float() @ b[k].float())
+            got = u[:, 16 * k:16 * (k + 1)].float()
+            assert torch.all((got - ref).abs() <= 2.0 ** -10 * ref.abs() + 1e-5 * (hi - lo)), k
 
 
 @pytest.mark.parametrize("n,size,n_out,rank", [(1130, 1536, 2048, 32), (257, 512, 1024, 32),
@@ -190,3 +191,35 @@ def test_qkv_lora_bwd_dx_matches_fp32(n, size, n_out, rank):
     torch.ops.talm.qkv_lora_bwd_dx(dcat, wt, u, a_t, dx)
     err = (dx.float() - ref).abs()
     assert torch.all(err <= 2e-3 * ref.abs() + 2e-3 * ref.abs().max()), float(err.max())
+
+
+@pytest.mark.parametrize("n,size,segs", [(1130, 1536, [(0, 1536), (1792, 256)]),
+                                         (65, 512, [(0, 512), (768, 256)]), (1, 64, [(64, 128)])])
+def test_lora_wgrad_matches_fp32(n, size, segs):
+    """dA_g = u_g^T x and dB_g = scaling_g dy_g^T t_g in fp32 (the reference rounds the fp16
+    GEMM output before its fp32 cast: within one fp16 rounding of the fp32 sums)."""
+    from talm_amd import _ops
+
+    _case(f"lora_wgrad n={n} H={size} segs={segs}")
+    g = torch.Generator().manual_seed(n)
+    n_out = max(lo + k for lo, k in segs)
+    x = torch.randn(n, size, generator=g).half().to(DEV)
+    dy = torch.randn(n, n_out, generator=g).half().to(DEV)
+    u = torch.randn(n, 16 * len(segs), generator=g).half().to(DEV)
+    t = torch.randn(n, 16 * len(segs), generator=g).half().to(DEV)
+    scal = [2.0, 0.5]
+    da = [torch.empty(16, size, device=DEV) for _ in segs]
+    db = [torch.empty(k, 16, device=DEV) for _lo, k in segs]
+    pad = segs + [(0, 0)]
+    ws = torch.empty(_ops.lora_wgrad_workspace_bytes(n, size, pad[0][1], pad[1][1]),
+                     dtype=torch.uint8, device=DEV)
+    two = len(segs) > 1
+    torch.ops.talm.lora_wgrad(x, dy, u, t, pad[0][0], pad[0][1], scal[0], da[0], db[0], pad[1][0],
+                              pad[1][1], scal[1], da[1] if two else None, db[1] if two else None,
+                              ws)
+    for k, (lo, seg) in enumerate(segs):
+        ref_a = u[:, 16 * k:16 * (k + 1)].float().t() @ x.float()
+        ref_b = scal[k] * (dy[:, lo:lo + seg].float().t() @ t[:, 16 * k:16 * (k + 1)].float())
+        for got, ref in ((da[k], ref_a), (db[k], ref_b)):
+            err = (got - ref).abs()
+            assert torch.all(err <= 1e-5 * ref.abs() + 1e-6 * n), float(err.max())
