@@ -34,7 +34,7 @@ constexpr int kWordsPerThread = 4;  // 32 weights per thread, four independent 1
 // convert to fp16" into one v_fma_mix (a single rounding of the exact product).
 __device__ __forceinline__ float mul_f32(float a, float b) {
   float p = a * b;
-  asm volatile("" : "+v"(p));
+  asm("" : "+v"(p));
   return p;
 }
 
@@ -64,22 +64,25 @@ __global__ __launch_bounds__(kThreads) void nf4_group_kernel(
   __syncthreads();
 
   const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kWordsPerThread) + threadIdx.x;
-  uint32_t words[kWordsPerThread];
-  float scales[kWordsPerThread];
+  // Every load of every word is issued before any is used: indices past the end are clamped to
+  // the last word (its store is skipped), so no load sits behind a branch and one wait covers
+  // the thread's whole batch.
+  uint32_t words[kWordsPerThread], codes[kWordsPerThread];
+  float a2[kWordsPerThread], o2[kWordsPerThread];
 #pragma unroll
   for (int j = 0; j < kWordsPerThread; ++j) {
-    const int64_t w = base + j * kThreads;
-    words[j] = 0u;
-    scales[j] = 0.f;
-    if (w < n_words) {
-      words[j] = __builtin_nontemporal_load(packed + w);
-      const int64_t row = w >> word_shift;
-      const int64_t blk2 = qblock2_shift >= 0 ? (row >> qblock2_shift)
-                                              : static_cast<int64_t>(static_cast<uint32_t>(row) / qblock2);
-      const float prod = mul_f32(s_code[absmax8[row]], absmax2[blk2]);
-      scales[j] = prod + offset2[blk2];
-    }
+    const int64_t w = min(base + j * kThreads, n_words - 1);
+    words[j] = __builtin_nontemporal_load(packed + w);
+    const int64_t row = w >> word_shift;
+    const int64_t blk2 = qblock2_shift >= 0 ? (row >> qblock2_shift)
+                                            : static_cast<int64_t>(static_cast<uint32_t>(row) / qblock2);
+    codes[j] = absmax8[row];
+    a2[j] = absmax2[blk2];
+    o2[j] = offset2[blk2];
   }
+  float scales[kWordsPerThread];
+#pragma unroll
+  for (int j = 0; j < kWordsPerThread; ++j) scales[j] = mul_f32(s_code[codes[j]], a2[j]) + o2[j];
 #pragma unroll
   for (int j = 0; j < kWordsPerThread; ++j) {
     const int64_t w = base + j * kThreads;
@@ -96,13 +99,18 @@ __global__ __launch_bounds__(kThreads) void nf4_words_kernel(const uint32_t* __r
   if (threadIdx.x < 16) s_levels[threadIdx.x] = kNF4Levels[threadIdx.x];
   __syncthreads();
   const int64_t base = static_cast<int64_t>(blockIdx.x) * (kThreads * kWordsPerThread) + threadIdx.x;
+  uint32_t words[kWordsPerThread];
+  float scales[kWordsPerThread];
+#pragma unroll
+  for (int j = 0; j < kWordsPerThread; ++j) {  // all loads first (clamped indices, no branch)
+    const int64_t w = min(base + j * kThreads, n_words - 1);
+    words[j] = __builtin_nontemporal_load(packed + w);
+    scales[j] = absmax[static_cast<uint32_t>(w) / words_per_block];
+  }
 #pragma unroll
   for (int j = 0; j < kWordsPerThread; ++j) {
     const int64_t w = base + j * kThreads;
-    if (w < n_words) {
-      const uint32_t word = __builtin_nontemporal_load(packed + w);
-      out[w] = dequant_word(word, absmax[static_cast<uint32_t>(w) / words_per_block], s_levels);
-    }
+    if (w < n_words) out[w] = dequant_word(words[j], scales[j], s_levels);
   }
 }
 
