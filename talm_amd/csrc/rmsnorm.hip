@@ -48,8 +48,11 @@ struct IO<uint16_t> {
   static __device__ __forceinline__ void store1(uint16_t* p, float v) { *p = f2h(v); }
 };
 
-// Forward, vector path. x = a (+ p); q = x; h = w * xhat; xhat = x * rstd.
-template <typename XT, typename OT, typename WT, bool ADD>
+// Forward, vector path, NC 8-column chunks per lane (NC = ceil(chunks / 64)). x = a (+ p);
+// q = x; h = w * xhat; xhat = x * rstd. Every load of the row is issued before any is used:
+// chunk indices past the row are clamped to its last chunk (their values are masked out and
+// their stores skipped), so no load waits behind a branch.
+template <typename XT, typename OT, typename WT, bool ADD, int NC>
 __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const XT* __restrict__ a,
                                                         const OT* __restrict__ p, XT* __restrict__ q,
                                                         OT* __restrict__ h, OT* __restrict__ xhat,
@@ -61,20 +64,25 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const XT* __restrict__ a
   if (row >= n_rows) return;
   const int n_chunks = n_cols / 8;
   const int64_t at = row * n_cols;
-  float x[kMaxChunks][8];
+  float x[NC][8], wv[NC][8];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lane + kWave * i, n_chunks - 1);
+    IO<XT>::load8(a + at + 8 * c, x[i]);
+    IO<WT>::load8(w + 8 * c, wv[i]);
+    if constexpr (ADD) {
+      float pv[8];
+      IO<OT>::load8(p + at + 8 * c, pv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[i][e] += pv[e];
+    }
+  }
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
+  for (int i = 0; i < NC; ++i) {
     const int c = lane + kWave * i;
     if (c < n_chunks) {
-      IO<XT>::load8(a + at + 8 * c, x[i]);
-      if constexpr (ADD) {
-        float pv[8];
-        IO<OT>::load8(p + at + 8 * c, pv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[i][e] += pv[e];
-        IO<XT>::store8(q + at + 8 * c, x[i]);
-      }
+      if constexpr (ADD) IO<XT>::store8(q + at + 8 * c, x[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += x[i][e] * x[i][e];
     }
@@ -83,15 +91,14 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const XT* __restrict__ a
   const float r = rsqrtf(ss / static_cast<float>(n_cols) + eps);
   if (lane == 0) rstd[row] = r;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
+  for (int i = 0; i < NC; ++i) {
     const int c = lane + kWave * i;
     if (c < n_chunks) {
-      float wv[8], xh[8], y[8];
-      IO<WT>::load8(w + 8 * c, wv);
+      float xh[8], y[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         xh[e] = x[i][e] * r;
-        y[e] = wv[e] * xh[e];
+        y[e] = wv[i][e] * xh[e];
       }
       IO<OT>::store8(h + at + 8 * c, y);
       IO<OT>::store8(xhat + at + 8 * c, xh);
@@ -100,7 +107,8 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const XT* __restrict__ a
 }
 
 // Backward, vector path. g = dy * w; dx = rstd * (g - xhat * mean(g * xhat)) (+ ds -> p).
-template <typename XT, typename OT, typename WT, bool ADD>
+// Loads first, as in the forward.
+template <typename XT, typename OT, typename WT, bool ADD, int NC>
 __global__ __launch_bounds__(kThreads) void rms_bwd_vec(XT* __restrict__ a, OT* __restrict__ p,
                                                         const XT* __restrict__ q,
                                                         const OT* __restrict__ h,
@@ -113,37 +121,36 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(XT* __restrict__ a, OT* 
   if (row >= n_rows) return;
   const int n_chunks = n_cols / 8;
   const int64_t at = row * n_cols;
-  float g[kMaxChunks][8], xh[kMaxChunks][8];
+  float g[NC][8], xh[NC][8], ds[NC][8];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lane + kWave * i, n_chunks - 1);
+    float wv[8];
+    IO<OT>::load8(h + at + 8 * c, g[i]);
+    IO<OT>::load8(xhat + at + 8 * c, xh[i]);
+    IO<WT>::load8(w + 8 * c, wv);
+    if constexpr (ADD) IO<XT>::load8(q + at + 8 * c, ds[i]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[i][e] *= wv[e];
+  }
+  const float r = rstd[row];
   float dot = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
-    const int c = lane + kWave * i;
-    if (c < n_chunks) {
-      float wv[8];
-      IO<OT>::load8(h + at + 8 * c, g[i]);
-      IO<OT>::load8(xhat + at + 8 * c, xh[i]);
-      IO<WT>::load8(w + 8 * c, wv);
+  for (int i = 0; i < NC; ++i)
+    if (lane + kWave * i < n_chunks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        g[i][e] *= wv[e];
-        dot += g[i][e] * xh[i][e];
-      }
-    }
-  }
+      for (int e = 0; e < 8; ++e) dot += g[i][e] * xh[i][e];
   const float cmean = wave_sum(dot) / static_cast<float>(n_cols);
-  const float r = rstd[row];
 #pragma unroll
-  for (int i = 0; i < kMaxChunks; ++i) {
+  for (int i = 0; i < NC; ++i) {
     const int c = lane + kWave * i;
     if (c < n_chunks) {
       float dx[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) dx[e] = r * (g[i][e] - xh[i][e] * cmean);
       if constexpr (ADD) {
-        float ds[8];
-        IO<XT>::load8(q + at + 8 * c, ds);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dx[e] += ds[e];
+        for (int e = 0; e < 8; ++e) dx[e] += ds[i][e];
         IO<OT>::store8(p + at + 8 * c, dx);
       }
       IO<XT>::store8(a + at + 8 * c, dx);
@@ -223,18 +230,35 @@ void launch(void* a, void* q, void* h, void* xhat, void* p, const void* weight, 
   OT* xo = static_cast<OT*>(xhat);
   OT* po = static_cast<OT*>(p);
   const WT* wv = static_cast<const WT*>(weight);
+  const int nc = (n_cols / 8 + kWave - 1) / kWave;  // chunks per lane on the vector path
   if (!backward) {
-    if (vec)
-      hipLaunchKernelGGL((rms_fwd_vec<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
-                         rstd, n_rows, n_cols, eps);
-    else
+    if (vec) {
+      switch (nc) {
+#define TALM_RMS_FWD(NC)                                                                          \
+  case NC:                                                                                        \
+    hipLaunchKernelGGL((rms_fwd_vec<XT, OT, WT, ADD, NC>), grid, block, 0, s, ax, po, qx, ho, xo, \
+                       wv, rstd, n_rows, n_cols, eps);                                            \
+    break;
+        TALM_RMS_FWD(1) TALM_RMS_FWD(2) TALM_RMS_FWD(3) TALM_RMS_FWD(4)
+        TALM_RMS_FWD(5) TALM_RMS_FWD(6) TALM_RMS_FWD(7) TALM_RMS_FWD(8)
+#undef TALM_RMS_FWD
+      }
+    } else
       hipLaunchKernelGGL((rms_fwd_any<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
                          rstd, n_rows, n_cols, eps);
   } else {
-    if (vec)
-      hipLaunchKernelGGL((rms_bwd_vec<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
-                         rstd, n_rows, n_cols);
-    else
+    if (vec) {
+      switch (nc) {
+#define TALM_RMS_BWD(NC)                                                                          \
+  case NC:                                                                                        \
+    hipLaunchKernelGGL((rms_bwd_vec<XT, OT, WT, ADD, NC>), grid, block, 0, s, ax, po, qx, ho, xo, \
+                       wv, rstd, n_rows, n_cols);                                                 \
+    break;
+        TALM_RMS_BWD(1) TALM_RMS_BWD(2) TALM_RMS_BWD(3) TALM_RMS_BWD(4)
+        TALM_RMS_BWD(5) TALM_RMS_BWD(6) TALM_RMS_BWD(7) TALM_RMS_BWD(8)
+#undef TALM_RMS_BWD
+      }
+    } else
       hipLaunchKernelGGL((rms_bwd_any<XT, OT, WT, ADD>), grid, block, 0, s, ax, po, qx, ho, xo, wv,
                          rstd, n_rows, n_cols);
   }
