@@ -263,17 +263,30 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
       // (solution/fused_head.py:178-182), the A operand of head_grad; in the chunk that holds
       // the vocabulary's last column, the columns past it become 0 (head_grad reads whole chunks)
       uint16_t* zrow = a.Z + static_cast<int64_t>(row) * a.ldz + (a.slice_col0[c] - a.slice_col0[0]);
+      // 8 chunks of 8 columns per lane in flight: all loads of a batch before any use (the
+      // chunk index is clamped, stores past the slice are skipped)
       const int cols = a.slice_cols[c];
-      for (int e0 = lane * 8; e0 < cols; e0 += kWave * 8) {
-        uint4 v = *reinterpret_cast<const uint4*>(zrow + e0);
-        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      const int chunks = (cols + 7) / 8;
+      constexpr int kBatch = 8;
+      for (int b0 = 0; b0 < chunks; b0 += kWave * kBatch) {
+        uint4 v[kBatch];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float p0 = e0 + 2 * q < cols ? __expf(lo_f(w[q]) - m) : 0.f;
-          const float p1 = e0 + 2 * q + 1 < cols ? __expf(hi_f(w[q]) - m) : 0.f;
-          w[q] = pack2(p0, p1);
+        for (int j = 0; j < kBatch; ++j) {
+          const int ch = min(b0 + j * kWave + lane, chunks - 1);
+          v[j] = *reinterpret_cast<const uint4*>(zrow + 8 * ch);
         }
-        *reinterpret_cast<uint4*>(zrow + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          const int ch = b0 + j * kWave + lane, e0 = 8 * ch;
+          uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float p0 = e0 + 2 * q < cols ? __expf(lo_f(w[q]) - m) : 0.f;
+            const float p1 = e0 + 2 * q + 1 < cols ? __expf(hi_f(w[q]) - m) : 0.f;
+            w[q] = pack2(p0, p1);
+          }
+          if (ch < chunks) *reinterpret_cast<uint4*>(zrow + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
       }
     }
     if (lane == 0) {
