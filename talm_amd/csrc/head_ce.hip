@@ -8,25 +8,29 @@
 //
 // The same recurrence here, shaped for MI355X. Slices are processed `group` at a time:
 //   head_logits   Z = H W^T over the group's columns; the epilogue rounds to fp16, stages the
-//                 tile in LDS, writes it to the group's logits buffer and emits, per (row,
-//                 128-column tile), the tile's max, first argmax, sum e^{z-max} and
-//                 sum e^{z-max} z.
+//                 tile in LDS and emits, per (row, 128-column tile), the tile's max m_t, first
+//                 argmax, sum e^{z-m_t} and sum e^{z-m_t} z; for labelled rows it also writes
+//                 P_t = fp16(e^{z - m_t}) to the group's buffer (the only copy of the logits
+//                 that reaches global memory).
 //   head_merge    one wavefront per row folds the tiles of each slice, in column order, into the
 //                 running statistics exactly as the reference's per-slice update, recording the
-//                 slice's running max m_c and rescale e^{m_old - m_c}; labelled rows' logits
-//                 become P = fp16(e^{z - m_c}) in place; after the last slice it writes token
+//                 slice's running max m_c and rescale e^{m_old - m_c}, and for labelled rows the
+//                 per-tile factors fp16(e^{m_t - m_c}); after the last slice it writes token
 //                 loss, entropy, argmax and correctness.
 //   head_grad     Y_c = P_c W_c for every slice of the group side by side, against the
-//                 transposed weight W^T [hidden, vocab] so that both operands are k-contiguous.
+//                 transposed weight W^T [hidden, vocab] so that both operands are k-contiguous;
+//                 P_c = fp16(P_t e^{m_t - m_c}), the reference's fp16(e^{z - m_c}) up to one
+//                 more fp16 rounding, is formed on the A fragments between LDS and the MFMAs.
 //   head_combine  acc = e^{m_old - m_c} acc + Y_c in slice order (the reference's rescale then
 //                 add), and after the last slice dH = acc / s - W16[target] in fp16.
 // The full [N, V] logits never exist: one group of slices (group * vchunk columns) at a time.
 //
-// Both GEMMs run the same tile core: 256 x 128 output tiles, four wavefronts of 128 x 64
-// (v_mfma_f32_32x32x16_f16), operands streamed by buffer_load_dwordx4 ... lds straight into a
-// three-stage LDS ring (two steps of 32 in flight while the third is multiplied), 16-byte chunks
-// XOR-swizzled so that fragment reads are free of bank conflicts, tiles mapped to XCDs so the
-// tiles that share an operand panel share an L2. Two workgroups per CU.
+// Both GEMMs run the tile core of mfma_tile.h (v_mfma_f32_32x32x16_f16, operands streamed by
+// buffer_load_dwordx4 ... lds straight into an LDS ring, 16-byte chunks XOR-swizzled so that
+// fragment reads are free of bank conflicts, tiles mapped to XCDs so the tiles that share an
+// operand panel share an L2) in one of two shapes picked per launch: Narrow, 256 x 128 tiles
+// with a three-stage ring of 32-deep steps and two workgroups per CU, or Wide, 256 x 256 tiles
+// with a two-stage ring of 64-deep steps and one workgroup of eight wavefronts per CU.
 #include "mfma_tile.h"
 
 #include <algorithm>
@@ -49,6 +53,13 @@ struct HeadShape : TileShape<256, BN, BK, STAGES, 2, BN / 64> {
 };
 using Narrow = HeadShape<128, 32, 3>;  // 72 KiB ring
 using Wide = HeadShape<256, 64, 2>;    // 128 KiB ring, 135 KiB with the staged logits tile
+// head_grad runs the same tiles with wavefronts of 64 x 128: half as many A fragments per
+// wavefront, each of which it scales between LDS and the MFMAs.
+using GradNarrow = TileShape<256, 128, 32, 3, 4, 1>;
+using GradWide = TileShape<256, 256, 64, 2, 4, 2>;
+static_assert(GradNarrow::kThreads == Narrow::kThreads && GradWide::kThreads == Wide::kThreads &&
+              GradNarrow::kPerCu == Narrow::kPerCu && GradWide::kPerCu == Wide::kPerCu,
+              "head_grad shapes launch like the logits shapes");
 constexpr int kBM = 256;
 
 struct Stat {
@@ -85,15 +96,17 @@ __device__ __forceinline__ Stat shfl_stat(Stat v, int off) {
 }
 
 // ------------------------------------------------------------------------------------------
-// GEMM1: Z[r][j] = fp16(sum_k H[r][k] W[j][k]) for the group's columns j < group_cols (W starts
-// at the group's first vocabulary row), plus the per-(row, 128-column tile) partial statistics.
+// GEMM1: z[r][j] = fp16(sum_k H[r][k] W[j][k]) for the group's columns j < group_cols (W starts
+// at the group's first vocabulary row) and the per-(row, 128-column tile) partial statistics;
+// rows r < n_p (the labelled rows when the gradient is wanted) store P[r][j] = fp16(e^{z - m_t})
+// with m_t the max of the row's 128-column tile, 0 past group_cols.
 // ------------------------------------------------------------------------------------------
 template <class S>
 __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_logits_kernel(
     const uint16_t* __restrict__ H, int64_t ldh, const uint16_t* __restrict__ W, int64_t ldw,
     int n_rows, int K, int group_cols, int first_col, uint16_t* __restrict__ Z, int64_t ldz,
     float4* __restrict__ part, int parts_per_row, int n_mtiles, int n_ntiles,
-    const int64_t* __restrict__ targets, float* __restrict__ ztarget) {
+    const int64_t* __restrict__ targets, float* __restrict__ ztarget, int n_p) {
   constexpr int kBN = S::kBN, kZS = S::kZS;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kLds];
 
@@ -133,13 +146,14 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_logits_kernel(
       }
   __syncthreads();
 
-  // Epilogue 2: partial statistics of one (row, 128-column statistics tile) per thread.
+  // Epilogue 2: partial statistics of one (row, 128-column statistics tile) per thread, which
+  // then replaces its z with P in LDS (stored for rows < n_p).
   {
     const int row = tid % kBM, st = tid / kBM, gr = m0 + row;
     const int c0 = n0 + st * kTile;  // the statistics tile's first column in the group
     const int valid = min(kTile, group_cols - c0);
     if (gr < n_rows && valid > 0) {
-      const uint16_t* zr = Zs + row * kZS + st * kTile;
+      uint16_t* zr = Zs + row * kZS + st * kTile;
       uint4 zv[kTile / 8];
 #pragma unroll
       for (int c = 0; c < kTile / 8; ++c) zv[c] = *reinterpret_cast<const uint4*>(zr + 8 * c);
@@ -158,35 +172,40 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_logits_kernel(
           }
         }
       }
+      // the logit at the target, when the target column is in this tile (one tile per row)
+      const int64_t rel = targets[gr] - (first_col + c0);
+      if (rel >= 0 && rel < valid) ztarget[gr] = h2f(zr[static_cast<int>(rel)]);
       float sum = 0.f, t = 0.f;
 #pragma unroll
       for (int c = 0; c < kTile / 8; ++c) {
         const uint32_t w4[4] = {zv[c].x, zv[c].y, zv[c].z, zv[c].w};
+        float ez[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int col = 8 * c + e;
           const float z = (e & 1) ? hi_f(w4[e >> 1]) : lo_f(w4[e >> 1]);
-          if (col < valid) {
-            const float ez = __expf(z - m);
-            sum += ez;
-            t += ez * z;
-          }
+          // columns past the group are z = 0 (zero weight rows) and get e^{-inf} = 0: no branch
+          ez[e] = __expf(col < valid ? z - m : -INFINITY);
+          sum += ez[e];
+          t += ez[e] * z;
         }
+        *reinterpret_cast<uint4*>(zr + 8 * c) = make_uint4(
+              pack2(ez[0], ez[1]), pack2(ez[2], ez[3]), pack2(ez[4], ez[5]), pack2(ez[6], ez[7]));
       }
       part[static_cast<int64_t>(gr) * parts_per_row + c0 / kTile] =
           make_float4(m, sum, t, __int_as_float(first_col + c0 + idx));
-      // the logit at the target, when the target column is in this tile (one tile per row)
-      const int64_t rel = targets[gr] - (first_col + c0);
-      if (rel >= 0 && rel < valid) ztarget[gr] = h2f(zr[static_cast<int>(rel)]);
     }
   }
+  if (n_p <= m0) return;
+  __syncthreads();
 
-  // Epilogue 3: the logits tile to global memory in 16-byte chunks (kBN / 8 per row).
+  // Epilogue 3: the P rows of the tile to global memory in 16-byte chunks (kBN / 8 per row); the
+  // chunk that holds the group's last column carries the zeros past it (head_grad reads chunks).
 #pragma unroll
   for (int it = 0; it < (kBM * kBN / 8) / S::kThreads; ++it) {
     const int c = it * S::kThreads + tid, row = c / (kBN / 8), kc = c % (kBN / 8);
     const int gr = m0 + row, gc = n0 + kc * 8;
-    if (gr < n_rows && gc < group_cols)
+    if (gr < n_p && gc < group_cols)
       *reinterpret_cast<uint4*>(Z + static_cast<int64_t>(gr) * ldz + gc) =
           *reinterpret_cast<const uint4*>(Zs + row * kZS + kc * 8);
   }
@@ -195,11 +214,19 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_logits_kernel(
 // ------------------------------------------------------------------------------------------
 // Running statistics, one wavefront per row, over the slices of one group.
 // ------------------------------------------------------------------------------------------
+// Factor of labelled row r and the group's 128-column tile t, e^{m_t - m_c} in fp16, where it
+// sits for head_grad: 128-row blocks b = r / 128 of [tile][block][128] halfs, and inside a block
+// the four rows r % 32 + 32 i (i < 4) next to each other, so that one 8-byte load gives a lane of
+// a 128-row wavefront the factors of its four A-fragment rows.
+__device__ __forceinline__ int64_t scale_index(int row, int tile, int n_blocks) {
+  return (static_cast<int64_t>(tile) * n_blocks + (row >> 7)) * 128 + (row & 31) * 4 + ((row >> 5) & 3);
+}
+
 struct MergeArgs {
   const float4* part;
   int parts_per_row;
-  uint16_t* Z;             // the group's logits; rows < n_grad become P = fp16(e^{z - m_c})
-  int64_t ldz;
+  uint16_t* scale;         // per-(labelled row, tile) factors, see scale_index
+  int scale_blocks;        // 128-row blocks per tile in `scale`
   const int64_t* targets;
   const float* ztarget;    // [n_rows] the logit at the target (written by head_logits)
   int n_rows;
@@ -259,34 +286,12 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
     const int64_t rel = target - a.slice_col0[c];
     if (labelled && rel >= 0 && rel < a.slice_cols[c]) zt = a.ztarget[row];
     if (row < a.n_grad) {
-      // the slice's logits of a labelled row become fp16(e^{z - m_c}) in place
-      // (solution/fused_head.py:178-182), the A operand of head_grad; in the chunk that holds
-      // the vocabulary's last column, the columns past it become 0 (head_grad reads whole chunks)
-      uint16_t* zrow = a.Z + static_cast<int64_t>(row) * a.ldz + (a.slice_col0[c] - a.slice_col0[0]);
-      // 8 chunks of 8 columns per lane in flight: all loads of a batch before any use (the
-      // chunk index is clamped, stores past the slice are skipped)
-      const int cols = a.slice_cols[c];
-      const int chunks = (cols + 7) / 8;
-      constexpr int kBatch = 8;
-      for (int b0 = 0; b0 < chunks; b0 += kWave * kBatch) {
-        uint4 v[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-          const int ch = min(b0 + j * kWave + lane, chunks - 1);
-          v[j] = *reinterpret_cast<const uint4*>(zrow + 8 * ch);
-        }
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-          const int ch = b0 + j * kWave + lane, e0 = 8 * ch;
-          uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float p0 = e0 + 2 * q < cols ? __expf(lo_f(w[q]) - m) : 0.f;
-            const float p1 = e0 + 2 * q + 1 < cols ? __expf(hi_f(w[q]) - m) : 0.f;
-            w[q] = pack2(p0, p1);
-          }
-          if (ch < chunks) *reinterpret_cast<uint4*>(zrow + e0) = make_uint4(w[0], w[1], w[2], w[3]);
-        }
+      // P_t = fp16(e^{z - m_t}) of each tile becomes the reference's fp16(e^{z - m_c})
+      // (solution/fused_head.py:178-182) through e^{m_t - m_c}, applied by head_grad
+      for (int tt = lane; tt < tiles; tt += kWave) {
+        const float mt = a.part[static_cast<int64_t>(row) * a.parts_per_row + tile0 + tt].x;
+        const float f = mt == -INFINITY ? 0.f : __expf(mt - m);
+        a.scale[scale_index(row, tile0 + tt, a.scale_blocks)] = f2h(f);
       }
     }
     if (lane == 0) {
@@ -308,10 +313,35 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// GEMM2: Y_c[r][h] = sum_j P[r][zc + j] W^T[h][col0 + zc + j] over slice c's columns (zc = c *
+// GEMM2: Y_c[r][h] = sum_j P_c[r][zc + j] W^T[h][col0 + zc + j] over slice c's columns (zc = c *
 // vchunk inside the group), for the first n_grad rows (the labelled rows, put first by the
-// caller); P = fp16(e^{z - m_c}) is what head_merge left in the logits buffer.
+// caller); P_c = fp16(P_t e^{m_t - m_c}) from head_logits' P_t and head_merge's factors.
 // ------------------------------------------------------------------------------------------
+
+// The A-fragment hook of head_grad: ring step kt covers columns [zc + kt BK, + BK) of one 128-column
+// tile (BK divides 128, zc is a multiple of BK); lane l of the wavefront owning rows
+// [r0, r0 + 32 FRAGS) multiplies fragment i (row r0 + 32 i + l % 32) by the row's factor of that
+// tile. r0 is a multiple of 32 FRAGS, so the lane's FRAGS factors are adjacent: one load per step.
+template <int BK, int FRAGS>
+struct TileScale {
+  static_assert(FRAGS == 2 || FRAGS == 4, "two or four 32-row A fragments per wavefront");
+  using Word = typename std::conditional<FRAGS == 4, uint2, uint32_t>::type;
+  const uint16_t* base;  // &scale[scale_index(r0 + lane % 32, 0, blocks)]
+  int64_t tile_stride;   // blocks * 128
+  int zc;
+  Word nxt, cur;
+  __device__ __forceinline__ void prefetch(int kt) {
+    nxt = *reinterpret_cast<const Word*>(base + ((zc + kt * BK) >> 7) * tile_stride);
+  }
+  __device__ __forceinline__ void advance() { cur = nxt; }
+  __device__ __forceinline__ half8_t apply(half8_t a, int i) const {
+    uint32_t w;
+    if constexpr (FRAGS == 4) w = i < 2 ? cur.x : cur.y;
+    else w = cur;
+    const uint16_t h = static_cast<uint16_t>((i & 1) ? w >> 16 : w & 0xffffu);
+    return a * __builtin_bit_cast(_Float16, h);
+  }
+};
 struct GradArgs {
   const uint16_t* Z;
   int64_t ldz;
@@ -323,6 +353,8 @@ struct GradArgs {
   int vchunk;
   int slice_cols[8];
   int ksplit;             // parts of each slice's columns, each with its own partial
+  const uint16_t* scale;  // per-(row, tile) factors of head_merge, see scale_index
+  int scale_blocks;
   float* Y;               // [n_slices * ksplit][n_grad][hidden] fp32
   int n_mtiles, n_ntiles, n_tiles;
 };
@@ -330,7 +362,7 @@ struct GradArgs {
 template <class S>
 __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradArgs a) {
   constexpr int kBN = S::kBN;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRingBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing];
 
   // hidden tiles vary fastest inside an XCD's range: the tiles in flight on one XCD share P rows
   const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_tiles));
@@ -354,6 +386,10 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
   la.init(a.Z + static_cast<int64_t>(m0) * a.ldz + zc, a.ldz, a.n_grad - m0, kn, wave, lane);
   lb.init(a.WT + static_cast<int64_t>(n0) * a.ldwt + a.col0 + zc, a.ldwt, a.hidden - n0, kn,
           wave, lane);
+  TileScale<S::kBK, S::kFragM> sc;
+  sc.base = a.scale + scale_index(m0 + wm * S::kWaveM + (lane & 31), 0, a.scale_blocks);
+  sc.tile_stride = static_cast<int64_t>(a.scale_blocks) * 128;
+  sc.zc = kn > 0 ? zc : 0;  // an empty part (zc may be the group's end) still loads in range
   Acc<S> acc;
   ring_gemm<S>(
       smem, (kn + S::kBK - 1) / S::kBK,
@@ -361,7 +397,7 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
         la.issue(slot, kt * S::kBK, wave);
         lb.issue(slot + S::kAChunks * 16, kt * S::kBK, wave);
       },
-      acc, lane, wave);
+      acc, lane, wave, sc);
 
   float* Y = a.Y + static_cast<int64_t>(piece) * a.n_grad * a.hidden;
 #pragma unroll
@@ -370,8 +406,8 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
     for (int j = 0; j < S::kFragN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int gr = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int gc = n0 + wn * 64 + j * 32 + (lane & 31);
+        const int gr = m0 + acc_row<S>(wm, i, v, lane);
+        const int gc = n0 + acc_col<S>(wn, j, lane);
         if (gr < a.n_grad && gc < a.hidden) Y[static_cast<int64_t>(gr) * a.hidden + gc] = acc[i][j][v];
       }
 }
@@ -521,9 +557,10 @@ GradPlan plan_grad(int64_t n_grad, int64_t hidden, int ns) {
 }
 
 struct Layout {
-  size_t z, part, run, ztarget, alpha, y, acc, total;
+  size_t z, part, scale, run, ztarget, alpha, y, acc, total;
   int64_t ldz;
   int parts_per_row;
+  int scale_blocks;  // 128-row blocks of the factor table: whole 256-row tiles of head_grad
 };
 
 Layout layout(int64_t n_rows, int64_t hidden, int64_t vocab, int64_t vchunk, int64_t n_grad,
@@ -537,9 +574,11 @@ Layout layout(int64_t n_rows, int64_t hidden, int64_t vocab, int64_t vchunk, int
   const int64_t pieces = n_grad > 0 ? std::max<int64_t>(group * plan_grad(n_grad, hidden, group).ksplit,
                                                         last * plan_grad(n_grad, hidden, last).ksplit)
                                     : 0;
+  l.scale_blocks = static_cast<int>((n_grad + kBM - 1) / kBM * 2);
   size_t off = 0;
-  l.z = off;      off = align_up(off + static_cast<size_t>(n_rows) * l.ldz * 2, 256);
+  l.z = off;      off = align_up(off + static_cast<size_t>(n_grad) * l.ldz * 2, 256);
   l.part = off;   off = align_up(off + static_cast<size_t>(n_rows) * l.parts_per_row * 16, 256);
+  l.scale = off;  off = align_up(off + static_cast<size_t>(l.parts_per_row) * l.scale_blocks * 128 * 2, 256);
   l.run = off;    off = align_up(off + static_cast<size_t>(n_rows) * 6 * 4, 256);
   l.ztarget = off; off = align_up(off + static_cast<size_t>(n_rows) * 4, 256);
   l.alpha = off;  off = align_up(off + static_cast<size_t>(group) * n_rows * 4, 256);
@@ -624,6 +663,7 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   uint16_t* Z = reinterpret_cast<uint16_t*>(ws + l.z);
   float4* part = reinterpret_cast<float4*>(ws + l.part);
+  uint16_t* scale = reinterpret_cast<uint16_t*>(ws + l.scale);
   float* run = reinterpret_cast<float*>(ws + l.run);
   float* ztarget = reinterpret_cast<float*>(ws + l.ztarget);
   float* alpha = reinterpret_cast<float*>(ws + l.alpha);
@@ -632,6 +672,7 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
   const hipStream_t s = as_stream(stream);
   const int rows = static_cast<int>(n_rows);
   const int mt = (rows + kBM - 1) / kBM;
+  const int n_p = grad_hidden ? static_cast<int>(n_grad) : 0;  // rows whose P is stored
 
   for (int64_t s0 = 0; s0 < slices; s0 += g) {
     const int ns = static_cast<int>(slices - s0 < g ? slices - s0 : g);
@@ -643,19 +684,20 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
                          dim3(Wide::kThreads), 0, s, hidden_states, ldh, weight + col0 * ldw, ldw,
                          rows, static_cast<int>(hidden), static_cast<int>(gcols),
                          static_cast<int>(col0), Z, l.ldz, part, l.parts_per_row, mt, nt, targets,
-                         ztarget);
+                         ztarget, n_p);
     } else {
       const int nt = static_cast<int>((gcols + Narrow::kBN - 1) / Narrow::kBN);
       hipLaunchKernelGGL((head_logits_kernel<Narrow>), dim3(static_cast<unsigned>(mt * nt)),
                          dim3(Narrow::kThreads), 0, s, hidden_states, ldh, weight + col0 * ldw,
                          ldw, rows, static_cast<int>(hidden), static_cast<int>(gcols),
                          static_cast<int>(col0), Z, l.ldz, part, l.parts_per_row, mt, nt, targets,
-                         ztarget);
+                         ztarget, n_p);
     }
     MergeArgs ma{};
-    ma.part = part; ma.parts_per_row = l.parts_per_row; ma.Z = Z; ma.ldz = l.ldz;
+    ma.part = part; ma.parts_per_row = l.parts_per_row;
+    ma.scale = scale; ma.scale_blocks = l.scale_blocks;
     ma.targets = targets; ma.ztarget = ztarget; ma.n_rows = rows;
-    ma.n_grad = grad_hidden ? static_cast<int>(n_grad) : 0;
+    ma.n_grad = n_p;
     ma.n_slices = ns; ma.vchunk = static_cast<int>(vchunk);
     for (int c = 0; c < ns; ++c) {
       const int64_t c0 = col0 + c * vchunk;
@@ -674,6 +716,7 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
       ga.n_grad = static_cast<int>(n_grad); ga.hidden = static_cast<int>(hidden);
       ga.vchunk = static_cast<int>(vchunk);
       for (int c = 0; c < ns; ++c) ga.slice_cols[c] = ma.slice_cols[c];
+      ga.scale = scale; ga.scale_blocks = l.scale_blocks;
       ga.Y = Y;
       const GradPlan gp = plan_grad(n_grad, hidden, ns);
       const int bn = gp.wide ? Wide::kBN : Narrow::kBN;
@@ -682,11 +725,11 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
       ga.n_ntiles = static_cast<int>((hidden + bn - 1) / bn);
       ga.n_tiles = ga.n_mtiles * ga.n_ntiles * ns * gp.ksplit;
       if (gp.wide)
-        hipLaunchKernelGGL((head_grad_kernel<Wide>), dim3(static_cast<unsigned>(ga.n_tiles)),
-                           dim3(Wide::kThreads), 0, s, ga);
+        hipLaunchKernelGGL((head_grad_kernel<GradWide>), dim3(static_cast<unsigned>(ga.n_tiles)),
+                           dim3(GradWide::kThreads), 0, s, ga);
       else
-        hipLaunchKernelGGL((head_grad_kernel<Narrow>), dim3(static_cast<unsigned>(ga.n_tiles)),
-                           dim3(Narrow::kThreads), 0, s, ga);
+        hipLaunchKernelGGL((head_grad_kernel<GradNarrow>), dim3(static_cast<unsigned>(ga.n_tiles)),
+                           dim3(GradNarrow::kThreads), 0, s, ga);
       CombineArgs ca{};
       ca.acc = accbuf; ca.Y = Y; ca.alpha = alpha; ca.run = run; ca.targets = targets;
       ca.W = weight; ca.ldw = ldw; ca.vocab = vocab; ca.grad = grad_hidden; ca.n_rows = rows;

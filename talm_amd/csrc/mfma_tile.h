@@ -11,6 +11,8 @@
 
 #include "common.h"
 
+#include <type_traits>
+
 namespace talm {
 namespace {
 
@@ -128,10 +130,21 @@ struct Loader {
 template <class S>
 using Acc = f32x16[S::kFragM][S::kFragN];
 
+// Scaling of the A fragments between their LDS read and the MFMAs, per ring step. The default
+// leaves them as read; a scaling hook loads step kt's factors in prefetch(kt) (one step ahead,
+// before the DMA group the next step waits for, so that wait covers them too), makes them current
+// in advance() and multiplies fragment i of the wavefront in apply().
+struct NoScale {
+  __device__ __forceinline__ void prefetch(int) {}
+  __device__ __forceinline__ void advance() {}
+  __device__ __forceinline__ half8_t apply(half8_t a, int) const { return a; }
+};
+
 // One step of the wavefront's block: BK / 16 x (kFragM A + kFragN B fragments, their MFMAs).
-template <class S>
+template <class S, class Scale = NoScale>
 __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uint4* __restrict__ Bs,
-                                         Acc<S>& acc, int lane, int wm, int wn) {
+                                         Acc<S>& acc, int lane, int wm, int wn,
+                                         const Scale& scale = Scale()) {
   constexpr int kSteps = S::kBK / 16;
   half8_t a[kSteps][S::kFragM], b[kSteps][S::kFragN];
 #pragma unroll
@@ -139,8 +152,8 @@ __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uin
     const int kc = ks * 2 + (lane >> 5);
 #pragma unroll
     for (int i = 0; i < S::kFragM; ++i)
-      a[ks][i] = __builtin_bit_cast(
-          half8_t, As[swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), kc)]);
+      a[ks][i] = scale.apply(__builtin_bit_cast(
+          half8_t, As[swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), kc)]), i);
 #pragma unroll
     for (int j = 0; j < S::kFragN; ++j)
       b[ks][j] = __builtin_bit_cast(
@@ -159,10 +172,11 @@ __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uin
 // at slot + A bytes, exactly Loader<S, BM>::kPer + Loader<S, BN>::kPer DMA instructions per
 // thread. Step kt waits for its own group (with three slots the next group stays in flight); one
 // barrier makes every wavefront's data visible and retires the slot read in step kt - 1, which
-// then receives step kt + STAGES - 1.
-template <class S, class Issue>
+// then receives step kt + STAGES - 1. scale.prefetch(kt + 1) is issued just before the group of
+// step kt + STAGES - 1, so the same wait that covers step kt + 1's operands covers its factors.
+template <class S, class Issue, class Scale = NoScale>
 __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& issue, Acc<S>& acc,
-                                          int lane, int wave) {
+                                          int lane, int wave, Scale&& scale = Scale()) {
   constexpr int kGroup = Loader<S, S::kBM>::kPer + Loader<S, S::kBN>::kPer;
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 #pragma unroll
@@ -171,21 +185,37 @@ __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& i
     for (int j = 0; j < S::kFragN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  // With a scaling hook every step issues a full group (past nk the loaders read zeros into a
+  // retired slot) and one factor load (clamped to the last step), so the compiler's own wait for
+  // the factors, which it places where step kt + 1's factors become current, is the same
+  // vmcnt(kGroup) as the ring's.
+  constexpr bool kScaled = !std::is_same<std::decay_t<Scale>, NoScale>::value;
 #pragma unroll
-  for (int st = 0; st < S::kStages - 1; ++st)
-    if (st < nk) issue(smem + st * S::kStageBytes, st);
+  for (int st = 0; st < S::kStages - 1; ++st) {
+    if (kScaled || st < nk) issue(smem + st * S::kStageBytes, st);
+    if (kScaled && st == 0) {  // step 0's factors right behind its group
+      asm volatile("" ::: "memory");
+      scale.prefetch(0);
+      asm volatile("" ::: "memory");
+    }
+  }
   int s = 0;  // slot of step kt
   for (int kt = 0; kt < nk; ++kt) {
     if (S::kStages == 3 && kt + 1 < nk) wait_vmcnt<kGroup>();
     else wait_vmcnt<0>();
     lds_barrier();
-    if (kt + S::kStages - 1 < nk) {
+    scale.advance();
+    if (kScaled) {
+      scale.prefetch(kt + 1 < nk ? kt + 1 : kt);
+      asm volatile("" ::: "memory");  // the factor load stays ahead of the group
+    }
+    if (kScaled || kt + S::kStages - 1 < nk) {
       const int s2 = s == 0 ? S::kStages - 1 : s - 1;  // slot (kt + STAGES - 1) % STAGES
       issue(smem + s2 * S::kStageBytes, kt + S::kStages - 1);
     }
     const unsigned char* st = smem + s * S::kStageBytes;
     mma_step<S>(reinterpret_cast<const uint4*>(st),
-                reinterpret_cast<const uint4*>(st + S::kAChunks * 16), acc, lane, wm, wn);
+                reinterpret_cast<const uint4*>(st + S::kAChunks * 16), acc, lane, wm, wn, scale);
     s = s + 1 == S::kStages ? 0 : s + 1;
   }
   __syncthreads();  // every wavefront is done with the ring before the caller reuses the LDS
