@@ -5,7 +5,7 @@
 // branch = t B^T and out[:, seg] += scaling * branch, and the rotary embedding on q and k.
 // Here that is two launches:
 //   lora_down   t = x A_g^T for every adapter g (rank 16 each) and ts = scaling_g * t: a
-//               register-only v_mfma_f32_16x16x32_f16 kernel, the reduction split over the four
+//               register-only v_mfma_f32_16x16x32_f16 kernel, the reduction split over the eight
 //               wavefronts of a workgroup (t is what the backward keeps, as in the reference).
 //   qkv_fwd     out = [x | ts] [W | B]^T + b with the rotary embedding applied in the epilogue:
 //               the LoRA up-projection is one more 64-deep step of the tile GEMM (the adapter's
@@ -25,7 +25,8 @@ constexpr int kMaxAdapters = 2;
 
 // ------------------------------------------------------------------------------------------
 // t[r][16 g + i] = fp16(sum_k x[r][k] A_g[i][k]); ts = fp16(scaling_g * the same fp32 sum).
-// One workgroup per 16 tokens, wavefront w takes the 32-deep k-steps w, w + 4, ...
+// One workgroup per 16 tokens, wavefront w takes the 32-deep k-steps w, w + 8, ..., issuing the
+// loads of kDownBatch steps before their MFMAs (steps past the reduction read zeros).
 // ------------------------------------------------------------------------------------------
 // Adapter g reduces over x's columns [xcol_g, xcol_g + k_g) against A_g [16][k_g] (the forward:
 // both over all of x; the backward: u = dy_seg B_g over each adapter's own output columns).
@@ -38,12 +39,66 @@ __device__ __forceinline__ half8_t gather_kmajor(const uint16_t* a, int k, int n
   return v;
 }
 
-__global__ __launch_bounds__(256) void lora_down_kernel(
+constexpr int kDownWaves = 8;
+constexpr int kDownBatch = 8;
+
+// One adapter's 16 x 16 block of one wavefront: sum over its k-steps of x[16 rows] A^T. A k-step
+// at or past klen reads x as zeros (out-of-range buffer offset) and A at a clamped, in-range k.
+template <bool KMAJOR>
+__device__ __forceinline__ f32x4 down_block(__amdgpu_buffer_rsrc_t rx, uint32_t xoff,
+                                            __amdgpu_buffer_rsrc_t ra, uint32_t aoff,
+                                            const uint16_t* a, int klen, int row, int kq, int wave) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = wave * 32; kb < klen; kb += 32 * kDownWaves * kDownBatch) {
+    half8_t xa[kDownBatch], wa[kDownBatch];
+    uint32_t g[KMAJOR ? kDownBatch : 1][8];  // k-major A: the 8 gathered halfs of each step
+#pragma unroll
+    for (int j = 0; j < kDownBatch; ++j) {
+      const int k = kb + 32 * kDownWaves * j;
+      const bool in = k < klen;
+      const uint32_t kbytes = static_cast<uint32_t>(k * 2);
+      xa[j] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, in ? xoff + kbytes : kOob, 0, 0));
+      if constexpr (KMAJOR) {
+        const uint16_t* ak = a + (min(k, klen - 32) + kq) * 16 + row;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g[j][e] = ak[e * 16];
+      } else {
+        wa[j] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra, in ? aoff + kbytes : kOob, 0, 0));
+      }
+    }
+    // every load of the batch is issued before the first use: the empty statements take the
+    // loaded registers, so the compiler waits for the batch here and not load by load
+#pragma unroll
+    for (int j = 0; j < kDownBatch; ++j) {
+      asm volatile("" : "+v"(xa[j]));
+      if constexpr (KMAJOR) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(g[j][e]));
+      } else {
+        asm volatile("" : "+v"(wa[j]));
+      }
+    }
+    if constexpr (KMAJOR) {
+#pragma unroll
+      for (int j = 0; j < kDownBatch; ++j) {
+        uint4 w;
+        w.x = g[j][0] | (g[j][1] << 16); w.y = g[j][2] | (g[j][3] << 16);
+        w.z = g[j][4] | (g[j][5] << 16); w.w = g[j][6] | (g[j][7] << 16);
+        wa[j] = __builtin_bit_cast(half8_t, w);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kDownBatch; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wa[j], acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+__global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int n_tokens, int k0len, int k1len, int xcol0,
     int xcol1, const uint16_t* __restrict__ a0, const uint16_t* __restrict__ a1, int n_adapters,
     int a_kmajor, float s0, float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts,
     int64_t ldt) {
-  __shared__ float red[4][kMaxAdapters][16][16 + 1];
+  __shared__ float red[kDownWaves][kMaxAdapters][16][16 + 1];
   const int m0 = blockIdx.x * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = lane & 15, kq = 8 * (lane >> 4);
@@ -55,22 +110,14 @@ __global__ __launch_bounds__(256) void lora_down_kernel(
   const uint32_t xoff = m0 + row < n_tokens ? static_cast<uint32_t>((row * ldx + kq) * 2) : kOob;
   const uint32_t aoff0 = static_cast<uint32_t>((row * k0len + kq) * 2);
   const uint32_t aoff1 = static_cast<uint32_t>((row * k1len + kq) * 2);
-  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = wave * 32; k0 < k0len; k0 += 128) {
-    const uint32_t kb = static_cast<uint32_t>(k0 * 2);
-    const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx0, xoff + kb, 0, 0));
-    const half8_t b = a_kmajor ? gather_kmajor(a0, k0 + kq, row)
-                               : __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra0, aoff0 + kb, 0, 0));
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc0, 0, 0, 0);
-  }
-  if (n_adapters > 1) {
-    for (int k0 = wave * 32; k0 < k1len; k0 += 128) {
-      const uint32_t kb = static_cast<uint32_t>(k0 * 2);
-      const half8_t a = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx1, xoff + kb, 0, 0));
-      const half8_t b = a_kmajor ? gather_kmajor(a1, k0 + kq, row)
-                                 : __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra1, aoff1 + kb, 0, 0));
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc1, 0, 0, 0);
-    }
+  const uint16_t* a1s = n_adapters > 1 ? a1 : a0;
+  f32x4 acc0, acc1 = {0.f, 0.f, 0.f, 0.f};
+  if (a_kmajor) {
+    acc0 = down_block<true>(rx0, xoff, ra0, aoff0, a0, k0len, row, kq, wave);
+    if (n_adapters > 1) acc1 = down_block<true>(rx1, xoff, ra1, aoff1, a1s, k1len, row, kq, wave);
+  } else {
+    acc0 = down_block<false>(rx0, xoff, ra0, aoff0, a0, k0len, row, kq, wave);
+    if (n_adapters > 1) acc1 = down_block<false>(rx1, xoff, ra1, aoff1, a1s, k1len, row, kq, wave);
   }
   // accumulator element v of lane l: token 4 * (l / 16) + v, rank l % 16
 #pragma unroll
@@ -80,10 +127,12 @@ __global__ __launch_bounds__(256) void lora_down_kernel(
   }
   __syncthreads();
   const int tid = threadIdx.x;
-  for (int e = tid; e < n_adapters * 256; e += 256) {
+  for (int e = tid; e < n_adapters * 256; e += 64 * kDownWaves) {
     const int g = e >> 8, r = (e >> 4) & 15, i = e & 15;
     if (m0 + r >= n_tokens) continue;
-    const float sum = red[0][g][r][i] + red[1][g][r][i] + red[2][g][r][i] + red[3][g][r][i];
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDownWaves; ++w) sum += red[w][g][r][i];
     const int64_t at = static_cast<int64_t>(m0 + r) * ldt + g * kRank + i;
     t[at] = f2h(sum);
     ts[at] = f2h((g == 0 ? s0 : s1) * sum);
@@ -338,10 +387,16 @@ __global__ __launch_bounds__(256) void lora_wgrad_partial_kernel(WgradArgs a) {
 #pragma unroll
   for (int i = 0; i < 32; ++i) acc[i] = 0.f;
   float* out = a.part + (static_cast<int64_t>(chunk) * a.cols + c) * 32;
+  // the chunk's column values are all loaded before use (rows past the batch are clamped to its
+  // last row and zeroed); their u / t rows in LDS are zero too
+  float v[kWgChunk];
   if (c < a.hidden) {  // dA column h: both adapters' u
     const uint16_t* xc = a.x + static_cast<int64_t>(r0) * a.ldx + c;
-    for (int r = 0; r < rn; ++r) {
-      const float xv = h2f(xc[static_cast<int64_t>(r) * a.ldx]);
+#pragma unroll
+    for (int r = 0; r < kWgChunk; ++r) v[r] = h2f(xc[static_cast<int64_t>(min(r, rn - 1)) * a.ldx]);
+#pragma unroll
+    for (int r = 0; r < kWgChunk; ++r) {
+      const float xv = r < rn ? v[r] : 0.f;
 #pragma unroll
       for (int i = 0; i < 32; ++i) acc[i] += su[r][i] * xv;
     }
@@ -349,8 +404,11 @@ __global__ __launch_bounds__(256) void lora_wgrad_partial_kernel(WgradArgs a) {
     const int cb = c - a.hidden, g = cb >= a.seg[0] ? 1 : 0;
     const int j = g ? cb - a.seg[0] : cb, col = (g ? a.lo[1] : a.lo[0]) + j;
     const uint16_t* yc = a.dy + static_cast<int64_t>(r0) * a.ldy + col;
-    for (int r = 0; r < rn; ++r) {
-      const float yv = h2f(yc[static_cast<int64_t>(r) * a.ldy]);
+#pragma unroll
+    for (int r = 0; r < kWgChunk; ++r) v[r] = h2f(yc[static_cast<int64_t>(min(r, rn - 1)) * a.ldy]);
+#pragma unroll
+    for (int r = 0; r < kWgChunk; ++r) {
+      const float yv = r < rn ? v[r] : 0.f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[i] += st[r][16 * g + i] * yv;
     }
@@ -405,7 +463,8 @@ TALM_API int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, in
   if (!x || !a0 || (two && !a1) || !t || !ts) return fail(TALM_EINVAL, "lora_down: null pointer");
   if (!aligned(x, 16) || !aligned(a0, 16) || (two && !aligned(a1, 16)))
     return fail(TALM_EINVAL, "lora_down: x and the A matrices must be 16-byte aligned");
-  hipLaunchKernelGGL(lora_down_kernel, dim3(static_cast<unsigned>((n_tokens + 15) / 16)), dim3(256),
+  hipLaunchKernelGGL(lora_down_kernel, dim3(static_cast<unsigned>((n_tokens + 15) / 16)),
+                     dim3(64 * kDownWaves),
                      0, as_stream(stream), x, ldx, static_cast<int>(n_tokens), static_cast<int>(k0),
                      static_cast<int>(two ? k1 : k0), static_cast<int>(xcol0),
                      static_cast<int>(two ? xcol1 : xcol0), a0, a1, n_adapters, a_kmajor ? 1 : 0,
