@@ -1,9 +1,11 @@
-"""Build libtalm.so (the gfx950 kernels behind include/talm.h) in-tree with hipcc.
+"""Build libtalm.so (the gfx950 kernels behind include/talm.h) and libtalm_torch.so (the
+torch.ops.talm.* custom ops over it) in-tree.
 
-    python -m talm_amd.build          # compile every csrc/*.hip for gfx950 and link
+    python -m talm_amd.build          # compile every csrc/*.hip for gfx950, link, then the ops
 
-Each source compiles to its own object in parallel under talm_amd/_build/, then one link makes
-talm_amd/libtalm.so. Only the `extern "C"` entry points are exported (-fvisibility=hidden).
+Each HIP source compiles to its own object in parallel under talm_amd/_build/, then one link makes
+talm_amd/libtalm.so; only the `extern "C"` entry points are exported (-fvisibility=hidden).
+csrc/torch_ops.cpp is host code only: g++ against PyTorch's headers, linked to libtalm.so.
 """
 
 import concurrent.futures
@@ -17,6 +19,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtalm.so"
+OPS_LIB = PKG / "libtalm_torch.so"
+INCLUDE = PKG.parent / "include"
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are switched off for every kernel (the compiler must not form
@@ -62,7 +66,30 @@ def build(verbose=False):
     if proc.returncode != 0:
         raise RuntimeError(f"link of libtalm.so failed:\n{proc.stdout}{proc.stderr}")
     os.replace(tmp, LIB)
+    build_ops()
     return LIB
+
+
+def build_ops():
+    """Compile csrc/torch_ops.cpp into libtalm_torch.so (needs libtalm.so); returns its path."""
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    includes = [INCLUDE, *map(Path, cpp_extension.include_paths()), Path("/opt/rocm/include")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = OPS_LIB.with_suffix(".so.tmp")
+    cmd = [shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-fvisibility=hidden", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DUSE_ROCM",
+           "-D__HIP_PLATFORM_AMD__=1", *[f"-I{p}" for p in includes],
+           str(CSRC / "torch_ops.cpp"), "-o", str(tmp), f"-L{PKG}", "-ltalm", f"-L{torch_lib}",
+           "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip", "-lhipblaslt", "-Wl,-rpath,$ORIGIN",
+           f"-Wl,-rpath,{torch_lib}"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build of libtalm_torch.so failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, OPS_LIB)
+    return OPS_LIB
 
 
 if __name__ == "__main__":

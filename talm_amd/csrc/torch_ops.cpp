@@ -1,0 +1,627 @@
+// `torch.ops.talm.*`: the PyTorch custom ops over the C-ABI of libtalm.so (include/talm.h).
+//
+// Each op checks device, dtype and layout of its tensors, then passes raw data pointers, sizes
+// and the current HIP stream of the tensors' device to one `extern "C"` entry point, and returns
+// nothing (outputs are the caller's tensors, marked as mutated in the schema). The ops are
+// registered for the CUDA (= HIP on ROCm) dispatch key only: CPU tensors raise
+// NotImplementedError from the dispatcher, never a CPU fallback. A rejected shape raises
+// ValueError, a failed launch RuntimeError (the message is talm_last_error()), as the reference's
+// launchers raise ValueError for unsupported shapes (solution/rmsnorm.py:113-114,
+// solution/qgroup.py:129-168).
+//
+// This layer is C++ so that a launch costs a few microseconds of host time: the QLoRA step
+// issues several hundred of these ops per optimizer step.
+//
+// `talm::gemm` is the one op here that is not a libtalm.so kernel: the plain fp16 projection
+// GEMMs of the layer group (solution/qgroup.py:346-355, cuBLAS in the reference) on hipBLASLt,
+// through PyTorch's own hipBLASLt handle and workspace, with the algorithm chosen once per shape
+// and kept (PyTorch's matmul asks hipBLASLt's heuristic on every call).
+#include <ATen/ATen.h>
+#include <ATen/hip/HIPContext.h>
+#include <hipblaslt/hipblaslt.h>
+#include <torch/library.h>
+
+#include <optional>
+#include <string>
+#include <unordered_map>
+
+#include "talm.h"
+
+namespace {
+
+using at::Tensor;
+using OptTensor = std::optional<Tensor>;
+
+void require(bool ok, const char* message) { TORCH_CHECK_VALUE(ok, message); }
+
+void require_fp16(const Tensor& t, const char* name) {
+  TORCH_CHECK_VALUE(t.is_cuda() && t.scalar_type() == at::kHalf, name,
+                    " must be a CUDA float16 tensor");
+}
+
+void* stream_of(const Tensor& t) {
+  return static_cast<void*>(at::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void* ptr(const Tensor& t) { return t.data_ptr(); }
+void* ptr(const OptTensor& t) { return t.has_value() ? t->data_ptr() : nullptr; }
+template <class T>
+T* as(const Tensor& t) { return static_cast<T*>(t.data_ptr()); }
+template <class T>
+T* as(const OptTensor& t) { return t.has_value() ? static_cast<T*>(t->data_ptr()) : nullptr; }
+
+void check(int status, const char* what) {
+  if (status == TALM_OK) return;
+  const char* m = talm_last_error();
+  const std::string message =
+      (m && *m) ? std::string(m) : std::string(what) + ": status " + std::to_string(status);
+  TORCH_CHECK_VALUE(status != TALM_EINVAL, message);
+  TORCH_CHECK(false, message);
+}
+
+int32_t dtype_code(at::ScalarType s) {
+  if (s == at::kFloat) return TALM_F32;
+  if (s == at::kHalf) return TALM_F16;
+  TORCH_CHECK_VALUE(false, "libtalm: unsupported dtype ", s);
+  return -1;
+}
+
+bool same_shape(const Tensor& t, int64_t rows, int64_t cols) {
+  return t.dim() == 2 && t.size(0) == rows && t.size(1) == cols;
+}
+
+// ------------------------------------------------------------------------------------------
+
+void nf4_group_dequant(const Tensor& packed, const Tensor& absmax8, const Tensor& code,
+                       const Tensor& absmax2, const Tensor& offset2, const Tensor& out,
+                       int64_t qblock, int64_t qblock2) {
+  require(packed.scalar_type() == at::kByte && absmax8.scalar_type() == at::kByte,
+          "packed/absmax8: uint8");
+  require(code.scalar_type() == at::kFloat && absmax2.scalar_type() == at::kFloat &&
+              offset2.scalar_type() == at::kFloat,
+          "code/absmax2/offset2: float32");
+  require_fp16(out, "out");
+  for (const Tensor* t : {&packed, &absmax8, &code, &absmax2, &offset2, &out})
+    require(t->is_contiguous() && t->device() == out.device(), "operands: contiguous, one device");
+  const int64_t n_rows = absmax8.numel();
+  require(code.numel() >= 256, "code: 256 entries");
+  require(packed.numel() * 2 == n_rows * qblock && out.numel() == n_rows * qblock,
+          "packed / out sizes do not match n_rows * qblock");
+  require(absmax2.numel() * qblock2 >= n_rows && offset2.numel() == absmax2.numel(),
+          "absmax2 / offset2 do not cover every block");
+  check(talm_nf4_group_dequant(as<uint8_t>(packed), as<uint8_t>(absmax8), as<float>(code),
+                               as<float>(absmax2), as<float>(offset2), as<uint16_t>(out), n_rows,
+                               static_cast<int32_t>(qblock), static_cast<int32_t>(qblock2),
+                               stream_of(out)),
+        "nf4_group_dequant");
+}
+
+void nf4_dequant(const Tensor& packed, const Tensor& absmax, const Tensor& out,
+                 int64_t blocksize) {
+  require(packed.scalar_type() == at::kByte && absmax.scalar_type() == at::kFloat,
+          "packed: uint8, absmax: float32");
+  require_fp16(out, "out");
+  require(packed.is_contiguous() && absmax.is_contiguous() && out.is_contiguous(),
+          "operands must be contiguous");
+  const int64_t n = out.numel();
+  require(packed.numel() * 2 >= n && absmax.numel() * blocksize >= n,
+          "packed / absmax do not cover out");
+  check(talm_nf4_dequant(as<uint8_t>(packed), as<float>(absmax), as<uint16_t>(out), n,
+                         static_cast<int32_t>(blocksize), stream_of(out)),
+        "nf4_dequant");
+}
+
+void rmsnorm(const Tensor& a, const OptTensor& q, const Tensor& h, const Tensor& xhat,
+             const OptTensor& p, const Tensor& weight, const Tensor& rstd, double eps,
+             int64_t backward) {
+  require(xhat.dim() == 2, "rmsnorm: [N, H] operands must be contiguous CUDA tensors of one shape");
+  const int64_t n_rows = xhat.size(0), n_cols = xhat.size(1);
+  const bool add = p.has_value();
+  require(!add || q.has_value(), "rmsnorm: p and q go together");
+  auto ok = [&](const Tensor& t) {
+    return t.is_cuda() && t.is_contiguous() && same_shape(t, n_rows, n_cols);
+  };
+  require(ok(a) && ok(h) && ok(xhat) && (!add || (ok(*p) && ok(*q))),
+          "rmsnorm: [N, H] operands must be contiguous CUDA tensors of one shape");
+  require(!add || a.scalar_type() == q->scalar_type(), "rmsnorm: q has a's dtype");
+  require(h.scalar_type() == xhat.scalar_type() && (!add || p->scalar_type() == h.scalar_type()),
+          "rmsnorm: h, xhat and p share the output dtype");
+  require(weight.is_contiguous() && weight.numel() == n_cols, "rmsnorm: weight [H]");
+  require(rstd.scalar_type() == at::kFloat && rstd.numel() == n_rows, "rmsnorm: rstd float32 [N]");
+  check(talm_rmsnorm(ptr(a), ptr(q), ptr(h), ptr(xhat), ptr(p), ptr(weight), as<float>(rstd),
+                     n_rows, n_cols, dtype_code(a.scalar_type()), dtype_code(h.scalar_type()),
+                     dtype_code(weight.scalar_type()), static_cast<float>(eps),
+                     backward ? 1 : 0, add ? 1 : 0, stream_of(xhat)),
+        "rmsnorm");
+}
+
+// q, out_q [T, Hq, D] and k, out_k [T, Hk, D] fp16 views (any token / head strides, unit column
+// stride); cos, sin float32 [T, D] with unit column stride. out_* may be q / k.
+void rope(const Tensor& q, const Tensor& k, const Tensor& cos, const Tensor& sin,
+          const Tensor& out_q, const Tensor& out_k, int64_t backward) {
+  require(q.dim() == 3 && k.dim() == 3, "rope: q/k must be [T, H, D] views with unit column stride");
+  const int64_t n_tokens = q.size(0), hq = q.size(1), dim = q.size(2), hk = k.size(1);
+  for (const auto& [t, heads] : {std::pair<const Tensor*, int64_t>{&q, hq}, {&k, hk},
+                                 {&out_q, hq}, {&out_k, hk}}) {
+    require_fp16(*t, "q/k");
+    require(t->dim() == 3 && t->size(0) == n_tokens && t->size(1) == heads &&
+                t->size(2) == dim && t->stride(2) == 1,
+            "rope: q/k must be [T, H, D] views with unit column stride");
+  }
+  for (const Tensor* t : {&cos, &sin})
+    require(t->is_cuda() && t->scalar_type() == at::kFloat && same_shape(*t, n_tokens, dim) &&
+                t->stride(1) == 1,
+            "rope: cos/sin float32 [T, D]");
+  require(cos.stride(0) == sin.stride(0), "rope: cos and sin share their token stride");
+  check(talm_rope(as<uint16_t>(q), as<uint16_t>(k), as<float>(cos), as<float>(sin),
+                  as<uint16_t>(out_q), as<uint16_t>(out_k), n_tokens, static_cast<int32_t>(hq),
+                  static_cast<int32_t>(hk), static_cast<int32_t>(dim), q.stride(0), q.stride(1),
+                  k.stride(0), k.stride(1), out_q.stride(0), out_q.stride(1), out_k.stride(0),
+                  out_k.stride(1), cos.stride(0), backward ? 1 : 0, stream_of(q)),
+        "rope");
+}
+
+void swiglu_fwd(const Tensor& gate, const Tensor& up, const Tensor& out) {
+  for (const Tensor* t : {&gate, &up, &out}) {
+    require_fp16(*t, "swiglu operand");
+    require(t->is_contiguous() && t->numel() == gate.numel(), "swiglu: contiguous, one size");
+  }
+  check(talm_swiglu_fwd(as<uint16_t>(gate), as<uint16_t>(up), as<uint16_t>(out), gate.numel(),
+                        stream_of(gate)),
+        "swiglu_fwd");
+}
+
+void swiglu_bwd(const Tensor& grad, const Tensor& gate, const Tensor& up, const Tensor& dgate,
+                const Tensor& dup) {
+  for (const Tensor* t : {&grad, &gate, &up, &dgate, &dup}) {
+    require_fp16(*t, "swiglu operand");
+    require(t->is_contiguous() && t->numel() == gate.numel(), "swiglu: contiguous, one size");
+  }
+  check(talm_swiglu_bwd(as<uint16_t>(grad), as<uint16_t>(gate), as<uint16_t>(up),
+                        as<uint16_t>(dgate), as<uint16_t>(dup), gate.numel(), stream_of(gate)),
+        "swiglu_bwd");
+}
+
+// weight fp16 [V, H] (unit column stride) -> weight_t fp16 [H, ldwt] (unit column stride,
+// ldwt >= V): the transpose, with columns [V, ldwt) zero.
+void head_weight_t(const Tensor& weight, const Tensor& weight_t) {
+  require_fp16(weight, "weight");
+  require_fp16(weight_t, "weight_t");
+  require(weight.dim() == 2 && weight_t.dim() == 2,
+          "head_weight_t: weight [V, H] and weight_t [H, >= V] with unit column stride");
+  const int64_t vocab = weight.size(0), size = weight.size(1);
+  require(weight.stride(1) == 1 && weight_t.stride(1) == 1 && weight_t.size(0) == size &&
+              weight_t.stride(0) >= vocab && weight_t.size(1) >= vocab,
+          "head_weight_t: weight [V, H] and weight_t [H, >= V] with unit column stride");
+  check(talm_head_weight_t(as<uint16_t>(weight), weight.stride(0), vocab, size,
+                           as<uint16_t>(weight_t), weight_t.stride(0), stream_of(weight)),
+        "head_weight_t");
+}
+
+// hidden fp16 [N, H] (unit column stride), weight fp16 [V, H] (unit column stride), weight_t its
+// head_weight_t transpose (needed with the gradient), targets int64 [N] with rows [0, n_grad)
+// exactly the labelled ones.
+void head_ce(const Tensor& hidden, const Tensor& weight, const OptTensor& weight_t,
+             const Tensor& targets, int64_t vchunk, int64_t n_grad, int64_t group,
+             const Tensor& token_loss, const Tensor& entropy, const Tensor& best_idx,
+             const Tensor& correct, const OptTensor& grad_hidden, const Tensor& workspace) {
+  require_fp16(hidden, "hidden");
+  require_fp16(weight, "weight");
+  require(hidden.dim() == 2 && weight.dim() == 2,
+          "head_ce: hidden [N, H] and weight [V, H] with unit column stride");
+  const int64_t n_rows = hidden.size(0), size = hidden.size(1), vocab = weight.size(0);
+  require(hidden.stride(1) == 1 && weight.stride(1) == 1 && weight.size(1) == size,
+          "head_ce: hidden [N, H] and weight [V, H] with unit column stride");
+  if (weight_t.has_value()) {
+    require_fp16(*weight_t, "weight_t");
+    require(weight_t->dim() == 2 && weight_t->stride(1) == 1 && weight_t->size(0) == size &&
+                weight_t->size(1) >= vocab,
+            "head_ce: weight_t [H, >= V], unit column stride");
+  }
+  require(targets.scalar_type() == at::kLong && targets.is_contiguous() &&
+              targets.numel() == n_rows,
+          "head_ce: targets int64 [N]");
+  for (const auto& [t, dt] : {std::pair<const Tensor*, at::ScalarType>{&token_loss, at::kFloat},
+                              {&entropy, at::kFloat}, {&best_idx, at::kInt}, {&correct, at::kInt}})
+    require(t->scalar_type() == dt && t->is_contiguous() && t->numel() == n_rows,
+            "head_ce: per-row outputs of N elements");
+  if (grad_hidden.has_value()) {
+    require_fp16(*grad_hidden, "grad_hidden");
+    require(grad_hidden->is_contiguous() && same_shape(*grad_hidden, n_rows, size),
+            "head_ce: grad_hidden contiguous [N, H]");
+  }
+  require(workspace.is_cuda() && workspace.is_contiguous(), "head_ce: workspace");
+  check(talm_head_ce(as<uint16_t>(hidden), hidden.stride(0), as<uint16_t>(weight),
+                     weight.stride(0), as<uint16_t>(weight_t),
+                     weight_t.has_value() ? weight_t->stride(0) : 0, as<int64_t>(targets),
+                     n_rows, size, vocab, vchunk, n_grad, static_cast<int32_t>(group),
+                     as<float>(token_loss), as<float>(entropy), as<int32_t>(best_idx),
+                     as<int32_t>(correct), as<uint16_t>(grad_hidden), workspace.data_ptr(),
+                     workspace.numel() * static_cast<int64_t>(workspace.element_size()),
+                     stream_of(hidden)),
+        "head_ce");
+}
+
+// Adapter g: t[:, 16g:16g+16] = x[:, xcol_g:xcol_g + k_g] A_g^T, ts = scaling_g * that;
+// x fp16 (unit column stride), A_g fp16 contiguous [16, k_g] (or [k_g, 16] with a_kmajor),
+// t / ts fp16 with one row stride.
+void lora_down(const Tensor& x, const Tensor& a0, const OptTensor& a1, int64_t k0, int64_t k1,
+               int64_t xcol0, int64_t xcol1, int64_t a_kmajor, double scaling0, double scaling1,
+               const Tensor& t, const Tensor& ts) {
+  require_fp16(x, "x");
+  require_fp16(a0, "a0");
+  require_fp16(t, "t");
+  require_fp16(ts, "ts");
+  require(x.dim() == 2 && t.dim() == 2 && ts.dim() == 2,
+          "lora_down: x [N, *], t/ts [N, 16 * adapters] with one row stride");
+  const int64_t n = x.size(0);
+  const int n_adapters = a1.has_value() ? 2 : 1;
+  for (int g = 0; g < n_adapters; ++g) {
+    const Tensor& a = g ? *a1 : a0;
+    const int64_t k = g ? k1 : k0, col = g ? xcol1 : xcol0;
+    require_fp16(a, "lora A");
+    const bool shape_ok = a.dim() == 2 && (a_kmajor ? (a.size(0) == k && a.size(1) == 16)
+                                                    : (a.size(0) == 16 && a.size(1) == k));
+    require(a.is_contiguous() && shape_ok && col + k <= x.size(1),
+            "lora_down: A [16, k] ([k, 16] k-major) inside x's columns");
+  }
+  require(x.stride(1) == 1 && t.stride(1) == 1 && ts.stride(1) == 1 && t.stride(0) == ts.stride(0) &&
+              t.size(0) == n && ts.size(0) == n && t.size(1) >= 16 * n_adapters &&
+              ts.size(1) >= 16 * n_adapters,
+          "lora_down: x [N, *], t/ts [N, 16 * adapters] with one row stride");
+  check(talm_lora_down(as<uint16_t>(x), x.stride(0), n, k0, k1, xcol0, xcol1, as<uint16_t>(a0),
+                       as<uint16_t>(a1), n_adapters, a_kmajor ? 1 : 0,
+                       static_cast<float>(scaling0), static_cast<float>(scaling1),
+                       as<uint16_t>(t), as<uint16_t>(ts), t.stride(0), stream_of(x)),
+        "lora_down");
+}
+
+void cos_sin_rows(const OptTensor& cos, const OptTensor& sin, int64_t n, const char* message) {
+  if (!cos.has_value()) return;
+  for (const OptTensor* v : {&cos, &sin})
+    require(v->has_value() && (*v)->is_cuda() && (*v)->scalar_type() == at::kFloat &&
+                (*v)->dim() == 2 && (*v)->stride(1) == 1 && (*v)->size(0) == n &&
+                (*v)->size(1) >= 128 && (*v)->stride(0) == cos->stride(0),
+            message);
+}
+
+// out [N, n_out] = x W^T + bias + the adapters' ts B^T on their columns, then the rotary
+// embedding (cos/sin fp32 [N, >= 128]) on the 128-column heads below rope_cols.
+void qkv_lora_fwd(const Tensor& x, const Tensor& weight, const OptTensor& bias,
+                  const OptTensor& ts, const OptTensor& b0, int64_t seg0_begin,
+                  int64_t seg0_end, const OptTensor& b1, int64_t seg1_begin, int64_t seg1_end,
+                  const OptTensor& cos, const OptTensor& sin, int64_t rope_cols,
+                  const Tensor& out) {
+  require_fp16(x, "x");
+  require_fp16(weight, "weight");
+  require_fp16(out, "out");
+  require(x.dim() == 2 && weight.dim() == 2,
+          "qkv_lora_fwd: x [N, H], weight [n_out, H], out [N, n_out], unit column strides");
+  const int64_t n = x.size(0), size = x.size(1), n_out = weight.size(0);
+  require(x.stride(1) == 1 && weight.stride(1) == 1 && out.dim() == 2 && out.stride(1) == 1 &&
+              weight.size(1) == size && same_shape(out, n, n_out),
+          "qkv_lora_fwd: x [N, H], weight [n_out, H], out [N, n_out], unit column strides");
+  if (bias.has_value()) {
+    require_fp16(*bias, "bias");
+    require(bias->is_contiguous() && bias->numel() == n_out, "qkv_lora_fwd: bias [n_out]");
+  }
+  int n_adapters = 0;
+  for (const OptTensor* b : {&b0, &b1}) {
+    if (!b->has_value()) continue;
+    ++n_adapters;
+    require_fp16(**b, "lora B");
+    require((*b)->is_contiguous() && (*b)->dim() == 2 && (*b)->size(1) == 16,
+            "qkv_lora_fwd: B [segment, 16]");
+  }
+  if (n_adapters) {
+    TORCH_CHECK_VALUE(ts.has_value(), "ts must be a CUDA float16 tensor");
+    require_fp16(*ts, "ts");
+    require(ts->dim() == 2 && ts->stride(1) == 1 && ts->size(0) == n &&
+                ts->size(1) >= 16 * n_adapters,
+            "qkv_lora_fwd: ts [N, 16 * adapters]");
+  }
+  cos_sin_rows(cos, sin, n, "qkv_lora_fwd: cos/sin fp32 [N, >= 128] with one row stride");
+  check(talm_qkv_lora_fwd(as<uint16_t>(x), x.stride(0), n, size, as<uint16_t>(weight),
+                          weight.stride(0), n_out, as<uint16_t>(bias), as<uint16_t>(ts),
+                          ts.has_value() ? ts->stride(0) : 0, n_adapters, as<uint16_t>(b0),
+                          seg0_begin, seg0_end, as<uint16_t>(b1), seg1_begin, seg1_end,
+                          as<float>(cos), as<float>(sin), cos.has_value() ? cos->stride(0) : 0,
+                          rope_cols, as<uint16_t>(out), out.stride(0), stream_of(x)),
+        "qkv_lora_fwd");
+}
+
+// dcat [N, q + k + v] = [rope_back(dq) | rope_back(dk) | dv] (cos/sin fp32 [N, >= 128], or None
+// for no rotation); every operand fp16 with unit column stride.
+void qkv_bwd_prep(const Tensor& dq, const Tensor& dk, const Tensor& dv, const OptTensor& cos,
+                  const OptTensor& sin, const Tensor& dcat) {
+  require(dcat.dim() == 2, "qkv_bwd_prep: dcat [N, columns] with unit column stride");
+  const int64_t n = dcat.size(0);
+  for (const auto& [v, name] : {std::pair<const Tensor*, const char*>{&dq, "dq"}, {&dk, "dk"},
+                                {&dv, "dv"}, {&dcat, "dcat"}}) {
+    require_fp16(*v, name);
+    TORCH_CHECK_VALUE(v->dim() == 2 && v->stride(1) == 1 && v->size(0) == n, "qkv_bwd_prep: ",
+                      name, " [N, columns] with unit column stride");
+  }
+  require(dcat.size(1) == dq.size(1) + dk.size(1) + dv.size(1),
+          "qkv_bwd_prep: dcat holds q, k and v");
+  cos_sin_rows(cos, sin, n, "qkv_bwd_prep: cos/sin fp32 [N, >= 128] with one row stride");
+  check(talm_qkv_bwd_prep(as<uint16_t>(dq), dq.stride(0), as<uint16_t>(dk), dk.stride(0),
+                          as<uint16_t>(dv), dv.stride(0), n, dq.size(1), dk.size(1), dv.size(1),
+                          as<float>(cos), as<float>(sin), cos.has_value() ? cos->stride(0) : 0,
+                          as<uint16_t>(dcat), dcat.stride(0), stream_of(dcat)),
+        "qkv_bwd_prep");
+}
+
+// dx [N, H] = dcat [N, n_out] W + u [N, r] A, from weight_t = W^T [H, >= n_out] and a_t = A^T
+// [H, r] (the adapters side by side); fp16, unit column strides.
+void qkv_lora_bwd_dx(const Tensor& dcat, const Tensor& weight_t, const OptTensor& u,
+                     const OptTensor& a_t, const Tensor& dx) {
+  for (const auto& [v, name] : {std::pair<const Tensor*, const char*>{&dcat, "dcat"},
+                                {&weight_t, "weight_t"}, {&dx, "dx"}}) {
+    require_fp16(*v, name);
+    TORCH_CHECK_VALUE(v->dim() == 2 && v->stride(1) == 1, "qkv_lora_bwd_dx: ", name,
+                      " unit column stride");
+  }
+  const int64_t n = dcat.size(0), n_out = dcat.size(1), size = weight_t.size(0);
+  require(weight_t.size(1) >= n_out && same_shape(dx, n, size),
+          "qkv_lora_bwd_dx: weight_t [H, >= n_out], dx [N, H]");
+  int64_t rank = 0;
+  if (u.has_value()) {
+    require_fp16(*u, "u");
+    TORCH_CHECK_VALUE(a_t.has_value(), "a_t must be a CUDA float16 tensor");
+    require_fp16(*a_t, "a_t");
+    require(u->dim() == 2 && a_t->dim() == 2, "qkv_lora_bwd_dx: u [N, r], a_t [H, r]");
+    rank = u->size(1);
+    require(u->stride(1) == 1 && a_t->stride(1) == 1 && u->size(0) == n &&
+                same_shape(*a_t, size, rank),
+            "qkv_lora_bwd_dx: u [N, r], a_t [H, r]");
+  }
+  check(talm_qkv_lora_bwd_dx(as<uint16_t>(dcat), dcat.stride(0), n, n_out,
+                             as<uint16_t>(weight_t), weight_t.stride(0), size, as<uint16_t>(u),
+                             u.has_value() ? u->stride(0) : 0, rank, as<uint16_t>(a_t),
+                             a_t.has_value() ? a_t->stride(0) : 0, as<uint16_t>(dx),
+                             dx.stride(0), stream_of(dcat)),
+        "qkv_lora_bwd_dx");
+}
+
+// fp32 dA_g [16, H] = u_g^T x, dB_g [seg_g, 16] = scaling_g dy[:, lo_g:lo_g+seg_g]^T t_g.
+void lora_wgrad(const Tensor& x, const Tensor& dy, const Tensor& u, const Tensor& t, int64_t lo0,
+                int64_t seg0, double scaling0, const Tensor& da0, const Tensor& db0, int64_t lo1,
+                int64_t seg1, double scaling1, const OptTensor& da1, const OptTensor& db1,
+                const Tensor& workspace) {
+  for (const auto& [v, name] : {std::pair<const Tensor*, const char*>{&x, "x"}, {&dy, "dy"},
+                                {&u, "u"}, {&t, "t"}}) {
+    require_fp16(*v, name);
+    TORCH_CHECK_VALUE(v->dim() == 2 && v->stride(1) == 1, "lora_wgrad: ", name,
+                      " unit column stride");
+  }
+  const int64_t n = x.size(0), size = x.size(1);
+  const bool two = da1.has_value();
+  TORCH_CHECK_VALUE(!two || db1.has_value(), "lora_wgrad: dB fp32 [segment, 16]");
+  for (int g = 0; g < (two ? 2 : 1); ++g) {
+    const Tensor& da = g ? *da1 : da0;
+    const Tensor& db = g ? *db1 : db0;
+    const int64_t seg = g ? seg1 : seg0;
+    require(da.is_cuda() && da.scalar_type() == at::kFloat && da.is_contiguous() &&
+                same_shape(da, 16, size),
+            "lora_wgrad: dA fp32 [16, H]");
+    require(db.is_cuda() && db.scalar_type() == at::kFloat && db.is_contiguous() &&
+                same_shape(db, seg, 16),
+            "lora_wgrad: dB fp32 [segment, 16]");
+  }
+  require(workspace.is_cuda() && workspace.is_contiguous(), "lora_wgrad: workspace");
+  if (n == 0) {  // no tokens: zero gradients, no launch
+    da0.zero_();
+    db0.zero_();
+    if (two) {
+      da1->zero_();
+      db1->zero_();
+    }
+    return;
+  }
+  check(talm_lora_wgrad(as<uint16_t>(x), x.stride(0), as<uint16_t>(dy), dy.stride(0),
+                        as<uint16_t>(u), u.stride(0), as<uint16_t>(t), t.stride(0), n, size,
+                        two ? 2 : 1, lo0, seg0, static_cast<float>(scaling0), as<float>(da0),
+                        as<float>(db0), lo1, seg1, static_cast<float>(scaling1), as<float>(da1),
+                        as<float>(db1), workspace.data_ptr(),
+                        workspace.numel() * static_cast<int64_t>(workspace.element_size()),
+                        stream_of(x)),
+        "lora_wgrad");
+}
+
+
+// ------------------------------------------------------------------------------------------
+// Plain fp16 GEMMs on hipBLASLt with cached plans.
+// ------------------------------------------------------------------------------------------
+struct GemmKey {
+  int device;
+  int64_t m, n, k, lda, ldb, ldd;
+  int trans_a, bias;
+  bool operator==(const GemmKey& o) const {
+    return device == o.device && m == o.m && n == o.n && k == o.k && lda == o.lda &&
+           ldb == o.ldb && ldd == o.ldd && trans_a == o.trans_a && bias == o.bias;
+  }
+};
+
+struct GemmKeyHash {
+  size_t operator()(const GemmKey& key) const {
+    size_t h = static_cast<size_t>(key.device);
+    for (int64_t v : {key.m, key.n, key.k, key.lda, key.ldb, key.ldd,
+                      static_cast<int64_t>(key.trans_a * 2 + key.bias)})
+      h = h * 1000003u ^ static_cast<size_t>(v);
+    return h;
+  }
+};
+
+struct GemmPlan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  size_t workspace = 0;
+};
+
+void lt_check(hipblasStatus_t status, const char* what) {
+  TORCH_CHECK(status == HIPBLAS_STATUS_SUCCESS, "gemm: hipBLASLt ", what, " failed (status ",
+              static_cast<int>(status), ")");
+}
+
+void destroy(GemmPlan& p) {
+  if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
+  if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
+  if (p.d) hipblasLtMatrixLayoutDestroy(p.d);
+  if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+  p = GemmPlan{};
+}
+
+// Plans per thread (forward launches come from the main thread, backward launches from the
+// autograd thread): a plan's bias pointer is set per call without a lock. Bounded: the token
+// count of a packed batch changes every step, so shapes keep arriving.
+struct PlanCache {
+  std::unordered_map<GemmKey, GemmPlan, GemmKeyHash> plans;
+  ~PlanCache() {
+    for (auto& kv : plans) destroy(kv.second);
+  }
+};
+thread_local PlanCache plan_cache;
+constexpr size_t kMaxPlans = 2048;
+
+// D [m, n] = op(A) [m, k] B [k, n] in hipBLASLt's column-major terms, fp16 in and out, fp32
+// accumulation; op(A) = A^T when trans_a (A stored k x m), else A (stored m x k); B stored k x n.
+const GemmPlan& plan_for(const GemmKey& key, hipblasLtHandle_t handle, size_t workspace_limit) {
+  auto it = plan_cache.plans.find(key);
+  if (it != plan_cache.plans.end()) return it->second;
+  if (plan_cache.plans.size() >= kMaxPlans) {
+    for (auto& kv : plan_cache.plans) destroy(kv.second);
+    plan_cache.plans.clear();
+  }
+  GemmPlan p;
+  try {
+    lt_check(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "descriptor");
+    const hipblasOperation_t op_a = key.trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+    const hipblasOperation_t op_b = HIPBLAS_OP_N;
+    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_a,
+                                             sizeof(op_a)), "transa");
+    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_b,
+                                             sizeof(op_b)), "transb");
+    if (key.bias) {
+      const hipblasLtEpilogue_t epilogue = HIPBLASLT_EPILOGUE_BIAS;
+      const hipDataType bias_type = HIP_R_16F;
+      lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epilogue,
+                                               sizeof(epilogue)), "epilogue");
+      lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE,
+                                               &bias_type, sizeof(bias_type)), "bias type");
+    }
+    lt_check(hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, key.trans_a ? key.k : key.m,
+                                         key.trans_a ? key.m : key.k, key.lda), "layout A");
+    lt_check(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, key.k, key.n, key.ldb), "layout B");
+    lt_check(hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16F, key.m, key.n, key.ldd), "layout D");
+    hipblasLtMatmulPreference_t pref = nullptr;
+    lt_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
+    const uint64_t limit = workspace_limit;
+    hipblasStatus_t st = hipblasLtMatmulPreferenceSetAttribute(
+        pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &limit, sizeof(limit));
+    hipblasLtMatmulHeuristicResult_t result{};
+    int found = 0;
+    if (st == HIPBLAS_STATUS_SUCCESS)
+      st = hipblasLtMatmulAlgoGetHeuristic(handle, p.desc, p.a, p.b, p.d, p.d, pref, 1, &result,
+                                           &found);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    lt_check(st, "heuristic");
+    TORCH_CHECK(found > 0, "gemm: hipBLASLt has no algorithm for m ", key.m, " n ", key.n, " k ",
+                key.k);
+    p.algo = result.algo;
+    p.workspace = result.workspaceSize;
+  } catch (...) {
+    destroy(p);
+    throw;
+  }
+  return plan_cache.plans.emplace(key, p).first->second;
+}
+
+// out [M, N] = a [M, K] b^T (+ bias [N]) with b [N, K] when b_t != 0, else a [M, K] b with
+// b [K, N]; fp16 operands with unit column stride, fp32 accumulation.
+void gemm(const Tensor& a, const Tensor& b, const OptTensor& bias, int64_t b_t,
+          const Tensor& out) {
+  require_fp16(a, "a");
+  require_fp16(b, "b");
+  require_fp16(out, "out");
+  require(a.dim() == 2 && b.dim() == 2 && out.dim() == 2 && a.stride(1) == 1 &&
+              b.stride(1) == 1 && out.stride(1) == 1,
+          "gemm: 2-D operands with unit column stride");
+  const int64_t m_rows = a.size(0), k = a.size(1), n_cols = out.size(1);
+  require(out.size(0) == m_rows && (b_t ? (b.size(0) == n_cols && b.size(1) == k)
+                                        : (b.size(0) == k && b.size(1) == n_cols)),
+          "gemm: a [M, K], b [N, K] (b_t) or [K, N], out [M, N]");
+  require(a.device() == b.device() && a.device() == out.device(), "gemm: one device");
+  if (bias.has_value()) {
+    require_fp16(*bias, "bias");
+    require(bias->is_contiguous() && bias->numel() == n_cols, "gemm: bias [N]");
+  }
+  require(k > 0, "gemm: empty reduction");
+  if (m_rows == 0 || n_cols == 0) return;
+  // column-major: out^T [N, M] = op(b) [N, K] a^T [K, M]
+  const GemmKey key{static_cast<int>(a.device().index()), n_cols, m_rows, k, b.stride(0),
+                    a.stride(0), out.stride(0), b_t ? 1 : 0, bias.has_value() ? 1 : 0};
+  hipblasLtHandle_t handle = at::cuda::getCurrentCUDABlasLtHandle();
+  void* workspace = at::cuda::getCUDABlasLtWorkspace();
+  const size_t workspace_size = at::cuda::getCUDABlasLtWorkspaceSize();
+  const GemmPlan& p = plan_for(key, handle, workspace_size);
+  if (bias.has_value()) {
+    const void* bias_ptr = bias->data_ptr();
+    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER,
+                                             &bias_ptr, sizeof(bias_ptr)), "bias");
+  }
+  const float alpha = 1.f, beta = 0.f;
+  lt_check(hipblasLtMatmul(handle, p.desc, &alpha, b.data_ptr(), p.a, a.data_ptr(), p.b, &beta,
+                           out.data_ptr(), p.d, out.data_ptr(), p.d, &p.algo, workspace,
+                           p.workspace, static_cast<hipStream_t>(stream_of(out))),
+           "matmul");
+}
+
+}  // namespace
+
+TORCH_LIBRARY(talm, m) {
+  m.def("nf4_group_dequant(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
+        "Tensor offset2, Tensor(a!) out, int qblock, int qblock2) -> ()");
+  m.def("nf4_dequant(Tensor packed, Tensor absmax, Tensor(a!) out, int blocksize) -> ()");
+  m.def("rmsnorm(Tensor(a!) a, Tensor(b!)? q, Tensor(c!) h, Tensor(d!) xhat, Tensor(e!)? p, "
+        "Tensor weight, Tensor(f!) rstd, float eps, int backward) -> ()");
+  m.def("rope(Tensor q, Tensor k, Tensor cos, Tensor sin, Tensor(a!) out_q, Tensor(b!) out_k, "
+        "int backward) -> ()");
+  m.def("swiglu_fwd(Tensor gate, Tensor up, Tensor(a!) out) -> ()");
+  m.def("swiglu_bwd(Tensor grad, Tensor gate, Tensor up, Tensor(a!) dgate, Tensor(b!) dup) -> ()");
+  m.def("head_weight_t(Tensor weight, Tensor(a!) weight_t) -> ()");
+  m.def("head_ce(Tensor hidden, Tensor weight, Tensor? weight_t, Tensor targets, int vchunk, "
+        "int n_grad, int group, Tensor(a!) token_loss, Tensor(b!) entropy, Tensor(c!) best_idx, "
+        "Tensor(d!) correct, Tensor(e!)? grad_hidden, Tensor(f!) workspace) -> ()");
+  m.def("lora_down(Tensor x, Tensor a0, Tensor? a1, int k0, int k1, int xcol0, int xcol1, "
+        "int a_kmajor, float scaling0, float scaling1, Tensor(a!) t, Tensor(b!) ts) -> ()");
+  m.def("qkv_lora_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? ts, Tensor? b0, "
+        "int seg0_begin, int seg0_end, Tensor? b1, int seg1_begin, int seg1_end, Tensor? cos, "
+        "Tensor? sin, int rope_cols, Tensor(a!) out) -> ()");
+  m.def("qkv_bwd_prep(Tensor dq, Tensor dk, Tensor dv, Tensor? cos, Tensor? sin, "
+        "Tensor(a!) dcat) -> ()");
+  m.def("qkv_lora_bwd_dx(Tensor dcat, Tensor weight_t, Tensor? u, Tensor? a_t, "
+        "Tensor(a!) dx) -> ()");
+  m.def("lora_wgrad(Tensor x, Tensor dy, Tensor u, Tensor t, int lo0, int seg0, float scaling0, "
+        "Tensor(a!) da0, Tensor(b!) db0, int lo1, int seg1, float scaling1, Tensor(c!)? da1, "
+        "Tensor(d!)? db1, Tensor(e!) workspace) -> ()");
+  m.def("gemm(Tensor a, Tensor b, Tensor? bias, int b_t, Tensor(a!) out) -> ()");
+}
+
+TORCH_LIBRARY_IMPL(talm, CUDA, m) {
+  m.impl("nf4_group_dequant", &nf4_group_dequant);
+  m.impl("nf4_dequant", &nf4_dequant);
+  m.impl("rmsnorm", &rmsnorm);
+  m.impl("rope", &rope);
+  m.impl("swiglu_fwd", &swiglu_fwd);
+  m.impl("swiglu_bwd", &swiglu_bwd);
+  m.impl("head_weight_t", &head_weight_t);
+  m.impl("head_ce", &head_ce);
+  m.impl("lora_down", &lora_down);
+  m.impl("qkv_lora_fwd", &qkv_lora_fwd);
+  m.impl("qkv_bwd_prep", &qkv_bwd_prep);
+  m.impl("qkv_lora_bwd_dx", &qkv_lora_bwd_dx);
+  m.impl("lora_wgrad", &lora_wgrad);
+  m.impl("gemm", &gemm);
+}

@@ -19,7 +19,6 @@ import os
 import weakref
 
 import torch
-import torch.nn.functional as F
 
 from . import _ops  # noqa: F401 - registers torch.ops.talm.*
 from .engaged import FELL_BACK, ON, RAN
@@ -231,19 +230,41 @@ class LayerGroup:
         return self._span_biases[key]
 
 
+def _rows(t):
+    """t [..., C] as a 2-D [R, C] view (a copy only when its columns are not unit-stride)."""
+    t2 = t.reshape(-1, t.shape[-1])
+    return t2 if t2.stride(-1) == 1 else t2.contiguous()
+
+
+def linear(x, weight, bias=None):
+    """x [..., K] W^T (+ b) for fp16 x and W [N, K]: torch.ops.talm.gemm (hipBLASLt)."""
+    x2 = _rows(x)
+    out = torch.empty(x2.shape[0], weight.shape[0], dtype=torch.float16, device=x.device)
+    torch.ops.talm.gemm(x2, weight, bias, 1, out)
+    return out.view(*x.shape[:-1], weight.shape[0])
+
+
+def matmul(dy, weight):
+    """dy [..., N] W for fp16 dy and W [N, K]: torch.ops.talm.gemm (hipBLASLt)."""
+    d2 = _rows(dy)
+    out = torch.empty(d2.shape[0], weight.shape[1], dtype=torch.float16, device=dy.device)
+    torch.ops.talm.gemm(d2, weight, None, 0, out)
+    return out.view(*dy.shape[:-1], weight.shape[1])
+
+
 class GroupLinear(torch.autograd.Function):
     """y = x W16^T + b on the layer group's dequantized weight; dx = dy W16 (solution/qgroup.py:
-    346-355)."""
+    346-355). Both GEMMs go to hipBLASLt through torch.ops.talm.gemm."""
 
     @staticmethod
     def forward(ctx, x, group, idx):
         ctx.group, ctx.idx = group, idx
-        return F.linear(x, group.weight("fwd", idx), group.biases[idx])
+        return linear(x, group.weight("fwd", idx), group.biases[idx])
 
     @staticmethod
     def backward(ctx, grad_out):
         weight = ctx.group.weight("bwd", ctx.idx)
-        return torch.matmul(grad_out.to(weight.dtype), weight), None, None
+        return matmul(grad_out.to(weight.dtype), weight), None, None
 
 
 _GROUPS = []

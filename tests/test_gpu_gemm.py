@@ -1,0 +1,72 @@
+"""torch.ops.talm.gemm: the layer group's plain fp16 GEMMs on hipBLASLt with cached plans
+(y = x W^T + b forward, dx = dy W backward; solution/qgroup.py:346-355), against an fp32 torch
+reference of the same product. fp16 output of an fp32-accumulated product: the tolerance is a
+few fp16 ulps of the output magnitude plus the accumulation-order term of K products."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(a, b, bias, b_t):
+    r = a.float() @ (b.float().t() if b_t else b.float())
+    return r + bias.float() if bias is not None else r
+
+
+def _close(out, ref, k):
+    tol = 4e-3 * ref.abs().amax().item() + 1e-3 * k ** 0.5 * 2 ** -10
+    err = (out.float() - ref).abs().max().item()
+    assert err <= tol, f"max error {err} > {tol}"
+
+
+@pytest.mark.parametrize("m,n,k,b_t,with_bias", [
+    (1167, 1536, 1536, 1, False),   # o_proj forward at a config-5 token count
+    (1167, 17920, 1536, 1, False),  # gate|up forward
+    (1167, 1536, 8960, 1, True),    # down forward, with a bias
+    (1167, 1536, 8960, 0, False),   # gate backward: dy [M, 8960] W [8960, 1536]
+    (1, 256, 64, 1, True),
+    (33, 40, 24, 0, False),
+])
+def test_gemm_matches_fp32_reference(m, n, k, b_t, with_bias):
+    import talm_amd._ops  # noqa: F401
+
+    g = torch.Generator("cpu").manual_seed(m * 7 + n + k)
+    a = torch.randn(m, k, generator=g).half().cuda()
+    b = (torch.randn(n, k, generator=g) * 0.05).half().cuda() if b_t else \
+        (torch.randn(k, n, generator=g) * 0.05).half().cuda()
+    bias = torch.randn(n, generator=g).half().cuda() if with_bias else None
+    out = torch.empty(m, n, dtype=torch.float16, device="cuda")
+    torch.ops.talm.gemm(a, b, bias, b_t, out)
+    torch.cuda.synchronize()
+    _close(out, _ref(a, b, bias, b_t), k)
+
+
+def test_gemm_strided_rows_and_plan_reuse():
+    """Row strides wider than the row (views of a wider buffer), and three calls in a row with
+    token counts that change, one repeated (the cached plan of an earlier shape is reused)."""
+    import talm_amd._ops  # noqa: F401
+
+    g = torch.Generator("cpu").manual_seed(5)
+    w = (torch.randn(384, 512, generator=g) * 0.05).half().cuda()
+    for m in (700, 1024, 700):
+        big = torch.randn(m, 640, generator=g).half().cuda()
+        a = big[:, 64:576]                       # [m, 512], row stride 640
+        out_big = torch.zeros(m, 400, dtype=torch.float16, device="cuda")
+        out = out_big[:, :384]                   # [m, 384], row stride 400
+        torch.ops.talm.gemm(a, w, None, 1, out)
+        torch.cuda.synchronize()
+        _close(out, _ref(a, w, None, 1), 512)
+        assert torch.all(out_big[:, 384:] == 0)  # nothing written past the view
+
+
+def test_gemm_rejects_bad_shapes():
+    import talm_amd._ops  # noqa: F401
+
+    a = torch.zeros(8, 16, dtype=torch.float16, device="cuda")
+    b = torch.zeros(4, 16, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        torch.ops.talm.gemm(a, b, None, 1, torch.empty(8, 5, dtype=torch.float16, device="cuda"))
+    with pytest.raises(ValueError):
+        torch.ops.talm.gemm(a.float(), b, None, 1,
+                            torch.empty(8, 4, dtype=torch.float16, device="cuda"))
