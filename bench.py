@@ -339,7 +339,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every box of this build has a single MI355X and "
-              "the kernel set runs unsharded (see DESIGN.md for how it would shard).",
+              "the kernel set runs unsharded (its multi-GPU sharding is a design, not code).",
               file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
