@@ -235,6 +235,46 @@ int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t 
                     int64_t seg1, float scaling1, float* da1, float* db1, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/*
+ * Variable-length causal attention with grouped KV heads, forward. Sequence s holds the packed
+ * rows [cu_seqlens[s], cu_seqlens[s+1]) (int32, device); row i attends to keys j <= i of its own
+ * sequence; query head h reads KV head h / (n_q_heads / n_kv_heads). q f16 [n_tokens, n_q_heads,
+ * head_dim], k / v f16 [n_tokens, n_kv_heads, head_dim] at element strides (token, head), unit
+ * column stride; out likewise [n_tokens, n_q_heads, head_dim]; lse f32 [n_q_heads, n_tokens] =
+ * log sum_j exp(scale q.k_j) per row. head_dim 128; strides multiples of 8; max_seqlen >= the
+ * longest sequence. Replaces the reference's per-KV-head memory-efficient attention launches
+ * (solution/unpad.py:199-294) with per-row causal SDPA semantics (solution/unpad.py:121-134).
+ */
+int talm_attn_fwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                  const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                  const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                  const int32_t* cu_seqlens, int32_t n_seqs, int32_t max_seqlen,
+                  int64_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                  float scale, uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                  float* lse, void* stream);
+
+/*
+ * Its backward: dq f16 [n_tokens, n_q_heads, head_dim], dk / dv f16 [n_tokens, n_kv_heads,
+ * head_dim] (any strides as above) from q, k, v, the forward's out and lse, and dout. dk / dv of
+ * a KV head sum its query heads' contributions in head order (deterministic). `workspace`
+ * (256-byte aligned) holds talm_attn_bwd_workspace(n_tokens, n_q_heads) bytes: rowsum(dout *
+ * out) and fp32 dk / dv partials per query head. Replaces the backward of the same launches
+ * (solution/unpad.py:199-294).
+ */
+int64_t talm_attn_bwd_workspace(int64_t n_tokens, int32_t n_q_heads);
+int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                  const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                  const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                  const uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                  const uint16_t* dout, int64_t do_stride_tok, int64_t do_stride_head,
+                  const float* lse, const int32_t* cu_seqlens, int32_t n_seqs,
+                  int32_t max_seqlen, int64_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads,
+                  int32_t head_dim, float scale, uint16_t* dq, int64_t dq_stride_tok,
+                  int64_t dq_stride_head, uint16_t* dk, int64_t dk_stride_tok,
+                  int64_t dk_stride_head, uint16_t* dv, int64_t dv_stride_tok,
+                  int64_t dv_stride_head, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

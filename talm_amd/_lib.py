@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -43,12 +43,18 @@ SIGNATURES = {
                           _P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P],
     "talm_head_ce": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P,
                      _P, _P, _P, _P, _I64, _P],
+    "talm_attn_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I32, _I32, _I64, _I32,
+                      _I32, _I32, _F32, _P, _I64, _I64, _P, _P],
+    "talm_attn_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
+                      _I64, _P, _P, _I32, _I32, _I64, _I32, _I32, _I32, _F32, _P, _I64, _I64, _P,
+                      _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
 }
 
 # Entry points that return a size instead of a status.
 SIZE_FUNCTIONS = {
     "talm_head_ce_workspace": [_I64, _I64, _I64, _I64, _I64, _I32],
     "talm_lora_wgrad_workspace": [_I64, _I64, _I64, _I64],
+    "talm_attn_bwd_workspace": [_I64, _I32],
 }
 
 _lock = threading.Lock()

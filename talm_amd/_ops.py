@@ -20,7 +20,7 @@ from . import _lib
 OPS_PATH = Path(__file__).resolve().parent / "libtalm_torch.so"
 OPS = ("nf4_group_dequant", "nf4_dequant", "rmsnorm", "rope", "swiglu_fwd", "swiglu_bwd",
        "head_weight_t", "head_ce", "lora_down", "qkv_lora_fwd", "qkv_bwd_prep", "qkv_lora_bwd_dx",
-       "lora_wgrad", "gemm")
+       "lora_wgrad", "gemm", "attn_fwd", "attn_bwd")
 
 _load_lock = threading.Lock()
 _loaded = False
@@ -63,4 +63,10 @@ def head_ce_workspace_bytes(n_rows, hidden, vocab, vchunk, n_grad, group):
 def lora_wgrad_workspace_bytes(n_tokens, hidden, seg0, seg1):
     size = _lib.lib().talm_lora_wgrad_workspace(n_tokens, hidden, seg0, seg1)
     _require(size >= 0, "lora_wgrad: unsupported shape")
+    return int(size)
+
+
+def attn_bwd_workspace_bytes(n_tokens, n_q_heads):
+    size = _lib.lib().talm_attn_bwd_workspace(n_tokens, n_q_heads)
+    _require(size >= 0, "attn_bwd: unsupported shape")
     return int(size)

@@ -1,0 +1,721 @@
+// Variable-length causal attention with grouped KV heads (GQA), forward and backward, on gfx950
+// fp16 MFMA with fp32 softmax statistics.
+//
+// Packed tokens: sequence s holds rows [cu[s], cu[s+1]); row i of a sequence attends to keys
+// j <= i of the same sequence. q [N, Hq, D], k / v [N, Hkv, D] (any token / head strides, unit
+// column stride), query head h reads KV head h / (Hq / Hkv); D = 128. This replaces the
+// reference's per-KV-head memory-efficient attention launches (solution/unpad.py:199-294), whose
+// semantics are per-row causal SDPA (solution/unpad.py:121-134).
+//
+// The forward is a flash-attention pass per (sequence, query head, 128-row query tile): four
+// wavefronts of 32 query rows, key tiles of 64 through a double-buffered LDS ring. Scores are
+// computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16), so each lane owns one query row
+// (its accumulator column): the online max / sum and the output rescale are per-lane scalars.
+// The exponentiated scores are already in the B-operand layout of O^T = V^T P^T: the reduction
+// over keys takes the accumulator's key order as its k-slot order, and V^T is read in that same
+// order from a transposed LDS copy of the V tile. The row statistics are kept in base 2
+// (scores times scale * log2 e); lse is written in natural-log units, [Hq, N].
+//
+// The backward (FlashAttention-2's recurrences: P = exp(S - lse), dV = P^T dO, dP = dO V^T,
+// dS = P (dP - rowsum(dO O)), dQ = scale dS K, dK = scale dS^T Q) runs as
+//   attn_bwd_dot    Dd[h][t] = sum_d dO O (fp32);
+//   attn_bwd_dq     per (sequence, query head, 128-row query tile): the forward's loop with
+//                   dP^T = V dO^T next to S^T, and dQ^T += K^T dS^T from a transposed K tile;
+//   attn_bwd_dkdv   per (sequence, query head, 128-key tile): each lane owns a key (S and dP
+//                   computed untransposed, so keys are accumulator columns), looping over
+//                   32-row query tiles: dV^T += dO^T P and dK^T += Q^T dS from transposed
+//                   Q / dO tiles; fp32 partials per query head;
+//   attn_bwd_reduce the partials of a KV head's query heads summed in head order (deterministic)
+//                   into dK, dV fp16.
+#include "mfma_tile.h"
+
+namespace talm {
+namespace {
+
+typedef uint16_t half4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;         // head dim
+constexpr int kKeys = 64;       // keys per tile
+constexpr int kKS = kD + 8;     // row stride (halfs) of a [keys][D] tile in LDS
+constexpr int kVS = kKeys + 4;  // row stride (halfs) of a transposed [D][keys] tile in LDS
+constexpr float kLn2 = 0.693147180559945309f;
+
+__device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+
+struct FwdArgs {
+  const uint16_t* q;
+  int64_t q_tok, q_head;
+  const uint16_t* k;
+  int64_t k_tok, k_head;
+  const uint16_t* v;
+  int64_t v_tok, v_head;
+  const int32_t* cu;
+  int group;          // query heads per KV head
+  int n_tiles;        // query tiles per sequence (of the longest)
+  float scale_log2;   // softmax scale * log2(e)
+  uint16_t* out;
+  int64_t o_tok, o_head;
+  float* lse;         // [Hq, n_tokens]
+  int64_t n_tokens;
+};
+
+template <int W>
+__global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
+  constexpr int kRows = 32 * W;                 // query rows per workgroup
+  constexpr int kChunks = kKeys * (kD / 8);     // 16-byte chunks of a K (or V) tile
+  constexpr int kPer = kChunks / (64 * W);      // chunks per thread
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeys * kKS];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][kD * kVS];
+
+  const int seq = blockIdx.z, head = blockIdx.y;
+  const int tile = a.n_tiles - 1 - static_cast<int>(blockIdx.x);  // longest tiles first
+  const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
+  const int q0 = tile * kRows;
+  if (q0 >= len) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int kvh = head / a.group;
+
+  // this lane's query row and its Q fragments (k-slots d = 16 s + 8 hh .. + 8)
+  const int qrow = q0 + 32 * wave + l32;
+  const int qr = min(qrow, len - 1);
+  half8_t qf[kD / 16];
+  {
+    const uint16_t* qp = a.q + static_cast<int64_t>(s0 + qr) * a.q_tok + head * a.q_head + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < kD / 16; ++s) qf[s] = *reinterpret_cast<const half8_t*>(qp + 16 * s);
+  }
+
+  const int kend = min(len, q0 + kRows);  // keys any row of this tile can see
+  const int n_kt = (kend + kKeys - 1) / kKeys;
+  const uint16_t* kbase = a.k + static_cast<int64_t>(s0) * a.k_tok + kvh * a.k_head;
+  const uint16_t* vbase = a.v + static_cast<int64_t>(s0) * a.v_tok + kvh * a.v_head;
+
+  // tile loads: chunk c = p * 64W + tid -> key c % 64, column chunk c / 64 (for V: 64 lanes
+  // of a wavefront read 64 keys of one 8-column chunk, so the transposed LDS writes of one
+  // instruction fill one row of vt)
+  uint4 kreg[kPer], vreg[kPer];
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int c = p * 64 * W + tid, key = min(kt * kKeys + (c & 63), len - 1), cc = c >> 6;
+      kreg[p] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
+      vreg[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int c = p * 64 * W + tid, key = c & 63, cc = c >> 6;
+      *reinterpret_cast<uint4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[p];
+      const uint32_t w4[4] = {vreg[p].x, vreg[p].y, vreg[p].z, vreg[p].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[buf][(8 * cc + 2 * e) * kVS + key] = static_cast<uint16_t>(w4[e] & 0xffffu);
+        vt[buf][(8 * cc + 2 * e + 1) * kVS + key] = static_cast<uint16_t>(w4[e] >> 16);
+      }
+    }
+  };
+
+  f32x16 o[kD / 32];
+#pragma unroll
+  for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[j][v] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+
+  load_tile(0);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int buf = kt & 1;
+    store_tile(buf);
+    if (kt + 1 < n_kt) load_tile(kt + 1);
+    __syncthreads();
+    const int k0 = kt * kKeys;
+    // S^T for keys k0 + 32 b + (8 (v / 4) + 4 hh + v % 4), this lane's query column
+    f32x16 st[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) st[b][v] = 0.f;
+      const uint16_t* kr = &ks[buf][(32 * b + l32) * kKS + 8 * hh];
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s)
+        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            *reinterpret_cast<const half8_t*>(kr + 16 * s), qf[s], st[b], 0, 0, 0);
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + 32 * b + 8 * (v >> 2) + 4 * hh + (v & 3);
+        const float t = (key <= qrow && key < len) ? st[b][v] * a.scale_log2 : -INFINITY;
+        st[b][v] = t;
+        mt = fmaxf(mt, t);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float m_new = fmaxf(m, mt);
+    const float alpha = m == -INFINITY ? 0.f : exp2_(m - m_new);
+    m = m_new;
+    float ps = 0.f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = exp2_(st[b][v] - m_new);
+        st[b][v] = p;
+        ps += p;
+      }
+    lsum = lsum * alpha + ps;
+#pragma unroll
+    for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[j][v] *= alpha;
+    // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per step in the accumulator's key order
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half8_t pb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(st[b][8 * h + e]);
+        const int kb = 32 * b + 16 * h + 4 * hh;
+#pragma unroll
+        for (int j = 0; j < kD / 32; ++j) {
+          const uint16_t* vr = &vt[buf][(32 * j + l32) * kVS + kb];
+          const half4_t lo = *reinterpret_cast<const half4_t*>(vr);
+          const half4_t hi = *reinterpret_cast<const half4_t*>(vr + 8);
+          const half8_t va = __builtin_bit_cast(
+              half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[j], 0, 0, 0);
+        }
+      }
+  }
+
+  // O = O^T / l through LDS: each wavefront stages its 32 rows x D, then 16-byte row stores
+  const float l_tot = lsum + __shfl_xor(lsum, 32, kWave);
+  const float inv = 1.f / l_tot;
+  __syncthreads();  // every wavefront is done with the tiles
+  uint16_t* os = &ks[0][0] + wave * 32 * kKS;
+#pragma unroll
+  for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * j + 8 * g + 4 * hh;
+      uint2 w;
+      w.x = pack2(o[j][4 * g] * inv, o[j][4 * g + 1] * inv);
+      w.y = pack2(o[j][4 * g + 2] * inv, o[j][4 * g + 3] * inv);
+      *reinterpret_cast<uint2*>(&os[l32 * kKS + d0]) = w;
+    }
+  if (hh == 0 && qrow < len)
+    a.lse[static_cast<int64_t>(head) * a.n_tokens + s0 + qrow] = (m + __log2f(l_tot)) * kLn2;
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < (32 * kD / 8) / 64; ++it) {
+    const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
+    const int row = q0 + 32 * wave + r;
+    if (row < len)
+      *reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(s0 + row) * a.o_tok + head * a.o_head + 8 * cc) =
+          *reinterpret_cast<const uint4*>(&os[r * kKS + 8 * cc]);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward
+// ------------------------------------------------------------------------------------------
+struct BwdArgs {
+  const uint16_t* q;
+  int64_t q_tok, q_head;
+  const uint16_t* k;
+  int64_t k_tok, k_head;
+  const uint16_t* v;
+  int64_t v_tok, v_head;
+  const uint16_t* o;
+  int64_t o_tok, o_head;
+  const uint16_t* dout;
+  int64_t do_tok, do_head;
+  const float* lse;    // [Hq, n_tokens], natural log
+  const int32_t* cu;
+  int group, n_q_heads, n_kv_heads;
+  int n_tiles;         // tiles per sequence (of the longest)
+  float scale, scale_log2;
+  int64_t n_tokens;
+  float* dd;           // [Hq, n_tokens]: rowsum(dO * O)
+  float* dk_part;      // [Hq, n_tokens, D] fp32
+  float* dv_part;      // [Hq, n_tokens, D] fp32
+  uint16_t* dq;
+  int64_t dq_tok, dq_head;
+  uint16_t* dk;
+  int64_t dk_tok, dk_head;
+  uint16_t* dv;
+  int64_t dv_tok, dv_head;
+};
+
+// Dd[h][t] = sum_d dO[t][h][d] * O[t][h][d]: 16 lanes per (token, head), 8 columns each.
+__global__ __launch_bounds__(256) void attn_bwd_dot_kernel(BwdArgs a) {
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;  // t * Hq + h
+  const int sub = threadIdx.x & 15;
+  const int64_t rows = a.n_tokens * a.n_q_heads;
+  const int64_t r = row < rows ? row : rows - 1;
+  const int64_t t = r / a.n_q_heads;
+  const int h = static_cast<int>(r % a.n_q_heads);
+  const uint4 x = *reinterpret_cast<const uint4*>(a.o + t * a.o_tok + h * a.o_head + 8 * sub);
+  const uint4 y = *reinterpret_cast<const uint4*>(a.dout + t * a.do_tok + h * a.do_head + 8 * sub);
+  float acc = lo_f(x.x) * lo_f(y.x) + hi_f(x.x) * hi_f(y.x) + lo_f(x.y) * lo_f(y.y) +
+              hi_f(x.y) * hi_f(y.y) + lo_f(x.z) * lo_f(y.z) + hi_f(x.z) * hi_f(y.z) +
+              lo_f(x.w) * lo_f(y.w) + hi_f(x.w) * hi_f(y.w);
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+  if (sub == 0 && row < rows) a.dd[static_cast<int64_t>(h) * a.n_tokens + t] = acc;
+}
+
+// dQ: the forward's structure, one query row per lane.
+template <int W>
+__global__ __launch_bounds__(64 * W, 1) void attn_bwd_dq_kernel(BwdArgs a) {
+  constexpr int kRows = 32 * W;
+  constexpr int kPer = kKeys * (kD / 8) / (64 * W);
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeys * kKS];   // K [key][d]
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kKeys * kKS];   // V [key][d]
+  __shared__ __attribute__((aligned(16))) uint16_t kts[2][kD * kVS];     // K^T [d][key]
+
+  const int seq = blockIdx.z, head = blockIdx.y;
+  const int tile = a.n_tiles - 1 - static_cast<int>(blockIdx.x);
+  const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
+  const int q0 = tile * kRows;
+  if (q0 >= len) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int kvh = head / a.group;
+  const int qrow = q0 + 32 * wave + l32;
+  const int qr = min(qrow, len - 1);
+  half8_t qf[kD / 16], df[kD / 16];
+  {
+    const uint16_t* qp = a.q + static_cast<int64_t>(s0 + qr) * a.q_tok + head * a.q_head + 8 * hh;
+    const uint16_t* dp = a.dout + static_cast<int64_t>(s0 + qr) * a.do_tok + head * a.do_head + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < kD / 16; ++s) {
+      qf[s] = *reinterpret_cast<const half8_t*>(qp + 16 * s);
+      df[s] = *reinterpret_cast<const half8_t*>(dp + 16 * s);
+    }
+  }
+  const float lse2 = a.lse[static_cast<int64_t>(head) * a.n_tokens + s0 + qr] * 1.44269504088896341f;
+  const float ddr = a.dd[static_cast<int64_t>(head) * a.n_tokens + s0 + qr];
+
+  const int kend = min(len, q0 + kRows);
+  const int n_kt = (kend + kKeys - 1) / kKeys;
+  const uint16_t* kbase = a.k + static_cast<int64_t>(s0) * a.k_tok + kvh * a.k_head;
+  const uint16_t* vbase = a.v + static_cast<int64_t>(s0) * a.v_tok + kvh * a.v_head;
+  uint4 kreg[kPer], vreg[kPer];
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int c = p * 64 * W + tid, key = min(kt * kKeys + (c & 63), len - 1), cc = c >> 6;
+      kreg[p] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
+      vreg[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int c = p * 64 * W + tid, key = c & 63, cc = c >> 6;
+      *reinterpret_cast<uint4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[p];
+      *reinterpret_cast<uint4*>(&vs[buf][key * kKS + 8 * cc]) = vreg[p];
+      const uint32_t w4[4] = {kreg[p].x, kreg[p].y, kreg[p].z, kreg[p].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kts[buf][(8 * cc + 2 * e) * kVS + key] = static_cast<uint16_t>(w4[e] & 0xffffu);
+        kts[buf][(8 * cc + 2 * e + 1) * kVS + key] = static_cast<uint16_t>(w4[e] >> 16);
+      }
+    }
+  };
+
+  f32x16 acc[kD / 32];
+#pragma unroll
+  for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
+
+  load_tile(0);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int buf = kt & 1;
+    store_tile(buf);
+    if (kt + 1 < n_kt) load_tile(kt + 1);
+    __syncthreads();
+    const int k0 = kt * kKeys;
+    f32x16 st[2], dpt[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) st[b][v] = dpt[b][v] = 0.f;
+      const uint16_t* kr = &ks[buf][(32 * b + l32) * kKS + 8 * hh];
+      const uint16_t* vr = &vs[buf][(32 * b + l32) * kKS + 8 * hh];
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s) {
+        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            *reinterpret_cast<const half8_t*>(kr + 16 * s), qf[s], st[b], 0, 0, 0);
+        dpt[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            *reinterpret_cast<const half8_t*>(vr + 16 * s), df[s], dpt[b], 0, 0, 0);
+      }
+    }
+    // dS^T = P^T (dP^T - Dd), P^T = exp2(S^T scale log2e - lse2), 0 where masked
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + 32 * b + 8 * (v >> 2) + 4 * hh + (v & 3);
+        const float p = (key <= qrow && key < len) ? exp2_(st[b][v] * a.scale_log2 - lse2) : 0.f;
+        st[b][v] = p * (dpt[b][v] - ddr);
+      }
+    // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        half8_t sb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sb[e] = static_cast<_Float16>(st[b][8 * h + e]);
+        const int kb = 32 * b + 16 * h + 4 * hh;
+#pragma unroll
+        for (int j = 0; j < kD / 32; ++j) {
+          const uint16_t* kr = &kts[buf][(32 * j + l32) * kVS + kb];
+          const half4_t lo = *reinterpret_cast<const half4_t*>(kr);
+          const half4_t hi = *reinterpret_cast<const half4_t*>(kr + 8);
+          const half8_t ka = __builtin_bit_cast(
+              half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, sb, acc[j], 0, 0, 0);
+        }
+      }
+  }
+
+  __syncthreads();
+  uint16_t* os = &ks[0][0] + wave * 32 * kKS;
+#pragma unroll
+  for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * j + 8 * g + 4 * hh;
+      uint2 w;
+      w.x = pack2(acc[j][4 * g] * a.scale, acc[j][4 * g + 1] * a.scale);
+      w.y = pack2(acc[j][4 * g + 2] * a.scale, acc[j][4 * g + 3] * a.scale);
+      *reinterpret_cast<uint2*>(&os[l32 * kKS + d0]) = w;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < (32 * kD / 8) / 64; ++it) {
+    const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
+    const int row = q0 + 32 * wave + r;
+    if (row < len)
+      *reinterpret_cast<uint4*>(a.dq + static_cast<int64_t>(s0 + row) * a.dq_tok + head * a.dq_head + 8 * cc) =
+          *reinterpret_cast<const uint4*>(&os[r * kKS + 8 * cc]);
+  }
+}
+
+// dK / dV partials of one query head: each lane owns one key of the workgroup's 32W keys.
+constexpr int kQT = 32;           // query rows per step of the dK / dV loop
+constexpr int kQS = kQT + 4;      // row stride (halfs) of a transposed [D][queries] tile
+
+template <int W>
+__global__ __launch_bounds__(64 * W, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
+  constexpr int kCols = 32 * W;                       // keys per workgroup
+  constexpr int kPer = kQT * (kD / 8) / (64 * W);     // 16-byte chunks of a Q / dO tile per thread
+  __shared__ __attribute__((aligned(16))) uint16_t qs[2][kQT * kKS];     // Q [q][d]
+  __shared__ __attribute__((aligned(16))) uint16_t ds[2][kQT * kKS];     // dO [q][d]
+  __shared__ __attribute__((aligned(16))) uint16_t qts[2][kD * kQS];     // Q^T [d][q]
+  __shared__ __attribute__((aligned(16))) uint16_t dts[2][kD * kQS];     // dO^T [d][q]
+  __shared__ __attribute__((aligned(16))) float ls[2][kQT];              // lse2 of the rows
+  __shared__ __attribute__((aligned(16))) float dds[2][kQT];             // Dd of the rows
+
+  const int seq = blockIdx.z, head = blockIdx.y;
+  const int tile = a.n_tiles - 1 - static_cast<int>(blockIdx.x);
+  const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
+  const int k0 = tile * kCols;
+  if (k0 >= len) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hh = lane >> 5, l32 = lane & 31;
+  const int kvh = head / a.group;
+  const int key = k0 + 32 * wave + l32;
+  const int kr_ = min(key, len - 1);
+  half8_t kf[kD / 16], vf[kD / 16];
+  {
+    const uint16_t* kp = a.k + static_cast<int64_t>(s0 + kr_) * a.k_tok + kvh * a.k_head + 8 * hh;
+    const uint16_t* vp = a.v + static_cast<int64_t>(s0 + kr_) * a.v_tok + kvh * a.v_head + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < kD / 16; ++s) {
+      kf[s] = *reinterpret_cast<const half8_t*>(kp + 16 * s);
+      vf[s] = *reinterpret_cast<const half8_t*>(vp + 16 * s);
+    }
+  }
+  const int qstart = (k0 / kQT) * kQT;                 // causal: rows below k0 see no key here
+  const int n_qt = (len - qstart + kQT - 1) / kQT;
+  const uint16_t* qbase = a.q + static_cast<int64_t>(s0) * a.q_tok + head * a.q_head;
+  const uint16_t* dbase = a.dout + static_cast<int64_t>(s0) * a.do_tok + head * a.do_head;
+  const float* lrow = a.lse + static_cast<int64_t>(head) * a.n_tokens + s0;
+  const float* drow = a.dd + static_cast<int64_t>(head) * a.n_tokens + s0;
+  // chunk c = p * 64W + tid -> query row c % 32, column chunk c / 32
+  uint4 qreg[kPer], dreg[kPer];
+  float lreg = 0.f, dreg1 = 0.f;
+  auto load_tile = [&](int qt) {
+    const int r0 = qstart + qt * kQT;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int c = p * 64 * W + tid, row = min(r0 + (c & 31), len - 1), cc = c >> 5;
+      qreg[p] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(row) * a.q_tok + 8 * cc);
+      dreg[p] = *reinterpret_cast<const uint4*>(dbase + static_cast<int64_t>(row) * a.do_tok + 8 * cc);
+    }
+    if (tid < kQT) {
+      const int row = min(r0 + tid, len - 1);
+      lreg = lrow[row] * 1.44269504088896341f;
+      dreg1 = drow[row];
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int c = p * 64 * W + tid, row = c & 31, cc = c >> 5;
+      *reinterpret_cast<uint4*>(&qs[buf][row * kKS + 8 * cc]) = qreg[p];
+      *reinterpret_cast<uint4*>(&ds[buf][row * kKS + 8 * cc]) = dreg[p];
+      const uint32_t q4[4] = {qreg[p].x, qreg[p].y, qreg[p].z, qreg[p].w};
+      const uint32_t d4[4] = {dreg[p].x, dreg[p].y, dreg[p].z, dreg[p].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qts[buf][(8 * cc + 2 * e) * kQS + row] = static_cast<uint16_t>(q4[e] & 0xffffu);
+        qts[buf][(8 * cc + 2 * e + 1) * kQS + row] = static_cast<uint16_t>(q4[e] >> 16);
+        dts[buf][(8 * cc + 2 * e) * kQS + row] = static_cast<uint16_t>(d4[e] & 0xffffu);
+        dts[buf][(8 * cc + 2 * e + 1) * kQS + row] = static_cast<uint16_t>(d4[e] >> 16);
+      }
+    }
+    if (tid < kQT) {
+      ls[buf][tid] = lreg;
+      dds[buf][tid] = dreg1;
+    }
+  };
+
+  f32x16 dka[kD / 32], dva[kD / 32];
+#pragma unroll
+  for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) dka[j][v] = dva[j][v] = 0.f;
+
+  load_tile(0);
+  for (int qt = 0; qt < n_qt; ++qt) {
+    const int buf = qt & 1;
+    store_tile(buf);
+    if (qt + 1 < n_qt) load_tile(qt + 1);
+    __syncthreads();
+    const int r0 = qstart + qt * kQT;
+    // S[q][key], dP[q][key]: rows q = 8 (v / 4) + 4 hh + v % 4 of the tile, column = this key
+    f32x16 sc, dp;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sc[v] = dp[v] = 0.f;
+    {
+      const uint16_t* qr = &qs[buf][l32 * kKS + 8 * hh];
+      const uint16_t* dr = &ds[buf][l32 * kKS + 8 * hh];
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s) {
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            *reinterpret_cast<const half8_t*>(qr + 16 * s), kf[s], sc, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            *reinterpret_cast<const half8_t*>(dr + 16 * s), vf[s], dp, 0, 0, 0);
+      }
+    }
+    // P and dS, 0 where masked (query row < key or past the sequence, key past the sequence)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int rb = 8 * g + 4 * hh;
+      const float4 l4 = *reinterpret_cast<const float4*>(&ls[buf][rb]);
+      const float4 d4 = *reinterpret_cast<const float4*>(&dds[buf][rb]);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = 4 * g + e, q = r0 + rb + e;
+        const bool valid = q >= key && q < len && key < len;
+        const float p = valid ? exp2_(sc[v] * a.scale_log2 - lv[e]) : 0.f;
+        sc[v] = p;
+        dp[v] = p * (dp[v] - dv[e]);
+      }
+    }
+    // dV^T[d][key] += dO^T[d][q] P[q][key];  dK^T[d][key] += Q^T[d][q] dS[q][key]
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      half8_t pb, sb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pb[e] = static_cast<_Float16>(sc[8 * h + e]);
+        sb[e] = static_cast<_Float16>(dp[8 * h + e]);
+      }
+      const int qb = 16 * h + 4 * hh;
+#pragma unroll
+      for (int j = 0; j < kD / 32; ++j) {
+        const uint16_t* dr = &dts[buf][(32 * j + l32) * kQS + qb];
+        const uint16_t* qr = &qts[buf][(32 * j + l32) * kQS + qb];
+        const half8_t da = __builtin_bit_cast(half8_t, __builtin_shufflevector(
+            *reinterpret_cast<const half4_t*>(dr), *reinterpret_cast<const half4_t*>(dr + 8),
+            0, 1, 2, 3, 4, 5, 6, 7));
+        const half8_t qa = __builtin_bit_cast(half8_t, __builtin_shufflevector(
+            *reinterpret_cast<const half4_t*>(qr), *reinterpret_cast<const half4_t*>(qr + 8),
+            0, 1, 2, 3, 4, 5, 6, 7));
+        dva[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, pb, dva[j], 0, 0, 0);
+        dka[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, sb, dka[j], 0, 0, 0);
+      }
+    }
+  }
+
+  // fp32 partials [head][token][d]: lane = key column, rows d = 32 j + 8 (v / 4) + 4 hh + v % 4
+  if (key < len) {
+    float* pk = a.dk_part + (static_cast<int64_t>(head) * a.n_tokens + s0 + key) * kD;
+    float* pv = a.dv_part + (static_cast<int64_t>(head) * a.n_tokens + s0 + key) * kD;
+#pragma unroll
+    for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * j + 8 * g + 4 * hh;
+        *reinterpret_cast<float4*>(pk + d0) = make_float4(
+            dka[j][4 * g] * a.scale, dka[j][4 * g + 1] * a.scale, dka[j][4 * g + 2] * a.scale,
+            dka[j][4 * g + 3] * a.scale);
+        *reinterpret_cast<float4*>(pv + d0) =
+            make_float4(dva[j][4 * g], dva[j][4 * g + 1], dva[j][4 * g + 2], dva[j][4 * g + 3]);
+      }
+  }
+}
+
+// dK / dV fp16 [token][kv head][d] = sum over the KV head's query heads, in head order.
+__global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // 4 columns each
+  const int64_t total = a.n_tokens * a.n_kv_heads * (kD / 4);
+  if (idx >= total) return;
+  const int c4 = static_cast<int>(idx % (kD / 4));
+  const int64_t tk = idx / (kD / 4);
+  const int kvh = static_cast<int>(tk % a.n_kv_heads);
+  const int64_t t = tk / a.n_kv_heads;
+  float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+  for (int g = 0; g < a.group; ++g) {
+    const int h = kvh * a.group + g;
+    const int64_t off = (static_cast<int64_t>(h) * a.n_tokens + t) * kD + 4 * c4;
+    const float4 xk = *reinterpret_cast<const float4*>(a.dk_part + off);
+    const float4 xv = *reinterpret_cast<const float4*>(a.dv_part + off);
+    sk.x += xk.x; sk.y += xk.y; sk.z += xk.z; sk.w += xk.w;
+    sv.x += xv.x; sv.y += xv.y; sv.z += xv.z; sv.w += xv.w;
+  }
+  *reinterpret_cast<uint2*>(a.dk + t * a.dk_tok + kvh * a.dk_head + 4 * c4) =
+      make_uint2(pack2(sk.x, sk.y), pack2(sk.z, sk.w));
+  *reinterpret_cast<uint2*>(a.dv + t * a.dv_tok + kvh * a.dv_head + 4 * c4) =
+      make_uint2(pack2(sv.x, sv.y), pack2(sv.z, sv.w));
+}
+
+}  // namespace
+}  // namespace talm
+
+using namespace talm;
+
+TALM_API int talm_attn_fwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                           const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                           const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                           const int32_t* cu_seqlens, int32_t n_seqs, int32_t max_seqlen,
+                           int64_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads,
+                           int32_t head_dim, float scale, uint16_t* out, int64_t o_stride_tok,
+                           int64_t o_stride_head, float* lse, void* stream) {
+  if (head_dim != kD)
+    return fail(TALM_EINVAL, "attn_fwd: head_dim %d (only %d)", head_dim, kD);
+  if (n_seqs < 0 || max_seqlen < 0 || n_tokens < 0 || n_q_heads < 1 || n_kv_heads < 1 ||
+      n_q_heads % n_kv_heads || n_tokens >= (int64_t{1} << 31))
+    return fail(TALM_EINVAL, "attn_fwd: bad shape (seqs %d, max_seqlen %d, tokens %lld, heads %d/%d)",
+                n_seqs, max_seqlen, (long long)n_tokens, n_q_heads, n_kv_heads);
+  for (int64_t s : {q_stride_tok, q_stride_head, k_stride_tok, k_stride_head, v_stride_tok,
+                    v_stride_head, o_stride_tok, o_stride_head})
+    if (s < 0 || s % 8)
+      return fail(TALM_EINVAL, "attn_fwd: strides must be non-negative multiples of 8 elements");
+  if (n_seqs == 0 || max_seqlen == 0 || n_tokens == 0) return ok();
+  if (!q || !k || !v || !cu_seqlens || !out || !lse) return fail(TALM_EINVAL, "attn_fwd: null pointer");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
+    return fail(TALM_EINVAL, "attn_fwd: q, k, v and out must be 16-byte aligned");
+  constexpr int W = 4;
+  FwdArgs a{};
+  a.q = q; a.q_tok = q_stride_tok; a.q_head = q_stride_head;
+  a.k = k; a.k_tok = k_stride_tok; a.k_head = k_stride_head;
+  a.v = v; a.v_tok = v_stride_tok; a.v_head = v_stride_head;
+  a.cu = cu_seqlens; a.group = n_q_heads / n_kv_heads;
+  a.n_tiles = (max_seqlen + 32 * W - 1) / (32 * W);
+  a.scale_log2 = scale * 1.44269504088896341f;
+  a.out = out; a.o_tok = o_stride_tok; a.o_head = o_stride_head;
+  a.lse = lse; a.n_tokens = n_tokens;
+  hipLaunchKernelGGL((attn_fwd_kernel<W>), dim3(static_cast<unsigned>(a.n_tiles),
+                     static_cast<unsigned>(n_q_heads), static_cast<unsigned>(n_seqs)),
+                     dim3(64 * W), 0, as_stream(stream), a);
+  return check_launch("attn_fwd");
+}
+
+TALM_API int64_t talm_attn_bwd_workspace(int64_t n_tokens, int32_t n_q_heads) {
+  if (n_tokens < 0 || n_q_heads < 1) return -1;
+  // Dd [Hq, N] f32, then the dK and dV partials [Hq, N, D] f32 each (256-byte aligned parts)
+  const int64_t dd = (n_tokens * n_q_heads * 4 + 255) / 256 * 256;
+  return dd + 2 * n_tokens * n_q_heads * kD * 4;
+}
+
+TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                           const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                           const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                           const uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                           const uint16_t* dout, int64_t do_stride_tok, int64_t do_stride_head,
+                           const float* lse, const int32_t* cu_seqlens, int32_t n_seqs,
+                           int32_t max_seqlen, int64_t n_tokens, int32_t n_q_heads,
+                           int32_t n_kv_heads, int32_t head_dim, float scale, uint16_t* dq,
+                           int64_t dq_stride_tok, int64_t dq_stride_head, uint16_t* dk,
+                           int64_t dk_stride_tok, int64_t dk_stride_head, uint16_t* dv,
+                           int64_t dv_stride_tok, int64_t dv_stride_head, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  if (head_dim != kD)
+    return fail(TALM_EINVAL, "attn_bwd: head_dim %d (only %d)", head_dim, kD);
+  if (n_seqs < 0 || max_seqlen < 0 || n_tokens < 0 || n_q_heads < 1 || n_kv_heads < 1 ||
+      n_q_heads % n_kv_heads || n_tokens >= (int64_t{1} << 31))
+    return fail(TALM_EINVAL, "attn_bwd: bad shape (seqs %d, max_seqlen %d, tokens %lld, heads %d/%d)",
+                n_seqs, max_seqlen, (long long)n_tokens, n_q_heads, n_kv_heads);
+  for (int64_t s : {q_stride_tok, q_stride_head, k_stride_tok, k_stride_head, v_stride_tok,
+                    v_stride_head, o_stride_tok, o_stride_head, do_stride_tok, do_stride_head,
+                    dq_stride_tok, dq_stride_head, dk_stride_tok, dk_stride_head, dv_stride_tok,
+                    dv_stride_head})
+    if (s < 0 || s % 8)
+      return fail(TALM_EINVAL, "attn_bwd: strides must be non-negative multiples of 8 elements");
+  const int64_t need = talm_attn_bwd_workspace(n_tokens, n_q_heads);
+  if (workspace_bytes < need)
+    return fail(TALM_EINVAL, "attn_bwd: workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)need);
+  if (n_seqs == 0 || max_seqlen == 0 || n_tokens == 0) return ok();
+  if (!q || !k || !v || !out || !dout || !lse || !cu_seqlens || !dq || !dk || !dv || !workspace)
+    return fail(TALM_EINVAL, "attn_bwd: null pointer");
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) ||
+      !aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 8) || !aligned(dv, 8) ||
+      !aligned(workspace, 256))
+    return fail(TALM_EINVAL, "attn_bwd: operands 16-byte aligned (dk, dv 8), workspace 256");
+  constexpr int W = 4;
+  BwdArgs a{};
+  a.q = q; a.q_tok = q_stride_tok; a.q_head = q_stride_head;
+  a.k = k; a.k_tok = k_stride_tok; a.k_head = k_stride_head;
+  a.v = v; a.v_tok = v_stride_tok; a.v_head = v_stride_head;
+  a.o = out; a.o_tok = o_stride_tok; a.o_head = o_stride_head;
+  a.dout = dout; a.do_tok = do_stride_tok; a.do_head = do_stride_head;
+  a.lse = lse; a.cu = cu_seqlens;
+  a.group = n_q_heads / n_kv_heads; a.n_q_heads = n_q_heads; a.n_kv_heads = n_kv_heads;
+  a.n_tiles = (max_seqlen + 32 * W - 1) / (32 * W);
+  a.scale = scale; a.scale_log2 = scale * 1.44269504088896341f;
+  a.n_tokens = n_tokens;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  a.dd = reinterpret_cast<float*>(ws);
+  a.dk_part = reinterpret_cast<float*>(ws + (n_tokens * n_q_heads * 4 + 255) / 256 * 256);
+  a.dv_part = a.dk_part + n_tokens * n_q_heads * kD;
+  a.dq = dq; a.dq_tok = dq_stride_tok; a.dq_head = dq_stride_head;
+  a.dk = dk; a.dk_tok = dk_stride_tok; a.dk_head = dk_stride_head;
+  a.dv = dv; a.dv_tok = dv_stride_tok; a.dv_head = dv_stride_head;
+  const hipStream_t s = as_stream(stream);
+  const int64_t rows = n_tokens * n_q_heads;
+  hipLaunchKernelGGL(attn_bwd_dot_kernel, dim3(static_cast<unsigned>((rows * 16 + 255) / 256)),
+                     dim3(256), 0, s, a);
+  const dim3 grid(static_cast<unsigned>(a.n_tiles), static_cast<unsigned>(n_q_heads),
+                  static_cast<unsigned>(n_seqs));
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<W>), grid, dim3(64 * W), 0, s, a);
+  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<W>), grid, dim3(64 * W), 0, s, a);
+  const int64_t red = n_tokens * n_kv_heads * (kD / 4);
+  hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3(static_cast<unsigned>((red + 255) / 256)),
+                     dim3(256), 0, s, a);
+  return check_launch("attn_bwd");
+}

@@ -431,6 +431,77 @@ void lora_wgrad(const Tensor& x, const Tensor& dy, const Tensor& u, const Tensor
 
 
 // ------------------------------------------------------------------------------------------
+// Variable-length causal GQA attention
+// ------------------------------------------------------------------------------------------
+void attn_heads(const Tensor& t, const char* name, int64_t n_tokens, int64_t heads) {
+  require_fp16(t, name);
+  TORCH_CHECK_VALUE(t.dim() == 3 && t.size(0) == n_tokens && t.size(1) == heads &&
+                        t.size(2) == 128 && t.stride(2) == 1,
+                    "attn: ", name, " must be an fp16 [N, heads, 128] view with unit column stride");
+}
+
+void attn_cu(const Tensor& cu, const Tensor& q) {
+  require(cu.is_cuda() && cu.scalar_type() == at::kInt && cu.dim() == 1 && cu.numel() >= 1 &&
+              cu.is_contiguous() && cu.device() == q.device(),
+          "attn: cu_seqlens int32 [n_seqs + 1] on the tensors' device");
+}
+
+// q [N, Hq, 128], k / v [N, Hkv, 128] fp16 views; out [N, Hq, 128]; lse f32 [Hq, N].
+void attn_fwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& cu,
+              int64_t max_seqlen, double scale, const Tensor& out, const Tensor& lse) {
+  require(q.dim() == 3 && k.dim() == 3, "attn: q [N, Hq, 128], k / v [N, Hkv, 128]");
+  const int64_t n = q.size(0), hq = q.size(1), hkv = k.size(1);
+  attn_heads(q, "q", n, hq);
+  attn_heads(k, "k", n, hkv);
+  attn_heads(v, "v", n, hkv);
+  attn_heads(out, "out", n, hq);
+  attn_cu(cu, q);
+  require(lse.is_cuda() && lse.scalar_type() == at::kFloat && lse.is_contiguous() &&
+              same_shape(lse, hq, n),
+          "attn_fwd: lse float32 [Hq, N]");
+  check(talm_attn_fwd(as<uint16_t>(q), q.stride(0), q.stride(1), as<uint16_t>(k), k.stride(0),
+                      k.stride(1), as<uint16_t>(v), v.stride(0), v.stride(1), as<int32_t>(cu),
+                      static_cast<int32_t>(cu.numel() - 1), static_cast<int32_t>(max_seqlen), n,
+                      static_cast<int32_t>(hq), static_cast<int32_t>(hkv), 128,
+                      static_cast<float>(scale), as<uint16_t>(out), out.stride(0), out.stride(1),
+                      as<float>(lse), stream_of(q)),
+        "attn_fwd");
+}
+
+void attn_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out,
+              const Tensor& dout, const Tensor& lse, const Tensor& cu, int64_t max_seqlen,
+              double scale, const Tensor& dq, const Tensor& dk, const Tensor& dv,
+              const Tensor& workspace) {
+  require(q.dim() == 3 && k.dim() == 3, "attn: q [N, Hq, 128], k / v [N, Hkv, 128]");
+  const int64_t n = q.size(0), hq = q.size(1), hkv = k.size(1);
+  attn_heads(q, "q", n, hq);
+  attn_heads(k, "k", n, hkv);
+  attn_heads(v, "v", n, hkv);
+  attn_heads(out, "out", n, hq);
+  attn_heads(dout, "dout", n, hq);
+  attn_heads(dq, "dq", n, hq);
+  attn_heads(dk, "dk", n, hkv);
+  attn_heads(dv, "dv", n, hkv);
+  attn_cu(cu, q);
+  require(lse.is_cuda() && lse.scalar_type() == at::kFloat && lse.is_contiguous() &&
+              same_shape(lse, hq, n),
+          "attn_bwd: lse float32 [Hq, N]");
+  require(workspace.is_cuda() && workspace.is_contiguous(), "attn_bwd: workspace");
+  check(talm_attn_bwd(as<uint16_t>(q), q.stride(0), q.stride(1), as<uint16_t>(k), k.stride(0),
+                      k.stride(1), as<uint16_t>(v), v.stride(0), v.stride(1), as<uint16_t>(out),
+                      out.stride(0), out.stride(1), as<uint16_t>(dout), dout.stride(0),
+                      dout.stride(1), as<float>(lse), as<int32_t>(cu),
+                      static_cast<int32_t>(cu.numel() - 1), static_cast<int32_t>(max_seqlen), n,
+                      static_cast<int32_t>(hq), static_cast<int32_t>(hkv), 128,
+                      static_cast<float>(scale), as<uint16_t>(dq), dq.stride(0), dq.stride(1),
+                      as<uint16_t>(dk), dk.stride(0), dk.stride(1), as<uint16_t>(dv),
+                      dv.stride(0), dv.stride(1), workspace.data_ptr(),
+                      workspace.numel() * static_cast<int64_t>(workspace.element_size()),
+                      stream_of(q)),
+        "attn_bwd");
+}
+
+// ------------------------------------------------------------------------------------------
 // Plain fp16 GEMMs on hipBLASLt with cached plans.
 // ------------------------------------------------------------------------------------------
 struct GemmKey {
@@ -607,6 +678,11 @@ TORCH_LIBRARY(talm, m) {
         "Tensor(a!) da0, Tensor(b!) db0, int lo1, int seg1, float scaling1, Tensor(c!)? da1, "
         "Tensor(d!)? db1, Tensor(e!) workspace) -> ()");
   m.def("gemm(Tensor a, Tensor b, Tensor? bias, int b_t, Tensor(a!) out) -> ()");
+  m.def("attn_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, float scale, "
+        "Tensor(a!) out, Tensor(b!) lse) -> ()");
+  m.def("attn_bwd(Tensor q, Tensor k, Tensor v, Tensor out, Tensor dout, Tensor lse, "
+        "Tensor cu_seqlens, int max_seqlen, float scale, Tensor(a!) dq, Tensor(b!) dk, "
+        "Tensor(c!) dv, Tensor(d!) workspace) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(talm, CUDA, m) {
@@ -624,4 +700,6 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("qkv_lora_bwd_dx", &qkv_lora_bwd_dx);
   m.impl("lora_wgrad", &lora_wgrad);
   m.impl("gemm", &gemm);
+  m.impl("attn_fwd", &attn_fwd);
+  m.impl("attn_bwd", &attn_bwd);
 }

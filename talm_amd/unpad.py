@@ -5,10 +5,10 @@ flat sequence [1, N] with per-row positions, runs the decoder on it and scatters
 outputs back. Attention must not cross rows: while the flat forward runs (`rows_context`), the
 registered "sdpa" attention interface runs causal attention that never crosses rows
 (`rows_sdpa`): all rows in one variable-length flash-attention launch per direction with the
-row offsets `cu_seqlens` and GQA heads shared, not repeated (`VarlenAttention`; the reference
-does the same with one memory-efficient launch per KV head, solution/unpad.py:199-294), else one
-SDPA call per row. Attention itself is not one of this package's kernels (it is PyTorch's);
-its `cu_seqlens` are the packing contract the other kernels use.
+row offsets `cu_seqlens` and GQA heads shared, not repeated (`VarlenAttention`: this package's
+HIP kernels for fp16 heads of 128, PyTorch's varlen flash attention otherwise; the reference
+launches one memory-efficient attention per KV head, solution/unpad.py:199-294), else one SDPA
+call per row.
 """
 
 import contextlib
@@ -16,6 +16,7 @@ import contextlib
 import torch
 import torch.nn.functional as F
 
+from . import _ops  # noqa: F401 - registers torch.ops.talm.*
 from .engaged import FELL_BACK, ON, RAN
 from .state import DISABLED, fallback
 
@@ -76,32 +77,63 @@ def is_right_padded(attention_mask, lengths):
     return bool((attention_mask.bool() == prefix).all().item())
 
 
+def _kernel_applies(q, k, v):
+    """The [N, H, D] views suit torch.ops.talm.attn_*: fp16, head_dim 128, strides of whole
+    16-byte chunks, 16-byte aligned."""
+    return (q.dtype == torch.float16 and q.shape[-1] == 128
+            and all(t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0
+                    for t in (q, k, v)))
+
+
 class VarlenAttention(torch.autograd.Function):
-    """Causal attention of every row of the flat sequence in ONE launch each way: PyTorch's
-    variable-length flash attention with the row offsets `cu_seqlens` and the KV heads shared by
-    the query heads of their group (GQA, no repeated K/V). Inputs are the [1, H, N, D] views the
-    attention interface receives; the output is [1, N, Hq, D] as SDPA's transposed output is.
-    Bit-identical to per-row `scaled_dot_product_attention(..., is_causal=True)` on this
-    backend (the same kernel family, one launch instead of one per row)."""
+    """Causal attention of every row of the flat sequence in ONE launch each way, with the row
+    offsets `cu_seqlens` and the KV heads shared by the query heads of their group (GQA, no
+    repeated K/V): this package's HIP kernels (`torch.ops.talm.attn_fwd` / `attn_bwd`) for fp16
+    heads of 128, else PyTorch's variable-length flash attention. Inputs are the [1, H, N, D]
+    views the attention interface receives; the output is [1, N, Hq, D] as SDPA's transposed
+    output is. Semantics of per-row `scaled_dot_product_attention(..., is_causal=True)`
+    (solution/unpad.py:121-134, :199-294)."""
 
     @staticmethod
     def forward(ctx, query, key, value, cu, max_len, scale):
         q, k, v = (t[0].transpose(0, 1) for t in (query, key, value))  # [N, H, D] views
+        ctx.max_len, ctx.scale = max_len, scale
+        ctx.kernel = _kernel_applies(q, k, v)
+        if ctx.kernel:
+            n, hq = q.shape[0], q.shape[1]
+            out = torch.empty(n, hq, q.shape[2], dtype=q.dtype, device=q.device)
+            lse = torch.empty(hq, n, dtype=torch.float32, device=q.device)
+            torch.ops.talm.attn_fwd(q, k, v, cu, max_len, scale, out, lse)
+            ctx.save_for_backward(q, k, v, out, lse, cu)
+            RAN["attn_kernel"] += 1
+            return out[None]
         out, lse, rng, unused, _ = torch.ops.aten._flash_attention_forward(
             q, k, v, cu, cu, max_len, max_len, 0.0, True, False, scale=scale)
         ctx.save_for_backward(q, k, v, out, lse, rng, unused, cu)
-        ctx.max_len, ctx.scale = max_len, scale
         return out[None]
 
     @staticmethod
     def backward(ctx, grad):
-        q, k, v, out, lse, rng, unused, cu = ctx.saved_tensors
         g = grad[0]
-        if not g.is_contiguous():
-            g = g.contiguous()
-        dq, dk, dv = torch.ops.aten._flash_attention_backward(
-            g, q, k, v, out, lse, cu, cu, ctx.max_len, ctx.max_len, 0.0, True, rng, unused,
-            scale=ctx.scale)
+        if ctx.kernel:
+            q, k, v, out, lse, cu = ctx.saved_tensors
+            if g.stride(-1) != 1 or g.stride(0) % 8 or g.stride(1) % 8 or g.data_ptr() % 16:
+                g = g.contiguous()
+            dq = torch.empty_like(out)
+            dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+            dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+            ws = torch.empty(_ops.attn_bwd_workspace_bytes(q.shape[0], q.shape[1]),
+                             dtype=torch.uint8, device=q.device)
+            torch.ops.talm.attn_bwd(q, k, v, out, g, lse, cu, ctx.max_len, ctx.scale, dq, dk, dv,
+                                    ws)
+            RAN["attn_kernel_bwd"] += 1
+        else:
+            q, k, v, out, lse, rng, unused, cu = ctx.saved_tensors
+            if not g.is_contiguous():
+                g = g.contiguous()
+            dq, dk, dv = torch.ops.aten._flash_attention_backward(
+                g, q, k, v, out, lse, cu, cu, ctx.max_len, ctx.max_len, 0.0, True, rng, unused,
+                scale=ctx.scale)
         return (dq.transpose(0, 1)[None], dk.transpose(0, 1)[None], dv.transpose(0, 1)[None],
                 None, None, None)
 

@@ -46,7 +46,8 @@ def test_patched_step_matches_eager_loss_curve(monkeypatch):
     assert engaged.RAN["fused_head"] == 0
     fused = _run(True, 6, monkeypatch)
     for name in ("fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "rope",
-                 "addnorm", "swiglu_inplace", "head", "varlen_attn"):
+                 "addnorm", "swiglu_inplace", "head", "varlen_attn", "attn_kernel",
+                 "attn_kernel_bwd"):
         assert engaged.RAN[name] > 0, f"{name} did not run"
     assert abs(fused[0] - eager[0]) <= 1e-3 * abs(eager[0]), (fused[0], eager[0])
     for a, b in zip(fused, eager):
@@ -54,9 +55,10 @@ def test_patched_step_matches_eager_loss_curve(monkeypatch):
 
 
 def test_varlen_attention_matches_per_row_sdpa():
-    """The one-launch variable-length attention (unpad.VarlenAttention) against causal SDPA per
-    row with GQA (the reference's per-row semantics, solution/unpad.py:121-134) on the config-5
-    row lengths: outputs and q/k/v gradients to one fp16 rounding."""
+    """The one-launch variable-length attention (unpad.VarlenAttention on the HIP kernels)
+    against PyTorch's causal SDPA per row with GQA (the reference's per-row semantics,
+    solution/unpad.py:121-134) on the config-5 row lengths, on the q|k|v buffer's views: outputs
+    and q/k/v gradients within one fp16 rounding of the largest magnitude (both sides round)."""
     import torch.nn.functional as F
 
     from talm_amd import unpad, workloads
