@@ -114,6 +114,20 @@ int talm_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const uint16_t* 
                     uint16_t* dgate, uint16_t* dup, int64_t n, void* stream);
 
 /*
+ * The same two SwiGLU passes on [rows, cols] fp16 views with row strides (elements): gate and up
+ * may be the two halves of one [rows, 2 cols] buffer (the fused MLP's gate|up GEMM output,
+ * solution/fused_proj.py:241-287, where the reference runs the flat kernels on a transposed
+ * buffer). cols and every row stride multiples of 8, pointers 16-byte aligned, rows <= 65535;
+ * outputs may alias inputs element for element.
+ */
+int talm_swiglu_fwd_rows(const uint16_t* gate, int64_t ld_gate, const uint16_t* up, int64_t ld_up,
+                         uint16_t* out, int64_t ld_out, int64_t rows, int64_t cols, void* stream);
+int talm_swiglu_bwd_rows(const uint16_t* grad, int64_t ld_grad, const uint16_t* gate,
+                         int64_t ld_gate, const uint16_t* up, int64_t ld_up, uint16_t* dgate,
+                         int64_t ld_dgate, uint16_t* dup, int64_t ld_dup, int64_t rows,
+                         int64_t cols, void* stream);
+
+/*
  * Bytes of workspace talm_head_ce needs (-1 for arguments it would reject). `group` vocabulary
  * slices are processed per step: the workspace holds their fp16 logits [n_rows, group * vchunk],
  * the per-tile statistics and the fp32 gradient partials [group, n_grad, hidden].

@@ -30,6 +30,8 @@ SIGNATURES = {
                   _I64, _I64, _I64, _I64, _I32, _P],
     "talm_swiglu_fwd": [_P, _P, _P, _I64, _P],
     "talm_swiglu_bwd": [_P, _P, _P, _P, _P, _I64, _P],
+    "talm_swiglu_fwd_rows": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P],
+    "talm_swiglu_bwd_rows": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P],
     "talm_head_weight_t": [_P, _I64, _I64, _I64, _P, _I64, _P],
     "talm_lora_down": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I32, _I32, _F32, _F32, _P,
                        _P, _I64, _P],

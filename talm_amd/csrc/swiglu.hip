@@ -1,8 +1,10 @@
 // SwiGLU for gfx950: forward silu(gate) * up and its backward, fp16 storage with fp32 math.
-// Flat, contiguous operands; each thread moves 8 elements per 16-byte access, two accesses in
-// flight per operand. Aliasing the outputs onto the inputs is allowed (the in-place backward and
+// Flat, contiguous operands (or [rows, cols] views with row strides, the *_rows entry points);
+// each thread moves 8 elements per 16-byte access, two accesses in flight per operand. Aliasing the outputs onto the inputs is allowed (the in-place backward and
 // the save-up forward): a thread loads all its operands before storing at the same offsets.
 #include "common.h"
+
+#include <initializer_list>
 
 namespace talm {
 namespace {
@@ -107,6 +109,48 @@ __global__ __launch_bounds__(kThreads) void swiglu_bwd_any(const uint16_t* grad,
   dup[i] = f2h(d * g * sig);
 }
 
+// Row-strided operands ([rows, cols] views, row strides in 16-byte vectors): one vector per
+// thread, row = blockIdx.y. Used where gate and up are the two halves of one [rows, 2 cols]
+// buffer (the fused MLP's gate|up GEMM output).
+struct RowArgs {
+  int64_t cols_vec, ld0, ld1, ld2, ld3, ld4;  // row strides of the operands in vectors
+};
+
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_rows(const uint4* gate, const uint4* up,
+                                                            uint4* out, RowArgs r) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (c >= r.cols_vec) return;
+  const int64_t row = blockIdx.y;
+  const uint4 gv = gate[row * r.ld0 + c], uv = up[row * r.ld1 + c];
+  float g[8], u[8], o[8];
+  unpack8(gv, g);
+  unpack8(uv, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = g[e] * sigmoid(g[e]) * u[e];
+  out[row * r.ld2 + c] = pack8(o);
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_rows(const uint4* grad, const uint4* gate,
+                                                            const uint4* up, uint4* dgate,
+                                                            uint4* dup, RowArgs r) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (c >= r.cols_vec) return;
+  const int64_t row = blockIdx.y;
+  const uint4 dv = grad[row * r.ld0 + c], gv = gate[row * r.ld1 + c], uv = up[row * r.ld2 + c];
+  float d[8], g[8], u[8], dg[8], du[8];
+  unpack8(dv, d);
+  unpack8(gv, g);
+  unpack8(uv, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float sig = sigmoid(g[e]);
+    du[e] = d[e] * g[e] * sig;
+    dg[e] = d[e] * u[e] * sig * (1.0f + g[e] * (1.0f - sig));
+  }
+  dgate[row * r.ld3 + c] = pack8(dg);
+  dup[row * r.ld4 + c] = pack8(du);
+}
+
 unsigned vec_blocks(int64_t n_vec) {
   // Enough workgroups to cover every CU several times over; the grid-stride loop takes the rest.
   const int64_t per_block = static_cast<int64_t>(kThreads) * kVecPerThread;
@@ -164,4 +208,56 @@ TALM_API int talm_swiglu_bwd(const uint16_t* grad, const uint16_t* gate, const u
                        dim3(kThreads), 0, s, grad + head, gate + head, up + head, dgate + head,
                        dup + head, tail);
   return check_launch("swiglu_bwd");
+}
+
+namespace {
+int rows_check(const char* what, int64_t rows, int64_t cols, std::initializer_list<int64_t> lds,
+               std::initializer_list<const void*> ptrs) {
+  if (rows < 0 || cols < 0 || cols % 8 || rows > 65535)
+    return fail(TALM_EINVAL, "%s: rows %lld (<= 65535), cols %lld (a multiple of 8)", what,
+                (long long)rows, (long long)cols);
+  for (int64_t ld : lds)
+    if (ld < cols || ld % 8)
+      return fail(TALM_EINVAL, "%s: row strides at least cols and multiples of 8", what);
+  for (const void* p : ptrs) {
+    if (!p) return fail(TALM_EINVAL, "%s: null pointer", what);
+    if (!aligned(p, 16)) return fail(TALM_EINVAL, "%s: operands 16-byte aligned", what);
+  }
+  return TALM_OK;
+}
+}  // namespace
+
+TALM_API int talm_swiglu_fwd_rows(const uint16_t* gate, int64_t ld_gate, const uint16_t* up,
+                                  int64_t ld_up, uint16_t* out, int64_t ld_out, int64_t rows,
+                                  int64_t cols, void* stream) {
+  if (rows == 0 || cols == 0) return ok();
+  if (int st = rows_check("swiglu_fwd_rows", rows, cols, {ld_gate, ld_up, ld_out},
+                          {gate, up, out}))
+    return st;
+  RowArgs r{cols / 8, ld_gate / 8, ld_up / 8, ld_out / 8, 0, 0};
+  hipLaunchKernelGGL(swiglu_fwd_rows,
+                     dim3(static_cast<unsigned>((r.cols_vec + kThreads - 1) / kThreads),
+                          static_cast<unsigned>(rows)),
+                     dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const uint4*>(gate),
+                     reinterpret_cast<const uint4*>(up), reinterpret_cast<uint4*>(out), r);
+  return check_launch("swiglu_fwd_rows");
+}
+
+TALM_API int talm_swiglu_bwd_rows(const uint16_t* grad, int64_t ld_grad, const uint16_t* gate,
+                                  int64_t ld_gate, const uint16_t* up, int64_t ld_up,
+                                  uint16_t* dgate, int64_t ld_dgate, uint16_t* dup,
+                                  int64_t ld_dup, int64_t rows, int64_t cols, void* stream) {
+  if (rows == 0 || cols == 0) return ok();
+  if (int st = rows_check("swiglu_bwd_rows", rows, cols,
+                          {ld_grad, ld_gate, ld_up, ld_dgate, ld_dup},
+                          {grad, gate, up, dgate, dup}))
+    return st;
+  RowArgs r{cols / 8, ld_grad / 8, ld_gate / 8, ld_up / 8, ld_dgate / 8, ld_dup / 8};
+  hipLaunchKernelGGL(swiglu_bwd_rows,
+                     dim3(static_cast<unsigned>((r.cols_vec + kThreads - 1) / kThreads),
+                          static_cast<unsigned>(rows)),
+                     dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const uint4*>(grad),
+                     reinterpret_cast<const uint4*>(gate), reinterpret_cast<const uint4*>(up),
+                     reinterpret_cast<uint4*>(dgate), reinterpret_cast<uint4*>(dup), r);
+  return check_launch("swiglu_bwd_rows");
 }

@@ -182,6 +182,34 @@ void swiglu_bwd(const Tensor& grad, const Tensor& gate, const Tensor& up, const 
         "swiglu_bwd");
 }
 
+// [rows, cols] fp16 views with unit column stride (any row strides); outputs may alias inputs.
+void swiglu_rows_view(const Tensor& t, int64_t rows, int64_t cols) {
+  require_fp16(t, "swiglu operand");
+  require(same_shape(t, rows, cols) && t.stride(1) == 1,
+          "swiglu_rows: [rows, cols] views with unit column stride, one shape");
+}
+
+void swiglu_fwd_rows(const Tensor& gate, const Tensor& up, const Tensor& out) {
+  require(gate.dim() == 2, "swiglu_rows: [rows, cols] views with unit column stride, one shape");
+  const int64_t rows = gate.size(0), cols = gate.size(1);
+  for (const Tensor* t : {&gate, &up, &out}) swiglu_rows_view(*t, rows, cols);
+  check(talm_swiglu_fwd_rows(as<uint16_t>(gate), gate.stride(0), as<uint16_t>(up), up.stride(0),
+                             as<uint16_t>(out), out.stride(0), rows, cols, stream_of(gate)),
+        "swiglu_fwd_rows");
+}
+
+void swiglu_bwd_rows(const Tensor& grad, const Tensor& gate, const Tensor& up,
+                     const Tensor& dgate, const Tensor& dup) {
+  require(gate.dim() == 2, "swiglu_rows: [rows, cols] views with unit column stride, one shape");
+  const int64_t rows = gate.size(0), cols = gate.size(1);
+  for (const Tensor* t : {&grad, &gate, &up, &dgate, &dup}) swiglu_rows_view(*t, rows, cols);
+  check(talm_swiglu_bwd_rows(as<uint16_t>(grad), grad.stride(0), as<uint16_t>(gate),
+                             gate.stride(0), as<uint16_t>(up), up.stride(0), as<uint16_t>(dgate),
+                             dgate.stride(0), as<uint16_t>(dup), dup.stride(0), rows, cols,
+                             stream_of(gate)),
+        "swiglu_bwd_rows");
+}
+
 // weight fp16 [V, H] (unit column stride) -> weight_t fp16 [H, ldwt] (unit column stride,
 // ldwt >= V): the transpose, with columns [V, ldwt) zero.
 void head_weight_t(const Tensor& weight, const Tensor& weight_t) {
@@ -507,10 +535,11 @@ void attn_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& o
 struct GemmKey {
   int device;
   int64_t m, n, k, lda, ldb, ldd;
-  int trans_a, bias;
+  int trans_a, trans_b, bias;
   bool operator==(const GemmKey& o) const {
     return device == o.device && m == o.m && n == o.n && k == o.k && lda == o.lda &&
-           ldb == o.ldb && ldd == o.ldd && trans_a == o.trans_a && bias == o.bias;
+           ldb == o.ldb && ldd == o.ldd && trans_a == o.trans_a && trans_b == o.trans_b &&
+           bias == o.bias;
   }
 };
 
@@ -518,7 +547,7 @@ struct GemmKeyHash {
   size_t operator()(const GemmKey& key) const {
     size_t h = static_cast<size_t>(key.device);
     for (int64_t v : {key.m, key.n, key.k, key.lda, key.ldb, key.ldd,
-                      static_cast<int64_t>(key.trans_a * 2 + key.bias)})
+                      static_cast<int64_t>(key.trans_a * 4 + key.trans_b * 2 + key.bias)})
       h = h * 1000003u ^ static_cast<size_t>(v);
     return h;
   }
@@ -556,8 +585,9 @@ struct PlanCache {
 thread_local PlanCache plan_cache;
 constexpr size_t kMaxPlans = 2048;
 
-// D [m, n] = op(A) [m, k] B [k, n] in hipBLASLt's column-major terms, fp16 in and out, fp32
-// accumulation; op(A) = A^T when trans_a (A stored k x m), else A (stored m x k); B stored k x n.
+// D [m, n] = op(A) [m, k] op(B) [k, n] in hipBLASLt's column-major terms, fp16 in and out, fp32
+// accumulation; op(A) = A^T when trans_a (A stored k x m), else A (stored m x k); op(B) = B^T
+// when trans_b (B stored n x k), else B (stored k x n).
 const GemmPlan& plan_for(const GemmKey& key, hipblasLtHandle_t handle, size_t workspace_limit) {
   auto it = plan_cache.plans.find(key);
   if (it != plan_cache.plans.end()) return it->second;
@@ -569,7 +599,7 @@ const GemmPlan& plan_for(const GemmKey& key, hipblasLtHandle_t handle, size_t wo
   try {
     lt_check(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "descriptor");
     const hipblasOperation_t op_a = key.trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-    const hipblasOperation_t op_b = HIPBLAS_OP_N;
+    const hipblasOperation_t op_b = key.trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N;
     lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_a,
                                              sizeof(op_a)), "transa");
     lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_b,
@@ -584,7 +614,8 @@ const GemmPlan& plan_for(const GemmKey& key, hipblasLtHandle_t handle, size_t wo
     }
     lt_check(hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, key.trans_a ? key.k : key.m,
                                          key.trans_a ? key.m : key.k, key.lda), "layout A");
-    lt_check(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, key.k, key.n, key.ldb), "layout B");
+    lt_check(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, key.trans_b ? key.n : key.k,
+                                         key.trans_b ? key.k : key.n, key.ldb), "layout B");
     lt_check(hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16F, key.m, key.n, key.ldd), "layout D");
     hipblasLtMatmulPreference_t pref = nullptr;
     lt_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
@@ -609,6 +640,23 @@ const GemmPlan& plan_for(const GemmKey& key, hipblasLtHandle_t handle, size_t wo
   return plan_cache.plans.emplace(key, p).first->second;
 }
 
+// D = op(A) op(B) (+ bias per row of D) (+ beta D) on the stream of `ref`.
+void run_gemm(const GemmKey& key, const void* a, const void* b, const void* bias, void* d,
+              float beta, const Tensor& ref) {
+  hipblasLtHandle_t handle = at::cuda::getCurrentCUDABlasLtHandle();
+  void* workspace = at::cuda::getCUDABlasLtWorkspace();
+  const size_t workspace_size = at::cuda::getCUDABlasLtWorkspaceSize();
+  const GemmPlan& p = plan_for(key, handle, workspace_size);
+  if (key.bias)
+    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias,
+                                             sizeof(bias)), "bias");
+  const float alpha = 1.f;
+  lt_check(hipblasLtMatmul(handle, p.desc, &alpha, a, p.a, b, p.b, &beta, d, p.d, d, p.d,
+                           &p.algo, workspace, p.workspace,
+                           static_cast<hipStream_t>(stream_of(ref))),
+           "matmul");
+}
+
 // out [M, N] = a [M, K] b^T (+ bias [N]) with b [N, K] when b_t != 0, else a [M, K] b with
 // b [K, N]; fp16 operands with unit column stride, fp32 accumulation.
 void gemm(const Tensor& a, const Tensor& b, const OptTensor& bias, int64_t b_t,
@@ -631,22 +679,40 @@ void gemm(const Tensor& a, const Tensor& b, const OptTensor& bias, int64_t b_t,
   require(k > 0, "gemm: empty reduction");
   if (m_rows == 0 || n_cols == 0) return;
   // column-major: out^T [N, M] = op(b) [N, K] a^T [K, M]
-  const GemmKey key{static_cast<int>(a.device().index()), n_cols, m_rows, k, b.stride(0),
-                    a.stride(0), out.stride(0), b_t ? 1 : 0, bias.has_value() ? 1 : 0};
-  hipblasLtHandle_t handle = at::cuda::getCurrentCUDABlasLtHandle();
-  void* workspace = at::cuda::getCUDABlasLtWorkspace();
-  const size_t workspace_size = at::cuda::getCUDABlasLtWorkspaceSize();
-  const GemmPlan& p = plan_for(key, handle, workspace_size);
-  if (bias.has_value()) {
-    const void* bias_ptr = bias->data_ptr();
-    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER,
-                                             &bias_ptr, sizeof(bias_ptr)), "bias");
-  }
-  const float alpha = 1.f, beta = 0.f;
-  lt_check(hipblasLtMatmul(handle, p.desc, &alpha, b.data_ptr(), p.a, a.data_ptr(), p.b, &beta,
-                           out.data_ptr(), p.d, out.data_ptr(), p.d, &p.algo, workspace,
-                           p.workspace, static_cast<hipStream_t>(stream_of(out))),
-           "matmul");
+  run_gemm(GemmKey{static_cast<int>(a.device().index()), n_cols, m_rows, k, b.stride(0),
+                   a.stride(0), out.stride(0), b_t ? 1 : 0, 0, bias.has_value() ? 1 : 0},
+           b.data_ptr(), a.data_ptr(), bias.has_value() ? bias->data_ptr() : nullptr,
+           out.data_ptr(), 0.f, out);
+}
+
+// Elements of t's storage from its first element on.
+int64_t storage_span(const Tensor& t) {
+  return static_cast<int64_t>(t.storage().nbytes() / t.element_size()) - t.storage_offset();
+}
+
+// The BLAS form: D [m, n] = op(A) [m, k] op(B) [k, n] (+ D when accumulate) in column-major
+// terms with leading dimensions lda, ldb, ldd (elements), each matrix starting at its tensor's
+// first element; the tensors' storage must cover every element the product touches (views of a
+// wider buffer are fine).
+void gemm_ex(const Tensor& a, int64_t trans_a, const Tensor& b, int64_t trans_b, const Tensor& d,
+             int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldd,
+             int64_t accumulate) {
+  require_fp16(a, "a");
+  require_fp16(b, "b");
+  require_fp16(d, "d");
+  require(a.device() == b.device() && a.device() == d.device(), "gemm_ex: one device");
+  require(m >= 0 && n >= 0 && k >= 1, "gemm_ex: m, n >= 0 and k >= 1");
+  if (m == 0 || n == 0) return;
+  // rows x cols of each stored (column-major) matrix
+  const int64_t ar = trans_a ? k : m, ac = trans_a ? m : k;
+  const int64_t br = trans_b ? n : k, bc = trans_b ? k : n;
+  require(lda >= ar && ldb >= br && ldd >= m, "gemm_ex: leading dimensions below the row count");
+  require((ac - 1) * lda + ar <= storage_span(a) && (bc - 1) * ldb + br <= storage_span(b) &&
+              (n - 1) * ldd + m <= storage_span(d),
+          "gemm_ex: an operand's storage does not cover the product");
+  run_gemm(GemmKey{static_cast<int>(a.device().index()), m, n, k, lda, ldb, ldd,
+                   trans_a ? 1 : 0, trans_b ? 1 : 0, 0},
+           a.data_ptr(), b.data_ptr(), nullptr, d.data_ptr(), accumulate ? 1.f : 0.f, d);
 }
 
 }  // namespace
@@ -661,6 +727,9 @@ TORCH_LIBRARY(talm, m) {
         "int backward) -> ()");
   m.def("swiglu_fwd(Tensor gate, Tensor up, Tensor(a!) out) -> ()");
   m.def("swiglu_bwd(Tensor grad, Tensor gate, Tensor up, Tensor(a!) dgate, Tensor(b!) dup) -> ()");
+  m.def("swiglu_fwd_rows(Tensor gate, Tensor up, Tensor(a!) out) -> ()");
+  m.def("swiglu_bwd_rows(Tensor grad, Tensor gate, Tensor up, Tensor(a!) dgate, "
+        "Tensor(b!) dup) -> ()");
   m.def("head_weight_t(Tensor weight, Tensor(a!) weight_t) -> ()");
   m.def("head_ce(Tensor hidden, Tensor weight, Tensor? weight_t, Tensor targets, int vchunk, "
         "int n_grad, int group, Tensor(a!) token_loss, Tensor(b!) entropy, Tensor(c!) best_idx, "
@@ -678,6 +747,8 @@ TORCH_LIBRARY(talm, m) {
         "Tensor(a!) da0, Tensor(b!) db0, int lo1, int seg1, float scaling1, Tensor(c!)? da1, "
         "Tensor(d!)? db1, Tensor(e!) workspace) -> ()");
   m.def("gemm(Tensor a, Tensor b, Tensor? bias, int b_t, Tensor(a!) out) -> ()");
+  m.def("gemm_ex(Tensor a, int trans_a, Tensor b, int trans_b, Tensor(a!) d, int m, int n, int k, "
+        "int lda, int ldb, int ldd, int accumulate) -> ()");
   m.def("attn_fwd(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, int max_seqlen, float scale, "
         "Tensor(a!) out, Tensor(b!) lse) -> ()");
   m.def("attn_bwd(Tensor q, Tensor k, Tensor v, Tensor out, Tensor dout, Tensor lse, "
@@ -692,6 +763,8 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("rope", &rope);
   m.impl("swiglu_fwd", &swiglu_fwd);
   m.impl("swiglu_bwd", &swiglu_bwd);
+  m.impl("swiglu_fwd_rows", &swiglu_fwd_rows);
+  m.impl("swiglu_bwd_rows", &swiglu_bwd_rows);
   m.impl("head_weight_t", &head_weight_t);
   m.impl("head_ce", &head_ce);
   m.impl("lora_down", &lora_down);
@@ -700,6 +773,7 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("qkv_lora_bwd_dx", &qkv_lora_bwd_dx);
   m.impl("lora_wgrad", &lora_wgrad);
   m.impl("gemm", &gemm);
+  m.impl("gemm_ex", &gemm_ex);
   m.impl("attn_fwd", &attn_fwd);
   m.impl("attn_bwd", &attn_bwd);
 }

@@ -1,0 +1,138 @@
+"""The decoder MLP down(silu(gate(x)) * up(x)) on a packed layer group as ONE autograd node
+(the reference's FusedMLP, solution/fused_proj.py:241-287).
+
+gate and up write the two halves of one [N, 2I] buffer, SwiGLU runs on the halves in place, and
+the input gradient accumulates its two products in one output:
+  forward   gu[:, :I] = x W_gate^T, gu[:, I:] = x W_up^T
+            act = silu(gu[:, :I]) * gu[:, I:]  (talm_swiglu_fwd_rows)
+            y = act W_down^T
+  backward  dact = dy W_down
+            dgate, dup over gu's halves        (talm_swiglu_bwd_rows, in place)
+            dx = dgate W_gate, then dx += dup W_up (the second GEMM accumulates: no add pass)
+One node instead of four (three GroupLinear nodes and the SwiGLU node) and no separate add of
+the gate and up input gradients: the step is bound by the host's launch rate. Every GEMM keeps
+the form and shape of the per-projection path: hipBLASLt's first-choice kernels for the single
+[N, 2I] product and for the 2I-deep input gradient (or the reference's transposed formulation)
+are several times slower here. Same products with fp32 accumulation as the per-projection
+path; the layers whose forward dequantization is split (qgroup.SPLIT_LAYERS) keep it.
+"""
+
+import os
+
+import torch
+
+from . import _ops  # noqa: F401 - registers torch.ops.talm.*
+from .engaged import FELL_BACK, RAN
+from .state import DISABLED, fallback
+
+GATE, UP, DOWN = 4, 5, 6
+ENABLED = os.environ.get("SOLUTION_DISABLE_FUSED_MLP") != "1"
+
+
+class FusedMLP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, group):
+        hidden = x.shape[-1]
+        x2 = x.reshape(-1, hidden)
+        if x2.stride(1) != 1:
+            x2 = x2.contiguous()
+        n_tok = x2.shape[0]
+        inter = group.shapes[GATE][0]
+        taken = 0
+        try:
+            w_gu = group.span("fwd", GATE, DOWN)
+            if w_gu is None:
+                raise RuntimeError("fused_mlp: gate and up are not one span of the layer")
+            taken = 2
+            gu = torch.empty(n_tok, 2 * inter, dtype=torch.float16, device=x.device)
+            torch.ops.talm.gemm(x2, w_gu[:inter], None, 1, gu[:, :inter])
+            torch.ops.talm.gemm(x2, w_gu[inter:], None, 1, gu[:, inter:])
+            del w_gu
+            w_down = group.span("fwd", DOWN, DOWN + 1)
+            if w_down is None:
+                raise RuntimeError("fused_mlp: down_proj is not a span of the layer")
+            taken = 3
+        except Exception:
+            if taken:
+                group.refund("fwd", taken)
+            raise
+        act = torch.empty(n_tok, inter, dtype=torch.float16, device=x.device)
+        torch.ops.talm.swiglu_fwd_rows(gu[:, :inter], gu[:, inter:], act)
+        y = torch.empty(n_tok, hidden, dtype=torch.float16, device=x.device)
+        torch.ops.talm.gemm(act, w_down, None, 1, y)
+        del act, w_down
+        ctx.save_for_backward(gu)
+        ctx.group, ctx.x_shape = group, x.shape
+        return y.view(*x.shape[:-1], hidden)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        (gu,) = ctx.saved_tensors
+        group = ctx.group
+        n_tok, inter = gu.shape[0], gu.shape[1] // 2
+        hidden = ctx.x_shape[-1]
+        dy = grad_out.reshape(n_tok, hidden)
+        if dy.dtype != torch.float16:
+            dy = dy.to(torch.float16)
+        if dy.stride(1) != 1:
+            dy = dy.contiguous()
+        w_down = group.weight("bwd", DOWN)
+        dact = torch.empty(n_tok, inter, dtype=torch.float16, device=dy.device)
+        torch.ops.talm.gemm(dy, w_down, None, 0, dact)
+        del w_down
+        gate, up = gu[:, :inter], gu[:, inter:]
+        torch.ops.talm.swiglu_bwd_rows(dact, gate, up, gate, up)
+        del dact
+        dx = torch.empty(n_tok, hidden, dtype=torch.float16, device=dy.device)
+        w_gu = group.span("bwd", GATE, DOWN)
+        if w_gu is not None:
+            w_gate, w_up = w_gu[:inter], w_gu[inter:]
+        else:  # split pass
+            w_gate, w_up = group.weight("bwd", GATE), group.weight("bwd", UP)
+        torch.ops.talm.gemm(gate, w_gate, None, 0, dx)
+        # dx += dup W_up in the column-major BLAS form: dx^T [H x N] += W_up^T [H x I] dup^T
+        torch.ops.talm.gemm_ex(w_up, 0, up, 0, dx, hidden, n_tok, inter, hidden, 2 * inter,
+                               hidden, 1)
+        return dx.view(ctx.x_shape), None
+
+
+def mlp_plan(mlp, x):
+    """The layer group when gate_proj, up_proj and down_proj are projections 4, 5, 6 of one
+    packed group (no LoRA, no hooks) and this forward pass dequantizes the whole layer."""
+    from .fused_proj import _no_hooks, _packed
+
+    if not ENABLED or not (x.is_cuda and x.dtype == torch.float16 and x.dim() >= 2) \
+            or "fused_mlp" in DISABLED or "qgroup" in DISABLED or "swiglu" in DISABLED:
+        return None
+    mods = [getattr(mlp, name, None) for name in ("gate_proj", "up_proj", "down_proj")]
+    if any(m is None for m in mods):
+        return None
+    tags = [_packed(m) for m in mods]
+    if any(t is None for t in tags) or tags[0][1] != GATE or tags[1][1] != UP or tags[2][1] != DOWN:
+        return None
+    group = tags[0][0]
+    if tags[1][0] is not group or tags[2][0] is not group or group.shapes[GATE][1] != x.shape[-1]:
+        return None
+    if any(group.biases[i] is not None for i in (GATE, UP, DOWN)):
+        return None
+    if not _no_hooks(mods + [mlp]) or group.split_now("fwd"):
+        return None
+    return group
+
+
+def fused_mlp_forward(mlp, x):
+    """FusedMLP when `mlp_plan` takes the layer, else None (the caller's own path runs)."""
+    group = mlp_plan(mlp, x)
+    if group is None:
+        return None
+    try:
+        y = FusedMLP.apply(x, group)
+    except Exception as exc:  # noqa: BLE001 - state.py convention
+        if not fallback("fused_mlp", exc):
+            raise
+        FELL_BACK["fused_mlp"] += 1
+        return None
+    if torch.is_grad_enabled() and x.requires_grad:
+        group.expected_bwd += 3
+    RAN["fused_mlp"] += 1
+    return y

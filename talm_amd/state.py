@@ -38,6 +38,7 @@ COMPONENTS = {
     "qkv_mfma": "q|k|v + LoRA + RoPE forward on MFMA -> the node's hipBLASLt GEMMs",
     "nf4_dequant": "per-projection NF4 dequantization kernel",
     "mlp_save_up": "opt-in MLP keeping only up and its input -> the MLP forward before it",
+    "fused_mlp": "the MLP as one node on the layer group -> the per-projection MLP",
 }
 
 

@@ -9,6 +9,7 @@ of the backward pass. Same kernels and arithmetic as swiglu.py, the same values.
 import torch
 
 from .engaged import FELL_BACK, ON, RAN
+from .fused_mlp import fused_mlp_forward
 from .state import DISABLED, fallback
 from .swiglu import activate, reference_grads, swiglu, swiglu_bwd, swiglu_fwd
 
@@ -38,8 +39,9 @@ class SwiGLUInPlaceGrad(torch.autograd.Function):
 
 
 def patch_qwen2_mlp_inplace():
-    """Qwen2MLP.forward through the in-place-backward node when gate and up are separate fresh
-    tensors of the same dtype (solution/swiglu_inplace.py:50-77)."""
+    """Qwen2MLP.forward as one FusedMLP node on a packed layer group (fused_mlp.py), else through
+    the in-place-backward node when gate and up are separate fresh tensors of the same dtype
+    (solution/swiglu_inplace.py:50-77)."""
     from transformers.models.qwen2 import modeling_qwen2
 
     from .patches import _in_chain
@@ -54,6 +56,9 @@ def patch_qwen2_mlp_inplace():
         if act != "silu" or not x.is_cuda or "swiglu" in DISABLED:
             FELL_BACK["swiglu_inplace"] += 1
             return previous(self, x)
+        y = fused_mlp_forward(self, x)
+        if y is not None:
+            return y
         gate, up = self.gate_proj(x), self.up_proj(x)
         if gate.dtype != up.dtype or gate.data_ptr() == up.data_ptr():
             FELL_BACK["swiglu_inplace"] += 1

@@ -285,6 +285,27 @@ def test_swiglu_config3_forward_backward_and_in_place():
     assert torch.equal(g3, out)
 
 
+def test_swiglu_rows_on_halves_equal_flat():
+    """The row-strided SwiGLU passes on the two halves of one [N, 2I] buffer (the fused MLP's
+    layout) give exactly the flat kernels' results (same arithmetic per element), in place too."""
+    _case("swiglu rows")
+    d = workloads.swiglu_inputs()
+    gate, up, grad = (d[k][:333].to(DEV) for k in ("gate", "up", "grad"))
+    inter = gate.shape[1]
+    gu = torch.cat([gate, up], 1)
+    out_flat = torch.empty_like(gate)
+    swiglu.swiglu_fwd(gate, up, out_flat)
+    out = torch.empty_like(gate)
+    torch.ops.talm.swiglu_fwd_rows(gu[:, :inter], gu[:, inter:], out)
+    assert torch.equal(out, out_flat)
+    dg, du = torch.empty_like(gate), torch.empty_like(up)
+    swiglu.swiglu_bwd(grad, gate, up, dg, du)
+    torch.ops.talm.swiglu_bwd_rows(grad, gu[:, :inter], gu[:, inter:], gu[:, :inter], gu[:, inter:])
+    assert torch.equal(gu[:, :inter], dg) and torch.equal(gu[:, inter:], du)
+    with pytest.raises(ValueError):  # columns must be whole 16-byte vectors
+        torch.ops.talm.swiglu_fwd_rows(gate[:, :12], up[:, :12], out[:, :12])
+
+
 @pytest.mark.parametrize("n", [1, 7, 8, 9, 1001, 4096 * 3 + 5])
 def test_swiglu_tails(n):
     _case(f"swiglu tail n={n}")

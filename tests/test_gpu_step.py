@@ -47,7 +47,7 @@ def test_patched_step_matches_eager_loss_curve(monkeypatch):
     fused = _run(True, 6, monkeypatch)
     for name in ("fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "rope",
                  "addnorm", "swiglu_inplace", "head", "varlen_attn", "attn_kernel",
-                 "attn_kernel_bwd"):
+                 "attn_kernel_bwd", "fused_mlp"):
         assert engaged.RAN[name] > 0, f"{name} did not run"
     assert abs(fused[0] - eager[0]) <= 1e-3 * abs(eager[0]), (fused[0], eager[0])
     for a, b in zip(fused, eager):
@@ -88,3 +88,46 @@ def test_varlen_attention_matches_per_row_sdpa():
     for a, b in ((out1, out2), (x1.grad, x2.grad)):
         torch.testing.assert_close(a.float(), b.float(), rtol=2 ** -10,
                                    atol=2 ** -10 * float(b.abs().max()))
+
+
+def test_fused_mlp_matches_per_projection_mlp(monkeypatch):
+    """FusedMLP (one node, feature-major activations, gate|up and their input gradient as single
+    GEMMs) against the per-projection path (GroupLinear x 3 + the in-place SwiGLU node) on the
+    same packed layer: output and input gradient within fp16 rounding, on a token count that is
+    not a multiple of 8 (the padded leading dimension), with the backward's whole-layer span and
+    its split form (two GEMMs, the second accumulating)."""
+    from talm_amd import fused_mlp, qgroup
+
+    print("[case] fused mlp vs per-projection mlp", flush=True)
+    config = qlora_model.qwen2_config(vocab_size=1000, hidden_size=512, intermediate_size=1024,
+                                      num_hidden_layers=3, num_attention_heads=4,
+                                      num_key_value_heads=2, head_dim=128)
+    model = qlora_model.build_model(config, seed=4)
+    layer = model.model.layers[0]
+    patches.apply()
+    try:
+        qgroup.setup_layer(layer)
+        group = layer._solution_layer_group
+        assert group is not None
+        g = torch.Generator("cpu").manual_seed(9)
+        x0 = torch.randn(1, 333, 512, generator=g).half().cuda()
+        dy = (torch.randn(1, 333, 512, generator=g) * 0.1).half().cuda()
+        results = []
+        for fused, split_bwd in ((False, False), (True, False), (True, True)):
+            monkeypatch.setattr(fused_mlp, "ENABLED", fused)
+            group.start_forward()
+            group.depth = 99
+            x = x0.clone().requires_grad_()
+            ran = engaged.RAN["fused_mlp"]
+            y = layer.mlp(x)
+            assert (engaged.RAN["fused_mlp"] > ran) == fused
+            if split_bwd:
+                group.depth = 0  # the backward dequantizes per projection
+            y.backward(dy)
+            results.append((y.detach().float(), x.grad.float()))
+        for y, dx in results[1:]:
+            torch.testing.assert_close(y, results[0][0], rtol=2e-3, atol=2e-3 * float(y.abs().max()))
+            torch.testing.assert_close(dx, results[0][1], rtol=2e-3,
+                                       atol=2e-3 * float(dx.abs().max()))
+    finally:
+        patches.unapply()
