@@ -4,8 +4,10 @@ Mirrors solution/qgroup.py: the seven 4-bit projections of a layer (q, k, v, o, 
 are packed into one contiguous set of buffers (the parameters become views of it, no memory is
 duplicated, :148-160) and dequantized by ONE launch when the layer's first projection runs, in
 the forward and in the backward; the other projections slice the cached fp16 buffer, which is
-dropped after its last expected use (`_take`, :273-289). The last layers (at the memory peak)
-dequantize projection by projection (`SPLIT_LAYERS`, :68-69, `dequantize_one`, :200-211).
+dropped after its last expected use (`_take`, :273-289). The reference dequantizes the last
+layers (at the memory peak) projection by projection (`SPLIT_LAYERS`, :68-69, `dequantize_one`,
+:200-211) to spare a T4's 16 GB one layer's fp16 buffer (94 MB for Qwen2.5-1.5B); with 288 GB
+of HBM that trade only costs launches, so here it is opt-in (SOLUTION_SPLIT_DEQUANT=1).
 
 The kernel (talm_nf4_group_dequant, talm_amd/csrc/nf4.hip) rebuilds each block's fp32 scale from
 the double-quantized absmax exactly as the reference kernel does (:72-91) and matches it bit for
@@ -28,8 +30,9 @@ from .state import DISABLED, fallback
 
 ROWS = 64  # the reference kernel's tile (rows of one program); kept as the packing granule
 NSEG = 7
-_SPLIT_OFF = os.environ.get("SOLUTION_DISABLE_SPLIT_DEQUANT") == "1"
-SPLIT_LAYERS = {"fwd": 0 if _SPLIT_OFF else 1, "bwd": 0 if _SPLIT_OFF else 2}
+_SPLIT_ON = os.environ.get("SOLUTION_SPLIT_DEQUANT") == "1" \
+    and os.environ.get("SOLUTION_DISABLE_SPLIT_DEQUANT") != "1"
+SPLIT_LAYERS = {"fwd": 1 if _SPLIT_ON else 0, "bwd": 2 if _SPLIT_ON else 0}
 PROJECTIONS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
                "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
 

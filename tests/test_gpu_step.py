@@ -39,15 +39,24 @@ def _run(patched, steps, monkeypatch):
     return losses
 
 
-def test_patched_step_matches_eager_loss_curve(monkeypatch):
-    print("[case] qlora step small model eager vs patched", flush=True)
+@pytest.mark.parametrize("split", [False, True])
+def test_patched_step_matches_eager_loss_curve(monkeypatch, split):
+    """With split, the last layers dequantize projection by projection (the reference's
+    memory-peak trade, opt-in here): their q|k|v and MLP nodes take the per-projection paths."""
+    from talm_amd import qgroup
+
+    print(f"[case] qlora step small model eager vs patched split={split}", flush=True)
+    if split:
+        monkeypatch.setattr(qgroup, "SPLIT_LAYERS", {"fwd": 1, "bwd": 2})
     engaged.reset()
     eager = _run(False, 6, monkeypatch)
     assert engaged.RAN["fused_head"] == 0
     fused = _run(True, 6, monkeypatch)
-    for name in ("fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "rope",
-                 "addnorm", "swiglu_inplace", "head", "varlen_attn", "attn_kernel",
-                 "attn_kernel_bwd", "fused_mlp"):
+    names = ["fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "addnorm",
+             "head", "varlen_attn", "attn_kernel", "attn_kernel_bwd", "fused_mlp"]
+    if split:  # the split last layer runs the per-projection MLP and the stand-alone RoPE
+        names += ["swiglu_inplace", "split", "rope"]
+    for name in names:
         assert engaged.RAN[name] > 0, f"{name} did not run"
     assert abs(fused[0] - eager[0]) <= 1e-3 * abs(eager[0]), (fused[0], eager[0])
     for a, b in zip(fused, eager):
@@ -99,6 +108,7 @@ def test_fused_mlp_matches_per_projection_mlp(monkeypatch):
     from talm_amd import fused_mlp, qgroup
 
     print("[case] fused mlp vs per-projection mlp", flush=True)
+    monkeypatch.setattr(qgroup, "SPLIT_LAYERS", {"fwd": 1, "bwd": 2})  # the reference's split
     config = qlora_model.qwen2_config(vocab_size=1000, hidden_size=512, intermediate_size=1024,
                                       num_hidden_layers=3, num_attention_heads=4,
                                       num_key_value_heads=2, head_dim=128)
