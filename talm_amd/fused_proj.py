@@ -399,10 +399,47 @@ def _packed(module):
     return getattr(module, "_solution_group", None)
 
 
+def _lora_state(attn):
+    """What can change between calls in the LoRA wrappers of q / k / v: adapter switches,
+    merging, the active adapter and its dropout's training flag and rate."""
+    from .lora import LoraLinear
+
+    state = []
+    for name in ("q_proj", "k_proj", "v_proj"):
+        module = getattr(attn, name, None)
+        if isinstance(module, LoraLinear):
+            adapters = tuple(module.active_adapters)
+            drop = module.lora_dropout[adapters[0]] if len(adapters) == 1 \
+                and adapters[0] in module.lora_dropout else None
+            state.append((module.disable_adapters, module.merged, adapters,
+                          getattr(drop, "training", None), getattr(drop, "p", None)))
+        else:
+            state.append(module)
+    return tuple(state)
+
+
 def qkv_plan(attn, x):
-    """(group, adapters, lora weights) when q_proj, k_proj and v_proj are projections 0, 1, 2 of
-    one packed layer group, each plain or a LoRA layer `lora_plan` takes, and this forward pass
-    dequantizes the whole layer; else None (solution/fused_proj.py:318-353)."""
+    """`qkv_plan_uncached` kept on the attention module for inputs of the same kind (device,
+    dtype, width, autocast, the set of disabled components and the LoRA wrappers' mutable state);
+    the per-call conditions (hooks, the pass's split decision) are checked every time."""
+    key = (x.is_cuda, x.dtype, x.dim() >= 2, x.shape[-1], torch.is_autocast_enabled("cuda"),
+           torch.get_autocast_dtype("cuda"), tuple(sorted(DISABLED)), _lora_state(attn))
+    cached = attn.__dict__.get("_talm_qkv_plan")
+    if cached is None or cached[0] != key:
+        plan = qkv_plan_uncached(attn, x)
+        modules = plan[3] if plan is not None else None
+        cached = (key, None if plan is None else plan[:3], modules)
+        attn.__dict__["_talm_qkv_plan"] = cached
+    plan, modules = cached[1], cached[2]
+    if plan is None or not _no_hooks(modules) or plan[0].split_now("fwd"):
+        return None
+    return plan
+
+
+def qkv_plan_uncached(attn, x):
+    """(group, adapters, lora weights, modules) when q_proj, k_proj and v_proj are projections
+    0, 1, 2 of one packed layer group, each plain or a LoRA layer `lora_plan` takes; else None
+    (solution/fused_proj.py:318-353). Hooks and the pass's split decision are the caller's."""
     from .lora import LoraLinear
 
     if not (x.is_cuda and x.dtype == torch.float16 and x.dim() >= 2) \
@@ -433,9 +470,7 @@ def qkv_plan(attn, x):
             return None
     if any(group.shapes[i][1] != x.shape[-1] for i in (Q, K, V)):
         return None
-    if not _no_hooks(modules) or group.split_now("fwd"):
-        return None
-    return group, tuple(adapters), weights
+    return group, tuple(adapters), weights, modules
 
 
 def _rope_ok(cos, sin, n_tok, head_dim):
@@ -474,7 +509,7 @@ def patch_qwen2_attention():
         rope = (cos[0] if cos.dim() == 3 else cos, sin[0] if sin.dim() == 3 else sin) \
             if hidden_states.shape[0] == 1 and _rope_ok(cos, sin, n_tok, self.head_dim) else None
         try:
-            q, k, v = FusedProjections.apply(hidden_states, group, Q, V + 1, adapters, (V - Q,),
+            q, k, v = FusedProjections.apply(hidden_states, group, Q, V + 1, adapters, (),
                                              rope, self.head_dim, *weights)
         except Exception as exc:  # noqa: BLE001 - state.py convention
             if not fallback("fused_proj", exc):
