@@ -303,16 +303,26 @@ def _mfma_backward(ctx, grads):
 
 
 def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
+    wanted = [ctx.needs_input_grad[8 + i] for i in range(2 * len(ctx.adapters))]
+    dx, lora_grads = _mfma_backward_core(grads, x2, rest, cos, sin, weight, ctx.sizes,
+                                         ctx.adapters, ctx.has_rope, wanted)
+    dx = None if dx is None else dx.view(ctx.x_shape)
+    return (dx, None, None, None, None, None, None, None, *lora_grads)
+
+
+def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_rope, wanted):
+    """dX [N, H] (None without `weight`) and the adapters' [dA, dB, ...] of the q|k|v node from
+    the gradients of its q, k, v outputs (fp16, unit column stride); `rest` holds (t, A16, B16)
+    per adapter, `wanted` which adapter gradients to form."""
     n_tok, size = x2.shape
     bounds = [0]
-    for s_ in ctx.sizes:
+    for s_ in sizes:
         bounds.append(bounds[-1] + s_)
     dys = [g.reshape(n_tok, -1) for g in grads]
     dcat = torch.empty(n_tok, bounds[-1], dtype=torch.float16, device=x2.device)
     torch.ops.talm.qkv_bwd_prep(dys[0], dys[1], dys[2], cos, sin, dcat)
-    if ctx.has_rope:
+    if has_rope:
         RAN["rope"] += 1
-    adapters = ctx.adapters
     halves = [rest[3 * k:3 * k + 3] for k in range(len(adapters))]  # (t, a16, b16)
     u = None
     if adapters:
@@ -336,14 +346,13 @@ def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
         torch.ops.talm.qkv_lora_bwd_dx(dcat, weight_t, u, a_t, dx)
         del weight_t
     lora_grads = [None] * (2 * len(adapters))
-    wanted = [ctx.needs_input_grad[8 + i] for i in range(2 * len(adapters))]
     if adapters and any(wanted):
         # all adapters' dA, dB in fp32 in one call (t of each adapter is a column view of one
         # [N, 16 * adapters] buffer when the forward ran on MFMA)
         t_all = halves[0][0]
         if len(adapters) > 1 and (halves[1][0].data_ptr() != t_all.data_ptr() + 32
                                   or halves[1][0].stride() != t_all.stride()):
-            return _weight_grads_ops(ctx, dcat, u, x2, halves, bounds, dx)
+            return dx, _weight_grads_ops(dcat, u, x2, halves, bounds, adapters, wanted)
         t_cat = torch.as_strided(t_all, (n_tok, 16 * len(adapters)), (t_all.stride(0), 1))
         segs = [(bounds[seg], bounds[seg + 1] - bounds[seg], s_) for seg, s_, _p in adapters]
         grads_ = [torch.empty(16, size, dtype=torch.float32, device=x2.device) if i % 2 == 0
@@ -357,8 +366,7 @@ def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
                                   grads_[2] if len(adapters) > 1 else None,
                                   grads_[3] if len(adapters) > 1 else None, ws)
         lora_grads = [g if w else None for g, w in zip(grads_, wanted)]
-    dx = None if dx is None else dx.view(ctx.x_shape)
-    return (dx, None, None, None, None, None, None, None, *lora_grads)
+    return dx, lora_grads
 
 
 def _ops_ws(n_tok, size, seg0, seg1):
@@ -367,19 +375,121 @@ def _ops_ws(n_tok, size, seg0, seg1):
     return _ops.lora_wgrad_workspace_bytes(n_tok, size, seg0, seg1)
 
 
-def _weight_grads_ops(ctx, dcat, u, x2, halves, bounds, dx):
+def _weight_grads_ops(dcat, u, x2, halves, bounds, adapters, wanted):
     """The adapters' dA / dB with the reference's ops (when their t are not one buffer)."""
     lora_grads = []
-    for k, (seg, scaling, _p) in enumerate(ctx.adapters):
+    for k, (seg, scaling, _p) in enumerate(adapters):
         t, _a16, _b16 = halves[k]
-        index = 8 + 2 * k
         uk = u[:, 16 * k:16 * (k + 1)]
-        lora_grads.append(torch.mm(uk.t(), x2).float() if ctx.needs_input_grad[index] else None)
+        lora_grads.append(torch.mm(uk.t(), x2).float() if wanted[2 * k] else None)
         dy = dcat[:, bounds[seg]:bounds[seg + 1]]
-        lora_grads.append(torch.mm((dy * scaling).t(), t).float()
-                          if ctx.needs_input_grad[index + 1] else None)
-    dx = None if dx is None else dx.view(ctx.x_shape)
-    return (dx, None, None, None, None, None, None, None, *lora_grads)
+        lora_grads.append(torch.mm((dy * scaling).t(), t).float() if wanted[2 * k + 1] else None)
+    return lora_grads
+
+
+class _NotApplicable(Exception):
+    """The one-node attention block does not take this call (nothing was consumed)."""
+
+
+class AttentionBlock(torch.autograd.Function):
+    """The whole attention half of a decoder layer as ONE node on MFMA: q|k|v (+ LoRA, + RoPE)
+    as in FusedProjections, the variable-length causal GQA attention of the packed rows
+    (torch.ops.talm.attn_fwd / attn_bwd) and o_proj on the layer group's weight
+    (solution/fused_proj.py:88-218 and :382-445, solution/unpad.py:199-294, solution/qgroup.py:
+    346-355). One node instead of FusedProjections + VarlenAttention + GroupLinear and the view
+    nodes between them: the step is bound by the host's launch rate. Same kernels, same values."""
+
+    @staticmethod
+    def forward(ctx, x, group, adapters, rope, head_dim, n_heads, n_kv, cu, max_len, scale,
+                *lora_weights):
+        x2 = x.reshape(-1, x.shape[-1])
+        n_tok = x2.shape[0]
+        sizes = [group.shapes[i][0] for i in (Q, K, V)]
+        bounds = [0, sizes[0], sizes[0] + sizes[1], sizes[0] + sizes[1] + sizes[2]]
+        weight = group.span("fwd", Q, V + 1)
+        if weight is None:
+            raise _NotApplicable()
+        halves = [_to_half(lora_weights[2 * k], lora_weights[2 * k + 1])
+                  for k in range(len(adapters))]
+        bias = group.span_bias(Q, V + 1)
+        if not (_mfma_ok(x2, weight, bias, bounds, adapters, halves, rope, head_dim)
+                and sizes[0] == n_heads * head_dim and sizes[1] == sizes[2] == n_kv * head_dim):
+            group.refund("fwd", V + 1 - Q)
+            raise _NotApplicable()
+        taken = V + 1 - Q
+        try:
+            out, t = _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope)
+            del weight
+            w_o = group.weight("fwd", O)
+            taken += 1
+            q = out[:, :bounds[1]].view(n_tok, n_heads, head_dim)
+            k = out[:, bounds[1]:bounds[2]].view(n_tok, n_kv, head_dim)
+            v = out[:, bounds[2]:].view(n_tok, n_kv, head_dim)
+            o = torch.empty(n_tok, n_heads, head_dim, dtype=torch.float16, device=x.device)
+            lse = torch.empty(n_heads, n_tok, dtype=torch.float32, device=x.device)
+            torch.ops.talm.attn_fwd(q, k, v, cu, max_len, scale, o, lse)
+            y = torch.empty(n_tok, w_o.shape[0], dtype=torch.float16, device=x.device)
+            torch.ops.talm.gemm(o.view(n_tok, -1), w_o, group.biases[O], 1, y)
+            del w_o
+        except Exception:
+            group.refund("fwd", taken)  # the per-node path takes them again
+            raise
+        saved = [x2, out, o, lse, cu]
+        for k_ in range(len(adapters)):
+            saved += [t[:, 16 * k_:16 * (k_ + 1)], halves[k_][0], halves[k_][1]]
+        saved += list(rope)
+        ctx.save_for_backward(*saved)
+        ctx.group, ctx.adapters, ctx.sizes, ctx.bounds = group, adapters, sizes, bounds
+        ctx.head_dim, ctx.n_heads, ctx.n_kv = head_dim, n_heads, n_kv
+        ctx.max_len, ctx.scale, ctx.x_shape = max_len, scale, x.shape
+        RAN["qkv_mfma"] += 1
+        RAN["rope"] += 1
+        RAN["attn_kernel"] += 1
+        return y.view(*x.shape[:-1], y.shape[1])
+
+    @staticmethod
+    def backward(ctx, grad):
+        from . import _ops
+
+        x2, out, o, lse, cu, *rest = ctx.saved_tensors
+        cos, sin = rest[-2:]
+        rest = rest[:-2]
+        group, bounds = ctx.group, ctx.bounds
+        n_tok = x2.shape[0]
+        dy = grad.reshape(n_tok, -1)
+        if dy.dtype != torch.float16:
+            dy = dy.to(torch.float16)
+        if dy.stride(1) != 1:
+            dy = dy.contiguous()
+        w_o = group.weight("bwd", O)
+        d_o = torch.empty(n_tok, w_o.shape[1], dtype=torch.float16, device=x2.device)
+        torch.ops.talm.gemm(dy, w_o, None, 0, d_o)
+        del w_o
+        hd, nh, nkv = ctx.head_dim, ctx.n_heads, ctx.n_kv
+        q = out[:, :bounds[1]].view(n_tok, nh, hd)
+        k = out[:, bounds[1]:bounds[2]].view(n_tok, nkv, hd)
+        v = out[:, bounds[2]:].view(n_tok, nkv, hd)
+        dqkv = torch.empty(n_tok, bounds[3], dtype=torch.float16, device=x2.device)
+        dq = dqkv[:, :bounds[1]]
+        dk = dqkv[:, bounds[1]:bounds[2]]
+        dv = dqkv[:, bounds[2]:]
+        ws = torch.empty(_ops.attn_bwd_workspace_bytes(n_tok, nh), dtype=torch.uint8,
+                         device=x2.device)
+        torch.ops.talm.attn_bwd(q, k, v, o, d_o.view(n_tok, nh, hd), lse, cu, ctx.max_len,
+                                ctx.scale, dq.view(n_tok, nh, hd), dk.view(n_tok, nkv, hd),
+                                dv.view(n_tok, nkv, hd), ws)
+        del ws, d_o
+        weight = group.span("bwd", Q, V + 1) if ctx.needs_input_grad[0] else None
+        wanted = [ctx.needs_input_grad[10 + i] for i in range(2 * len(ctx.adapters))]
+        if weight is None and ctx.needs_input_grad[0]:
+            weights = [group.weight("bwd", i) for i in (Q, K, V)]
+            weight = torch.cat(weights, 0)
+        dx, lora_grads = _mfma_backward_core((dq, dk, dv), x2, rest, cos, sin, weight,
+                                             ctx.sizes, ctx.adapters, True, wanted)
+        RAN["attn_kernel_bwd"] += 1
+        RAN["qkv_mfma_bwd"] += 1
+        dx = None if dx is None else dx.view(ctx.x_shape)
+        return (dx, None, None, None, None, None, None, None, None, None, *lora_grads)
 
 
 _HOOK_DICTS = ("_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks")
@@ -479,6 +589,64 @@ def _rope_ok(cos, sin, n_tok, head_dim):
             and cos.stride(-1) == 1 and sin.stride(-1) == 1 and "rope" not in DISABLED)
 
 
+ATTN_BLOCK = os.environ.get("SOLUTION_DISABLE_ATTN_BLOCK") != "1"
+
+
+def _rows_attention(cfg):
+    """The model's attention is the registered "sdpa" interface wrapped for packed rows (the
+    semantics the block restates)."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    if getattr(cfg, "_attn_implementation", None) != "sdpa":
+        return False
+    try:
+        return bool(getattr(ALL_ATTENTION_FUNCTIONS["sdpa"], "_solution_rows", False))
+    except KeyError:
+        return False
+
+
+def _attention_block(attn, x, group, adapters, weights, rope, n_tok):
+    """The layer's attention as one AttentionBlock node when the packed-rows context provides
+    cu_seqlens, the rotary embedding goes in place, o_proj is the group's plain projection and
+    the heads suit the attention kernel; else None (the per-node path runs)."""
+    from . import unpad
+    from .qgroup import _linear4bit
+
+    if not ATTN_BLOCK or "attn_block" in DISABLED or rope is None or not unpad._cu \
+            or unpad._cu[-1] is None or "varlen_attention" in DISABLED:
+        return None
+    cu, max_len, total = unpad._cu[-1]
+    dropout = 0.0 if not attn.training else attn.attention_dropout
+    o_proj = getattr(attn, "o_proj", None)
+    tag = _packed(o_proj) if o_proj is not None else None
+    cfg = attn.config
+    n_heads = getattr(cfg, "num_attention_heads", None)
+    n_kv = getattr(cfg, "num_key_value_heads", None)
+    if total != n_tok or dropout != 0.0 or attn.sliding_window is not None or tag is None \
+            or tag[0] is not group or tag[1] != O or _linear4bit(o_proj) is not o_proj \
+            or attn.head_dim != 128 or not n_heads or not n_kv or n_heads % n_kv \
+            or not _no_hooks([o_proj]) or not _rows_attention(cfg):
+        return None
+    try:
+        y = AttentionBlock.apply(x, group, adapters, rope, attn.head_dim, n_heads, n_kv, cu,
+                                 max_len, attn.scaling, *weights)
+    except _NotApplicable:
+        return None
+    except Exception as exc:  # noqa: BLE001 - state.py convention
+        if not fallback("attn_block", exc):
+            raise
+        return None
+    if torch.is_grad_enabled():
+        # the backward takes o_proj's weight whenever it runs, q|k|v's only for dX
+        group.expected_bwd += 3 * x.requires_grad + (
+            x.requires_grad or any(w.requires_grad for w in weights))
+    COUNTS["attn"] += 1
+    RAN["fused_proj"] += 1
+    RAN["varlen_attn"] += 1
+    RAN["attn_block"] += 1
+    return y
+
+
 def patch_qwen2_attention():
     """`Qwen2Attention.forward` with q|k|v (+ LoRA, + RoPE in place) as one FusedProjections
     node when `qkv_plan` takes the layer; transformers' own forward otherwise
@@ -508,6 +676,9 @@ def patch_qwen2_attention():
         n_tok = hidden_states.numel() // hidden_states.shape[-1]
         rope = (cos[0] if cos.dim() == 3 else cos, sin[0] if sin.dim() == 3 else sin) \
             if hidden_states.shape[0] == 1 and _rope_ok(cos, sin, n_tok, self.head_dim) else None
+        y = _attention_block(self, hidden_states, group, adapters, weights, rope, n_tok)
+        if y is not None:
+            return y, None
         try:
             q, k, v = FusedProjections.apply(hidden_states, group, Q, V + 1, adapters, (),
                                              rope, self.head_dim, *weights)

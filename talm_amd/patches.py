@@ -14,7 +14,7 @@ the original code outside the exact situation it was written for. Installed here
   the causal LM (fused_head.py, `patch_qwen2_causal_lm` below).
 
 Switches: SOLUTION_DISABLE_<PART>=1 leaves a part out (RMSNORM, ADDNORM, ROPE, SWIGLU_INPLACE,
-GROUP, LORA, FUSED_PROJ, FUSED_HEAD, UNPAD, FUSED_MLP), as in the reference
+GROUP, LORA, FUSED_PROJ, FUSED_HEAD, UNPAD, FUSED_MLP, ATTN_BLOCK), as in the reference
 (solution/__init__.py:51-84).
 """
 

@@ -39,6 +39,7 @@ COMPONENTS = {
     "nf4_dequant": "per-projection NF4 dequantization kernel",
     "mlp_save_up": "opt-in MLP keeping only up and its input -> the MLP forward before it",
     "fused_mlp": "the MLP as one node on the layer group -> the per-projection MLP",
+    "attn_block": "q|k|v, attention and o_proj as one node -> the per-node attention",
 }
 
 

@@ -53,7 +53,7 @@ def test_patched_step_matches_eager_loss_curve(monkeypatch, split):
     assert engaged.RAN["fused_head"] == 0
     fused = _run(True, 6, monkeypatch)
     names = ["fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "addnorm",
-             "head", "varlen_attn", "attn_kernel", "attn_kernel_bwd", "fused_mlp"]
+             "head", "varlen_attn", "attn_kernel", "attn_kernel_bwd", "fused_mlp", "attn_block"]
     if split:  # the split last layer runs the per-projection MLP and the stand-alone RoPE
         names += ["swiglu_inplace", "split", "rope"]
     for name in names:
@@ -139,5 +139,67 @@ def test_fused_mlp_matches_per_projection_mlp(monkeypatch):
             torch.testing.assert_close(y, results[0][0], rtol=2e-3, atol=2e-3 * float(y.abs().max()))
             torch.testing.assert_close(dx, results[0][1], rtol=2e-3,
                                        atol=2e-3 * float(dx.abs().max()))
+    finally:
+        patches.unapply()
+
+
+def test_attention_block_matches_per_node_attention(monkeypatch):
+    """AttentionBlock (q|k|v + LoRA + RoPE, the packed rows' attention and o_proj as one node)
+    against the per-node path (FusedProjections, VarlenAttention, GroupLinear) on one packed
+    layer with ragged rows (one of a single token): output, input gradient and the LoRA
+    gradients within fp16 rounding, with the backward's whole-layer span and with the backward
+    dequantizing per projection."""
+    from talm_amd import fused_proj, qgroup, unpad
+
+    print("[case] attention block vs per-node attention", flush=True)
+    monkeypatch.setattr(qgroup, "SPLIT_LAYERS", {"fwd": 1, "bwd": 2})
+    config = qlora_model.qwen2_config(vocab_size=1000, hidden_size=512, intermediate_size=1024,
+                                      num_hidden_layers=3, num_attention_heads=4,
+                                      num_key_value_heads=2, head_dim=128)
+    model = qlora_model.build_model(config, seed=6)
+    layer = model.model.layers[0]
+    attn = layer.self_attn
+    lora = [p for p in attn.parameters() if p.requires_grad]
+    assert len(lora) == 4
+    with torch.no_grad():
+        for p in lora:
+            if p.abs().sum() == 0:
+                p.normal_(0, 0.02)
+    patches.apply()
+    try:
+        qgroup.setup_layer(layer)
+        group = layer._solution_layer_group
+        assert group is not None
+        lengths = [120, 77, 1, 135]
+        bounds, start = [], 0
+        for n in lengths:
+            bounds.append((start, start + n))
+            start += n
+        positions = torch.cat([torch.arange(n) for n in lengths])[None].cuda()
+        g = torch.Generator("cpu").manual_seed(11)
+        x0 = torch.randn(1, start, 512, generator=g).half().cuda()
+        dy = (torch.randn(1, start, 512, generator=g) * 0.1).half().cuda()
+        cos, sin = model.model.rotary_emb(x0.float(), positions)
+        results = []
+        for block, split_bwd in ((False, False), (True, False), (True, True)):
+            monkeypatch.setattr(fused_proj, "ATTN_BLOCK", block)
+            group.start_forward()
+            group.depth = 99
+            x = x0.clone().requires_grad_()
+            for p in lora:
+                p.grad = None
+            ran, fused = engaged.RAN["attn_block"], engaged.RAN["fused_proj"]
+            with unpad.rows_context(bounds, device=x.device), \
+                    torch.autocast("cuda", dtype=torch.float16):
+                y, _ = attn(x, position_embeddings=(cos, sin), attention_mask=None)
+            assert (engaged.RAN["attn_block"] > ran) == block
+            assert engaged.RAN["fused_proj"] > fused
+            if split_bwd:
+                group.depth = 0  # the backward dequantizes per projection
+            y.backward(dy)
+            results.append([y.detach().float(), x.grad.float()] + [p.grad.float() for p in lora])
+        for other in results[1:]:
+            for a, b in zip(other, results[0]):
+                torch.testing.assert_close(a, b, rtol=2e-3, atol=2e-3 * float(b.abs().max()))
     finally:
         patches.unapply()
