@@ -33,6 +33,9 @@ namespace talm {
 namespace {
 
 typedef uint16_t half4_t __attribute__((ext_vector_type(4)));
+// 16-byte register chunks as a native vector: HIP's uint4 struct is copied with memcpy, which
+// keeps a register array of them on the stack when it is stored whole into LDS.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;         // head dim
 constexpr int kKeys = 64;       // keys per tile
@@ -41,6 +44,35 @@ constexpr int kVS = kKeys + 4;  // row stride (halfs) of a transposed [D][keys] 
 constexpr float kLn2 = 0.693147180559945309f;
 
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The tile loop of every kernel below: n tiles through registers into a two-slot LDS ring, the
+// global loads two tiles ahead of the tile being computed (register slot = LDS slot = tile & 1,
+// unrolled by two so both stay static). load(slot, tile) fills a slot's registers,
+// store(slot) writes them to that LDS slot, compute(tile, slot) consumes it. The loads are
+// unconditional (clamped to the last tile): a conditional one makes the compiler wait for it.
+// The barrier only waits for LDS (lgkmcnt): the loads stay in flight across it.
+template <class Load, class Store, class Compute>
+__device__ __forceinline__ void tile_pipeline(int n, Load&& load, Store&& store,
+                                              Compute&& compute) {
+  load(0, 0);
+  load(1, min(1, n - 1));
+  int t = 0;
+  for (; t + 1 < n; t += 2) {
+    store(0);
+    load(0, min(t + 2, n - 1));
+    __syncthreads();
+    compute(t, 0);
+    store(1);
+    load(1, min(t + 3, n - 1));
+    __syncthreads();
+    compute(t + 1, 1);
+  }
+  if (t < n) {
+    store(0);
+    __syncthreads();
+    compute(t, 0);
+  }
+}
 
 struct FwdArgs {
   const uint16_t* q;
@@ -94,21 +126,21 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
   // tile loads: chunk c = p * 64W + tid -> key c % 64, column chunk c / 64 (for V: 64 lanes
   // of a wavefront read 64 keys of one 8-column chunk, so the transposed LDS writes of one
   // instruction fill one row of vt)
-  uint4 kreg[kPer], vreg[kPer];
-  auto load_tile = [&](int kt) {
+  u32x4 kreg[2][kPer], vreg[2][kPer];
+  auto load_tile = [&](int slot, int kt) {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int c = p * 64 * W + tid, key = min(kt * kKeys + (c & 63), len - 1), cc = c >> 6;
-      kreg[p] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
-      vreg[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
+      kreg[slot][p] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
+      vreg[slot][p] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int c = p * 64 * W + tid, key = c & 63, cc = c >> 6;
-      *reinterpret_cast<uint4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[p];
-      const uint32_t w4[4] = {vreg[p].x, vreg[p].y, vreg[p].z, vreg[p].w};
+      *reinterpret_cast<u32x4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[buf][p];
+      const uint32_t w4[4] = {vreg[buf][p].x, vreg[buf][p].y, vreg[buf][p].z, vreg[buf][p].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         vt[buf][(8 * cc + 2 * e) * kVS + key] = static_cast<uint16_t>(w4[e] & 0xffffu);
@@ -124,12 +156,7 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
     for (int v = 0; v < 16; ++v) o[j][v] = 0.f;
   float m = -INFINITY, lsum = 0.f;
 
-  load_tile(0);
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int buf = kt & 1;
-    store_tile(buf);
-    if (kt + 1 < n_kt) load_tile(kt + 1);
-    __syncthreads();
+  auto compute = [&](int kt, int buf) {
     const int k0 = kt * kKeys;
     // S^T for keys k0 + 32 b + (8 (v / 4) + 4 hh + v % 4), this lane's query column
     f32x16 st[2];
@@ -190,7 +217,8 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
           o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[j], 0, 0, 0);
         }
       }
-  }
+  };
+  tile_pipeline(n_kt, load_tile, store_tile, compute);
 
   // O = O^T / l through LDS: each wavefront stages its 32 rows x D, then 16-byte row stores
   const float l_tot = lsum + __shfl_xor(lsum, 32, kWave);
@@ -215,8 +243,8 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
     const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
     const int row = q0 + 32 * wave + r;
     if (row < len)
-      *reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(s0 + row) * a.o_tok + head * a.o_head + 8 * cc) =
-          *reinterpret_cast<const uint4*>(&os[r * kKS + 8 * cc]);
+      *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(s0 + row) * a.o_tok + head * a.o_head + 8 * cc) =
+          *reinterpret_cast<const u32x4*>(&os[r * kKS + 8 * cc]);
   }
 }
 
@@ -259,8 +287,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(BwdArgs a) {
   const int64_t r = row < rows ? row : rows - 1;
   const int64_t t = r / a.n_q_heads;
   const int h = static_cast<int>(r % a.n_q_heads);
-  const uint4 x = *reinterpret_cast<const uint4*>(a.o + t * a.o_tok + h * a.o_head + 8 * sub);
-  const uint4 y = *reinterpret_cast<const uint4*>(a.dout + t * a.do_tok + h * a.do_head + 8 * sub);
+  const u32x4 x = *reinterpret_cast<const u32x4*>(a.o + t * a.o_tok + h * a.o_head + 8 * sub);
+  const u32x4 y = *reinterpret_cast<const u32x4*>(a.dout + t * a.do_tok + h * a.do_head + 8 * sub);
   float acc = lo_f(x.x) * lo_f(y.x) + hi_f(x.x) * hi_f(y.x) + lo_f(x.y) * lo_f(y.y) +
               hi_f(x.y) * hi_f(y.y) + lo_f(x.z) * lo_f(y.z) + hi_f(x.z) * hi_f(y.z) +
               lo_f(x.w) * lo_f(y.w) + hi_f(x.w) * hi_f(y.w);
@@ -305,22 +333,22 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dq_kernel(BwdArgs a) {
   const int n_kt = (kend + kKeys - 1) / kKeys;
   const uint16_t* kbase = a.k + static_cast<int64_t>(s0) * a.k_tok + kvh * a.k_head;
   const uint16_t* vbase = a.v + static_cast<int64_t>(s0) * a.v_tok + kvh * a.v_head;
-  uint4 kreg[kPer], vreg[kPer];
-  auto load_tile = [&](int kt) {
+  u32x4 kreg[2][kPer], vreg[2][kPer];
+  auto load_tile = [&](int slot, int kt) {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int c = p * 64 * W + tid, key = min(kt * kKeys + (c & 63), len - 1), cc = c >> 6;
-      kreg[p] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
-      vreg[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
+      kreg[slot][p] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
+      vreg[slot][p] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int c = p * 64 * W + tid, key = c & 63, cc = c >> 6;
-      *reinterpret_cast<uint4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[p];
-      *reinterpret_cast<uint4*>(&vs[buf][key * kKS + 8 * cc]) = vreg[p];
-      const uint32_t w4[4] = {kreg[p].x, kreg[p].y, kreg[p].z, kreg[p].w};
+      *reinterpret_cast<u32x4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[buf][p];
+      *reinterpret_cast<u32x4*>(&vs[buf][key * kKS + 8 * cc]) = vreg[buf][p];
+      const uint32_t w4[4] = {kreg[buf][p].x, kreg[buf][p].y, kreg[buf][p].z, kreg[buf][p].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         kts[buf][(8 * cc + 2 * e) * kVS + key] = static_cast<uint16_t>(w4[e] & 0xffffu);
@@ -335,12 +363,7 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
 
-  load_tile(0);
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int buf = kt & 1;
-    store_tile(buf);
-    if (kt + 1 < n_kt) load_tile(kt + 1);
-    __syncthreads();
+  auto compute = [&](int kt, int buf) {
     const int k0 = kt * kKeys;
     f32x16 st[2], dpt[2];
 #pragma unroll
@@ -385,7 +408,8 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dq_kernel(BwdArgs a) {
           acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, sb, acc[j], 0, 0, 0);
         }
       }
-  }
+  };
+  tile_pipeline(n_kt, load_tile, store_tile, compute);
 
   __syncthreads();
   uint16_t* os = &ks[0][0] + wave * 32 * kKS;
@@ -405,8 +429,8 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dq_kernel(BwdArgs a) {
     const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
     const int row = q0 + 32 * wave + r;
     if (row < len)
-      *reinterpret_cast<uint4*>(a.dq + static_cast<int64_t>(s0 + row) * a.dq_tok + head * a.dq_head + 8 * cc) =
-          *reinterpret_cast<const uint4*>(&os[r * kKS + 8 * cc]);
+      *reinterpret_cast<u32x4*>(a.dq + static_cast<int64_t>(s0 + row) * a.dq_tok + head * a.dq_head + 8 * cc) =
+          *reinterpret_cast<const u32x4*>(&os[r * kKS + 8 * cc]);
   }
 }
 
@@ -452,30 +476,28 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
   const float* lrow = a.lse + static_cast<int64_t>(head) * a.n_tokens + s0;
   const float* drow = a.dd + static_cast<int64_t>(head) * a.n_tokens + s0;
   // chunk c = p * 64W + tid -> query row c % 32, column chunk c / 32
-  uint4 qreg[kPer], dreg[kPer];
-  float lreg = 0.f, dreg1 = 0.f;
-  auto load_tile = [&](int qt) {
+  u32x4 qreg[2][kPer], dreg[2][kPer];
+  float lreg[2], dreg1[2];
+  auto load_tile = [&](int slot, int qt) {
     const int r0 = qstart + qt * kQT;
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int c = p * 64 * W + tid, row = min(r0 + (c & 31), len - 1), cc = c >> 5;
-      qreg[p] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(row) * a.q_tok + 8 * cc);
-      dreg[p] = *reinterpret_cast<const uint4*>(dbase + static_cast<int64_t>(row) * a.do_tok + 8 * cc);
+      qreg[slot][p] = *reinterpret_cast<const u32x4*>(qbase + static_cast<int64_t>(row) * a.q_tok + 8 * cc);
+      dreg[slot][p] = *reinterpret_cast<const u32x4*>(dbase + static_cast<int64_t>(row) * a.do_tok + 8 * cc);
     }
-    if (tid < kQT) {
-      const int row = min(r0 + tid, len - 1);
-      lreg = lrow[row] * 1.44269504088896341f;
-      dreg1 = drow[row];
-    }
+    const int row = min(r0 + (tid & (kQT - 1)), len - 1);  // every thread: no branch
+    lreg[slot] = lrow[row] * 1.44269504088896341f;
+    dreg1[slot] = drow[row];
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       const int c = p * 64 * W + tid, row = c & 31, cc = c >> 5;
-      *reinterpret_cast<uint4*>(&qs[buf][row * kKS + 8 * cc]) = qreg[p];
-      *reinterpret_cast<uint4*>(&ds[buf][row * kKS + 8 * cc]) = dreg[p];
-      const uint32_t q4[4] = {qreg[p].x, qreg[p].y, qreg[p].z, qreg[p].w};
-      const uint32_t d4[4] = {dreg[p].x, dreg[p].y, dreg[p].z, dreg[p].w};
+      *reinterpret_cast<u32x4*>(&qs[buf][row * kKS + 8 * cc]) = qreg[buf][p];
+      *reinterpret_cast<u32x4*>(&ds[buf][row * kKS + 8 * cc]) = dreg[buf][p];
+      const uint32_t q4[4] = {qreg[buf][p].x, qreg[buf][p].y, qreg[buf][p].z, qreg[buf][p].w};
+      const uint32_t d4[4] = {dreg[buf][p].x, dreg[buf][p].y, dreg[buf][p].z, dreg[buf][p].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         qts[buf][(8 * cc + 2 * e) * kQS + row] = static_cast<uint16_t>(q4[e] & 0xffffu);
@@ -485,8 +507,8 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
       }
     }
     if (tid < kQT) {
-      ls[buf][tid] = lreg;
-      dds[buf][tid] = dreg1;
+      ls[buf][tid] = lreg[buf];
+      dds[buf][tid] = dreg1[buf];
     }
   };
 
@@ -496,12 +518,7 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) dka[j][v] = dva[j][v] = 0.f;
 
-  load_tile(0);
-  for (int qt = 0; qt < n_qt; ++qt) {
-    const int buf = qt & 1;
-    store_tile(buf);
-    if (qt + 1 < n_qt) load_tile(qt + 1);
-    __syncthreads();
+  auto compute = [&](int qt, int buf) {
     const int r0 = qstart + qt * kQT;
     // S[q][key], dP[q][key]: rows q = 8 (v / 4) + 4 hh + v % 4 of the tile, column = this key
     f32x16 sc, dp;
@@ -559,7 +576,8 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
         dka[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, sb, dka[j], 0, 0, 0);
       }
     }
-  }
+  };
+  tile_pipeline(n_qt, load_tile, store_tile, compute);
 
   // fp32 partials [head][token][d]: lane = key column, rows d = 32 j + 8 (v / 4) + 4 hh + v % 4
   if (key < len) {
