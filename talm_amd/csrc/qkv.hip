@@ -142,7 +142,9 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
 // ------------------------------------------------------------------------------------------
 // out = [x | ts] [W | B]^T + bias, rotary embedding on the columns below rope_cols.
 // ------------------------------------------------------------------------------------------
-using QkvShape = TileShape<128, 128, 64, 2, 2, 2>;  // 4 wavefronts of 64 x 64, 64 KiB ring
+// 8 wavefronts of 32 x 64 (two per SIMD) and a 3-slot ring (96 KiB): the token count gives few
+// 128-row tiles, so each CU's tile must keep its L2 -> LDS stream busy on its own.
+using QkvShape = TileShape<128, 128, 64, 3, 4, 2>;
 constexpr int kQZS = 128 + 8;                       // staged tile row stride (halfs)
 static_assert(128 * kQZS * 2 <= QkvShape::kRing, "the staged tile reuses the ring");
 
