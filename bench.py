@@ -240,7 +240,7 @@ def step_workload(args):
     for mode in ("patched", "eager") if not args.no_eager else ("patched",):
         torch.cuda.empty_cache()
         model = qlora_model.build_model(seed=1)
-        trainer = qlora_model.Trainer(model, steps=n_steps)
+        trainer = qlora_model.Trainer(model, steps=n_steps, fused_adapters=mode == "patched")
         if mode == "patched":
             patches.apply()
             engaged.reset()

@@ -289,6 +289,37 @@ int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head
                   int64_t dv_stride_head, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/*
+ * fp16 copies of the LoRA adapters' fp32 weights, every adapter in one launch. `table` (device
+ * memory, int64, 8-byte aligned) holds 9 entries per tensor: the fp32 weight's address (a
+ * row-major contiguous [rows, cols] matrix), its element count, its column count, the element
+ * offset of its fp16 copy in `out` (-1: none), the element offset of a transposed fp16 copy in
+ * `out` (-1: none; out[t_off + c * ld_t + r] = fp16(w[r, c])), that copy's row stride ld_t, and
+ * three optimizer addresses (gradient, first and second moment, fp32, same layout as the weight;
+ * unused here). Conversions round to nearest even (as .to(float16)). max_numel bounds every
+ * element count; n_tensors <= 65535. Replaces the adapters' fp16 casts, one foreach copy per
+ * refresh (solution/lora.py:57-137), and the q|k|v backward's concatenation and transposition of
+ * the two A matrices (solution/fused_proj.py:202-209 forms u A per adapter instead).
+ */
+int talm_lora_mirror(const int64_t* table, int32_t n_tensors, int64_t max_numel, uint16_t* out,
+                     void* stream);
+
+/*
+ * One AdamW step (decoupled weight decay, bias-corrected moments: w -= lr*wd*w; m = b1 m +
+ * (1-b1) g; v = b2 v + (1-b2) g^2; w -= lr/(1-b1^t) * m / (sqrt(v)/sqrt(1-b2^t) + eps)) of every
+ * tensor in `table` (layout above, optimizer addresses required), then the same fp16 copies as
+ * talm_lora_mirror of the updated weights. t = *step_in + 1 (device fp32); one thread writes
+ * *step_out (a different address): t, or *step_in when *found_inf is nonzero — then no weight or
+ * moment changes (the copies are still written). grad_scale (device fp32, may be NULL) divides
+ * the gradients; found_inf may be NULL. Replaces torch.optim.AdamW(fused=True) on the LoRA
+ * parameters plus the next forward's fp16 casts (solution/lora.py:57-137): the scale and inf
+ * flag of torch.amp.GradScaler are taken on the device, as by PyTorch's fused optimizers.
+ */
+int talm_lora_adamw(const int64_t* table, int32_t n_tensors, int64_t max_numel, float lr,
+                    float beta1, float beta2, float eps, float weight_decay, const float* step_in,
+                    float* step_out, const float* grad_scale, const float* found_inf,
+                    uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -530,6 +530,49 @@ void attn_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& o
 }
 
 // ------------------------------------------------------------------------------------------
+// LoRA adapters: fp16 copies and the fused AdamW step over a device table (9 int64 per tensor,
+// layout in include/talm.h; the addresses in it are the caller's to keep alive).
+// ------------------------------------------------------------------------------------------
+void adapter_table(const Tensor& table, int64_t n_tensors, const Tensor& out, const char* what) {
+  TORCH_CHECK_VALUE(table.is_cuda() && table.scalar_type() == at::kLong && table.is_contiguous() &&
+                        table.numel() >= 9 * n_tensors && out.device() == table.device(),
+                    what, ": table int64 [n_tensors, 9] on the copies' device");
+  require_fp16(out, "out");
+  require(out.is_contiguous(), "lora adapters: out must be contiguous");
+}
+
+void lora_mirror(const Tensor& table, int64_t n_tensors, int64_t max_numel, const Tensor& out) {
+  adapter_table(table, n_tensors, out, "lora_mirror");
+  check(talm_lora_mirror(as<int64_t>(table), static_cast<int32_t>(n_tensors), max_numel,
+                         as<uint16_t>(out), stream_of(out)),
+        "lora_mirror");
+}
+
+void lora_adamw(const Tensor& table, int64_t n_tensors, int64_t max_numel, double lr,
+                double beta1, double beta2, double eps, double weight_decay,
+                const Tensor& step_in, const Tensor& step_out, const OptTensor& grad_scale,
+                const OptTensor& found_inf, const Tensor& out) {
+  adapter_table(table, n_tensors, out, "lora_adamw");
+  for (const Tensor* t : {&step_in, &step_out})
+    require(t->is_cuda() && t->scalar_type() == at::kFloat && t->numel() == 1 &&
+                t->device() == out.device(),
+            "lora_adamw: step counters float32 [1] on the copies' device");
+  require(step_in.data_ptr() != step_out.data_ptr(), "lora_adamw: step_in and step_out alias");
+  for (const OptTensor* t : {&grad_scale, &found_inf})
+    if (t->has_value())
+      require((*t)->is_cuda() && (*t)->scalar_type() == at::kFloat && (*t)->numel() == 1 &&
+                  (*t)->device() == out.device(),
+              "lora_adamw: grad_scale / found_inf float32 [1] on the copies' device");
+  check(talm_lora_adamw(as<int64_t>(table), static_cast<int32_t>(n_tensors), max_numel,
+                        static_cast<float>(lr), static_cast<float>(beta1),
+                        static_cast<float>(beta2), static_cast<float>(eps),
+                        static_cast<float>(weight_decay), as<float>(step_in),
+                        as<float>(step_out), as<float>(grad_scale), as<float>(found_inf),
+                        as<uint16_t>(out), stream_of(out)),
+        "lora_adamw");
+}
+
+// ------------------------------------------------------------------------------------------
 // Plain fp16 GEMMs on hipBLASLt with cached plans.
 // ------------------------------------------------------------------------------------------
 struct GemmKey {
@@ -754,6 +797,10 @@ TORCH_LIBRARY(talm, m) {
   m.def("attn_bwd(Tensor q, Tensor k, Tensor v, Tensor out, Tensor dout, Tensor lse, "
         "Tensor cu_seqlens, int max_seqlen, float scale, Tensor(a!) dq, Tensor(b!) dk, "
         "Tensor(c!) dv, Tensor(d!) workspace) -> ()");
+  m.def("lora_mirror(Tensor table, int n_tensors, int max_numel, Tensor(a!) out) -> ()");
+  m.def("lora_adamw(Tensor table, int n_tensors, int max_numel, float lr, float beta1, "
+        "float beta2, float eps, float weight_decay, Tensor step_in, Tensor(a!) step_out, "
+        "Tensor? grad_scale, Tensor? found_inf, Tensor(b!) out) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(talm, CUDA, m) {
@@ -776,4 +823,6 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("gemm_ex", &gemm_ex);
   m.impl("attn_fwd", &attn_fwd);
   m.impl("attn_bwd", &attn_bwd);
+  m.impl("lora_mirror", &lora_mirror);
+  m.impl("lora_adamw", &lora_adamw);
 }

@@ -26,7 +26,7 @@ import torch
 import torch.nn.functional as F
 
 from .engaged import FELL_BACK, ON, RAN
-from .lora import _power_of_two, _to_half, lora_plan
+from .lora import _power_of_two, _to_half, adapters_t, lora_plan
 from .rope import rope_
 from .state import DISABLED, fallback
 
@@ -87,6 +87,8 @@ class FusedProjections(torch.autograd.Function):
                 RAN["rope"] += 1
             RAN["qkv_mfma"] += 1
             ctx.mfma = True
+            ctx.a_t = adapters_t([lora_weights[2 * k] for k in range(len(adapters))]) \
+                if adapters and torch.is_grad_enabled() else None
             return FusedProjections._finish(ctx, x, out, sizes, bounds, compact, saved, group,
                                             first, last, adapters, states, rope, head_dim)
         ctx.mfma = False
@@ -305,15 +307,18 @@ def _mfma_backward(ctx, grads):
 def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
     wanted = [ctx.needs_input_grad[8 + i] for i in range(2 * len(ctx.adapters))]
     dx, lora_grads = _mfma_backward_core(grads, x2, rest, cos, sin, weight, ctx.sizes,
-                                         ctx.adapters, ctx.has_rope, wanted)
+                                         ctx.adapters, ctx.has_rope, wanted,
+                                         getattr(ctx, "a_t", None))
     dx = None if dx is None else dx.view(ctx.x_shape)
     return (dx, None, None, None, None, None, None, None, *lora_grads)
 
 
-def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_rope, wanted):
+def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_rope, wanted,
+                        a_t=None):
     """dX [N, H] (None without `weight`) and the adapters' [dA, dB, ...] of the q|k|v node from
     the gradients of its q, k, v outputs (fp16, unit column stride); `rest` holds (t, A16, B16)
-    per adapter, `wanted` which adapter gradients to form."""
+    per adapter, `wanted` which adapter gradients to form, `a_t` the adapters' A^T side by side
+    ([H, 16 per adapter] fp16; formed here when None)."""
     n_tok, size = x2.shape
     bounds = [0]
     for s_ in sizes:
@@ -341,7 +346,8 @@ def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_
 
         weight_t = transpose_weight_exact(weight)
         del weight
-        a_t = torch.cat([a16 for _t, a16, _b in halves], 0).t().contiguous() if adapters else None
+        if a_t is None and adapters:
+            a_t = torch.cat([a16 for _t, a16, _b in halves], 0).t().contiguous()
         dx = torch.empty(n_tok, size, dtype=torch.float16, device=x2.device)
         torch.ops.talm.qkv_lora_bwd_dx(dcat, weight_t, u, a_t, dx)
         del weight_t
@@ -442,6 +448,8 @@ class AttentionBlock(torch.autograd.Function):
         ctx.group, ctx.adapters, ctx.sizes, ctx.bounds = group, adapters, sizes, bounds
         ctx.head_dim, ctx.n_heads, ctx.n_kv = head_dim, n_heads, n_kv
         ctx.max_len, ctx.scale, ctx.x_shape = max_len, scale, x.shape
+        ctx.a_t = adapters_t([lora_weights[2 * k] for k in range(len(adapters))]) \
+            if adapters and torch.is_grad_enabled() else None
         RAN["qkv_mfma"] += 1
         RAN["rope"] += 1
         RAN["attn_kernel"] += 1
@@ -485,7 +493,7 @@ class AttentionBlock(torch.autograd.Function):
             weights = [group.weight("bwd", i) for i in (Q, K, V)]
             weight = torch.cat(weights, 0)
         dx, lora_grads = _mfma_backward_core((dq, dk, dv), x2, rest, cos, sin, weight,
-                                             ctx.sizes, ctx.adapters, True, wanted)
+                                             ctx.sizes, ctx.adapters, True, wanted, ctx.a_t)
         RAN["attn_kernel_bwd"] += 1
         RAN["qkv_mfma_bwd"] += 1
         dx = None if dx is None else dx.view(ctx.x_shape)

@@ -4,8 +4,8 @@ Mirrors solution/lora.py: `LoraProjectionTorch` runs PEFT's LoRA arithmetic op f
 GEMM on the layer group's dequantized weight, dropout, the two fp16 adapter GEMMs, `* scaling`
 folded into the add when it is a power of two >= 1 (exact), the fp16 add onto the base output —
 but keeps only the layer input x for the backward and replays the dropout there from the saved
-generator state (:151-231). `HalfCopies` keeps the fp16 copies of the fp32 adapter weights,
-refreshed at most once per optimizer step (:57-114).
+generator state (:151-231). The fp16 copies of the fp32 adapter weights come from
+`adapters.COPIES` (one launch per optimizer step for every adapter, :57-114).
 
 PEFT is not available here, so `LoraLinear` stands in for PEFT's LoRA wrapper of a 4-bit layer:
 the attributes the reference reads (`base_layer`, `lora_A`/`lora_B`/`lora_dropout` keyed by the
@@ -14,82 +14,38 @@ under fp16 autocast as its own forward.
 """
 
 import math
-import weakref
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .adapters import COPIES
 from .engaged import FELL_BACK, ON, RAN
 from .state import DISABLED, fallback
 
 
-def _key(param):
-    return param.data_ptr(), param._version
-
-
-class HalfCopies:
-    """fp16 copies of fp32 tensors (the adapters' weights), all refreshed in one foreach copy at
-    the first `get` after any of them changed (storage or version counter) or after an optimizer
-    step (`invalidate`)."""
-
-    def __init__(self):
-        self.entries = []
-        self.slots = {}
-
-    def get(self, param):
-        slot = self.slots.get(id(param))
-        if slot is None or self.entries[slot][0]() is not param:
-            slot = len(self.entries)
-            self.entries.append([weakref.ref(param), None, None, None])
-            self.slots[id(param)] = slot
-        entry = self.entries[slot]
-        if entry[1] != _key(param):
-            self.refresh()
-        return entry[2]
-
-    def invalidate(self, *_args, **_kwargs):
-        for entry in self.entries:
-            entry[1] = entry[2] = entry[3] = None
-
-    @torch.no_grad()
-    def refresh(self):
-        live = [entry for entry in self.entries if entry[0]() is not None]
-        if len(live) != len(self.entries):
-            self.entries = live
-            self.slots = {id(entry[0]()): slot for slot, entry in enumerate(live)}
-        stale = {}
-        for entry in live:
-            param = entry[0]()
-            if entry[1] != _key(param):
-                stale.setdefault(param.device, []).append((entry, param.detach()))
-        if stale:
-            RAN["lora_cast"] += 1
-        for device, items in stale.items():
-            sizes = [param.numel() for _, param in items]
-            flat = torch.empty(sum(sizes), dtype=torch.float16, device=device)
-            copies = [part.view(param.shape) for part, (_, param) in zip(flat.split(sizes), items)]
-            torch._foreach_copy_(copies, [param for _, param in items])
-            for (entry, param), copy in zip(items, copies):
-                entry[1], entry[2], entry[3] = _key(param), copy, param.untyped_storage()
-
-
-_half = HalfCopies()
 _hooks = []
 
 
 def _to_half(lora_a, lora_b):
     if not _hooks:
         return lora_a.to(torch.float16), lora_b.to(torch.float16)
-    return _half.get(lora_a), _half.get(lora_b)
+    return COPIES.half(lora_a), COPIES.half(lora_b)
+
+
+def adapters_t(lora_as):
+    """A^T of a q|k|v node's adapters side by side ([hidden, 16 per adapter] fp16)."""
+    if not _hooks:
+        return torch.cat([a.detach() for a in lora_as], 0).t().to(torch.float16).contiguous()
+    return COPIES.pair_t(tuple(lora_as))
 
 
 def install_cast_cache():
-    """The optimizer step post-hook that invalidates every fp16 copy (once per process)."""
+    """The optimizer step post-hook that retires the fp16 copies (once per process)."""
     if not _hooks:
         from torch.optim.optimizer import register_optimizer_step_post_hook
 
-        _hooks.append(register_optimizer_step_post_hook(_half.invalidate))
+        _hooks.append(register_optimizer_step_post_hook(COPIES.invalidate))
 
 
 def _power_of_two(value):

@@ -107,12 +107,21 @@ def make_batch(seed, step, vocab, batch=4, seq=512, lo=128, hi=512, device="cuda
 class Trainer:
     """AdamW + fp16 GradScaler + clipping + cosine schedule over `steps` optimizer steps."""
 
-    def __init__(self, model, steps=64, lr=2e-4, weight_decay=0.01, max_grad_norm=1.0):
+    def __init__(self, model, steps=64, lr=2e-4, weight_decay=0.01, max_grad_norm=1.0,
+                 fused_adapters=False):
         self.model = model
         self.params = lora_parameters(model)
-        # fused AdamW takes the GradScaler's scale and inf flag as device tensors, so the step
-        # needs no host synchronization (the unfused path reads the inf flag on the host)
-        self.opt = torch.optim.AdamW(self.params, lr=lr, weight_decay=weight_decay, fused=True)
+        # both optimizers take the GradScaler's scale and inf flag as device tensors, so the step
+        # needs no host synchronization (an unfused optimizer's step reads the inf flag on the
+        # host). `fused_adapters`: this package's one-launch AdamW, which also writes the next
+        # forward's fp16 adapter copies; else PyTorch's fused AdamW (the reference's setup).
+        if fused_adapters:
+            from .adapters import AdapterAdamW
+
+            self.opt = AdapterAdamW(self.params, lr=lr, weight_decay=weight_decay)
+        else:
+            self.opt = torch.optim.AdamW(self.params, lr=lr, weight_decay=weight_decay,
+                                         fused=True)
         self.sched = torch.optim.lr_scheduler.LambdaLR(
             self.opt, lambda i: 0.5 * (1.0 + math.cos(math.pi * min(i, steps) / steps)))
         self.scaler = torch.amp.GradScaler("cuda")

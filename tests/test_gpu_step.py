@@ -24,7 +24,7 @@ def _run(patched, steps, monkeypatch):
         for p in qlora_model.lora_parameters(model):
             if p.abs().sum() == 0:
                 p.normal_(0, 0.02)
-    trainer = qlora_model.Trainer(model, steps=steps)
+    trainer = qlora_model.Trainer(model, steps=steps, fused_adapters=patched)
     if patched:
         patches.apply()
         monkeypatch.setattr(fused_head, "VOCAB_CHUNK", 384)  # several slices of 1000 tokens
@@ -53,7 +53,8 @@ def test_patched_step_matches_eager_loss_curve(monkeypatch, split):
     assert engaged.RAN["fused_head"] == 0
     fused = _run(True, 6, monkeypatch)
     names = ["fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "addnorm",
-             "head", "varlen_attn", "attn_kernel", "attn_kernel_bwd", "fused_mlp", "attn_block"]
+             "head", "varlen_attn", "attn_kernel", "attn_kernel_bwd", "fused_mlp", "attn_block",
+             "adapter_adamw"]
     if split:  # the split last layer runs the per-projection MLP and the stand-alone RoPE
         names += ["swiglu_inplace", "split", "rope"]
     for name in names:
