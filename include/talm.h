@@ -320,6 +320,22 @@ int talm_lora_adamw(const int64_t* table, int32_t n_tensors, int64_t max_numel, 
                     float* step_out, const float* grad_scale, const float* found_inf,
                     uint16_t* out, void* stream);
 
+/*
+ * out [n_tokens, n_out] fp16 (row stride ldo) = x [n_tokens, k] fp16 (row stride ldx) W^T with W
+ * [n_out, k] in the layer group's NF4 form, dequantized inside the GEMM (never written out):
+ * packed [n_out * k / 2] (two weights per byte, high nibble first), absmax8 [n_out * k / 64]
+ * (the second-level code index of each 64-weight block), code f32 [256], absmax2 / offset2 f32
+ * [n_out * k / 16384] (one per 256 blocks), all starting at the weight's first element (which
+ * must start a 16384-weight group). The fp16 weights are bit-identical to talm_nf4_group_dequant's;
+ * fp32 accumulation. blocksize 64 and blocksize2 256 only; k a multiple of 64, n_out of 8, x /
+ * packed / out 16-byte aligned. Replaces the dequantization of the layer's weights plus the
+ * projection GEMM on them (solution/qgroup.py:72-99, :346-355) for a projection it serves.
+ */
+int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t k,
+                  const uint8_t* packed, const uint8_t* absmax8, const float* code,
+                  const float* absmax2, const float* offset2, int64_t n_out, int32_t blocksize,
+                  int32_t blocksize2, uint16_t* out, int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -52,6 +52,7 @@ SIGNATURES = {
                       _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
     "talm_lora_mirror": [_P, _I32, _I64, _P, _P],
     "talm_lora_adamw": [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _P, _P, _P, _P, _P, _P],
+    "talm_nf4_gemm": [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I64, _P],
 }
 
 # Entry points that return a size instead of a status.

@@ -10,46 +10,13 @@
 // Arithmetic is the reference's bit for bit: the scale is rounded after the product and after
 // the offset (no fused multiply-add anywhere in this file), the level times the scale is one
 // fp32 product and one round-to-nearest-even to fp16.
-#include "common.h"
-
-// hipcc contracts a * b + c into v_fma_f32 by default (also through HIP's rounding-mode helpers,
-// whose header definitions carry the contraction flag): contraction is switched off for this
-// whole file and the products and sums below are plain operators, each rounded on its own.
-#pragma clang fp contract(off)
+#include "nf4_code.h"
 
 namespace talm {
 namespace {
 
-// The 16 NormalFloat levels (QLoRA, Dettmers et al. 2023), as in solution/qgroup.py:60-63.
-__constant__ float kNF4Levels[16] = {
-    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
-    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
-    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
-    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
-
 constexpr int kThreads = 256;
 constexpr int kWordsPerThread = 4;  // 32 weights per thread, four independent 128-bit stores
-
-// The fp32 product, materialized: the empty asm keeps the backend from folding "multiply, then
-// convert to fp16" into one v_fma_mix (a single rounding of the exact product).
-__device__ __forceinline__ float mul_f32(float a, float b) {
-  float p = a * b;
-  asm("" : "+v"(p));
-  return p;
-}
-
-// Eight weights of one packed word (4 bytes, high nibble first) scaled and packed to 4 x 2 fp16.
-__device__ __forceinline__ uint4 dequant_word(uint32_t word, float scale, const float* levels) {
-  uint32_t out[4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const uint32_t byte = (word >> (8 * b)) & 0xffu;
-    const float first = mul_f32(levels[byte >> 4], scale);
-    const float second = mul_f32(levels[byte & 15u], scale);
-    out[b] = pack2(first, second);
-  }
-  return make_uint4(out[0], out[1], out[2], out[3]);
-}
 
 // Grouped kernel: word w covers weights [8w, 8w + 8) of absmax block w >> word_shift.
 __global__ __launch_bounds__(kThreads) void nf4_group_kernel(
@@ -82,7 +49,7 @@ __global__ __launch_bounds__(kThreads) void nf4_group_kernel(
   }
   float scales[kWordsPerThread];
 #pragma unroll
-  for (int j = 0; j < kWordsPerThread; ++j) scales[j] = mul_f32(s_code[codes[j]], a2[j]) + o2[j];
+  for (int j = 0; j < kWordsPerThread; ++j) scales[j] = block_scale(s_code[codes[j]], a2[j], o2[j]);
 #pragma unroll
   for (int j = 0; j < kWordsPerThread; ++j) {
     const int64_t w = base + j * kThreads;

@@ -573,6 +573,36 @@ void lora_adamw(const Tensor& table, int64_t n_tensors, int64_t max_numel, doubl
 }
 
 // ------------------------------------------------------------------------------------------
+// y = x W^T on the NF4 form of W (dequantized inside the GEMM).
+// ------------------------------------------------------------------------------------------
+void nf4_gemm(const Tensor& x, const Tensor& packed, const Tensor& absmax8, const Tensor& code,
+              const Tensor& absmax2, const Tensor& offset2, int64_t n_out, int64_t blocksize,
+              int64_t blocksize2, const Tensor& out) {
+  require_fp16(x, "x");
+  require_fp16(out, "out");
+  require(x.dim() == 2 && out.dim() == 2 && x.stride(1) == 1 && out.stride(1) == 1 &&
+              out.size(0) == x.size(0) && out.size(1) == n_out,
+          "nf4_gemm: x [N, K], out [N, n_out] with unit column stride");
+  const int64_t n = x.size(0), k = x.size(1);
+  for (const Tensor* t : {&packed, &absmax8, &code, &absmax2, &offset2})
+    require(t->is_cuda() && t->is_contiguous() && t->device() == x.device(),
+            "nf4_gemm: packed, absmax8, code, absmax2, offset2 contiguous on x's device");
+  require(packed.scalar_type() == at::kByte && absmax8.scalar_type() == at::kByte &&
+              code.scalar_type() == at::kFloat && absmax2.scalar_type() == at::kFloat &&
+              offset2.scalar_type() == at::kFloat,
+          "nf4_gemm: packed / absmax8 uint8, code / absmax2 / offset2 float32");
+  require(k % 64 == 0 && packed.numel() >= n_out * k / 2 && absmax8.numel() >= n_out * k / 64 &&
+              code.numel() >= 256 && absmax2.numel() >= n_out * k / 16384 &&
+              offset2.numel() >= n_out * k / 16384,
+          "nf4_gemm: the NF4 buffers do not cover [n_out, K]");
+  check(talm_nf4_gemm(as<uint16_t>(x), x.stride(0), n, k, as<uint8_t>(packed), as<uint8_t>(absmax8),
+                      as<float>(code), as<float>(absmax2), as<float>(offset2), n_out,
+                      static_cast<int32_t>(blocksize), static_cast<int32_t>(blocksize2),
+                      as<uint16_t>(out), out.stride(0), stream_of(x)),
+        "nf4_gemm");
+}
+
+// ------------------------------------------------------------------------------------------
 // Plain fp16 GEMMs on hipBLASLt with cached plans.
 // ------------------------------------------------------------------------------------------
 struct GemmKey {
@@ -798,6 +828,8 @@ TORCH_LIBRARY(talm, m) {
         "Tensor cu_seqlens, int max_seqlen, float scale, Tensor(a!) dq, Tensor(b!) dk, "
         "Tensor(c!) dv, Tensor(d!) workspace) -> ()");
   m.def("lora_mirror(Tensor table, int n_tensors, int max_numel, Tensor(a!) out) -> ()");
+  m.def("nf4_gemm(Tensor x, Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
+        "Tensor offset2, int n_out, int blocksize, int blocksize2, Tensor(a!) out) -> ()");
   m.def("lora_adamw(Tensor table, int n_tensors, int max_numel, float lr, float beta1, "
         "float beta2, float eps, float weight_decay, Tensor step_in, Tensor(a!) step_out, "
         "Tensor? grad_scale, Tensor? found_inf, Tensor(b!) out) -> ()");
@@ -824,5 +856,6 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("attn_fwd", &attn_fwd);
   m.impl("attn_bwd", &attn_bwd);
   m.impl("lora_mirror", &lora_mirror);
+  m.impl("nf4_gemm", &nf4_gemm);
   m.impl("lora_adamw", &lora_adamw);
 }

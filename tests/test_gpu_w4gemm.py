@@ -1,0 +1,91 @@
+"""talm_nf4_gemm (y = x W^T on the NF4 form of W, dequantized inside the GEMM) on the config-1
+layer's packed buffers: with x the identity the output is W^T, which must equal the grouped
+dequant kernel's fp16 weights bit for bit (pinned to the oracle in test_gpu_kernels.py); on
+random x the output is within one fp16 rounding of the fp32 product of those weights, for the
+q, k, gate|up and down slices of the layer and ragged token counts."""
+
+import pytest
+import torch
+
+from talm_amd import _ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+# (name, first projection, projections): slices of the packed layer (q, k, v, o, gate, up, down)
+SLICES = [("q", 0, 1), ("k", 1, 1), ("gate|up", 4, 2), ("down", 6, 1)]
+
+
+def _layer():
+    d = workloads.nf4_layer()
+    dev = {k: v.cuda() for k, v in d.items() if torch.is_tensor(v)}
+    n = d["n"]
+    w16 = torch.empty(n, dtype=torch.float16, device="cuda")
+    torch.ops.talm.nf4_group_dequant(dev["packed"], dev["absmax8"], dev["code"], dev["absmax2"],
+                                     dev["offset2"], w16, 64, 256)
+    return d, dev, w16
+
+
+def _slice(d, dev, w16, first, count):
+    shapes = d["shapes"]
+    e0 = sum(a * b for a, b in shapes[:first])
+    rows = sum(shapes[i][0] for i in range(first, first + count))
+    k = shapes[first][1]
+    assert e0 % 16384 == 0
+    parts = dict(packed=dev["packed"][e0 // 2:], absmax8=dev["absmax8"][e0 // 64:],
+                 absmax2=dev["absmax2"][e0 // 16384:], offset2=dev["offset2"][e0 // 16384:])
+    return parts, w16[e0:e0 + rows * k].view(rows, k), rows, k
+
+
+def _gemm(x, parts, code, rows):
+    out = torch.full((x.shape[0], rows), float("nan"), dtype=torch.float16, device="cuda")
+    torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], code, parts["absmax2"],
+                            parts["offset2"], rows, 64, 256, out)
+    return out
+
+
+@pytest.mark.parametrize("name,first,count", SLICES)
+def test_identity_input_gives_the_dequantized_weights(name, first, count):
+    print(f"[case] nf4_gemm identity {name}", flush=True)
+    _ops.load()
+    d, dev, w16 = _layer()
+    parts, w, rows, k = _slice(d, dev, w16, first, count)
+    eye = torch.eye(k, dtype=torch.float16, device="cuda")
+    out = _gemm(eye, parts, dev["code"], rows)
+    # every output is 1 * w plus exact zeros: the weight's value exactly (a weight of -0, from a
+    # negative block scale times the 0 level, sums to +0 with the other zero products)
+    want = w.t().contiguous()
+    same = out.view(torch.int16) == want.view(torch.int16)
+    assert bool((same | ((out == 0) & (want == 0))).all()), int((~same).sum())
+
+
+@pytest.mark.parametrize("name,first,count", SLICES)
+@pytest.mark.parametrize("n_tok", [1, 37, 333, 1367])
+def test_matches_fp32_product_of_dequantized_weights(name, first, count, n_tok):
+    print(f"[case] nf4_gemm {name} tokens={n_tok}", flush=True)
+    _ops.load()
+    d, dev, w16 = _layer()
+    parts, w, rows, k = _slice(d, dev, w16, first, count)
+    g = torch.Generator().manual_seed(n_tok)
+    x = torch.randn(n_tok, k, generator=g).half().cuda()
+    out = _gemm(x, parts, dev["code"], rows)
+    ref = x.float() @ w.float().t()
+    torch.testing.assert_close(out.float(), ref, rtol=2 ** -10,
+                               atol=2 ** -11 * float(ref.abs().max()))
+
+
+def test_row_stride_and_rejects_bad_shapes():
+    print("[case] nf4_gemm strides and errors", flush=True)
+    _ops.load()
+    d, dev, w16 = _layer()
+    parts, w, rows, k = _slice(d, dev, w16, 4, 2)
+    base = torch.randn(300, k + 64).half().cuda()
+    x = base[:, 32:32 + k]  # row stride k + 64
+    out = torch.empty(300, 2 * rows, dtype=torch.float16, device="cuda")[:, rows:]
+    torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], dev["code"], parts["absmax2"],
+                            parts["offset2"], rows, 64, 256, out)
+    ref = x.float() @ w.float().t()
+    torch.testing.assert_close(out.float(), ref, rtol=2 ** -10,
+                               atol=2 ** -11 * float(ref.abs().max()))
+    with pytest.raises(ValueError):
+        torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], dev["code"],
+                                parts["absmax2"], parts["offset2"], rows, 128, 256, out)
