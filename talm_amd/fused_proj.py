@@ -87,8 +87,9 @@ class FusedProjections(torch.autograd.Function):
                 RAN["rope"] += 1
             RAN["qkv_mfma"] += 1
             ctx.mfma = True
+            # for the backward's dX (forward runs with grad mode off: ask the node's inputs)
             ctx.a_t = adapters_t([lora_weights[2 * k] for k in range(len(adapters))]) \
-                if adapters and torch.is_grad_enabled() else None
+                if adapters and ctx.needs_input_grad[0] else None
             return FusedProjections._finish(ctx, x, out, sizes, bounds, compact, saved, group,
                                             first, last, adapters, states, rope, head_dim)
         ctx.mfma = False
@@ -448,8 +449,9 @@ class AttentionBlock(torch.autograd.Function):
         ctx.group, ctx.adapters, ctx.sizes, ctx.bounds = group, adapters, sizes, bounds
         ctx.head_dim, ctx.n_heads, ctx.n_kv = head_dim, n_heads, n_kv
         ctx.max_len, ctx.scale, ctx.x_shape = max_len, scale, x.shape
+        # for the backward's dX (forward runs with grad mode off: ask the node's inputs)
         ctx.a_t = adapters_t([lora_weights[2 * k] for k in range(len(adapters))]) \
-            if adapters and torch.is_grad_enabled() else None
+            if adapters and ctx.needs_input_grad[0] else None
         RAN["qkv_mfma"] += 1
         RAN["rope"] += 1
         RAN["attn_kernel"] += 1
