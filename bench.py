@@ -224,7 +224,7 @@ def run_steps(model, trainer, n_steps, seed, timed_from):
         if i == timed_from:
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-        losses.append(trainer.step(batches[i]))
+        losses.append(trainer.step(batches[i], batches[i + 1] if i + 1 < n_steps else None))
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / max(1, n_steps - timed_from)
     return [float(x) for x in losses], ms, torch.cuda.max_memory_allocated()

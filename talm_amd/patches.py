@@ -90,7 +90,7 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
     from .engaged import FELL_BACK, RAN
     from .fused_head import fused_head_loss
     from .rmsnorm import link_next_norms
-    from .unpad import is_right_padded, rows_context, unpad_batch
+    from .unpad import is_right_padded, rows_context, take_prefetched, unpad_batch
 
     stage.clear()
     kwargs.pop("return_dict", None)
@@ -107,7 +107,8 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
     if unpad:
         try:
             idx, positions, bounds, lengths, counts = unpad_batch(
-                attention_mask, shift.to(attention_mask.device))
+                attention_mask, shift.to(attention_mask.device),
+                values=take_prefetched(attention_mask, labels))
             if _unpad["checked"] < 3:
                 _unpad["checked"] += 1
                 if not is_right_padded(attention_mask, lengths):

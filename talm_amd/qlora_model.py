@@ -127,8 +127,14 @@ class Trainer:
         self.scaler = torch.amp.GradScaler("cuda")
         self.max_grad_norm = max_grad_norm
 
-    def step(self, batch):
-        """One optimizer step; returns the loss tensor (not synchronized)."""
+    def step(self, batch, next_batch=None):
+        """One optimizer step; returns the loss tensor (not synchronized). With `next_batch`, the
+        packing statistics of that batch are copied to the host ahead of time (no host sync in
+        the next step)."""
+        if next_batch is not None:
+            from .unpad import prefetch
+
+            prefetch(next_batch["attention_mask"], next_batch["labels"])
         with torch.autocast("cuda", dtype=torch.float16):
             out = self.model(**batch)
         loss = out.loss

@@ -22,6 +22,8 @@ from .state import DISABLED, fallback
 
 _rows = []
 _cu = []
+_ahead = {}  # batch key -> (pinned host values, event): row statistics copied ahead of time
+_AHEAD_MAX = 4
 
 
 @contextlib.contextmanager
@@ -32,7 +34,9 @@ def rows_context(bounds, device=None):
     if device is not None:
         ends = [e for s, e in bounds if e > s]
         if ends:
-            cu = (torch.tensor([0] + ends, dtype=torch.int32, device=device),
+            # pinned and asynchronous: a pageable copy would wait for the stream to drain
+            cu = (torch.tensor([0] + ends, dtype=torch.int32).pin_memory().to(
+                      device, non_blocking=True),
                   max(e - s for s, e in bounds if e > s), ends[-1])
     _rows.append(bounds)
     _cu.append(cu)
@@ -43,22 +47,69 @@ def rows_context(bounds, device=None):
         _cu.pop()
 
 
-def unpad_batch(attention_mask, targets=None):
+def _row_values(attention_mask, targets=None):
+    """[B] row lengths of a right-padded mask, then (with `targets`, [B * T] shifted labels) the
+    labelled count among the real tokens and among all positions, as one device vector."""
+    batch, seq = attention_mask.shape
+    lengths = attention_mask.to(torch.int64).sum(1)
+    if targets is None:
+        return lengths
+    lab = targets.reshape(batch, seq) >= 0
+    prefix = torch.arange(seq, device=attention_mask.device)[None] < lengths[:, None]
+    return torch.cat((lengths, torch.stack(((lab & prefix).sum(), lab.sum()))))
+
+
+def _batch_key(attention_mask, labels):
+    return (attention_mask.data_ptr(), attention_mask._version, tuple(attention_mask.shape),
+            labels.data_ptr(), labels._version, tuple(labels.shape))
+
+
+def prefetch(attention_mask, labels):
+    """Start the host copy of a coming batch's row statistics (GPU-side packing's one host
+    input): queued now, read by that batch's `unpad_batch` without waiting for the stream.
+    A training loop that knows its next batch calls this one step ahead, so no step stalls the
+    host on the GPU's backlog (solution/unpad.py:66-92 syncs once per step)."""
+    if not (attention_mask.is_cuda and attention_mask.dim() == 2 and labels.dim() == 2
+            and tuple(labels.shape) == tuple(attention_mask.shape)):
+        return
+    shift = torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:].reshape(-1)
+    values = _row_values(attention_mask, shift.to(attention_mask.device))
+    host = torch.empty(values.shape, dtype=torch.int64, pin_memory=True)
+    host.copy_(values, non_blocking=True)
+    event = torch.cuda.Event()
+    event.record()
+    while len(_ahead) >= _AHEAD_MAX:
+        _ahead.pop(next(iter(_ahead)))
+    _ahead[_batch_key(attention_mask, labels)] = (host, event)
+
+
+def take_prefetched(attention_mask, labels):
+    """The row statistics `prefetch` started for this batch (a host list), or None."""
+    if not _ahead or labels is None:
+        return None
+    hit = _ahead.pop(_batch_key(attention_mask, labels), None)
+    if hit is None:
+        return None
+    host, event = hit
+    event.synchronize()  # queued a step ago: long done
+    return host.tolist()
+
+
+def unpad_batch(attention_mask, targets=None, values=None):
     """From a right-padded [B, T] mask: flat indices of the real tokens, their positions inside
-    their rows, the row bounds in the flat sequence and the lengths (one host sync). With
-    `targets` ([B * T] shifted labels) also `counts` = [labelled among the gathered positions,
-    labelled among all positions] from the same host copy (solution/unpad.py:66-92)."""
+    their rows, the row bounds in the flat sequence and the lengths (one host sync, or none when
+    `values` holds what `take_prefetched` returned). With `targets` ([B * T] shifted labels) also
+    `counts` = [labelled among the gathered positions, labelled among all positions] from the
+    same host copy (solution/unpad.py:66-92)."""
     batch, seq = attention_mask.shape
     device = attention_mask.device
-    lengths_gpu = attention_mask.to(torch.int64).sum(1)
     counts = None
+    if values is None:
+        values = _row_values(attention_mask, targets).tolist()
     if targets is None:
-        lengths = lengths_gpu.tolist()
+        lengths = values[:batch]
     else:
-        lab = targets.reshape(batch, seq) >= 0
-        prefix = torch.arange(seq, device=device)[None] < lengths_gpu[:, None]
-        values = torch.cat((lengths_gpu, torch.stack(((lab & prefix).sum(), lab.sum())))).tolist()
-        lengths, counts = values[:batch], values[batch:]
+        lengths, counts = values[:batch], values[batch:batch + 2]
     idx, positions, bounds, start = [], [], [], 0
     for b, length in enumerate(lengths):
         ar = torch.arange(length, device=device)

@@ -30,9 +30,11 @@ def _run(patched, steps, monkeypatch):
         monkeypatch.setattr(fused_head, "VOCAB_CHUNK", 384)  # several slices of 1000 tokens
     losses = []
     try:
+        batches = [qlora_model.make_batch(seed=5, step=step, vocab=1000, seq=256, lo=64, hi=256)
+                   for step in range(steps)]
         for step in range(steps):
-            batch = qlora_model.make_batch(seed=5, step=step, vocab=1000, seq=256, lo=64, hi=256)
-            losses.append(float(trainer.step(batch)))
+            ahead = batches[step + 1] if step + 1 < steps else None
+            losses.append(float(trainer.step(batches[step], ahead)))
     finally:
         if patched:
             patches.unapply()
