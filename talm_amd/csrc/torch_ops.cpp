@@ -18,8 +18,13 @@
 // and kept (PyTorch's matmul asks hipBLASLt's heuristic on every call).
 #include <ATen/ATen.h>
 #include <ATen/hip/HIPContext.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 #include <torch/library.h>
+
+#include <atomic>
+#include <mutex>
+#include <vector>
 
 #include <optional>
 #include <string>
@@ -631,7 +636,27 @@ struct GemmPlan {
   hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
   hipblasLtMatmulAlgo_t algo{};
   size_t workspace = 0;
+  int generation = 0;  // of the measured table it was planned under
 };
+
+// Measured solutions (gemm_tuning.py): for products of this layout, m and k with n in
+// [n_lo, n_hi), hipBLASLt's solution `index`, validated against the exact shape when planned
+// (hipBLASLt's heuristic otherwise). Installing a table re-plans every shape at its next call.
+struct TunedRange {
+  int64_t trans_a, trans_b, m, k, n_lo, n_hi, index;
+};
+std::mutex tuned_mutex;
+std::vector<TunedRange> tuned_table;
+std::atomic<int> tuned_generation{0};
+
+int64_t tuned_index(const GemmKey& key) {
+  std::lock_guard<std::mutex> lock(tuned_mutex);
+  for (const TunedRange& r : tuned_table)
+    if (r.trans_a == key.trans_a && r.trans_b == key.trans_b && r.m == key.m && r.k == key.k &&
+        key.n >= r.n_lo && key.n < r.n_hi)
+      return r.index;
+  return -1;
+}
 
 void lt_check(hipblasStatus_t status, const char* what) {
   TORCH_CHECK(status == HIPBLAS_STATUS_SUCCESS, "gemm: hipBLASLt ", what, " failed (status ",
@@ -661,35 +686,69 @@ constexpr size_t kMaxPlans = 2048;
 // D [m, n] = op(A) [m, k] op(B) [k, n] in hipBLASLt's column-major terms, fp16 in and out, fp32
 // accumulation; op(A) = A^T when trans_a (A stored k x m), else A (stored m x k); op(B) = B^T
 // when trans_b (B stored n x k), else B (stored k x n).
+// Descriptor and layouts of a plan (no algorithm yet).
+void describe(const GemmKey& key, GemmPlan& p) {
+  lt_check(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "descriptor");
+  const hipblasOperation_t op_a = key.trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  const hipblasOperation_t op_b = key.trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_a,
+                                           sizeof(op_a)), "transa");
+  lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_b,
+                                           sizeof(op_b)), "transb");
+  if (key.bias) {
+    const hipblasLtEpilogue_t epilogue = HIPBLASLT_EPILOGUE_BIAS;
+    const hipDataType bias_type = HIP_R_16F;
+    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epilogue,
+                                             sizeof(epilogue)), "epilogue");
+    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE,
+                                             &bias_type, sizeof(bias_type)), "bias type");
+  }
+  lt_check(hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, key.trans_a ? key.k : key.m,
+                                       key.trans_a ? key.m : key.k, key.lda), "layout A");
+  lt_check(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, key.trans_b ? key.n : key.k,
+                                       key.trans_b ? key.k : key.n, key.ldb), "layout B");
+  lt_check(hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16F, key.m, key.n, key.ldd), "layout D");
+}
+
+// The measured table's solution for `key` when hipBLASLt confirms it supports this product.
+bool tuned_algo(const GemmKey& key, hipblasLtHandle_t handle, size_t workspace_limit,
+                GemmPlan& p) {
+  const int64_t index = tuned_index(key);
+  if (index < 0) return false;
+  std::vector<int> ids{static_cast<int>(index)};
+  std::vector<hipblasLtMatmulHeuristicResult_t> found;
+  if (hipblaslt_ext::getAlgosFromIndex(handle, ids, found) != HIPBLAS_STATUS_SUCCESS ||
+      found.empty())
+    return false;
+  const float alpha = 1.f, beta = 0.f;
+  size_t workspace = 0;
+  if (hipblaslt_ext::matmulIsAlgoSupported(handle, p.desc, &alpha, p.a, p.b, &beta, p.d, p.d,
+                                           found[0].algo, workspace) != HIPBLAS_STATUS_SUCCESS ||
+      workspace > workspace_limit)
+    return false;
+  p.algo = found[0].algo;
+  p.workspace = workspace;
+  return true;
+}
+
 const GemmPlan& plan_for(const GemmKey& key, hipblasLtHandle_t handle, size_t workspace_limit) {
+  const int generation = tuned_generation.load();
   auto it = plan_cache.plans.find(key);
-  if (it != plan_cache.plans.end()) return it->second;
+  if (it != plan_cache.plans.end()) {
+    if (it->second.generation == generation) return it->second;
+    destroy(it->second);
+    plan_cache.plans.erase(it);
+  }
   if (plan_cache.plans.size() >= kMaxPlans) {
     for (auto& kv : plan_cache.plans) destroy(kv.second);
     plan_cache.plans.clear();
   }
   GemmPlan p;
+  p.generation = generation;
   try {
-    lt_check(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F), "descriptor");
-    const hipblasOperation_t op_a = key.trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-    const hipblasOperation_t op_b = key.trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_a,
-                                             sizeof(op_a)), "transa");
-    lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_b,
-                                             sizeof(op_b)), "transb");
-    if (key.bias) {
-      const hipblasLtEpilogue_t epilogue = HIPBLASLT_EPILOGUE_BIAS;
-      const hipDataType bias_type = HIP_R_16F;
-      lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epilogue,
-                                               sizeof(epilogue)), "epilogue");
-      lt_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE,
-                                               &bias_type, sizeof(bias_type)), "bias type");
-    }
-    lt_check(hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16F, key.trans_a ? key.k : key.m,
-                                         key.trans_a ? key.m : key.k, key.lda), "layout A");
-    lt_check(hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16F, key.trans_b ? key.n : key.k,
-                                         key.trans_b ? key.k : key.n, key.ldb), "layout B");
-    lt_check(hipblasLtMatrixLayoutCreate(&p.d, HIP_R_16F, key.m, key.n, key.ldd), "layout D");
+    describe(key, p);
+    if (tuned_algo(key, handle, workspace_limit, p))
+      return plan_cache.plans.emplace(key, p).first->second;
     hipblasLtMatmulPreference_t pref = nullptr;
     lt_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
     const uint64_t limit = workspace_limit;
@@ -788,6 +847,123 @@ void gemm_ex(const Tensor& a, int64_t trans_a, const Tensor& b, int64_t trans_b,
            a.data_ptr(), b.data_ptr(), nullptr, d.data_ptr(), accumulate ? 1.f : 0.f, d);
 }
 
+// Installs the measured table: int64 [rows, 7] on the CPU (trans_a, trans_b, m, k, n_lo, n_hi,
+// solution index); an empty table restores hipBLASLt's heuristic everywhere.
+void gemm_algo_table(const Tensor& rows) {
+  require(!rows.is_cuda() && rows.scalar_type() == at::kLong && rows.dim() == 2 &&
+              rows.size(1) == 7 && rows.is_contiguous(),
+          "gemm_algo_table: int64 [rows, 7] on the CPU");
+  std::vector<TunedRange> table;
+  const int64_t* v = rows.data_ptr<int64_t>();
+  for (int64_t r = 0; r < rows.size(0); ++r, v += 7)
+    table.push_back(TunedRange{v[0], v[1], v[2], v[3], v[4], v[5], v[6]});
+  {
+    std::lock_guard<std::mutex> lock(tuned_mutex);
+    tuned_table.swap(table);
+  }
+  tuned_generation.fetch_add(1);
+}
+
+int64_t gemm_lib_version() {
+  int version = 0;
+  lt_check(hipblasLtGetVersion(at::cuda::getCurrentCUDABlasLtHandle(), &version), "version");
+  return version;
+}
+
+// Times every hipBLASLt solution that supports D = op(A) op(B) (the BLAS form of gemm_ex, D
+// overwritten) on the current stream: `reps` launches each after two warm-up launches. Returns
+// [best solution index, its µs, the heuristic's first choice's index, its µs] (float64, CPU).
+// For building the measured table; only D's contents change.
+Tensor gemm_tune(const Tensor& a, int64_t trans_a, const Tensor& b, int64_t trans_b,
+                 const Tensor& d, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb,
+                 int64_t ldd, int64_t reps) {
+  require_fp16(a, "a");
+  require_fp16(b, "b");
+  require_fp16(d, "d");
+  require(m > 0 && n > 0 && k > 0 && reps > 0, "gemm_tune: positive sizes and reps");
+  const int64_t ar = trans_a ? k : m, ac = trans_a ? m : k;
+  const int64_t br = trans_b ? n : k, bc = trans_b ? k : n;
+  require(lda >= ar && ldb >= br && ldd >= m &&
+              (ac - 1) * lda + ar <= storage_span(a) && (bc - 1) * ldb + br <= storage_span(b) &&
+              (n - 1) * ldd + m <= storage_span(d),
+          "gemm_tune: operands do not cover the product");
+  const GemmKey key{static_cast<int>(a.device().index()), m, n, k, lda, ldb, ldd,
+                    trans_a ? 1 : 0, trans_b ? 1 : 0, 0};
+  hipblasLtHandle_t handle = at::cuda::getCurrentCUDABlasLtHandle();
+  void* workspace = at::cuda::getCUDABlasLtWorkspace();
+  const size_t limit = at::cuda::getCUDABlasLtWorkspaceSize();
+  const hipStream_t stream = static_cast<hipStream_t>(stream_of(d));
+  GemmPlan p;
+  std::vector<hipblasLtMatmulHeuristicResult_t> all;
+  double out[4] = {-1, -1, -1, -1};
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  try {
+    describe(key, p);
+    lt_check(hipblaslt_ext::getAllAlgos(handle, hipblaslt_ext::GemmType::HIPBLASLT_GEMM,
+                                        trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N,
+                                        trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N, HIP_R_16F,
+                                        HIP_R_16F, HIP_R_16F, HIP_R_16F, HIPBLAS_COMPUTE_32F, all),
+             "getAllAlgos");
+    TORCH_CHECK(hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess,
+                "gemm_tune: events");
+    const float alpha = 1.f, beta = 0.f;
+    auto time = [&](hipblasLtMatmulAlgo_t& algo, size_t ws) -> double {
+      for (int i = 0; i < 2; ++i)
+        if (hipblasLtMatmul(handle, p.desc, &alpha, a.data_ptr(), p.a, b.data_ptr(), p.b, &beta,
+                            d.data_ptr(), p.d, d.data_ptr(), p.d, &algo, workspace, ws,
+                            stream) != HIPBLAS_STATUS_SUCCESS)
+          return -1;
+      TORCH_CHECK(hipEventRecord(e0, stream) == hipSuccess, "gemm_tune: event");
+      for (int64_t i = 0; i < reps; ++i)
+        hipblasLtMatmul(handle, p.desc, &alpha, a.data_ptr(), p.a, b.data_ptr(), p.b, &beta,
+                        d.data_ptr(), p.d, d.data_ptr(), p.d, &algo, workspace, ws, stream);
+      TORCH_CHECK(hipEventRecord(e1, stream) == hipSuccess &&
+                      hipEventSynchronize(e1) == hipSuccess,
+                  "gemm_tune: event");
+      float ms = 0.f;
+      TORCH_CHECK(hipEventElapsedTime(&ms, e0, e1) == hipSuccess, "gemm_tune: event");
+      return 1e3 * ms / reps;
+    };
+    for (auto& r : all) {
+      size_t ws = 0;
+      if (hipblaslt_ext::matmulIsAlgoSupported(handle, p.desc, &alpha, p.a, p.b, &beta, p.d,
+                                               p.d, r.algo, ws) != HIPBLAS_STATUS_SUCCESS ||
+          ws > limit)
+        continue;
+      const double us = time(r.algo, ws);
+      if (us > 0 && (out[1] < 0 || us < out[1])) {
+        out[0] = hipblaslt_ext::getIndexFromAlgo(r.algo);
+        out[1] = us;
+      }
+    }
+    hipblasLtMatmulPreference_t pref = nullptr;
+    lt_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
+    const uint64_t lim = limit;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &lim,
+                                          sizeof(lim));
+    hipblasLtMatmulHeuristicResult_t first{};
+    int found = 0;
+    const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(handle, p.desc, p.a, p.b, p.d, p.d,
+                                                               pref, 1, &first, &found);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (st == HIPBLAS_STATUS_SUCCESS && found > 0) {
+      out[2] = hipblaslt_ext::getIndexFromAlgo(first.algo);
+      out[3] = time(first.algo, first.workspaceSize);
+    }
+  } catch (...) {
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    destroy(p);
+    throw;
+  }
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  destroy(p);
+  Tensor result = at::empty({4}, at::TensorOptions().dtype(at::kDouble));
+  for (int i = 0; i < 4; ++i) result.data_ptr<double>()[i] = out[i];
+  return result;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(talm, m) {
@@ -828,6 +1004,10 @@ TORCH_LIBRARY(talm, m) {
         "Tensor cu_seqlens, int max_seqlen, float scale, Tensor(a!) dq, Tensor(b!) dk, "
         "Tensor(c!) dv, Tensor(d!) workspace) -> ()");
   m.def("lora_mirror(Tensor table, int n_tensors, int max_numel, Tensor(a!) out) -> ()");
+  m.def("gemm_algo_table(Tensor rows) -> ()", &gemm_algo_table);
+  m.def("gemm_lib_version() -> int", &gemm_lib_version);
+  m.def("gemm_tune(Tensor a, int trans_a, Tensor b, int trans_b, Tensor(a!) d, int m, int n, "
+        "int k, int lda, int ldb, int ldd, int reps) -> Tensor");
   m.def("nf4_gemm(Tensor x, Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
         "Tensor offset2, int n_out, int blocksize, int blocksize2, Tensor(a!) out) -> ()");
   m.def("lora_adamw(Tensor table, int n_tensors, int max_numel, float lr, float beta1, "
@@ -856,6 +1036,7 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("attn_fwd", &attn_fwd);
   m.impl("attn_bwd", &attn_bwd);
   m.impl("lora_mirror", &lora_mirror);
+  m.impl("gemm_tune", &gemm_tune);
   m.impl("nf4_gemm", &nf4_gemm);
   m.impl("lora_adamw", &lora_adamw);
 }

@@ -11,11 +11,12 @@ the original code outside the exact situation it was written for. Installed here
 - grouped NF4 dequantization of the 4-bit projections (qgroup.py), the LoRA node (lora.py) and
   q|k|v as one projection node with the rotary embedding in place (fused_proj.py);
 - padding removal with per-row attention (unpad.py) and the fused LM head + cross-entropy of
-  the causal LM (fused_head.py, `patch_qwen2_causal_lm` below).
+  the causal LM (fused_head.py, `patch_qwen2_causal_lm` below);
+- the measured hipBLASLt solution table of the decoder's GEMMs (gemm_tuning.py).
 
 Switches: SOLUTION_DISABLE_<PART>=1 leaves a part out (RMSNORM, ADDNORM, ROPE, SWIGLU_INPLACE,
-GROUP, LORA, FUSED_PROJ, FUSED_HEAD, UNPAD, FUSED_MLP, ATTN_BLOCK), as in the reference
-(solution/__init__.py:51-84).
+GROUP, LORA, FUSED_PROJ, FUSED_HEAD, UNPAD, FUSED_MLP, ATTN_BLOCK, GEMM_TABLE), as in the
+reference (solution/__init__.py:51-84).
 """
 
 import os
@@ -211,6 +212,10 @@ def apply():
     from . import _lib
 
     _lib.lib()
+    with installing("gemm_table"):
+        from . import gemm_tuning
+
+        gemm_tuning.load()
     if not _off("SWIGLU_INPLACE"):
         with installing("swiglu"):
             from .swiglu_inplace import patch_qwen2_mlp_inplace

@@ -40,6 +40,7 @@ COMPONENTS = {
     "mlp_save_up": "opt-in MLP keeping only up and its input -> the MLP forward before it",
     "fused_mlp": "the MLP as one node on the layer group -> the per-projection MLP",
     "attn_block": "q|k|v, attention and o_proj as one node -> the per-node attention",
+    "gemm_table": "measured hipBLASLt solutions (gemm_tuning.py) -> hipBLASLt's heuristic",
 }
 
 

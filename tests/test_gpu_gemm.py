@@ -70,3 +70,39 @@ def test_gemm_rejects_bad_shapes():
     with pytest.raises(ValueError):
         torch.ops.talm.gemm(a.float(), b, None, 1,
                             torch.empty(8, 4, dtype=torch.float16, device="cuda"))
+
+
+def _colmajor(buf, rows, cols, ld):
+    """The column-major rows x cols matrix with leading dimension ld at the start of buf."""
+    return buf[:cols * ld].view(cols, ld)[:, :rows].t()
+
+
+def test_measured_table_products_match_reference():
+    """Each product form of the measured hipBLASLt table (gemm_tuning.product_forms) through
+    gemm_ex with the table installed, then with hipBLASLt's heuristic (empty table): both within
+    the fp32-reference tolerance, at a bucket's middle and at an odd token count. The table is
+    the one committed for this hipBLASLt and architecture, so load() installs rows."""
+    import talm_amd._ops  # noqa: F401
+    from talm_amd import gemm_tuning
+
+    try:
+        assert gemm_tuning.load() > 0, "the committed table does not match this hipBLASLt"
+        for name, ta, tb, m, k, lda, ldb, ldd in gemm_tuning.product_forms():
+            for n in (1216, 1167):
+                g = torch.Generator("cpu").manual_seed(n + m + k + ta)
+                a = (torch.randn((m if ta else k) * lda, generator=g) * 0.05).half().cuda()
+                b = torch.randn((k if tb else n) * ldb, generator=g).half().cuda()
+                ma = _colmajor(a, k if ta else m, m if ta else k, lda).float()
+                mb = _colmajor(b, n if tb else k, k if tb else n, ldb).float()
+                ref = (ma.t() if ta else ma) @ (mb.t() if tb else mb)
+                for installed in (True, False):
+                    if not installed:
+                        torch.ops.talm.gemm_algo_table(torch.empty(0, 7, dtype=torch.int64))
+                    d = torch.zeros(n * ldd, dtype=torch.float16, device="cuda")
+                    torch.ops.talm.gemm_ex(a, ta, b, tb, d, m, n, k, lda, ldb, ldd, 0)
+                    torch.cuda.synchronize()
+                    _close(_colmajor(d, m, n, ldd), ref, k)
+                    assert torch.all(d.view(n, ldd)[:, m:] == 0), name
+                gemm_tuning.load()
+    finally:
+        torch.ops.talm.gemm_algo_table(torch.empty(0, 7, dtype=torch.int64))
