@@ -209,9 +209,10 @@ def kernel_suite(args, only):
     return results
 
 
-def run_steps(model, trainer, n_steps, seed, timed_from):
-    """Run n_steps optimizer steps; time steps [timed_from, n_steps) between two device syncs.
-    Returns (losses, ms_per_timed_step, peak_bytes)."""
+def run_steps(model, trainer, n_steps, seed, timed_from, before_timing=None):
+    """Run n_steps optimizer steps; time steps [timed_from, n_steps) between two device syncs
+    (`before_timing()` runs just before the first timed step). Returns (losses,
+    ms_per_timed_step, peak_bytes)."""
     from talm_amd import qlora_model
 
     vocab = model.config.vocab_size
@@ -222,6 +223,8 @@ def run_steps(model, trainer, n_steps, seed, timed_from):
     t0 = None
     for i in range(n_steps):
         if i == timed_from:
+            if before_timing is not None:
+                before_timing()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
         losses.append(trainer.step(batches[i], batches[i + 1] if i + 1 < n_steps else None))
@@ -241,18 +244,36 @@ def step_workload(args):
         torch.cuda.empty_cache()
         model = qlora_model.build_model(seed=1)
         trainer = qlora_model.Trainer(model, steps=n_steps, fused_adapters=mode == "patched")
+        runner, prepare, graphed = trainer, None, None
         if mode == "patched":
             patches.apply()
             engaged.reset()
+            if not args.no_graph:
+                from talm_amd.step_graph import GraphedTrainer
+
+                # forward + backward replayed from one HIP graph per 64-token bucket; every
+                # bucket of the workload's token range (4 rows of 128..512) is captured before
+                # the timed steps, as the reference warms its kernels up before training
+                graphed = runner = GraphedTrainer(trainer, bucket=64,
+                                                  warm_steps=max(1, min(args.warmup, 2)))
+                prepare = lambda: graphed.prepare(4 * 128, 4 * 512)  # noqa: E731
         try:
-            losses, ms, peak = run_steps(model, trainer, n_steps, seed=7, timed_from=args.warmup)
+            losses, ms, peak = run_steps(model, runner, n_steps, seed=7,
+                                         timed_from=max(args.warmup, 1 if graphed else 0),
+                                         before_timing=prepare)
         finally:
             if mode == "patched":
                 ran = dict(engaged.RAN)
                 patches.unapply()
+            if graphed is not None:
+                graph_info = {"graphs": len(graphed.graphs), "replays": graphed.replays,
+                              "capture_s": round(graphed.capture_seconds, 2), "bucket": 64}
+                graphed.close()
         out[mode] = {"losses": losses, "ms_per_step": ms, "peak_bytes": peak}
         if mode == "patched":
             out[mode]["engaged"] = ran
+            if graphed is not None:
+                out[mode]["hip_graph"] = graph_info
         print(f"[bench] step {mode}: {ms:.2f} ms/step, peak {peak / 2**30:.2f} GiB, "
               f"loss {losses[0]:.4f} -> {losses[-1]:.4f}", flush=True)
         del model, trainer
@@ -336,6 +357,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--workload", choices=("step", "kernels"), default="step")
     ap.add_argument("--no-eager", action="store_true", help="skip the eager loss-curve run")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="run the patched step eagerly (no HIP graph replay)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every box of this build has a single MI355X and "
@@ -386,6 +409,8 @@ def main():
             line["loss_curve_max_rel_diff"] = round(max(rel), 6)
             line["loss_curve_mean_rel_diff"] = round(sum(rel) / len(rel), 6)
         line["engaged"] = {k: v for k, v in sorted(p["engaged"].items()) if v}
+        if "hip_graph" in p:  # engaged counts: eager warm-up steps and graph captures
+            line["hip_graph"] = p["hip_graph"]
     line["kernels"] = kernels
     if line_roofline is not None:
         line["roofline"] = line_roofline

@@ -153,8 +153,10 @@ int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t vocab, int64
  * fused_head_vocab_kernel and the accumulator addmm (solution/fused_head.py:88-182, :236-251,
  * :356-383).
  *   hidden_states f16 [n_rows, hidden] (row stride ldh), weight f16 [vocab, hidden] (row
- *   stride ldw), targets i64 [n_rows] (-100 = ignore). Rows [0, n_grad) must be exactly the
- *   labelled rows (the caller orders rows labelled-first, solution/fused_head.py:290-299).
+ *   stride ldw), targets i64 [n_rows] (-100 = ignore). Rows [0, n_grad) are the gradient
+ *   rows: every labelled row must be among them (the caller orders rows labelled-first,
+ *   solution/fused_head.py:290-299, or passes n_grad = n_rows); an ignored row among them
+ *   costs gradient work and gets a zero gradient.
  *   weight_t: talm_head_weight_t of the same weight (row stride ldwt); required when the
  *   gradient is requested (n_grad > 0 and grad_hidden not NULL), ignored otherwise.
  * Writes per row: token_loss f32 (log s + m - z_target, 0 unlabelled), entropy f32

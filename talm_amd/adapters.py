@@ -48,6 +48,11 @@ class AdapterCopies:
         self.keys = []          # per weight: the key its copy in `buffer` was made from
         self.loose = {}         # id(weight) or pair ids -> (key(s), copy) made outside a layout
         self.adopted_by = None  # the optimizer whose step wrote `buffer`
+        # rewrite `buffer` in place instead of a fresh buffer per refresh / optimizer step: for a
+        # step replayed from a HIP graph, whose forward reads the copies at the address it was
+        # captured with. The caller guarantees that every backward reading the copies has run
+        # before the next optimizer step (a training loop does).
+        self.in_place = False
 
     # -- registration and layout ------------------------------------------------------------
     def _position(self, param):
@@ -108,11 +113,19 @@ class AdapterCopies:
     def refresh(self, device):
         if self.layout is None or not self._alive():
             self._build_layout(device)
-        size = self.layout[2]
-        buffer = torch.empty(max(size, 1), dtype=torch.float16, device=device)
+        buffer = self.reusable(device)
         torch.ops.talm.lora_mirror(self.table, len(self.params), self.max_numel(), buffer)
         self.adopt(buffer, None)
         RAN["lora_cast"] += 1
+
+    def reusable(self, device):
+        """The buffer the next copies go to: the current one in place mode when it has the
+        layout's size, else a fresh one."""
+        size = max(self.layout[2], 1)
+        b = self.buffer
+        if self.in_place and b is not None and b.numel() == size and b.device == device:
+            return b
+        return torch.empty(size, dtype=torch.float16, device=device)
 
     def adopt(self, buffer, optimizer):
         """`buffer` holds the copies of the current layout, made from the weights as they are."""
@@ -125,7 +138,10 @@ class AdapterCopies:
         if optimizer is not None and optimizer is self.adopted_by:
             self.adopted_by = None  # its step wrote the copies
             return
-        self.buffer = None
+        if self.in_place:
+            self.keys = []  # stale: the next use rewrites the same buffer
+        else:
+            self.buffer = None
         self.loose = {}
 
     def _current(self, pos, param):
@@ -258,8 +274,7 @@ class AdapterAdamW(torch.optim.Optimizer):
             if copies.layout is None or not copies._alive():
                 copies._build_layout(device)
             if buffer is None:
-                buffer = torch.empty(max(copies.layout[2], 1), dtype=torch.float16,
-                                     device=device)
+                buffer = copies.reusable(device)
             steps = self._state(group, params, device)
             rows = []
             for p, (h, t, ld) in zip(params, copies.entries(params)):

@@ -461,8 +461,12 @@ __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
   }
   const float s = a.run[a.n_rows + row];
   const int64_t tgt = a.targets[row];
-  // rows [0, n_grad) are labelled by contract; a target outside [0, vocab) (a broken contract)
-  // must not make the kernel read outside the weight: its W[target] term is left out
+  if (tgt < 0) {  // an ignored row among the gradient rows: zero gradient, as for the others
+    *reinterpret_cast<uint2*>(a.grad + at) = make_uint2(0u, 0u);
+    return;
+  }
+  // a target at or past the vocabulary (a broken contract) must not make the kernel read
+  // outside the weight: its W[target] term is left out
   uint2 wv = make_uint2(0u, 0u);
   if (tgt >= 0 && tgt < a.vocab) wv = *reinterpret_cast<const uint2*>(a.W + tgt * a.ldw + col);
   const float g0 = v.x / s - lo_f(wv.x), g1 = v.y / s - hi_f(wv.x);

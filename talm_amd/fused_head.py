@@ -46,8 +46,9 @@ def _slice_width(vocab_chunk, vocab):
 def head_ce(h16, w16, targets, vocab_chunk=VOCAB_CHUNK, n_grad=None, need_grad=True,
             group=GROUP, weight_t=None):
     """One talm_head_ce call. h16 fp16 [N, H], w16 fp16 [V, H] (unit column strides), targets
-    int64 [N]. With `need_grad`, rows [0, n_grad) must be the labelled rows (labelled-first order;
-    n_grad defaults to counting them, one host sync) and `weight_t` is w16's transpose from
+    int64 [N]. With `need_grad`, rows [0, n_grad) are the gradient rows: every labelled row must
+    be among them (labelled-first order; n_grad defaults to counting them, one host sync), and an
+    ignored row among them gets a zero gradient and `weight_t` is w16's transpose from
     `head_weights` (built here when not given). Returns per-row token_loss, entropy, best_idx
     (int32), correct (int32) and grad (fp16 [N, H] or None)."""
     n, size = h16.shape
@@ -204,15 +205,19 @@ class FusedHeadLossVocab(torch.autograd.Function):
 
 
 def fused_head_loss(hidden, weight, targets, num_items=None, vocab_chunk=None, *,
-                    token_chunk=None, n_labelled=None, return_argmax=False):
+                    token_chunk=None, n_labelled=None, return_argmax=False, grad_all_rows=False):
     """hidden [N, H] (fp16/fp32, may require grad), weight [V, H] frozen, targets [N] int64 already
     shifted (-100 = ignore). Returns (loss, token_loss[N], token_entropy[N], correct[N]) and, with
     `return_argmax`, the per-token argmax [N] (int32) as a fifth element
     (solution/fused_head.py:447-462). `n_labelled`: the exact host count of targets >= 0 when the
-    caller has it (saves a host sync). `token_chunk` (the reference's token-chunked path) runs
-    the same kernel `token_chunk` rows at a time."""
+    caller has it (saves a host sync). `grad_all_rows`: every row is a gradient row (no
+    labelled-first reordering, no count; an ignored row's gradient is zero), so no launch depends
+    on a host value of the targets (a step captured in a HIP graph). `token_chunk` (the
+    reference's token-chunked path) runs the same kernel `token_chunk` rows at a time."""
     need_grad = torch.is_grad_enabled() and hidden.requires_grad
     vchunk = vocab_chunk or VOCAB_CHUNK
+    if grad_all_rows:
+        n_labelled = hidden.shape[0]
     if token_chunk is None or token_chunk >= hidden.shape[0]:
         loss, token_loss, entropy, correct, best_idx = FusedHeadLossVocab.apply(
             hidden, weight, targets, num_items, vchunk, need_grad, n_labelled)

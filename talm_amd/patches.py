@@ -91,7 +91,8 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
     from .engaged import FELL_BACK, RAN
     from .fused_head import fused_head_loss
     from .rmsnorm import link_next_norms
-    from .unpad import is_right_padded, rows_context, take_prefetched, unpad_batch
+    from .unpad import (is_right_padded, rows_context, static_n_tokens, take_prefetched,
+                        unpad_batch)
 
     stage.clear()
     kwargs.pop("return_dict", None)
@@ -105,6 +106,12 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
              and tuple(input_ids.shape) == (batch, seq)
              and not getattr(self.model, "has_sliding_layers", True))
     counts = None
+    n_static = static_n_tokens()
+    if n_static is not None:
+        if not unpad:
+            raise ValueError("fixed-shape packing needs a right-padded [B, T] batch with a mask")
+        return _static_forward(self, input_ids, attention_mask, labels, shift, n_static,
+                               num_items, kwargs, output_cls, stage)
     if unpad:
         try:
             idx, positions, bounds, lengths, counts = unpad_batch(
@@ -160,6 +167,51 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
                       hidden_states=outputs.hidden_states, attentions=outputs.attentions)
 
 
+def _static_forward(self, input_ids, mask, labels, shift, n_tokens, num_items, kwargs,
+                    output_cls, stage):
+    """`_fused_forward` with the fixed-shape packing of `unpad.static_tokens` (a step captured in
+    a HIP graph): the batch is packed into `n_tokens` rows on the device, the pad rows form their
+    own sequence labelled -100, and the head takes every row as a gradient row (an ignored row's
+    gradient is zero), so no shape or launch depends on a host value of the batch."""
+    from types import SimpleNamespace
+
+    from .engaged import RAN
+    from .fused_head import fused_head_loss
+    from .rmsnorm import link_next_norms
+    from .unpad import rows_context_static, unpad_static
+
+    import torch
+
+    batch, seq = labels.shape
+    src, positions, cu, rows_targets = unpad_static(mask, shift.to(mask.device), n_tokens)
+    ids = torch.cat((input_ids.reshape(-1), input_ids.new_zeros(1))).index_select(0, src)
+    RAN["fused_head"] += 1
+    RAN["unpad"] += 1
+    link_next_norms(self.model)
+    stage.append("unpadded")
+    with rows_context_static(cu, seq, n_tokens):
+        outputs = self.model(input_ids=ids[None], attention_mask={"full_attention": None},
+                             position_ids=positions, past_key_values=None, inputs_embeds=None,
+                             use_cache=False, **kwargs)
+    stage.append("head")
+    hidden = outputs.last_hidden_state
+    loss, token_loss, token_entropy, correct, argmax = fused_head_loss(
+        hidden.reshape(-1, hidden.shape[-1]), self.lm_head.weight, rows_targets, num_items,
+        return_argmax=True, grad_all_rows=True)
+    # back to [B, T]: the pad rows all land on one extra slot, dropped
+    full_loss = token_loss.new_zeros(batch * seq + 1)
+    full_entropy = token_entropy.new_zeros(batch * seq + 1)
+    full_loss.index_copy_(0, src, token_loss)
+    full_entropy.index_copy_(0, src, token_entropy)
+    LAST_STEP.clear()
+    LAST_STEP.append(SimpleNamespace(
+        token_entropy=full_entropy[:-1].view(batch, seq),
+        token_loss=full_loss[:-1].view(batch, seq), correct=correct.sum(),
+        labelled=(rows_targets >= 0).sum(), argmax=argmax))
+    return output_cls(loss=loss, logits=None, past_key_values=None,
+                      hidden_states=outputs.hidden_states, attentions=outputs.attentions)
+
+
 def patch_qwen2_causal_lm():
     """`Qwen2ForCausalLM.forward` through `_fused_forward` in training with labels; the original
     forward otherwise (solution/patches.py:116-159)."""
@@ -180,7 +232,9 @@ def patch_qwen2_causal_lm():
         if "fused_head" not in DISABLED \
                 and _fused_forward_applies(self, labels, logits_to_keep, kwargs):
             device = self.lm_head.weight.device
-            rng_state = torch.cuda.get_rng_state(device)
+            # a step captured in a HIP graph has no fallback (it raises): no generator state
+            rng_state = None if torch.cuda.is_current_stream_capturing() \
+                else torch.cuda.get_rng_state(device)
             stage = []
             for _ in range(2):
                 try:
@@ -189,7 +243,7 @@ def patch_qwen2_causal_lm():
                                           dict(kwargs), CausalLMOutputWithPast, stage)
                 except Exception as exc:  # noqa: BLE001 - state.py convention
                     component = "unpad" if stage[-1:] == ["unpadded"] else "fused_head"
-                    if not fallback(component, exc):
+                    if rng_state is None or not fallback(component, exc):
                         raise
                 _restart(device, rng_state)
                 if "fused_head" in DISABLED:

@@ -139,10 +139,15 @@ class Trainer:
             out = self.model(**batch)
         loss = out.loss
         self.scaler.scale(loss).backward()
+        self.optimizer_tail()
+        return loss.detach()
+
+    def optimizer_tail(self):
+        """After the backward: unscale, clip, the optimizer step, the scale update, the
+        schedule, and the gradients released."""
         self.scaler.unscale_(self.opt)
         torch.nn.utils.clip_grad_norm_(self.params, self.max_grad_norm)
         self.scaler.step(self.opt)
         self.scaler.update()
         self.sched.step()
         self.opt.zero_grad(set_to_none=True)
-        return loss.detach()

@@ -1,0 +1,150 @@
+"""The QLoRA training step replayed from HIP graphs, one graph per token bucket.
+
+`qlora_model.Trainer.step` issues about 900 kernels per step from Python: autograd nodes, module
+calls and the C++ op layer's launches. On MI355X that took about 21 ms of host time per step,
+against about 20 ms of GPU time, so the host set the step time and no faster kernel could lower
+it. `GraphedTrainer` captures the forward and backward of the step once per bucket of
+`bucket` packed tokens and then replays it, one graph launch per step:
+
+- the batch is packed on the device into exactly `n_bucket` rows (`unpad.static_tokens`, read
+  by the causal-LM patch): the real tokens first, as in eager packing, then a pad sequence
+  labelled -100 that attends only to itself. Its loss and every gradient through it are exactly
+  zero, so the step computes the same values as the eager packing of the same batch. The only
+  difference is rounding where a library GEMM picks another algorithm for the larger row count;
+- the head takes every row as a gradient row, with no labelled-first count read on the host;
+- the batch tensors are copied into the static input buffers the graph reads;
+- the LoRA gradients are the graph's own tensors, handed to the parameters after each replay.
+
+The optimizer tail stays eager: GradScaler unscale and update, clipping, `AdapterAdamW` and the
+learning-rate schedule. It is about ten launches, and their host cost overlaps the graph's GPU
+time. `AdapterAdamW` rewrites the adapters' fp16 copies in place (`COPIES.in_place`), at the
+address the captured forward reads. The graphs share one memory pool and run one at a time on
+one stream. A tensor a replay leaves behind (loss, gradients) is read before the next replay.
+
+Capture needs a warmed-up trainer (`warm_steps` eager steps: optimizer state, GradScaler
+scale, the head's transposed weight, hipBLASLt plans). `prepare(lo, hi)` captures every bucket
+of a token range ahead of time, like the reference's kernel warm-up (solution/warmup.py); a
+bucket met for the first time is captured on the spot.
+"""
+
+import time
+
+import torch
+
+from . import unpad
+from .adapters import COPIES, AdapterAdamW
+
+_BATCH_KEYS = ("input_ids", "attention_mask", "labels")
+
+
+class GraphedTrainer:
+    """Wraps a `qlora_model.Trainer` whose optimizer is `AdapterAdamW` and whose model runs the
+    patched path (`apply()`): `step(batch, next_batch)` as the trainer's, replayed from graphs."""
+
+    def __init__(self, trainer, bucket=64, warm_steps=3):
+        if not isinstance(trainer.opt, AdapterAdamW):
+            raise ValueError("GraphedTrainer: the trainer's optimizer must be AdapterAdamW")
+        if bucket < 1:
+            raise ValueError(f"GraphedTrainer: bucket {bucket}")
+        self.trainer = trainer
+        self.bucket = int(bucket)
+        self.warm_steps = int(warm_steps)
+        self.steps = 0
+        self.static = None
+        self.graphs = {}           # bucket -> (graph, loss, gradients)
+        self.pool = None
+        self.capture_seconds = 0.0
+        self.replays = 0
+        COPIES.in_place = True
+
+    # -- batches ----------------------------------------------------------------------------------
+    def n_tokens(self, batch):
+        """Real tokens of a right-padded batch: from the statistics `unpad.prefetch` copied to the
+        host a step ahead, or one host sync for a batch that was not prefetched."""
+        mask, labels = batch["attention_mask"], batch["labels"]
+        values = unpad.take_prefetched(mask, labels)
+        if values is None:
+            values = unpad._row_values(mask).tolist()
+        return int(sum(values[:mask.shape[0]]))
+
+    def bucket_of(self, n_tokens):
+        return max(self.bucket, -(-int(n_tokens) // self.bucket) * self.bucket)
+
+    def _stage(self, batch):
+        if self.static is None:
+            self.static = {k: torch.empty_like(batch[k]) for k in _BATCH_KEYS}
+        for k in _BATCH_KEYS:
+            dst, src = self.static[k], batch[k]
+            if src.shape != dst.shape or src.dtype != dst.dtype or src.device != dst.device:
+                raise ValueError(f"GraphedTrainer: batch '{k}' {tuple(src.shape)} {src.dtype} "
+                                 f"differs from the captured {tuple(dst.shape)} {dst.dtype}")
+            dst.copy_(src, non_blocking=True)
+
+    # -- graphs -----------------------------------------------------------------------------------
+    def capture(self, n_bucket):
+        """Capture the forward + backward of a step packed into `n_bucket` rows."""
+        t = self.trainer
+        if self.static is None or self.steps < self.warm_steps:
+            raise RuntimeError("GraphedTrainer: capture after the warm-up steps")
+        n_bucket = int(n_bucket)
+        b, s = self.static["attention_mask"].shape
+        if n_bucket % self.bucket or not 0 < n_bucket < b * s + self.bucket:
+            raise ValueError(f"GraphedTrainer: bucket {n_bucket} for a [{b}, {s}] batch")
+        start = time.perf_counter()
+        held = [p.grad for p in t.params]
+        for p in t.params:
+            p.grad = None
+        graph = torch.cuda.CUDAGraph()
+        with unpad.static_tokens(n_bucket):
+            with torch.cuda.graph(graph, pool=self.pool):
+                with torch.autocast("cuda", dtype=torch.float16):
+                    out = t.model(**self.static)
+                t.scaler.scale(out.loss).backward()
+        if self.pool is None:
+            self.pool = graph.pool()
+        grads = [p.grad for p in t.params]
+        if any(g is None for g in grads):
+            raise RuntimeError("GraphedTrainer: a LoRA parameter got no gradient in the capture")
+        for p, g in zip(t.params, held):
+            p.grad = g
+        entry = (graph, out.loss.detach(), grads)
+        self.graphs[n_bucket] = entry
+        self.capture_seconds += time.perf_counter() - start
+        return entry
+
+    def prepare(self, lo_tokens, hi_tokens):
+        """Capture every bucket that a batch of lo_tokens..hi_tokens real tokens can fall in."""
+        for nb in range(self.bucket_of(lo_tokens), self.bucket_of(hi_tokens) + 1, self.bucket):
+            if nb not in self.graphs:
+                self.capture(nb)
+
+    def close(self):
+        """Drop the graphs and their pool; the adapters' copies go back to fresh buffers."""
+        self.graphs.clear()
+        self.pool = None
+        self.static = None
+        COPIES.in_place = False
+
+    # -- the step ---------------------------------------------------------------------------------
+    def step(self, batch, next_batch=None):
+        """One optimizer step; returns the loss tensor (not synchronized)."""
+        t = self.trainer
+        if self.steps < self.warm_steps:
+            loss = t.step(batch, next_batch)
+            self._stage(batch)
+            self.steps += 1
+            return loss
+        n = self.n_tokens(batch)
+        if next_batch is not None:
+            unpad.prefetch(next_batch["attention_mask"], next_batch["labels"])
+        self._stage(batch)
+        nb = self.bucket_of(n)
+        entry = self.graphs.get(nb) or self.capture(nb)
+        graph, loss, grads = entry
+        graph.replay()
+        self.replays += 1
+        for p, g in zip(t.params, grads):
+            p.grad = g
+        t.optimizer_tail()
+        self.steps += 1
+        return loss.clone()

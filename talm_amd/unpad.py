@@ -121,6 +121,63 @@ def unpad_batch(attention_mask, targets=None, values=None):
     return out if targets is None else out + (counts,)
 
 
+_static = []  # token counts of the fixed-shape packing in force (innermost last)
+
+
+@contextlib.contextmanager
+def static_tokens(n_tokens):
+    """While it is open, the causal-LM patch packs every batch into exactly `n_tokens` rows on the
+    device (`unpad_static`): no host value of the batch is read, so the forward and backward can
+    be captured in a HIP graph and replayed for any batch of at most `n_tokens` real tokens."""
+    _static.append(int(n_tokens))
+    try:
+        yield
+    finally:
+        _static.pop()
+
+
+def static_n_tokens():
+    return _static[-1] if _static else None
+
+
+def unpad_static(attention_mask, targets, n_tokens):
+    """Packing into a fixed row count with device ops only. The real tokens of the right-padded
+    [B, T] mask come first, in row order (as `unpad_batch`); the remaining n_tokens - N rows form
+    one more sequence that attends only to itself and is labelled -100, so its loss and every
+    gradient that flows through it are exactly zero (the head gives ignored rows a zero gradient,
+    and no other sequence reads its keys). Returns (src, positions [1, n_tokens], cu_seqlens
+    int32 [B + 2], targets [n_tokens]): src indexes the flat [B * T + 1] batch whose last element
+    is the pad slot. The caller guarantees N <= n_tokens."""
+    batch, seq = attention_mask.shape
+    device = attention_mask.device
+    # elementwise ops and single-block sums only (no library scan, no host value): every launch
+    # here can be recorded in a HIP graph
+    lengths = attention_mask.sum(1, dtype=torch.int32)
+    k = torch.arange(batch + 2, dtype=torch.int32, device=device)
+    before = k[:, None] > k[None, :batch]                       # [B + 2, B]: row b < k
+    cu = torch.where(k == batch + 1, n_tokens, (before * lengths[None, :]).sum(1, dtype=torch.int32))
+    cu = cu.to(torch.int32)
+    j = torch.arange(n_tokens, dtype=torch.int32, device=device)
+    row = torch.searchsorted(cu[1:batch + 1], j, right=True)
+    pos = j - cu.index_select(0, row)
+    src = torch.where(row < batch, row * seq + pos, batch * seq)
+    ext = torch.cat((targets.reshape(-1), targets.new_full((1,), -100)))
+    return src, pos.to(torch.int64)[None], cu, ext.index_select(0, src)
+
+
+@contextlib.contextmanager
+def rows_context_static(cu, max_len, total):
+    """`rows_context` for `unpad_static`'s packing: cu_seqlens already on the device, no host row
+    bounds (the per-row fallback attention cannot run; the varlen kernel must)."""
+    _rows.append(None)
+    _cu.append((cu, max_len, total))
+    try:
+        yield
+    finally:
+        _rows.pop()
+        _cu.pop()
+
+
 def is_right_padded(attention_mask, lengths):
     seq = attention_mask.shape[1]
     prefix = torch.arange(seq, device=attention_mask.device)[None] < \

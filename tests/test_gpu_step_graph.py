@@ -1,0 +1,103 @@
+"""The QLoRA step replayed from HIP graphs (step_graph.GraphedTrainer) on a small tied Qwen2
+(the parity model of test_gpu_step.py): against the same steps run eagerly with the same
+fixed-shape packing (bit-identical losses and LoRA weights: the same kernels on the same shapes
+in the same order), and against the eagerly packed patched step (the loss curve within the
+north star's 0.5%). The token counts are chosen so that buckets repeat after other buckets ran,
+one batch fills its bucket exactly (an empty pad sequence) and one is the largest batch."""
+
+import pytest
+import torch
+
+from talm_amd import fused_head, patches, qlora_model, unpad
+from talm_amd.step_graph import GraphedTrainer
+
+pytestmark = pytest.mark.gpu
+
+SEQ, VOCAB, BUCKET, WARM = 256, 1000, 64, 2
+# real tokens per step: eager warm-up, then 640 (bucket 640, no pad rows), 300 (320), 630 (640
+# again), 1024 (the largest), 310 (320 again), 600 (640)
+LENGTHS = [(200, 100, 64, 256), (256, 130, 70, 90), (250, 150, 100, 140), (256, 128, 128, 128),
+           (64, 100, 70, 66), (256, 200, 90, 84), (256, 256, 256, 256), (64, 64, 64, 118),
+           (100, 200, 150, 150)]
+
+
+def _batch(step, lengths):
+    g = torch.Generator().manual_seed(11 * 1000 + step)
+    lengths = torch.tensor(lengths)
+    ids = torch.randint(0, VOCAB, (len(lengths), SEQ), generator=g)
+    mask = torch.arange(SEQ)[None, :] < lengths[:, None]
+    labels = torch.where(mask, ids, torch.full_like(ids, -100))
+    ids = torch.where(mask, ids, torch.zeros_like(ids))
+    return {"input_ids": ids.cuda(), "attention_mask": mask.to(torch.int64).cuda(),
+            "labels": labels.cuda()}
+
+
+def _model():
+    config = qlora_model.qwen2_config(vocab_size=VOCAB, hidden_size=512, intermediate_size=1024,
+                                      num_hidden_layers=3, num_attention_heads=4,
+                                      num_key_value_heads=2, head_dim=128)
+    model = qlora_model.build_model(config, seed=3)
+    with torch.no_grad():
+        for p in qlora_model.lora_parameters(model):
+            if p.abs().sum() == 0:
+                p.normal_(0, 0.02)
+    return model
+
+
+def _run(mode, monkeypatch):
+    """mode: "graph" (GraphedTrainer), "static" (eager steps under the same fixed-shape packing)
+    or "eager" (the patched step with host-list packing). Returns (losses, LoRA weights,
+    trainer-or-None)."""
+    steps = len(LENGTHS)
+    model = _model()
+    trainer = qlora_model.Trainer(model, steps=steps, fused_adapters=True)
+    patches.apply()
+    monkeypatch.setattr(fused_head, "VOCAB_CHUNK", 384)
+    gt = GraphedTrainer(trainer, bucket=BUCKET, warm_steps=WARM) if mode == "graph" else None
+    if mode == "static":
+        from talm_amd.adapters import COPIES
+        monkeypatch.setattr(COPIES, "in_place", True)
+    losses = []
+    try:
+        batches = [_batch(i, lengths) for i, lengths in enumerate(LENGTHS)]
+        for i in range(steps):
+            ahead = batches[i + 1] if i + 1 < steps else None
+            if mode == "graph":
+                loss = gt.step(batches[i], ahead)
+            elif mode == "static" and i >= WARM:
+                nb = -(-sum(LENGTHS[i]) // BUCKET) * BUCKET
+                with unpad.static_tokens(nb):
+                    loss = trainer.step(batches[i], ahead)
+            else:
+                loss = trainer.step(batches[i], ahead)
+            losses.append(float(loss))
+        weights = [p.detach().clone() for p in trainer.params]
+        info = None if gt is None else (gt.replays, sorted(gt.graphs))
+    finally:
+        if gt is not None:
+            gt.close()
+        patches.unapply()
+    del model, trainer, gt
+    torch.cuda.empty_cache()
+    return losses, weights, info
+
+
+def test_graphed_step_matches_eager_static_step_bitwise(monkeypatch):
+    print("[case] graphed step vs eager fixed-shape step (bitwise)", flush=True)
+    ref_losses, ref_weights, _ = _run("static", monkeypatch)
+    losses, weights, (replays, buckets) = _run("graph", monkeypatch)
+    print(f"[graph] losses {losses}\n[static] losses {ref_losses}", flush=True)
+    assert replays == len(LENGTHS) - WARM
+    assert buckets == [320, 640, 1024]
+    assert losses == ref_losses
+    for w, r in zip(weights, ref_weights):
+        assert torch.equal(w, r), (w - r).abs().max().item()
+
+
+def test_graphed_step_matches_eager_loss_curve(monkeypatch):
+    print("[case] graphed step vs eager host-packed patched step (curve)", flush=True)
+    ref_losses, _, _ = _run("eager", monkeypatch)
+    losses, _, _ = _run("graph", monkeypatch)
+    print(f"[graph] losses {losses}\n[eager] losses {ref_losses}", flush=True)
+    for a, b in zip(losses, ref_losses):
+        assert abs(a - b) <= 5e-3 * abs(b), (losses, ref_losses)
