@@ -437,6 +437,111 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce_kernel(WgradArgs a) {
   }
 }
 
+// The same partials on MFMA (v_mfma_f32_32x32x16_f16), for 128-token chunks. Workgroup
+// (128 columns, chunk) stages the chunk's column values transposed in LDS, [column][token], a
+// token pair written as one dword, so that a fragment's 8 tokens are one 16-byte read; u^T and
+// t^T ([i][token], 32 columns each) sit next to them. Each wavefront reduces its 32 columns
+// against the 32 u columns (dA columns) or the 32 t columns (dB rows; the adapter's 16 are kept)
+// over the chunk's tokens: C[column][i] = sum_token X^T[column][token] M^T[i][token]. Needs
+// hidden % 32 == 0 and 8-aligned segments, offsets and row strides (16-byte loads); other shapes
+// take the kernel above. Same partial layout, so the same ordered reduction follows.
+constexpr int kWmTok = 128;         // tokens per chunk
+constexpr int kWmCols = 128;        // columns per workgroup: 4 wavefronts x 32
+constexpr int kWmLd = kWmTok + 8;   // LDS row stride in halves (272 bytes, 16-byte multiple)
+
+__device__ __forceinline__ void put_pair_columns(uint16_t (*rows)[kWmLd], int col, int pair,
+                                                 uint4 va, uint4 vb) {
+  // va / vb: 8 consecutive columns of tokens 2 pair and 2 pair + 1
+  const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    *reinterpret_cast<uint32_t*>(&rows[col + 2 * e][2 * pair]) = (wa[e] & 0xffffu) | (wb[e] << 16);
+    *reinterpret_cast<uint32_t*>(&rows[col + 2 * e + 1][2 * pair]) =
+        (wa[e] >> 16) | (wb[e] & 0xffff0000u);
+  }
+}
+
+__global__ __launch_bounds__(256) void lora_wgrad_mfma_kernel(WgradArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kWmCols][kWmLd];
+  __shared__ __attribute__((aligned(16))) uint16_t ms[2][32][kWmLd];  // u^T, t^T
+  constexpr int kPairs = kWmTok / 2;
+  const int chunk = blockIdx.y, r0 = chunk * kWmTok;
+  const int rn = min(kWmTok, a.n_tokens - r0);
+  const int c0 = blockIdx.x * kWmCols;
+  const int tid = threadIdx.x;
+  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+  // the column values: item = (8-column group, token pair); rows past the batch are clamped to
+  // its last row for the load and zeroed
+  for (int it = tid; it < (kWmCols / 8) * kPairs; it += 256) {
+    const int p = it % kPairs, g = it / kPairs;
+    const int c = c0 + 8 * g;
+    uint4 va = zero, vb = zero;
+    if (c < a.cols) {
+      const uint16_t* src;
+      int64_t ld;
+      if (c < a.hidden) {
+        src = a.x + c;
+        ld = a.ldx;
+      } else {
+        const int cb = c - a.hidden;
+        src = a.dy + (cb >= a.seg[0] ? a.lo[1] + cb - a.seg[0] : a.lo[0] + cb);
+        ld = a.ldy;
+      }
+      const int ra = min(2 * p, rn - 1), rb = min(2 * p + 1, rn - 1);
+      va = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + ra) * ld);
+      vb = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + rb) * ld);
+      if (2 * p >= rn) va = zero;
+      if (2 * p + 1 >= rn) vb = zero;
+    }
+    put_pair_columns(xs, 8 * g, p, va, vb);
+  }
+  // u^T and t^T: item = (which, 8-column group of 32, token pair); columns of a missing adapter
+  // are zero
+  const bool need_u = c0 < a.hidden, need_t = c0 + kWmCols > a.hidden;
+  const int rank = kRank * a.n_adapters;
+  for (int it = tid; it < 2 * 4 * kPairs; it += 256) {
+    const int p = it % kPairs, q = (it / kPairs) % 4, which = it / (4 * kPairs);
+    if (which ? !need_t : !need_u) continue;
+    uint4 va = zero, vb = zero;
+    if (8 * q < rank) {
+      const uint16_t* src = (which ? a.t : a.u) + 8 * q;
+      const int64_t ld = which ? a.ldt : a.ldu;
+      const int ra = min(2 * p, rn - 1), rb = min(2 * p + 1, rn - 1);
+      va = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + ra) * ld);
+      vb = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + rb) * ld);
+      if (2 * p >= rn) va = zero;
+      if (2 * p + 1 >= rn) vb = zero;
+    }
+    put_pair_columns(ms[which], 8 * q, p, va, vb);
+  }
+  __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63;
+  const int cw = c0 + 32 * wave;
+  if (cw >= a.cols) return;  // no barrier follows
+  const int which = cw < a.hidden ? 0 : 1;  // hidden % 32 == 0: one kind per wavefront
+  f32x16 acc = {};
+#pragma unroll
+  for (int ks = 0; ks < kWmTok / 16; ++ks) {
+    const int kc = ks * 2 + (lane >> 5);
+    const half8_t av = *reinterpret_cast<const half8_t*>(&xs[32 * wave + (lane & 31)][8 * kc]);
+    const half8_t bv = *reinterpret_cast<const half8_t*>(&ms[which][lane & 31][8 * kc]);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
+  }
+  const int n = lane & 31;
+  float* out = a.part + static_cast<int64_t>(chunk) * a.cols * 32;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int c = cw + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+    if (c >= a.cols) continue;
+    int i = n;
+    if (which) {  // dB row of adapter g: its 16 t columns, stored at 0..15
+      i = n - (c - a.hidden >= a.seg[0] ? kRank : 0);
+      if (i < 0 || i >= kRank) continue;
+    }
+    out[static_cast<int64_t>(c) * 32 + i] = acc[v];
+  }
+}
+
 bool fits32(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t{1} << 31); }
 
 }  // namespace
@@ -653,11 +758,23 @@ TALM_API int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy,
   a.scaling[1] = two ? scaling1 : 0.f; a.da[1] = two ? da1 : da0; a.db[1] = two ? db1 : db0;
   a.part = static_cast<float*>(workspace);
   a.cols = static_cast<int>(hidden + seg0 + (two ? seg1 : 0));
-  a.chunks = static_cast<int>((n_tokens + kWgChunk - 1) / kWgChunk);
   const hipStream_t s = as_stream(stream);
-  hipLaunchKernelGGL(lora_wgrad_partial_kernel,
-                     dim3(static_cast<unsigned>((a.cols + 255) / 256), static_cast<unsigned>(a.chunks)),
-                     dim3(256), 0, s, a);
+  const bool mfma = hidden % 32 == 0 && seg0 % 8 == 0 && lo0 % 8 == 0 &&
+                    (!two || (seg1 % 8 == 0 && lo1 % 8 == 0)) && ldx % 8 == 0 && ldy % 8 == 0 &&
+                    ldu % 8 == 0 && ldt % 8 == 0 && aligned(x, 16) && aligned(dy, 16) &&
+                    aligned(u, 16) && aligned(t, 16);
+  if (mfma) {
+    a.chunks = static_cast<int>((n_tokens + kWmTok - 1) / kWmTok);
+    hipLaunchKernelGGL(lora_wgrad_mfma_kernel,
+                       dim3(static_cast<unsigned>((a.cols + kWmCols - 1) / kWmCols),
+                            static_cast<unsigned>(a.chunks)),
+                       dim3(256), 0, s, a);
+  } else {
+    a.chunks = static_cast<int>((n_tokens + kWgChunk - 1) / kWgChunk);
+    hipLaunchKernelGGL(lora_wgrad_partial_kernel,
+                       dim3(static_cast<unsigned>((a.cols + 255) / 256), static_cast<unsigned>(a.chunks)),
+                       dim3(256), 0, s, a);
+  }
   hipLaunchKernelGGL(lora_wgrad_reduce_kernel,
                      dim3(static_cast<unsigned>((static_cast<int64_t>(a.cols) * 32 + 255) / 256)),
                      dim3(256), 0, s, a);

@@ -194,10 +194,14 @@ def test_qkv_lora_bwd_dx_matches_fp32(n, size, n_out, rank):
 
 
 @pytest.mark.parametrize("n,size,segs", [(1130, 1536, [(0, 1536), (1792, 256)]),
-                                         (65, 512, [(0, 512), (768, 256)]), (1, 64, [(64, 128)])])
+                                         (65, 512, [(0, 512), (768, 256)]), (1, 64, [(64, 128)]),
+                                         (300, 96, [(0, 96), (128, 32)]),
+                                         (70, 40, [(0, 40), (48, 24)])])
 def test_lora_wgrad_matches_fp32(n, size, segs):
     """dA_g = u_g^T x and dB_g = scaling_g dy_g^T t_g in fp32 (the reference rounds the fp16
-    GEMM output before its fp32 cast: within one fp16 rounding of the fp32 sums)."""
+    GEMM output before its fp32 cast: within one fp16 rounding of the fp32 sums). The MFMA
+    kernel takes the 32-aligned hidden sizes (a workgroup of the 96 case holds both dA columns
+    and dB rows, and a wavefront's dB rows span both adapters); hidden 40 takes the VALU one."""
     from talm_amd import _ops
 
     _case(f"lora_wgrad n={n} H={size} segs={segs}")
