@@ -1,20 +1,20 @@
 """The decoder MLP down(silu(gate(x)) * up(x)) on a packed layer group as ONE autograd node
 (the reference's FusedMLP, solution/fused_proj.py:241-287).
 
-gate and up write the two halves of one [N, 2I] buffer, SwiGLU runs on the halves in place, and
-the input gradient accumulates its two products in one output:
-  forward   gu[:, :I] = x W_gate^T, gu[:, I:] = x W_up^T
+gate and up are adjacent projections of the layer buffer, so [W_gate; W_up] is one [2I, H]
+view, and their outputs are the two halves of one [N, 2I] buffer:
+  forward   gu = x [W_gate; W_up]^T            (one GEMM: gu[:, :I] = gate, gu[:, I:] = up)
             act = silu(gu[:, :I]) * gu[:, I:]  (talm_swiglu_fwd_rows)
             y = act W_down^T
   backward  dact = dy W_down
             dgate, dup over gu's halves        (talm_swiglu_bwd_rows, in place)
-            dx = dgate W_gate, then dx += dup W_up (the second GEMM accumulates: no add pass)
-One node instead of four (three GroupLinear nodes and the SwiGLU node) and no separate add of
-the gate and up input gradients: the step is bound by the host's launch rate. Every GEMM keeps
-the form and shape of the per-projection path: hipBLASLt's first-choice kernels for the single
-[N, 2I] product and for the 2I-deep input gradient (or the reference's transposed formulation)
-are several times slower here. Same products with fp32 accumulation as the per-projection
-path; the layers whose forward dequantization is split (qgroup.SPLIT_LAYERS) keep it.
+            dx = [dgate | dup] [W_gate; W_up]  (one GEMM reducing over 2I)
+One node instead of four (three GroupLinear nodes and the SwiGLU node), no separate add of the
+gate and up input gradients. hipBLASLt's heuristic choice for the 2I-deep input gradient is
+about twice as slow as two I-deep products; the measured solution table (gemm_tuning.py) names
+one about 15% faster than the two products together. Same products with fp32 accumulation as
+the per-projection path; the layers whose dequantization is split (qgroup.SPLIT_LAYERS) take
+two products.
 """
 
 import os
@@ -44,9 +44,9 @@ class FusedMLP(torch.autograd.Function):
             if w_gu is None:
                 raise RuntimeError("fused_mlp: gate and up are not one span of the layer")
             taken = 2
+            # [gate | up] = x [W_gate; W_up]^T: one GEMM into the two halves of one buffer
             gu = torch.empty(n_tok, 2 * inter, dtype=torch.float16, device=x.device)
-            torch.ops.talm.gemm(x2, w_gu[:inter], None, 1, gu[:, :inter])
-            torch.ops.talm.gemm(x2, w_gu[inter:], None, 1, gu[:, inter:])
+            torch.ops.talm.gemm(x2, w_gu, None, 1, gu)
             del w_gu
             w_down = group.span("fwd", DOWN, DOWN + 1)
             if w_down is None:
@@ -86,13 +86,14 @@ class FusedMLP(torch.autograd.Function):
         dx = torch.empty(n_tok, hidden, dtype=torch.float16, device=dy.device)
         w_gu = group.span("bwd", GATE, DOWN)
         if w_gu is not None:
-            w_gate, w_up = w_gu[:inter], w_gu[inter:]
+            # dx = [dgate | dup] [W_gate; W_up]: one GEMM with the reduction over both halves
+            torch.ops.talm.gemm(gu, w_gu, None, 0, dx)
         else:  # split pass
             w_gate, w_up = group.weight("bwd", GATE), group.weight("bwd", UP)
-        torch.ops.talm.gemm(gate, w_gate, None, 0, dx)
-        # dx += dup W_up in the column-major BLAS form: dx^T [H x N] += W_up^T [H x I] dup^T
-        torch.ops.talm.gemm_ex(w_up, 0, up, 0, dx, hidden, n_tok, inter, hidden, 2 * inter,
-                               hidden, 1)
+            torch.ops.talm.gemm(gate, w_gate, None, 0, dx)
+            # dx += dup W_up in the column-major BLAS form: dx^T [H x N] += W_up^T [H x I] dup^T
+            torch.ops.talm.gemm_ex(w_up, 0, up, 0, dx, hidden, n_tok, inter, hidden, 2 * inter,
+                                   hidden, 1)
         return dx.view(ctx.x_shape), None
 
 

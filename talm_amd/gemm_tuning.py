@@ -38,10 +38,10 @@ def product_forms():
     return (
         ("o_fwd", 1, 0, h, h, h, h, h),
         ("o_dx", 0, 0, h, h, h, h, h),
-        ("gate_up_fwd", 1, 0, i, h, h, h, 2 * i),
+        ("gate_up_fwd", 1, 0, 2 * i, h, h, h, 2 * i),
         ("down_fwd", 1, 0, h, i, i, i, h),
         ("down_dx", 0, 0, i, h, i, h, i),
-        ("gate_up_dx", 0, 0, h, i, h, 2 * i, h),
+        ("gate_up_dx", 0, 0, h, 2 * i, h, 2 * i, h),
     )
 
 
