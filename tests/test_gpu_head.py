@@ -25,12 +25,13 @@ def _case(msg):
     print(f"[case] {msg}", flush=True)
 
 
-def _run(h16, w16, t, num_items=None, vchunk=8192, grad_scale=3.0):
+def _run(h16, w16, t, num_items=None, vchunk=8192, grad_scale=3.0, grad_all_rows=False):
     x = torch.from_numpy(h16).to(DEV).requires_grad_()
     w = torch.from_numpy(w16).to(DEV)
     tt = torch.from_numpy(t).to(DEV)
     loss, tl, ent, corr, arg = fused_head.fused_head_loss(x, w, tt, num_items, vchunk,
-                                                          return_argmax=True)
+                                                          return_argmax=True,
+                                                          grad_all_rows=grad_all_rows)
     (loss * grad_scale).backward()
     return {"loss": float(loss), "token_loss": tl.cpu().numpy(), "entropy": ent.cpu().numpy(),
             "correct": corr.cpu().numpy(), "best_idx": arg.cpu().numpy(),
@@ -91,6 +92,24 @@ def test_head_label_edge_cases(labels):
         t[33] = 1234
     res = _run(h16, w16, t, vchunk=1024)
     _check(res, h16, w16, t, 1024, what=labels)
+
+
+@pytest.mark.parametrize("labels", ["mixed", "none", "one", "all"])
+def test_head_every_row_a_gradient_row(labels):
+    """grad_all_rows (the fixed-shape step captured in a HIP graph): no labelled-first
+    reordering, every row goes through the gradient GEMM; an ignored row's gradient is exactly
+    zero and the rest matches the oracle to the same bars."""
+    _case(f"head every row a gradient row, labels={labels}")
+    h16, w16, t = exact_head_case(150, 64, 5000, 12)
+    if labels == "none":
+        t[:] = -100
+    elif labels == "one":
+        t[:] = -100
+        t[77] = 4321
+    elif labels == "all":
+        t = np.random.default_rng(13).integers(0, 5000, 150)
+    res = _run(h16, w16, t, vchunk=1024, grad_all_rows=True)
+    _check(res, h16, w16, t, 1024, what=f"all rows {labels}")
 
 
 @pytest.mark.parametrize("num_items", [None, 7, "tensor"])
