@@ -41,6 +41,8 @@ constexpr int kD = 128;         // head dim
 constexpr int kKeys = 64;       // keys per tile
 constexpr int kKS = kD + 8;     // row stride (halfs) of a [keys][D] tile in LDS
 constexpr int kVS = kKeys + 4;  // row stride (halfs) of a transposed [D][keys] tile in LDS
+constexpr int kQT = 32;           // query rows per step of the dK / dV loop
+constexpr int kQS = kQT + 4;      // row stride (halfs) of a transposed [D][queries] tile
 constexpr float kLn2 = 0.693147180559945309f;
 
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -297,17 +299,24 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(BwdArgs a) {
   if (sub == 0 && row < rows) a.dd[static_cast<int64_t>(h) * a.n_tokens + t] = acc;
 }
 
-// dQ: the forward's structure, one query row per lane.
+// LDS of the dQ and dK / dV bodies: both run in one launch (attn_bwd_kernel) and carve one
+// buffer, so the launch needs the larger of the two.
+constexpr int kDqLds = 2 * (2 * kKeys * kKS + kD * kVS) * 2;
+constexpr int kDkdvLds = 2 * (2 * kQT * kKS + 2 * kD * kQS) * 2 + 2 * 2 * kQT * 4;
+constexpr int kBwdLds = kDqLds > kDkdvLds ? kDqLds : kDkdvLds;
+
+// dQ: the forward's structure, one query row per lane; `tile` is the query tile.
 template <int W>
-__global__ __launch_bounds__(64 * W, 1) void attn_bwd_dq_kernel(BwdArgs a) {
+__device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned char* smem) {
   constexpr int kRows = 32 * W;
   constexpr int kPer = kKeys * (kD / 8) / (64 * W);
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeys * kKS];   // K [key][d]
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][kKeys * kKS];   // V [key][d]
-  __shared__ __attribute__((aligned(16))) uint16_t kts[2][kD * kVS];     // K^T [d][key]
+  typedef uint16_t KeyTile[kKeys * kKS];
+  typedef uint16_t KeyTileT[kD * kVS];
+  KeyTile* ks = reinterpret_cast<KeyTile*>(smem);                          // K [key][d]
+  KeyTile* vs = reinterpret_cast<KeyTile*>(smem + 2 * sizeof(KeyTile));    // V [key][d]
+  KeyTileT* kts = reinterpret_cast<KeyTileT*>(smem + 4 * sizeof(KeyTile)); // K^T [d][key]
 
   const int seq = blockIdx.z, head = blockIdx.y;
-  const int tile = a.n_tiles - 1 - static_cast<int>(blockIdx.x);
   const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
   const int q0 = tile * kRows;
   if (q0 >= len) return;
@@ -435,22 +444,24 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dq_kernel(BwdArgs a) {
 }
 
 // dK / dV partials of one query head: each lane owns one key of the workgroup's 32W keys.
-constexpr int kQT = 32;           // query rows per step of the dK / dV loop
-constexpr int kQS = kQT + 4;      // row stride (halfs) of a transposed [D][queries] tile
 
+// dK / dV partials of one query head; `tile` is the key tile.
 template <int W>
-__global__ __launch_bounds__(64 * W, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
+__device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsigned char* smem) {
   constexpr int kCols = 32 * W;                       // keys per workgroup
   constexpr int kPer = kQT * (kD / 8) / (64 * W);     // 16-byte chunks of a Q / dO tile per thread
-  __shared__ __attribute__((aligned(16))) uint16_t qs[2][kQT * kKS];     // Q [q][d]
-  __shared__ __attribute__((aligned(16))) uint16_t ds[2][kQT * kKS];     // dO [q][d]
-  __shared__ __attribute__((aligned(16))) uint16_t qts[2][kD * kQS];     // Q^T [d][q]
-  __shared__ __attribute__((aligned(16))) uint16_t dts[2][kD * kQS];     // dO^T [d][q]
-  __shared__ __attribute__((aligned(16))) float ls[2][kQT];              // lse2 of the rows
-  __shared__ __attribute__((aligned(16))) float dds[2][kQT];             // Dd of the rows
+  typedef uint16_t RowTile[kQT * kKS];
+  typedef uint16_t RowTileT[kD * kQS];
+  typedef float RowStat[kQT];
+  unsigned char* p = smem;
+  RowTile* qs = reinterpret_cast<RowTile*>(p);   p += 2 * sizeof(RowTile);    // Q [q][d]
+  RowTile* ds = reinterpret_cast<RowTile*>(p);   p += 2 * sizeof(RowTile);    // dO [q][d]
+  RowTileT* qts = reinterpret_cast<RowTileT*>(p); p += 2 * sizeof(RowTileT);  // Q^T [d][q]
+  RowTileT* dts = reinterpret_cast<RowTileT*>(p); p += 2 * sizeof(RowTileT);  // dO^T [d][q]
+  RowStat* ls = reinterpret_cast<RowStat*>(p);   p += 2 * sizeof(RowStat);    // lse2 of the rows
+  RowStat* dds = reinterpret_cast<RowStat*>(p);                               // Dd of the rows
 
   const int seq = blockIdx.z, head = blockIdx.y;
-  const int tile = a.n_tiles - 1 - static_cast<int>(blockIdx.x);
   const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
   const int k0 = tile * kCols;
   if (k0 >= len) return;
@@ -597,6 +608,20 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_dkdv_kernel(BwdArgs a) {
   }
 }
 
+// dQ and the dK / dV partials in one launch: they read the same inputs and write disjoint
+// outputs, and each alone has fewer workgroups than the chip has CUs (its time is its longest
+// workgroup's), so side by side they share the chip. Even blockIdx.x: query tile of dQ, longest
+// (last) first; odd: key tile of dK / dV, longest (first) first.
+template <int W>
+__global__ __launch_bounds__(64 * W, 1) void attn_bwd_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kBwdLds];
+  const int bx = static_cast<int>(blockIdx.x) >> 1;
+  if ((blockIdx.x & 1) == 0)
+    attn_bwd_dq<W>(a, a.n_tiles - 1 - bx, smem);
+  else
+    attn_bwd_dkdv<W>(a, bx, smem);
+}
+
 // dK / dV fp16 [token][kv head][d] = sum over the KV head's query heads, in head order.
 __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // 4 columns each
@@ -728,10 +753,9 @@ TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
   const int64_t rows = n_tokens * n_q_heads;
   hipLaunchKernelGGL(attn_bwd_dot_kernel, dim3(static_cast<unsigned>((rows * 16 + 255) / 256)),
                      dim3(256), 0, s, a);
-  const dim3 grid(static_cast<unsigned>(a.n_tiles), static_cast<unsigned>(n_q_heads),
+  const dim3 grid(static_cast<unsigned>(2 * a.n_tiles), static_cast<unsigned>(n_q_heads),
                   static_cast<unsigned>(n_seqs));
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<W>), grid, dim3(64 * W), 0, s, a);
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<W>), grid, dim3(64 * W), 0, s, a);
+  hipLaunchKernelGGL((attn_bwd_kernel<W>), grid, dim3(64 * W), 0, s, a);
   const int64_t red = n_tokens * n_kv_heads * (kD / 4);
   hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3(static_cast<unsigned>((red + 255) / 256)),
                      dim3(256), 0, s, a);
