@@ -144,7 +144,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
 // ------------------------------------------------------------------------------------------
 // 8 wavefronts of 32 x 64 (two per SIMD) and a 3-slot ring (96 KiB): the token count gives few
 // 128-row tiles, so each CU's tile must keep its L2 -> LDS stream busy on its own.
-using QkvShape = TileShape<128, 128, 64, 3, 4, 2>;
+using QkvShape = TileShape<64, 128, 64, 3, 2, 2>;
 constexpr int kQZS = 128 + 8;                       // staged tile row stride (halfs)
 static_assert(128 * kQZS * 2 <= QkvShape::kRing, "the staged tile reuses the ring");
 
