@@ -251,10 +251,10 @@ def step_workload(args):
             if not args.no_graph:
                 from talm_amd.step_graph import GraphedTrainer
 
-                # forward + backward replayed from one HIP graph per 32-token bucket; every
+                # forward + backward replayed from one HIP graph per 16-token bucket; every
                 # bucket of the workload's token range (4 rows of 128..512) is captured before
                 # the timed steps, as the reference warms its kernels up before training
-                graphed = runner = GraphedTrainer(trainer, bucket=32,
+                graphed = runner = GraphedTrainer(trainer, bucket=16,
                                                   warm_steps=max(1, min(args.warmup, 2)))
                 prepare = lambda: graphed.prepare(4 * 128, 4 * 512)  # noqa: E731
         try:

@@ -41,7 +41,7 @@ class GraphedTrainer:
     """Wraps a `qlora_model.Trainer` whose optimizer is `AdapterAdamW` and whose model runs the
     patched path (`apply()`): `step(batch, next_batch)` as the trainer's, replayed from graphs."""
 
-    def __init__(self, trainer, bucket=32, warm_steps=2):
+    def __init__(self, trainer, bucket=16, warm_steps=2):
         if not isinstance(trainer.opt, AdapterAdamW):
             raise ValueError("GraphedTrainer: the trainer's optimizer must be AdapterAdamW")
         if bucket < 1:
