@@ -13,8 +13,7 @@ its root) on the CPU, citing the file:line it follows:
 - `swiglu`   SwiGLU forward / backward
 - `head`     vocabulary-chunked LM head + cross-entropy with the online log-sum-exp and the
              rescaled gradient accumulator, and its closed-form (two-pass) twin
-- `codebook` the NF4 level table and the double-quant code table from their published
-             constructions
+- `codebook` the NF4 level table from its published construction
 
 How each function is pinned (the checks live in tests/test_oracle.py):
 - NF4: the level table against the QLoRA normal-quantile construction; the fp32 -> fp16 rounding
@@ -30,7 +29,8 @@ How each function is pinned (the checks live in tests/test_oracle.py):
   invariance), the gradient against finite differences of the loss, the argmax against numpy's
   first-maximum on planted ties (solution/test_kernels.py:250-282), the label shift and the
   ignore index (solution/test_kernels.py:497-519).
-- codebook: the dynamic (double-quant) table's size, symmetry and sortedness; its values have
-  no reference vector in the reference tree (bitsandbytes is not vendored): parity unpinned,
-  but it is an input of the kernels, not an output.
+- every function also against the committed golden fixtures of tests/golden/ (expected values
+  from PyTorch: float64 autograd, float32 elementwise ops, a float64 full softmax), in
+  tests/test_golden.py. The double-quant code table is such a fixture (an input, not an
+  oracle function).
 """

@@ -142,11 +142,12 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
 // ------------------------------------------------------------------------------------------
 // out = [x | ts] [W | B]^T + bias, rotary embedding on the columns below rope_cols.
 // ------------------------------------------------------------------------------------------
-// 8 wavefronts of 32 x 64 (two per SIMD) and a 3-slot ring (96 KiB): the token count gives few
-// 128-row tiles, so each CU's tile must keep its L2 -> LDS stream busy on its own.
+// 64 x 128 tiles of 4 wavefronts of 32 x 64, a 3-slot ring (72 KiB) and two workgroups per CU:
+// the token count gives few row tiles, so the smaller tile doubles the workgroups in flight and
+// each keeps its own L2 -> LDS stream busy.
 using QkvShape = TileShape<64, 128, 64, 3, 2, 2>;
-constexpr int kQZS = 128 + 8;                       // staged tile row stride (halfs)
-static_assert(128 * kQZS * 2 <= QkvShape::kRing, "the staged tile reuses the ring");
+constexpr int kQZS = QkvShape::kBN + 8;             // staged tile row stride (halfs)
+static_assert(QkvShape::kBM * kQZS * 2 <= QkvShape::kRing, "the staged tile reuses the ring");
 
 // An operand whose k range has two parts: steps [0, nk1) read `base1` (k < k1), the steps after
 // them read `base2` (k in [lo2, hi2), counted from 0 again). The per-lane row and chunk do not depend on the part; the
@@ -259,7 +260,7 @@ __global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void proj_ext
       },
       acc, lane, wave);
 
-  // Epilogue: + bias, fp16, staged in LDS ([128][kQZS] halfs)
+  // Epilogue: + bias, fp16, staged in LDS ([kBM][kQZS] halfs)
   uint16_t* Zs = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
   for (int i = 0; i < S::kFragM; ++i)

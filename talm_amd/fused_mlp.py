@@ -13,8 +13,8 @@ One node instead of four (three GroupLinear nodes and the SwiGLU node), no separ
 gate and up input gradients. hipBLASLt's heuristic choice for the 2I-deep input gradient is
 about twice as slow as two I-deep products; the measured solution table (gemm_tuning.py) names
 one about 15% faster than the two products together. Same products with fp32 accumulation as
-the per-projection path; the layers whose dequantization is split (qgroup.SPLIT_LAYERS) take
-two products.
+the per-projection path. Once "qgroup" is off (the weights come projection by projection) the
+backward takes two products.
 """
 
 import os
@@ -38,24 +38,14 @@ class FusedMLP(torch.autograd.Function):
             x2 = x2.contiguous()
         n_tok = x2.shape[0]
         inter = group.shapes[GATE][0]
-        taken = 0
-        try:
-            w_gu = group.span("fwd", GATE, DOWN)
-            if w_gu is None:
-                raise RuntimeError("fused_mlp: gate and up are not one span of the layer")
-            taken = 2
-            # [gate | up] = x [W_gate; W_up]^T: one GEMM into the two halves of one buffer
-            gu = torch.empty(n_tok, 2 * inter, dtype=torch.float16, device=x.device)
-            torch.ops.talm.gemm(x2, w_gu, None, 1, gu)
-            del w_gu
-            w_down = group.span("fwd", DOWN, DOWN + 1)
-            if w_down is None:
-                raise RuntimeError("fused_mlp: down_proj is not a span of the layer")
-            taken = 3
-        except Exception:
-            if taken:
-                group.refund("fwd", taken)
-            raise
+        w_gu = group.span(GATE, DOWN)
+        if w_gu is None:
+            raise RuntimeError("fused_mlp: gate and up are not one span of the layer")
+        # [gate | up] = x [W_gate; W_up]^T: one GEMM into the two halves of one buffer
+        gu = torch.empty(n_tok, 2 * inter, dtype=torch.float16, device=x.device)
+        torch.ops.talm.gemm(x2, w_gu, None, 1, gu)
+        del w_gu
+        w_down = group.weight(DOWN)
         act = torch.empty(n_tok, inter, dtype=torch.float16, device=x.device)
         torch.ops.talm.swiglu_fwd_rows(gu[:, :inter], gu[:, inter:], act)
         y = torch.empty(n_tok, hidden, dtype=torch.float16, device=x.device)
@@ -76,7 +66,7 @@ class FusedMLP(torch.autograd.Function):
             dy = dy.to(torch.float16)
         if dy.stride(1) != 1:
             dy = dy.contiguous()
-        w_down = group.weight("bwd", DOWN)
+        w_down = group.weight(DOWN)
         dact = torch.empty(n_tok, inter, dtype=torch.float16, device=dy.device)
         torch.ops.talm.gemm(dy, w_down, None, 0, dact)
         del w_down
@@ -84,12 +74,12 @@ class FusedMLP(torch.autograd.Function):
         torch.ops.talm.swiglu_bwd_rows(dact, gate, up, gate, up)
         del dact
         dx = torch.empty(n_tok, hidden, dtype=torch.float16, device=dy.device)
-        w_gu = group.span("bwd", GATE, DOWN)
+        w_gu = group.span(GATE, DOWN)
         if w_gu is not None:
             # dx = [dgate | dup] [W_gate; W_up]: one GEMM with the reduction over both halves
             torch.ops.talm.gemm(gu, w_gu, None, 0, dx)
-        else:  # split pass
-            w_gate, w_up = group.weight("bwd", GATE), group.weight("bwd", UP)
+        else:  # "qgroup" is off: the projections' own weights
+            w_gate, w_up = group.weight(GATE), group.weight(UP)
             torch.ops.talm.gemm(gate, w_gate, None, 0, dx)
             # dx += dup W_up in the column-major BLAS form: dx^T [H x N] += W_up^T [H x I] dup^T
             torch.ops.talm.gemm_ex(w_up, 0, up, 0, dx, hidden, n_tok, inter, hidden, 2 * inter,
@@ -99,7 +89,7 @@ class FusedMLP(torch.autograd.Function):
 
 def mlp_plan(mlp, x):
     """The layer group when gate_proj, up_proj and down_proj are projections 4, 5, 6 of one
-    packed group (no LoRA, no hooks) and this forward pass dequantizes the whole layer."""
+    packed group (no LoRA, no bias, no hooks)."""
     from .fused_proj import _no_hooks, _packed
 
     if not ENABLED or not (x.is_cuda and x.dtype == torch.float16 and x.dim() >= 2) \
@@ -116,7 +106,7 @@ def mlp_plan(mlp, x):
         return None
     if any(group.biases[i] is not None for i in (GATE, UP, DOWN)):
         return None
-    if not _no_hooks(mods + [mlp]) or group.split_now("fwd"):
+    if not _no_hooks(mods + [mlp]):
         return None
     return group
 
@@ -133,7 +123,5 @@ def fused_mlp_forward(mlp, x):
             raise
         FELL_BACK["fused_mlp"] += 1
         return None
-    if torch.is_grad_enabled() and x.requires_grad:
-        group.expected_bwd += 3
     RAN["fused_mlp"] += 1
     return y

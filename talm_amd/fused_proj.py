@@ -42,13 +42,11 @@ class FusedProjections(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, group, first, last, adapters, compact, rope, head_dim, *lora_weights):
-        ctx.fetched, states = False, []
+        states = []
         try:
             return FusedProjections._forward(ctx, x, group, first, last, adapters, compact, rope,
                                              head_dim, lora_weights, states)
         except Exception:
-            if ctx.fetched:
-                group.refund("fwd", last - first)
             drawn = [state for state in states if state is not None]
             if drawn:
                 torch.cuda.set_rng_state(drawn[0], x.device)
@@ -63,8 +61,7 @@ class FusedProjections(torch.autograd.Function):
         bounds = [0]
         for size in sizes:
             bounds.append(bounds[-1] + size)
-        weight = group.span("fwd", first, last)
-        ctx.fetched = weight is not None
+        weight = group.span(first, last)
         bias = group.span_bias(first, last)
         halves = [_to_half(lora_weights[2 * k], lora_weights[2 * k + 1])
                   for k in range(len(adapters))]
@@ -93,6 +90,8 @@ class FusedProjections(torch.autograd.Function):
             return FusedProjections._finish(ctx, x, out, sizes, bounds, compact, saved, group,
                                             first, last, adapters, states, rope, head_dim)
         ctx.mfma = False
+        if weight is None:  # "qgroup" is off: the projections' own dequantization, stacked
+            weight = torch.cat([group.weight(i) for i in range(first, last)], 0)
         out = F.linear(x2, weight, bias)
         del weight
         saved = [x2]
@@ -177,13 +176,13 @@ class FusedProjections(torch.autograd.Function):
         dys = [dcat[:, bounds[i]:bounds[i + 1]] for i in range(len(ctx.sizes))]
         dx = None
         if ctx.needs_input_grad[0]:
-            weight = group.span("bwd", ctx.first, ctx.last)
+            weight = group.span(ctx.first, ctx.last)
             if weight is not None:
                 dx = torch.mm(dcat, weight)
                 del weight
             else:
                 for i, dy in enumerate(dys):
-                    weight = group.weight("bwd", ctx.first + i)
+                    weight = group.weight(ctx.first + i)
                     if dx is None:
                         dx = torch.mm(dy, weight)
                     else:
@@ -280,7 +279,9 @@ def _mfma_bwd_ok(ctx, grads):
             return False
     if any(ctx.sizes[seg] % 32 for seg, _s, _p in ctx.adapters):
         return False
-    return len(ctx.sizes) == 3
+    # q|k|v (three outputs, RoPE-back in the concatenation), or one projection without RoPE
+    # whose gradient is the GEMM operand as it is
+    return len(ctx.sizes) == 3 or (len(ctx.sizes) == 1 and not ctx.has_rope)
 
 
 def _mfma_backward(ctx, grads):
@@ -294,15 +295,10 @@ def _mfma_backward(ctx, grads):
     if ctx.has_rope:
         cos, sin = rest[-2:]
         rest = rest[:-2]
-    weight = group.span("bwd", ctx.first, ctx.last) if ctx.needs_input_grad[0] else None
+    weight = group.span(ctx.first, ctx.last) if ctx.needs_input_grad[0] else None
     if ctx.needs_input_grad[0] and weight is None:
         return None
-    try:
-        return _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight)
-    except Exception:
-        if weight is not None:  # the ops path takes the weight again
-            group.refund("bwd", ctx.last - ctx.first)
-        raise
+    return _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight)
 
 
 def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
@@ -325,8 +321,13 @@ def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_
     for s_ in sizes:
         bounds.append(bounds[-1] + s_)
     dys = [g.reshape(n_tok, -1) for g in grads]
-    dcat = torch.empty(n_tok, bounds[-1], dtype=torch.float16, device=x2.device)
-    torch.ops.talm.qkv_bwd_prep(dys[0], dys[1], dys[2], cos, sin, dcat)
+    if len(dys) == 1:
+        dcat = dys[0]
+        if dcat.stride(0) % 8 or dcat.data_ptr() % 16:
+            dcat = dcat.contiguous()
+    else:
+        dcat = torch.empty(n_tok, bounds[-1], dtype=torch.float16, device=x2.device)
+        torch.ops.talm.qkv_bwd_prep(dys[0], dys[1], dys[2], cos, sin, dcat)
     if has_rope:
         RAN["rope"] += 1
     halves = [rest[3 * k:3 * k + 3] for k in range(len(adapters))]  # (t, a16, b16)
@@ -413,7 +414,7 @@ class AttentionBlock(torch.autograd.Function):
         n_tok = x2.shape[0]
         sizes = [group.shapes[i][0] for i in (Q, K, V)]
         bounds = [0, sizes[0], sizes[0] + sizes[1], sizes[0] + sizes[1] + sizes[2]]
-        weight = group.span("fwd", Q, V + 1)
+        weight = group.span(Q, V + 1)
         if weight is None:
             raise _NotApplicable()
         halves = [_to_half(lora_weights[2 * k], lora_weights[2 * k + 1])
@@ -421,26 +422,19 @@ class AttentionBlock(torch.autograd.Function):
         bias = group.span_bias(Q, V + 1)
         if not (_mfma_ok(x2, weight, bias, bounds, adapters, halves, rope, head_dim)
                 and sizes[0] == n_heads * head_dim and sizes[1] == sizes[2] == n_kv * head_dim):
-            group.refund("fwd", V + 1 - Q)
             raise _NotApplicable()
-        taken = V + 1 - Q
-        try:
-            out, t = _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope)
-            del weight
-            w_o = group.weight("fwd", O)
-            taken += 1
-            q = out[:, :bounds[1]].view(n_tok, n_heads, head_dim)
-            k = out[:, bounds[1]:bounds[2]].view(n_tok, n_kv, head_dim)
-            v = out[:, bounds[2]:].view(n_tok, n_kv, head_dim)
-            o = torch.empty(n_tok, n_heads, head_dim, dtype=torch.float16, device=x.device)
-            lse = torch.empty(n_heads, n_tok, dtype=torch.float32, device=x.device)
-            torch.ops.talm.attn_fwd(q, k, v, cu, max_len, scale, o, lse)
-            y = torch.empty(n_tok, w_o.shape[0], dtype=torch.float16, device=x.device)
-            torch.ops.talm.gemm(o.view(n_tok, -1), w_o, group.biases[O], 1, y)
-            del w_o
-        except Exception:
-            group.refund("fwd", taken)  # the per-node path takes them again
-            raise
+        out, t = _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope)
+        del weight
+        w_o = group.weight(O)
+        q = out[:, :bounds[1]].view(n_tok, n_heads, head_dim)
+        k = out[:, bounds[1]:bounds[2]].view(n_tok, n_kv, head_dim)
+        v = out[:, bounds[2]:].view(n_tok, n_kv, head_dim)
+        o = torch.empty(n_tok, n_heads, head_dim, dtype=torch.float16, device=x.device)
+        lse = torch.empty(n_heads, n_tok, dtype=torch.float32, device=x.device)
+        torch.ops.talm.attn_fwd(q, k, v, cu, max_len, scale, o, lse)
+        y = torch.empty(n_tok, w_o.shape[0], dtype=torch.float16, device=x.device)
+        torch.ops.talm.gemm(o.view(n_tok, -1), w_o, group.biases[O], 1, y)
+        del w_o
         saved = [x2, out, o, lse, cu]
         for k_ in range(len(adapters)):
             saved += [t[:, 16 * k_:16 * (k_ + 1)], halves[k_][0], halves[k_][1]]
@@ -471,7 +465,7 @@ class AttentionBlock(torch.autograd.Function):
             dy = dy.to(torch.float16)
         if dy.stride(1) != 1:
             dy = dy.contiguous()
-        w_o = group.weight("bwd", O)
+        w_o = group.weight(O)
         d_o = torch.empty(n_tok, w_o.shape[1], dtype=torch.float16, device=x2.device)
         torch.ops.talm.gemm(dy, w_o, None, 0, d_o)
         del w_o
@@ -489,11 +483,10 @@ class AttentionBlock(torch.autograd.Function):
                                 ctx.scale, dq.view(n_tok, nh, hd), dk.view(n_tok, nkv, hd),
                                 dv.view(n_tok, nkv, hd), ws)
         del ws, d_o
-        weight = group.span("bwd", Q, V + 1) if ctx.needs_input_grad[0] else None
+        weight = group.span(Q, V + 1) if ctx.needs_input_grad[0] else None
         wanted = [ctx.needs_input_grad[10 + i] for i in range(2 * len(ctx.adapters))]
         if weight is None and ctx.needs_input_grad[0]:
-            weights = [group.weight("bwd", i) for i in (Q, K, V)]
-            weight = torch.cat(weights, 0)
+            weight = torch.cat([group.weight(i) for i in (Q, K, V)], 0)
         dx, lora_grads = _mfma_backward_core((dq, dk, dv), x2, rest, cos, sin, weight,
                                              ctx.sizes, ctx.adapters, True, wanted, ctx.a_t)
         RAN["attn_kernel_bwd"] += 1
@@ -541,7 +534,7 @@ def _lora_state(attn):
 def qkv_plan(attn, x):
     """`qkv_plan_uncached` kept on the attention module for inputs of the same kind (device,
     dtype, width, autocast, the set of disabled components and the LoRA wrappers' mutable state);
-    the per-call conditions (hooks, the pass's split decision) are checked every time."""
+    the per-call condition (no module hooks) is checked every time."""
     key = (x.is_cuda, x.dtype, x.dim() >= 2, x.shape[-1], torch.is_autocast_enabled("cuda"),
            torch.get_autocast_dtype("cuda"), tuple(sorted(DISABLED)), _lora_state(attn))
     cached = attn.__dict__.get("_talm_qkv_plan")
@@ -551,7 +544,7 @@ def qkv_plan(attn, x):
         cached = (key, None if plan is None else plan[:3], modules)
         attn.__dict__["_talm_qkv_plan"] = cached
     plan, modules = cached[1], cached[2]
-    if plan is None or not _no_hooks(modules) or plan[0].split_now("fwd"):
+    if plan is None or not _no_hooks(modules):
         return None
     return plan
 
@@ -559,7 +552,7 @@ def qkv_plan(attn, x):
 def qkv_plan_uncached(attn, x):
     """(group, adapters, lora weights, modules) when q_proj, k_proj and v_proj are projections
     0, 1, 2 of one packed layer group, each plain or a LoRA layer `lora_plan` takes; else None
-    (solution/fused_proj.py:318-353). Hooks and the pass's split decision are the caller's."""
+    (solution/fused_proj.py:318-353). Hooks are the caller's."""
     from .lora import LoraLinear
 
     if not (x.is_cuda and x.dtype == torch.float16 and x.dim() >= 2) \
@@ -646,10 +639,6 @@ def _attention_block(attn, x, group, adapters, weights, rope, n_tok):
         if not fallback("attn_block", exc):
             raise
         return None
-    if torch.is_grad_enabled():
-        # the backward takes o_proj's weight whenever it runs, q|k|v's only for dX
-        group.expected_bwd += 3 * x.requires_grad + (
-            x.requires_grad or any(w.requires_grad for w in weights))
     COUNTS["attn"] += 1
     RAN["fused_proj"] += 1
     RAN["varlen_attn"] += 1
@@ -701,8 +690,6 @@ def patch_qwen2_attention():
                             past_key_values=past_key_values, **kwargs)
         COUNTS["attn"] += 1
         RAN["fused_proj"] += 1
-        if torch.is_grad_enabled() and hidden_states.requires_grad:
-            group.expected_bwd += 3
         hidden_shape = (*input_shape, -1, self.head_dim)
         query_states = q.view(hidden_shape).transpose(1, 2)
         key_states = k.view(hidden_shape).transpose(1, 2)

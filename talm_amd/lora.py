@@ -1,28 +1,33 @@
-"""The 4-bit projections that carry a LoRA adapter (q_proj, v_proj) as one autograd node.
+"""LoRA adapters on the 4-bit projections: PEFT's module layout, the fp16 adapter copies, and the
+fast path of a LoRA projection outside the fused q|k|v node.
 
-Mirrors solution/lora.py: `LoraProjectionTorch` runs PEFT's LoRA arithmetic op for op — the base
-GEMM on the layer group's dequantized weight, dropout, the two fp16 adapter GEMMs, `* scaling`
-folded into the add when it is a power of two >= 1 (exact), the fp16 add onto the base output —
-but keeps only the layer input x for the backward and replays the dropout there from the saved
-generator state (:151-231). The fp16 copies of the fp32 adapter weights come from
-`adapters.COPIES` (one launch per optimizer step for every adapter, :57-114).
+`LoraLinear` stands in for PEFT's LoRA wrapper of a 4-bit layer (PEFT and bitsandbytes are not
+available here): the attributes the reference reads (`base_layer`, `lora_A` / `lora_B` /
+`lora_dropout` keyed by adapter name, `scaling`, `active_adapters`, `disable_adapters`, `merged`)
+and PEFT's forward under fp16 autocast, result = base(x) + scaling * B(A(dropout(x))), as its own
+forward (the eager path every patched path is checked against).
 
-PEFT is not available here, so `LoraLinear` stands in for PEFT's LoRA wrapper of a 4-bit layer:
-the attributes the reference reads (`base_layer`, `lora_A`/`lora_B`/`lora_dropout` keyed by the
-adapter name, `scaling`, `active_adapters`, `disable_adapters`, `merged`) and PEFT's forward
-under fp16 autocast as its own forward.
+The reference runs such a projection as its own autograd node with PEFT's ops
+(`LoraProjectionTorch`, solution/lora.py:151-231). Here it is the q|k|v node of fused_proj.py
+with ONE projection and one adapter (`patch_lora`): without dropout, two MFMA launches forward —
+t = x A^T (talm_lora_down) and y = [x | s t] [W | B]^T + b (talm_qkv_lora_fwd: the adapter term
+accumulated with the base product and rounded once) — and on the backward u = s dy B
+(talm_lora_down), dx = dy W + u A (talm_qkv_lora_bwd_dx) and dA, dB (talm_lora_wgrad); with
+dropout, the node's PyTorch ops with the mask replayed from the saved generator state.
+
+The fp16 copies of the fp32 adapter weights come from `adapters.COPIES` (one launch per
+optimizer step for every adapter; solution/lora.py:57-114 keeps a cast cache instead).
 """
 
 import math
+from collections import namedtuple
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from .adapters import COPIES
 from .engaged import FELL_BACK, ON, RAN
 from .state import DISABLED, fallback
-
 
 _hooks = []
 
@@ -49,78 +54,10 @@ def install_cast_cache():
 
 
 def _power_of_two(value):
-    """A power of two >= 1: branch * value is exact in fp16, so one rounding of
-    out + value * branch equals PEFT's rounded product then rounded add (:140-148)."""
+    """Whether `value` is a power of two >= 1: then branch * value is exact in fp16, and one
+    rounding of out + value * branch equals PEFT's rounded product followed by a rounded add."""
     mantissa, _ = math.frexp(value)
     return value >= 1 and mantissa == 0.5
-
-
-class LoraProjectionTorch(torch.autograd.Function):
-    """y = x W^T + bias + scaling * B(A(dropout(x))) on a packed 4-bit base (solution/lora.py:
-    151-231): PEFT's ops, keeping only x (and the generator state for the dropout replay)."""
-
-    @staticmethod
-    def forward(ctx, x, x_base, lora_a, lora_b, group, idx, scaling, p):
-        ctx.rng_state = None
-        fetched = False
-        try:
-            x2 = x.reshape(-1, x.shape[-1])
-            weight = group.weight("fwd", idx)
-            fetched = True
-            out = F.linear(x2, weight, group.biases[idx])
-            a16, b16 = _to_half(lora_a, lora_b)
-            if p > 0:
-                ctx.rng_state = torch.cuda.get_rng_state(x.device)
-                xd = torch.native_dropout(x2, p, True)[0]
-            else:
-                xd = x2
-            t = torch.mm(xd, a16.t())
-            del xd
-            branch = torch.mm(t, b16.t())
-            if _power_of_two(scaling):
-                out.add_(branch, alpha=scaling)
-            else:
-                out.add_(branch.mul_(scaling))
-        except Exception:
-            if fetched:
-                group.refund("fwd")
-            if ctx.rng_state is not None:
-                torch.cuda.set_rng_state(ctx.rng_state, x.device)
-            raise
-        ctx.save_for_backward(x2, t, a16, b16)
-        ctx.group, ctx.idx, ctx.scaling, ctx.p = group, idx, scaling, p
-        ctx.x_shape = x.shape
-        return out.view(*x.shape[:-1], out.shape[1])
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        x2, t, a16, b16 = ctx.saved_tensors
-        dy = grad_out.reshape(-1, grad_out.shape[-1])
-        if dy.dtype != torch.float16:
-            dy = dy.to(torch.float16)
-        mask = None
-        xd = x2
-        if ctx.rng_state is not None:
-            device = x2.device
-            current = torch.cuda.get_rng_state(device)
-            torch.cuda.set_rng_state(ctx.rng_state, device)
-            try:
-                xd, mask = torch.native_dropout(x2, ctx.p, True)
-            finally:
-                torch.cuda.set_rng_state(current, device)
-        g = dy * ctx.scaling
-        u = torch.mm(g, b16)
-        dx_lora = dx_base = None
-        if ctx.needs_input_grad[0]:
-            dx_lora = torch.mm(u, a16)
-            if mask is not None:
-                dx_lora = torch.ops.aten.native_dropout_backward(dx_lora, mask, 1.0 / (1.0 - ctx.p))
-            dx_lora = dx_lora.view(ctx.x_shape)
-        if ctx.needs_input_grad[1]:
-            dx_base = torch.mm(dy, ctx.group.weight("bwd", ctx.idx)).view(ctx.x_shape)
-        da = torch.mm(u.t(), xd).float() if ctx.needs_input_grad[2] else None
-        db = torch.mm(g.t(), t).float() if ctx.needs_input_grad[3] else None
-        return dx_lora, dx_base, da, db, None, None, None, None
 
 
 class LoraLinear(nn.Module):
@@ -163,54 +100,79 @@ class LoraLinear(nn.Module):
         return result
 
 
-def _autocast_fp16():
-    return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.float16
+# What the fast path needs of one LoRA projection: its packed base (group, index in the group),
+# the fp32 adapter weights, the scaling and the dropout rate in force.
+Adapter = namedtuple("Adapter", "group idx lora_a lora_b scaling p")
 
 
-def lora_plan(module, x):
-    """(group, idx, A, B, scaling, p) when this LoRA layer can take the node, else None
-    (solution/lora.py:241-281)."""
-    if not (x.is_cuda and x.dtype == torch.float16 and x.dim() >= 2):
-        return None
+def _dropout_rate(module):
+    """The dropout rate in force (0 for Identity or in eval mode), None for another module."""
+    if isinstance(module, nn.Identity):
+        return 0.0
+    if isinstance(module, nn.Dropout):
+        return float(module.p) if module.training else 0.0
+    return None
+
+
+def _single_adapter(module):
+    """The one plain adapter (name) the LoRA layer applies, or None: exactly one active adapter,
+    not merged, not disabled, without a weight-decomposition variant or a bias."""
     if getattr(module, "disable_adapters", True) or getattr(module, "merged", True):
         return None
-    adapters = module.active_adapters
-    if len(adapters) != 1:
+    active = list(module.active_adapters)
+    if len(active) != 1:
         return None
-    name = adapters[0]
+    name = active[0]
     if name not in module.lora_A or name in getattr(module, "lora_variant", {}) \
             or getattr(module, "lora_bias", {}).get(name, False):
         return None
+    return name
+
+
+def lora_plan(module, x):
+    """An `Adapter` when the LoRA layer's forward on `x` can run as the package's node: fp16
+    CUDA input under fp16 autocast, a packed 4-bit base whose shape matches, one plain rank-r
+    adapter with bias-free fp32 A [r, in] and B [out, r], a dropout rate in [0, 1). Else None
+    (the layer's own forward runs; the reference's conditions, solution/lora.py:241-281)."""
+    if not (x.is_cuda and x.dtype == torch.float16 and x.dim() >= 2) or "qgroup" in DISABLED:
+        return None
+    if not (torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == torch.float16):
+        return None
+    name = _single_adapter(module)
     tag = getattr(module.base_layer, "_solution_group", None)
-    if tag is None or "qgroup" in DISABLED or not _autocast_fp16():
+    if name is None or tag is None:
         return None
-    lin_a, lin_b = module.lora_A[name], module.lora_B[name]
-    if not isinstance(lin_a, nn.Linear) or not isinstance(lin_b, nn.Linear) \
-            or lin_a.bias is not None or lin_b.bias is not None:
+    down, up = module.lora_A[name], module.lora_B[name]
+    if not (isinstance(down, nn.Linear) and isinstance(up, nn.Linear)) \
+            or down.bias is not None or up.bias is not None:
         return None
-    lora_a, lora_b = lin_a.weight, lin_b.weight
-    rank, n_in = lora_a.shape
-    if lora_b.shape[1] != rank or n_in != x.shape[-1] or lora_a.dtype != torch.float32 \
-            or lora_b.dtype != torch.float32 or not lora_a.is_cuda:
-        return None
+    lora_a, lora_b = down.weight, up.weight
     group, idx = tag
-    if tuple(group.shapes[idx]) != (lora_b.shape[0], n_in):
+    rank, n_in = lora_a.shape
+    if lora_a.dtype != torch.float32 or lora_b.dtype != torch.float32 or not lora_a.is_cuda \
+            or tuple(lora_b.shape) != (group.shapes[idx][0], rank) or n_in != x.shape[-1] \
+            or group.shapes[idx][1] != n_in:
         return None
-    dropout = module.lora_dropout[name]
-    if isinstance(dropout, nn.Dropout):
-        p = float(dropout.p) if dropout.training else 0.0
-    elif isinstance(dropout, nn.Identity):
-        p = 0.0
-    else:
+    p = _dropout_rate(module.lora_dropout[name])
+    if p is None or not 0.0 <= p < 1.0:
         return None
-    if not 0.0 <= p < 1.0:
-        return None
-    return group, idx, lora_a, lora_b, float(module.scaling[name]), p
+    return Adapter(group, idx, lora_a, lora_b, float(module.scaling[name]), p)
+
+
+def lora_projection(x, plan):
+    """y = x W^T + b + scaling * B(A(dropout(x))) as the q|k|v node on one projection."""
+    from .fused_proj import FusedProjections
+
+    (y,) = FusedProjections.apply(x, plan.group, plan.idx, plan.idx + 1,
+                                  ((0, plan.scaling, plan.p),), (), None, 0, plan.lora_a,
+                                  plan.lora_b)
+    return y
 
 
 def patch_lora():
-    """Route LoraLinear.forward through `LoraProjectionTorch` in the plain case
-    (solution/lora.py:284-321)."""
+    """`LoraLinear.forward` through `lora_projection` when `lora_plan` takes the call; the
+    layer's own forward otherwise (a failure turns "lora" off, state.py)."""
     install_cast_cache()
     ON.add("lora")
     if getattr(LoraLinear.forward, "_solution_lora", False):
@@ -218,19 +180,18 @@ def patch_lora():
     original = LoraLinear.forward
 
     def forward(self, x, *args, **kwargs):
-        plan = None if (args or kwargs or "lora" in DISABLED) else lora_plan(self, x)
+        plan = None
+        if not (args or kwargs) and "lora" not in DISABLED:
+            plan = lora_plan(self, x)
         if plan is not None:
-            group, idx, lora_a, lora_b, scaling, p = plan
             try:
-                out = LoraProjectionTorch.apply(x, x, lora_a, lora_b, group, idx, scaling, p)
+                y = lora_projection(x, plan)
             except Exception as exc:  # noqa: BLE001 - state.py convention
                 if not fallback("lora", exc):
                     raise
             else:
-                if torch.is_grad_enabled() and x.requires_grad:
-                    group.expected_bwd += 1
                 RAN["lora"] += 1
-                return out
+                return y
         FELL_BACK["lora"] += 1
         return original(self, x, *args, **kwargs)
 

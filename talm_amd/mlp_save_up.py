@@ -21,10 +21,10 @@ class SwiGLUSaveUp(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, group):
-        weight = group.weight("fwd", GATE)
+        weight = group.weight(GATE)
         gate = F.linear(x, weight, group.biases[GATE])
         del weight
-        up = F.linear(x, group.weight("fwd", UP), group.biases[UP])
+        up = F.linear(x, group.weight(UP), group.biases[UP])
         swiglu_fwd(gate, up, gate)
         ctx.group = group
         ctx.save_for_backward(x, up)
@@ -34,14 +34,14 @@ class SwiGLUSaveUp(torch.autograd.Function):
     def backward(ctx, grad):
         x, up = ctx.saved_tensors
         group = ctx.group
-        weight = group.weight("bwd", GATE)
+        weight = group.weight(GATE)
         gate = F.linear(x, weight, group.biases[GATE])
         grad = grad.to(gate.dtype).contiguous()
         swiglu_bwd(grad, gate, up, gate, up)
         del grad
         dx = torch.matmul(gate, weight)
         del gate, weight
-        dx += torch.matmul(up, group.weight("bwd", UP))
+        dx += torch.matmul(up, group.weight(UP))
         return dx, None
 
 
@@ -84,7 +84,6 @@ def patch_qwen2_mlp_save_up():
                 if not fallback("mlp_save_up", exc):
                     raise
             else:
-                group.expected_bwd += 2
                 RAN["mlp_save_up"] += 1
                 return self.down_proj(act)
         FELL_BACK["mlp_save_up"] += 1

@@ -49,8 +49,9 @@ LAST_STEP = []  # the per-token outputs of the last fused forward (Soup's Chunke
 
 
 def _restart(device, rng_state):
-    """Before a forward that failed part-way runs again: the generator back to `rng_state` and
-    the layer groups' pass bookkeeping reset (solution/patches.py:55-63)."""
+    """Before a forward that failed part-way runs again: the generator back to `rng_state`
+    (the same dropout masks are drawn again) and the resident dequantized layer dropped
+    (solution/patches.py:55-63)."""
     import torch
 
     from . import qgroup
@@ -178,7 +179,7 @@ def _static_forward(self, input_ids, mask, labels, shift, n_tokens, num_items, k
     from .engaged import RAN
     from .fused_head import fused_head_loss
     from .rmsnorm import link_next_norms
-    from .unpad import rows_context_static, unpad_static
+    from .unpad import rows_context_static, static_max_len, unpad_static
 
     import torch
 
@@ -189,7 +190,7 @@ def _static_forward(self, input_ids, mask, labels, shift, n_tokens, num_items, k
     RAN["unpad"] += 1
     link_next_norms(self.model)
     stage.append("unpadded")
-    with rows_context_static(cu, seq, n_tokens):
+    with rows_context_static(cu, static_max_len(seq), n_tokens):
         outputs = self.model(input_ids=ids[None], attention_mask={"full_attention": None},
                              position_ids=positions, past_key_values=None, inputs_embeds=None,
                              use_cache=False, **kwargs)
@@ -266,10 +267,11 @@ def apply():
     from . import _lib
 
     _lib.lib()
-    with installing("gemm_table"):
-        from . import gemm_tuning
+    if not _off("GEMM_TABLE"):
+        with installing("gemm_table"):
+            from . import gemm_tuning
 
-        gemm_tuning.load()
+            gemm_tuning.load()
     if not _off("SWIGLU_INPLACE"):
         with installing("swiglu"):
             from .swiglu_inplace import patch_qwen2_mlp_inplace
@@ -332,7 +334,7 @@ def unapply():
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
     from transformers.models.qwen2 import modeling_qwen2
 
-    from . import rmsnorm
+    from . import qgroup, rmsnorm
     from .lora import LoraLinear
     from .nf4_linear import Linear4bit
 
@@ -346,4 +348,5 @@ def unapply():
     modeling_qwen2.apply_rotary_pos_emb = _root(modeling_qwen2.apply_rotary_pos_emb)
     ALL_ATTENTION_FUNCTIONS["sdpa"] = _root(ALL_ATTENTION_FUNCTIONS["sdpa"])
     rmsnorm.LAYER_FORWARDS.clear()
+    qgroup.release()
     ON.clear()

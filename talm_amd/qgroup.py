@@ -1,40 +1,50 @@
-"""One NF4 dequantization launch per decoder layer and pass (the HIP grouped kernel).
+"""The seven 4-bit projections of a decoder layer as one packed weight set, dequantized by ONE
+kernel launch (talm_nf4_group_dequant, talm_amd/csrc/nf4.hip).
 
-Mirrors solution/qgroup.py: the seven 4-bit projections of a layer (q, k, v, o, gate, up, down)
-are packed into one contiguous set of buffers (the parameters become views of it, no memory is
-duplicated, :148-160) and dequantized by ONE launch when the layer's first projection runs, in
-the forward and in the backward; the other projections slice the cached fp16 buffer, which is
-dropped after its last expected use (`_take`, :273-289). The reference dequantizes the last
-layers (at the memory peak) projection by projection (`SPLIT_LAYERS`, :68-69, `dequantize_one`,
-:200-211) to spare a T4's 16 GB one layer's fp16 buffer (94 MB for Qwen2.5-1.5B); with 288 GB
-of HBM that trade only costs launches, so here it is opt-in (SOLUTION_SPLIT_DEQUANT=1).
+What stays as in the reference (solution/qgroup.py): the launch site `launch(...)` with its
+signature (:94-99), the packing of q, k, v, o, gate, up, down into contiguous packed / absmax8 /
+absmax2 buffers with the modules' parameters turned into views of them (no memory duplicated,
+:148-160), `GroupLinear` (y = x W^T + b, dx = dy W) and `span` (adjacent projections as one
+[sum of out, in] view, for the q|k|v and gate|up GEMMs).
 
-The kernel (talm_nf4_group_dequant, talm_amd/csrc/nf4.hip) rebuilds each block's fp32 scale from
-the double-quantized absmax exactly as the reference kernel does (:72-91) and matches it bit for
-bit; `launch` keeps the reference's launch-site signature (:94-99).
+What this build does its own way is the lifetime of the fp16 weights. The reference keeps a
+cache per pass and counts uses (the forward's seven, the backward's expected uses reported by
+every node, refunds when a node fails, per-projection "split" passes for the last layers at a
+T4's memory peak: :263-343). Here each GPU holds exactly ONE resident dequantized layer:
 
-Graceful degradation (state.py): an unexpected error in `weight` turns "qgroup" off and the
-weight comes from the per-projection dequantization of that projection (the same values).
+- a decoder layer's forward makes its group resident when it begins (`enter_layer`);
+- every projection request, forward or backward, reads the resident buffer when its group is
+  the resident one, and otherwise dequantizes its group (one launch) and makes it resident.
+
+Autograd runs the decoder's backward layer by layer (each layer's input gradient needs its whole
+branch), so the backward dequantizes each layer once, and the last layer's forward buffer serves
+its backward with no launch at all. Correctness never depends on how often a projection is used:
+a request from a group that is not resident simply dequantizes it again (a checkpointed layer's
+recomputation, a fallback path, two models interleaved), so nothing is counted, refunded or reset
+when a step is cut short. The price is that one fp16 layer (94 MB for Qwen2.5-1.5B) stays
+allocated between steps, against 288 GB of HBM.
+
+Graceful degradation (state.py): an unexpected error here turns "qgroup" off; each projection
+then takes the per-projection dequantization (nf4_dequant.py, the same values) and the 4-bit
+layer its own forward.
 """
 
-import os
 import weakref
+from collections import namedtuple
 
 import torch
 
 from . import _ops  # noqa: F401 - registers torch.ops.talm.*
 from .engaged import FELL_BACK, ON, RAN
 from .nf4_dequant import dequantize_4bit
-from .quant import NF4_LEVELS
 from .state import DISABLED, fallback
 
-ROWS = 64  # the reference kernel's tile (rows of one program); kept as the packing granule
 NSEG = 7
-_SPLIT_ON = os.environ.get("SOLUTION_SPLIT_DEQUANT") == "1" \
-    and os.environ.get("SOLUTION_DISABLE_SPLIT_DEQUANT") != "1"
-SPLIT_LAYERS = {"fwd": 1 if _SPLIT_ON else 0, "bwd": 2 if _SPLIT_ON else 0}
 PROJECTIONS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
                "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+# device -> (group, fp16 buffer of all its weights): the one dequantized layer per GPU
+_RESIDENT = {}
 
 
 def launch(packed, absmax8, code, absmax2, offset2, levels, out, n_rows, qblock, qblock2):
@@ -47,190 +57,162 @@ def launch(packed, absmax8, code, absmax2, offset2, levels, out, n_rows, qblock,
                                      int(qblock), int(qblock2))
 
 
-def _state_ok(state, first):
-    return (state is not None and state.quant_type == "nf4" and state.nested
-            and state.blocksize == first.blocksize
-            and state.state2.blocksize == first.state2.blocksize
-            and len(state.shape) == 2 and state.absmax.dtype == torch.uint8
-            and state.state2.absmax.dtype == torch.float32
-            and torch.equal(state.state2.code, first.state2.code))
+def release():
+    """Drop every GPU's resident layer (a forward that failed part-way is about to run again;
+    the patches are being removed)."""
+    _RESIDENT.clear()
+
+
+def reset_passes():
+    """The reference's name for the step-boundary reset (solution/qgroup.py:358-366)."""
+    release()
+
+
+def _nf4_layout(state):
+    """(blocksize, second-level blocksize) of an NF4 state with double-quantized uint8 absmax,
+    else None."""
+    if state is None or getattr(state, "quant_type", None) != "nf4" \
+            or not getattr(state, "nested", False) or len(getattr(state, "shape", ())) != 2:
+        return None
+    inner = state.state2
+    if state.absmax.dtype != torch.uint8 or inner.absmax.dtype != torch.float32:
+        return None
+    return state.blocksize, inner.blocksize
+
+
+# One projection inside the group: its element range, its [out, in] shape, its fp16 bias.
+Segment = namedtuple("Segment", "start stop shape bias")
 
 
 class LayerGroup:
-    """The seven 4-bit projections of one decoder layer, packed, with per-pass caches."""
+    """The seven 4-bit projections of one decoder layer, packed into one set of buffers."""
 
     def __init__(self, modules):
-        assert len(modules) == NSEG
+        if len(modules) != NSEG:
+            raise ValueError(f"a layer group has {NSEG} projections, got {len(modules)}")
         states = [m.weight.quant_state for m in modules]
-        first = states[0]
-        if not all(_state_ok(s, first) for s in states):
-            raise ValueError("unsupported quant state")
-        if first.blocksize % 8 or first.blocksize & (first.blocksize - 1):
-            raise ValueError("block size is not a power of two >= 8")
-        double = first.blocksize * first.state2.blocksize
-        for s in states:
-            if (s.shape[0] * s.shape[1]) % double:
-                raise ValueError("weight size not a multiple of the absmax double-block")
-        device = modules[0].weight.device
-        self.qblock, self.qblock2 = first.blocksize, first.state2.blocksize
-        self.shapes = [tuple(s.shape) for s in states]
-        self.numels = [a * b for a, b in self.shapes]
-        self.elem_bounds = [0]
-        for n in self.numels:
-            self.elem_bounds.append(self.elem_bounds[-1] + n)
-        total = self.elem_bounds[-1]
-        packed = torch.cat([m.weight.data.view(-1) for m in modules])
-        absmax8 = torch.cat([s.absmax.view(-1) for s in states])
-        absmax2 = torch.cat([s.state2.absmax.view(-1) for s in states])
-        p = a = c = 0
+        layouts = {_nf4_layout(s) for s in states}
+        if len(layouts) != 1 or None in layouts:
+            raise ValueError("the projections do not share one NF4 double-quant layout")
+        (qblock, qblock2), = layouts
+        code = states[0].state2.code
+        if any(not torch.equal(s.state2.code, code) for s in states[1:]):
+            raise ValueError("the projections use different second-level code tables")
+        if qblock < 8 or qblock & (qblock - 1):
+            raise ValueError(f"block size {qblock} is not a power of two >= 8")
+        span2 = qblock * qblock2  # weights per second-level scale
+        segments, start = [], 0
         for m, s in zip(modules, states):
             n = s.shape[0] * s.shape[1]
-            m.weight.data = packed[p:p + n // 2].view(-1, 1)
-            s.absmax = absmax8[a:a + n // self.qblock]
-            s.state2.absmax = absmax2[c:c + n // double]
-            p += n // 2
-            a += n // self.qblock
-            c += n // double
-        self.packed, self.absmax8, self.absmax2 = packed, absmax8, absmax2
-        self.code = first.state2.code.contiguous()
-        offsets = torch.stack([s.offset.reshape(()).to(torch.float32) for s in states]).to(device)
-        self.offset2 = torch.cat([offsets[i:i + 1].expand(n // double)
-                                  for i, n in enumerate(self.numels)]).contiguous()
-        self.n_rows = total // self.qblock
-        if total >= 2 ** 40:
+            if n % span2:
+                raise ValueError(f"{n} weights are not whole second-level blocks of {span2}")
+            bias = None if m.bias is None else m.bias.detach().to(torch.float16)
+            segments.append(Segment(start, start + n, tuple(s.shape), bias))
+            start += n
+        if start >= 2 ** 40:
             raise ValueError("layer too large")
-        self.levels = None
-        self.biases = [None if m.bias is None else m.bias.detach().to(torch.float16)
-                       for m in modules]
+        self.qblock, self.qblock2, self.segments = qblock, qblock2, segments
+        self.numel = start
+        self.device = modules[0].weight.device
+        # one buffer per field, in projection order; each parameter becomes a view of its part
+        self.packed = torch.cat([m.weight.data.reshape(-1) for m in modules])
+        self.absmax8 = torch.cat([s.absmax.reshape(-1) for s in states])
+        self.absmax2 = torch.cat([s.state2.absmax.reshape(-1) for s in states])
+        for m, s, seg in zip(modules, states, segments):
+            m.weight.data = self.packed[seg.start // 2:seg.stop // 2].view(-1, 1)
+            s.absmax = self.absmax8[seg.start // qblock:seg.stop // qblock]
+            s.state2.absmax = self.absmax2[seg.start // span2:seg.stop // span2]
+        self.code = code.contiguous()
+        # each projection's offset repeated over its second-level blocks: no lookup per block
+        self.offset2 = torch.cat([
+            s.offset.reshape(1).to(device=self.device, dtype=torch.float32)
+            .expand((seg.stop - seg.start) // span2) for s, seg in zip(states, segments)])
         self.modules = [weakref.ref(m) for m in modules]
-        self._span_biases = {}
-        self.cache = {"fwd": [None, 0], "bwd": [None, 0]}
-        self.expected_bwd = 0
-        self.split_left = 0
-        self.checkpointed = False
-        self.depth = None
-        self.row_bounds = [e // self.qblock for e in self.elem_bounds]
-        self.splittable = all(r0 % self.qblock2 == 0 for r0 in self.row_bounds[:-1])
+        self._bias_spans = {}
 
-    def dequantize_all(self):
-        out = torch.empty(self.elem_bounds[-1], dtype=torch.float16, device=self.packed.device)
-        launch(self.packed, self.absmax8, self.code, self.absmax2, self.offset2, self.levels, out,
-               self.n_rows, self.qblock, self.qblock2)
+    # -- shapes ----------------------------------------------------------------------------------
+    @property
+    def shapes(self):
+        return [seg.shape for seg in self.segments]
+
+    @property
+    def biases(self):
+        return [seg.bias for seg in self.segments]
+
+    # -- dequantization ----------------------------------------------------------------------------
+    def dequantize(self, first=0, last=NSEG):
+        """fp16 weights of projections first .. last - 1 (one launch): the kernel runs on their
+        slice of the packed buffers, which starts on a second-level block."""
+        lo, hi = self.segments[first].start, self.segments[last - 1].stop
+        out = torch.empty(hi - lo, dtype=torch.float16, device=self.packed.device)
+        row0 = lo // self.qblock
+        launch(self.packed[lo // 2:], self.absmax8[row0:], self.code,
+               self.absmax2[row0 // self.qblock2:], self.offset2[row0 // self.qblock2:], None,
+               out, (hi - lo) // self.qblock, self.qblock, self.qblock2)
         return out
 
     def dequantize_one(self, idx):
-        """fp16 [out, in] of projection `idx` alone: the same kernel on that weight's slice of
-        the packed buffers (it starts on an absmax2 block, so the block indices stay right)."""
-        r0, r1 = self.row_bounds[idx], self.row_bounds[idx + 1]
-        b0 = r0 // self.qblock2
-        out = torch.empty(self.numels[idx], dtype=torch.float16, device=self.packed.device)
-        launch(self.packed[r0 * (self.qblock // 2):], self.absmax8[r0:], self.code,
-               self.absmax2[b0:], self.offset2[b0:], self.levels, out, r1 - r0, self.qblock,
-               self.qblock2)
-        return out.view(self.shapes[idx])
+        return self.dequantize(idx, idx + 1).view(self.segments[idx].shape)
 
-    def weight(self, which, idx):
-        """fp16 [out, in] of projection `idx`; one dequant launch per pass per layer. Once
-        "qgroup" is off, the per-projection dequantization of that projection (same values)."""
-        if "qgroup" not in DISABLED:
-            try:
-                return self._weight(which, idx)
-            except Exception as exc:  # noqa: BLE001 - state.py convention
-                if not fallback("qgroup", exc):
-                    raise
-        return self.reference_weight(idx)
-
-    def reference_weight(self, idx):
-        if self.cache["fwd"][0] is not None or self.cache["bwd"][0] is not None:
-            self.reset()
-        FELL_BACK["group"] += 1
-        module = self.modules[idx]()
-        return dequantize_4bit(module.weight.data, module.weight.quant_state)
-
-    def reset(self):
-        self.cache = {"fwd": [None, 0], "bwd": [None, 0]}
-        self.expected_bwd = 0
-        self.split_left = 0
-
-    def refund(self, which, uses=1):
-        entry = self.cache[which]
-        if entry[0] is not None:
-            entry[1] += uses
-
-    def start_forward(self, checkpointed=False):
-        fwd, bwd = self.cache["fwd"], self.cache["bwd"]
-        fwd[0] = bwd[0] = None
-        fwd[1] = bwd[1] = 0
-        self.expected_bwd = self.split_left = 0
-        self.checkpointed = checkpointed
-
-    def split_now(self, which):
-        return (self.cache[which][0] is None and self.depth is not None
-                and self.depth < SPLIT_LAYERS[which] and self.splittable) or self.checkpointed
-
-    def _take(self, which, uses):
-        entry = self.cache[which]
-        if entry[0] is None:
-            entry[0] = self.dequantize_all()
-            RAN["group"] += 1
-            if which == "fwd":
-                entry[1] = NSEG
-            else:
-                entry[1] = max(self.expected_bwd, 1)
-                self.expected_bwd = 0
-        buf = entry[0]
-        entry[1] -= uses
-        if entry[1] <= 0:
-            entry[0] = None
+    def resident(self):
+        """This layer's fp16 weights [numel]: the GPU's resident buffer when it is this group's,
+        else one launch that makes it so."""
+        held = _RESIDENT.get(self.device)
+        if held is not None and held[0] is self:
+            return held[1]
+        buf = self.dequantize()
+        RAN["group"] += 1
+        _RESIDENT[self.device] = (self, buf)
         return buf
 
-    def _weight(self, which, idx):
-        if self.split_now(which):
-            if self.checkpointed:
-                self.expected_bwd = 0
-                if not self.splittable:
-                    RAN["group"] += 1
-                    full = self.dequantize_all()
-                    return full[self.elem_bounds[idx]:self.elem_bounds[idx + 1]].view(
-                        self.shapes[idx])
-            elif which == "bwd":
-                if self.split_left == 0:
-                    self.split_left = max(self.expected_bwd, 1)
-                    self.expected_bwd = 0
-                self.split_left -= 1
-            RAN["split"] += 1
-            return self.dequantize_one(idx)
-        buf = self._take(which, 1)
-        return buf[self.elem_bounds[idx]:self.elem_bounds[idx + 1]].view(self.shapes[idx])
+    def begin_forward(self):
+        """The layer's forward begins: its weights become resident now, with one launch."""
+        held = _RESIDENT.pop(self.device, None)
+        del held  # the previous layer's buffer goes back to the allocator first
+        self.resident()
 
-    def span(self, which, first, last):
-        """fp16 [sum of out, in] of the adjacent projections first .. last - 1 as ONE view of the
-        layer's buffer, counted as last - first uses; None in a split pass or once off."""
+    # -- views -------------------------------------------------------------------------------------
+    def span(self, first, last):
+        """fp16 [sum of out, in] of the adjacent projections first .. last - 1 as one view of the
+        resident buffer; None once "qgroup" is off or when dequantization fails (state.py), and
+        the caller then takes them one at a time with `weight`."""
         if "qgroup" in DISABLED:
             return None
         try:
-            if self.split_now(which):
-                return None
-            buf = self._take(which, last - first)
+            buf = self.resident()
         except Exception as exc:  # noqa: BLE001 - state.py convention
             if not fallback("qgroup", exc):
                 raise
             return None
-        rows = sum(self.shapes[i][0] for i in range(first, last))
-        return buf[self.elem_bounds[first]:self.elem_bounds[last]].view(rows, self.shapes[first][1])
+        segs = self.segments[first:last]
+        rows = sum(seg.shape[0] for seg in segs)
+        return buf[segs[0].start:segs[-1].stop].view(rows, segs[0].shape[1])
+
+    def weight(self, idx):
+        """fp16 [out, in] of projection `idx` (the per-projection dequantization once "qgroup"
+        is off: the same values)."""
+        view = self.span(idx, idx + 1)
+        return view if view is not None else self.reference_weight(idx)
+
+    def reference_weight(self, idx):
+        FELL_BACK["group"] += 1
+        module = self.modules[idx]()
+        return dequantize_4bit(module.weight.data, module.weight.quant_state)
 
     def span_bias(self, first, last):
+        """The fp16 biases of projections first .. last - 1 end to end (zeros stand in for a
+        projection without one: adding 0 is exact), or None when none has one; built once."""
         key = (first, last)
-        if key not in self._span_biases:
-            parts = self.biases[first:last]
-            if all(b is None for b in parts):
-                self._span_biases[key] = None
+        if key not in self._bias_spans:
+            segs = self.segments[first:last]
+            if all(seg.bias is None for seg in segs):
+                self._bias_spans[key] = None
             else:
-                ref = next(b for b in parts if b is not None)
-                self._span_biases[key] = torch.cat([
-                    b if b is not None else ref.new_zeros(self.shapes[first + i][0])
-                    for i, b in enumerate(parts)])
-        return self._span_biases[key]
+                self._bias_spans[key] = torch.cat([
+                    seg.bias if seg.bias is not None else
+                    torch.zeros(seg.shape[0], dtype=torch.float16, device=self.device)
+                    for seg in segs])
+        return self._bias_spans[key]
 
 
 def _rows(t):
@@ -262,25 +244,12 @@ class GroupLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, group, idx):
         ctx.group, ctx.idx = group, idx
-        return linear(x, group.weight("fwd", idx), group.biases[idx])
+        return linear(x, group.weight(idx), group.biases[idx])
 
     @staticmethod
     def backward(ctx, grad_out):
-        weight = ctx.group.weight("bwd", ctx.idx)
+        weight = ctx.group.weight(ctx.idx)
         return matmul(grad_out.to(weight.dtype), weight), None, None
-
-
-_GROUPS = []
-
-
-def reset_passes():
-    alive = []
-    for ref in _GROUPS:
-        group = ref()
-        if group is not None:
-            group.reset()
-            alive.append(ref)
-    _GROUPS[:] = alive
 
 
 def _linear4bit(module):
@@ -290,63 +259,60 @@ def _linear4bit(module):
     return base if isinstance(base, Linear4bit) else None
 
 
+def _find(layer, path):
+    obj = layer
+    for part in path.split("."):
+        obj = getattr(obj, part, None)
+        if obj is None:
+            return None
+    return obj
+
+
 def _pack(layer):
+    """The decoder layer's LayerGroup, or None when its projections are not seven frozen fp16
+    4-bit layers of one layout (each projection then runs its own layer's forward)."""
     modules = []
     for path in PROJECTIONS:
-        obj = layer
-        for part in path.split("."):
-            obj = getattr(obj, part, None)
-            if obj is None:
-                return None
-        base = _linear4bit(obj)
-        if base is None or base.weight.requires_grad or not base.weight.is_cuda:
-            return None
-        if base.bias is not None and base.bias.requires_grad:
-            return None
-        if getattr(base, "compute_dtype", None) not in (None, torch.float16):
+        base = _find(layer, path)
+        base = None if base is None else _linear4bit(base)
+        if base is None or base.weight.requires_grad or not base.weight.is_cuda \
+                or (base.bias is not None and base.bias.requires_grad) \
+                or getattr(base, "compute_dtype", None) not in (None, torch.float16):
             return None
         modules.append(base)
     try:
         group = LayerGroup(modules)
     except ValueError:
         return None
-    attn = getattr(layer, "self_attn", None)
-    layer_idx = getattr(attn, "layer_idx", None)
-    n_layers = getattr(getattr(attn, "config", None), "num_hidden_layers", None)
-    if isinstance(layer_idx, int) and isinstance(n_layers, int) and 0 <= layer_idx < n_layers:
-        group.depth = n_layers - 1 - layer_idx
     for idx, base in enumerate(modules):
         base._solution_group = (group, idx)
-    _GROUPS.append(weakref.ref(group))
     return group
 
 
 def setup_layer(layer):
-    if getattr(layer, "_solution_group_done", False):
-        return
-    layer._solution_group_done = True
-    layer._solution_layer_group = _pack(layer)
+    if not getattr(layer, "_solution_group_done", False):
+        layer._solution_group_done = True
+        layer._solution_layer_group = _pack(layer)
 
 
 def enter_layer(layer):
-    """The decoder layer's forward begins: pack on first use, then start its passes afresh."""
+    """The decoder layer's forward begins: pack on first use, then make its weights resident."""
     if "qgroup" in DISABLED:
         return
     try:
-        if not getattr(layer, "_solution_group_done", False):
-            setup_layer(layer)
-        group = getattr(layer, "_solution_layer_group", None)
+        setup_layer(layer)
+        group = layer._solution_layer_group
         if group is not None:
-            group.start_forward(bool(getattr(layer, "training", False)
-                                     and getattr(layer, "gradient_checkpointing", False)))
+            group.begin_forward()
     except Exception as exc:  # noqa: BLE001 - state.py convention
         if not fallback("qgroup", exc):
             raise
 
 
 def patch_group_dequant():
-    """`Qwen2DecoderLayer.forward` packs its layer on first use (enter_layer); the 4-bit linear
-    layer routes packed modules through GroupLinear for fp16 inputs (solution/qgroup.py:498-545)."""
+    """`Qwen2DecoderLayer.forward` makes its layer's weights resident as it begins; the 4-bit
+    linear layer routes packed modules through GroupLinear for fp16 inputs
+    (solution/qgroup.py:498-545)."""
     from transformers.models.qwen2 import modeling_qwen2
 
     from .nf4_linear import Linear4bit
@@ -374,14 +340,10 @@ def patch_group_dequant():
                 and x.dtype == torch.float16:
             group, idx = tag
             try:
-                out = GroupLinear.apply(x, group, idx)
+                return GroupLinear.apply(x, group, idx)
             except Exception as exc:  # noqa: BLE001 - state.py convention
                 if not fallback("qgroup", exc):
                     raise
-            else:
-                if torch.is_grad_enabled() and x.requires_grad:
-                    group.expected_bwd += 1
-                return out
         FELL_BACK["group"] += 1
         return lin_forward(self, x)
 
@@ -389,7 +351,3 @@ def patch_group_dequant():
     linear_forward._original = lin_forward
     Linear4bit.forward = linear_forward
     return True
-
-
-def nf4_levels(device):
-    return torch.tensor(NF4_LEVELS, dtype=torch.float32, device=device)

@@ -13,7 +13,6 @@ the synthetic model: bitsandbytes is not available here, so its quantizer's exac
 is not reproduced (the dequantization, which the kernels implement, does not depend on it).
 """
 
-import numpy as np
 import torch
 
 NF4_LEVELS = (-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
@@ -23,18 +22,19 @@ NF4_LEVELS = (-1.0, -0.6961928009986877, -0.5250730514526367, -0.394917488098144
 
 
 def dynamic_map():
-    """bitsandbytes' signed dynamic map (create_dynamic_map(signed=True)), float32 [256] sorted:
-    for each decade 10^(i-6), i = 0..6, the midpoints of 2^i + 1 points evenly spaced on [0.1, 1]
-    times the decade, with both signs, plus 0 and 1."""
-    data = []
+    """bitsandbytes' signed dynamic map (create_dynamic_map(signed=True), the code table of its
+    double quantization), float32 [256] sorted. Decade e = 10^(i - 6), i = 0..6, holds the
+    midpoints of the 2^i + 1 float32 points torch.linspace(0.1, 1) places on [0.1, 1], scaled by
+    e, with both signs; then 0 and 1. The float32 linspace matters: its points (and so 22 of the
+    256 entries) differ by one ulp from a float64 linspace rounded to float32. The committed
+    fixture tests/golden/dynamic_map.txt holds the table bit for bit."""
+    values = [0.0, 1.0]
     for i in range(7):
-        bounds = np.linspace(0.1, 1, 2 ** i + 1, dtype=np.float32)
-        means = (bounds[:-1] + bounds[1:]) / np.float32(2.0)
-        decade = np.float32(10.0 ** (i - 6))
-        data += list((decade * means).astype(np.float32))
-        data += list((-decade * means).astype(np.float32))
-    data += [0.0, 1.0]
-    return torch.from_numpy(np.sort(np.array(data, dtype=np.float32)))
+        points = torch.linspace(0.1, 1.0, 2 ** i + 1, dtype=torch.float32)
+        mids = (points[1:] + points[:-1]) / 2.0
+        for sign in (1.0, -1.0):
+            values += (sign * 10.0 ** (i - 6) * mids).tolist()
+    return torch.tensor(sorted(values), dtype=torch.float32)
 
 
 class NF4Weight:

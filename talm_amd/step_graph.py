@@ -31,7 +31,7 @@ import time
 
 import torch
 
-from . import unpad
+from . import patches, unpad
 from .adapters import COPIES, AdapterAdamW
 
 _BATCH_KEYS = ("input_ids", "attention_mask", "labels")
@@ -51,7 +51,7 @@ class GraphedTrainer:
         self.warm_steps = int(warm_steps)
         self.steps = 0
         self.static = None
-        self.graphs = {}           # bucket -> (graph, loss, gradients)
+        self.graphs = {}           # bucket -> (graph, loss, gradients, per-token metrics)
         self.pool = None
         self.capture_seconds = 0.0
         self.replays = 0
@@ -95,7 +95,8 @@ class GraphedTrainer:
         for p in t.params:
             p.grad = None
         graph = torch.cuda.CUDAGraph()
-        with unpad.static_tokens(n_bucket):
+        # the pad sequence is shorter than one bucket step (a full bucket when no token is real)
+        with unpad.static_tokens(n_bucket, max_pad=self.bucket):
             with torch.cuda.graph(graph, pool=self.pool):
                 with torch.autocast("cuda", dtype=torch.float16):
                     out = t.model(**self.static)
@@ -107,7 +108,11 @@ class GraphedTrainer:
             raise RuntimeError("GraphedTrainer: a LoRA parameter got no gradient in the capture")
         for p, g in zip(t.params, held):
             p.grad = g
-        entry = (graph, out.loss.detach(), grads)
+        # the per-token metrics (patches.LAST_STEP) this graph writes on every replay: kept with
+        # the graph, so their memory stays this graph's (no other capture in the shared pool
+        # reuses it) and a replay of this bucket can hand them out again
+        metrics = patches.LAST_STEP[-1] if patches.LAST_STEP else None
+        entry = (graph, out.loss.detach(), grads, metrics)
         self.graphs[n_bucket] = entry
         self.capture_seconds += time.perf_counter() - start
         return entry
@@ -140,9 +145,12 @@ class GraphedTrainer:
         self._stage(batch)
         nb = self.bucket_of(n)
         entry = self.graphs.get(nb) or self.capture(nb)
-        graph, loss, grads = entry
+        graph, loss, grads, metrics = entry
         graph.replay()
         self.replays += 1
+        patches.LAST_STEP.clear()
+        if metrics is not None:
+            patches.LAST_STEP.append(metrics)
         for p, g in zip(t.params, grads):
             p.grad = g
         t.optimizer_tail()

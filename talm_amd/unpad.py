@@ -12,6 +12,7 @@ call per row.
 """
 
 import contextlib
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -22,7 +23,8 @@ from .state import DISABLED, fallback
 
 _rows = []
 _cu = []
-_ahead = {}  # batch key -> (pinned host values, event): row statistics copied ahead of time
+_ahead = {}  # batch key -> (mask ref, labels ref, pinned host values, event): row statistics
+             # copied ahead of time
 _AHEAD_MAX = 4
 
 
@@ -80,17 +82,23 @@ def prefetch(attention_mask, labels):
     event.record()
     while len(_ahead) >= _AHEAD_MAX:
         _ahead.pop(next(iter(_ahead)))
-    _ahead[_batch_key(attention_mask, labels)] = (host, event)
+    _ahead[_batch_key(attention_mask, labels)] = (
+        weakref.ref(attention_mask), weakref.ref(labels), host, event)
 
 
 def take_prefetched(attention_mask, labels):
-    """The row statistics `prefetch` started for this batch (a host list), or None."""
+    """The row statistics `prefetch` started for this batch (a host list), or None. An entry
+    counts only for the very tensors it was made from: the key (address, version, shape) alone
+    would also match a later batch the allocator placed at a freed batch's address, and that
+    batch would get the other one's row lengths."""
     if not _ahead or labels is None:
         return None
     hit = _ahead.pop(_batch_key(attention_mask, labels), None)
     if hit is None:
         return None
-    host, event = hit
+    mask_ref, labels_ref, host, event = hit
+    if mask_ref() is not attention_mask or labels_ref() is not labels:
+        return None
     event.synchronize()  # queued a step ago: long done
     return host.tolist()
 
@@ -121,15 +129,18 @@ def unpad_batch(attention_mask, targets=None, values=None):
     return out if targets is None else out + (counts,)
 
 
-_static = []  # token counts of the fixed-shape packing in force (innermost last)
+_static = []  # (token count, longest pad sequence) of the fixed-shape packing in force
 
 
 @contextlib.contextmanager
-def static_tokens(n_tokens):
+def static_tokens(n_tokens, max_pad=None):
     """While it is open, the causal-LM patch packs every batch into exactly `n_tokens` rows on the
     device (`unpad_static`): no host value of the batch is read, so the forward and backward can
-    be captured in a HIP graph and replayed for any batch of at most `n_tokens` real tokens."""
-    _static.append(int(n_tokens))
+    be captured in a HIP graph and replayed for any batch of at most `n_tokens` real tokens.
+    `max_pad` bounds the pad sequence's length (n_tokens minus the real tokens) for every batch
+    the packing will serve; the attention's grid must cover it (default: n_tokens)."""
+    n_tokens = int(n_tokens)
+    _static.append((n_tokens, n_tokens if max_pad is None else min(int(max_pad), n_tokens)))
     try:
         yield
     finally:
@@ -137,7 +148,13 @@ def static_tokens(n_tokens):
 
 
 def static_n_tokens():
-    return _static[-1] if _static else None
+    return _static[-1][0] if _static else None
+
+
+def static_max_len(seq):
+    """The longest sequence of the packing in force with rows of at most `seq` tokens: a real
+    row, or the pad sequence."""
+    return max(int(seq), _static[-1][1]) if _static else int(seq)
 
 
 def unpad_static(attention_mask, targets, n_tokens):
@@ -156,7 +173,9 @@ def unpad_static(attention_mask, targets, n_tokens):
     k = torch.arange(batch + 2, dtype=torch.int32, device=device)
     before = k[:, None] > k[None, :batch]                       # [B + 2, B]: row b < k
     cu = torch.where(k == batch + 1, n_tokens, (before * lengths[None, :]).sum(1, dtype=torch.int32))
-    cu = cu.to(torch.int32)
+    # a batch with more real tokens than rows (a caller's wrong count) loses its last tokens
+    # instead of sending the attention past the [n_tokens] buffers
+    cu = cu.clamp(0, n_tokens).to(torch.int32)
     j = torch.arange(n_tokens, dtype=torch.int32, device=device)
     row = torch.searchsorted(cu[1:batch + 1], j, right=True)
     pos = j - cu.index_select(0, row)

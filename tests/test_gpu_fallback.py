@@ -1,0 +1,157 @@
+"""Graceful degradation around real launches (talm_amd/state.py, after solution/state.py and the
+fault-injection tests of solution/test_fallback.py): a launch site made to raise on its n-th call
+must leave the result equal to the original code path's, turn exactly that component off with
+one `[solution] fallback:` line, and keep later calls on the original path; out-of-memory must
+propagate out of the training step. Strict mode (the suite's default) is off in these tests."""
+
+import pytest
+import torch
+
+from talm_amd import fused_head, patches, qgroup, qlora_model, rmsnorm, rope, state
+
+pytestmark = pytest.mark.gpu
+
+PREFIX = "[solution] fallback: "
+
+
+class Injector:
+    """Replaces a module function by one that raises on chosen calls and counts every call."""
+
+    def __init__(self, monkeypatch, capsys):
+        self.monkeypatch, self.capsys = monkeypatch, capsys
+
+    def fail(self, module, name, on_call=1, exc=None):
+        real = getattr(module, name)
+        count = {"calls": 0}
+
+        def wrapper(*args, **kwargs):
+            count["calls"] += 1
+            if count["calls"] == on_call:
+                raise exc if exc is not None else RuntimeError("injected failure")
+            return real(*args, **kwargs)
+
+        self.monkeypatch.setattr(module, name, wrapper)
+        return count
+
+    def lines(self):
+        return [line for line in self.capsys.readouterr().out.splitlines()
+                if line.startswith(PREFIX)]
+
+
+@pytest.fixture
+def inject(monkeypatch, capsys):
+    monkeypatch.setattr(state, "STRICT", False)
+    saved = dict(state.DISABLED)
+    state.DISABLED.clear()
+    yield Injector(monkeypatch, capsys)
+    patches.unapply()
+    state.DISABLED.clear()
+    state.DISABLED.update(saved)
+
+
+def _qwen_norm(hidden=1536):
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
+
+    norm = Qwen2RMSNorm(hidden, eps=1e-6).cuda().requires_grad_(False)
+    with torch.no_grad():
+        norm.weight.normal_(1.0, 0.1)
+    return norm
+
+
+def test_rmsnorm_launch_failure_runs_transformers_norm(inject):
+    print("[case] fallback: rmsnorm launch fails on call 1", flush=True)
+    norm = _qwen_norm()
+    x = torch.randn(2, 37, 1536, device="cuda")
+    with torch.autocast("cuda", dtype=torch.float16):
+        original = patches._root(type(norm).forward)
+        ref = original(norm, x)
+        patches.apply()
+        count = inject.fail(rmsnorm, "launch")
+        first, second = norm(x), norm(x)
+    assert torch.equal(first, ref) and torch.equal(second, ref)
+    assert count["calls"] == 1  # the second call did not try the kernel again
+    assert state.DISABLED == {"rmsnorm": "RuntimeError: injected failure"}
+    assert inject.lines() == [f"{PREFIX}rmsnorm: RuntimeError: injected failure"]
+
+
+def test_rope_launch_failure_runs_transformers_rotation(inject):
+    print("[case] fallback: rope launch fails on call 1", flush=True)
+    from transformers.models.qwen2 import modeling_qwen2
+
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 40, 12, 128, generator=g).half().cuda().transpose(1, 2)
+    k = torch.randn(1, 40, 2, 128, generator=g).half().cuda().transpose(1, 2)
+    cos, sin = (t.cuda() for t in torch.randn(2, 1, 40, 128, generator=g).unbind(0))
+    ref = patches._root(modeling_qwen2.apply_rotary_pos_emb)(q, k, cos, sin)
+    patches.apply()
+    count = inject.fail(rope, "_launch")
+    for _ in range(2):
+        out = modeling_qwen2.apply_rotary_pos_emb(q, k, cos, sin)
+        assert all(torch.equal(a, b) for a, b in zip(out, ref))
+    assert count["calls"] == 1
+    assert list(state.DISABLED) == ["rope"]
+
+
+def _tiny(steps):
+    config = qlora_model.qwen2_config(vocab_size=1000, hidden_size=512, intermediate_size=1024,
+                                      num_hidden_layers=2, num_attention_heads=4,
+                                      num_key_value_heads=2, head_dim=128)
+    model = qlora_model.build_model(config, seed=3)
+    with torch.no_grad():
+        for p in qlora_model.lora_parameters(model):
+            if p.abs().sum() == 0:
+                p.normal_(0, 0.02)
+    trainer = qlora_model.Trainer(model, steps=steps, fused_adapters=False)
+    batches = [qlora_model.make_batch(seed=9, step=i, vocab=1000, seq=128, lo=32, hi=128)
+               for i in range(steps)]
+    return trainer, batches
+
+
+def _losses(trainer, batches):
+    return [float(trainer.step(b)) for b in batches]
+
+
+@pytest.mark.parametrize("where", ["fused_head", "qgroup", "addnorm"])
+def test_failure_inside_the_step_keeps_the_loss_curve(inject, where):
+    """A launch failing mid-step: the step's loss stays on the eager path's curve (the
+    component's original code computes the rest), the component is off afterwards."""
+    print(f"[case] fallback inside the step: {where}", flush=True)
+    eager = _losses(*_tiny(3))
+    trainer, batches = _tiny(3)
+    patches.apply()
+    if where == "fused_head":  # the whole fused forward runs again as transformers' forward
+        inject.fail(fused_head, "fused_head_loss")
+    elif where == "qgroup":    # the layer's weights come from the per-projection dequant
+        inject.fail(qgroup, "launch", on_call=2)
+    else:                      # the add + norm of the second layer runs as add, then norm
+        inject.fail(rmsnorm, "launch", on_call=3)
+    losses = _losses(trainer, batches)
+    print(f"[eager] {eager}\n[{where}] {losses}", flush=True)
+    for a, b in zip(losses, eager):
+        assert abs(a - b) <= 5e-3 * abs(b), (losses, eager)
+    assert list(state.DISABLED) == [where]
+    assert len(inject.lines()) == 1
+
+
+def test_out_of_memory_inside_the_step_propagates(inject):
+    print("[case] fallback: out of memory propagates", flush=True)
+    trainer, batches = _tiny(1)
+    patches.apply()
+    inject.fail(rmsnorm, "launch", on_call=2,
+                exc=torch.cuda.OutOfMemoryError("HIP out of memory (injected)"))
+    with pytest.raises(torch.cuda.OutOfMemoryError):
+        trainer.step(batches[0])
+    assert state.DISABLED == {}
+    assert inject.lines() == []
+
+
+def test_restart_rewinds_the_generator():
+    """A fused forward that failed part-way runs again from the same generator state, so a
+    dropout mask drawn before the failure is drawn again (solution/patches.py:55-63)."""
+    print("[case] fallback: _restart rewinds the CUDA generator", flush=True)
+    device = torch.device("cuda", torch.cuda.current_device())
+    saved = torch.cuda.get_rng_state(device)
+    first = torch.rand(1000, device=device)
+    patches._restart(device, saved)
+    again = torch.rand(1000, device=device)
+    assert torch.equal(first, again)

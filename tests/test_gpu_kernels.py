@@ -91,10 +91,11 @@ def test_nf4_per_projection_bit_exact(rows, cols, blocksize):
     assert np.array_equal(f16_bits(out).reshape(-1), ref)
 
 
-def test_layer_group_packs_and_dequantizes_once_per_pass():
-    """The LayerGroup bookkeeping (solution/qgroup.py:121-343) on 4-bit layers quantized by this
-    package: one grouped launch serves the seven projections, bit-identical to each layer's own
-    per-projection dequantization, and the buffer is dropped after the seventh use."""
+def test_layer_group_packs_and_keeps_one_resident_layer():
+    """The packed layer group on 4-bit layers quantized by this package: one grouped launch
+    serves the seven projections, bit-identical to each layer's own per-projection
+    dequantization; the weights stay resident until another group's request displaces them,
+    after which a request dequantizes again (never a stale buffer)."""
     _case("layer group")
     from types import SimpleNamespace
 
@@ -103,25 +104,40 @@ def test_layer_group_packs_and_dequantizes_once_per_pass():
 
     g = torch.Generator().manual_seed(7)
     shapes = [(256, 512), (64, 512), (64, 512), (512, 512), (1024, 512), (1024, 512), (512, 1024)]
-    mods = [Linear4bit.from_weight((torch.randn(o, i, generator=g) * 0.05).to(DEV),
-                                   bias=torch.randn(o, generator=g).to(DEV) if k < 3 else None)
-            for k, (o, i) in enumerate(shapes)]
+
+    def layer_of(scale):
+        mods = [Linear4bit.from_weight((torch.randn(o, i, generator=g) * scale).to(DEV),
+                                       bias=torch.randn(o, generator=g).to(DEV) if k < 3 else None)
+                for k, (o, i) in enumerate(shapes)]
+        return mods, SimpleNamespace(
+            self_attn=SimpleNamespace(q_proj=mods[0], k_proj=mods[1], v_proj=mods[2],
+                                      o_proj=mods[3]),
+            mlp=SimpleNamespace(gate_proj=mods[4], up_proj=mods[5], down_proj=mods[6]))
+
+    mods, layer = layer_of(0.05)
     refs = [dequantize_4bit(m.weight.data, m.weight.quant_state) for m in mods]
-    layer = SimpleNamespace(
-        self_attn=SimpleNamespace(q_proj=mods[0], k_proj=mods[1], v_proj=mods[2], o_proj=mods[3]),
-        mlp=SimpleNamespace(gate_proj=mods[4], up_proj=mods[5], down_proj=mods[6]))
     group = qgroup._pack(layer)
     assert group is not None
+    other = qgroup._pack(layer_of(0.02)[1])
+    qgroup.release()
     before = RAN["group"]
-    group.start_forward()
+    group.begin_forward()
     for idx, ref in enumerate(refs):
-        w = group.weight("fwd", idx)
-        assert torch.equal(w, ref), idx
-    assert RAN["group"] == before + 1 and group.cache["fwd"][0] is None
+        assert torch.equal(group.weight(idx), ref), idx
+    assert RAN["group"] == before + 1  # one launch for the seven projections
+    q_k_v = group.span(0, 3)
+    assert q_k_v.shape == (384, 512) and torch.equal(q_k_v, torch.cat(refs[:3]))
+    assert torch.equal(group.span_bias(0, 3), torch.cat([m.bias.half() for m in mods[:3]]))
+    other.begin_forward()                  # another layer displaces it
+    assert RAN["group"] == before + 2
+    for idx, ref in enumerate(refs):       # dequantized again, once, on the first request
+        assert torch.equal(group.weight(idx), ref), idx
+    assert RAN["group"] == before + 3
     for m, ref in zip(mods, refs):  # the parameters became views of the packed buffers
         assert torch.equal(dequantize_4bit(m.weight.data, m.weight.quant_state), ref)
     for idx, ref in enumerate(refs):
         assert torch.equal(group.dequantize_one(idx), ref)
+    qgroup.release()
 
 
 # ------------------------------------------------------------------------------- RMSNorm -----

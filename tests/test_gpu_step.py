@@ -41,26 +41,33 @@ def _run(patched, steps, monkeypatch):
     return losses
 
 
-@pytest.mark.parametrize("split", [False, True])
-def test_patched_step_matches_eager_loss_curve(monkeypatch, split):
-    """With split, the last layers dequantize projection by projection (the reference's
-    memory-peak trade, opt-in here): their q|k|v and MLP nodes take the per-projection paths."""
-    from talm_amd import qgroup
+@pytest.mark.parametrize("path", ["fused", "per_node", "lora_node"])
+def test_patched_step_matches_eager_loss_curve(monkeypatch, path):
+    """fused: every node of the package (the attention half and the MLP as one node each);
+    per_node: q|k|v node + varlen attention + GroupLinear and the per-projection MLP with the
+    in-place SwiGLU; lora_node: without the q|k|v node (SOLUTION_DISABLE_FUSED_PROJ=1), q_proj
+    and v_proj run as the single-projection LoRA node and RoPE as its own kernel."""
+    from talm_amd import fused_mlp, fused_proj
 
-    print(f"[case] qlora step small model eager vs patched split={split}", flush=True)
-    if split:
-        monkeypatch.setattr(qgroup, "SPLIT_LAYERS", {"fwd": 1, "bwd": 2})
+    print(f"[case] qlora step small model eager vs patched path={path}", flush=True)
+    if path == "per_node":
+        monkeypatch.setattr(fused_proj, "ATTN_BLOCK", False)
+        monkeypatch.setattr(fused_mlp, "ENABLED", False)
+    if path == "lora_node":
+        monkeypatch.setenv("SOLUTION_DISABLE_FUSED_PROJ", "1")
     engaged.reset()
     eager = _run(False, 6, monkeypatch)
     assert engaged.RAN["fused_head"] == 0
     fused = _run(True, 6, monkeypatch)
-    names = ["fused_head", "unpad", "group", "fused_proj", "qkv_mfma", "qkv_mfma_bwd", "addnorm",
-             "head", "varlen_attn", "attn_kernel", "attn_kernel_bwd", "fused_mlp", "attn_block",
-             "adapter_adamw"]
-    if split:  # the split last layer runs the per-projection MLP and the stand-alone RoPE
-        names += ["swiglu_inplace", "split", "rope"]
+    names = ["fused_head", "unpad", "group", "addnorm", "head", "varlen_attn", "attn_kernel",
+             "attn_kernel_bwd", "adapter_adamw"]
+    names += {"fused": ["fused_proj", "qkv_mfma", "qkv_mfma_bwd", "fused_mlp", "attn_block"],
+              "per_node": ["fused_proj", "qkv_mfma", "qkv_mfma_bwd", "swiglu_inplace"],
+              "lora_node": ["lora", "qkv_mfma", "qkv_mfma_bwd", "rope", "fused_mlp"]}[path]
     for name in names:
         assert engaged.RAN[name] > 0, f"{name} did not run"
+    if path == "lora_node":
+        assert engaged.RAN["fused_proj"] == 0 and engaged.RAN["attn_block"] == 0
     assert abs(fused[0] - eager[0]) <= 1e-3 * abs(eager[0]), (fused[0], eager[0])
     for a, b in zip(fused, eager):
         assert abs(a - b) <= 5e-3 * abs(b), (fused, eager)
@@ -106,12 +113,12 @@ def test_fused_mlp_matches_per_projection_mlp(monkeypatch):
     """FusedMLP (one node, feature-major activations, gate|up and their input gradient as single
     GEMMs) against the per-projection path (GroupLinear x 3 + the in-place SwiGLU node) on the
     same packed layer: output and input gradient within fp16 rounding, on a token count that is
-    not a multiple of 8 (the padded leading dimension), with the backward's whole-layer span and
-    its split form (two GEMMs, the second accumulating)."""
-    from talm_amd import fused_mlp, qgroup
+    not a multiple of 8 (the padded leading dimension), with the backward's gate|up span and its
+    per-projection form (two GEMMs, the second accumulating: the weights "qgroup" gives once it
+    is off)."""
+    from talm_amd import fused_mlp, qgroup, state
 
     print("[case] fused mlp vs per-projection mlp", flush=True)
-    monkeypatch.setattr(qgroup, "SPLIT_LAYERS", {"fwd": 1, "bwd": 2})  # the reference's split
     config = qlora_model.qwen2_config(vocab_size=1000, hidden_size=512, intermediate_size=1024,
                                       num_hidden_layers=3, num_attention_heads=4,
                                       num_key_value_heads=2, head_dim=128)
@@ -128,15 +135,16 @@ def test_fused_mlp_matches_per_projection_mlp(monkeypatch):
         results = []
         for fused, split_bwd in ((False, False), (True, False), (True, True)):
             monkeypatch.setattr(fused_mlp, "ENABLED", fused)
-            group.start_forward()
-            group.depth = 99
+            qgroup.release()
+            group.begin_forward()
             x = x0.clone().requires_grad_()
             ran = engaged.RAN["fused_mlp"]
             y = layer.mlp(x)
             assert (engaged.RAN["fused_mlp"] > ran) == fused
-            if split_bwd:
-                group.depth = 0  # the backward dequantizes per projection
+            if split_bwd:  # the backward takes each projection's own dequantization
+                monkeypatch.setitem(state.DISABLED, "qgroup", "test")
             y.backward(dy)
+            monkeypatch.delitem(state.DISABLED, "qgroup", raising=False)
             results.append((y.detach().float(), x.grad.float()))
         for y, dx in results[1:]:
             torch.testing.assert_close(y, results[0][0], rtol=2e-3, atol=2e-3 * float(y.abs().max()))
@@ -150,12 +158,11 @@ def test_attention_block_matches_per_node_attention(monkeypatch):
     """AttentionBlock (q|k|v + LoRA + RoPE, the packed rows' attention and o_proj as one node)
     against the per-node path (FusedProjections, VarlenAttention, GroupLinear) on one packed
     layer with ragged rows (one of a single token): output, input gradient and the LoRA
-    gradients within fp16 rounding, with the backward's whole-layer span and with the backward
-    dequantizing per projection."""
-    from talm_amd import fused_proj, qgroup, unpad
+    gradients within fp16 rounding, with the backward's q|k|v span and with the backward taking
+    each projection's own dequantization (what "qgroup" gives once it is off)."""
+    from talm_amd import fused_proj, qgroup, state, unpad
 
     print("[case] attention block vs per-node attention", flush=True)
-    monkeypatch.setattr(qgroup, "SPLIT_LAYERS", {"fwd": 1, "bwd": 2})
     config = qlora_model.qwen2_config(vocab_size=1000, hidden_size=512, intermediate_size=1024,
                                       num_hidden_layers=3, num_attention_heads=4,
                                       num_key_value_heads=2, head_dim=128)
@@ -186,8 +193,8 @@ def test_attention_block_matches_per_node_attention(monkeypatch):
         results = []
         for block, split_bwd in ((False, False), (True, False), (True, True)):
             monkeypatch.setattr(fused_proj, "ATTN_BLOCK", block)
-            group.start_forward()
-            group.depth = 99
+            qgroup.release()
+            group.begin_forward()
             x = x0.clone().requires_grad_()
             for p in lora:
                 p.grad = None
@@ -198,8 +205,9 @@ def test_attention_block_matches_per_node_attention(monkeypatch):
             assert (engaged.RAN["attn_block"] > ran) == block
             assert engaged.RAN["fused_proj"] > fused
             if split_bwd:
-                group.depth = 0  # the backward dequantizes per projection
+                monkeypatch.setitem(state.DISABLED, "qgroup", "test")
             y.backward(dy)
+            monkeypatch.delitem(state.DISABLED, "qgroup", raising=False)
             results.append([y.detach().float(), x.grad.float()] + [p.grad.float() for p in lora])
         for other in results[1:]:
             for a, b in zip(other, results[0]):

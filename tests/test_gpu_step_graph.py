@@ -3,7 +3,9 @@
 fixed-shape packing (bit-identical losses and LoRA weights: the same kernels on the same shapes
 in the same order), and against the eagerly packed patched step (the loss curve within the
 north star's 0.5%). The token counts are chosen so that buckets repeat after other buckets ran,
-one batch fills its bucket exactly (an empty pad sequence) and one is the largest batch."""
+one batch fills its bucket exactly (an empty pad sequence), one leaves a one-row pad sequence
+(with 16-token buckets, the bench's default) and one is the largest batch. The per-token metrics
+each replay leaves in patches.LAST_STEP must be that replay's, bit for bit."""
 
 import pytest
 import torch
@@ -13,12 +15,13 @@ from talm_amd.step_graph import GraphedTrainer
 
 pytestmark = pytest.mark.gpu
 
-SEQ, VOCAB, BUCKET, WARM = 256, 1000, 64, 2
-# real tokens per step: eager warm-up, then 640 (bucket 640, no pad rows), 300 (320), 630 (640
-# again), 1024 (the largest), 310 (320 again), 600 (640)
+SEQ, VOCAB, WARM = 256, 1000, 2
+# real tokens per step: eager warm-up, then 640 (no pad rows with 16- and 64-token buckets), 640,
+# 300, 630, 1024 (the largest), 310, 607 (a one-row pad sequence with 16-token buckets)
 LENGTHS = [(200, 100, 64, 256), (256, 130, 70, 90), (250, 150, 100, 140), (256, 128, 128, 128),
            (64, 100, 70, 66), (256, 200, 90, 84), (256, 256, 256, 256), (64, 64, 64, 118),
-           (100, 200, 150, 150)]
+           (100, 200, 150, 157)]
+BUCKETS = {16: [304, 320, 608, 640, 1024], 64: [320, 640, 1024]}
 
 
 def _batch(step, lengths):
@@ -44,20 +47,26 @@ def _model():
     return model
 
 
-def _run(mode, monkeypatch):
+def _metrics():
+    m = patches.LAST_STEP[-1]
+    return [t.detach().clone() for t in (m.token_loss, m.token_entropy, m.correct, m.labelled,
+                                         m.argmax)]
+
+
+def _run(mode, monkeypatch, bucket=64):
     """mode: "graph" (GraphedTrainer), "static" (eager steps under the same fixed-shape packing)
     or "eager" (the patched step with host-list packing). Returns (losses, LoRA weights,
-    trainer-or-None)."""
+    (replays, buckets) or None, per-step metrics of patches.LAST_STEP)."""
     steps = len(LENGTHS)
     model = _model()
     trainer = qlora_model.Trainer(model, steps=steps, fused_adapters=True)
     patches.apply()
     monkeypatch.setattr(fused_head, "VOCAB_CHUNK", 384)
-    gt = GraphedTrainer(trainer, bucket=BUCKET, warm_steps=WARM) if mode == "graph" else None
+    gt = GraphedTrainer(trainer, bucket=bucket, warm_steps=WARM) if mode == "graph" else None
     if mode == "static":
         from talm_amd.adapters import COPIES
         monkeypatch.setattr(COPIES, "in_place", True)
-    losses = []
+    losses, metrics = [], []
     try:
         batches = [_batch(i, lengths) for i, lengths in enumerate(LENGTHS)]
         for i in range(steps):
@@ -65,12 +74,13 @@ def _run(mode, monkeypatch):
             if mode == "graph":
                 loss = gt.step(batches[i], ahead)
             elif mode == "static" and i >= WARM:
-                nb = -(-sum(LENGTHS[i]) // BUCKET) * BUCKET
-                with unpad.static_tokens(nb):
+                nb = -(-sum(LENGTHS[i]) // bucket) * bucket
+                with unpad.static_tokens(nb, max_pad=bucket):
                     loss = trainer.step(batches[i], ahead)
             else:
                 loss = trainer.step(batches[i], ahead)
             losses.append(float(loss))
+            metrics.append(_metrics())
         weights = [p.detach().clone() for p in trainer.params]
         info = None if gt is None else (gt.replays, sorted(gt.graphs))
     finally:
@@ -79,25 +89,30 @@ def _run(mode, monkeypatch):
         patches.unapply()
     del model, trainer, gt
     torch.cuda.empty_cache()
-    return losses, weights, info
+    return losses, weights, info, metrics
 
 
-def test_graphed_step_matches_eager_static_step_bitwise(monkeypatch):
-    print("[case] graphed step vs eager fixed-shape step (bitwise)", flush=True)
-    ref_losses, ref_weights, _ = _run("static", monkeypatch)
-    losses, weights, (replays, buckets) = _run("graph", monkeypatch)
+@pytest.mark.parametrize("bucket", [16, 64])
+def test_graphed_step_matches_eager_static_step_bitwise(monkeypatch, bucket):
+    print(f"[case] graphed step vs eager fixed-shape step (bitwise), bucket {bucket}", flush=True)
+    ref_losses, ref_weights, _, ref_metrics = _run("static", monkeypatch, bucket)
+    losses, weights, (replays, buckets), metrics = _run("graph", monkeypatch, bucket)
     print(f"[graph] losses {losses}\n[static] losses {ref_losses}", flush=True)
     assert replays == len(LENGTHS) - WARM
-    assert buckets == [320, 640, 1024]
+    assert buckets == BUCKETS[bucket]
     assert losses == ref_losses
     for w, r in zip(weights, ref_weights):
         assert torch.equal(w, r), (w - r).abs().max().item()
+    names = ("token_loss", "token_entropy", "correct", "labelled", "argmax")
+    for step, (got, ref) in enumerate(zip(metrics, ref_metrics)):
+        for name, a, b in zip(names, got, ref):
+            assert torch.equal(a, b), f"step {step}: LAST_STEP.{name} differs from the eager step"
 
 
 def test_graphed_step_matches_eager_loss_curve(monkeypatch):
     print("[case] graphed step vs eager host-packed patched step (curve)", flush=True)
-    ref_losses, _, _ = _run("eager", monkeypatch)
-    losses, _, _ = _run("graph", monkeypatch)
+    ref_losses, _, _, _ = _run("eager", monkeypatch)
+    losses, _, _, _ = _run("graph", monkeypatch, 16)
     print(f"[graph] losses {losses}\n[eager] losses {ref_losses}", flush=True)
     for a, b in zip(losses, ref_losses):
         assert abs(a - b) <= 5e-3 * abs(b), (losses, ref_losses)
