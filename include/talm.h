@@ -252,6 +252,25 @@ int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t 
                     int64_t workspace_bytes, void* stream);
 
 /*
+ * talm_lora_wgrad without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has
+ * no counterpart in the reference. Same arguments, kernels and results as talm_lora_wgrad; the
+ * fp32 partials live in a fixed array of TALM_LORA_WGRAD_SCRATCH_BYTES in the library's device
+ * memory, one per GPU (held until the process ends), whose address is looked up on the first
+ * call on each device. Calls whose partials need more than that (talm_lora_wgrad_workspace(...)
+ * > TALM_LORA_WGRAD_SCRATCH_BYTES: about 4992 tokens with hidden 1536 and adapters on 1536 +
+ * 256 columns) are rejected with TALM_EINVAL. It calls no allocator. The stream must belong to
+ * the current device. Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (concurrent streams, or threads) race and must be serialized by the caller.
+ */
+#define TALM_LORA_WGRAD_SCRATCH_BYTES (32ll << 20)
+int talm_lora_wgrad_noalloc(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t ldy,
+                            const uint16_t* u, int64_t ldu, const uint16_t* t, int64_t ldt,
+                            int64_t n_tokens, int64_t hidden, int32_t n_adapters, int64_t lo0,
+                            int64_t seg0, float scaling0, float* da0, float* db0, int64_t lo1,
+                            int64_t seg1, float scaling1, float* da1, float* db1, void* stream);
+
+/*
  * Variable-length causal attention with grouped KV heads, forward. Sequence s holds the packed
  * rows [cu_seqlens[s], cu_seqlens[s+1]) (int32, device); row i attends to keys j <= i of its own
  * sequence; query head h reads KV head h / (n_q_heads / n_kv_heads). q f16 [n_tokens, n_q_heads,

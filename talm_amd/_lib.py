@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -37,6 +37,8 @@ SIGNATURES = {
                        _P, _I64, _P],
     "talm_lora_wgrad": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _I64, _I64, _F32,
                         _P, _P, _I64, _I64, _F32, _P, _P, _P, _I64, _P],
+    "talm_lora_wgrad_noalloc": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _I64,
+                                _I64, _F32, _P, _P, _I64, _I64, _F32, _P, _P, _P],
     "talm_qkv_bwd_prep": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P,
                           _I64, _P],
     "talm_qkv_lora_bwd_dx": [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P,

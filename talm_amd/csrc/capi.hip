@@ -33,4 +33,4 @@ int check_launch(const char* what) {
 
 TALM_API const char* talm_last_error(void) { return g_error; }
 
-TALM_API int talm_abi_version(void) { return 8; }
+TALM_API int talm_abi_version(void) { return 9; }

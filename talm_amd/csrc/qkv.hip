@@ -13,6 +13,8 @@
 //               term is accumulated in fp32 with the base product and rounded once. Tiles of
 //               128 columns are whole heads, so the epilogue rotates each (j, j + 64) pair of
 //               the staged fp16 tile in LDS before the coalesced store.
+#include <mutex>
+
 #include "mfma_tile.h"
 
 namespace talm {
@@ -726,12 +728,15 @@ TALM_API int64_t talm_lora_wgrad_workspace(int64_t n_tokens, int64_t hidden, int
   return chunks * (hidden + seg0 + seg1) * 32 * 4;
 }
 
-TALM_API int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t ldy,
-                             const uint16_t* u, int64_t ldu, const uint16_t* t, int64_t ldt,
-                             int64_t n_tokens, int64_t hidden, int32_t n_adapters,
-                             int64_t lo0, int64_t seg0, float scaling0, float* da0, float* db0,
-                             int64_t lo1, int64_t seg1, float scaling1, float* da1, float* db1,
-                             void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+// Validates the arguments of the two wgrad entry points (everything but the workspace) and fills
+// `a` (partials not yet assigned); TALM_OK or TALM_EINVAL with the message set.
+int wgrad_args(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t ldy, const uint16_t* u,
+               int64_t ldu, const uint16_t* t, int64_t ldt, int64_t n_tokens, int64_t hidden,
+               int32_t n_adapters, int64_t lo0, int64_t seg0, float scaling0, float* da0,
+               float* db0, int64_t lo1, int64_t seg1, float scaling1, float* da1, float* db1,
+               WgradArgs& a) {
   const bool two = n_adapters > 1;
   if (n_tokens < 0 || hidden < 1 || n_adapters < 1 || n_adapters > kMaxAdapters || seg0 < 1 ||
       lo0 < 0 || (two && (seg1 < 1 || lo1 < 0)) || ldx < hidden || ldu < 16 * n_adapters ||
@@ -742,14 +747,9 @@ TALM_API int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy,
                 "%lld+%lld / %lld+%lld)",
                 (long long)n_tokens, (long long)hidden, n_adapters, (long long)lo0,
                 (long long)seg0, (long long)lo1, (long long)seg1);
-  const int64_t need = talm_lora_wgrad_workspace(n_tokens, hidden, seg0, two ? seg1 : 0);
-  if (workspace_bytes < need)
-    return fail(TALM_EINVAL, "lora_wgrad: workspace of %lld bytes, %lld needed",
-                (long long)workspace_bytes, (long long)need);
-  if (n_tokens == 0) return ok();  // the caller zeroes the gradients of an empty batch
-  if (!x || !dy || !u || !t || !da0 || !db0 || (two && (!da1 || !db1)) || !workspace)
+  if (n_tokens > 0 && (!x || !dy || !u || !t || !da0 || !db0 || (two && (!da1 || !db1))))
     return fail(TALM_EINVAL, "lora_wgrad: null pointer");
-  WgradArgs a{};
+  a = WgradArgs{};
   a.x = x; a.ldx = ldx; a.dy = dy; a.ldy = ldy; a.u = u; a.ldu = ldu; a.t = t; a.ldt = ldt;
   a.n_tokens = static_cast<int>(n_tokens); a.hidden = static_cast<int>(hidden);
   a.n_adapters = n_adapters;
@@ -757,21 +757,26 @@ TALM_API int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy,
   a.da[0] = da0; a.db[0] = db0;
   a.lo[1] = two ? static_cast<int>(lo1) : 0; a.seg[1] = two ? static_cast<int>(seg1) : 0;
   a.scaling[1] = two ? scaling1 : 0.f; a.da[1] = two ? da1 : da0; a.db[1] = two ? db1 : db0;
-  a.part = static_cast<float*>(workspace);
   a.cols = static_cast<int>(hidden + seg0 + (two ? seg1 : 0));
-  const hipStream_t s = as_stream(stream);
-  const bool mfma = hidden % 32 == 0 && seg0 % 8 == 0 && lo0 % 8 == 0 &&
-                    (!two || (seg1 % 8 == 0 && lo1 % 8 == 0)) && ldx % 8 == 0 && ldy % 8 == 0 &&
-                    ldu % 8 == 0 && ldt % 8 == 0 && aligned(x, 16) && aligned(dy, 16) &&
-                    aligned(u, 16) && aligned(t, 16);
+  return TALM_OK;
+}
+
+// Enqueues the two passes of the weight gradients on `s` with the partials at `a.part` (every
+// partial the reduction uses is written by the first pass: nothing needs clearing).
+int wgrad_launch(WgradArgs& a, hipStream_t s) {
+  const bool two = a.n_adapters > 1;
+  const bool mfma = a.hidden % 32 == 0 && a.seg[0] % 8 == 0 && a.lo[0] % 8 == 0 &&
+                    (!two || (a.seg[1] % 8 == 0 && a.lo[1] % 8 == 0)) && a.ldx % 8 == 0 &&
+                    a.ldy % 8 == 0 && a.ldu % 8 == 0 && a.ldt % 8 == 0 && aligned(a.x, 16) &&
+                    aligned(a.dy, 16) && aligned(a.u, 16) && aligned(a.t, 16);
   if (mfma) {
-    a.chunks = static_cast<int>((n_tokens + kWmTok - 1) / kWmTok);
+    a.chunks = (a.n_tokens + kWmTok - 1) / kWmTok;
     hipLaunchKernelGGL(lora_wgrad_mfma_kernel,
                        dim3(static_cast<unsigned>((a.cols + kWmCols - 1) / kWmCols),
                             static_cast<unsigned>(a.chunks)),
                        dim3(256), 0, s, a);
   } else {
-    a.chunks = static_cast<int>((n_tokens + kWgChunk - 1) / kWgChunk);
+    a.chunks = (a.n_tokens + kWgChunk - 1) / kWgChunk;
     hipLaunchKernelGGL(lora_wgrad_partial_kernel,
                        dim3(static_cast<unsigned>((a.cols + 255) / 256), static_cast<unsigned>(a.chunks)),
                        dim3(256), 0, s, a);
@@ -780,4 +785,83 @@ TALM_API int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy,
                      dim3(static_cast<unsigned>((static_cast<int64_t>(a.cols) * 32 + 255) / 256)),
                      dim3(256), 0, s, a);
   return check_launch("lora_wgrad");
+}
+
+// The partials of the allocation-free entry point: one array per GPU, in the code object's
+// device memory (allocated when the module loads on that GPU, held until the process ends).
+// Host code never passes `scratch` itself to a kernel (on the host it names a stand-in, not
+// the device address): the address comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kWgradScratchBytes = TALM_LORA_WGRAD_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kWgradScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kMaxDevices] = {};  // device address of `scratch` per device, set once
+
+// The current device's address of `scratch` (looked up on the first call on that device).
+int wgrad_scratch(float** out) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess)
+    return fail(TALM_EHIP, "lora_wgrad_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return fail(TALM_EINVAL, "lora_wgrad_noalloc: device %d beyond %d", device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[device]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return fail(TALM_EHIP, "lora_wgrad_noalloc: hipGetSymbolAddress: %s",
+                  hipGetErrorString(err));
+    g_scratch[device] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch[device];
+  return TALM_OK;
+}
+
+}  // namespace
+
+TALM_API int talm_lora_wgrad(const uint16_t* x, int64_t ldx, const uint16_t* dy, int64_t ldy,
+                             const uint16_t* u, int64_t ldu, const uint16_t* t, int64_t ldt,
+                             int64_t n_tokens, int64_t hidden, int32_t n_adapters,
+                             int64_t lo0, int64_t seg0, float scaling0, float* da0, float* db0,
+                             int64_t lo1, int64_t seg1, float scaling1, float* da1, float* db1,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  WgradArgs a;
+  int status = wgrad_args(x, ldx, dy, ldy, u, ldu, t, ldt, n_tokens, hidden, n_adapters, lo0,
+                          seg0, scaling0, da0, db0, lo1, seg1, scaling1, da1, db1, a);
+  if (status != TALM_OK) return status;
+  const int64_t need =
+      talm_lora_wgrad_workspace(n_tokens, hidden, seg0, n_adapters > 1 ? seg1 : 0);
+  if (workspace_bytes < need)
+    return fail(TALM_EINVAL, "lora_wgrad: workspace of %lld bytes, %lld needed",
+                (long long)workspace_bytes, (long long)need);
+  if (n_tokens == 0) return ok();  // the caller zeroes the gradients of an empty batch
+  if (!workspace) return fail(TALM_EINVAL, "lora_wgrad: null pointer");
+  a.part = static_cast<float*>(workspace);
+  return wgrad_launch(a, as_stream(stream));
+}
+
+TALM_API int talm_lora_wgrad_noalloc(const uint16_t* x, int64_t ldx, const uint16_t* dy,
+                                     int64_t ldy, const uint16_t* u, int64_t ldu,
+                                     const uint16_t* t, int64_t ldt, int64_t n_tokens,
+                                     int64_t hidden, int32_t n_adapters, int64_t lo0,
+                                     int64_t seg0, float scaling0, float* da0, float* db0,
+                                     int64_t lo1, int64_t seg1, float scaling1, float* da1,
+                                     float* db1, void* stream) {
+  WgradArgs a;
+  int status = wgrad_args(x, ldx, dy, ldy, u, ldu, t, ldt, n_tokens, hidden, n_adapters, lo0,
+                          seg0, scaling0, da0, db0, lo1, seg1, scaling1, da1, db1, a);
+  if (status != TALM_OK) return status;
+  const int64_t need =
+      talm_lora_wgrad_workspace(n_tokens, hidden, seg0, n_adapters > 1 ? seg1 : 0);
+  if (need > kWgradScratchBytes)
+    return fail(TALM_EINVAL,
+                "lora_wgrad_noalloc: %lld tokens x %d columns need %lld bytes of partials, "
+                "above the fixed scratch of %lld bytes (use talm_lora_wgrad with a workspace)",
+                (long long)n_tokens, a.cols, (long long)need, (long long)kWgradScratchBytes);
+  if (n_tokens == 0) return ok();
+  status = wgrad_scratch(&a.part);
+  if (status != TALM_OK) return status;
+  return wgrad_launch(a, as_stream(stream));
 }
