@@ -2,11 +2,15 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME,...]
 
-Per kernel: K timed launches after W warm-up launches. The launches are
-captured once in a HIP graph of `--reps` back-to-back launches and the graph is replayed, with
-HIP events recorded on the launch stream around the replays, so the average duration is the
-kernel's, not Python's launch overhead. Achieved throughput divides the ALGORITHMIC bytes (or
-FLOPs) of one launch, stated next to each kernel below, by that average duration.
+Default workload: configuration 5, the full QLoRA step (the JSON line's `value`, mean ms per
+step). Then the kernel suite of configurations 1-4. Per kernel: the launches are captured in a
+HIP graph of `--reps` back-to-back launches and the graph is replayed (>= 200 timed launches),
+with HIP events recorded on the launch stream around each replay; the reported duration is the
+median over the replays of the per-launch average, so it is the kernel's time, not Python's
+launch overhead. The bandwidth-bound kernels read and write a rotating set of buffers whose total
+footprint is more than twice the 256 MB last-level cache, so their GB/s are HBM rates, not cache
+rates. Achieved throughput divides the ALGORITHMIC bytes (or FLOPs) of one launch, stated next to
+each kernel below, by that duration.
 
 The last line printed is one JSON object (the driver's contract); per-kernel results ride in
 its "kernels" list.
@@ -14,7 +18,9 @@ its "kernels" list.
 
 import argparse
 import json
+import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -26,6 +32,7 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, GB/s
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, TFLOP/s
+LLC_BYTES = 256 * 2**20    # MI355X last-level (Infinity) cache
 
 METRIC = "QLoRA step ms (Qwen2.5-1.5B shape, B4xS512); kernel HBM GB/s & MFMA %"
 
@@ -46,32 +53,41 @@ MEASURED_TRAFFIC = {
 
 
 def graph_time_ms(fn, steps, warmup, reps):
-    """Average duration (ms) of one fn() launch: `reps` launches captured in one graph,
-    replayed until `steps` launches are timed."""
-    for _ in range(max(1, warmup)):
-        fn()
+    """Duration (ms) of one fn(i) launch, i = 0 .. reps - 1 selecting the buffer set: `reps`
+    launches captured in one graph, the graph replayed until at least `steps` launches are timed,
+    each replay between two events on the capture stream. Returns (median over replays of the
+    per-launch average, mean over all launches, launches timed)."""
+    for i in range(max(1, warmup)):
+        fn(i % reps)
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        fn()  # first launch outside capture on the side stream
+        fn(0)  # first launch outside capture on the side stream
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
-            for _ in range(reps):
-                fn()
+            for i in range(reps):
+                fn(i)
     torch.cuda.synchronize()
-    replays = max(1, steps // reps)
+    replays = max(3, math.ceil(steps / reps))
     graph.replay()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    end.synchronize()
-    return start.elapsed_time(end) / (replays * reps), replays * reps
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    with torch.cuda.stream(stream):
+        events[0].record(stream)
+        for r in range(replays):
+            graph.replay()
+            events[r + 1].record(stream)
+    events[-1].synchronize()
+    per = [events[r].elapsed_time(events[r + 1]) / reps for r in range(replays)]
+    return statistics.median(per), sum(per) / replays, replays * reps
+
+
+def rotation(bytes_per_set, cap=64):
+    """How many buffer sets of `bytes_per_set` bytes rotate so that their footprint is more than
+    twice the last-level cache (a set is then evicted before it is used again)."""
+    return max(2, min(cap, math.ceil(2.2 * LLC_BYTES / bytes_per_set)))
 
 
 def kernel_suite(args, only):
@@ -80,12 +96,15 @@ def kernel_suite(args, only):
     dev = "cuda"
     results = []
 
-    def record(name, ms, count, bytes_=None, flops=None, config=""):
-        entry = {"kernel": name, "config": config, "us": round(ms * 1e3, 3), "launches": count}
+    def record(name, timing, bytes_=None, flops=None, config="", sets=1):
+        ms, mean_ms, count = timing
+        entry = {"kernel": name, "config": config, "us": round(ms * 1e3, 3),
+                 "us_mean": round(mean_ms * 1e3, 3), "launches": count, "buffer_sets": sets}
         if bytes_ is not None:
             gbs = bytes_ / (ms * 1e-3) / 1e9
             entry.update(bytes=int(bytes_), gbs=round(gbs, 1),
-                         hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+                         hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                         footprint_mb=round(sets * bytes_ / 1e6, 1))
         if flops is not None:
             tf = flops / (ms * 1e-3) / 1e12
             entry.update(flops=int(flops), tflops=round(tf, 1),
@@ -96,86 +115,126 @@ def kernel_suite(args, only):
     def want(name):
         return not only or name in only
 
+    def timed(fn, sets):
+        # every buffer set is used the same number of times per replay
+        reps = sets * max(1, math.ceil(args.reps / sets)) if sets > 1 else args.reps
+        return graph_time_ms(lambda i: fn(i % sets), args.steps, args.warmup, reps)
+
     if "copy" in only:
         # calibration for the HBM byte counters: a plain 512 MiB device copy reads and writes
         # exactly 512 MiB per launch (run only when named explicitly)
         src = torch.empty(2**28, dtype=torch.float16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
-        ms, cnt = graph_time_ms(lambda: dst.copy_(src), args.steps, args.warmup, args.reps)
-        record("copy_512MiB", ms, cnt, bytes_=2 * 2**29, config="calibration")
+        record("copy_512MiB", timed(lambda i: dst.copy_(src), 1), bytes_=2 * 2**29,
+               config="calibration")
         del src, dst
 
     if want("nf4_group"):
         d = workloads.nf4_layer()
-        t = {k: d[k].to(dev) for k in ("packed", "absmax8", "code", "absmax2", "offset2")}
-        out = torch.empty(d["n"], dtype=torch.float16, device=dev)
         n_rows = d["absmax8"].numel()
+        # packed + absmax8 + absmax2 + offsets (7 x 4) + code + fp16 out
+        algo = d["n"] // 2 + n_rows + 4 * d["absmax2"].numel() + 28 + 1024 + 2 * d["n"]
+        k = rotation(algo)
+        sets = [{key: d[key].to(dev) for key in ("packed", "absmax8", "code", "absmax2",
+                                                  "offset2")} for _ in range(k)]
+        outs = [torch.empty(d["n"], dtype=torch.float16, device=dev) for _ in range(k)]
 
-        def fn():
+        def fn(i):
+            t = sets[i]
             qgroup.launch(t["packed"], t["absmax8"], t["code"], t["absmax2"], t["offset2"],
-                          None, out, n_rows, 64, 256)
+                          None, outs[i], n_rows, 64, 256)
 
-        ms, cnt = graph_time_ms(fn, args.steps, args.warmup, args.reps)
-        # packed + absmax8 + absmax2 + offsets(7 x 4) + code + fp16 out
-        algo = d["n"] // 2 + n_rows + 4 * t["absmax2"].numel() + 28 + 1024 + 2 * d["n"]
-        record("nf4_group_dequant", ms, cnt, bytes_=algo, config="1: Qwen2.5-1.5B layer")
+        record("nf4_group_dequant", timed(fn, k), bytes_=algo, config="1: Qwen2.5-1.5B layer",
+               sets=k)
+        del sets, outs
 
-    d2 = workloads.norm_rope() if (want("addnorm_fwd") or want("addnorm_bwd")
-                                   or want("rope")) else None
-    if d2 is not None and (want("addnorm_fwd") or want("addnorm_bwd")):
-        n, hdim = d2["n"], 1536
-        x, br, w = d2["residual"].to(dev), d2["x"].to(dev), d2["weight"].to(dev)
-        total = torch.empty_like(x)
-        y = torch.empty_like(x)
-        xhat = torch.empty_like(x)
-        rstd = torch.empty(n, dtype=torch.float32, device=dev)
-        dy, ds = d2["dy"].to(dev), d2["ds"].to(dev)
-        dx = torch.empty_like(x)
-        db = torch.empty_like(x)
+    d2 = workloads.norm_rope() if any(want(x) for x in ("addnorm_fwd", "addnorm_bwd", "rope",
+                                                         "stacked")) else None
+    # config 2's shapes, and (with "stacked") the 28 layers' rows in one launch: the per-launch
+    # floor of these 10-18 MB kernels apart from their streaming rate
+    norm_stacks = [st for st in (1, 28) if d2 is not None and (
+        (st == 1 and (want("addnorm_fwd") or want("addnorm_bwd"))) or (st == 28 and want("stacked")))]
+    rope_stacks = [st for st in (1, 28) if d2 is not None and (
+        (st == 1 and want("rope")) or (st == 28 and want("stacked")))]
+    for stack in norm_stacks:
+        name_sfx = "" if stack == 1 else "_stacked28"
+        n, hdim = d2["n"] * stack, 1536
+        nbytes = 10 * n * hdim + 4 * n + 4 * hdim
+        k = rotation(nbytes)
+        w = d2["weight"].to(dev)
 
-        def fwd():
-            rmsnorm.launch(x, w, y, xhat, rstd, 1e-6, 0, p=br, q=total)
+        def norm_set():
+            x = d2["residual"].to(dev).repeat(stack, 1)
+            br = d2["x"].to(dev).repeat(stack, 1)
+            return {"x": x, "br": br, "total": torch.empty_like(x), "y": torch.empty_like(x),
+                    "xhat": torch.empty_like(x),
+                    "rstd": torch.empty(n, dtype=torch.float32, device=dev),
+                    "dy": d2["dy"].to(dev).repeat(stack, 1), "ds": d2["ds"].to(dev).repeat(stack, 1),
+                    "dx": torch.empty_like(x), "db": torch.empty_like(x)}
 
-        def bwd():
-            rmsnorm.launch(dx, w, dy, xhat, rstd, 1e-6, 1, p=db, q=ds)
+        sets = [norm_set() for _ in range(k)]
 
-        fwd()
-        if want("addnorm_fwd"):
-            ms, cnt = graph_time_ms(fwd, args.steps, args.warmup, args.reps)
-            record("add_rmsnorm_fwd", ms, cnt, bytes_=10 * n * hdim + 4 * n + 4 * hdim,
-                   config=f"2: N={n}")
-        if want("addnorm_bwd"):
-            ms, cnt = graph_time_ms(bwd, args.steps, args.warmup, args.reps)
-            record("add_rmsnorm_bwd", ms, cnt, bytes_=10 * n * hdim + 4 * n + 4 * hdim,
-                   config=f"2: N={n}")
+        def fwd(i):
+            s_ = sets[i]
+            rmsnorm.launch(s_["x"], w, s_["y"], s_["xhat"], s_["rstd"], 1e-6, 0, p=s_["br"],
+                           q=s_["total"])
 
-    if d2 is not None and want("rope"):
-        n = d2["n"]
-        qkv = torch.randn(n, 2048, device=dev).half()
-        q = qkv[:, :1536].view(n, 12, 128)
-        k = qkv[:, 1536:1792].view(n, 2, 128)
-        cos, sin = d2["cos"].to(dev), d2["sin"].to(dev)
+        def bwd(i):
+            s_ = sets[i]
+            rmsnorm.launch(s_["dx"], w, s_["dy"], s_["xhat"], s_["rstd"], 1e-6, 1, p=s_["db"],
+                           q=s_["ds"])
 
-        def fn():
-            rope.rope_(q, k, cos, sin, backward=False)
+        for i in range(k):
+            fwd(i)
+        cfg = f"2: N={d2['n']}" + ("" if stack == 1 else f" x 28 layers in one launch ({n} rows)")
+        if want("addnorm_fwd") or stack > 1:
+            record("add_rmsnorm_fwd" + name_sfx, timed(fwd, k), bytes_=nbytes, config=cfg, sets=k)
+        if want("addnorm_bwd") or stack > 1:
+            record("add_rmsnorm_bwd" + name_sfx, timed(bwd, k), bytes_=nbytes, config=cfg, sets=k)
+        del sets
 
-        ms, cnt = graph_time_ms(fn, args.steps, args.warmup, args.reps)
-        record("rope_inplace", ms, cnt, bytes_=8192 * n, config=f"2: N={n}")
+    for stack in rope_stacks:
+        n = d2["n"] * stack
+        nbytes = 8192 * n
+        k = rotation(nbytes)
+
+        def rope_set():
+            qkv = torch.randn(n, 2048, device=dev).half()
+            return (qkv[:, :1536].view(n, 12, 128), qkv[:, 1536:1792].view(n, 2, 128),
+                    d2["cos"].to(dev).repeat(stack, 1), d2["sin"].to(dev).repeat(stack, 1))
+
+        sets = [rope_set() for _ in range(k)]
+
+        def fn(i):
+            q, k_, cos, sin = sets[i]
+            rope.rope_(q, k_, cos, sin, backward=False)
+
+        cfg = f"2: N={d2['n']}" + ("" if stack == 1 else f" x 28 layers in one launch ({n} rows)")
+        record("rope_inplace" + ("" if stack == 1 else "_stacked28"), timed(fn, k),
+               bytes_=nbytes, config=cfg, sets=k)
+        del sets
 
     if want("swiglu_fwd") or want("swiglu_bwd"):
         d3 = workloads.swiglu_inputs()
-        gate, up, grad = (d3[k].to(dev) for k in ("gate", "up", "grad"))
-        out = torch.empty_like(gate)
-        dgate, dup = torch.empty_like(gate), torch.empty_like(up)
-        n = gate.numel()
-        if want("swiglu_fwd"):
-            ms, cnt = graph_time_ms(lambda: swiglu.swiglu_fwd(gate, up, out), args.steps,
-                                    args.warmup, args.reps)
-            record("swiglu_fwd", ms, cnt, bytes_=6 * n, config="3: [2048, 8960]")
-        if want("swiglu_bwd"):
-            ms, cnt = graph_time_ms(lambda: swiglu.swiglu_bwd(grad, gate, up, dgate, dup),
-                                    args.steps, args.warmup, args.reps)
-            record("swiglu_bwd", ms, cnt, bytes_=10 * n, config="3: [2048, 8960]")
+        n = d3["gate"].numel()
+        for name, per_elem in (("swiglu_fwd", 6), ("swiglu_bwd", 10)):
+            if not want(name):
+                continue
+            k = rotation(per_elem * n)
+            sets = [{key: d3[key].to(dev) for key in ("gate", "up", "grad")} for _ in range(k)]
+            for s_ in sets:
+                s_["out"], s_["dgate"], s_["dup"] = (torch.empty_like(s_["gate"])
+                                                     for _ in range(3))
+            if name == "swiglu_fwd":
+                def fn(i):
+                    s_ = sets[i]
+                    swiglu.swiglu_fwd(s_["gate"], s_["up"], s_["out"])
+            else:
+                def fn(i):
+                    s_ = sets[i]
+                    swiglu.swiglu_bwd(s_["grad"], s_["gate"], s_["up"], s_["dgate"], s_["dup"])
+            record(name, timed(fn, k), bytes_=per_elem * n, config="3: [2048, 8960]", sets=k)
+            del sets
     if want("head"):
         from talm_amd import _ops, fused_head
 
@@ -199,12 +258,13 @@ def kernel_suite(args, only):
                          dtype=torch.uint8, device=dev)
         wt = fused_head.transpose_weight(w16)  # built once per frozen weight, outside the timing
 
-        def fn():
+        def fn(i):
             torch.ops.talm.head_ce(h16, w16, wt, tt, vchunk, n_lab, group, *outs, ws)
 
-        ms, cnt = graph_time_ms(fn, max(10, args.steps // 20), args.warmup, 4)
+        # compute-bound (the 467 MB weight streams from HBM on every call anyway): one set
+        timing = graph_time_ms(fn, 200, 3, 10)
         flops = 2.0 * vocab * hdim * (n + n_lab)
-        record("head_ce_fwd_bwd", ms, cnt, flops=flops,
+        record("head_ce_fwd_bwd", timing, flops=flops,
                config=f"4: N={n} H={hdim} V={vocab} N_lab={n_lab} vchunk={vchunk}")
     return results
 
@@ -281,50 +341,84 @@ def step_workload(args):
     return out
 
 
-def cpu_baseline_step(seconds):
-    """The reference's eager path on the host cores, bounded: one decoder layer of the QLoRA
-    model (fp32, forward + backward) on a config-5 token count, timed and scaled to 28 layers,
-    plus the head + cross-entropy oracle on a row sample scaled to the token count."""
-    import numpy as np
+def cpu_host():
+    """Core counts and CPU model of the host the CPU baseline ran on."""
+    model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"threads": torch.get_num_threads(), "cpu_count": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0)), "cpu_model": model}
 
-    from oracle import head as head_oracle
-    from talm_amd import qlora_model
 
-    torch.manual_seed(0)
-    n_tok = 1280  # 4 rows of 128-512 tokens: the mean of config 5
-    cfg = qlora_model.qwen2_config(num_hidden_layers=1)
-    from transformers.models.qwen2.modeling_qwen2 import Qwen2DecoderLayer, Qwen2RotaryEmbedding
+def cpu_model_from(model):
+    """The QLoRA model moved to the host for the reference's CPU eager path: fp32 compute, the
+    tied embedding in fp32, the 4-bit layers dequantizing with the oracle's PyTorch CPU
+    restatement of bitsandbytes' dequantize_4bit (the product has no CPU path)."""
+    from oracle import nf4 as nf4_oracle
+    from talm_amd import nf4_linear
 
-    layer = Qwen2DecoderLayer(cfg, 0).float()
-    rot = Qwen2RotaryEmbedding(cfg)
-    x = torch.randn(1, n_tok, cfg.hidden_size, requires_grad=True)
-    pos = torch.arange(n_tok)[None]
-    pe = rot(x, pos)
-    mask = torch.full((n_tok, n_tok), float("-inf")).triu(1)[None, None]
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        y = layer(x, attention_mask=mask, position_embeddings=pe, position_ids=pos)
-        y.float().sum().backward()
-        reps += 1
-        if time.perf_counter() - t0 > seconds / 2:
-            break
-    layer_ms = (time.perf_counter() - t0) * 1e3 / reps
-    rows = 16
-    rng = np.random.default_rng(0)
-    h = rng.standard_normal((rows, cfg.hidden_size)).astype(np.float16)
-    w = (rng.standard_normal((cfg.vocab_size, cfg.hidden_size)) * 0.02).astype(np.float16)
-    t = rng.integers(0, cfg.vocab_size, rows)
-    t1 = time.perf_counter()
-    head_oracle.head_ce(h, w, t, vchunk=8192)
-    head_ms = (time.perf_counter() - t1) * 1e3 * n_tok / rows
-    threads = torch.get_num_threads()
-    return {"value": round(28 * layer_ms + head_ms, 1), "unit": "ms/step (estimated)",
-            "cores": threads, "kind": "port",
-            "sample": f"1 Qwen2.5-1.5B decoder layer fwd+bwd in fp32 PyTorch CPU eager on "
-                      f"{n_tok} tokens ({reps} reps, {layer_ms:.0f} ms) x 28 layers + the head/CE "
-                      f"oracle on {rows} rows x full vocabulary scaled to {n_tok} rows "
-                      f"({head_ms:.0f} ms); {threads} threads, {os.cpu_count()} CPUs visible"}
+    model = model.to("cpu")
+    embed = model.model.embed_tokens
+    embed.weight.data = embed.weight.data.float()
+    for module in model.modules():
+        if isinstance(module, nf4_linear.Linear4bit):
+            module.compute_dtype = torch.float32
+            if module.bias is not None:
+                module.bias.data = module.bias.data.float()
+    nf4_linear.dequantize_4bit = nf4_oracle.dequant_state_torch
+    return model
+
+
+def cpu_baseline_step(n_timed=2, seed=7):
+    """The reference's CPU eager path, measured: the unpatched QLoRA step of configuration 5
+    (the same Qwen2.5-1.5B-shaped model and B4 x S512 batches as the GPU runs) in fp32 PyTorch
+    on the host cores — per projection NF4 dequantization + F.linear, PEFT's LoRA, transformers'
+    SDPA attention on the padded batch, full logits and cross-entropy, backward, clipping and
+    AdamW — 1 warm-up step, then `n_timed` timed steps (the planned "2-step CPU sample")."""
+    from talm_amd import nf4_linear, qlora_model
+
+    real_dequant = nf4_linear.dequantize_4bit
+    torch.cuda.empty_cache()
+    model = cpu_model_from(qlora_model.build_model(seed=1))
+    try:
+        params = qlora_model.lora_parameters(model)
+        opt = torch.optim.AdamW(params, lr=2e-4, weight_decay=0.01)
+        vocab = model.config.vocab_size
+        times, tokens, losses = [], 0, []
+        for i in range(1 + n_timed):
+            # the warm-up step (thread pools, allocator) runs on one short row
+            batch = qlora_model.make_batch(seed, i, vocab, device="cpu") if i else \
+                qlora_model.make_batch(seed, i, vocab, batch=1, seq=128, lo=64, hi=128,
+                                       device="cpu")
+            t0 = time.perf_counter()
+            out = model(**batch)
+            out.loss.backward()
+            torch.nn.utils.clip_grad_norm_(params, 1.0)
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            dt = time.perf_counter() - t0
+            losses.append(out.loss.item())
+            print(f"[bench] cpu step {i}: {dt:.2f} s, loss {losses[-1]:.4f}", flush=True)
+            if i > 0:
+                times.append(dt)
+                tokens += int(batch["attention_mask"].sum())
+    finally:
+        nf4_linear.dequantize_4bit = real_dequant
+    del model
+    host = cpu_host()
+    ms = 1e3 * sum(times) / len(times)
+    return {"value": round(ms, 1), "unit": "ms/step", "cores": host["threads"], "kind": "port",
+            "sample": f"{n_timed} timed steps (after a 1-row warm-up step) of the unpatched "
+                      f"config-5 QLoRA step in fp32 PyTorch CPU eager (B4 x S512 padded, "
+                      f"{tokens} real tokens in the timed steps; bitsandbytes' dequantize_4bit "
+                      f"as the oracle's PyTorch restatement), losses "
+                      f"{', '.join(f'{x:.4f}' for x in losses[1:])}",
+            "host": host, "step_seconds": [round(t, 2) for t in times]}
 
 
 def cpu_baseline_nf4(seconds):
@@ -416,7 +510,7 @@ def main():
     if line_roofline is not None:
         line["roofline"] = line_roofline
     if args.cpu_seconds > 0:
-        line["cpu_baseline"] = (cpu_baseline_step(args.cpu_seconds) if step is not None
+        line["cpu_baseline"] = (cpu_baseline_step() if step is not None
                                 else cpu_baseline_nf4(args.cpu_seconds))
     print(json.dumps(line), flush=True)
 

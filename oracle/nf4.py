@@ -102,3 +102,22 @@ def dequant_np(packed, absmax, blocksize, n):
     vals = np.stack([NF4_LEVELS[codes >> 4], NF4_LEVELS[codes & 15]], axis=1).reshape(-1)[:n]
     scale = np.repeat(np.asarray(absmax, np.float32), blocksize)[:n]
     return (vals * scale).astype(np.float16).view(np.uint16)
+
+
+def dequant_state_torch(packed, state):
+    """The reference's CPU eager dequantization of one 4-bit projection with PyTorch CPU ops (the
+    `cpu_baseline` leg of bench.py times the unpatched step with it): bitsandbytes'
+    dequantize_4bit as the reference's tests restate it (`_nf4_manual`, solution/test_fuzz.py:
+    860-868) after the double-quant absmax is rebuilt (code[absmax8] * absmax2 + offset, each
+    rounded in fp32: solution/qgroup.py:12-14). Returns fp16 [out, in], bit-identical to
+    `group_dequant` on the same bytes (tests/test_oracle.py)."""
+    import torch
+
+    codes = packed.reshape(-1).to(torch.int64)
+    levels = torch.tensor(NF4_LEVELS, dtype=torch.float32)
+    inner = state.state2
+    blk2 = torch.arange(state.absmax.numel()) // inner.blocksize
+    absmax = inner.code[state.absmax.to(torch.int64)] * inner.absmax[blk2] + state.offset
+    vals = torch.stack((levels[codes >> 4], levels[codes & 15]), 1).reshape(-1)
+    vals = vals * absmax.repeat_interleave(state.blocksize)[:vals.numel()]
+    return vals.to(torch.float16).view(state.shape)

@@ -45,18 +45,21 @@ class QuantState:
 
 
 class MatMul4Bit(torch.autograd.Function):
-    """y = x W16^T + b with W16 dequantized per call, forward and backward."""
+    """y = x W^T + b with W dequantized per call (fp16) and cast to x's dtype, forward and
+    backward (bitsandbytes' MatMul4Bit: dx = dy W in the input's dtype)."""
 
     @staticmethod
     def forward(ctx, x, packed, state, bias):
-        ctx.packed, ctx.state = packed, state
-        return F.linear(x, dequantize_4bit(packed, state), bias)
+        ctx.packed, ctx.state, ctx.dtype = packed, state, x.dtype
+        weight = dequantize_4bit(packed, state).to(x.dtype)
+        return F.linear(x, weight, None if bias is None else bias.to(x.dtype))
 
     @staticmethod
     def backward(ctx, grad):
         grad_x = None
         if ctx.needs_input_grad[0]:
-            grad_x = torch.matmul(grad.to(torch.float16), dequantize_4bit(ctx.packed, ctx.state))
+            weight = dequantize_4bit(ctx.packed, ctx.state).to(ctx.dtype)
+            grad_x = torch.matmul(grad.to(ctx.dtype), weight)
         return grad_x, None, None, None
 
 

@@ -153,3 +153,23 @@ def test_solution_package_is_the_drop_in_name():
     assert sstate.DISABLED is state.DISABLED
     for name in solution.patches.__all__:
         assert hasattr(solution.patches, name), name
+
+
+def test_linking_the_next_norms_adds_no_submodule(clean_apply):
+    """link_next_norms records each decoder layer's follower norm without making it a submodule
+    of the layer (the module tree and state_dict keep their keys)."""
+    from talm_amd import qlora_model, rmsnorm
+
+    patches.apply()
+    config = qlora_model.qwen2_config(vocab_size=64, hidden_size=64, intermediate_size=128,
+                                      num_hidden_layers=3, num_attention_heads=2,
+                                      num_key_value_heads=1, head_dim=32)
+    from transformers import Qwen2Model
+
+    model = Qwen2Model(config)
+    keys = list(model.state_dict())
+    rmsnorm.link_next_norms(model)
+    assert list(model.state_dict()) == keys
+    layers = model.layers
+    assert layers[0].__dict__["_talm_next_norm"]() is layers[1].input_layernorm
+    assert layers[2].__dict__["_talm_next_norm"]() is model.norm

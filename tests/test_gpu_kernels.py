@@ -150,8 +150,8 @@ def test_add_rmsnorm_config2_forward_backward(x_dtype):
     d = workloads.norm_rope()
     x, br, w = d["residual"].to(x_dtype), d["x"], d["weight"]
     xd, bd, wd = x.to(DEV), br.to(DEV), w.to(DEV)
-    total, y = rmsnorm.AddRMSNorm.apply(xd.clone().requires_grad_(), bd.clone().requires_grad_(),
-                                        wd, d["eps"], torch.float16)
+    total, y = rmsnorm.NormNode.apply(xd.clone().requires_grad_(), bd.clone().requires_grad_(),
+                                      wd, d["eps"], torch.float16)
     np_x = to_np(x).astype(np.float64)
     q, y_ref, xhat_ref, rstd_ref = norm_oracle.forward(np_x, to_np(w), d["eps"], p=to_np(br),
                                                        x_dtype=np.float64, out_dtype=np.float64,
@@ -161,7 +161,7 @@ def test_add_rmsnorm_config2_forward_backward(x_dtype):
     # backward through the same node: ds (sum's gradient) and dy
     xs = xd.clone().requires_grad_()
     bs = bd.clone().requires_grad_()
-    total, y = rmsnorm.AddRMSNorm.apply(xs, bs, wd, d["eps"], torch.float16)
+    total, y = rmsnorm.NormNode.apply(xs, bs, wd, d["eps"], torch.float16)
     ds = d["ds"].to(x_dtype).to(DEV)
     torch.autograd.backward([total, y], [ds, d["dy"].to(DEV)])
     dx_ref, db_ref = norm_oracle.backward(to_np(d["dy"]), xhat_ref, to_np(w), rstd_ref,

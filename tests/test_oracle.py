@@ -356,3 +356,19 @@ def test_head_no_labels_and_single_label(n_lab):
     assert (out["grad"][n_lab:] == 0).all() and (out["token_loss"][n_lab:] == 0).all()
     ref = head.head_direct(h, w, t)
     assert np.all(np.abs(out["entropy"] - ref["entropy"]) <= 2e-5 + 1e-5 * ref["zmax"])
+
+
+def test_torch_cpu_dequant_equals_the_group_oracle():
+    """The PyTorch CPU restatement bench.py's CPU baseline runs equals the C oracle bit for bit
+    on a quantized projection (bitsandbytes' QuantState layout of nf4_linear.Linear4bit)."""
+    from talm_amd.nf4_linear import Linear4bit
+
+    g = torch.Generator().manual_seed(5)
+    layer = Linear4bit.from_weight(torch.randn(256, 128, generator=g) * 0.05)
+    state = layer.weight.quant_state
+    ours = nf4.dequant_state_torch(layer.weight.data, state)
+    n_blk2 = state.absmax.numel() // state.state2.blocksize
+    ref = nf4.group_dequant(layer.weight.data.numpy(), state.absmax.numpy(),
+                            state.state2.code.numpy(), state.state2.absmax.numpy(),
+                            np.full(n_blk2, float(state.offset), np.float32))
+    assert np.array_equal(ours.view(torch.int16).numpy().view(np.uint16).reshape(-1), ref)
