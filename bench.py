@@ -129,6 +129,30 @@ def kernel_suite(args, only):
                config="calibration")
         del src, dst
 
+    if want("ceilings"):
+        # what PyTorch's own elementwise kernels reach on the traffic mixes of the bandwidth
+        # kernels (same byte counts, cold buffers rotated like theirs): the practical HBM
+        # ceiling of each mix on this box, next to the 8 TB/s peak
+        n_nf4 = 46792704
+        cases = [
+            ("ceiling_fill_0r1w", "write-only fill, 93.6 MB (the NF4 output)", 2 * n_nf4,
+             lambda: {"d": torch.empty(n_nf4, dtype=torch.float16, device=dev)},
+             lambda t: t["d"].fill_(1.0)),
+            ("ceiling_copy_1r1w", "copy of 36.7 MB", 4 * 2048 * 8960,
+             lambda: {"s": torch.ones(2048, 8960, dtype=torch.float16, device=dev),
+                      "d": torch.empty(2048, 8960, dtype=torch.float16, device=dev)},
+             lambda t: t["d"].copy_(t["s"])),
+            ("ceiling_add_2r1w", "c = a + b on [2048, 8960] fp16 (the SwiGLU forward mix)",
+             6 * 2048 * 8960,
+             lambda: {k: torch.ones(2048, 8960, dtype=torch.float16, device=dev) for k in "abc"},
+             lambda t: torch.add(t["a"], t["b"], out=t["c"])),
+        ]
+        for name, what, nbytes, make, op in cases:
+            k = rotation(nbytes)
+            sets = [make() for _ in range(k)]
+            record(name, timed(lambda i: op(sets[i]), k), bytes_=nbytes, config=what, sets=k)
+            del sets
+
     if want("nf4_group"):
         d = workloads.nf4_layer()
         n_rows = d["absmax8"].numel()

@@ -12,7 +12,13 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kVecPerThread = 2;  // 16 elements per thread per grid step
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)) with v_exp_f32 and v_rcp_f32 (1 ulp each; an IEEE fp32
+// division is a ~10-instruction sequence). At 8 elements per 16-byte access the kernels are
+// close to VALU-bound on gfx950 (no packed fp32 math here), so the reciprocal matters: the
+// results are fp16, far coarser than these roundings.
+__device__ __forceinline__ float sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
 
 __device__ __forceinline__ void unpack8(const uint4& a, float* v) {
   v[0] = lo_f(a.x); v[1] = hi_f(a.x); v[2] = lo_f(a.y); v[3] = hi_f(a.y);

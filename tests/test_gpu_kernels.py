@@ -53,12 +53,14 @@ def test_nf4_group_dequant_config1_bit_exact():
         start += n
 
 
-@pytest.mark.parametrize("n_rows,qblock,qblock2", [(256, 64, 256), (1, 8, 1), (37, 128, 5),
-                                                   (1000, 64, 3), (2, 4096, 1)])
-def test_nf4_group_dequant_edge_shapes(n_rows, qblock, qblock2):
-    """Partial last workgroup, odd second-level blocks, wide blocks; subnormal-producing scales
-    (offset chosen so some block scales land near zero)."""
-    _case(f"nf4 group rows={n_rows} qblock={qblock} qblock2={qblock2}")
+@pytest.mark.parametrize("n_rows,qblock,qblock2,shift", [
+    (256, 64, 256, 0), (1, 8, 1, 0), (37, 128, 5, 0), (1000, 64, 3, 0), (2, 4096, 1, 0),
+    (33, 32, 7, 0), (1000, 64, 256, 4), (77, 16, 3, 0)])
+def test_nf4_group_dequant_edge_shapes(n_rows, qblock, qblock2, shift):
+    """Partial last workgroup and wavefront, odd second-level blocks, blocks of 8 to 4096
+    weights (16-byte chunks of codes from 32 up, 8-weight words below), codes that start 4
+    bytes past a 16-byte boundary (`shift`: the word path); subnormal-producing scales."""
+    _case(f"nf4 group rows={n_rows} qblock={qblock} qblock2={qblock2} shift={shift}")
     g = torch.Generator().manual_seed(n_rows + qblock)
     n = n_rows * qblock
     n2 = -(-n_rows // qblock2)
@@ -70,7 +72,9 @@ def test_nf4_group_dequant_edge_shapes(n_rows, qblock, qblock2):
     ref = nf4_oracle.group_dequant(packed.numpy(), absmax8.numpy(), code.numpy(), absmax2.numpy(),
                                    offset2.numpy(), qblock, qblock2)
     out = torch.empty(n, dtype=torch.float16, device=DEV)
-    torch.ops.talm.nf4_group_dequant(packed.to(DEV), absmax8.to(DEV), code.to(DEV),
+    dev_packed = torch.empty(n // 2 + shift, dtype=torch.uint8, device=DEV)[shift:]
+    dev_packed.copy_(packed)
+    torch.ops.talm.nf4_group_dequant(dev_packed, absmax8.to(DEV), code.to(DEV),
                                      absmax2.to(DEV), offset2.to(DEV), out, qblock, qblock2)
     assert np.array_equal(f16_bits(out), ref)
 
