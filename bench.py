@@ -173,7 +173,7 @@ def kernel_suite(args, only):
         del sets, outs
 
     d2 = workloads.norm_rope() if any(want(x) for x in ("addnorm_fwd", "addnorm_bwd", "rope",
-                                                         "stacked")) else None
+                                                         "stacked", "attn")) else None
     # config 2's shapes, and (with "stacked") the 28 layers' rows in one launch: the per-launch
     # floor of these 10-18 MB kernels apart from their streaming rate
     norm_stacks = [st for st in (1, 28) if d2 is not None and (
@@ -237,6 +237,42 @@ def kernel_suite(args, only):
         record("rope_inplace" + ("" if stack == 1 else "_stacked28"), timed(fn, k),
                bytes_=nbytes, config=cfg, sets=k)
         del sets
+
+    if want("attn") and d2 is not None:
+        # the varlen causal GQA attention of one layer at config 2's lengths, on q|k|v views of
+        # one [N, 2048] buffer as in the step; algorithmic FLOPs over the causal pairs: 2 GEMMs
+        # forward (S, P V), 5 backward (S, dP, dV, dQ, dK), 2 * Hq * D FLOP per pair and GEMM
+        from talm_amd import _ops
+
+        lengths, cu = d2["lengths"], d2["cu_seqlens"].to(dev)
+        n, hq, hkv, hd = d2["n"], 12, 2, 128
+        pairs = int(sum(int(x) * (int(x) + 1) // 2 for x in lengths))
+        unit = 2.0 * hq * hd * pairs
+        g = torch.Generator().manual_seed(5)
+        qkv = torch.randn(n, 2048, generator=g).half().to(dev)
+        dqkv = torch.empty_like(qkv)
+        q = qkv[:, :1536].view(n, hq, hd)
+        k = qkv[:, 1536:1792].view(n, hkv, hd)
+        v = qkv[:, 1792:].view(n, hkv, hd)
+        o = torch.empty(n, hq, hd, dtype=torch.float16, device=dev)
+        lse = torch.empty(hq, n, dtype=torch.float32, device=dev)
+        do = (0.1 * torch.randn(n, hq, hd, generator=g)).half().to(dev)
+        ws = torch.empty(_ops.attn_bwd_workspace_bytes(n, hq), dtype=torch.uint8, device=dev)
+        max_len, scale = int(lengths.max()), hd ** -0.5
+
+        def fwd(i):
+            torch.ops.talm.attn_fwd(q, k, v, cu, max_len, scale, o, lse)
+
+        def bwd(i):
+            torch.ops.talm.attn_bwd(q, k, v, o, do, lse, cu, max_len, scale,
+                                    dqkv[:, :1536].view(n, hq, hd),
+                                    dqkv[:, 1536:1792].view(n, hkv, hd),
+                                    dqkv[:, 1792:].view(n, hkv, hd), ws)
+
+        fwd(0)
+        cfg = f"2: lengths {[int(x) for x in lengths]}, Hq 12, Hkv 2, D 128"
+        record("attn_fwd", timed(fwd, 1), flops=2 * unit, config=cfg)
+        record("attn_bwd", timed(bwd, 1), flops=5 * unit, config=cfg)
 
     if want("swiglu_fwd") or want("swiglu_bwd"):
         d3 = workloads.swiglu_inputs()
@@ -496,7 +532,8 @@ def main():
     kernel_args = args if step is None else argparse.Namespace(
         **{**vars(args), "steps": 200, "warmup": 10})
     kernels = kernel_suite(kernel_args, only)
-    dominant = max(kernels, key=lambda e: e["us"]) if kernels else None
+    measured = [e for e in kernels if not e["kernel"].startswith("ceiling_")]
+    dominant = max(measured, key=lambda e: e["us"]) if measured else None
     line_roofline = None
     traffic = MEASURED_TRAFFIC.get(dominant["kernel"]) if dominant is not None else None
     if dominant is not None and "tflops" in dominant:

@@ -85,7 +85,8 @@ struct FwdArgs {
   int64_t v_tok, v_head;
   const int32_t* cu;
   int group;          // query heads per KV head
-  int n_tiles;        // query tiles per sequence (of the longest)
+  int head_chunks;    // workgroups per KV head (group / heads per workgroup)
+  int n_tiles;        // 32-row query tiles per sequence (of the longest)
   float scale_log2;   // softmax scale * log2(e)
   uint16_t* out;
   int64_t o_tok, o_head;
@@ -93,25 +94,120 @@ struct FwdArgs {
   int64_t n_tokens;
 };
 
-template <int W>
-__global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
-  constexpr int kRows = 32 * W;                 // query rows per workgroup
-  constexpr int kChunks = kKeys * (kD / 8);     // 16-byte chunks of a K (or V) tile
-  constexpr int kPer = kChunks / (64 * W);      // chunks per thread
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeys * kKS];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[2][kD * kVS];
+// K and V tiles of the forward in LDS: [64 keys][128 d] fp16 without padding, 16 chunks of 16
+// bytes per row, chunk c of row r at position c ^ tile_swz(r). The direct-to-LDS loads write
+// 1 KiB per wavefront instruction contiguously (4 rows); the swizzle makes both reads free of
+// bank conflicts: the 16-byte row reads of the S = K Q^T operand (8 consecutive rows of one
+// chunk per LDS cycle: tile_swz takes 8 distinct values on them) and the transposing 8-byte
+// reads of the P V operand (4 rows x 2 adjacent chunks per 16 lanes: the pair positions
+// (c / 2) ^ (r & 3) are distinct).
+constexpr int kTileBytes = kKeys * kD * 2;  // 16 KiB
 
-  const int seq = blockIdx.z, head = blockIdx.y;
+__device__ __forceinline__ int tile_swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+__device__ __forceinline__ int tile_chunk(int row, int chunk) { return row * 16 + (chunk ^ tile_swz(row)); }
+
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane i receives element e (0..3) from
+// row 4 e + i / 4 of the 16 x 4 matrix formed by the four halves at each lane's address, column
+// i % 4 (checked on the GPU with an in-bounds probe). With lane j pointing at row K0 + j / 4,
+// columns D0 + 4 (j % 4) of a row-major [keys][d] tile, lane i gets keys K0 .. K0 + 3 of column
+// D0 + i: the transpose of 4 x 16 elements.
+typedef short short4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ half4_t read_tr(const unsigned char* lds) {
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(lds));
+  return __builtin_bit_cast(half4_t, v);
+}
+
+// A 32 x 16 operand of v_mfma_f32_32x32x16_f16 read transposed from a swizzled [rows][128]
+// tile: A[m][k] = tile[row0 + key(k)][col0 + m], lane l holding m = l % 32 and k-slots
+// 8 (l / 32) .. + 7, whose rows follow the accumulator order of the 32-row blocks: slots
+// 8 hh + e hold rows row0 + 4 hh + e (e < 4) and row0 + 8 + 4 hh + e - 4 (e >= 4).
+__device__ __forceinline__ half8_t read_tr_operand(const unsigned char* tile, int row0, int col0,
+                                                   int lane) {
+  const int g = lane >> 4, i = lane & 15, hh = g >> 1;
+  const int col = col0 + 16 * (g & 1) + 4 * (i & 3);
+  half4_t part[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = row0 + 8 * r + 4 * hh + (i >> 2);
+    part[r] = read_tr(tile + tile_chunk(row, col >> 3) * 16 + (col & 7) * 2);
+  }
+  return __builtin_bit_cast(half8_t, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// One [64][128] tile from global rows base[r * ld + c] (r < rows_valid, else zeros) into `dst`
+// with direct-to-LDS 16-byte loads: block b (rows 4 b .. 4 b + 3) by wavefront b % W.
+template <int W>
+__device__ __forceinline__ void dma_tile(const uint16_t* base, int64_t ld, int rows_valid,
+                                         unsigned char* dst, int wave, int lane) {
+  const __amdgpu_buffer_rsrc_t rsrc = buffer_rsrc(base);
+  const int row_in = lane >> 4, pos = lane & 15;
+#pragma unroll
+  for (int it = 0; it < (kKeys / 4 + W - 1) / W; ++it) {
+    const int b = wave + it * W;
+    if (b >= kKeys / 4) break;
+    const int row = 4 * b + row_in;
+    const int chunk = pos ^ tile_swz(row);
+    const uint32_t off = row < rows_valid ? static_cast<uint32_t>((row * ld + chunk * 8) * 2) : kOob;
+    dma16(rsrc, dst + b * 1024, off);
+  }
+}
+
+// wait_vmcnt with a count known at run time (at most 16)
+__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
+  switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 12: wait_vmcnt<12>(); break;
+    case 14: wait_vmcnt<14>(); break;
+    case 16: wait_vmcnt<16>(); break;
+    default: wait_vmcnt<0>(); break;
+  }
+}
+
+// Forward, one workgroup per (sequence, 32-row query tile, W query heads of one KV head), with
+// S groups of W wavefronts: group g takes the key tiles g, g + S, g + 2 S, ..., one wavefront per
+// head, so the serial key loop of a long query tile is S times shorter (its length, not the
+// chip, bounds the kernel at these sequence lengths); the groups' partial results are merged
+// through LDS at the end. The K / V tiles of the KV head are loaded once for the W heads.
+// Scores are computed transposed, S^T = K Q^T, so each lane owns one query row: the online
+// max / sum and the output rescale are per-lane scalars, and the exponentiated scores are
+// already the B operand of O^T = V^T P^T, whose A operand is read transposed from the row-major
+// V tile. Two LDS slots per group: the next tiles' loads fly during this step's math.
+template <int W, int S>
+__global__ __launch_bounds__(64 * W * S) void attn_fwd_kernel(FwdArgs a) {
+  constexpr int kStepBytes = S * 2 * kTileBytes;        // the K and V tiles of one step
+  constexpr int kRing = 2 * kStepBytes;
+  constexpr int kMerge = (S - 1) * W * (64 * 64 * 4 + 64 * 8);  // partial O, m, l per wavefront
+  constexpr int kStage = W * 32 * kKS * 2;              // fp16 output rows per head
+  constexpr int kSmem = kRing > kMerge + kStage ? kRing : kMerge + kStage;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmem];
+
+  const int seq = blockIdx.z;
+  const int kvh = static_cast<int>(blockIdx.y) / a.head_chunks;
+  const int hc = static_cast<int>(blockIdx.y) % a.head_chunks;
   const int tile = a.n_tiles - 1 - static_cast<int>(blockIdx.x);  // longest tiles first
   const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
-  const int q0 = tile * kRows;
-  if (q0 >= len) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q0 = tile * 32;
+  if (q0 >= len) return;  // the whole workgroup, before any barrier
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wavefront index in a scalar register: everything the branches, loop bounds and the
+  // direct-to-LDS addresses derive from it stays wavefront-uniform
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hw = wave % W, grp = wave / W;  // head slot, key group
   const int hh = lane >> 5, l32 = lane & 31;
-  const int kvh = head / a.group;
+  const int head = kvh * a.group + hc * W + hw;
 
-  // this lane's query row and its Q fragments (k-slots d = 16 s + 8 hh .. + 8)
-  const int qrow = q0 + 32 * wave + l32;
+  // this lane's query row and its Q fragments (the B operand: k-slots d = 16 s + 8 hh .. + 8)
+  const int qrow = q0 + l32;
   const int qr = min(qrow, len - 1);
   half8_t qf[kD / 16];
   {
@@ -120,35 +216,23 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
     for (int s = 0; s < kD / 16; ++s) qf[s] = *reinterpret_cast<const half8_t*>(qp + 16 * s);
   }
 
-  const int kend = min(len, q0 + kRows);  // keys any row of this tile can see
+  const int kend = min(len, q0 + 32);  // keys any row of this tile can see
   const int n_kt = (kend + kKeys - 1) / kKeys;
+  const int n_steps = (n_kt + S - 1) / S;
+  const int key_lim = min(qrow, len - 1);  // the last key this lane's row may see
   const uint16_t* kbase = a.k + static_cast<int64_t>(s0) * a.k_tok + kvh * a.k_head;
   const uint16_t* vbase = a.v + static_cast<int64_t>(s0) * a.v_tok + kvh * a.v_head;
-
-  // tile loads: chunk c = p * 64W + tid -> key c % 64, column chunk c / 64 (for V: 64 lanes
-  // of a wavefront read 64 keys of one 8-column chunk, so the transposed LDS writes of one
-  // instruction fill one row of vt)
-  u32x4 kreg[2][kPer], vreg[2][kPer];
-  auto load_tile = [&](int slot, int kt) {
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int c = p * 64 * W + tid, key = min(kt * kKeys + (c & 63), len - 1), cc = c >> 6;
-      kreg[slot][p] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
-      vreg[slot][p] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int c = p * 64 * W + tid, key = c & 63, cc = c >> 6;
-      *reinterpret_cast<u32x4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[buf][p];
-      const uint32_t w4[4] = {vreg[buf][p].x, vreg[buf][p].y, vreg[buf][p].z, vreg[buf][p].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt[buf][(8 * cc + 2 * e) * kVS + key] = static_cast<uint16_t>(w4[e] & 0xffffu);
-        vt[buf][(8 * cc + 2 * e + 1) * kVS + key] = static_cast<uint16_t>(w4[e] >> 16);
-      }
-    }
+  // the group's W wavefronts load its tile: 16 blocks of 1 KiB per K or V tile, block b by
+  // wavefront b % W of the group
+  auto slot_of = [&](int step) { return smem + (step & 1) * kStepBytes + grp * 2 * kTileBytes; };
+  auto issue = [&](int step) {  // the group's tile of `step`, if it exists
+    const int kt = step * S + grp;
+    if (kt >= n_kt) return;
+    unsigned char* slot = slot_of(step);
+    const int r0 = kt * kKeys;
+    dma_tile<W>(kbase + static_cast<int64_t>(r0) * a.k_tok, a.k_tok, len - r0, slot, hw, lane);
+    dma_tile<W>(vbase + static_cast<int64_t>(r0) * a.v_tok, a.v_tok, len - r0, slot + kTileBytes,
+                hw, lane);
   };
 
   f32x16 o[kD / 32];
@@ -156,9 +240,24 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
   for (int j = 0; j < kD / 32; ++j)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[j][v] = 0.f;
+  // m: the reference maximum of the row's scaled scores (log2 units), raised only when the
+  // row's maximum exceeds it by more than kLazy (the exponentials stay <= 2^kLazy, far inside
+  // fp16, and the final O / l uses the same reference: exact up to rounding)
+  constexpr float kLazy = 8.f;
   float m = -INFINITY, lsum = 0.f;
+  const float c = a.scale_log2;
 
-  auto compute = [&](int kt, int buf) {
+  issue(0);
+  for (int step = 0; step < n_steps; ++step) {
+    const int kt = step * S + grp;
+    // this group's tile of the step has landed (the next step's loads are not issued yet)
+    wait_vmcnt<0>();
+    lds_barrier();  // every group's tile has; everyone is done with step - 1 (its slots are free)
+    issue(step + 1);
+    if (kt >= n_kt) continue;  // this group has no tile left (barriers stay matched: no return)
+    const unsigned char* ks = slot_of(step);
+    const unsigned char* vs = ks + kTileBytes;
+    const uint4* k16 = reinterpret_cast<const uint4*>(ks);
     const int k0 = kt * kKeys;
     // S^T for keys k0 + 32 b + (8 (v / 4) + 4 hh + v % 4), this lane's query column
     f32x16 st[2];
@@ -166,40 +265,53 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) st[b][v] = 0.f;
-      const uint16_t* kr = &ks[buf][(32 * b + l32) * kKS + 8 * hh];
 #pragma unroll
       for (int s = 0; s < kD / 16; ++s)
         st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            *reinterpret_cast<const half8_t*>(kr + 16 * s), qf[s], st[b], 0, 0, 0);
+            __builtin_bit_cast(half8_t, k16[tile_chunk(32 * b + l32, 2 * s + hh)]), qf[s], st[b],
+            0, 0, 0);
+    }
+    // causal / length mask only on a tile that reaches past the first query row of the
+    // workgroup or past the sequence: a real (uniform) branch; the empty volatile asm keeps the
+    // compiler from turning it into selects executed on every tile
+    if (k0 + kKeys - 1 > q0 || k0 + kKeys > len) {
+      asm volatile("");
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = k0 + 32 * b + 8 * (v >> 2) + 4 * hh + (v & 3);
+          st[b][v] = key > key_lim ? -INFINITY : st[b][v];
+        }
     }
     float mt = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = k0 + 32 * b + 8 * (v >> 2) + 4 * hh + (v & 3);
-        const float t = (key <= qrow && key < len) ? st[b][v] * a.scale_log2 : -INFINITY;
-        st[b][v] = t;
-        mt = fmaxf(mt, t);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float m_new = fmaxf(m, mt);
-    const float alpha = m == -INFINITY ? 0.f : exp2_(m - m_new);
-    m = m_new;
+      for (int v = 0; v < 16; ++v) mt = fmaxf(mt, st[b][v]);
+    mt = c * fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const bool grow = mt > m + kLazy;
+    if (__ballot(grow)) {  // some row's maximum moved: rescale those rows
+      asm volatile("");
+      const float m_new = grow ? mt : m;
+      const float alpha = exp2_(m - m_new);  // 0 on the first tile (m = -inf), 1 if unchanged
+      m = m_new;
+      lsum *= alpha;
+#pragma unroll
+      for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[j][v] *= alpha;
+    }
     float ps = 0.f;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = exp2_(st[b][v] - m_new);
-        st[b][v] = p;
-        ps += p;
+        const float pv = exp2_(__builtin_fmaf(st[b][v], c, -m));
+        st[b][v] = pv;
+        ps += pv;
       }
-    lsum = lsum * alpha + ps;
-#pragma unroll
-    for (int j = 0; j < kD / 32; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[j][v] *= alpha;
+    lsum += ps;
     // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per step in the accumulator's key order
 #pragma unroll
     for (int b = 0; b < 2; ++b)
@@ -208,25 +320,49 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
         half8_t pb;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(st[b][8 * h + e]);
-        const int kb = 32 * b + 16 * h + 4 * hh;
 #pragma unroll
-        for (int j = 0; j < kD / 32; ++j) {
-          const uint16_t* vr = &vt[buf][(32 * j + l32) * kVS + kb];
-          const half4_t lo = *reinterpret_cast<const half4_t*>(vr);
-          const half4_t hi = *reinterpret_cast<const half4_t*>(vr + 8);
-          const half8_t va = __builtin_bit_cast(
-              half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, o[j], 0, 0, 0);
-        }
+        for (int j = 0; j < kD / 32; ++j)
+          o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              read_tr_operand(vs, 32 * b + 16 * h, 32 * j, lane), pb, o[j], 0, 0, 0);
       }
-  };
-  tile_pipeline(n_kt, load_tile, store_tile, compute);
+  }
+  lsum += __shfl_xor(lsum, 32, kWave);  // the row's sum over both halves of the lanes
 
-  // O = O^T / l through LDS: each wavefront stages its 32 rows x D, then 16-byte row stores
-  const float l_tot = lsum + __shfl_xor(lsum, 32, kWave);
-  const float inv = 1.f / l_tot;
+  // merge the groups into group 0: each other group's wavefront leaves its (m, l, O) in LDS
   __syncthreads();  // every wavefront is done with the tiles
-  uint16_t* os = &ks[0][0] + wave * 32 * kKS;
+  float* part_o = reinterpret_cast<float*>(smem);                        // [group-1][W][64][64]
+  float* part_ml = part_o + (S - 1) * W * 64 * 64;                       // [group-1][W][64][2]
+  if (grp > 0) {
+    float* po = part_o + ((grp - 1) * W + hw) * 64 * 64;
+#pragma unroll
+    for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) po[(16 * j + v) * 64 + lane] = o[j][v];
+    float* pml = part_ml + ((grp - 1) * W + hw) * 64 * 2;
+    pml[2 * lane] = m;
+    pml[2 * lane + 1] = lsum;
+  }
+  __syncthreads();
+  if (grp > 0) return;  // no barrier follows for the other groups
+#pragma unroll
+  for (int g = 1; g < S; ++g) {
+    const float* po = part_o + ((g - 1) * W + hw) * 64 * 64;
+    const float* pml = part_ml + ((g - 1) * W + hw) * 64 * 2;
+    const float m2 = pml[2 * lane], l2 = pml[2 * lane + 1];
+    const float m_new = fmaxf(m, m2);
+    const float a1 = m == -INFINITY ? 0.f : exp2_(m - m_new);
+    const float a2 = m2 == -INFINITY ? 0.f : exp2_(m2 - m_new);
+    m = m_new;
+    lsum = lsum * a1 + l2 * a2;
+#pragma unroll
+    for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[j][v] = o[j][v] * a1 + po[(16 * j + v) * 64 + lane] * a2;
+  }
+
+  // O = O^T / l through LDS: each head stages its 32 rows x D, then 16-byte row stores
+  const float inv = 1.f / lsum;
+  uint16_t* os = reinterpret_cast<uint16_t*>(smem + kMerge) + hw * 32 * kKS;
 #pragma unroll
   for (int j = 0; j < kD / 32; ++j)
 #pragma unroll
@@ -238,12 +374,14 @@ __global__ __launch_bounds__(64 * W, 1) void attn_fwd_kernel(FwdArgs a) {
       *reinterpret_cast<uint2*>(&os[l32 * kKS + d0]) = w;
     }
   if (hh == 0 && qrow < len)
-    a.lse[static_cast<int64_t>(head) * a.n_tokens + s0 + qrow] = (m + __log2f(l_tot)) * kLn2;
-  __syncthreads();
+    a.lse[static_cast<int64_t>(head) * a.n_tokens + s0 + qrow] = (m + __log2f(lsum)) * kLn2;
+  // the wavefront reads back its own staging rows (the other groups have exited: no workgroup
+  // barrier): its LDS writes complete first, and the compiler keeps the order
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
   for (int it = 0; it < (32 * kD / 8) / 64; ++it) {
-    const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
-    const int row = q0 + 32 * wave + r;
+    const int cc16 = it * 64 + lane, r = cc16 / (kD / 8), cc = cc16 % (kD / 8);
+    const int row = q0 + r;
     if (row < len)
       *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(s0 + row) * a.o_tok + head * a.o_head + 8 * cc) =
           *reinterpret_cast<const u32x4*>(&os[r * kKS + 8 * cc]);
@@ -668,23 +806,36 @@ TALM_API int talm_attn_fwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
                     v_stride_head, o_stride_tok, o_stride_head})
     if (s < 0 || s % 8)
       return fail(TALM_EINVAL, "attn_fwd: strides must be non-negative multiples of 8 elements");
+  if (k_stride_tok >= (int64_t{1} << 23) || v_stride_tok >= (int64_t{1} << 23))
+    return fail(TALM_EINVAL, "attn_fwd: k / v token strides must be below 2^23 elements");
   if (n_seqs == 0 || max_seqlen == 0 || n_tokens == 0) return ok();
   if (!q || !k || !v || !cu_seqlens || !out || !lse) return fail(TALM_EINVAL, "attn_fwd: null pointer");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
     return fail(TALM_EINVAL, "attn_fwd: q, k, v and out must be 16-byte aligned");
-  constexpr int W = 4;
+  const int group = n_q_heads / n_kv_heads;
+  // query heads per workgroup: the largest of 4, 3, 2, 1 that divides the group; two groups
+  // of wavefronts split each workgroup's key tiles
+  int w = 1;
+  for (int cand : {4, 3, 2})
+    if (group % cand == 0) { w = cand; break; }
   FwdArgs a{};
   a.q = q; a.q_tok = q_stride_tok; a.q_head = q_stride_head;
   a.k = k; a.k_tok = k_stride_tok; a.k_head = k_stride_head;
   a.v = v; a.v_tok = v_stride_tok; a.v_head = v_stride_head;
-  a.cu = cu_seqlens; a.group = n_q_heads / n_kv_heads;
-  a.n_tiles = (max_seqlen + 32 * W - 1) / (32 * W);
+  a.cu = cu_seqlens; a.group = group; a.head_chunks = group / w;
+  a.n_tiles = (max_seqlen + 31) / 32;
   a.scale_log2 = scale * 1.44269504088896341f;
   a.out = out; a.o_tok = o_stride_tok; a.o_head = o_stride_head;
   a.lse = lse; a.n_tokens = n_tokens;
-  hipLaunchKernelGGL((attn_fwd_kernel<W>), dim3(static_cast<unsigned>(a.n_tiles),
-                     static_cast<unsigned>(n_q_heads), static_cast<unsigned>(n_seqs)),
-                     dim3(64 * W), 0, as_stream(stream), a);
+  const dim3 grid(static_cast<unsigned>(a.n_tiles), static_cast<unsigned>(n_kv_heads * a.head_chunks),
+                  static_cast<unsigned>(n_seqs));
+  const hipStream_t s = as_stream(stream);
+  switch (w) {
+    case 4: hipLaunchKernelGGL((attn_fwd_kernel<4, 2>), grid, dim3(512), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((attn_fwd_kernel<3, 2>), grid, dim3(384), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_fwd_kernel<2, 2>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((attn_fwd_kernel<1, 2>), grid, dim3(128), 0, s, a); break;
+  }
   return check_launch("attn_fwd");
 }
 
