@@ -321,23 +321,23 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
 // The A-fragment hook of head_grad: ring step kt covers columns [zc + kt BK, + BK) of one 128-column
 // tile (BK divides 128, zc is a multiple of BK); lane l of the wavefront owning rows
 // [r0, r0 + 32 FRAGS) multiplies fragment i (row r0 + 32 i + l % 32) by the row's factor of that
-// tile. r0 is a multiple of 32 FRAGS, so the lane's FRAGS factors are adjacent: one load per step.
-template <int BK, int FRAGS>
+// tile. r0 is a multiple of 32 FRAGS, so the lane's FRAGS factors are adjacent: one load per step,
+// into the register set of the step's ring slot.
+template <int BK, int FRAGS, int SLOTS>
 struct TileScale {
   static_assert(FRAGS == 2 || FRAGS == 4, "two or four 32-row A fragments per wavefront");
   using Word = typename std::conditional<FRAGS == 4, uint2, uint32_t>::type;
   const uint16_t* base;  // &scale[scale_index(r0 + lane % 32, 0, blocks)]
   int64_t tile_stride;   // blocks * 128
   int zc;
-  Word nxt, cur;
-  __device__ __forceinline__ void prefetch(int kt) {
-    nxt = *reinterpret_cast<const Word*>(base + ((zc + kt * BK) >> 7) * tile_stride);
+  Word f[SLOTS];
+  __device__ __forceinline__ void prefetch(int kt, int slot) {
+    f[slot] = *reinterpret_cast<const Word*>(base + ((zc + kt * BK) >> 7) * tile_stride);
   }
-  __device__ __forceinline__ void advance() { cur = nxt; }
-  __device__ __forceinline__ half8_t apply(half8_t a, int i) const {
+  __device__ __forceinline__ half8_t apply(half8_t a, int i, int slot) const {
     uint32_t w;
-    if constexpr (FRAGS == 4) w = i < 2 ? cur.x : cur.y;
-    else w = cur;
+    if constexpr (FRAGS == 4) w = i < 2 ? f[slot].x : f[slot].y;
+    else w = f[slot];
     const uint16_t h = static_cast<uint16_t>((i & 1) ? w >> 16 : w & 0xffffu);
     return a * __builtin_bit_cast(_Float16, h);
   }
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
   la.init(a.Z + static_cast<int64_t>(m0) * a.ldz + zc, a.ldz, a.n_grad - m0, kn, wave, lane);
   lb.init(a.WT + static_cast<int64_t>(n0) * a.ldwt + a.col0 + zc, a.ldwt, a.hidden - n0, kn,
           wave, lane);
-  TileScale<S::kBK, S::kFragM> sc;
+  TileScale<S::kBK, S::kFragM, S::kStages> sc;
   sc.base = a.scale + scale_index(m0 + wm * S::kWaveM + (lane & 31), 0, a.scale_blocks);
   sc.tile_stride = static_cast<int64_t>(a.scale_blocks) * 128;
   sc.zc = kn > 0 ? zc : 0;  // an empty part (zc may be the group's end) still loads in range

@@ -37,7 +37,7 @@ struct TileShape {
   static constexpr int kStageBytes = (kAChunks + kBChunks) * 16;
   static constexpr int kRing = STAGES * kStageBytes;
   static constexpr int kPerCu = 512 / kThreads;
-  static_assert(STAGES == 2 || STAGES == 3, "ring depth");
+  static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
   static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "32x32 MFMA blocks");
   static_assert(BK == 32 || BK == 64, "swizzle keys exist for 4 and 8 chunks per row");
   static_assert(kRing <= 160 * 1024, "LDS per CU");
@@ -131,20 +131,21 @@ template <class S>
 using Acc = f32x16[S::kFragM][S::kFragN];
 
 // Scaling of the A fragments between their LDS read and the MFMAs, per ring step. The default
-// leaves them as read; a scaling hook loads step kt's factors in prefetch(kt) (one step ahead,
-// before the DMA group the next step waits for, so that wait covers them too), makes them current
-// in advance() and multiplies fragment i of the wavefront in apply().
+// leaves them as read; a scaling hook loads step kt's factors into its register set `slot` (the
+// step's ring slot) in prefetch(kt, slot), issued right before step kt's DMA group so that the
+// wait for that group covers them too, and multiplies fragment i of the wavefront by them in
+// apply(a, i, slot). The ring is unrolled by its depth, so `slot` is a compile-time index and no
+// register is copied (a copy of a loaded register would wait for its load).
 struct NoScale {
-  __device__ __forceinline__ void prefetch(int) {}
-  __device__ __forceinline__ void advance() {}
-  __device__ __forceinline__ half8_t apply(half8_t a, int) const { return a; }
+  __device__ __forceinline__ void prefetch(int, int) {}
+  __device__ __forceinline__ half8_t apply(half8_t a, int, int) const { return a; }
 };
 
 // One step of the wavefront's block: BK / 16 x (kFragM A + kFragN B fragments, their MFMAs).
 template <class S, class Scale = NoScale>
 __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uint4* __restrict__ Bs,
                                          Acc<S>& acc, int lane, int wm, int wn,
-                                         const Scale& scale = Scale()) {
+                                         const Scale& scale = Scale(), int slot = 0) {
   constexpr int kSteps = S::kBK / 16;
   half8_t a[kSteps][S::kFragM], b[kSteps][S::kFragN];
 #pragma unroll
@@ -153,7 +154,7 @@ __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uin
 #pragma unroll
     for (int i = 0; i < S::kFragM; ++i)
       a[ks][i] = scale.apply(__builtin_bit_cast(
-          half8_t, As[swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), kc)]), i);
+          half8_t, As[swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), kc)]), i, slot);
 #pragma unroll
     for (int j = 0; j < S::kFragN; ++j)
       b[ks][j] = __builtin_bit_cast(
@@ -168,16 +169,30 @@ __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uin
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks][i], b[ks][j], acc[i][j], 0, 0, 0);
 }
 
+// Wait until at most `later` whole groups of N operations are in flight (later <= 2).
+template <int N>
+__device__ __forceinline__ void wait_groups(int later) {
+  if (later >= 2) wait_vmcnt<2 * N>();
+  else if (later == 1) wait_vmcnt<N>();
+  else wait_vmcnt<0>();
+}
+
 // acc = sum over nk steps. issue(slot, kt) enqueues step kt's A block at `slot` and its B block
 // at slot + A bytes, exactly Loader<S, BM>::kPer + Loader<S, BN>::kPer DMA instructions per
-// thread. Step kt waits for its own group (with three slots the next group stays in flight); one
-// barrier makes every wavefront's data visible and retires the slot read in step kt - 1, which
-// then receives step kt + STAGES - 1. scale.prefetch(kt + 1) is issued just before the group of
-// step kt + STAGES - 1, so the same wait that covers step kt + 1's operands covers its factors.
+// thread. Step kt lives in ring slot kt % STAGES, and STAGES - 1 steps are in flight ahead of the
+// one being computed: step kt waits for its own group only (the groups of steps kt + 1 ..
+// kt + STAGES - 2 stay in flight), one barrier makes every wavefront's data visible and retires
+// the slot read in step kt - 1, which then receives step kt + STAGES - 1. With a scaling hook,
+// step kt's factors are loaded right before its group and every step issues a full group (past
+// nk the loaders read zeros into a retired slot) and one factor load (clamped to the last step,
+// step 0 when nk is 0), so every wait counts whole groups. The step loop is unrolled by STAGES: slot indices and LDS
+// offsets are compile-time constants.
 template <class S, class Issue, class Scale = NoScale>
 __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& issue, Acc<S>& acc,
                                           int lane, int wave, Scale&& scale = Scale()) {
-  constexpr int kGroup = Loader<S, S::kBM>::kPer + Loader<S, S::kBN>::kPer;
+  constexpr bool kScaled = !std::is_same<std::decay_t<Scale>, NoScale>::value;
+  constexpr int kGroup = Loader<S, S::kBM>::kPer + Loader<S, S::kBN>::kPer + (kScaled ? 1 : 0);
+  constexpr int kSt = S::kStages;
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 #pragma unroll
   for (int i = 0; i < S::kFragM; ++i)
@@ -185,38 +200,30 @@ __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& i
     for (int j = 0; j < S::kFragN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-  // With a scaling hook every step issues a full group (past nk the loaders read zeros into a
-  // retired slot) and one factor load (clamped to the last step), so the compiler's own wait for
-  // the factors, which it places where step kt + 1's factors become current, is the same
-  // vmcnt(kGroup) as the ring's.
-  constexpr bool kScaled = !std::is_same<std::decay_t<Scale>, NoScale>::value;
-#pragma unroll
-  for (int st = 0; st < S::kStages - 1; ++st) {
-    if (kScaled || st < nk) issue(smem + st * S::kStageBytes, st);
-    if (kScaled && st == 0) {  // step 0's factors right behind its group
-      asm volatile("" ::: "memory");
-      scale.prefetch(0);
-      asm volatile("" ::: "memory");
-    }
-  }
-  int s = 0;  // slot of step kt
-  for (int kt = 0; kt < nk; ++kt) {
-    if (S::kStages == 3 && kt + 1 < nk) wait_vmcnt<kGroup>();
-    else wait_vmcnt<0>();
-    lds_barrier();
-    scale.advance();
+  auto issue_step = [&](int slot, int kt) {
     if (kScaled) {
-      scale.prefetch(kt + 1 < nk ? kt + 1 : kt);
-      asm volatile("" ::: "memory");  // the factor load stays ahead of the group
+      asm volatile("" ::: "memory");  // the factor load stays right before its group
+      scale.prefetch(kt < nk ? kt : (nk > 0 ? nk - 1 : 0), slot);  // in range when nk is 0
+      asm volatile("" ::: "memory");
     }
-    if (kScaled || kt + S::kStages - 1 < nk) {
-      const int s2 = s == 0 ? S::kStages - 1 : s - 1;  // slot (kt + STAGES - 1) % STAGES
-      issue(smem + s2 * S::kStageBytes, kt + S::kStages - 1);
+    issue(smem + slot * S::kStageBytes, kt);
+  };
+#pragma unroll
+  for (int st = 0; st < kSt - 1; ++st)
+    if (kScaled || st < nk) issue_step(st, st);
+  for (int kb = 0; kb < nk; kb += kSt) {
+#pragma unroll
+    for (int i = 0; i < kSt; ++i) {  // step kt = kb + i in slot i
+      const int kt = kb + i;
+      if (kt >= nk) break;
+      wait_groups<kGroup>(kScaled ? kSt - 2 : min(kSt - 2, nk - 1 - kt));
+      lds_barrier();
+      if (kScaled || kt + kSt - 1 < nk) issue_step((i + kSt - 1) % kSt, kt + kSt - 1);
+      const unsigned char* st = smem + i * S::kStageBytes;
+      mma_step<S>(reinterpret_cast<const uint4*>(st),
+                  reinterpret_cast<const uint4*>(st + S::kAChunks * 16), acc, lane, wm, wn, scale,
+                  i);
     }
-    const unsigned char* st = smem + s * S::kStageBytes;
-    mma_step<S>(reinterpret_cast<const uint4*>(st),
-                reinterpret_cast<const uint4*>(st + S::kAChunks * 16), acc, lane, wm, wn, scale);
-    s = s + 1 == S::kStages ? 0 : s + 1;
   }
   __syncthreads();  // every wavefront is done with the ring before the caller reuses the LDS
 }
