@@ -46,7 +46,9 @@ class AdapterCopies:
         self.table = None       # device int64 [weights, 9] of `layout` (optimizer columns 0)
         self.buffer = None      # flat fp16: copies of the current layout
         self.keys = []          # per weight: the key its copy in `buffer` was made from
-        self.loose = {}         # id(weight) or pair ids -> (key(s), copy) made outside a layout
+        # id(weight) or pair ids -> (weakref(s), key(s), copy) made outside a layout; the
+        # weakrefs tell a live weight from a freed one whose id and storage a new one reuses
+        self.loose = {}
         self.adopted_by = None  # the optimizer whose step wrote `buffer`
         # rewrite `buffer` in place instead of a fresh buffer per refresh / optimizer step: for a
         # step replayed from a HIP graph, whose forward reads the copies at the address it was
@@ -163,10 +165,10 @@ class AdapterCopies:
             return self.buffer[h_off:h_off + param.numel()].view(param.shape)
         key = _key(param)
         hit = self.loose.get(id(param))
-        if hit is None or hit[0] != key:
-            hit = (key, param.detach().to(torch.float16))
+        if hit is None or hit[0]() is not param or hit[1] != key:
+            hit = (weakref.ref(param), key, param.detach().to(torch.float16))
             self.loose[id(param)] = hit
-        return hit[1]
+        return hit[2]
 
     def pair_t(self, params):
         """[cols, sum of rows] fp16: the weights' transposes side by side (A^T of a q|k|v node's
@@ -175,6 +177,8 @@ class AdapterCopies:
         positions = tuple(self._position(p) for p in params)
         ids = tuple(id(p) for p in params)
         k = self.pair_index.get(ids)
+        if k is not None and self.pairs[k] != positions:  # ids of freed weights, reused
+            k = None
         if k is None or not known:
             if k is None:
                 self.pair_index[ids] = len(self.pairs)
@@ -189,11 +193,11 @@ class AdapterCopies:
                 return self.buffer[t_off:t_off + cols * width].view(cols, width)
         keys = tuple(_key(p) for p in params)
         hit = self.loose.get(ids)
-        if hit is None or hit[0] != keys:
-            hit = (keys, torch.cat([p.detach() for p in params], 0).t().to(torch.float16)
-                   .contiguous())
+        if hit is None or any(r() is not p for r, p in zip(hit[0], params)) or hit[1] != keys:
+            hit = (tuple(weakref.ref(p) for p in params), keys,
+                   torch.cat([p.detach() for p in params], 0).t().to(torch.float16).contiguous())
             self.loose[ids] = hit
-        return hit[1]
+        return hit[2]
 
 
 COPIES = AdapterCopies()
