@@ -13,7 +13,10 @@ it. `GraphedTrainer` captures the forward and backward of the step once per buck
   difference is rounding where a library GEMM picks another algorithm for the larger row count;
 - the head takes every row as a gradient row, with no labelled-first count read on the host;
 - the batch tensors are copied into the static input buffers the graph reads;
-- the LoRA gradients are the graph's own tensors, handed to the parameters after each replay.
+- the LoRA gradients live in one set of buffers shared by every graph: each capture starts
+  by zeroing them (fill kernels, part of the graph) and the backward accumulates into them
+  in place, so 97 buckets hold one gradient set, not 97. They are handed to the parameters
+  after each replay.
 
 The optimizer tail stays eager: GradScaler unscale and update, clipping, `AdapterAdamW` and the
 learning-rate schedule. It is about ten launches, and their host cost overlaps the graph's GPU
@@ -53,6 +56,7 @@ class GraphedTrainer:
         self.static = None
         self.graphs = {}           # bucket -> (graph, loss, gradients, per-token metrics)
         self.pool = None
+        self.grads = None          # the LoRA gradient buffers every graph writes
         self.capture_seconds = 0.0
         self.replays = 0
         COPIES.in_place = True
@@ -92,20 +96,27 @@ class GraphedTrainer:
             raise ValueError(f"GraphedTrainer: bucket {n_bucket} for a [{b}, {s}] batch")
         start = time.perf_counter()
         held = [p.grad for p in t.params]
-        for p in t.params:
-            p.grad = None
+        if self.grads is None:  # outside the graphs' pool: they outlive every capture
+            self.grads = [torch.zeros_like(p) for p in t.params]
+        for p, g in zip(t.params, self.grads):
+            p.grad = g
         graph = torch.cuda.CUDAGraph()
         # the pad sequence is shorter than one bucket step (a full bucket when no token is real)
         with unpad.static_tokens(n_bucket, max_pad=self.bucket):
             with torch.cuda.graph(graph, pool=self.pool):
+                for g in self.grads:
+                    g.zero_()
                 with torch.autocast("cuda", dtype=torch.float16):
                     out = t.model(**self.static)
                 t.scaler.scale(out.loss).backward()
         if self.pool is None:
             self.pool = graph.pool()
-        grads = [p.grad for p in t.params]
-        if any(g is None for g in grads):
-            raise RuntimeError("GraphedTrainer: a LoRA parameter got no gradient in the capture")
+        # the backward accumulated into the shared buffers in place (it replaces a parameter's
+        # .grad only when it cannot add into it)
+        if any(p.grad is not g for p, g in zip(t.params, self.grads)):
+            raise RuntimeError("GraphedTrainer: the backward did not accumulate into the shared "
+                               "gradient buffers")
+        grads = self.grads
         for p, g in zip(t.params, held):
             p.grad = g
         # the per-token metrics (patches.LAST_STEP) this graph writes on every replay: kept with
@@ -127,6 +138,7 @@ class GraphedTrainer:
         """Drop the graphs and their pool; the adapters' copies go back to fresh buffers."""
         self.graphs.clear()
         self.pool = None
+        self.grads = None
         self.static = None
         COPIES.in_place = False
 
