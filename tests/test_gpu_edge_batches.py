@@ -1,0 +1,175 @@
+"""The patched causal LM on edge batches against the unpatched forward.
+
+The reference checks its step on batches its public rows do not contain
+(solution/test_robustness.py:85-99 lists them): a row with no labelled token, rows without
+padding, a one-token row, rows of the full 512-token window, a batch with no labelled token at
+all, every position labelled, a single row, token counts that are no multiple of any block size,
+and masks that are not right-padded (left padding, a hole in a row). The padding removal must
+switch itself off on the last two instead of failing.
+
+Here those cases go through this build's QLoRA model: NF4 double-quant base and LoRA r16/a32 on
+q and v, under fp16 autocast. The comparison is against the unpatched forward, i.e. the padded
+batch with full logits and PyTorch's cross-entropy. It covers both packings of the patch:
+- the dynamic one, with host-side row statistics;
+- the fixed-shape one (`unpad.static_tokens`), which the HIP-graph step captures and which
+  takes right-padded rows only.
+
+Compared, with fp16 tolerances (the two paths round differently):
+- the loss (NaN on both sides when nothing is labelled);
+- the per-token loss, entropy and accuracy that `patches.LAST_STEP` hands to the trainer,
+  scattered back to [B, T];
+- the labelled count;
+- the LoRA gradients (zeros on both sides when nothing is labelled).
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from talm_amd import engaged, patches, qlora_model, unpad
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 640
+
+
+def _model():
+    config = qlora_model.qwen2_config(vocab_size=VOCAB, hidden_size=256, intermediate_size=512,
+                                      num_hidden_layers=2, num_attention_heads=2,
+                                      num_key_value_heads=1, head_dim=128)
+    model = qlora_model.build_model(config, seed=4)
+    with torch.no_grad():  # B starts non-zero, so the adapters take part in the first step
+        gen = torch.Generator(device="cuda").manual_seed(11)
+        for p in qlora_model.lora_parameters(model):
+            if p.abs().sum() == 0:
+                p.copy_(0.02 * torch.randn(p.shape, generator=gen, device="cuda"))
+    return model
+
+
+def _batch(lengths, prompt=3, left=False, labelled_rows=None, every_position=False, hole=False,
+           seed=0):
+    """input_ids, attention_mask and labels the way a causal-LM collator lays them out: rows of
+    the given lengths padded to the longest (on the right unless `left`), -100 on the first
+    `prompt` tokens of each row and on the padding, no labels on rows outside `labelled_rows`,
+    every real token labelled with `every_position`, and with `hole` one masked (and unlabelled)
+    position inside the first row."""
+    gen = torch.Generator().manual_seed(seed)
+    batch, seq = len(lengths), max(lengths)
+    ids = torch.randint(0, VOCAB - 1, (batch, seq), generator=gen)
+    mask = torch.zeros(batch, seq, dtype=torch.long)
+    labels = torch.full((batch, seq), -100, dtype=torch.long)
+    for row, n in enumerate(lengths):
+        span = slice(seq - n, seq) if left else slice(0, n)
+        mask[row, span] = 1
+        target = ids[row, span].clone()
+        if not every_position:
+            target[:prompt] = -100
+        if labelled_rows is not None and row not in labelled_rows:
+            target[:] = -100
+        labels[row, span] = target
+    if hole:
+        mask[0, 4] = 0
+        labels[0, 4] = -100
+    ids[mask == 0] = VOCAB - 1
+    return ids.cuda(), mask.cuda(), labels.cuda()
+
+
+CASES = {
+    "a row without labels": ([26, 11, 19, 22], {"labelled_rows": {0, 1, 3}}),
+    "no padding": ([21, 21, 21, 21], {}),
+    "a one-token row": ([26, 1, 19, 6], {}),
+    "full-window rows": ([512, 512, 512, 512], {"prompt": 497}),
+    "full and short rows": ([512, 3, 512, 8], {"prompt": 2}),
+    "no label in the batch": ([26, 11, 19, 22], {"labelled_rows": set()}),
+    "every position labelled": ([26, 11, 19, 22], {"every_position": True}),
+    "a single row": ([39], {}),
+    "a single one-token row": ([1], {"every_position": True}),
+    "odd token counts": ([17, 3, 29, 1], {"prompt": 2}),
+    "left padding": ([26, 11, 19, 22], {"left": True}),
+    "a hole in the mask": ([26, 11, 19, 22], {"hole": True}),
+}
+NOT_RIGHT_PADDED = ("left padding", "a hole in the mask")
+
+
+def _step(model, ids, mask, labels, num_items):
+    """One forward and backward under fp16 autocast: the loss, the LoRA gradients (and the
+    model's own outputs)."""
+    for p in qlora_model.lora_parameters(model):
+        p.grad = None
+    with torch.autocast("cuda", dtype=torch.float16):
+        out = model(input_ids=ids, attention_mask=mask, labels=labels,
+                    num_items_in_batch=num_items)
+    out.loss.backward()
+    grads = [p.grad.detach().clone() if p.grad is not None else torch.zeros_like(p)
+             for p in qlora_model.lora_parameters(model)]
+    return out, grads
+
+
+def _per_token(logits, labels):
+    """The per-token values the trainer reads, from full logits: loss, entropy, correct count."""
+    batch, seq = labels.shape
+    shift = F.pad(labels, (0, 1), value=-100)[:, 1:]
+    z = logits.float()
+    loss = F.cross_entropy(z.reshape(-1, z.shape[-1]), shift.reshape(-1), ignore_index=-100,
+                           reduction="none").view(batch, seq)
+    entropy = torch.logsumexp(z, -1) - (torch.softmax(z, -1) * z).sum(-1)
+    correct = ((logits.argmax(-1) == shift) & (shift >= 0)).sum()
+    return loss, entropy, int(correct), int((shift >= 0).sum())
+
+
+@pytest.mark.parametrize("packing", ["dynamic", "fixed"])
+@pytest.mark.parametrize("case", list(CASES))
+def test_patched_forward_matches_unpatched_on_edge_batches(monkeypatch, case, packing):
+    print(f"[case] edge batch {case!r} packing={packing}", flush=True)
+    if packing == "fixed" and case in NOT_RIGHT_PADDED:
+        pytest.skip("the fixed-shape packing serves right-padded batches only (the step graph "
+                    "captures those; others take the dynamic path)")
+    lengths, options = CASES[case]
+    ids, mask, labels = _batch(lengths, **options)
+    num_items = (labels[:, 1:] != -100).sum()
+    model = _model()
+
+    patches.unapply()
+    ref, ref_grads = _step(model, ids, mask, labels, num_items)
+    ref_loss, ref_entropy, ref_correct, n_labelled = _per_token(ref.logits.detach(), labels)
+
+    monkeypatch.setenv("SOLUTION_DISABLE_GEMM_TABLE", "1")
+    monkeypatch.setitem(patches._unpad, "enabled", True)
+    monkeypatch.setitem(patches._unpad, "checked", 0)
+    patches.apply()
+    engaged.reset()
+    try:
+        if packing == "fixed":
+            n_rows = (sum(lengths) + 63) // 64 * 64 + 64  # room for a pad sequence
+            with unpad.static_tokens(n_rows):
+                out, grads = _step(model, ids, mask, labels, num_items)
+        else:
+            out, grads = _step(model, ids, mask, labels, num_items)
+        step = patches.LAST_STEP[-1]
+    finally:
+        patches.unapply()
+
+    assert out.logits is None, "the fused head keeps no logits"
+    assert engaged.RAN["fused_head"] == 1
+    right_padded = case not in NOT_RIGHT_PADDED
+    assert patches._unpad["enabled"] is right_padded, "padding removal on a mask it cannot pack"
+    assert (engaged.RAN["unpad"] == 1) is right_padded
+    assert int(step.labelled) == n_labelled
+    if n_labelled == 0:
+        assert torch.isnan(out.loss) and torch.isnan(ref.loss)
+    else:
+        torch.testing.assert_close(out.loss.float(), ref.loss.float(), rtol=2e-2, atol=1e-3)
+    unlabelled = F.pad(labels, (0, 1), value=-100)[:, 1:] < 0
+    torch.testing.assert_close(step.token_loss.float(), ref_loss, rtol=3e-2, atol=2e-2)
+    assert (step.token_loss[unlabelled] == 0).all()
+    real = mask.bool()
+    torch.testing.assert_close(step.token_entropy.float()[real], ref_entropy[real], rtol=3e-2,
+                               atol=2e-2)
+    assert abs(int(step.correct) - ref_correct) <= max(1, n_labelled // 50)
+    for got, want in zip(grads, ref_grads):
+        assert torch.isfinite(got).all(), "non-finite LoRA gradient"
+        if n_labelled == 0:
+            assert (got == 0).all() and (want == 0).all()
+        else:
+            scale = float(want.abs().max())
+            torch.testing.assert_close(got, want, rtol=3e-2, atol=3e-2 * scale + 1e-7)

@@ -1,0 +1,99 @@
+"""The opt-in MLP node that keeps `up` and its input and recomputes `gate` in the backward
+(`mlp_save_up.SwiGLUSaveUp`, SOLUTION_MLP_SAVE_UP=1; the reference's solution/mlp_save_up.py:
+51-140) against the MLP path it replaces: the per-projection MLP with the in-place SwiGLU
+backward.
+
+- Same model, same batch, one patched forward and backward each: the forward computes the same
+  products and the same activation kernel, so the losses agree to fp16 rounding. The LoRA
+  gradients, which flow through the MLP's input gradient dx = dgate W_gate + dup W_up, agree
+  within fp16 tolerances.
+- The node runs on every decoder layer, and nothing falls back.
+- Over six training steps, the save-up path's loss curve stays within 0.5% of the eager
+  (unpatched) path's.
+"""
+
+import pytest
+import torch
+
+from talm_amd import engaged, fused_mlp, patches, qlora_model, state
+
+pytestmark = pytest.mark.gpu
+
+LAYERS = 3
+
+
+def _config():
+    return qlora_model.qwen2_config(vocab_size=1000, hidden_size=512, intermediate_size=1024,
+                                    num_hidden_layers=LAYERS, num_attention_heads=4,
+                                    num_key_value_heads=2, head_dim=128)
+
+
+def _model(seed=3):
+    model = qlora_model.build_model(_config(), seed=seed)
+    with torch.no_grad():
+        gen = torch.Generator(device="cuda").manual_seed(9)
+        for p in qlora_model.lora_parameters(model):
+            if p.abs().sum() == 0:
+                p.copy_(0.02 * torch.randn(p.shape, generator=gen, device="cuda"))
+    return model
+
+
+def _forward_backward(model, batch):
+    for p in qlora_model.lora_parameters(model):
+        p.grad = None
+    ids, mask, labels = batch["input_ids"], batch["attention_mask"], batch["labels"]
+    with torch.autocast("cuda", dtype=torch.float16):
+        out = model(input_ids=ids, attention_mask=mask, labels=labels)
+    out.loss.backward()
+    return float(out.loss), [p.grad.detach().clone() for p in qlora_model.lora_parameters(model)]
+
+
+def test_save_up_node_matches_the_in_place_mlp(monkeypatch):
+    print("[case] save-up MLP node vs in-place SwiGLU MLP, small model", flush=True)
+    monkeypatch.setenv("SOLUTION_MLP_SAVE_UP", "1")
+    monkeypatch.setattr(fused_mlp, "ENABLED", False)  # the replaced path: per-projection MLP
+    model = _model()
+    batch = qlora_model.make_batch(seed=5, step=0, vocab=1000, seq=256, lo=64, hi=256)
+    patches.apply()
+    try:
+        engaged.reset()
+        save_loss, save_grads = _forward_backward(model, batch)
+        assert engaged.RAN["mlp_save_up"] == LAYERS and engaged.FELL_BACK["mlp_save_up"] == 0
+        monkeypatch.setitem(state.DISABLED, "mlp_save_up", "switched off by the test")
+        engaged.reset()
+        ref_loss, ref_grads = _forward_backward(model, batch)
+        assert engaged.RAN["mlp_save_up"] == 0 and engaged.RAN["swiglu_inplace"] == LAYERS
+    finally:
+        patches.unapply()
+    assert abs(save_loss - ref_loss) <= 1e-4 * abs(ref_loss), (save_loss, ref_loss)
+    for got, want in zip(save_grads, ref_grads):
+        assert torch.isfinite(got).all()
+        scale = float(want.abs().max())
+        torch.testing.assert_close(got, want, rtol=2e-2, atol=2e-2 * scale + 1e-8)
+
+
+def test_save_up_step_matches_eager_loss_curve(monkeypatch):
+    print("[case] save-up MLP training steps vs eager, small model", flush=True)
+
+    def run(patched):
+        model = _model()
+        trainer = qlora_model.Trainer(model, steps=6, fused_adapters=patched)
+        batches = [qlora_model.make_batch(seed=5, step=s, vocab=1000, seq=256, lo=64, hi=256)
+                   for s in range(6)]
+        if patched:
+            patches.apply()
+        try:
+            return [float(trainer.step(batches[s], batches[s + 1] if s + 1 < 6 else None))
+                    for s in range(6)]
+        finally:
+            if patched:
+                patches.unapply()
+
+    eager = run(False)
+    monkeypatch.setenv("SOLUTION_MLP_SAVE_UP", "1")
+    engaged.reset()
+    saved = run(True)
+    assert engaged.RAN["mlp_save_up"] > 0 and engaged.FELL_BACK["mlp_save_up"] == 0
+    assert abs(saved[0] - eager[0]) <= 1e-3 * abs(eager[0]), (saved[0], eager[0])
+    for a, b in zip(saved, eager):
+        assert abs(a - b) <= 5e-3 * abs(b), (saved, eager)
