@@ -47,8 +47,10 @@ MEASURED_TRAFFIC = {
     "add_rmsnorm_bwd": 18.1e6,
     "rope_inplace": 10.1e6,
     "swiglu_fwd": 110.1e6,
-    "swiglu_bwd": 183.6e6,
-    "head_ce_fwd_bwd": 4546e6,
+    "swiglu_bwd": 183.5e6,
+    "attn_fwd": 14.2e6,
+    "attn_bwd": 66.4e6,  # its three dispatches: dot, the dQ / dK / dV kernel, the reduction
+    "head_ce_fwd_bwd": 4571e6,
 }
 
 
