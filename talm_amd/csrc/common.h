@@ -17,6 +17,8 @@ int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)))
 int ok();
 // TALM_OK, or TALM_EHIP with the launch error of the last kernel enqueued on this thread.
 int check_launch(const char* what);
+// Compute units of the current device (queried once per device).
+int device_cus();
 
 constexpr int kWave = 64;
 

@@ -41,25 +41,21 @@ namespace {
 constexpr int kThreads = 256;        // block size of the merge, combine and transpose kernels
 constexpr int kTile = 128;           // statistics granule (columns)
 
-// GEMM tile shapes of the head: 256 x BN, every wavefront 128 x 64, two wavefronts per SIMD.
-// Narrow runs two 256-thread workgroups per CU; Wide one 512-thread workgroup that moves a third
-// fewer bytes per FLOP. The logits epilogue stages the fp16 tile in LDS ([256][BN + 8] halfs).
-template <int BN, int BK, int STAGES>
-struct HeadShape : TileShape<256, BN, BK, STAGES, 2, BN / 64> {
-  static constexpr int kZS = BN + 8;
-  static constexpr int kRingBytes = TileShape<256, BN, BK, STAGES, 2, BN / 64>::kRing;
-  static constexpr int kLds = kRingBytes > 256 * kZS * 2 ? kRingBytes : 256 * kZS * 2;
-  static_assert(kLds <= 160 * 1024, "LDS per CU");
-};
-using Narrow = HeadShape<128, 32, 3>;  // 72 KiB ring
-using Wide = HeadShape<256, 64, 2>;    // 128 KiB ring, 135 KiB with the staged logits tile
-// head_grad runs the same tiles with wavefronts of 64 x 128: half as many A fragments per
-// wavefront, each of which it scales between LDS and the MFMAs.
+// head_logits: 256 vocabulary rows (A = W) x 256 token rows (B = H) per tile, 64-deep steps
+// through a two-slot ring, eight wavefronts of 128 vocabulary rows x 64 tokens. In the
+// accumulator layout of v_mfma_f32_32x32x16_f16 a lane holds one column (a token) and 16 rows
+// (vocabulary entries) of each 32 x 32 block, so a wavefront's 128 rows, one statistics tile,
+// are 64 values in lane l and 64 in lane l ^ 32 for each of its tokens: the per-token statistics
+// need no LDS staging and one cross-lane exchange.
+using LogitsShape = TileShape<256, 256, 64, 2, 2, 4>;
+static_assert(LogitsShape::kWaveM == 128 && LogitsShape::kFragM == 4,
+              "one statistics tile of 4 x 32 rows per wavefront");
+// head_grad: 256 (labelled rows) x BN (hidden) tiles, wavefronts of 64 x 128 (two A fragments,
+// each scaled between LDS and the MFMAs). Narrow runs two 256-thread workgroups per CU with a
+// three-stage ring of 32-deep steps; Wide one 512-thread workgroup that moves a third fewer bytes
+// per FLOP.
 using GradNarrow = TileShape<256, 128, 32, 3, 4, 1>;
 using GradWide = TileShape<256, 256, 64, 2, 4, 2>;
-static_assert(GradNarrow::kThreads == Narrow::kThreads && GradWide::kThreads == Wide::kThreads &&
-              GradNarrow::kPerCu == Narrow::kPerCu && GradWide::kPerCu == Wide::kPerCu,
-              "head_grad shapes launch like the logits shapes");
 constexpr int kBM = 256;
 
 struct Stat {
@@ -95,119 +91,313 @@ __device__ __forceinline__ Stat shfl_stat(Stat v, int off) {
   return r;
 }
 
+// The value of lane l ^ 32. v_permlane32_swap exchanges the upper 32 lanes of its first operand
+// with the lower 32 lanes of its second: with a register as both, lanes >= 32 find their
+// partner's value in the first result, lanes < 32 in the second.
+__device__ __forceinline__ uint32_t other_half(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ float other_half(float v) {
+  return __builtin_bit_cast(float, other_half(__builtin_bit_cast(uint32_t, v)));
+}
+__device__ __forceinline__ int other_half(int v) {
+  return static_cast<int>(other_half(static_cast<uint32_t>(v)));
+}
+
 // ------------------------------------------------------------------------------------------
 // GEMM1: z[r][j] = fp16(sum_k H[r][k] W[j][k]) for the group's columns j < group_cols (W starts
-// at the group's first vocabulary row) and the per-(row, 128-column tile) partial statistics;
-// rows r < n_p (the labelled rows when the gradient is wanted) store P[r][j] = fp16(e^{z - m_t})
-// with m_t the max of the row's 128-column tile, 0 past group_cols.
+// at the group's first vocabulary row) and the per-(row, 128-column tile) partial statistics
+// (max m_t, first argmax, sum e^{z - m_t}, sum e^{z - m_t} z, and the logit at the target when
+// the tile holds it); rows r < n_p (the labelled rows when the gradient is wanted) store
+// P[r][j] = fp16(e^{z - m_t}), 0 past group_cols.
+//
+// Persistent: one workgroup per CU walks its tiles (each XCD one contiguous range, token tiles
+// fastest, so the tiles in flight on an XCD share weight rows in its L2). When a tile's last ring
+// step is read, the next tile's first step is issued into the ring and lands while the epilogue
+// of the finished tile runs from registers.
 // ------------------------------------------------------------------------------------------
-template <class S>
-__global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_logits_kernel(
-    const uint16_t* __restrict__ H, int64_t ldh, const uint16_t* __restrict__ W, int64_t ldw,
-    int n_rows, int K, int group_cols, int first_col, uint16_t* __restrict__ Z, int64_t ldz,
-    float4* __restrict__ part, int parts_per_row, int n_mtiles, int n_ntiles,
-    const int64_t* __restrict__ targets, float* __restrict__ ztarget, int n_p) {
-  constexpr int kBN = S::kBN, kZS = S::kZS;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kLds];
+struct LogitsArgs {
+  const uint16_t* H;
+  int64_t ldh;
+  const uint16_t* W;  // the group's first vocabulary row
+  int64_t ldw;
+  int n_rows, K, group_cols, first_col;
+  uint16_t* Z;
+  int64_t ldz;
+  float4* part;
+  int parts_per_row;
+  const int64_t* targets;
+  float* ztarget;
+  int n_p;
+  int n_ttiles, n_tiles;
+};
 
-  // row tiles vary fastest inside an XCD's range: the tiles in flight on one XCD share weight rows
-  const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(n_mtiles * n_ntiles));
-  const int ntile = static_cast<int>(tile / n_mtiles);
-  const int mtile = static_cast<int>(tile % n_mtiles);
-  const int m0 = mtile * kBM, n0 = ntile * kBN;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Row of the statistics tile held in z[k] of a lane in half h (lane >> 5): i * 32 + 8 q + 4 h + w
+// for k = i * 16 + 4 q + w (the accumulator layout of block i).
+__device__ __forceinline__ int stat_row(int k, int h) {
+  return (k >> 4) * 32 + 8 * ((k >> 2) & 3) + 4 * h + (k & 3);
+}
+
+__device__ __forceinline__ void put_part(const LogitsArgs& a, int tok, int c0, float m, float s,
+                                         float t, int idx) {
+  a.part[static_cast<int64_t>(tok) * a.parts_per_row + (c0 >> 7)] =
+      make_float4(m, s, t, __int_as_float(a.first_col + c0 + idx));
+}
+
+// Whether this lane holds the target's row of the statistics tile (rarely: one tile per row), and
+// the target's index k in z; `valid` counts the group's columns from the tile's first on.
+__device__ __forceinline__ bool target_here(int64_t target, int valid, int tok, int c0, int h,
+                                            const LogitsArgs& a, int& k) {
+  const int64_t rel = target - (a.first_col + c0);
+  const int r = static_cast<int>(rel & 127);
+  k = ((r >> 5) << 4) | (((r >> 3) & 3) << 2) | (r & 3);
+  return tok < a.n_rows && rel >= 0 && rel < min(valid, 128) && ((rel >> 2) & 1) == h;
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// Statistics and P of one (token, statistics tile) from this lane's 64 rounded logits, packed in
+// pairs: zp[k / 2] holds rows stat_row(k, h) and stat_row(k + 1, h) (k even), and the 64 of lane
+// l ^ 32. When a lane of the wavefront holds its token's target row, the pairs also go to the
+// lanes' 128-byte LDS rows `zs`, from which that lane reads the target's logit. Rows at or past
+// `valid` (the tile holding the group's end) are not vocabulary: their logits are -65504 (see
+// the kernel), which gives e = 0 and P = 0 and takes no part in the maximum or the argmax.
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {  // v_cvt_pk_f16_f32
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){lo, hi}, half2_t));
+}
+
+__device__ __forceinline__ void tile_stats(const uint32_t (&zp)[32], float mx, uint16_t* zs,
+                                           int lane, int tok, int64_t target, int c0, int valid,
+                                           const LogitsArgs& a) {
+  const int h = lane >> 5;
+  int kt;
+  const bool hit = target_here(target, valid, tok, c0, h, a, kt);
+  if (__builtin_amdgcn_ballot_w64(hit)) {
+#pragma unroll
+    for (int k = 0; k < 32; k += 4)
+      *reinterpret_cast<uint4*>(zs + 2 * k) = make_uint4(zp[k], zp[k + 1], zp[k + 2], zp[k + 3]);
+  }
+  auto zh = [&](int k) {  // row stat_row(k, h) as fp16
+    return __builtin_bit_cast(half2_t, zp[k >> 1])[k & 1];
+  };
+  // maximum of the rounded logits (`mx`: of this lane's)
+  const float m = fmaxf(mx, other_half(mx));
+  const _Float16 m16 = static_cast<_Float16>(m);  // exact
+  // first argmax: the smallest row whose logit equals the maximum (-0 and +0 compare equal)
+  int idx = 1 << 30;
+#pragma unroll
+  for (int k = 63; k >= 0; --k) {
+    // the row (without 4 h, added once below) through a scalar register set right here: as
+    // plain constants, the 64 rows would be hoisted into vector registers across the tile loop
+    int row;
+    asm volatile("s_mov_b32 %0, %1" : "=s"(row) : "i"(stat_row(k, 0)));
+    if (zh(k) >= m16) idx = row;
+  }
+  idx += 4 * h;
+  idx = min(idx, other_half(idx));
+  // e = e^{z - m} = 2^u with u = z log2(e) - m log2(e), the sums s = sum e and
+  // t = sum e z = m s + (sum e u) / log2(e), and P, block by block: after exchanging half of the
+  // fp16 pairs with lane l ^ 32, a lane holds the 8 consecutive rows i * 32 + 8 (q + h) for
+  // q = 0, 2, one 16-byte store each
+  const float nm = -m * kLog2e;
+  float s = 0.f, tu = 0.f;
+  const bool store_p = tok < a.n_p;
+  uint16_t* zrow = a.Z + static_cast<int64_t>(tok) * a.ldz + c0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t pk[8];
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      float e2[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float arg = fmaf(static_cast<float>(zh(i * 16 + v + u)), kLog2e, nm);
+        const float e = __builtin_amdgcn_exp2f(arg);
+        s += e;
+        tu = fmaf(e, arg, tu);
+        e2[u] = e;
+      }
+      pk[v >> 1] = pack_h2(e2[0], e2[1]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q += 2) {
+      uint32_t x[2] = {pk[2 * q], pk[2 * q + 1]};
+      uint32_t y[2] = {pk[2 * q + 2], pk[2 * q + 3]};
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        // lanes < 32 receive the other half's x in y, lanes >= 32 the other half's y in x
+        const auto r = __builtin_amdgcn_permlane32_swap(x[u], y[u], false, false);
+        x[u] = r[0];
+        y[u] = r[1];
+      }
+      if (store_p)
+        *reinterpret_cast<uint4*>(zrow + i * 32 + 8 * (q + h)) = make_uint4(x[0], x[1], y[0], y[1]);
+    }
+  }
+  s += other_half(s);
+  tu += other_half(tu);
+  const float t = fmaf(tu, 1.f / kLog2e, m * s);
+  if (tok < a.n_rows && h == 0) put_part(a, tok, c0, m, s, t, idx);
+  if (hit) a.ztarget[tok] = h2f(zs[kt]);
+}
+
+// One ring step of the logits kernel: for each 16-deep slice ks, the wavefront's 4 A and 2 B
+// fragments and their 8 MFMAs. With 128-byte rows (8 chunks), the swizzled chunk of slice ks is
+// the slice-0 chunk with bits 1-2 XOR-ed by ks, so every fragment's address is its slice-0 byte
+// offset `fo` XOR 32 ks. The XOR goes through an opaque scalar: otherwise the compiler keeps all
+// 24 addresses of the step (and those of the other slot) in registers across the tile loop.
+template <class S>
+__device__ __forceinline__ void logits_step(const unsigned char* st, const uint32_t (&fo)[6],
+                                            Acc<S>& acc) {
+  static_assert(S::kCpr == 8 && S::kFragM == 4 && S::kFragN == 2, "the logits tile shape");
+#pragma unroll
+  for (int ks = 0; ks < S::kBK / 16; ++ks) {
+    uint32_t x;
+    asm volatile("s_mov_b32 %0, %1" : "=s"(x) : "i"(32 * ks));
+    half8_t f[6];
+#pragma unroll
+    for (int q = 0; q < 6; ++q) f[q] = *reinterpret_cast<const half8_t*>(st + (fo[q] ^ x));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
+  }
+}
+
+template <class S>
+__global__ __launch_bounds__(S::kThreads, 1) void head_logits_kernel(LogitsArgs a) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing];
+  constexpr int kSt = S::kStages;
+  static_assert(kSt == 2, "the first step of each tile waits for every outstanding operation");
+  static_assert(S::kStageBytes >= S::kThreads * 128, "a 128-byte LDS row per lane in slot 1");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 
-  Loader<S, kBM> la;
-  Loader<S, kBN> lb;
-  la.init(H + static_cast<int64_t>(m0) * ldh, ldh, n_rows - m0, K, wave, lane);
-  lb.init(W + static_cast<int64_t>(n0) * ldw, ldw, group_cols - n0, K, wave, lane);
-  Acc<S> acc;
-  ring_gemm<S>(
-      smem, (K + S::kBK - 1) / S::kBK,
-      [&](unsigned char* slot, int kt) {
-        la.issue(slot, kt * S::kBK, wave);
-        lb.issue(slot + S::kAChunks * 16, kt * S::kBK, wave);
-      },
-      acc, lane, wave);
-
-  // Epilogue 1: fp16 logits tile into LDS ([kBM][kZS] halfs).
-  uint16_t* Zs = reinterpret_cast<uint16_t*>(smem);
-#pragma unroll
-  for (int i = 0; i < S::kFragM; ++i)
-#pragma unroll
-    for (int j = 0; j < S::kFragN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int col = wn * 64 + j * 32 + (lane & 31);
-        Zs[row * kZS + col] = f2h(acc[i][j][v]);
-      }
-  __syncthreads();
-
-  // Epilogue 2: partial statistics of one (row, 128-column statistics tile) per thread, which
-  // then replaces its z with P in LDS (stored for rows < n_p).
-  {
-    const int row = tid % kBM, st = tid / kBM, gr = m0 + row;
-    const int c0 = n0 + st * kTile;  // the statistics tile's first column in the group
-    const int valid = min(kTile, group_cols - c0);
-    if (gr < n_rows && valid > 0) {
-      uint16_t* zr = Zs + row * kZS + st * kTile;
-      uint4 zv[kTile / 8];
-#pragma unroll
-      for (int c = 0; c < kTile / 8; ++c) zv[c] = *reinterpret_cast<const uint4*>(zr + 8 * c);
-      float m = -INFINITY;
-      int idx = 0;
-#pragma unroll
-      for (int c = 0; c < kTile / 8; ++c) {
-        const uint32_t w4[4] = {zv[c].x, zv[c].y, zv[c].z, zv[c].w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int col = 8 * c + e;
-          const float z = (e & 1) ? hi_f(w4[e >> 1]) : lo_f(w4[e >> 1]);
-          if (col < valid && z > m) {
-            m = z;
-            idx = col;
-          }
-        }
-      }
-      // the logit at the target, when the target column is in this tile (one tile per row)
-      const int64_t rel = targets[gr] - (first_col + c0);
-      if (rel >= 0 && rel < valid) ztarget[gr] = h2f(zr[static_cast<int>(rel)]);
-      float sum = 0.f, t = 0.f;
-#pragma unroll
-      for (int c = 0; c < kTile / 8; ++c) {
-        const uint32_t w4[4] = {zv[c].x, zv[c].y, zv[c].z, zv[c].w};
-        float ez[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int col = 8 * c + e;
-          const float z = (e & 1) ? hi_f(w4[e >> 1]) : lo_f(w4[e >> 1]);
-          // columns past the group are z = 0 (zero weight rows) and get e^{-inf} = 0: no branch
-          ez[e] = __expf(col < valid ? z - m : -INFINITY);
-          sum += ez[e];
-          t += ez[e] * z;
-        }
-        *reinterpret_cast<uint4*>(zr + 8 * c) = make_uint4(
-              pack2(ez[0], ez[1]), pack2(ez[2], ez[3]), pack2(ez[4], ez[5]), pack2(ez[6], ez[7]));
-      }
-      part[static_cast<int64_t>(gr) * parts_per_row + c0 / kTile] =
-          make_float4(m, sum, t, __int_as_float(first_col + c0 + idx));
-    }
+  // this workgroup's tiles: first, first + stride, ... below end
+  const uint32_t nwg = gridDim.x, n_tiles = static_cast<uint32_t>(a.n_tiles);
+  uint32_t first = blockIdx.x, stride = nwg, end = n_tiles;
+  if (nwg % kXcds == 0) {  // workgroup b runs on XCD b % 8: give each XCD a contiguous range
+    const uint32_t x = blockIdx.x % kXcds, q = n_tiles / kXcds, r = n_tiles % kXcds;
+    const uint32_t start = x * q + min(x, r);
+    first = start + blockIdx.x / kXcds;
+    stride = nwg / kXcds;
+    end = start + q + (x < r ? 1u : 0u);
   }
-  if (n_p <= m0) return;
-  __syncthreads();
+  const int nk = (a.K + S::kBK - 1) / S::kBK;
 
-  // Epilogue 3: the P rows of the tile to global memory in 16-byte chunks (kBN / 8 per row); the
-  // chunk that holds the group's last column carries the zeros past it (head_grad reads chunks).
+  // slice-0 byte offsets of the wavefront's fragments in a stage: A (weight rows) then B (tokens)
+  uint32_t fo[6];
 #pragma unroll
-  for (int it = 0; it < (kBM * kBN / 8) / S::kThreads; ++it) {
-    const int c = it * S::kThreads + tid, row = c / (kBN / 8), kc = c % (kBN / 8);
-    const int gr = m0 + row, gc = n0 + kc * 8;
-    if (gr < n_p && gc < group_cols)
-      *reinterpret_cast<uint4*>(Z + static_cast<int64_t>(gr) * ldz + gc) =
-          *reinterpret_cast<const uint4*>(Zs + row * kZS + kc * 8);
+  for (int i = 0; i < 4; ++i)
+    fo[i] = 16u * swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    fo[4 + j] = S::kAChunks * 16u + 16u * swz<S::kCpr>(wn * S::kWaveN + j * 32 + (lane & 31), lane >> 5);
+
+  Loader<S, S::kBM> la;
+  Loader<S, S::kBN> lb;
+  la.lanes(a.ldw, a.K, wave, lane);
+  lb.lanes(a.ldh, a.K, wave, lane);
+  auto start_tile = [&](uint32_t tile) {
+    const int tt = static_cast<int>(tile % a.n_ttiles), vt = static_cast<int>(tile / a.n_ttiles);
+    la.rows(a.W + static_cast<int64_t>(vt) * S::kBM * a.ldw, a.ldw, min(a.group_cols - vt * S::kBM, S::kBM));
+    lb.rows(a.H + static_cast<int64_t>(tt) * S::kBN * a.ldh, a.ldh, min(a.n_rows - tt * S::kBN, S::kBN));
+    if (nk > 0) {
+      // step 0 through an opaque zero: the addresses are tile-invariant, and hoisting them out of
+      // the tile loop would hold eight more registers across it
+      int k0;
+      asm volatile("s_mov_b32 %0, 0" : "=s"(k0));
+      la.issue(smem, k0, wave);
+      lb.issue(smem + S::kAChunks * 16, k0, wave);
+    }
+  };
+  if (first >= end) return;
+  start_tile(first);
+  for (uint32_t tile = first;;) {
+    const int tt = static_cast<int>(tile % a.n_ttiles), vt = static_cast<int>(tile / a.n_ttiles);
+    const int c0 = vt * S::kBM + wm * S::kWaveM;  // the wavefront's first column in the group
+    const int valid = a.group_cols - c0;         // of its rows, those that are vocabulary
+    // Accumulators start at 0, or at -65504 (fp16's lowest finite value) for rows past the group's
+    // end: their weight rows read as zeros, so their logits stay -65504 exactly, and e^{z - m}
+    // is 0 for them whenever a vocabulary logit of the tile exceeds -65400 (a tile whose logits
+    // all round to -65504 or below has overflowed fp16 anyway). Row i * 32 + 8 q + 4 h + w is past
+    // the end when (valid - 1 - 4 h) - (i * 32 + 8 q + w) < 0: its sign bit selects the value
+    // without a mask register per row.
+    Acc<S> acc;
+#pragma unroll
+    for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < S::kFragN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    if (valid < S::kWaveM) {  // uniform, rare
+      asm volatile("");  // keeps the branch (no selects on every tile)
+      const int lim = valid - 1 - 4 * (lane >> 5);
+      constexpr int kLowest = static_cast<int>(0xc77fe000u);  // -65504.f
+#pragma unroll
+      for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+        for (int j = 0; j < S::kFragN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            acc[i][j][v] =
+                __int_as_float(((lim - (i * 32 + 8 * (v >> 2) + (v & 3))) >> 31) & kLowest);
+    }
+    for (int kb = 0; kb < nk; kb += kSt) {
+#pragma unroll
+      for (int i = 0; i < kSt; ++i) {  // step kt = kb + i in slot i
+        const int kt = kb + i;
+        if (kt >= nk) break;
+        wait_vmcnt<0>();  // this step's group (and, at step 0, the previous epilogue's stores)
+        lds_barrier();
+        if (kt + 1 < nk) {
+          unsigned char* slot = smem + ((i + 1) % kSt) * S::kStageBytes;
+          la.issue(slot, (kt + 1) * S::kBK, wave);
+          lb.issue(slot + S::kAChunks * 16, (kt + 1) * S::kBK, wave);
+        }
+        logits_step<S>(smem + i * S::kStageBytes, fo, acc);
+      }
+    }
+    // every wavefront has read the last step: slot 0 takes the next tile's first step, slot 1
+    // serves the epilogue's rare paths (a 128-byte row per lane)
+    lds_barrier();
+    const uint32_t next = tile + stride;
+    if (next < end) start_tile(next);
+
+    // epilogue from registers: the wavefront's statistics tile and two 32-token columns, rounded
+    // to fp16 first (the logits the reference sees; half the registers of the sums)
+    uint32_t zp[S::kFragN][32];
+    float mx[S::kFragN];
+#pragma unroll
+    for (int j = 0; j < S::kFragN; ++j) {
+      half2_t m2;
+#pragma unroll
+      for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const half2_t z2 = __builtin_convertvector((float2_t){acc[i][j][v], acc[i][j][v + 1]}, half2_t);
+          m2 = i == 0 && v == 0 ? z2 : __builtin_elementwise_max(m2, z2);
+          zp[j][i * 8 + v / 2] = __builtin_bit_cast(uint32_t, z2);
+        }
+      mx[j] = fmaxf(static_cast<float>(m2[0]), static_cast<float>(m2[1]));
+    }
+    uint16_t* zs = reinterpret_cast<uint16_t*>(smem + S::kStageBytes) + tid * 64;
+    if (valid > 0) {
+#pragma unroll
+      for (int j = 0; j < S::kFragN; ++j) {
+        const int tok = tt * S::kBN + wn * S::kWaveN + j * 32 + (lane & 31);
+        const int64_t target = tok < a.n_rows ? a.targets[tok] : -1;
+        tile_stats(zp[j], mx[j], zs, lane, tok, target, c0, valid, a);
+      }
+    }
+    if (next >= end) break;
+    tile = next;
   }
 }
 
@@ -523,15 +713,9 @@ double fill(int64_t blocks, int per_cu) {
   return rounds ? static_cast<double>(blocks) / static_cast<double>(rounds * slots) : 0.0;
 }
 
-// The Wide shape moves a third fewer bytes per FLOP (~20% faster per tile); pick it unless the
-// launch fills the chip clearly worse with it.
+// GradWide moves a third fewer bytes per FLOP (~20% faster per tile); pick it unless the launch
+// fills the chip clearly worse with it.
 constexpr double kWideGain = 1.2;
-
-bool logits_wide(int64_t n_rows, int64_t gcols) {
-  const int64_t mt = (n_rows + kBM - 1) / kBM;
-  return kWideGain * fill(mt * ((gcols + Wide::kBN - 1) / Wide::kBN), Wide::kPerCu) >=
-         fill(mt * ((gcols + Narrow::kBN - 1) / Narrow::kBN), Narrow::kPerCu);
-}
 
 // The gradient GEMM's output [n_grad, hidden] per slice is small: besides the shape, each slice's
 // columns may be split into `ksplit` parts (each its own fp32 partial, summed by head_combine) so
@@ -546,11 +730,11 @@ GradPlan plan_grad(int64_t n_grad, int64_t hidden, int ns) {
   GradPlan best{true, 1};
   double best_score = -1.0;
   for (int wide = 1; wide >= 0; --wide) {
-    const int bn = wide ? Wide::kBN : Narrow::kBN;
+    const int bn = wide ? GradWide::kBN : GradNarrow::kBN;
     for (int ks = 1; ks <= 4; ++ks) {
       const int64_t blocks = mt * ((hidden + bn - 1) / bn) * ns * ks;
       const double score = (wide ? kWideGain : 1.0) * (1.0 - 0.03 * (ks - 1)) *
-                           fill(blocks, wide ? Wide::kPerCu : Narrow::kPerCu);
+                           fill(blocks, wide ? GradWide::kPerCu : GradNarrow::kPerCu);
       if (score > best_score + 1e-9) {
         best_score = score;
         best = GradPlan{wide != 0, ks};
@@ -675,28 +859,24 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
   float* accbuf = reinterpret_cast<float*>(ws + l.acc);
   const hipStream_t s = as_stream(stream);
   const int rows = static_cast<int>(n_rows);
-  const int mt = (rows + kBM - 1) / kBM;
   const int n_p = grad_hidden ? static_cast<int>(n_grad) : 0;  // rows whose P is stored
 
   for (int64_t s0 = 0; s0 < slices; s0 += g) {
     const int ns = static_cast<int>(slices - s0 < g ? slices - s0 : g);
     const int64_t col0 = s0 * vchunk;
     const int64_t gcols = (s0 + ns == slices) ? vocab - col0 : ns * vchunk;
-    if (logits_wide(rows, gcols)) {
-      const int nt = static_cast<int>((gcols + Wide::kBN - 1) / Wide::kBN);
-      hipLaunchKernelGGL((head_logits_kernel<Wide>), dim3(static_cast<unsigned>(mt * nt)),
-                         dim3(Wide::kThreads), 0, s, hidden_states, ldh, weight + col0 * ldw, ldw,
-                         rows, static_cast<int>(hidden), static_cast<int>(gcols),
-                         static_cast<int>(col0), Z, l.ldz, part, l.parts_per_row, mt, nt, targets,
-                         ztarget, n_p);
-    } else {
-      const int nt = static_cast<int>((gcols + Narrow::kBN - 1) / Narrow::kBN);
-      hipLaunchKernelGGL((head_logits_kernel<Narrow>), dim3(static_cast<unsigned>(mt * nt)),
-                         dim3(Narrow::kThreads), 0, s, hidden_states, ldh, weight + col0 * ldw,
-                         ldw, rows, static_cast<int>(hidden), static_cast<int>(gcols),
-                         static_cast<int>(col0), Z, l.ldz, part, l.parts_per_row, mt, nt, targets,
-                         ztarget, n_p);
-    }
+    LogitsArgs la{};
+    la.H = hidden_states; la.ldh = ldh; la.W = weight + col0 * ldw; la.ldw = ldw;
+    la.n_rows = rows; la.K = static_cast<int>(hidden); la.group_cols = static_cast<int>(gcols);
+    la.first_col = static_cast<int>(col0); la.Z = Z; la.ldz = l.ldz; la.part = part;
+    la.parts_per_row = l.parts_per_row; la.targets = targets; la.ztarget = ztarget; la.n_p = n_p;
+    la.n_ttiles = (rows + LogitsShape::kBN - 1) / LogitsShape::kBN;
+    la.n_tiles = la.n_ttiles * static_cast<int>((gcols + LogitsShape::kBM - 1) / LogitsShape::kBM);
+    // one workgroup per CU (a multiple of 8, one range per XCD) or one per tile, if fewer
+    int wgs = std::min(la.n_tiles, device_cus());
+    if (wgs >= kXcds) wgs -= wgs % kXcds;
+    hipLaunchKernelGGL((head_logits_kernel<LogitsShape>), dim3(static_cast<unsigned>(wgs)),
+                       dim3(LogitsShape::kThreads), 0, s, la);
     MergeArgs ma{};
     ma.part = part; ma.parts_per_row = l.parts_per_row;
     ma.scale = scale; ma.scale_blocks = l.scale_blocks;
@@ -723,7 +903,7 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
       ga.scale = scale; ga.scale_blocks = l.scale_blocks;
       ga.Y = Y;
       const GradPlan gp = plan_grad(n_grad, hidden, ns);
-      const int bn = gp.wide ? Wide::kBN : Narrow::kBN;
+      const int bn = gp.wide ? GradWide::kBN : GradNarrow::kBN;
       ga.ksplit = gp.ksplit;
       ga.n_mtiles = static_cast<int>((n_grad + kBM - 1) / kBM);
       ga.n_ntiles = static_cast<int>((hidden + bn - 1) / bn);

@@ -116,6 +116,25 @@ struct Loader {
       off[p] = row < rows_valid ? static_cast<uint32_t>((row * ld + kc * 8) * 2) : kOob;
     }
   }
+  // The same operand with rows past `rows_valid` cut off by the descriptor's range instead of by
+  // per-lane offsets: `lanes` sets the offsets, which depend on the lane only (all rows read), once;
+  // `rows` points the descriptor at a tile (scalar registers only), so a kernel that walks tiles
+  // keeps one set of offsets. rows_valid * ld * 2 must stay below 2^32.
+  __device__ __forceinline__ void lanes(int64_t ld, int k_valid_, int wave, int lane) {
+    k_lo = 0;
+    k_valid = k_valid_;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int row = kRowsPerBlock * (p * S::kWaves + wave) + lane / S::kCpr;
+      const int kc = (lane % S::kCpr) ^ swz_key<S::kCpr>(row);
+      kc8[p] = kc * 8;
+      off[p] = static_cast<uint32_t>((row * ld + kc * 8) * 2);
+    }
+  }
+  __device__ __forceinline__ void rows(const uint16_t* base, int64_t ld, int rows_valid) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0,
+                                             static_cast<int>(rows_valid * ld * 2), 0x00020000);
+  }
   // operands of step k0 into the stage block at `dst`
   __device__ __forceinline__ void issue(unsigned char* dst, int k0, int wave) {
 #pragma unroll
