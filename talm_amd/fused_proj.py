@@ -34,6 +34,41 @@ Q, K, V, O, GATE, UP, DOWN = range(7)
 QKV_MFMA = os.environ.get("SOLUTION_DISABLE_QKV_MFMA") != "1"
 COUNTS = {"attn": 0, "attn_fallback": 0}
 
+# Adapter weight gradients written straight into buffers that a caller owns (the graphed step):
+# id(parameter) -> (parameter, fp32 buffer of its shape). A q|k|v node then writes the weight's
+# gradient into its buffer, overwriting it (every adapter weight gets exactly one contribution
+# per backward), and returns None for that input, so autograd adds nothing into .grad and the
+# buffer needs no clearing first. GRAD_WRITTEN collects the ids written, for the caller to check.
+GRAD_INTO = {}
+GRAD_WRITTEN = set()
+
+
+def _grad_targets(params):
+    """The registered buffer of each parameter (None where there is none)."""
+    if not GRAD_INTO:
+        return [None] * len(params)
+    out = []
+    for p in params:
+        hit = GRAD_INTO.get(id(p))
+        out.append(hit[1] if hit is not None and hit[0] is p else None)
+    return out
+
+
+def _deliver(lora_grads, params):
+    """Gradients for the node's adapter inputs: those with a registered buffer go into it
+    (None is returned for them), the others to autograd."""
+    if not GRAD_INTO:
+        return lora_grads
+    out = list(lora_grads)
+    for i, (g, buf) in enumerate(zip(lora_grads, _grad_targets(params))):
+        if g is None or buf is None:
+            continue
+        if g is not buf:
+            buf.copy_(g)
+        GRAD_WRITTEN.add(id(params[i]))
+        out[i] = None
+    return out
+
 
 class FusedProjections(torch.autograd.Function):
     """y_i = x W_i^T + b_i (+ scaling_i * B_i(A_i(dropout_i(x)))) for the adjacent packed
@@ -55,6 +90,7 @@ class FusedProjections(torch.autograd.Function):
     @staticmethod
     def _forward(ctx, x, group, first, last, adapters, compact, rope, head_dim, lora_weights,
                  states):
+        ctx.lora_params = tuple(lora_weights)
         x2 = x.reshape(-1, x.shape[-1])
         n_tok = x2.shape[0]
         sizes = [group.shapes[i][0] for i in range(first, last)]
@@ -215,7 +251,8 @@ class FusedProjections(torch.autograd.Function):
                               else None)
             del xd, mask
         dx = None if dx is None else dx.view(ctx.x_shape)
-        return (dx, None, None, None, None, None, None, None, *lora_grads)
+        return (dx, None, None, None, None, None, None, None,
+                *_deliver(lora_grads, ctx.lora_params))
 
 
 def _mfma_ok(x2, weight, bias, bounds, adapters, halves, rope, head_dim):
@@ -305,17 +342,19 @@ def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
     wanted = [ctx.needs_input_grad[8 + i] for i in range(2 * len(ctx.adapters))]
     dx, lora_grads = _mfma_backward_core(grads, x2, rest, cos, sin, weight, ctx.sizes,
                                          ctx.adapters, ctx.has_rope, wanted,
-                                         getattr(ctx, "a_t", None))
+                                         getattr(ctx, "a_t", None),
+                                         _grad_targets(ctx.lora_params))
     dx = None if dx is None else dx.view(ctx.x_shape)
-    return (dx, None, None, None, None, None, None, None, *lora_grads)
+    return (dx, None, None, None, None, None, None, None, *_deliver(lora_grads, ctx.lora_params))
 
 
 def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_rope, wanted,
-                        a_t=None):
+                        a_t=None, outs=None):
     """dX [N, H] (None without `weight`) and the adapters' [dA, dB, ...] of the q|k|v node from
     the gradients of its q, k, v outputs (fp16, unit column stride); `rest` holds (t, A16, B16)
     per adapter, `wanted` which adapter gradients to form, `a_t` the adapters' A^T side by side
-    ([H, 16 per adapter] fp16; formed here when None)."""
+    ([H, 16 per adapter] fp16; formed here when None); `outs` optional fp32 buffers for the
+    adapter gradients (written in place and returned as themselves)."""
     n_tok, size = x2.shape
     bounds = [0]
     for s_ in sizes:
@@ -363,9 +402,12 @@ def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_
             return dx, _weight_grads_ops(dcat, u, x2, halves, bounds, adapters, wanted)
         t_cat = torch.as_strided(t_all, (n_tok, 16 * len(adapters)), (t_all.stride(0), 1))
         segs = [(bounds[seg], bounds[seg + 1] - bounds[seg], s_) for seg, s_, _p in adapters]
-        grads_ = [torch.empty(16, size, dtype=torch.float32, device=x2.device) if i % 2 == 0
-                  else torch.empty(segs[i // 2][1], 16, dtype=torch.float32, device=x2.device)
+        shapes = [(16, size) if i % 2 == 0 else (segs[i // 2][1], 16)
                   for i in range(2 * len(adapters))]
+        outs = outs or [None] * len(shapes)
+        grads_ = [o if o is not None and tuple(o.shape) == shp and o.dtype == torch.float32
+                  and o.is_contiguous() else torch.empty(shp, dtype=torch.float32, device=x2.device)
+                  for o, shp in zip(outs, shapes)]
         pad = segs + [(0, 0, 0.0)]
         ws = torch.empty(_ops_ws(n_tok, size, pad[0][1], pad[1][1]), dtype=torch.uint8,
                          device=x2.device)
@@ -443,6 +485,7 @@ class AttentionBlock(torch.autograd.Function):
         ctx.group, ctx.adapters, ctx.sizes, ctx.bounds = group, adapters, sizes, bounds
         ctx.head_dim, ctx.n_heads, ctx.n_kv = head_dim, n_heads, n_kv
         ctx.max_len, ctx.scale, ctx.x_shape = max_len, scale, x.shape
+        ctx.lora_params = tuple(lora_weights)
         # for the backward's dX (forward runs with grad mode off: ask the node's inputs)
         ctx.a_t = adapters_t([lora_weights[2 * k] for k in range(len(adapters))]) \
             if adapters and ctx.needs_input_grad[0] else None
@@ -488,11 +531,13 @@ class AttentionBlock(torch.autograd.Function):
         if weight is None and ctx.needs_input_grad[0]:
             weight = torch.cat([group.weight(i) for i in (Q, K, V)], 0)
         dx, lora_grads = _mfma_backward_core((dq, dk, dv), x2, rest, cos, sin, weight,
-                                             ctx.sizes, ctx.adapters, True, wanted, ctx.a_t)
+                                             ctx.sizes, ctx.adapters, True, wanted, ctx.a_t,
+                                             _grad_targets(ctx.lora_params))
         RAN["attn_kernel_bwd"] += 1
         RAN["qkv_mfma_bwd"] += 1
         dx = None if dx is None else dx.view(ctx.x_shape)
-        return (dx, None, None, None, None, None, None, None, None, None, *lora_grads)
+        return (dx, None, None, None, None, None, None, None, None, None,
+                *_deliver(lora_grads, ctx.lora_params))
 
 
 _HOOK_DICTS = ("_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks")

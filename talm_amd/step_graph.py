@@ -13,10 +13,13 @@ it. `GraphedTrainer` captures the forward and backward of the step once per buck
   difference is rounding where a library GEMM picks another algorithm for the larger row count;
 - the head takes every row as a gradient row, with no labelled-first count read on the host;
 - the batch tensors are copied into the static input buffers the graph reads;
-- the LoRA gradients live in one set of buffers shared by every graph: each capture starts
-  by zeroing them (fill kernels, part of the graph) and the backward accumulates into them
-  in place, so 97 buckets hold one gradient set, not 97. They are handed to the parameters
-  after each replay.
+- the LoRA gradients live in one set of buffers shared by every graph, so 97 buckets hold one
+  gradient set, not 97. The q|k|v nodes write each adapter weight's gradient straight into its
+  buffer (`fused_proj.GRAD_INTO`: one contribution per weight and backward, so the buffers need
+  no clearing and autograd adds nothing: about 230 fill and add launches fewer per step). If
+  some adapter's gradient does not come from such a node, the bucket is captured again the
+  general way: the graph zeroes the buffers (fill kernels) and the backward accumulates into
+  them. They are handed to the parameters after each replay.
 
 The optimizer tail stays eager: GradScaler unscale and update, clipping, `AdapterAdamW` and the
 learning-rate schedule. It is about ten launches, and their host cost overlaps the graph's GPU
@@ -34,7 +37,7 @@ import time
 
 import torch
 
-from . import patches, unpad
+from . import fused_proj, patches, unpad
 from .adapters import COPIES, AdapterAdamW
 
 _BATCH_KEYS = ("input_ids", "attention_mask", "labels")
@@ -57,6 +60,7 @@ class GraphedTrainer:
         self.graphs = {}           # bucket -> (graph, loss, gradients, per-token metrics)
         self.pool = None
         self.grads = None          # the LoRA gradient buffers every graph writes
+        self.direct_grads = True   # the nodes write them (False: zero, then accumulate)
         self.capture_seconds = 0.0
         self.replays = 0
         COPIES.in_place = True
@@ -101,18 +105,36 @@ class GraphedTrainer:
         for p, g in zip(t.params, self.grads):
             p.grad = g
         graph = torch.cuda.CUDAGraph()
-        # the pad sequence is shorter than one bucket step (a full bucket when no token is real)
-        with unpad.static_tokens(n_bucket, max_pad=self.bucket):
-            with torch.cuda.graph(graph, pool=self.pool):
-                for g in self.grads:
-                    g.zero_()
-                with torch.autocast("cuda", dtype=torch.float16):
-                    out = t.model(**self.static)
-                t.scaler.scale(out.loss).backward()
+        direct = self.direct_grads
+        if direct:
+            fused_proj.GRAD_INTO.update((id(p), (p, g)) for p, g in zip(t.params, self.grads))
+            fused_proj.GRAD_WRITTEN.clear()
+        try:
+            # the pad sequence is shorter than one bucket step (a full bucket when no token is
+            # real)
+            with unpad.static_tokens(n_bucket, max_pad=self.bucket):
+                with torch.cuda.graph(graph, pool=self.pool):
+                    if not direct:
+                        for g in self.grads:
+                            g.zero_()
+                    with torch.autocast("cuda", dtype=torch.float16):
+                        out = t.model(**self.static)
+                    t.scaler.scale(out.loss).backward()
+        finally:
+            fused_proj.GRAD_INTO.clear()
         if self.pool is None:
             self.pool = graph.pool()
-        # the backward accumulated into the shared buffers in place (it replaces a parameter's
-        # .grad only when it cannot add into it)
+        if direct and any(id(p) not in fused_proj.GRAD_WRITTEN for p in t.params):
+            # some gradient went through autograd into an uncleared buffer: capture this bucket
+            # (and every later one) the general way
+            del graph, out
+            self.direct_grads = False
+            for p, g in zip(t.params, held):
+                p.grad = g
+            self.capture_seconds += time.perf_counter() - start
+            return self.capture(n_bucket)
+        # the backward wrote or accumulated into the shared buffers in place (autograd replaces
+        # a parameter's .grad only when it cannot add into it)
         if any(p.grad is not g for p, g in zip(t.params, self.grads)):
             raise RuntimeError("GraphedTrainer: the backward did not accumulate into the shared "
                                "gradient buffers")

@@ -82,7 +82,7 @@ def _run(mode, monkeypatch, bucket=64):
             losses.append(float(loss))
             metrics.append(_metrics())
         weights = [p.detach().clone() for p in trainer.params]
-        info = None if gt is None else (gt.replays, sorted(gt.graphs))
+        info = None if gt is None else (gt.replays, sorted(gt.graphs), gt.direct_grads)
     finally:
         if gt is not None:
             gt.close()
@@ -96,10 +96,11 @@ def _run(mode, monkeypatch, bucket=64):
 def test_graphed_step_matches_eager_static_step_bitwise(monkeypatch, bucket):
     print(f"[case] graphed step vs eager fixed-shape step (bitwise), bucket {bucket}", flush=True)
     ref_losses, ref_weights, _, ref_metrics = _run("static", monkeypatch, bucket)
-    losses, weights, (replays, buckets), metrics = _run("graph", monkeypatch, bucket)
+    losses, weights, (replays, buckets, direct), metrics = _run("graph", monkeypatch, bucket)
     print(f"[graph] losses {losses}\n[static] losses {ref_losses}", flush=True)
     assert replays == len(LENGTHS) - WARM
     assert buckets == BUCKETS[bucket]
+    assert direct, "the q|k|v nodes did not write every adapter gradient into its buffer"
     assert losses == ref_losses
     for w, r in zip(weights, ref_weights):
         assert torch.equal(w, r), (w - r).abs().max().item()
