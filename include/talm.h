@@ -56,6 +56,24 @@ int talm_nf4_group_dequant(const uint8_t* packed, const uint8_t* absmax8, const 
                            int64_t n_rows, int32_t qblock, int32_t qblock2, void* stream);
 
 /*
+ * The same grouped dequantization written transposed, for the backward's input-gradient GEMMs
+ * (dX = dY W reads W^T as the k-contiguous operand). No counterpart of its own in the reference,
+ * whose backward multiplies by the row-major weight of qgroup.launch (solution/qgroup.py:72-99,
+ * :346-355); the values are talm_nf4_group_dequant's, bit for bit.
+ *   segs  i64 [n_seg][5]: for each projection W [rows, cols]: the element index of its first
+ *         weight in packed / absmax8 (a multiple of qblock), rows, cols, the element offset of
+ *         W^T in `out` and the row stride of W^T (so projections with the same cols can sit
+ *         side by side in one W^T: q|k|v, gate|up);
+ *   out   f16 [out_numel]: out[dst + c * ld + r] = W[r][c].
+ * qblock: power of two >= 64; rows a multiple of 8, cols of 64; ld >= rows, ld and dst multiples
+ * of 8; n_seg <= 8. packed and out 16-byte aligned.
+ */
+int talm_nf4_group_dequant_t(const uint8_t* packed, const uint8_t* absmax8, const float* code,
+                             const float* absmax2, const float* offset2, const int64_t* segs,
+                             int32_t n_seg, int32_t qblock, int32_t qblock2, uint16_t* out,
+                             int64_t out_numel, void* stream);
+
+/*
  * Per-projection NF4 dequantization with an fp32 absmax per block (bitsandbytes'
  * dequantize_blockwise + offset already applied).
  * Replaces nf4_dequant.nf4_dequantize / nf4_dequant_pairs_kernel (solution/nf4_dequant.py:38-91).

@@ -141,6 +141,97 @@ __global__ __launch_bounds__(kThreads) void nf4_bytes_kernel(const uint8_t* __re
   out[i] = pack2(mul_f32(kNF4Levels[byte >> 4], scale), mul_f32(kNF4Levels[byte & 15u], scale));
 }
 
+// Transposed grouped kernel: W^T of each projection of a packed layer, for the backward's
+// input-gradient GEMMs (dX = dY W reads W^T as the k-contiguous operand). A tile is 64 weight
+// rows x 256 columns of one projection (64-weight absmax blocks lie inside one row). Thread
+// (p, ci) reads the 32 columns 32 ci .. of rows 2 p and 2 p + 1 with one 16-byte load each (eight
+// lanes read a row's 128 bytes) and packs the two rows' values of each column into one 32-bit
+// LDS word: the tile is stored transposed, [column][row pair], with the pair index XOR-ed by
+// 4 ci so that the eight lanes writing one pair position hit different banks, and so that four
+// consecutive pairs stay adjacent. Then each W^T row of the tile (64 values, 128 bytes) is
+// written by eight lanes with 16-byte stores. Values are the grouped kernel's bit for bit.
+constexpr int kTRows = 64, kTCols = 256;
+constexpr int kTStride = kTRows / 2 + 4;  // words per LDS column: 16-byte aligned rows
+constexpr int kMaxTSeg = 8;
+static_assert(kTRows / 2 * (kTCols / 32) == kThreads, "one row pair and 32 columns per thread");
+
+struct TSegs {
+  int64_t start[kMaxTSeg];  // first weight element of the projection in the packed buffers
+  int64_t dst[kMaxTSeg];    // element offset of its W^T (row 0, column 0) in the output
+  int32_t rows[kMaxTSeg], cols[kMaxTSeg], ld[kMaxTSeg];  // W [rows, cols]; W^T row stride
+  int32_t col_tiles[kMaxTSeg];
+  int32_t tile0[kMaxTSeg + 1];  // first tile of each projection in the grid
+  int n_seg;
+};
+
+template <bool kPow2>
+__global__ __launch_bounds__(kThreads) void nf4_group_t_kernel(
+    const uint8_t* __restrict__ packed, const uint8_t* __restrict__ absmax8,
+    const float* __restrict__ code, const float* __restrict__ absmax2,
+    const float* __restrict__ offset2, uint16_t* __restrict__ out, TSegs s, int qblock_shift,
+    uint32_t qblock2, int qblock2_shift) {
+  __shared__ float s_code[256];
+  __shared__ float s_levels[16];
+  __shared__ __attribute__((aligned(16))) uint32_t s_t[kTCols * kTStride];
+  s_code[threadIdx.x] = code[threadIdx.x];
+  if (threadIdx.x < 16) s_levels[threadIdx.x] = kNF4Levels[threadIdx.x];
+  // workgroup b runs on XCD b % 8: each XCD takes one contiguous range of tiles, so the
+  // neighbouring tiles of a row band, which read the same cache lines of codes, share an L2
+  const uint32_t n_tiles = static_cast<uint32_t>(s.tile0[s.n_seg]);
+  const uint32_t xcd = blockIdx.x % 8, per = n_tiles / 8, extra = n_tiles % 8;
+  const int tile = static_cast<int>(xcd * per + min(xcd, extra) + blockIdx.x / 8);
+  int g = 0;
+  while (g + 1 < s.n_seg && tile >= s.tile0[g + 1]) ++g;
+  const int local = tile - s.tile0[g];
+  const int r0 = local / s.col_tiles[g] * kTRows, c0 = local % s.col_tiles[g] * kTCols;
+  const int rows = s.rows[g], cols = s.cols[g];
+  const int p = threadIdx.x >> 3, ci = threadIdx.x & 7;
+  const bool col_ok = c0 + 32 * ci < cols;
+  const int cc = col_ok ? c0 + 32 * ci : c0;  // a column chunk past the end reads the first
+  u32x4 w[2];
+  uint32_t a8[2];
+  float a2[2], o2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {  // both rows' loads before any use (rows past the end clamped)
+    const int r = min(r0 + 2 * p + h, rows - 1);
+    const int64_t e = s.start[g] + static_cast<int64_t>(r) * cols + cc;
+    w[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + e / 2));
+    const int64_t blk = e >> qblock_shift;
+    const int64_t blk2 = kPow2 ? (blk >> qblock2_shift)
+                               : static_cast<int64_t>(static_cast<uint32_t>(blk) / qblock2);
+    a8[h] = absmax8[blk];
+    a2[h] = absmax2[blk2];
+    o2[h] = offset2[blk2];
+  }
+  __syncthreads();  // the tables in LDS
+  float scale[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) scale[h] = block_scale(s_code[a8[h]], a2[h], o2[h]);
+  uint32_t* col = s_t + (32 * ci) * kTStride + (p ^ (4 * ci));
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {  // word j / 8, byte (j % 8) / 2, high nibble first
+    uint32_t pair = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t word = w[h][j >> 3];
+      const uint32_t byte = (word >> (8 * ((j & 7) >> 1))) & 0xffu;
+      const uint32_t nib = (j & 1) ? (byte & 15u) : (byte >> 4);
+      pair |= static_cast<uint32_t>(f2h(mul_f32(s_levels[nib], scale[h]))) << (16 * h);
+    }
+    col[j * kTStride] = pair;
+  }
+  __syncthreads();
+  uint16_t* dst = out + s.dst[g];
+#pragma unroll
+  for (int k = 0; k < kTCols * (kTRows / 8) / kThreads; ++k) {
+    const int id = k * kThreads + threadIdx.x;
+    const int c = id >> 3, oc = id & 7;  // W^T row c0 + c: rows r0 + 8 oc .. + 7 of W
+    if (c0 + c < cols && r0 + 8 * oc < rows)
+      *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(c0 + c) * s.ld[g] + r0 + 8 * oc) =
+          *reinterpret_cast<const uint4*>(s_t + c * kTStride + ((4 * oc) ^ (4 * (c >> 5))));
+  }
+}
+
 int log2_exact(int64_t v) {
   if (v <= 0 || (v & (v - 1))) return -1;
   int s = 0;
@@ -188,6 +279,56 @@ TALM_API int talm_nf4_group_dequant(const uint8_t* packed, const uint8_t* absmax
                      absmax2, offset2, reinterpret_cast<uint4*>(out), n_words, qshift - 3,
                      static_cast<uint32_t>(qblock2), log2_exact(qblock2));
   return check_launch("nf4_group_dequant");
+}
+
+TALM_API int talm_nf4_group_dequant_t(const uint8_t* packed, const uint8_t* absmax8,
+                                      const float* code, const float* absmax2,
+                                      const float* offset2, const int64_t* segs, int32_t n_seg,
+                                      int32_t qblock, int32_t qblock2, uint16_t* out,
+                                      int64_t out_numel, void* stream) {
+  const int qshift = log2_exact(qblock);
+  if (qshift < 6)
+    return fail(TALM_EINVAL, "nf4_group_dequant_t: qblock %d is not a power of two >= 64", qblock);
+  if (qblock2 < 1) return fail(TALM_EINVAL, "nf4_group_dequant_t: qblock2 %d < 1", qblock2);
+  if (n_seg < 0 || n_seg > kMaxTSeg)
+    return fail(TALM_EINVAL, "nf4_group_dequant_t: %d projections (at most %d)", n_seg, kMaxTSeg);
+  if (n_seg == 0) return ok();
+  if (!packed || !absmax8 || !code || !absmax2 || !offset2 || !out || !segs)
+    return fail(TALM_EINVAL, "nf4_group_dequant_t: null pointer");
+  if (!aligned(packed, 16) || !aligned(out, 16))
+    return fail(TALM_EINVAL, "nf4_group_dequant_t: packed and out must be 16-byte aligned");
+  TSegs t{};
+  t.n_seg = n_seg;
+  int64_t tiles = 0;
+  for (int g = 0; g < n_seg; ++g) {
+    const int64_t start = segs[5 * g], rows = segs[5 * g + 1], cols = segs[5 * g + 2];
+    const int64_t dst = segs[5 * g + 3], ld = segs[5 * g + 4];
+    if (start < 0 || start % qblock || rows < 8 || rows % 8 || cols < 64 || cols % 64 ||
+        rows > (1 << 24) || cols > (1 << 24) || ld < rows || ld % 8 || ld > (1 << 30) ||
+        dst < 0 || dst % 8 || dst + (cols - 1) * ld + rows > out_numel)
+      return fail(TALM_EINVAL,
+                  "nf4_group_dequant_t: projection %d (start %lld, [%lld, %lld], W^T at %lld "
+                  "stride %lld): start a multiple of qblock, rows a multiple of 8, columns of "
+                  "64, stride >= rows and a multiple of 8, inside the %lld-element output",
+                  g, (long long)start, (long long)rows, (long long)cols, (long long)dst,
+                  (long long)ld, (long long)out_numel);
+    t.start[g] = start;
+    t.dst[g] = dst;
+    t.rows[g] = static_cast<int32_t>(rows);
+    t.cols[g] = static_cast<int32_t>(cols);
+    t.ld[g] = static_cast<int32_t>(ld);
+    t.col_tiles[g] = static_cast<int32_t>((cols + kTCols - 1) / kTCols);
+    t.tile0[g] = static_cast<int32_t>(tiles);
+    tiles += (rows + kTRows - 1) / kTRows * t.col_tiles[g];
+    if (tiles > 0x7fffffff) return fail(TALM_EINVAL, "nf4_group_dequant_t: too many weights");
+  }
+  t.tile0[n_seg] = static_cast<int32_t>(tiles);
+  const int q2shift = log2_exact(qblock2);
+  auto kernel = q2shift >= 0 ? nf4_group_t_kernel<true> : nf4_group_t_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+                     as_stream(stream), packed, absmax8, code, absmax2, offset2, out, t, qshift,
+                     static_cast<uint32_t>(qblock2), q2shift);
+  return check_launch("nf4_group_dequant_t");
 }
 
 TALM_API int talm_nf4_dequant(const uint8_t* packed, const float* absmax, uint16_t* out, int64_t n,

@@ -101,6 +101,37 @@ void nf4_group_dequant(const Tensor& packed, const Tensor& absmax8, const Tensor
         "nf4_group_dequant");
 }
 
+// W^T of projections of a packed layer: segs holds (start, rows, cols, dst, ld) per projection.
+void nf4_group_dequant_t(const Tensor& packed, const Tensor& absmax8, const Tensor& code,
+                         const Tensor& absmax2, const Tensor& offset2, at::IntArrayRef segs,
+                         const Tensor& out, int64_t qblock, int64_t qblock2) {
+  require(packed.scalar_type() == at::kByte && absmax8.scalar_type() == at::kByte,
+          "packed/absmax8: uint8");
+  require(code.scalar_type() == at::kFloat && absmax2.scalar_type() == at::kFloat &&
+              offset2.scalar_type() == at::kFloat,
+          "code/absmax2/offset2: float32");
+  require_fp16(out, "out");
+  for (const Tensor* t : {&packed, &absmax8, &code, &absmax2, &offset2, &out})
+    require(t->is_contiguous() && t->device() == out.device(), "operands: contiguous, one device");
+  require(code.numel() >= 256, "code: 256 entries");
+  require(segs.size() % 5 == 0, "segs: five integers per projection");
+  require(qblock > 0 && qblock2 > 0, "qblock / qblock2 positive");
+  for (size_t g = 0; g < segs.size(); g += 5) {
+    const int64_t end = segs[g] + segs[g + 1] * segs[g + 2];  // one past the last weight
+    require(segs[g] >= 0 && segs[g + 1] > 0 && segs[g + 2] > 0 && end <= packed.numel() * 2 &&
+                (end + qblock - 1) / qblock <= absmax8.numel() &&
+                ((end + qblock - 1) / qblock + qblock2 - 1) / qblock2 <= absmax2.numel() &&
+                offset2.numel() == absmax2.numel(),
+            "nf4_group_dequant_t: a projection outside the packed buffers");
+  }
+  check(talm_nf4_group_dequant_t(as<uint8_t>(packed), as<uint8_t>(absmax8), as<float>(code),
+                                 as<float>(absmax2), as<float>(offset2), segs.data(),
+                                 static_cast<int32_t>(segs.size() / 5),
+                                 static_cast<int32_t>(qblock), static_cast<int32_t>(qblock2),
+                                 as<uint16_t>(out), out.numel(), stream_of(out)),
+        "nf4_group_dequant_t");
+}
+
 void nf4_dequant(const Tensor& packed, const Tensor& absmax, const Tensor& out,
                  int64_t blocksize) {
   require(packed.scalar_type() == at::kByte && absmax.scalar_type() == at::kFloat,
@@ -969,6 +1000,8 @@ Tensor gemm_tune(const Tensor& a, int64_t trans_a, const Tensor& b, int64_t tran
 TORCH_LIBRARY(talm, m) {
   m.def("nf4_group_dequant(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
         "Tensor offset2, Tensor(a!) out, int qblock, int qblock2) -> ()");
+  m.def("nf4_group_dequant_t(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
+        "Tensor offset2, int[] segs, Tensor(a!) out, int qblock, int qblock2) -> ()");
   m.def("nf4_dequant(Tensor packed, Tensor absmax, Tensor(a!) out, int blocksize) -> ()");
   m.def("rmsnorm(Tensor(a!) a, Tensor(b!)? q, Tensor(c!) h, Tensor(d!) xhat, Tensor(e!)? p, "
         "Tensor weight, Tensor(f!) rstd, float eps, int backward) -> ()");
@@ -1017,6 +1050,7 @@ TORCH_LIBRARY(talm, m) {
 
 TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("nf4_group_dequant", &nf4_group_dequant);
+  m.impl("nf4_group_dequant_t", &nf4_group_dequant_t);
   m.impl("nf4_dequant", &nf4_dequant);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("rope", &rope);

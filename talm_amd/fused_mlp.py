@@ -66,16 +66,25 @@ class FusedMLP(torch.autograd.Function):
             dy = dy.to(torch.float16)
         if dy.stride(1) != 1:
             dy = dy.contiguous()
-        w_down = group.weight(DOWN)
+        # the input gradients multiply by W; the group's W^T blocks [in, out] let them run in the
+        # forward's product form (x W^T), which hipBLASLt runs faster at these shapes
         dact = torch.empty(n_tok, inter, dtype=torch.float16, device=dy.device)
-        torch.ops.talm.gemm(dy, w_down, None, 0, dact)
-        del w_down
+        w_down_t = group.span_t(DOWN, DOWN + 1)
+        if w_down_t is not None:
+            torch.ops.talm.gemm(dy, w_down_t, None, 1, dact)
+        else:
+            torch.ops.talm.gemm(dy, group.weight(DOWN), None, 0, dact)
+        del w_down_t
         gate, up = gu[:, :inter], gu[:, inter:]
         torch.ops.talm.swiglu_bwd_rows(dact, gate, up, gate, up)
         del dact
         dx = torch.empty(n_tok, hidden, dtype=torch.float16, device=dy.device)
-        w_gu = group.span(GATE, DOWN)
-        if w_gu is not None:
+        w_gu_t = group.span_t(GATE, DOWN)
+        w_gu = None if w_gu_t is not None else group.span(GATE, DOWN)
+        if w_gu_t is not None:
+            # dx = [dgate | dup] [W_gate; W_up] = gu ([W_gate; W_up]^T)^T: one GEMM
+            torch.ops.talm.gemm(gu, w_gu_t, None, 1, dx)
+        elif w_gu is not None:
             # dx = [dgate | dup] [W_gate; W_up]: one GEMM with the reduction over both halves
             torch.ops.talm.gemm(gu, w_gu, None, 0, dx)
         else:  # "qgroup" is off: the projections' own weights

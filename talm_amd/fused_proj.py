@@ -332,29 +332,33 @@ def _mfma_backward(ctx, grads):
     if ctx.has_rope:
         cos, sin = rest[-2:]
         rest = rest[:-2]
-    weight = group.span(ctx.first, ctx.last) if ctx.needs_input_grad[0] else None
-    if ctx.needs_input_grad[0] and weight is None:
-        return None
-    return _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight)
+    weight = weight_t = None
+    if ctx.needs_input_grad[0]:
+        weight_t = group.span_t(ctx.first, ctx.last)
+        weight = None if weight_t is not None else group.span(ctx.first, ctx.last)
+        if weight is None and weight_t is None:
+            return None
+    return _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight, weight_t)
 
 
-def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight):
+def _mfma_backward_ops(ctx, grads, x2, rest, cos, sin, weight, weight_t=None):
     wanted = [ctx.needs_input_grad[8 + i] for i in range(2 * len(ctx.adapters))]
     dx, lora_grads = _mfma_backward_core(grads, x2, rest, cos, sin, weight, ctx.sizes,
                                          ctx.adapters, ctx.has_rope, wanted,
                                          getattr(ctx, "a_t", None),
-                                         _grad_targets(ctx.lora_params))
+                                         _grad_targets(ctx.lora_params), weight_t)
     dx = None if dx is None else dx.view(ctx.x_shape)
     return (dx, None, None, None, None, None, None, None, *_deliver(lora_grads, ctx.lora_params))
 
 
 def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_rope, wanted,
-                        a_t=None, outs=None):
+                        a_t=None, outs=None, weight_t=None):
     """dX [N, H] (None without `weight`) and the adapters' [dA, dB, ...] of the q|k|v node from
     the gradients of its q, k, v outputs (fp16, unit column stride); `rest` holds (t, A16, B16)
     per adapter, `wanted` which adapter gradients to form, `a_t` the adapters' A^T side by side
     ([H, 16 per adapter] fp16; formed here when None); `outs` optional fp32 buffers for the
-    adapter gradients (written in place and returned as themselves)."""
+    adapter gradients (written in place and returned as themselves); `weight_t` the layer
+    group's W^T [H, >= sum of out] when it holds one (then `weight` is not needed)."""
     n_tok, size = x2.shape
     bounds = [0]
     for s_ in sizes:
@@ -382,11 +386,12 @@ def _mfma_backward_core(grads, x2, rest, cos, sin, weight, sizes, adapters, has_
         torch.ops.talm.lora_down(dcat, halves[0][2], b1, ks[0], ks[1], lo[0], lo[1], 1, scal[0],
                                  scal[1], t_tmp, u)
     dx = None
-    if weight is not None:
+    if weight_t is None and weight is not None:
         from .fused_head import transpose_weight_exact
 
         weight_t = transpose_weight_exact(weight)
         del weight
+    if weight_t is not None:
         if a_t is None and adapters:
             a_t = torch.cat([a16 for _t, a16, _b in halves], 0).t().contiguous()
         dx = torch.empty(n_tok, size, dtype=torch.float16, device=x2.device)
@@ -508,10 +513,16 @@ class AttentionBlock(torch.autograd.Function):
             dy = dy.to(torch.float16)
         if dy.stride(1) != 1:
             dy = dy.contiguous()
-        w_o = group.weight(O)
-        d_o = torch.empty(n_tok, w_o.shape[1], dtype=torch.float16, device=x2.device)
-        torch.ops.talm.gemm(dy, w_o, None, 0, d_o)
-        del w_o
+        # d_o = dy W_o: with the group's W_o^T [in, out], in the product form of the forward
+        w_o_t = group.span_t(O, O + 1)
+        if w_o_t is not None:
+            d_o = torch.empty(n_tok, w_o_t.shape[0], dtype=torch.float16, device=x2.device)
+            torch.ops.talm.gemm(dy, w_o_t, None, 1, d_o)
+        else:
+            w_o = group.weight(O)
+            d_o = torch.empty(n_tok, w_o.shape[1], dtype=torch.float16, device=x2.device)
+            torch.ops.talm.gemm(dy, w_o, None, 0, d_o)
+        del w_o_t
         hd, nh, nkv = ctx.head_dim, ctx.n_heads, ctx.n_kv
         q = out[:, :bounds[1]].view(n_tok, nh, hd)
         k = out[:, bounds[1]:bounds[2]].view(n_tok, nkv, hd)
@@ -526,13 +537,17 @@ class AttentionBlock(torch.autograd.Function):
                                 ctx.scale, dq.view(n_tok, nh, hd), dk.view(n_tok, nkv, hd),
                                 dv.view(n_tok, nkv, hd), ws)
         del ws, d_o
-        weight = group.span(Q, V + 1) if ctx.needs_input_grad[0] else None
+        weight = weight_t = None
+        if ctx.needs_input_grad[0]:
+            weight_t = group.span_t(Q, V + 1)
+            if weight_t is None:
+                weight = group.span(Q, V + 1)
+                if weight is None:
+                    weight = torch.cat([group.weight(i) for i in (Q, K, V)], 0)
         wanted = [ctx.needs_input_grad[10 + i] for i in range(2 * len(ctx.adapters))]
-        if weight is None and ctx.needs_input_grad[0]:
-            weight = torch.cat([group.weight(i) for i in (Q, K, V)], 0)
         dx, lora_grads = _mfma_backward_core((dq, dk, dv), x2, rest, cos, sin, weight,
                                              ctx.sizes, ctx.adapters, True, wanted, ctx.a_t,
-                                             _grad_targets(ctx.lora_params))
+                                             _grad_targets(ctx.lora_params), weight_t)
         RAN["attn_kernel_bwd"] += 1
         RAN["qkv_mfma_bwd"] += 1
         dx = None if dx is None else dx.view(ctx.x_shape)

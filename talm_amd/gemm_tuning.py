@@ -42,6 +42,9 @@ def product_forms():
         ("down_fwd", 1, 0, h, i, i, i, h),
         ("down_dx", 0, 0, i, h, i, h, i),
         ("gate_up_dx", 0, 0, h, 2 * i, h, 2 * i, h),
+        # the input gradients in the forward's form, on the group's transposed weights
+        ("down_dx_t", 1, 0, i, h, h, h, i),
+        ("gate_up_dx_t", 1, 0, h, 2 * i, 2 * i, 2 * i, h),
     )
 
 

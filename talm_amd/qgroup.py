@@ -24,6 +24,13 @@ recomputation, a fallback path, two models interleaved), so nothing is counted, 
 when a step is cut short. The price is that one fp16 layer (94 MB for Qwen2.5-1.5B) stays
 allocated between steps, against 288 GB of HBM.
 
+The backward multiplies by W^T (dX = dY W reads W as the k-contiguous operand of the product in
+the form the forward uses): `resident_t` holds ONE layer's weights dequantized transposed
+(talm_nf4_group_dequant_t, the same values), laid out as four row-major blocks [in, sum of out]:
+q|k|v, o, gate|up, down. `span_t` hands out a block. Each layer's backward makes its group's
+transposed buffer resident with one launch, as the forward does with the row-major one, and
+drops the row-major buffer the forward left behind.
+
 Graceful degradation (state.py): an unexpected error here turns "qgroup" off; each projection
 then takes the per-projection dequantization (nf4_dequant.py, the same values) and the 4-bit
 layer its own forward.
@@ -45,6 +52,10 @@ PROJECTIONS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self
 
 # device -> (group, fp16 buffer of all its weights): the one dequantized layer per GPU
 _RESIDENT = {}
+# device -> (group, fp16 buffer of its W^T blocks): the backward's one transposed layer per GPU
+_RESIDENT_T = {}
+# the blocks of the transposed buffer: projections used as one [in, sum of out] operand
+T_BLOCKS = ((0, 1, 2), (3,), (4, 5), (6,))
 
 
 def launch(packed, absmax8, code, absmax2, offset2, levels, out, n_rows, qblock, qblock2):
@@ -61,6 +72,7 @@ def release():
     """Drop every GPU's resident layer (a forward that failed part-way is about to run again;
     the patches are being removed)."""
     _RESIDENT.clear()
+    _RESIDENT_T.clear()
 
 
 def reset_passes():
@@ -129,6 +141,7 @@ class LayerGroup:
             .expand((seg.stop - seg.start) // span2) for s, seg in zip(states, segments)])
         self.modules = [weakref.ref(m) for m in modules]
         self._bias_spans = {}
+        self.t_layout = self._transposed_layout()
 
     # -- shapes ----------------------------------------------------------------------------------
     @property
@@ -151,6 +164,74 @@ class LayerGroup:
                out, (hi - lo) // self.qblock, self.qblock, self.qblock2)
         return out
 
+    def _transposed_layout(self):
+        """(per projection (block, W^T element offset, row stride), per block (offset, in,
+        width)) of the transposed buffer, or None when the kernel cannot write it (block sizes
+        below 64, rows not multiples of 8 or columns of 64, a block's projections of different
+        input sizes)."""
+        if self.qblock < 64:
+            return None
+        per_proj, blocks, off = [None] * NSEG, [], 0
+        for b, members in enumerate(T_BLOCKS):
+            cols = {self.segments[i].shape[1] for i in members}
+            width = sum(self.segments[i].shape[0] for i in members)
+            if len(cols) != 1 or any(self.segments[i].shape[0] % 8 for i in members):
+                return None
+            (cin,) = cols
+            if cin % 64:
+                return None
+            o_off = 0
+            for i in members:
+                per_proj[i] = (b, off + o_off, width)
+                o_off += self.segments[i].shape[0]
+            blocks.append((off, cin, width))
+            off += cin * width
+        return per_proj, blocks
+
+    def dequantize_t(self):
+        """The layer's W^T blocks (one launch): block b at blocks[b][0], [in, width] row-major."""
+        per_proj, _blocks = self.t_layout
+        segs = []
+        for i, seg in enumerate(self.segments):
+            _b, dst, ld = per_proj[i]
+            segs += [seg.start, seg.shape[0], seg.shape[1], dst, ld]
+        out = torch.empty(self.numel, dtype=torch.float16, device=self.packed.device)
+        torch.ops.talm.nf4_group_dequant_t(self.packed, self.absmax8, self.code, self.absmax2,
+                                           self.offset2, segs, out, self.qblock, self.qblock2)
+        return out
+
+    def resident_t(self):
+        """This layer's transposed buffer: the GPU's resident one when it is this group's, else
+        one launch that makes it so (the forward's row-major buffer is dropped: the backward has
+        begun)."""
+        held = _RESIDENT_T.get(self.device)
+        if held is not None and held[0] is self:
+            return held[1]
+        _RESIDENT.pop(self.device, None)
+        _RESIDENT_T.pop(self.device, None)
+        buf = self.dequantize_t()
+        RAN["group_t"] += 1
+        _RESIDENT_T[self.device] = (self, buf)
+        return buf
+
+    def span_t(self, first, last):
+        """fp16 W^T [in, sum of out] of projections first .. last - 1 when they are one block of
+        the transposed buffer (q|k|v, o, gate|up, down), else None, as when "qgroup" is off or
+        dequantization fails (the caller then takes the row-major weight)."""
+        if "qgroup" in DISABLED or self.t_layout is None:
+            return None
+        members = tuple(range(first, last))
+        if members not in T_BLOCKS:
+            return None
+        try:
+            buf = self.resident_t()
+        except Exception as exc:  # noqa: BLE001 - state.py convention
+            if not fallback("qgroup", exc):
+                raise
+            return None
+        off, cin, width = self.t_layout[1][T_BLOCKS.index(members)]
+        return buf[off:off + cin * width].view(cin, width)
+
     def dequantize_one(self, idx):
         return self.dequantize(idx, idx + 1).view(self.segments[idx].shape)
 
@@ -168,7 +249,8 @@ class LayerGroup:
     def begin_forward(self):
         """The layer's forward begins: its weights become resident now, with one launch."""
         held = _RESIDENT.pop(self.device, None)
-        del held  # the previous layer's buffer goes back to the allocator first
+        held_t = _RESIDENT_T.pop(self.device, None)  # the last backward's: not read by a forward
+        del held, held_t  # the previous buffers go back to the allocator first
         self.resident()
 
     # -- views -------------------------------------------------------------------------------------

@@ -53,6 +53,69 @@ def test_nf4_group_dequant_config1_bit_exact():
         start += n
 
 
+def test_nf4_group_dequant_transposed_config1_bit_exact():
+    """The backward's transposed layer (talm_nf4_group_dequant_t): every projection of the
+    config-1 layer written as W^T into the four blocks q|k|v, o, gate|up, down, bit for bit the
+    oracle's W transposed; the bytes around each block stay untouched."""
+    _case("nf4 group transposed config1")
+    d = workloads.nf4_layer()
+    ref = nf4_oracle.group_dequant(d["packed"].numpy(), d["absmax8"].numpy(), d["code"].numpy(),
+                                   d["absmax2"].numpy(), d["offset2"].numpy())
+    t = {k: d[k].to(DEV) for k in ("packed", "absmax8", "code", "absmax2", "offset2")}
+    blocks = ((0, 1, 2), (3,), (4, 5), (6,))
+    segs, placed, start, off = [], [], 0, 0
+    starts = np.cumsum([0] + [r * c for r, c in d["shapes"]])
+    for members in blocks:
+        cols = d["shapes"][members[0]][1]
+        width = sum(d["shapes"][i][0] for i in members)
+        o_off = 0
+        for i in members:
+            rows = d["shapes"][i][0]
+            segs += [int(starts[i]), rows, cols, off + o_off, width]
+            placed.append((i, off, cols, width, o_off))
+            o_off += rows
+        off += cols * width
+    pad = 64
+    out = torch.full((d["n"] + 2 * pad,), float("nan"), dtype=torch.float16, device=DEV)
+    torch.ops.talm.nf4_group_dequant_t(t["packed"], t["absmax8"], t["code"], t["absmax2"],
+                                       t["offset2"], segs, out[pad:pad + d["n"]], 64, 256)
+    got = f16_bits(out)
+    assert np.all(np.isnan(out[:pad].float().cpu().numpy()))
+    assert np.all(np.isnan(out[pad + d["n"]:].float().cpu().numpy()))
+    for i, blk, cols, width, o_off in placed:
+        rows = d["shapes"][i][0]
+        w = ref[starts[i]:starts[i] + rows * cols].reshape(rows, cols)
+        wt = got[pad + blk:pad + blk + cols * width].reshape(cols, width)[:, o_off:o_off + rows]
+        assert np.array_equal(wt, w.T), (i, rows, cols)
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 64), (136, 192), (264, 128)])
+def test_nf4_group_dequant_transposed_partial_tiles(rows, cols):
+    """Row counts that leave a partial 128-row tile (8-row chunks past the end are not
+    written), into a W^T with a wider row stride whose other columns stay untouched."""
+    _case(f"nf4 group transposed {rows}x{cols}")
+    g = torch.Generator().manual_seed(rows * cols)
+    n = rows * cols
+    n_rows = n // 64
+    n2 = -(-n_rows // 4)
+    packed = torch.randint(0, 256, (n // 2,), generator=g, dtype=torch.int32).to(torch.uint8)
+    absmax8 = torch.randint(0, 256, (n_rows,), generator=g, dtype=torch.int32).to(torch.uint8)
+    code = workloads.dynamic_map()
+    absmax2 = torch.rand(n2, generator=g) * 0.045 + 0.005
+    offset2 = torch.full((n2,), 0.01)
+    ref = nf4_oracle.group_dequant(packed.numpy(), absmax8.numpy(), code.numpy(),
+                                   absmax2.numpy(), offset2.numpy(), 64, 4).reshape(rows, cols)
+    ld, o_off = rows + 24, 8
+    out = torch.full((cols * ld,), float("nan"), dtype=torch.float16, device=DEV)
+    torch.ops.talm.nf4_group_dequant_t(packed.to(DEV), absmax8.to(DEV), code.to(DEV),
+                                       absmax2.to(DEV), offset2.to(DEV), [0, rows, cols, o_off, ld],
+                                       out, 64, 4)
+    got = f16_bits(out).reshape(cols, ld)
+    assert np.array_equal(got[:, o_off:o_off + rows], ref.T)
+    rest = out.view(cols, ld).float().cpu().numpy()
+    assert np.all(np.isnan(rest[:, :o_off])) and np.all(np.isnan(rest[:, o_off + rows:]))
+
+
 @pytest.mark.parametrize("n_rows,qblock,qblock2,shift", [
     (256, 64, 256, 0), (1, 8, 1, 0), (37, 128, 5, 0), (1000, 64, 3, 0), (2, 4096, 1, 0),
     (33, 32, 7, 0), (1000, 64, 256, 4), (77, 16, 3, 0)])
@@ -141,6 +204,16 @@ def test_layer_group_packs_and_keeps_one_resident_layer():
         assert torch.equal(dequantize_4bit(m.weight.data, m.weight.quant_state), ref)
     for idx, ref in enumerate(refs):
         assert torch.equal(group.dequantize_one(idx), ref)
+    # the backward's transposed blocks: one launch for the layer, the row-major buffer dropped
+    before_t = RAN["group_t"]
+    for members in qgroup.T_BLOCKS:
+        wt = group.span_t(members[0], members[-1] + 1)
+        assert torch.equal(wt, torch.cat([refs[i] for i in members]).t()), members
+    assert RAN["group_t"] == before_t + 1
+    assert group.span_t(0, 2) is None and group.span_t(3, 5) is None  # not one block
+    assert qgroup._RESIDENT.get(group.device) is None
+    group.begin_forward()  # a forward drops the transposed buffer again
+    assert qgroup._RESIDENT_T.get(group.device) is None
     qgroup.release()
 
 
