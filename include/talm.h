@@ -74,6 +74,20 @@ int talm_nf4_group_dequant_t(const uint8_t* packed, const uint8_t* absmax8, cons
                              int64_t out_numel, void* stream);
 
 /*
+ * Split-K fp16 GEMM: out [m, n] = f16(a [m, k] b [n, k]^T), fp32 accumulation, both operands
+ * k-contiguous. No counterpart of its own: it replaces the library GEMM (cuBLAS in the reference,
+ * GroupLinear / F.linear, solution/qgroup.py:346-355) for the MLP's long-reduction products
+ * (down projection, input gradient on the transposed gate|up weight). The workspace holds one
+ * fp32 partial [m, n] per K part (talm_gemm_splitk_workspace bytes, -1 for an unsupported
+ * shape); the partials are summed in part order (deterministic).
+ * n, k, lda, ldb, ldo multiples of 8; lda, ldb >= k, below 2^22; ldo >= n; 16-byte aligned.
+ */
+int64_t talm_gemm_splitk_workspace(int64_t m, int64_t n, int64_t k);
+int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                     uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/*
  * Per-projection NF4 dequantization with an fp32 absmax per block (bitsandbytes'
  * dequantize_blockwise + offset already applied).
  * Replaces nf4_dequant.nf4_dequantize / nf4_dequant_pairs_kernel (solution/nf4_dequant.py:38-91).

@@ -56,6 +56,7 @@ SIGNATURES = {
     "talm_lora_mirror": [_P, _I32, _I64, _P, _P],
     "talm_lora_adamw": [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _P, _P, _P, _P, _P, _P],
     "talm_nf4_gemm": [_P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I64, _P],
+    "talm_gemm_splitk": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
 }
 
 # Entry points that return a size instead of a status.
@@ -63,6 +64,7 @@ SIZE_FUNCTIONS = {
     "talm_head_ce_workspace": [_I64, _I64, _I64, _I64, _I64, _I32],
     "talm_lora_wgrad_workspace": [_I64, _I64, _I64, _I64],
     "talm_attn_bwd_workspace": [_I64, _I32],
+    "talm_gemm_splitk_workspace": [_I64, _I64, _I64],
 }
 
 _lock = threading.Lock()

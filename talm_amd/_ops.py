@@ -7,7 +7,8 @@ are the caller's tensors, annotated as mutated). They are registered for the CUD
 dispatch key only: a CPU tensor raises NotImplementedError from the dispatcher, never a CPU
 fallback. Importing this module loads both libraries or raises (no fallback).
 
-The workspace sizes of head_ce and lora_wgrad are plain functions over the C-ABI's size queries.
+The workspace sizes of head_ce, lora_wgrad, attn_bwd and gemm_splitk are plain functions over the
+C-ABI's size queries.
 """
 
 import threading
@@ -22,7 +23,7 @@ OPS = ("nf4_group_dequant", "nf4_dequant", "rmsnorm", "rope", "swiglu_fwd", "swi
        "swiglu_fwd_rows", "swiglu_bwd_rows",
        "head_weight_t", "head_ce", "lora_down", "qkv_lora_fwd", "qkv_bwd_prep", "qkv_lora_bwd_dx",
        "lora_wgrad", "gemm", "gemm_ex", "attn_fwd", "attn_bwd", "lora_mirror", "lora_adamw",
-       "nf4_gemm")
+       "nf4_gemm", "nf4_group_dequant_t", "gemm_splitk")
 
 _load_lock = threading.Lock()
 _loaded = False
@@ -72,3 +73,10 @@ def attn_bwd_workspace_bytes(n_tokens, n_q_heads):
     size = _lib.lib().talm_attn_bwd_workspace(n_tokens, n_q_heads)
     _require(size >= 0, "attn_bwd: unsupported shape")
     return int(size)
+
+
+def gemm_splitk_workspace_bytes(m, n, k):
+    size = _lib.lib().talm_gemm_splitk_workspace(m, n, k)
+    if size < 0:
+        raise ValueError(f"gemm_splitk: unsupported shape m={m} n={n} k={k}")
+    return size

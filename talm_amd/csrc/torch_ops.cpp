@@ -132,6 +132,25 @@ void nf4_group_dequant_t(const Tensor& packed, const Tensor& absmax8, const Tens
         "nf4_group_dequant_t");
 }
 
+// out [m, n] = a [m, k] b [n, k]^T (fp16, fp32 accumulation) as K parts plus a reduction.
+void gemm_splitk(const Tensor& a, const Tensor& b, const Tensor& out, const Tensor& workspace) {
+  for (const auto& [v, name] : {std::pair<const Tensor*, const char*>{&a, "a"}, {&b, "b"},
+                                {&out, "out"}}) {
+    require_fp16(*v, name);
+    TORCH_CHECK_VALUE(v->dim() == 2 && v->stride(1) == 1, "gemm_splitk: ", name,
+                      " unit column stride");
+  }
+  const int64_t m = a.size(0), k = a.size(1), n = b.size(0);
+  require(b.size(1) == k && same_shape(out, m, n), "gemm_splitk: a [m, k], b [n, k], out [m, n]");
+  require(workspace.is_cuda() && workspace.is_contiguous() && workspace.device() == out.device(),
+          "gemm_splitk: workspace");
+  check(talm_gemm_splitk(as<uint16_t>(a), a.stride(0), as<uint16_t>(b), b.stride(0),
+                         as<uint16_t>(out), out.stride(0), m, n, k, workspace.data_ptr(),
+                         workspace.numel() * static_cast<int64_t>(workspace.element_size()),
+                         stream_of(out)),
+        "gemm_splitk");
+}
+
 void nf4_dequant(const Tensor& packed, const Tensor& absmax, const Tensor& out,
                  int64_t blocksize) {
   require(packed.scalar_type() == at::kByte && absmax.scalar_type() == at::kFloat,
@@ -1003,6 +1022,7 @@ TORCH_LIBRARY(talm, m) {
   m.def("nf4_group_dequant_t(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
         "Tensor offset2, int[] segs, Tensor(a!) out, int qblock, int qblock2) -> ()");
   m.def("nf4_dequant(Tensor packed, Tensor absmax, Tensor(a!) out, int blocksize) -> ()");
+  m.def("gemm_splitk(Tensor a, Tensor b, Tensor(a!) out, Tensor(b!) workspace) -> ()");
   m.def("rmsnorm(Tensor(a!) a, Tensor(b!)? q, Tensor(c!) h, Tensor(d!) xhat, Tensor(e!)? p, "
         "Tensor weight, Tensor(f!) rstd, float eps, int backward) -> ()");
   m.def("rope(Tensor q, Tensor k, Tensor cos, Tensor sin, Tensor(a!) out_q, Tensor(b!) out_k, "
@@ -1051,6 +1071,7 @@ TORCH_LIBRARY(talm, m) {
 TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("nf4_group_dequant", &nf4_group_dequant);
   m.impl("nf4_group_dequant_t", &nf4_group_dequant_t);
+  m.impl("gemm_splitk", &gemm_splitk);
   m.impl("nf4_dequant", &nf4_dequant);
   m.impl("rmsnorm", &rmsnorm);
   m.impl("rope", &rope);

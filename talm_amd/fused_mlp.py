@@ -21,12 +21,32 @@ import os
 
 import torch
 
-from . import _ops  # noqa: F401 - registers torch.ops.talm.*
+from . import _ops
 from .engaged import FELL_BACK, RAN
 from .state import DISABLED, fallback
 
 GATE, UP, DOWN = 4, 5, 6
 ENABLED = os.environ.get("SOLUTION_DISABLE_FUSED_MLP") != "1"
+# the long-reduction products (K >= SPLITK_MIN_K: the down projection and the input gradient on
+# the transposed gate|up weight) on this package's split-K MFMA GEMM instead of hipBLASLt
+SPLITK = os.environ.get("SOLUTION_DISABLE_SPLITK") != "1"
+SPLITK_MIN_K = 4096
+
+
+def _linear(a, w, out):
+    """out = a w^T (fp16, both k-contiguous): split-K MFMA GEMM for long reductions, else
+    hipBLASLt."""
+    if SPLITK and a.shape[1] >= SPLITK_MIN_K and "splitk" not in DISABLED:
+        try:
+            ws = torch.empty(_ops.gemm_splitk_workspace_bytes(a.shape[0], w.shape[0], a.shape[1]),
+                             dtype=torch.uint8, device=a.device)
+            torch.ops.talm.gemm_splitk(a, w, out, ws)
+            RAN["splitk"] += 1
+            return
+        except Exception as exc:  # noqa: BLE001 - state.py convention
+            if not fallback("splitk", exc):
+                raise
+    torch.ops.talm.gemm(a, w, None, 1, out)
 
 
 class FusedMLP(torch.autograd.Function):
@@ -49,7 +69,7 @@ class FusedMLP(torch.autograd.Function):
         act = torch.empty(n_tok, inter, dtype=torch.float16, device=x.device)
         torch.ops.talm.swiglu_fwd_rows(gu[:, :inter], gu[:, inter:], act)
         y = torch.empty(n_tok, hidden, dtype=torch.float16, device=x.device)
-        torch.ops.talm.gemm(act, w_down, None, 1, y)
+        _linear(act, w_down, y)
         del act, w_down
         ctx.save_for_backward(gu)
         ctx.group, ctx.x_shape = group, x.shape
@@ -83,7 +103,7 @@ class FusedMLP(torch.autograd.Function):
         w_gu = None if w_gu_t is not None else group.span(GATE, DOWN)
         if w_gu_t is not None:
             # dx = [dgate | dup] [W_gate; W_up] = gu ([W_gate; W_up]^T)^T: one GEMM
-            torch.ops.talm.gemm(gu, w_gu_t, None, 1, dx)
+            _linear(gu, w_gu_t, dx)
         elif w_gu is not None:
             # dx = [dgate | dup] [W_gate; W_up]: one GEMM with the reduction over both halves
             torch.ops.talm.gemm(gu, w_gu, None, 0, dx)

@@ -106,3 +106,46 @@ def test_measured_table_products_match_reference():
                 gemm_tuning.load()
     finally:
         torch.ops.talm.gemm_algo_table(torch.empty(0, 7, dtype=torch.int64))
+
+
+@pytest.mark.parametrize("m,n,k,lda_pad,ldo_pad", [
+    (1312, 1536, 8960, 0, 0),     # the MLP's down projection at a config-5 token count
+    (1312, 1536, 17920, 0, 0),    # its input gradient on the transposed gate|up weight
+    (2048, 1536, 17920, 8, 16),   # the largest bucket, strided operands
+    (37, 24, 136, 0, 8),          # one partial tile, one K part
+    (513, 1000, 4096, 24, 0),     # partial row and column tiles, several parts
+    (1, 8, 8, 0, 0),
+])
+def test_gemm_splitk_matches_fp32_reference(m, n, k, lda_pad, ldo_pad):
+    """talm_gemm_splitk (K parts on the MFMA tile core, fp32 partials summed in part order)
+    against the fp32 product; a second call gives the same bits (no atomics, fixed order)."""
+    from talm_amd import _ops
+
+    g = torch.Generator("cpu").manual_seed(m + 3 * n + k)
+    a_full = torch.randn(m, k + lda_pad, generator=g).half().cuda()
+    a = a_full[:, :k]
+    b = (torch.randn(n, k, generator=g) * 0.05).half().cuda()
+    out_full = torch.full((m, n + ldo_pad), float("nan"), dtype=torch.float16, device="cuda")
+    out = out_full[:, :n]
+    ws = torch.empty(_ops.gemm_splitk_workspace_bytes(m, n, k), dtype=torch.uint8, device="cuda")
+    torch.ops.talm.gemm_splitk(a, b, out, ws)
+    ref = a.float() @ b.float().t()
+    _close(out, ref, k)
+    again = torch.empty_like(out)
+    torch.ops.talm.gemm_splitk(a, b, again, ws)
+    assert torch.equal(again, out)
+    if ldo_pad:
+        assert torch.isnan(out_full[:, n:].float()).all(), "columns past n were written"
+
+
+def test_gemm_splitk_rejects_bad_shapes():
+    from talm_amd import _ops
+
+    a = torch.zeros(4, 12, dtype=torch.float16, device="cuda")  # k not a multiple of 8
+    b = torch.zeros(8, 12, dtype=torch.float16, device="cuda")
+    out = torch.empty(4, 8, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        _ops.gemm_splitk_workspace_bytes(4, 8, 12)
+    with pytest.raises(ValueError):
+        torch.ops.talm.gemm_splitk(a, b, out, torch.empty(1 << 16, dtype=torch.uint8,
+                                                          device="cuda"))
