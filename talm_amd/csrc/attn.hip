@@ -135,6 +135,36 @@ __device__ __forceinline__ half8_t read_tr_operand(const unsigned char* tile, in
   return __builtin_bit_cast(half8_t, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// The same operand's two halves issued as inline assembly. The compiler does not track these
+// reads: it adds no wait for the direct-to-LDS loads in flight before them (it cannot tell that
+// those write the other ring slot, and would wait for all of them), and the caller waits for the
+// results itself with lgkm_wait8 before using them.
+__device__ __forceinline__ half4_t read_tr_untracked(const unsigned char* lds) {
+  const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const unsigned char*)(lds)));
+  half4_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+__device__ __forceinline__ void read_tr_operand_untracked(const unsigned char* tile, int row0,
+                                                          int col0, int lane, half4_t& lo,
+                                                          half4_t& hi) {
+  const int g = lane >> 4, i = lane & 15, hh = g >> 1;
+  const int col = col0 + 16 * (g & 1) + 4 * (i & 3);
+  const int row = row0 + 4 * hh + (i >> 2);
+  lo = read_tr_untracked(tile + tile_chunk(row, col >> 3) * 16 + (col & 7) * 2);
+  hi = read_tr_untracked(tile + tile_chunk(row + 8, col >> 3) * 16 + (col & 7) * 2);
+}
+// Wait until at most N LDS / scalar-memory operations of the wavefront are outstanding; the
+// eight registers count as rewritten here, so no copy of them is made before the wait.
+template <int N>
+__device__ __forceinline__ void lgkm_wait8(half4_t (&r)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                 "+v"(r[6]), "+v"(r[7])
+               : "n"(N));
+}
+
 // One [64][128] tile from global rows base[r * ld + c] (r < rows_valid, else zeros) into `dst`
 // with direct-to-LDS 16-byte loads: block b (rows 4 b .. 4 b + 3) by wavefront b % W.
 template <int W>
@@ -302,6 +332,14 @@ __global__ __launch_bounds__(64 * W * S) void attn_fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[j][v] *= alpha;
     }
+    // V^T operands of the four 16-key groups (b, h), read untracked two groups at a time
+    half4_t vt[2][8];
+    auto read_v = [&](int grp16, int buf) {
+#pragma unroll
+      for (int j = 0; j < kD / 32; ++j)
+        read_tr_operand_untracked(vs, 16 * grp16, 32 * j, lane, vt[buf][2 * j], vt[buf][2 * j + 1]);
+    };
+    read_v(0, 0);
     float ps = 0.f;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
@@ -314,17 +352,24 @@ __global__ __launch_bounds__(64 * W * S) void attn_fwd_kernel(FwdArgs a) {
     lsum += ps;
     // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per step in the accumulator's key order
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        half8_t pb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(st[b][8 * h + e]);
-#pragma unroll
-        for (int j = 0; j < kD / 32; ++j)
-          o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-              read_tr_operand(vs, 32 * b + 16 * h, 32 * j, lane), pb, o[j], 0, 0, 0);
+    for (int g16 = 0; g16 < 4; ++g16) {
+      const int b = g16 >> 1, h = g16 & 1, buf = g16 & 1;
+      if (g16 < 3) {
+        read_v(g16 + 1, buf ^ 1);
+        lgkm_wait8<8>(vt[buf]);  // group g16's reads have returned (the next group's may not)
+      } else {
+        lgkm_wait8<0>(vt[buf]);
       }
+      half8_t pb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(st[b][8 * h + e]);
+#pragma unroll
+      for (int j = 0; j < kD / 32; ++j)
+        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(half8_t, __builtin_shufflevector(vt[buf][2 * j], vt[buf][2 * j + 1],
+                                                                0, 1, 2, 3, 4, 5, 6, 7)),
+            pb, o[j], 0, 0, 0);
+    }
   }
   lsum += __shfl_xor(lsum, 32, kWave);  // the row's sum over both halves of the lanes
 
@@ -454,7 +499,7 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
   KeyTile* vs = reinterpret_cast<KeyTile*>(smem + 2 * sizeof(KeyTile));    // V [key][d]
   KeyTileT* kts = reinterpret_cast<KeyTileT*>(smem + 4 * sizeof(KeyTile)); // K^T [d][key]
 
-  const int seq = blockIdx.z, head = blockIdx.y;
+  const int seq = blockIdx.y, head = blockIdx.x;
   const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
   const int q0 = tile * kRows;
   if (q0 >= len) return;
@@ -599,7 +644,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
   RowStat* ls = reinterpret_cast<RowStat*>(p);   p += 2 * sizeof(RowStat);    // lse2 of the rows
   RowStat* dds = reinterpret_cast<RowStat*>(p);                               // Dd of the rows
 
-  const int seq = blockIdx.z, head = blockIdx.y;
+  const int seq = blockIdx.y, head = blockIdx.x;
   const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
   const int k0 = tile * kCols;
   if (k0 >= len) return;
@@ -748,16 +793,21 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
 
 // dQ and the dK / dV partials in one launch: they read the same inputs and write disjoint
 // outputs, and each alone has fewer workgroups than the chip has CUs (its time is its longest
-// workgroup's), so side by side they share the chip. Even blockIdx.x: query tile of dQ, longest
-// (last) first; odd: key tile of dK / dV, longest (first) first.
+// workgroup's), so side by side they share the chip. The grid is (query head, sequence,
+// 2 x rank): every sequence's longest work is dispatched first, rank by rank, so the workgroups
+// that wait for a free CU are the shortest ones. Rank r of a sequence of n tiles is dQ query tile
+// n - 1 - r (even z) and dK / dV key tile r (odd z); ranks past n exit at once.
 template <int W>
 __global__ __launch_bounds__(64 * W, 1) void attn_bwd_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[kBwdLds];
-  const int bx = static_cast<int>(blockIdx.x) >> 1;
-  if ((blockIdx.x & 1) == 0)
-    attn_bwd_dq<W>(a, a.n_tiles - 1 - bx, smem);
+  const int rank = static_cast<int>(blockIdx.z) >> 1;
+  const int len = a.cu[blockIdx.y + 1] - a.cu[blockIdx.y];
+  const int n_own = (len + 32 * W - 1) / (32 * W);
+  if (rank >= n_own) return;  // the whole workgroup, before any barrier
+  if ((blockIdx.z & 1) == 0)
+    attn_bwd_dq<W>(a, n_own - 1 - rank, smem);
   else
-    attn_bwd_dkdv<W>(a, bx, smem);
+    attn_bwd_dkdv<W>(a, rank, smem);
 }
 
 // dK / dV fp16 [token][kv head][d] = sum over the KV head's query heads, in head order.
@@ -870,6 +920,8 @@ TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
                     dv_stride_head})
     if (s < 0 || s % 8)
       return fail(TALM_EINVAL, "attn_bwd: strides must be non-negative multiples of 8 elements");
+  if (n_seqs > 65535 || (max_seqlen + 127) / 128 > 32767)
+    return fail(TALM_EINVAL, "attn_bwd: at most 65535 sequences of at most 4194176 tokens");
   const int64_t need = talm_attn_bwd_workspace(n_tokens, n_q_heads);
   if (workspace_bytes < need)
     return fail(TALM_EINVAL, "attn_bwd: workspace of %lld bytes, %lld needed",
@@ -904,8 +956,8 @@ TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
   const int64_t rows = n_tokens * n_q_heads;
   hipLaunchKernelGGL(attn_bwd_dot_kernel, dim3(static_cast<unsigned>((rows * 16 + 255) / 256)),
                      dim3(256), 0, s, a);
-  const dim3 grid(static_cast<unsigned>(2 * a.n_tiles), static_cast<unsigned>(n_q_heads),
-                  static_cast<unsigned>(n_seqs));
+  const dim3 grid(static_cast<unsigned>(n_q_heads), static_cast<unsigned>(n_seqs),
+                  static_cast<unsigned>(2 * a.n_tiles));
   hipLaunchKernelGGL((attn_bwd_kernel<W>), grid, dim3(64 * W), 0, s, a);
   const int64_t red = n_tokens * n_kv_heads * (kD / 4);
   hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3(static_cast<unsigned>((red + 255) / 256)),
