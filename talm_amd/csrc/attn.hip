@@ -7,26 +7,29 @@
 // reference's per-KV-head memory-efficient attention launches (solution/unpad.py:199-294), whose
 // semantics are per-row causal SDPA (solution/unpad.py:121-134).
 //
-// The forward is a flash-attention pass per (sequence, query head, 128-row query tile): four
-// wavefronts of 32 query rows, key tiles of 64 through a double-buffered LDS ring. Scores are
-// computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16), so each lane owns one query row
-// (its accumulator column): the online max / sum and the output rescale are per-lane scalars.
-// The exponentiated scores are already in the B-operand layout of O^T = V^T P^T: the reduction
-// over keys takes the accumulator's key order as its k-slot order, and V^T is read in that same
-// order from a transposed LDS copy of the V tile. The row statistics are kept in base 2
-// (scores times scale * log2 e); lse is written in natural-log units, [Hq, N].
+// The forward is a flash-attention pass per (sequence, 32-row query tile, query heads of one KV
+// head), its key tiles of 64 split between two groups of wavefronts and streamed with
+// direct-to-LDS loads. Scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16), so
+// each lane owns one query row (its accumulator column): the online max / sum and the output
+// rescale are per-lane scalars. The exponentiated scores are already in the B-operand layout of
+// O^T = V^T P^T: the reduction over keys takes the accumulator's key order as its k-slot order,
+// and V^T is read in that same order from the row-major V tile with transposing LDS reads. The
+// row statistics are kept in base 2 (scores times scale * log2 e); lse is written in natural-log
+// units, [Hq, N].
 //
 // The backward (FlashAttention-2's recurrences: P = exp(S - lse), dV = P^T dO, dP = dO V^T,
 // dS = P (dP - rowsum(dO O)), dQ = scale dS K, dK = scale dS^T Q) runs as
 //   attn_bwd_dot    Dd[h][t] = sum_d dO O (fp32);
 //   attn_bwd_dq     per (sequence, query head, 128-row query tile): the forward's loop with
-//                   dP^T = V dO^T next to S^T, and dQ^T += K^T dS^T from a transposed K tile;
+//                   dP^T = V dO^T next to S^T, and dQ^T += K^T dS^T with K^T read transposed
+//                   from the K tile;
 //   attn_bwd_dkdv   per (sequence, query head, 128-key tile): each lane owns a key (S and dP
 //                   computed untransposed, so keys are accumulator columns), looping over
-//                   32-row query tiles: dV^T += dO^T P and dK^T += Q^T dS from transposed
-//                   Q / dO tiles; fp32 partials per query head;
+//                   64-row query tiles: dV^T += dO^T P and dK^T += Q^T dS with Q^T and dO^T read
+//                   transposed from the row-major tiles; fp32 partials per query head;
 //   attn_bwd_reduce the partials of a KV head's query heads summed in head order (deterministic)
 //                   into dK, dV fp16.
+// The dQ and dK / dV bodies run in one launch.
 #include "mfma_tile.h"
 
 namespace talm {
@@ -40,41 +43,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kD = 128;         // head dim
 constexpr int kKeys = 64;       // keys per tile
 constexpr int kKS = kD + 8;     // row stride (halfs) of a [keys][D] tile in LDS
-constexpr int kVS = kKeys + 4;  // row stride (halfs) of a transposed [D][keys] tile in LDS
-constexpr int kQT = 32;           // query rows per step of the dK / dV loop
-constexpr int kQS = kQT + 4;      // row stride (halfs) of a transposed [D][queries] tile
 constexpr float kLn2 = 0.693147180559945309f;
 
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// The tile loop of every kernel below: n tiles through registers into a two-slot LDS ring, the
-// global loads two tiles ahead of the tile being computed (register slot = LDS slot = tile & 1,
-// unrolled by two so both stay static). load(slot, tile) fills a slot's registers,
-// store(slot) writes them to that LDS slot, compute(tile, slot) consumes it. The loads are
-// unconditional (clamped to the last tile): a conditional one makes the compiler wait for it.
-// The barrier only waits for LDS (lgkmcnt): the loads stay in flight across it.
-template <class Load, class Store, class Compute>
-__device__ __forceinline__ void tile_pipeline(int n, Load&& load, Store&& store,
-                                              Compute&& compute) {
-  load(0, 0);
-  load(1, min(1, n - 1));
-  int t = 0;
-  for (; t + 1 < n; t += 2) {
-    store(0);
-    load(0, min(t + 2, n - 1));
-    __syncthreads();
-    compute(t, 0);
-    store(1);
-    load(1, min(t + 3, n - 1));
-    __syncthreads();
-    compute(t + 1, 1);
-  }
-  if (t < n) {
-    store(0);
-    __syncthreads();
-    compute(t, 0);
-  }
-}
 
 struct FwdArgs {
   const uint16_t* q;
@@ -96,14 +67,16 @@ struct FwdArgs {
 
 // K and V tiles of the forward in LDS: [64 keys][128 d] fp16 without padding, 16 chunks of 16
 // bytes per row, chunk c of row r at position c ^ tile_swz(r). The direct-to-LDS loads write
-// 1 KiB per wavefront instruction contiguously (4 rows); the swizzle makes both reads free of
-// bank conflicts: the 16-byte row reads of the S = K Q^T operand (8 consecutive rows of one
-// chunk per LDS cycle: tile_swz takes 8 distinct values on them) and the transposing 8-byte
-// reads of the P V operand (4 rows x 2 adjacent chunks per 16 lanes: the pair positions
-// (c / 2) ^ (r & 3) are distinct).
+// 1 KiB per wavefront instruction contiguously (4 rows). gfx950's LDS serves a 16-byte read in
+// phases of 16 lanes over 64 four-byte banks (measured with the SQ_LDS_BANK_CONFLICT counter), so
+// a 256-byte row spans every bank once and a chunk's banks depend on its position alone. The
+// 4-bit key makes both reads conflict-free: the 16-byte row reads of the S = K Q^T operand
+// (16 consecutive rows of one chunk per phase: the key takes 16 distinct values on them) and the
+// transposing 8-byte reads (4 consecutive rows x 4 adjacent chunks per 32-lane phase: with
+// r = 4a + t and c = 4b + u the position is 4 (b ^ t) + (u ^ a % 4), 16 distinct values).
 constexpr int kTileBytes = kKeys * kD * 2;  // 16 KiB
 
-__device__ __forceinline__ int tile_swz(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+__device__ __forceinline__ int tile_swz(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
 __device__ __forceinline__ int tile_chunk(int row, int chunk) { return row * 16 + (chunk ^ tile_swz(row)); }
 
 // ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane i receives element e (0..3) from
@@ -111,30 +84,10 @@ __device__ __forceinline__ int tile_chunk(int row, int chunk) { return row * 16 
 // i % 4 (checked on the GPU with an in-bounds probe). With lane j pointing at row K0 + j / 4,
 // columns D0 + 4 (j % 4) of a row-major [keys][d] tile, lane i gets keys K0 .. K0 + 3 of column
 // D0 + i: the transpose of 4 x 16 elements.
-typedef short short4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ half4_t read_tr(const unsigned char* lds) {
-  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) short4_t*)(lds));
-  return __builtin_bit_cast(half4_t, v);
-}
-
 // A 32 x 16 operand of v_mfma_f32_32x32x16_f16 read transposed from a swizzled [rows][128]
 // tile: A[m][k] = tile[row0 + key(k)][col0 + m], lane l holding m = l % 32 and k-slots
 // 8 (l / 32) .. + 7, whose rows follow the accumulator order of the 32-row blocks: slots
 // 8 hh + e hold rows row0 + 4 hh + e (e < 4) and row0 + 8 + 4 hh + e - 4 (e >= 4).
-__device__ __forceinline__ half8_t read_tr_operand(const unsigned char* tile, int row0, int col0,
-                                                   int lane) {
-  const int g = lane >> 4, i = lane & 15, hh = g >> 1;
-  const int col = col0 + 16 * (g & 1) + 4 * (i & 3);
-  half4_t part[2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const int row = row0 + 8 * r + 4 * hh + (i >> 2);
-    part[r] = read_tr(tile + tile_chunk(row, col >> 3) * 16 + (col & 7) * 2);
-  }
-  return __builtin_bit_cast(half8_t, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
 // The same operand's two halves issued as inline assembly. The compiler does not track these
 // reads: it adds no wait for the direct-to-LDS loads in flight before them (it cannot tell that
 // those write the other ring slot, and would wait for all of them), and the caller waits for the
@@ -155,14 +108,23 @@ __device__ __forceinline__ void read_tr_operand_untracked(const unsigned char* t
   lo = read_tr_untracked(tile + tile_chunk(row, col >> 3) * 16 + (col & 7) * 2);
   hi = read_tr_untracked(tile + tile_chunk(row + 8, col >> 3) * 16 + (col & 7) * 2);
 }
-// Wait until at most N LDS / scalar-memory operations of the wavefront are outstanding; the
-// eight registers count as rewritten here, so no copy of them is made before the wait.
-template <int N>
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4_t read_f4_untracked(const float* lds) {
+  const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const float*)(lds)));
+  f32x4_t r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+__device__ __forceinline__ void lgkm_wait_f4(f32x4_t (&r)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]));
+}
+// Wait until every LDS (and scalar-memory) operation of the wavefront has returned; the eight
+// registers count as rewritten here, so no copy of them is made before the wait.
 __device__ __forceinline__ void lgkm_wait8(half4_t (&r)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(%8)"
+  asm volatile("s_waitcnt lgkmcnt(0)"
                : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
-                 "+v"(r[6]), "+v"(r[7])
-               : "n"(N));
+                 "+v"(r[6]), "+v"(r[7]));
 }
 
 // One [64][128] tile from global rows base[r * ld + c] (r < rows_valid, else zeros) into `dst`
@@ -180,26 +142,6 @@ __device__ __forceinline__ void dma_tile(const uint16_t* base, int64_t ld, int r
     const int chunk = pos ^ tile_swz(row);
     const uint32_t off = row < rows_valid ? static_cast<uint32_t>((row * ld + chunk * 8) * 2) : kOob;
     dma16(rsrc, dst + b * 1024, off);
-  }
-}
-
-// wait_vmcnt with a count known at run time (at most 16)
-__device__ __forceinline__ void wait_vmcnt_dyn(int n) {
-  switch (n) {
-    case 0: wait_vmcnt<0>(); break;
-    case 1: wait_vmcnt<1>(); break;
-    case 2: wait_vmcnt<2>(); break;
-    case 3: wait_vmcnt<3>(); break;
-    case 4: wait_vmcnt<4>(); break;
-    case 5: wait_vmcnt<5>(); break;
-    case 6: wait_vmcnt<6>(); break;
-    case 7: wait_vmcnt<7>(); break;
-    case 8: wait_vmcnt<8>(); break;
-    case 10: wait_vmcnt<10>(); break;
-    case 12: wait_vmcnt<12>(); break;
-    case 14: wait_vmcnt<14>(); break;
-    case 16: wait_vmcnt<16>(); break;
-    default: wait_vmcnt<0>(); break;
   }
 }
 
@@ -354,12 +296,8 @@ __global__ __launch_bounds__(64 * W * S) void attn_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int g16 = 0; g16 < 4; ++g16) {
       const int b = g16 >> 1, h = g16 & 1, buf = g16 & 1;
-      if (g16 < 3) {
-        read_v(g16 + 1, buf ^ 1);
-        lgkm_wait8<8>(vt[buf]);  // group g16's reads have returned (the next group's may not)
-      } else {
-        lgkm_wait8<0>(vt[buf]);
-      }
+      lgkm_wait8(vt[buf]);  // group g16's reads have returned
+      if (g16 < 3) read_v(g16 + 1, buf ^ 1);  // the next group's fly during these MFMAs
       half8_t pb;
 #pragma unroll
       for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(st[b][8 * h + e]);
@@ -482,28 +420,46 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(BwdArgs a) {
   if (sub == 0 && row < rows) a.dd[static_cast<int64_t>(h) * a.n_tokens + t] = acc;
 }
 
-// LDS of the dQ and dK / dV bodies: both run in one launch (attn_bwd_kernel) and carve one
-// buffer, so the launch needs the larger of the two.
-constexpr int kDqLds = 2 * (2 * kKeys * kKS + kD * kVS) * 2;
-constexpr int kDkdvLds = 2 * (2 * kQT * kKS + 2 * kD * kQS) * 2 + 2 * 2 * kQT * 4;
-constexpr int kBwdLds = kDqLds > kDkdvLds ? kDqLds : kDkdvLds;
+// The dQ and dK / dV bodies below stream their tiles with the forward's direct-to-LDS loads into
+// the swizzled [64][128] layout (tile_chunk): 16-byte row reads give the operands taken row by
+// row, and the transposing reads (read_tr_operand_untracked) give K^T, Q^T and dO^T straight
+// from the same tiles, so no transposed copy is written. A two-slot ring, one tile ahead; the
+// loop is unrolled by two so every slot address is a compile-time offset.
+constexpr int kBwdSlot = 2 * kTileBytes + 2048;  // two tiles (+ per-wavefront lse / Dd rows: dK / dV)
+constexpr int kBwdLds = 2 * kBwdSlot;
 
-// dQ: the forward's structure, one query row per lane; `tile` is the query tile.
+// Runs body(tile, slot) for tile = 0 .. n - 1 in ring slot tile & 1, after issue(tile + 1, slot)
+// put the next tile in flight into the other slot. Each tile's loads are waited for (this
+// wavefront's, then the barrier for everyone's) right before its body, and the barrier also
+// retires the slot the previous body read. Unrolled by two, so every slot address is a
+// compile-time offset. (A third slot, two tiles in flight, measured slower.)
+template <class Issue, class Body>
+__device__ __forceinline__ void ring2(int n, Issue&& issue, Body&& body) {
+  issue(0, 0);
+  for (int t = 0; t < n; t += 2) {
+    wait_vmcnt<0>();
+    lds_barrier();
+    if (t + 1 < n) issue(t + 1, 1);
+    body(t, 0);
+    if (t + 1 >= n) break;
+    wait_vmcnt<0>();
+    lds_barrier();
+    if (t + 2 < n) issue(t + 2, 0);
+    body(t + 1, 1);
+  }
+}
+
+// dQ: the forward's structure, one query row per lane (S^T = K Q^T, dP^T = V dO^T, then
+// dQ^T += K^T dS^T with K^T read transposed from the K tile); `tile` is the 32W-row query tile.
 template <int W>
 __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned char* smem) {
   constexpr int kRows = 32 * W;
-  constexpr int kPer = kKeys * (kD / 8) / (64 * W);
-  typedef uint16_t KeyTile[kKeys * kKS];
-  typedef uint16_t KeyTileT[kD * kVS];
-  KeyTile* ks = reinterpret_cast<KeyTile*>(smem);                          // K [key][d]
-  KeyTile* vs = reinterpret_cast<KeyTile*>(smem + 2 * sizeof(KeyTile));    // V [key][d]
-  KeyTileT* kts = reinterpret_cast<KeyTileT*>(smem + 4 * sizeof(KeyTile)); // K^T [d][key]
-
   const int seq = blockIdx.y, head = blockIdx.x;
   const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
   const int q0 = tile * kRows;
   if (q0 >= len) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5, l32 = lane & 31;
   const int kvh = head / a.group;
   const int qrow = q0 + 32 * wave + l32;
@@ -520,33 +476,18 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
   }
   const float lse2 = a.lse[static_cast<int64_t>(head) * a.n_tokens + s0 + qr] * 1.44269504088896341f;
   const float ddr = a.dd[static_cast<int64_t>(head) * a.n_tokens + s0 + qr];
+  const int wq0 = q0 + 32 * wave;  // the wavefront's first query row
 
   const int kend = min(len, q0 + kRows);
   const int n_kt = (kend + kKeys - 1) / kKeys;
   const uint16_t* kbase = a.k + static_cast<int64_t>(s0) * a.k_tok + kvh * a.k_head;
   const uint16_t* vbase = a.v + static_cast<int64_t>(s0) * a.v_tok + kvh * a.v_head;
-  u32x4 kreg[2][kPer], vreg[2][kPer];
-  auto load_tile = [&](int slot, int kt) {
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int c = p * 64 * W + tid, key = min(kt * kKeys + (c & 63), len - 1), cc = c >> 6;
-      kreg[slot][p] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(key) * a.k_tok + 8 * cc);
-      vreg[slot][p] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(key) * a.v_tok + 8 * cc);
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int c = p * 64 * W + tid, key = c & 63, cc = c >> 6;
-      *reinterpret_cast<u32x4*>(&ks[buf][key * kKS + 8 * cc]) = kreg[buf][p];
-      *reinterpret_cast<u32x4*>(&vs[buf][key * kKS + 8 * cc]) = vreg[buf][p];
-      const uint32_t w4[4] = {kreg[buf][p].x, kreg[buf][p].y, kreg[buf][p].z, kreg[buf][p].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kts[buf][(8 * cc + 2 * e) * kVS + key] = static_cast<uint16_t>(w4[e] & 0xffffu);
-        kts[buf][(8 * cc + 2 * e + 1) * kVS + key] = static_cast<uint16_t>(w4[e] >> 16);
-      }
-    }
+  auto issue = [&](int kt, int slot) {
+    unsigned char* dst = smem + slot * kBwdSlot;
+    const int r0 = kt * kKeys;
+    dma_tile<W>(kbase + static_cast<int64_t>(r0) * a.k_tok, a.k_tok, len - r0, dst, wave, lane);
+    dma_tile<W>(vbase + static_cast<int64_t>(r0) * a.v_tok, a.v_tok, len - r0, dst + kTileBytes,
+                wave, lane);
   };
 
   f32x16 acc[kD / 32];
@@ -555,56 +496,75 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
 
-  auto compute = [&](int kt, int buf) {
+  auto body = [&](int kt, int slot) {
+    const unsigned char* ks = smem + slot * kBwdSlot;
+    const uint4* k16 = reinterpret_cast<const uint4*>(ks);
+    const uint4* v16 = reinterpret_cast<const uint4*>(ks + kTileBytes);
     const int k0 = kt * kKeys;
+    if (k0 > wq0 + 31) return;  // every key of the tile is after every row of the wavefront
     f32x16 st[2], dpt[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) st[b][v] = dpt[b][v] = 0.f;
-      const uint16_t* kr = &ks[buf][(32 * b + l32) * kKS + 8 * hh];
-      const uint16_t* vr = &vs[buf][(32 * b + l32) * kKS + 8 * hh];
 #pragma unroll
       for (int s = 0; s < kD / 16; ++s) {
         st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            *reinterpret_cast<const half8_t*>(kr + 16 * s), qf[s], st[b], 0, 0, 0);
+            __builtin_bit_cast(half8_t, k16[tile_chunk(32 * b + l32, 2 * s + hh)]), qf[s], st[b],
+            0, 0, 0);
         dpt[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            *reinterpret_cast<const half8_t*>(vr + 16 * s), df[s], dpt[b], 0, 0, 0);
+            __builtin_bit_cast(half8_t, v16[tile_chunk(32 * b + l32, 2 * s + hh)]), df[s],
+            dpt[b], 0, 0, 0);
       }
     }
-    // dS^T = P^T (dP^T - Dd), P^T = exp2(S^T scale log2e - lse2), 0 where masked
+    // K^T operands of the first 16-key group, read while the scores are turned into dS^T
+    half4_t kt_[2][8];
+    auto read_k = [&](int g16, int buf) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+      for (int j = 0; j < kD / 32; ++j)
+        read_tr_operand_untracked(ks, 16 * g16, 32 * j, lane, kt_[buf][2 * j], kt_[buf][2 * j + 1]);
+    };
+    read_k(0, 0);
+    // dS^T = P^T (dP^T - Dd), P^T = exp2(S^T scale log2e - lse2); 0 where masked (only on a tile
+    // that reaches past the wavefront's first row or past the sequence: a uniform branch)
+    if (k0 + kKeys - 1 > wq0 || k0 + kKeys > len) {
+      asm volatile("");
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int key = k0 + 32 * b + 8 * (v >> 2) + 4 * hh + (v & 3);
-        const float p = (key <= qrow && key < len) ? exp2_(st[b][v] * a.scale_log2 - lse2) : 0.f;
-        st[b][v] = p * (dpt[b][v] - ddr);
-      }
-    // dQ^T[d][q] += K^T[d][key] dS^T[key][q]
+      for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        half8_t sb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sb[e] = static_cast<_Float16>(st[b][8 * h + e]);
-        const int kb = 32 * b + 16 * h + 4 * hh;
-#pragma unroll
-        for (int j = 0; j < kD / 32; ++j) {
-          const uint16_t* kr = &kts[buf][(32 * j + l32) * kVS + kb];
-          const half4_t lo = *reinterpret_cast<const half4_t*>(kr);
-          const half4_t hi = *reinterpret_cast<const half4_t*>(kr + 8);
-          const half8_t ka = __builtin_bit_cast(
-              half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, sb, acc[j], 0, 0, 0);
+        for (int v = 0; v < 16; ++v) {
+          const int key = k0 + 32 * b + 8 * (v >> 2) + 4 * hh + (v & 3);
+          const float p = (key <= qrow && key < len) ? exp2_(st[b][v] * a.scale_log2 - lse2) : 0.f;
+          st[b][v] = p * (dpt[b][v] - ddr);
         }
-      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          st[b][v] = exp2_(st[b][v] * a.scale_log2 - lse2) * (dpt[b][v] - ddr);
+    }
+    // dQ^T[d][q] += K^T[d][key] dS^T[key][q], 16 keys per step in the accumulator's key order
+#pragma unroll
+    for (int g16 = 0; g16 < 4; ++g16) {
+      const int b = g16 >> 1, h = g16 & 1, buf = g16 & 1;
+      lgkm_wait8(kt_[buf]);
+      if (g16 < 3) read_k(g16 + 1, buf ^ 1);
+      half8_t sb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sb[e] = static_cast<_Float16>(st[b][8 * h + e]);
+#pragma unroll
+      for (int j = 0; j < kD / 32; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(half8_t, __builtin_shufflevector(kt_[buf][2 * j], kt_[buf][2 * j + 1],
+                                                                0, 1, 2, 3, 4, 5, 6, 7)),
+            sb, acc[j], 0, 0, 0);
+    }
   };
-  tile_pipeline(n_kt, load_tile, store_tile, compute);
+  ring2(n_kt, issue, body);
 
-  __syncthreads();
-  uint16_t* os = &ks[0][0] + wave * 32 * kKS;
+  __syncthreads();  // every wavefront is done with the ring: it becomes the output staging
+  uint16_t* os = reinterpret_cast<uint16_t*>(smem) + wave * 32 * kKS;
 #pragma unroll
   for (int j = 0; j < kD / 32; ++j)
 #pragma unroll
@@ -615,7 +575,8 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
       w.y = pack2(acc[j][4 * g + 2] * a.scale, acc[j][4 * g + 3] * a.scale);
       *reinterpret_cast<uint2*>(&os[l32 * kKS + d0]) = w;
     }
-  __syncthreads();
+  // the wavefront reads back its own staging rows: its LDS writes complete first
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
   for (int it = 0; it < (32 * kD / 8) / 64; ++it) {
     const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
@@ -626,33 +587,25 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
   }
 }
 
-// dK / dV partials of one query head: each lane owns one key of the workgroup's 32W keys.
-
-// dK / dV partials of one query head; `tile` is the key tile.
+// dK / dV partials of one query head; `tile` is the 32W-key tile, each lane owns one key (S and
+// dP untransposed: keys are accumulator columns), looping over 64-row query tiles: dV^T += dO^T P
+// and dK^T += Q^T dS with Q^T and dO^T read transposed from the row-major tiles. Each slot holds
+// the Q tile, the dO tile, then each wavefront's copy of the tile's 64 lse and 64 Dd values.
 template <int W>
 __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsigned char* smem) {
-  constexpr int kCols = 32 * W;                       // keys per workgroup
-  constexpr int kPer = kQT * (kD / 8) / (64 * W);     // 16-byte chunks of a Q / dO tile per thread
-  typedef uint16_t RowTile[kQT * kKS];
-  typedef uint16_t RowTileT[kD * kQS];
-  typedef float RowStat[kQT];
-  unsigned char* p = smem;
-  RowTile* qs = reinterpret_cast<RowTile*>(p);   p += 2 * sizeof(RowTile);    // Q [q][d]
-  RowTile* ds = reinterpret_cast<RowTile*>(p);   p += 2 * sizeof(RowTile);    // dO [q][d]
-  RowTileT* qts = reinterpret_cast<RowTileT*>(p); p += 2 * sizeof(RowTileT);  // Q^T [d][q]
-  RowTileT* dts = reinterpret_cast<RowTileT*>(p); p += 2 * sizeof(RowTileT);  // dO^T [d][q]
-  RowStat* ls = reinterpret_cast<RowStat*>(p);   p += 2 * sizeof(RowStat);    // lse2 of the rows
-  RowStat* dds = reinterpret_cast<RowStat*>(p);                               // Dd of the rows
-
+  constexpr int kCols = 32 * W;  // keys per workgroup
+  constexpr int kRowsT = kKeys;  // query rows per tile
   const int seq = blockIdx.y, head = blockIdx.x;
   const int s0 = a.cu[seq], len = a.cu[seq + 1] - s0;
   const int k0 = tile * kCols;
   if (k0 >= len) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5, l32 = lane & 31;
   const int kvh = head / a.group;
   const int key = k0 + 32 * wave + l32;
   const int kr_ = min(key, len - 1);
+  const int wk0 = k0 + 32 * wave;  // the wavefront's first key
   half8_t kf[kD / 16], vf[kD / 16];
   {
     const uint16_t* kp = a.k + static_cast<int64_t>(s0 + kr_) * a.k_tok + kvh * a.k_head + 8 * hh;
@@ -663,47 +616,26 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
       vf[s] = *reinterpret_cast<const half8_t*>(vp + 16 * s);
     }
   }
-  const int qstart = (k0 / kQT) * kQT;                 // causal: rows below k0 see no key here
-  const int n_qt = (len - qstart + kQT - 1) / kQT;
+  const int qstart = k0;  // causal: rows below k0 see no key here (k0 is a multiple of 64)
+  const int n_qt = (len - qstart + kRowsT - 1) / kRowsT;
   const uint16_t* qbase = a.q + static_cast<int64_t>(s0) * a.q_tok + head * a.q_head;
   const uint16_t* dbase = a.dout + static_cast<int64_t>(s0) * a.do_tok + head * a.do_head;
-  const float* lrow = a.lse + static_cast<int64_t>(head) * a.n_tokens + s0;
-  const float* drow = a.dd + static_cast<int64_t>(head) * a.n_tokens + s0;
-  // chunk c = p * 64W + tid -> query row c % 32, column chunk c / 32
-  u32x4 qreg[2][kPer], dreg[2][kPer];
-  float lreg[2], dreg1[2];
-  auto load_tile = [&](int slot, int qt) {
-    const int r0 = qstart + qt * kQT;
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int c = p * 64 * W + tid, row = min(r0 + (c & 31), len - 1), cc = c >> 5;
-      qreg[slot][p] = *reinterpret_cast<const u32x4*>(qbase + static_cast<int64_t>(row) * a.q_tok + 8 * cc);
-      dreg[slot][p] = *reinterpret_cast<const u32x4*>(dbase + static_cast<int64_t>(row) * a.do_tok + 8 * cc);
-    }
-    const int row = min(r0 + (tid & (kQT - 1)), len - 1);  // every thread: no branch
-    lreg[slot] = lrow[row] * 1.44269504088896341f;
-    dreg1[slot] = drow[row];
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      const int c = p * 64 * W + tid, row = c & 31, cc = c >> 5;
-      *reinterpret_cast<u32x4*>(&qs[buf][row * kKS + 8 * cc]) = qreg[buf][p];
-      *reinterpret_cast<u32x4*>(&ds[buf][row * kKS + 8 * cc]) = dreg[buf][p];
-      const uint32_t q4[4] = {qreg[buf][p].x, qreg[buf][p].y, qreg[buf][p].z, qreg[buf][p].w};
-      const uint32_t d4[4] = {dreg[buf][p].x, dreg[buf][p].y, dreg[buf][p].z, dreg[buf][p].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qts[buf][(8 * cc + 2 * e) * kQS + row] = static_cast<uint16_t>(q4[e] & 0xffffu);
-        qts[buf][(8 * cc + 2 * e + 1) * kQS + row] = static_cast<uint16_t>(q4[e] >> 16);
-        dts[buf][(8 * cc + 2 * e) * kQS + row] = static_cast<uint16_t>(d4[e] & 0xffffu);
-        dts[buf][(8 * cc + 2 * e + 1) * kQS + row] = static_cast<uint16_t>(d4[e] >> 16);
-      }
-    }
-    if (tid < kQT) {
-      ls[buf][tid] = lreg[buf];
-      dds[buf][tid] = dreg1[buf];
-    }
+  const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.lse + static_cast<int64_t>(head) * a.n_tokens + s0), 0, len * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
+      a.dd + static_cast<int64_t>(head) * a.n_tokens + s0, 0, len * 4, 0x00020000);
+  auto issue = [&](int qt, int slot) {
+    unsigned char* dst = smem + slot * kBwdSlot;
+    const int r0 = qstart + qt * kRowsT;
+    dma_tile<W>(qbase + static_cast<int64_t>(r0) * a.q_tok, a.q_tok, len - r0, dst, wave, lane);
+    dma_tile<W>(dbase + static_cast<int64_t>(r0) * a.do_tok, a.do_tok, len - r0, dst + kTileBytes,
+                wave, lane);
+    // the tile's 64 lse and 64 Dd values, one 4-byte load per lane (rows past len read 0), into
+    // this wavefront's own copy (read by it alone)
+    const uint32_t off = static_cast<uint32_t>((r0 + lane) * 4);
+    unsigned char* st = dst + 2 * kTileBytes + wave * 512;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (lds_ptr_t)(st), 4, off, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(drs, (lds_ptr_t)(st + 256), 4, off, 0, 0, 0);
   };
 
   f32x16 dka[kD / 32], dva[kD / 32];
@@ -712,66 +644,92 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
 #pragma unroll
     for (int v = 0; v < 16; ++v) dka[j][v] = dva[j][v] = 0.f;
 
-  auto compute = [&](int qt, int buf) {
-    const int r0 = qstart + qt * kQT;
-    // S[q][key], dP[q][key]: rows q = 8 (v / 4) + 4 hh + v % 4 of the tile, column = this key
-    f32x16 sc, dp;
+  auto body = [&](int qt, int slot) {
+    const unsigned char* qs = smem + slot * kBwdSlot;
+    const unsigned char* ds = qs + kTileBytes;
+    const uint4* q16 = reinterpret_cast<const uint4*>(qs);
+    const uint4* d16 = reinterpret_cast<const uint4*>(ds);
+    const float* ls = reinterpret_cast<const float*>(qs + 2 * kTileBytes + wave * 512);
+    const float* dds = ls + 64;
+    const int r0 = qstart + qt * kRowsT;
+    if (r0 + kRowsT - 1 < wk0) return;  // every row of the tile is before every key of the wavefront
+    // S[q][key], dP[q][key] for the tile's 32-row blocks: rows q = 32 blk + 8 (v / 4) + 4 hh + v % 4
+    f32x16 sc[2], dp[2];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) sc[v] = dp[v] = 0.f;
-    {
-      const uint16_t* qr = &qs[buf][l32 * kKS + 8 * hh];
-      const uint16_t* dr = &ds[buf][l32 * kKS + 8 * hh];
+    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[blk][v] = dp[blk][v] = 0.f;
 #pragma unroll
       for (int s = 0; s < kD / 16; ++s) {
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            *reinterpret_cast<const half8_t*>(qr + 16 * s), kf[s], sc, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            *reinterpret_cast<const half8_t*>(dr + 16 * s), vf[s], dp, 0, 0, 0);
+        sc[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(half8_t, q16[tile_chunk(32 * blk + l32, 2 * s + hh)]), kf[s],
+            sc[blk], 0, 0, 0);
+        dp[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(half8_t, d16[tile_chunk(32 * blk + l32, 2 * s + hh)]), vf[s],
+            dp[blk], 0, 0, 0);
       }
     }
-    // P and dS, 0 where masked (query row < key or past the sequence, key past the sequence)
+    // dO^T and Q^T operands of the first 16-row group, read while P and dS are formed
+    half4_t tr[2][2][8];  // [buf][dO, Q][4 j x 2 halves]
+    auto read_t = [&](int g16, int buf) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int rb = 8 * g + 4 * hh;
-      const float4 l4 = *reinterpret_cast<const float4*>(&ls[buf][rb]);
-      const float4 d4 = *reinterpret_cast<const float4*>(&dds[buf][rb]);
-      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-      const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int v = 4 * g + e, q = r0 + rb + e;
-        const bool valid = q >= key && q < len && key < len;
-        const float p = valid ? exp2_(sc[v] * a.scale_log2 - lv[e]) : 0.f;
-        sc[v] = p;
-        dp[v] = p * (dp[v] - dv[e]);
+      for (int j = 0; j < kD / 32; ++j) {
+        read_tr_operand_untracked(ds, 16 * g16, 32 * j, lane, tr[buf][0][2 * j], tr[buf][0][2 * j + 1]);
+        read_tr_operand_untracked(qs, 16 * g16, 32 * j, lane, tr[buf][1][2 * j], tr[buf][1][2 * j + 1]);
       }
+    };
+    read_t(0, 0);
+    // P and dS, 0 where masked (query row < key or past the sequence, key past the sequence);
+    // the rows' lse and Dd come from the slot with untracked reads as well
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      f32x4_t l4[4], d4[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        l4[g] = read_f4_untracked(&ls[32 * blk + 8 * g + 4 * hh]);
+        d4[g] = read_f4_untracked(&dds[32 * blk + 8 * g + 4 * hh]);
+      }
+      lgkm_wait_f4(l4);
+      lgkm_wait_f4(d4);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * g + e, q = r0 + 32 * blk + 8 * g + 4 * hh + e;
+          const bool valid = q >= key && q < len && key < len;
+          const float p =
+              valid ? exp2_(sc[blk][v] * a.scale_log2 - l4[g][e] * 1.44269504088896341f) : 0.f;
+          sc[blk][v] = p;
+          dp[blk][v] = p * (dp[blk][v] - d4[g][e]);
+        }
     }
     // dV^T[d][key] += dO^T[d][q] P[q][key];  dK^T[d][key] += Q^T[d][q] dS[q][key]
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int g16 = 0; g16 < 4; ++g16) {
+      const int blk = g16 >> 1, h = g16 & 1, buf = g16 & 1;
+      lgkm_wait8(tr[buf][0]);
+      lgkm_wait8(tr[buf][1]);
+      if (g16 < 3) read_t(g16 + 1, buf ^ 1);
       half8_t pb, sb;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        pb[e] = static_cast<_Float16>(sc[8 * h + e]);
-        sb[e] = static_cast<_Float16>(dp[8 * h + e]);
+        pb[e] = static_cast<_Float16>(sc[blk][8 * h + e]);
+        sb[e] = static_cast<_Float16>(dp[blk][8 * h + e]);
       }
-      const int qb = 16 * h + 4 * hh;
 #pragma unroll
       for (int j = 0; j < kD / 32; ++j) {
-        const uint16_t* dr = &dts[buf][(32 * j + l32) * kQS + qb];
-        const uint16_t* qr = &qts[buf][(32 * j + l32) * kQS + qb];
-        const half8_t da = __builtin_bit_cast(half8_t, __builtin_shufflevector(
-            *reinterpret_cast<const half4_t*>(dr), *reinterpret_cast<const half4_t*>(dr + 8),
-            0, 1, 2, 3, 4, 5, 6, 7));
-        const half8_t qa = __builtin_bit_cast(half8_t, __builtin_shufflevector(
-            *reinterpret_cast<const half4_t*>(qr), *reinterpret_cast<const half4_t*>(qr + 8),
-            0, 1, 2, 3, 4, 5, 6, 7));
-        dva[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(da, pb, dva[j], 0, 0, 0);
-        dka[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, sb, dka[j], 0, 0, 0);
+        dva[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(half8_t, __builtin_shufflevector(tr[buf][0][2 * j], tr[buf][0][2 * j + 1],
+                                                                0, 1, 2, 3, 4, 5, 6, 7)),
+            pb, dva[j], 0, 0, 0);
+        dka[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            __builtin_bit_cast(half8_t, __builtin_shufflevector(tr[buf][1][2 * j], tr[buf][1][2 * j + 1],
+                                                                0, 1, 2, 3, 4, 5, 6, 7)),
+            sb, dka[j], 0, 0, 0);
       }
     }
   };
-  tile_pipeline(n_qt, load_tile, store_tile, compute);
+  ring2(n_qt, issue, body);
 
   // fp32 partials [head][token][d]: lane = key column, rows d = 32 j + 8 (v / 4) + 4 hh + v % 4
   if (key < len) {
@@ -799,7 +757,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
 // n - 1 - r (even z) and dK / dV key tile r (odd z); ranks past n exit at once.
 template <int W>
 __global__ __launch_bounds__(64 * W, 1) void attn_bwd_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kBwdLds];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kBwdLds];
   const int rank = static_cast<int>(blockIdx.z) >> 1;
   const int len = a.cu[blockIdx.y + 1] - a.cu[blockIdx.y];
   const int n_own = (len + 32 * W - 1) / (32 * W);
@@ -920,6 +878,9 @@ TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
                     dv_stride_head})
     if (s < 0 || s % 8)
       return fail(TALM_EINVAL, "attn_bwd: strides must be non-negative multiples of 8 elements");
+  if (q_stride_tok >= (int64_t{1} << 23) || k_stride_tok >= (int64_t{1} << 23) ||
+      v_stride_tok >= (int64_t{1} << 23) || do_stride_tok >= (int64_t{1} << 23))
+    return fail(TALM_EINVAL, "attn_bwd: q / k / v / dout token strides must be below 2^23 elements");
   if (n_seqs > 65535 || (max_seqlen + 127) / 128 > 32767)
     return fail(TALM_EINVAL, "attn_bwd: at most 65535 sequences of at most 4194176 tokens");
   const int64_t need = talm_attn_bwd_workspace(n_tokens, n_q_heads);
