@@ -49,7 +49,7 @@ MEASURED_TRAFFIC = {
     "swiglu_fwd": 110.1e6,
     "swiglu_bwd": 183.5e6,
     "attn_fwd": 14.2e6,
-    "attn_bwd": 66.4e6,  # its three dispatches: dot, the dQ / dK / dV kernel, the reduction
+    "attn_bwd": 56.0e6,  # its three dispatches: dot, the dQ / dK / dV kernel, the reduction
     "head_ce_fwd_bwd": 4583e6,
 }
 
