@@ -80,3 +80,10 @@ def gemm_splitk_workspace_bytes(m, n, k):
     if size < 0:
         raise ValueError(f"gemm_splitk: unsupported shape m={m} n={n} k={k}")
     return size
+
+
+def nf4_gemm_workspace_bytes(n_tokens, rows, cols, transpose):
+    size = _lib.lib().talm_nf4_gemm_workspace(n_tokens, rows, cols, 1 if transpose else 0)
+    if size < 0:
+        raise ValueError(f"nf4_gemm: unsupported shape tokens={n_tokens} W=[{rows}, {cols}]")
+    return size

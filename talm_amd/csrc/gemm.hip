@@ -11,14 +11,12 @@
 // the chip in one round. A second kernel sums the partials of each element in part order
 // (deterministic) and rounds to fp16 once.
 #include "mfma_tile.h"
-
-#include <algorithm>
+#include "splitk.h"
 
 namespace talm {
 namespace {
 
 using SplitShape = TileShape<256, 256, 64, 2, 2, 4>;
-constexpr int kReduceThreads = 256;
 
 struct SplitArgs {
   const uint16_t* A;
@@ -73,43 +71,6 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void gemm_splitk_kernel(Spl
       }
 }
 
-// out[r][c .. c + 7] = fp16(sum over parts p = 0, 1, ... of part[p][r][c .. c + 7]).
-__global__ __launch_bounds__(kReduceThreads) void splitk_reduce_kernel(
-    const float* __restrict__ part, int parts, int64_t mn, int N, uint16_t* __restrict__ out,
-    int64_t ldo) {
-  const int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kReduceThreads + threadIdx.x) * 8;
-  if (e0 >= mn) return;
-  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int p = 0; p < parts; ++p) {
-    const float4 x = *reinterpret_cast<const float4*>(part + p * mn + e0);
-    const float4 y = *reinterpret_cast<const float4*>(part + p * mn + e0 + 4);
-    s[0] += x.x; s[1] += x.y; s[2] += x.z; s[3] += x.w;
-    s[4] += y.x; s[5] += y.y; s[6] += y.z; s[7] += y.w;
-  }
-  const int64_t r = e0 / N, c = e0 % N;
-  *reinterpret_cast<uint4*>(out + r * ldo + c) =
-      make_uint4(pack2(s[0], s[1]), pack2(s[2], s[3]), pack2(s[4], s[5]), pack2(s[6], s[7]));
-}
-
-struct SplitPlan {
-  int parts, steps_per_part, n_mtiles, n_ntiles;
-};
-
-// As many K parts as fill the chip's CUs in one round with the output tiles, each of at least 16
-// steps; no empty part.
-SplitPlan plan_split(int64_t m, int64_t n, int64_t k) {
-  SplitPlan p{};
-  p.n_mtiles = static_cast<int>((m + SplitShape::kBM - 1) / SplitShape::kBM);
-  p.n_ntiles = static_cast<int>((n + SplitShape::kBN - 1) / SplitShape::kBN);
-  const int64_t steps = (k + SplitShape::kBK - 1) / SplitShape::kBK;
-  const int64_t tiles = static_cast<int64_t>(p.n_mtiles) * p.n_ntiles;
-  int64_t parts = std::max<int64_t>(1, std::min<int64_t>(device_cus() / std::max<int64_t>(tiles, 1),
-                                                         steps / 16));
-  p.steps_per_part = static_cast<int>((steps + parts - 1) / parts);
-  p.parts = static_cast<int>((steps + p.steps_per_part - 1) / p.steps_per_part);
-  return p;
-}
-
 bool splitk_shape_ok(int64_t m, int64_t n, int64_t k) {
   return m >= 1 && n >= 8 && k >= 8 && n % 8 == 0 && k % 8 == 0 && m <= (1 << 24) &&
          n <= (1 << 24) && k <= (1 << 24);
@@ -122,7 +83,7 @@ using namespace talm;
 
 TALM_API int64_t talm_gemm_splitk_workspace(int64_t m, int64_t n, int64_t k) {
   if (!splitk_shape_ok(m, n, k)) return -1;
-  return static_cast<int64_t>(plan_split(m, n, k).parts) * m * n * 4;
+  return static_cast<int64_t>(plan_split(m, n, k, SplitShape::kBM, SplitShape::kBN, SplitShape::kBK).parts) * m * n * 4;
 }
 
 TALM_API int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
@@ -139,7 +100,7 @@ TALM_API int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b,
   if (!a || !b || !out || !workspace) return fail(TALM_EINVAL, "gemm_splitk: null pointer");
   if (!aligned(a, 16) || !aligned(b, 16) || !aligned(out, 16) || !aligned(workspace, 16))
     return fail(TALM_EINVAL, "gemm_splitk: operands and workspace must be 16-byte aligned");
-  const SplitPlan p = plan_split(m, n, k);
+  const SplitPlan p = plan_split(m, n, k, SplitShape::kBM, SplitShape::kBN, SplitShape::kBK);
   const int64_t need = static_cast<int64_t>(p.parts) * m * n * 4;
   if (workspace_bytes < need)
     return fail(TALM_EINVAL, "gemm_splitk: workspace of %lld bytes, %lld needed",
@@ -154,10 +115,6 @@ TALM_API int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b,
   const hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL((gemm_splitk_kernel<SplitShape>), dim3(static_cast<unsigned>(args.n_tiles)),
                      dim3(SplitShape::kThreads), 0, s, args);
-  const int64_t mn = m * n;
-  hipLaunchKernelGGL(splitk_reduce_kernel,
-                     dim3(static_cast<unsigned>((mn / 8 + kReduceThreads - 1) / kReduceThreads)),
-                     dim3(kReduceThreads), 0, s, static_cast<const float*>(workspace), p.parts, mn,
-                     static_cast<int>(n), out, ldo);
+  launch_splitk_reduce(static_cast<const float*>(workspace), p.parts, m, n, out, ldo, s);
   return check_launch("gemm_splitk");
 }

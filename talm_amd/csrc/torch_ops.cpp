@@ -628,17 +628,22 @@ void lora_adamw(const Tensor& table, int64_t n_tensors, int64_t max_numel, doubl
 }
 
 // ------------------------------------------------------------------------------------------
-// y = x W^T on the NF4 form of W (dequantized inside the GEMM).
+// Products on the NF4 form of W [rows, cols] (dequantized inside the GEMM): out = x W^T
+// (transpose false: x [N, cols], out [N, rows]) or out = x W (transpose true: x [N, rows],
+// out [N, cols]); the workspace holds split-K partials (talm_nf4_gemm_workspace bytes).
 // ------------------------------------------------------------------------------------------
 void nf4_gemm(const Tensor& x, const Tensor& packed, const Tensor& absmax8, const Tensor& code,
-              const Tensor& absmax2, const Tensor& offset2, int64_t n_out, int64_t blocksize,
-              int64_t blocksize2, const Tensor& out) {
+              const Tensor& absmax2, const Tensor& offset2, int64_t rows, int64_t cols,
+              bool transpose, int64_t blocksize, int64_t blocksize2, const Tensor& out,
+              const Tensor& workspace) {
   require_fp16(x, "x");
   require_fp16(out, "out");
+  const int64_t k = transpose ? rows : cols, n_out = transpose ? cols : rows;
   require(x.dim() == 2 && out.dim() == 2 && x.stride(1) == 1 && out.stride(1) == 1 &&
-              out.size(0) == x.size(0) && out.size(1) == n_out,
-          "nf4_gemm: x [N, K], out [N, n_out] with unit column stride");
-  const int64_t n = x.size(0), k = x.size(1);
+              x.size(1) == k && out.size(0) == x.size(0) && out.size(1) == n_out,
+          "nf4_gemm: x [N, K], out [N, n_out] with unit column stride (K, n_out = cols, rows, "
+          "or rows, cols with transpose)");
+  const int64_t n = x.size(0);
   for (const Tensor* t : {&packed, &absmax8, &code, &absmax2, &offset2})
     require(t->is_cuda() && t->is_contiguous() && t->device() == x.device(),
             "nf4_gemm: packed, absmax8, code, absmax2, offset2 contiguous on x's device");
@@ -646,14 +651,18 @@ void nf4_gemm(const Tensor& x, const Tensor& packed, const Tensor& absmax8, cons
               code.scalar_type() == at::kFloat && absmax2.scalar_type() == at::kFloat &&
               offset2.scalar_type() == at::kFloat,
           "nf4_gemm: packed / absmax8 uint8, code / absmax2 / offset2 float32");
-  require(k % 64 == 0 && packed.numel() >= n_out * k / 2 && absmax8.numel() >= n_out * k / 64 &&
-              code.numel() >= 256 && absmax2.numel() >= n_out * k / 16384 &&
-              offset2.numel() >= n_out * k / 16384,
-          "nf4_gemm: the NF4 buffers do not cover [n_out, K]");
-  check(talm_nf4_gemm(as<uint16_t>(x), x.stride(0), n, k, as<uint8_t>(packed), as<uint8_t>(absmax8),
-                      as<float>(code), as<float>(absmax2), as<float>(offset2), n_out,
-                      static_cast<int32_t>(blocksize), static_cast<int32_t>(blocksize2),
-                      as<uint16_t>(out), out.stride(0), stream_of(x)),
+  require(cols % 64 == 0 && packed.numel() >= rows * cols / 2 &&
+              absmax8.numel() >= rows * cols / 64 && code.numel() >= 256 &&
+              absmax2.numel() >= rows * cols / 16384 && offset2.numel() >= rows * cols / 16384,
+          "nf4_gemm: the NF4 buffers do not cover [rows, cols]");
+  require(workspace.is_cuda() && workspace.is_contiguous() && workspace.device() == x.device(),
+          "nf4_gemm: workspace contiguous on x's device");
+  check(talm_nf4_gemm(as<uint16_t>(x), x.stride(0), n, as<uint8_t>(packed), as<uint8_t>(absmax8),
+                      as<float>(code), as<float>(absmax2), as<float>(offset2), rows, cols,
+                      transpose ? 1 : 0, static_cast<int32_t>(blocksize),
+                      static_cast<int32_t>(blocksize2), as<uint16_t>(out), out.stride(0),
+                      workspace.numel() ? workspace.data_ptr() : nullptr,
+                      workspace.numel() * workspace.element_size(), stream_of(x)),
         "nf4_gemm");
 }
 
@@ -1062,7 +1071,8 @@ TORCH_LIBRARY(talm, m) {
   m.def("gemm_tune(Tensor a, int trans_a, Tensor b, int trans_b, Tensor(a!) d, int m, int n, "
         "int k, int lda, int ldb, int ldd, int reps) -> Tensor");
   m.def("nf4_gemm(Tensor x, Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
-        "Tensor offset2, int n_out, int blocksize, int blocksize2, Tensor(a!) out) -> ()");
+        "Tensor offset2, int rows, int cols, bool transpose, int blocksize, int blocksize2, "
+        "Tensor(a!) out, Tensor(b!) workspace) -> ()");
   m.def("lora_adamw(Tensor table, int n_tensors, int max_numel, float lr, float beta1, "
         "float beta2, float eps, float weight_decay, Tensor step_in, Tensor(a!) step_out, "
         "Tensor? grad_scale, Tensor? found_inf, Tensor(b!) out) -> ()");

@@ -1,125 +1,179 @@
-// y = x W^T with W in the layer group's NF4 form (double-quantized absmax, 64-weight blocks),
-// fp16 MFMA on gfx950: the weight is dequantized into LDS inside the GEMM, never written to HBM
-// (SURVEY's W4A16 row; replaces the dequantization of the layer's buffer + hipBLASLt's fp16
-// GEMM for the projections it serves, solution/qgroup.py:72-99 and :346-355).
+// The decoder's products on a weight W [rows, cols] held in the layer group's NF4 form
+// (double-quantized absmax, 64-weight blocks along a row), fp16 MFMA on gfx950, with the weight
+// dequantized into LDS inside the GEMM and never written to HBM (SURVEY's W4A16 row; it replaces
+// the dequantization of the layer's buffer + the fp16 GEMM on it for the projections it serves,
+// solution/qgroup.py:72-99 and :346-355):
+//   forward     out [M, rows] = x [M, cols] W^T        ("nt": the reduction runs along W's rows)
+//   input grad  out [M, cols] = dy [M, rows] W         ("nn": the reduction runs across W's rows)
 //
-// Tiles of 128 tokens x 256 weight rows, 8 wavefronts of 64 x 64 (v_mfma_f32_32x32x16_f16),
-// 64-deep k steps (one NF4 block per weight row and step). Both operands go through registers
-// into 2-slot LDS buffers in the swizzled layout the MFMA fragment reads expect (mfma_tile.h):
-//   A (x): two 16-byte chunks per thread and step;
-//   B: each thread loads 16 bytes (32 weights of one row) and the row's block-scale inputs, then
-//      dequantizes them exactly as nf4_group_kernel does (fp32 level x scale, one rounding to
-//      fp16) into four 16-byte chunks.
-// Step kt: barrier; MFMAs on slot kt % 2; the registers of step kt + 1 (loaded kDepth steps
-// earlier, into register set (kt + 1) % kDepth) into slot (kt + 1) % 2; loads of step
-// kt + 1 + kDepth into that register set. kDepth steps of MFMAs and dequantization cover each
-// load's latency (one step, ~0.5 µs, does not). Loads past the last step are clamped, so no load
-// sits behind a branch (the compiler would wait for it at the join). (Operand DMA straight into LDS, as in the other GEMMs, would make
-// the compiler wait for it before every LDS access of the dequantization.)
-// The fp16 weights are bit-identical to the dequantized buffer's; the products are the fp16
-// GEMM's with fp32 accumulation (only the summation order differs from hipBLASLt's).
+// Why it pays on this chip: the fp16 GEMMs of the step are bound by the operand stream from L2
+// into the CUs (about 16 bytes per clock per CU for direct-to-LDS loads), not by the MFMA pipe.
+// A 256 x 256 tile of fp16 operands moves 64 KiB per 64-deep step; with the weight read as NF4
+// codes it moves 32 KiB of activations plus 8 KiB of codes, and the dequantization (VALU and LDS
+// writes) runs beside the MFMAs of the other wavefronts.
+//
+// Tiles of 256 tokens x 256 output columns, 8 wavefronts of 128 x 64 (v_mfma_f32_32x32x16_f16),
+// 64-deep steps through a two-slot LDS ring:
+//   A (activations) streams from global memory straight into LDS (buffer_load ... lds, the
+//     swizzled layout of mfma_tile.h);
+//   B (weights): each thread loads 16 bytes of codes (32 weights of one row and one block) and
+//     the block's scale inputs two steps ahead into registers, and dequantizes them exactly as
+//     the group dequant kernel does (fp32 level x scale, one rounding to fp16) into the other
+//     slot while the MFMAs read this one. "nt" stores them as [256 out rows][64 k] (the MFMA
+//     fragment layout); "nn" stores W's rows as they are, [64 k rows][256 out columns], and
+//     reads its fragments with the transposing ds_read_b64_tr_b16.
+// K is cut into parts when the output has too few tiles to fill the chip (fp32 partials summed
+// in part order by splitk_reduce_kernel, deterministic). The fp16 weights are bit-identical to
+// talm_nf4_group_dequant's; the products are fp16 GEMMs with fp32 accumulation.
 #include "mfma_tile.h"
 #include "nf4_code.h"
+#include "splitk.h"
 
 namespace talm {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
-using W4Shape = TileShape<128, 256, 64, 2, 2, 4>;
-constexpr int kW4AStage = W4Shape::kAChunks * 16;          // 16 KiB of x per step
-constexpr int kW4BStage = W4Shape::kBN * W4Shape::kBK * 2;  // 32 KiB of fp16 weights per step
-constexpr int kW4Lds = 2 * kW4AStage + 2 * kW4BStage;
-constexpr int kW4APer = W4Shape::kAChunks / W4Shape::kThreads;  // A chunks per thread and step
-static_assert(kW4APer * W4Shape::kThreads == W4Shape::kAChunks, "whole A chunks per thread");
-constexpr int kDepth = 2;  // register sets of loaded steps in flight (even: LDS slots stay static)
-static_assert(kDepth % 2 == 0, "an even depth keeps the two LDS slots' indices constant");
-constexpr int kW4ZS = W4Shape::kBN + 8;  // staged output tile row stride (halfs)
-static_assert(W4Shape::kBM * kW4ZS * 2 <= kW4Lds, "the staged tile reuses the operand buffers");
-static_assert(W4Shape::kThreads == 2 * W4Shape::kBN, "two threads per weight row and step");
+using W4Shape = TileShape<256, 256, 64, 2, 2, 4>;
+constexpr int kW4ZS = W4Shape::kBN + 8;  // staged fp16 output row stride (halfs)
+constexpr int kW4Lds = W4Shape::kRing > W4Shape::kBM * kW4ZS * 2 ? W4Shape::kRing
+                                                                 : W4Shape::kBM * kW4ZS * 2;
+static_assert(W4Shape::kThreads == 512, "the B mapping assumes 512 threads");
 
 struct W4Args {
-  const uint16_t* x;       // [n_tokens][ldx]
-  int64_t ldx;
-  int n_tokens, k;         // k: multiple of 64
-  const uint8_t* packed;   // [n_out][k / 2], two weights per byte, high nibble first
-  const uint8_t* absmax8;  // [n_out * k / 64]: second-level code index of each block
+  const uint16_t* a;       // [M][lda]: x ("nt") or dy ("nn")
+  int64_t lda;
+  int M, N, K;             // out [M, N], reduction K
+  int w_cols;              // W's row length (the NF4 blocks run along it)
+  const uint8_t* packed;   // W [rows][w_cols], two weights per byte, high nibble first
+  const uint8_t* absmax8;  // [rows * w_cols / 64]
   const float* code;       // [256]
-  const float* absmax2;    // [(n_out * k) / 16384]
-  const float* offset2;    // [(n_out * k) / 16384]
-  int n_out;
-  uint16_t* out;           // [n_tokens][ldo]
+  const float* absmax2;    // [rows * w_cols / 16384]
+  const float* offset2;
+  uint16_t* out;           // [M][ldo] when parts == 1
   int64_t ldo;
-  int n_mtiles, n_ntiles;
+  float* part;             // [parts][M][N] when parts > 1
+  int steps_per_part, n_mtiles, n_ntiles, n_tiles, parts;
 };
 
+// The "nn" B tile: [64 k rows][256 columns] fp16, 32 chunks of 16 bytes per row, chunk c of row r
+// at position c ^ 4 (r & 3). A transposing read of one 32 x 16 fragment touches 4 consecutive rows
+// x 4 adjacent chunks per 32-lane phase: positions 4 ((c0 / 4) ^ t) + u, 16 distinct banks groups.
+__device__ __forceinline__ int nn_pos(int row, int chunk) { return row * 32 + (chunk ^ ((row & 3) << 2)); }
+
+// One step of the wavefront's 128 x 64 block: per 16-deep slice ks its fragments, its MFMAs, then
+// extra(ks) (the dequantization of the next stage, interleaved so that its VALU work issues
+// while the slice's MFMAs run).
+template <bool kNN, class Extra>
+__device__ __forceinline__ void w4_mma(const uint4* __restrict__ As, const unsigned char* __restrict__ Bs,
+                                       Acc<W4Shape>& acc, int lane, int wm, int wn, Extra&& extra) {
+  using S = W4Shape;
+  constexpr int kSteps = S::kBK / 16;
+#pragma unroll
+  for (int ks = 0; ks < kSteps; ++ks) {
+    half8_t a[S::kFragM], b[S::kFragN];
+    const int kc = ks * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < S::kFragM; ++i)
+      a[i] = __builtin_bit_cast(half8_t, As[swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), kc)]);
+#pragma unroll
+    for (int j = 0; j < S::kFragN; ++j) {
+      if constexpr (!kNN) {
+        b[j] = __builtin_bit_cast(
+            half8_t, reinterpret_cast<const uint4*>(Bs)[swz<S::kCpr>(wn * S::kWaveN + j * 32 + (lane & 31), kc)]);
+      } else {
+        // lane (g = lane / 16, i = lane % 16) points at row 16 ks + 8 (g / 2) + i / 4 (+ 4),
+        // columns col .. col + 3 with col = the fragment's 16 (g % 2) + 4 (i % 4): it receives
+        // k-slots 8 (g / 2) + 0..3 (+ 4..7) of column n = lane % 32
+        const int g = lane >> 4, i = lane & 15;
+        const int row = ks * 16 + 8 * (g >> 1) + (i >> 2);
+        const int col = wn * S::kWaveN + j * 32 + 16 * (g & 1) + 4 * (i & 3);
+        const unsigned char* p0 = Bs + nn_pos(row, col >> 3) * 16 + (col & 7) * 2;
+        const unsigned char* p1 = Bs + nn_pos(row + 4, col >> 3) * 16 + (col & 7) * 2;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p0));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p1));
+        b[j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < S::kFragN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    extra(ks);
+  }
+}
+
+// Word j (8 weights) of the 16 bytes of codes a thread loaded for a step, looked up in its
+// block's table of scaled levels, into its 16-byte chunk of the B stage. The pointers are restrict-qualified, so
+// these LDS accesses carry alias scopes of their own.
+template <bool kNN>
+__device__ __forceinline__ void w4_dequant_word(uint32_t word, const Nf4Table& table,
+                                                uint4* __restrict__ bs, int tid, int j) {
+  const uint4 v = nf4_lookup_word(word, table);
+  if constexpr (!kNN)
+    bs[swz<W4Shape::kCpr>(tid >> 1, 4 * (tid & 1) + j)] = v;
+  else
+    bs[nn_pos(tid >> 3, 4 * (tid & 7) + j)] = v;
+}
+
+template <bool kNN>
 __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a) {
   using S = W4Shape;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kW4Lds];
-  __shared__ float s_code[256];
-  __shared__ float s_levels[16];
+  // one LDS object (the ring / output staging, then the code table): with several,
+  // the compiler tags their accesses with alias scopes and then waits for the ring's
+  // direct-to-LDS loads before every LDS access of the same object
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kW4Lds + 256 * 4];
+  float* const s_code = reinterpret_cast<float*>(smem + kW4Lds);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
   if (tid < 256) s_code[tid] = a.code[tid];
-  if (tid < 16) s_levels[tid] = kNF4Levels[tid];
 
-  // consecutive tiles walk the token tiles of one weight panel (the panel stays in L2)
-  const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_mtiles * a.n_ntiles));
-  const int ntile = static_cast<int>(tile / a.n_mtiles), mtile = static_cast<int>(tile % a.n_mtiles);
-  const int m0 = mtile * S::kBM, n0 = ntile * S::kBN;
-  const int nk = a.k / S::kBK;
+  // row tiles vary fastest, then column tiles, then K parts: tiles in flight on one XCD share
+  // the codes of their column tile and K part in its L2
+  const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_tiles));
+  const int mt = static_cast<int>(tile % a.n_mtiles);
+  const int rest = static_cast<int>(tile / a.n_mtiles);
+  const int nt = rest % a.n_ntiles, kp = rest / a.n_ntiles;
+  const int m0 = mt * S::kBM, n0 = nt * S::kBN;
+  const int k0 = kp * a.steps_per_part * S::kBK;
+  const int nk = min(a.steps_per_part, a.K / S::kBK - kp * a.steps_per_part);  // >= 1
 
-  uint4* const a_slot[2] = {reinterpret_cast<uint4*>(smem),
-                            reinterpret_cast<uint4*>(smem + kW4AStage)};
-  uint4* const b_slot[2] = {reinterpret_cast<uint4*>(smem + 2 * kW4AStage),
-                            reinterpret_cast<uint4*>(smem + 2 * kW4AStage + kW4BStage)};
+  Loader<S, S::kBM> la;
+  la.init(a.a + static_cast<int64_t>(m0) * a.lda + k0, a.lda, a.M - m0, nk * S::kBK, wave, lane);
 
-  // A: chunk c = tid + j * threads of the stage is row c / 8, k chunk c % 8; rows past the
-  // batch read its last row (their outputs are not stored)
-  const uint16_t* a_src[kW4APer];
-  int a_dst[kW4APer];
-#pragma unroll
-  for (int j = 0; j < kW4APer; ++j) {
-    const int c = tid + j * S::kThreads, row = c / S::kCpr, kc = c % S::kCpr;
-    a_src[j] = a.x + static_cast<int64_t>(min(m0 + row, a.n_tokens - 1)) * a.ldx + 8 * kc;
-    a_dst[j] = swz<S::kCpr>(row, kc);
+  // B: this thread's 16 bytes of codes per step. "nt": weight row n0 + tid / 2 (clamped: the
+  // columns of rows past N are not stored), k half tid % 2. "nn": weight row k0 + 64 kt + tid / 8
+  // (below K: K is a multiple of 64), 32 columns n0 + 32 (tid % 8) (clamped to the last 32 of the
+  // row: columns past N are not stored). e0 is the first weight's element index at step 0, e_step
+  // the advance per step (rows * cols < 2^31).
+  uint32_t e0, e_step;
+  if constexpr (!kNN) {
+    e0 = static_cast<uint32_t>(min(n0 + (tid >> 1), a.N - 1)) * a.w_cols + k0 + 32 * (tid & 1);
+    e_step = S::kBK;
+  } else {
+    e0 = static_cast<uint32_t>(k0 + (tid >> 3)) * a.w_cols + min(n0 + 32 * (tid & 7), a.w_cols - 32);
+    e_step = static_cast<uint32_t>(S::kBK) * a.w_cols;
   }
-  u32x4 ar[kDepth][kW4APer];
-  auto a_load = [&](int r, int kt) {
-    kt = min(kt, nk - 1);
-#pragma unroll
-    for (int j = 0; j < kW4APer; ++j)
-      ar[r][j] = *reinterpret_cast<const u32x4*>(a_src[j] + S::kBK * kt);
-  };
-  auto a_store = [&](int r, uint4* slot) {
-#pragma unroll
-    for (int j = 0; j < kW4APer; ++j)
-      slot[a_dst[j]] = make_uint4(ar[r][j][0], ar[r][j][1], ar[r][j][2], ar[r][j][3]);
-  };
-
-  // B: this thread's weight row (clamped past n_out: its columns are not stored) and 16-byte half
-  const int br = tid >> 1, bh = tid & 1;
-  const int64_t brow = min(n0 + br, a.n_out - 1);
-  const uint8_t* const bp = a.packed + brow * (a.k / 2) + 16 * bh;
-  const uint8_t* const b8 = a.absmax8 + brow * (a.k / 64);
-  const int64_t belem = brow * a.k;
-  u32x4 bw[kDepth];
-  uint32_t bcode[kDepth];
-  float ba2[kDepth], bo2[kDepth];
+  u32x4 bw[2];
+  uint32_t bcode[2];
+  float ba2[2], bo2[2];
   auto b_load = [&](int r, int kt) {
-    kt = min(kt, nk - 1);
-    bw[r] = *reinterpret_cast<const u32x4*>(bp + 32 * kt);
-    bcode[r] = b8[kt];
-    const int64_t blk = (belem + 64 * static_cast<int64_t>(kt)) >> 14;
-    ba2[r] = a.absmax2[blk];
-    bo2[r] = a.offset2[blk];
+    const uint32_t e = e0 + e_step * static_cast<uint32_t>(min(kt, nk - 1));
+    bw[r] = *reinterpret_cast<const u32x4*>(a.packed + (e >> 1));
+    bcode[r] = a.absmax8[e >> 6];
+    ba2[r] = a.absmax2[e >> 14];
+    bo2[r] = a.offset2[e >> 14];
   };
-  auto b_store = [&](int r, uint4* slot) {
-    const float scale = block_scale(s_code[bcode[r]], ba2[r], bo2[r]);
+  auto b_table = [&](int r) { return nf4_table(block_scale(s_code[bcode[r]], ba2[r], bo2[r])); };
+  auto b_store = [&](int r, unsigned char* bs) {
+    const Nf4Table table = b_table(r);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      slot[swz<S::kCpr>(br, 4 * bh + j)] = dequant_word(bw[r][j], scale, s_levels);
+      w4_dequant_word<kNN>(bw[r][j], table, reinterpret_cast<uint4*>(bs), tid, j);
   };
 
   Acc<S> acc;
@@ -130,41 +184,55 @@ __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-#pragma unroll
-  for (int r = 0; r < kDepth; ++r) {
-    a_load(r, r);
-    b_load(r, r);
-  }
-  __syncthreads();  // the code / level tables
-  a_store(0, a_slot[0]);
-  b_store(0, b_slot[0]);
-  a_load(0, kDepth);
-  b_load(0, kDepth);
-  // step kt + h: slot h % 2 holds it; the register set of step kt + h + 1 goes into the other
-  // slot and is reloaded with step kt + h + 1 + kDepth (kt a multiple of kDepth: the indices are
-  // constants once h is)
-  auto step = [&](int kt, int h) {
-    __syncthreads();  // the stores of the step before are visible; the slot it read is free
-    mma_step<S>(a_slot[h & 1], b_slot[h & 1], acc, lane, wm, wn);
-    const int r = (h + 1) % kDepth;
-    a_store(r, a_slot[(h + 1) & 1]);
-    b_store(r, b_slot[(h + 1) & 1]);
-    a_load(r, kt + h + 1 + kDepth);
-    b_load(r, kt + h + 1 + kDepth);
+  constexpr int kABytes = S::kAChunks * 16;
+  __syncthreads();  // the code table
+  // Step kt computes slot kt % 2 while A(kt + 1) and the codes of step kt + 2 load and the codes
+  // of step kt + 1 (register set (kt + 1) % 2, loaded a step earlier) are dequantized into the
+  // other slot. Every load of a step is waited for at the next step's top (vmcnt 0), so the
+  // order in which the compiler issues them does not matter. Past the last step the codes loads
+  // and the dequantization still run (B reads the last step's codes into the retired slot).
+  b_load(0, 0);
+  b_load(1, 1);
+  la.issue(smem, 0, wave);
+  b_store(0, smem + kABytes);
+  auto step = [&](int kt, int h) {  // step kt = kb + h in slot h
+    unsigned char* const cur = smem + h * S::kStageBytes;
+    unsigned char* const nxt = smem + (h ^ 1) * S::kStageBytes;
+    wait_vmcnt<0>();
+    lds_barrier();  // slot h complete (A landed, B stored); every wavefront is done with slot h ^ 1
+    // (issued behind a branch, as in the other ring kernels: the compiler then adds no wait for
+    // it before this step's LDS reads of the other slot)
+    if (kt + 1 < nk) la.issue(nxt, (kt + 1) * S::kBK, wave);
+    b_load(h, kt + 2);  // set h held the codes of step kt, stored in the step before
+    const Nf4Table table = b_table(h ^ 1);
+    w4_mma<kNN>(reinterpret_cast<const uint4*>(cur), cur + kABytes, acc, lane, wm, wn, [&](int ks) {
+      w4_dequant_word<kNN>(bw[h ^ 1][ks], table, reinterpret_cast<uint4*>(nxt + kABytes), tid, ks);
+    });
   };
-  int kt = 0;
-  for (; kt + kDepth <= nk; kt += kDepth) {
-#pragma unroll
-    for (int h = 0; h < kDepth; ++h) step(kt, h);
+  int kb = 0;
+  for (; kb + 2 <= nk; kb += 2) {
+    step(kb, 0);
+    step(kb + 1, 1);
   }
-  // the last nk % kDepth steps (outside the loop: its back edge then only sees whole trips, and
-  // the compiler's waits there stay kDepth steps deep)
-#pragma unroll
-  for (int h = 0; h < kDepth - 1; ++h)
-    if (kt + h < nk) step(kt, h);
-  __syncthreads();  // every wavefront is done with the operand buffers
+  if (kb < nk) step(kb, 0);
+  __syncthreads();  // every wavefront is done with the ring (and every load has landed)
 
-  // epilogue: fp16 tile staged in LDS, then 16-byte row stores
+  if (a.parts > 1) {
+    float* P = a.part + static_cast<int64_t>(kp) * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < S::kFragM; ++i)
+#pragma unroll
+      for (int j = 0; j < S::kFragN; ++j) {
+        const int gc = n0 + acc_col<S>(wn, j, lane);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int gr = m0 + acc_row<S>(wm, i, v, lane);
+          if (gr < a.M && gc < a.N) P[static_cast<int64_t>(gr) * a.N + gc] = acc[i][j][v];
+        }
+      }
+    return;
+  }
+  // fp16 tile staged in LDS, then 16-byte row stores
   uint16_t* zs = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
   for (int i = 0; i < S::kFragM; ++i)
@@ -176,14 +244,27 @@ __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a)
     }
   __syncthreads();
   constexpr int kChunksPerRow = S::kBN / 8;
-#pragma unroll
+#pragma unroll 4
   for (int it = 0; it < (S::kBM * kChunksPerRow) / S::kThreads; ++it) {
     const int c = it * S::kThreads + tid, row = c / kChunksPerRow, kc = c % kChunksPerRow;
     const int gr = m0 + row, gc = n0 + kc * 8;
-    if (gr < a.n_tokens && gc < a.n_out)
+    if (gr < a.M && gc < a.N)
       *reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(gr) * a.ldo + gc) =
           *reinterpret_cast<const uint4*>(zs + row * kW4ZS + kc * 8);
   }
+}
+
+SplitPlan w4_plan(int64_t m, int64_t n, int64_t k) {
+  return plan_split(m, n, k, W4Shape::kBM, W4Shape::kBN, W4Shape::kBK);
+}
+
+// rows x cols of W, the product's (M, N, K) and whether W's layout supports it
+bool w4_shape_ok(bool nn, int64_t m, int64_t rows, int64_t cols) {
+  if (m < 0 || m > (1 << 24) || rows < 64 || cols < 64 || rows > (1 << 20) || cols > (1 << 20) ||
+      rows * cols >= (int64_t{1} << 31))
+    return false;
+  if (cols % 64 || (rows * cols) % 16384) return false;
+  return nn ? rows % 64 == 0 : rows % 8 == 0;
 }
 
 }  // namespace
@@ -191,35 +272,64 @@ __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a)
 
 using namespace talm;
 
-TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t k,
-                           const uint8_t* packed, const uint8_t* absmax8, const float* code,
-                           const float* absmax2, const float* offset2, int64_t n_out,
+TALM_API int64_t talm_nf4_gemm_workspace(int64_t n_tokens, int64_t rows, int64_t cols,
+                                         int32_t transpose) {
+  const bool nn = transpose != 0;
+  if (!w4_shape_ok(nn, n_tokens, rows, cols)) return -1;
+  const int64_t n = nn ? cols : rows, k = nn ? rows : cols;
+  const SplitPlan p = w4_plan(n_tokens, n, k);
+  return p.parts > 1 ? static_cast<int64_t>(p.parts) * n_tokens * n * 4 : 0;
+}
+
+TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_t* packed,
+                           const uint8_t* absmax8, const float* code, const float* absmax2,
+                           const float* offset2, int64_t rows, int64_t cols, int32_t transpose,
                            int32_t blocksize, int32_t blocksize2, uint16_t* out, int64_t ldo,
-                           void* stream) {
+                           void* workspace, int64_t workspace_bytes, void* stream) {
   using S = W4Shape;
+  const bool nn = transpose != 0;
   if (blocksize != 64 || blocksize2 != 256)
     return fail(TALM_EINVAL, "nf4_gemm: blocksizes %d / %d (64 / 256 supported)", blocksize,
                 blocksize2);
-  if (n_tokens < 0 || k < 64 || k % 64 || n_out < 1 || ldx < k || ldx % 8 || ldo < n_out ||
-      ldo % 8 || n_out % 8 || n_tokens > (1 << 30) || n_out > (1 << 30) || k > (1 << 20) ||
-      (n_out * k) % 16384 || !(S::kBM * ldx * 2 < (int64_t{1} << 31)))
+  const int64_t n = nn ? cols : rows, k = nn ? rows : cols;
+  if (!w4_shape_ok(nn, n_tokens, rows, cols) || ldx < k || ldx % 8 || ldo < n || ldo % 8 ||
+      !(S::kBM * ldx * 2 < (int64_t{1} << 31)))
     return fail(TALM_EINVAL,
-                "nf4_gemm: bad shape (tokens %lld, k %lld, n_out %lld, ldx %lld, ldo %lld): k a "
-                "multiple of 64, n_out a multiple of 8, n_out * k whole 16384-weight groups",
-                (long long)n_tokens, (long long)k, (long long)n_out, (long long)ldx,
-                (long long)ldo);
+                "nf4_gemm: bad shape (tokens %lld, W [%lld, %lld], %s, ldx %lld, ldo %lld): W's "
+                "row length a multiple of 64, its rows a multiple of %d, whole 16384-weight "
+                "groups, strides multiples of 8 covering the rows",
+                (long long)n_tokens, (long long)rows, (long long)cols, nn ? "dy W" : "x W^T",
+                (long long)ldx, (long long)ldo, nn ? 64 : 8);
   if (n_tokens == 0) return ok();
   if (!x || !packed || !absmax8 || !code || !absmax2 || !offset2 || !out)
     return fail(TALM_EINVAL, "nf4_gemm: null pointer");
   if (!aligned(x, 16) || !aligned(packed, 16) || !aligned(out, 16))
     return fail(TALM_EINVAL, "nf4_gemm: x, packed and out must be 16-byte aligned");
+  const SplitPlan p = w4_plan(n_tokens, n, k);
+  if (p.parts > 1) {
+    const int64_t need = static_cast<int64_t>(p.parts) * n_tokens * n * 4;
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
+      return fail(TALM_EINVAL, "nf4_gemm: workspace of %lld bytes, %lld needed (16-byte aligned)",
+                  (long long)workspace_bytes, (long long)need);
+  }
   W4Args a{};
-  a.x = x; a.ldx = ldx; a.n_tokens = static_cast<int>(n_tokens); a.k = static_cast<int>(k);
+  a.a = x; a.lda = ldx;
+  a.M = static_cast<int>(n_tokens); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
+  a.w_cols = static_cast<int>(cols);
   a.packed = packed; a.absmax8 = absmax8; a.code = code; a.absmax2 = absmax2; a.offset2 = offset2;
-  a.n_out = static_cast<int>(n_out); a.out = out; a.ldo = ldo;
-  a.n_mtiles = static_cast<int>((n_tokens + S::kBM - 1) / S::kBM);
-  a.n_ntiles = static_cast<int>((n_out + S::kBN - 1) / S::kBN);
-  hipLaunchKernelGGL(w4_gemm_kernel, dim3(static_cast<unsigned>(a.n_mtiles * a.n_ntiles)),
-                     dim3(S::kThreads), 0, as_stream(stream), a);
+  a.out = out; a.ldo = ldo;
+  a.part = static_cast<float*>(workspace);
+  a.steps_per_part = p.steps_per_part;
+  a.n_mtiles = p.n_mtiles; a.n_ntiles = p.n_ntiles; a.parts = p.parts;
+  a.n_tiles = p.n_mtiles * p.n_ntiles * p.parts;
+  const hipStream_t s = as_stream(stream);
+  if (nn)
+    hipLaunchKernelGGL(w4_gemm_kernel<true>, dim3(static_cast<unsigned>(a.n_tiles)),
+                       dim3(S::kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(w4_gemm_kernel<false>, dim3(static_cast<unsigned>(a.n_tiles)),
+                       dim3(S::kThreads), 0, s, a);
+  if (p.parts > 1)
+    launch_splitk_reduce(static_cast<const float*>(workspace), p.parts, n_tokens, n, out, ldo, s);
   return check_launch("nf4_gemm");
 }

@@ -10,7 +10,9 @@ view, and their outputs are the two halves of one [N, 2I] buffer:
             dgate, dup over gu's halves        (talm_swiglu_bwd_rows, in place)
             dx = [dgate | dup] [W_gate; W_up]  (one GEMM reducing over 2I)
 One node instead of four (three GroupLinear nodes and the SwiGLU node), no separate add of the
-gate and up input gradients. hipBLASLt's heuristic choice for the 2I-deep input gradient is
+gate and up input gradients. The backward's dx product reads [W_gate; W_up] as NF4 codes
+(talm_nf4_gemm, dequantized inside the GEMM) while the layer group serves that block that way
+(qgroup.W4_BLOCKS). hipBLASLt's heuristic choice for the 2I-deep input gradient is
 about twice as slow as two I-deep products; the measured solution table (gemm_tuning.py) names
 one about 15% faster than the two products together. Same products with fp32 accumulation as
 the per-projection path. Once "qgroup" is off (the weights come projection by projection) the
@@ -99,6 +101,16 @@ class FusedMLP(torch.autograd.Function):
         torch.ops.talm.swiglu_bwd_rows(dact, gate, up, gate, up)
         del dact
         dx = torch.empty(n_tok, hidden, dtype=torch.float16, device=dy.device)
+        if (GATE, UP) in group.w4_blocks():
+            # dx = [dgate | dup] [W_gate; W_up] with the weights read as NF4 codes (the
+            # transposed buffer leaves them out)
+            try:
+                group.nf4_gemm(gu, GATE, DOWN, True, dx)
+                RAN["w4a16"] += 1
+                return dx.view(ctx.x_shape), None
+            except Exception as exc:  # noqa: BLE001 - state.py convention
+                if not fallback("w4a16", exc):
+                    raise
         w_gu_t = group.span_t(GATE, DOWN)
         w_gu = None if w_gu_t is not None else group.span(GATE, DOWN)
         if w_gu_t is not None:

@@ -29,13 +29,16 @@ the form the forward uses): `resident_t` holds ONE layer's weights dequantized t
 (talm_nf4_group_dequant_t, the same values), laid out as four row-major blocks [in, sum of out]:
 q|k|v, o, gate|up, down. `span_t` hands out a block. Each layer's backward makes its group's
 transposed buffer resident with one launch, as the forward does with the row-major one, and
-drops the row-major buffer the forward left behind.
+drops the row-major buffer the forward left behind. The gate|up block is left out of it while
+the NF4 dequant-GEMM serves that input gradient (`nf4_gemm`, W4_BLOCKS): its weights are then
+read as 4-bit codes and never written out in fp16.
 
 Graceful degradation (state.py): an unexpected error here turns "qgroup" off; each projection
 then takes the per-projection dequantization (nf4_dequant.py, the same values) and the 4-bit
 layer its own forward.
 """
 
+import os
 import weakref
 from collections import namedtuple
 
@@ -56,6 +59,11 @@ _RESIDENT = {}
 _RESIDENT_T = {}
 # the blocks of the transposed buffer: projections used as one [in, sum of out] operand
 T_BLOCKS = ((0, 1, 2), (3,), (4, 5), (6,))
+# blocks whose input gradient runs on the NF4 dequant-GEMM (talm_nf4_gemm, the weights read as
+# 4-bit codes and dequantized inside the GEMM): the transposed buffer leaves them out. gate|up,
+# where that GEMM is faster than the split-K GEMM on the transposed weights plus their share of
+# the transposed dequantization.
+W4_BLOCKS = ((4, 5),) if os.environ.get("SOLUTION_DISABLE_W4A16") != "1" else ()
 
 
 def launch(packed, absmax8, code, absmax2, offset2, levels, out, n_rows, qblock, qblock2):
@@ -188,11 +196,21 @@ class LayerGroup:
             off += cin * width
         return per_proj, blocks
 
-    def dequantize_t(self):
-        """The layer's W^T blocks (one launch): block b at blocks[b][0], [in, width] row-major."""
+    def w4_blocks(self):
+        """The transposed buffer's blocks served by the NF4 dequant-GEMM now (left out of it)."""
+        if "w4a16" in DISABLED:
+            return ()
+        return tuple(b for b in W4_BLOCKS if self.w4_ok(b[0], b[-1] + 1))
+
+    def dequantize_t(self, skip=()):
+        """The layer's W^T blocks (one launch): block b at blocks[b][0], [in, width] row-major;
+        the blocks in `skip` are not written."""
         per_proj, _blocks = self.t_layout
+        left_out = {i for b in skip for i in b}
         segs = []
         for i, seg in enumerate(self.segments):
+            if i in left_out:
+                continue
             _b, dst, ld = per_proj[i]
             segs += [seg.start, seg.shape[0], seg.shape[1], dst, ld]
         out = torch.empty(self.numel, dtype=torch.float16, device=self.packed.device)
@@ -200,18 +218,19 @@ class LayerGroup:
                                            self.offset2, segs, out, self.qblock, self.qblock2)
         return out
 
-    def resident_t(self):
-        """This layer's transposed buffer: the GPU's resident one when it is this group's, else
-        one launch that makes it so (the forward's row-major buffer is dropped: the backward has
-        begun)."""
+    def resident_t(self, need=None):
+        """This layer's transposed buffer: the GPU's resident one when it is this group's and
+        holds block `need`, else one launch that makes it so (the forward's row-major buffer is
+        dropped: the backward has begun)."""
         held = _RESIDENT_T.get(self.device)
-        if held is not None and held[0] is self:
+        if held is not None and held[0] is self and need not in held[2]:
             return held[1]
         _RESIDENT.pop(self.device, None)
         _RESIDENT_T.pop(self.device, None)
-        buf = self.dequantize_t()
+        skip = tuple(b for b in self.w4_blocks() if b != need)
+        buf = self.dequantize_t(skip)
         RAN["group_t"] += 1
-        _RESIDENT_T[self.device] = (self, buf)
+        _RESIDENT_T[self.device] = (self, buf, skip)
         return buf
 
     def span_t(self, first, last):
@@ -224,13 +243,37 @@ class LayerGroup:
         if members not in T_BLOCKS:
             return None
         try:
-            buf = self.resident_t()
+            buf = self.resident_t(members)
         except Exception as exc:  # noqa: BLE001 - state.py convention
             if not fallback("qgroup", exc):
                 raise
             return None
         off, cin, width = self.t_layout[1][T_BLOCKS.index(members)]
         return buf[off:off + cin * width].view(cin, width)
+
+    # -- the NF4 dequant-GEMM ------------------------------------------------------------------------
+    def w4_ok(self, first, last):
+        """Projections first .. last - 1 are one [sum of out, in] matrix talm_nf4_gemm takes:
+        64-weight blocks in groups of 256, starting on a second-level block, one input size."""
+        segs = self.segments[first:last]
+        cols = {seg.shape[1] for seg in segs}
+        rows = sum(seg.shape[0] for seg in segs)
+        return (self.qblock == 64 and self.qblock2 == 256 and len(cols) == 1
+                and segs[0].start % (64 * 256) == 0 and next(iter(cols)) % 64 == 0
+                and rows % 64 == 0 and "qgroup" not in DISABLED)
+
+    def nf4_gemm(self, x, first, last, transpose, out):
+        """out = x W^T (transpose False: the forward) or x W (True: the input gradient) with W the
+        [sum of out, in] rows of projections first .. last - 1 read as NF4 codes and dequantized
+        inside the GEMM (the same fp16 weights as `span`)."""
+        segs = self.segments[first:last]
+        rows, cols = sum(seg.shape[0] for seg in segs), segs[0].shape[1]
+        lo, span2 = segs[0].start, self.qblock * self.qblock2
+        ws = torch.empty(_ops.nf4_gemm_workspace_bytes(x.shape[0], rows, cols, transpose),
+                         dtype=torch.uint8, device=x.device)
+        torch.ops.talm.nf4_gemm(x, self.packed[lo // 2:], self.absmax8[lo // self.qblock:],
+                                self.code, self.absmax2[lo // span2:], self.offset2[lo // span2:],
+                                rows, cols, transpose, self.qblock, self.qblock2, out, ws)
 
     def dequantize_one(self, idx):
         return self.dequantize(idx, idx + 1).view(self.segments[idx].shape)

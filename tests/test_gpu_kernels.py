@@ -204,12 +204,15 @@ def test_layer_group_packs_and_keeps_one_resident_layer():
         assert torch.equal(dequantize_4bit(m.weight.data, m.weight.quant_state), ref)
     for idx, ref in enumerate(refs):
         assert torch.equal(group.dequantize_one(idx), ref)
-    # the backward's transposed blocks: one launch for the layer, the row-major buffer dropped
+    # the backward's transposed blocks: one launch for the layer, the row-major buffer dropped;
+    # a block the NF4 dequant-GEMM serves is left out of it and costs a second launch when asked
+    # for (after a fallback)
     before_t = RAN["group_t"]
-    for members in qgroup.T_BLOCKS:
+    w4 = group.w4_blocks()
+    for members in [b for b in qgroup.T_BLOCKS if b not in w4] + list(w4):
         wt = group.span_t(members[0], members[-1] + 1)
         assert torch.equal(wt, torch.cat([refs[i] for i in members]).t()), members
-    assert RAN["group_t"] == before_t + 1
+    assert RAN["group_t"] == before_t + 1 + (1 if w4 else 0)
     assert group.span_t(0, 2) is None and group.span_t(3, 5) is None  # not one block
     assert qgroup._RESIDENT.get(group.device) is None
     group.begin_forward()  # a forward drops the transposed buffer again

@@ -1,8 +1,11 @@
-"""talm_nf4_gemm (y = x W^T on the NF4 form of W, dequantized inside the GEMM) on the config-1
-layer's packed buffers: with x the identity the output is W^T, which must equal the grouped
-dequant kernel's fp16 weights bit for bit (pinned to the oracle in test_gpu_kernels.py); on
-random x the output is within one fp16 rounding of the fp32 product of those weights, for the
-q, k, gate|up and down slices of the layer and ragged token counts."""
+"""talm_nf4_gemm (products on the NF4 form of a weight W [rows, cols], dequantized inside the
+GEMM) on the config-1 layer's packed buffers, in both forms: the forward x W^T and the input
+gradient dy W. With x the identity the output is W^T (forward) or W (input gradient), which must
+equal the grouped dequant kernel's fp16 weights bit for bit (that kernel is pinned to the oracle
+in test_gpu_kernels.py); on random x the output is within one fp16 rounding of the fp32 product
+of those weights, for the q|k|v, o, gate|up and down slices of the layer, ragged token counts and
+the K-split shapes (down forward, gate|up input gradient). A second call on the same buffers is
+bit-identical (the split-K partials are summed in a fixed order)."""
 
 import pytest
 import torch
@@ -12,7 +15,7 @@ from talm_amd import _ops, workloads
 pytestmark = pytest.mark.gpu
 
 # (name, first projection, projections): slices of the packed layer (q, k, v, o, gate, up, down)
-SLICES = [("q", 0, 1), ("k", 1, 1), ("gate|up", 4, 2), ("down", 6, 1)]
+SLICES = [("q|k|v", 0, 3), ("o", 3, 1), ("gate|up", 4, 2), ("down", 6, 1)]
 
 
 def _layer():
@@ -29,63 +32,80 @@ def _slice(d, dev, w16, first, count):
     shapes = d["shapes"]
     e0 = sum(a * b for a, b in shapes[:first])
     rows = sum(shapes[i][0] for i in range(first, first + count))
-    k = shapes[first][1]
+    cols = shapes[first][1]
     assert e0 % 16384 == 0
     parts = dict(packed=dev["packed"][e0 // 2:], absmax8=dev["absmax8"][e0 // 64:],
                  absmax2=dev["absmax2"][e0 // 16384:], offset2=dev["offset2"][e0 // 16384:])
-    return parts, w16[e0:e0 + rows * k].view(rows, k), rows, k
+    return parts, w16[e0:e0 + rows * cols].view(rows, cols), rows, cols
 
 
-def _gemm(x, parts, code, rows):
-    out = torch.full((x.shape[0], rows), float("nan"), dtype=torch.float16, device="cuda")
+def _gemm(x, parts, code, rows, cols, transpose, out=None):
+    n_out = cols if transpose else rows
+    if out is None:
+        out = torch.full((x.shape[0], n_out), float("nan"), dtype=torch.float16, device="cuda")
+    ws = torch.empty(_ops.nf4_gemm_workspace_bytes(x.shape[0], rows, cols, transpose),
+                     dtype=torch.uint8, device="cuda")
     torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], code, parts["absmax2"],
-                            parts["offset2"], rows, 64, 256, out)
+                            parts["offset2"], rows, cols, transpose, 64, 256, out, ws)
     return out
 
 
+@pytest.mark.parametrize("transpose", [False, True], ids=["xWt", "dyW"])
 @pytest.mark.parametrize("name,first,count", SLICES)
-def test_identity_input_gives_the_dequantized_weights(name, first, count):
-    print(f"[case] nf4_gemm identity {name}", flush=True)
+def test_identity_input_gives_the_dequantized_weights(name, first, count, transpose):
+    print(f"[case] nf4_gemm identity {name} transpose={transpose}", flush=True)
     _ops.load()
     d, dev, w16 = _layer()
-    parts, w, rows, k = _slice(d, dev, w16, first, count)
+    parts, w, rows, cols = _slice(d, dev, w16, first, count)
+    k = rows if transpose else cols
     eye = torch.eye(k, dtype=torch.float16, device="cuda")
-    out = _gemm(eye, parts, dev["code"], rows)
+    out = _gemm(eye, parts, dev["code"], rows, cols, transpose)
     # every output is 1 * w plus exact zeros: the weight's value exactly (a weight of -0, from a
     # negative block scale times the 0 level, sums to +0 with the other zero products)
-    want = w.t().contiguous()
+    want = w if transpose else w.t().contiguous()
     same = out.view(torch.int16) == want.view(torch.int16)
     assert bool((same | ((out == 0) & (want == 0))).all()), int((~same).sum())
 
 
+@pytest.mark.parametrize("transpose", [False, True], ids=["xWt", "dyW"])
 @pytest.mark.parametrize("name,first,count", SLICES)
 @pytest.mark.parametrize("n_tok", [1, 37, 333, 1367])
-def test_matches_fp32_product_of_dequantized_weights(name, first, count, n_tok):
-    print(f"[case] nf4_gemm {name} tokens={n_tok}", flush=True)
+def test_matches_fp32_product_of_dequantized_weights(name, first, count, n_tok, transpose):
+    print(f"[case] nf4_gemm {name} tokens={n_tok} transpose={transpose}", flush=True)
     _ops.load()
     d, dev, w16 = _layer()
-    parts, w, rows, k = _slice(d, dev, w16, first, count)
+    parts, w, rows, cols = _slice(d, dev, w16, first, count)
     g = torch.Generator().manual_seed(n_tok)
+    k = rows if transpose else cols
     x = torch.randn(n_tok, k, generator=g).half().cuda()
-    out = _gemm(x, parts, dev["code"], rows)
-    ref = x.float() @ w.float().t()
+    out = _gemm(x, parts, dev["code"], rows, cols, transpose)
+    ref = x.float() @ (w.float() if transpose else w.float().t())
     torch.testing.assert_close(out.float(), ref, rtol=2 ** -10,
                                atol=2 ** -11 * float(ref.abs().max()))
+    again = _gemm(x, parts, dev["code"], rows, cols, transpose)
+    assert torch.equal(again.view(torch.int16), out.view(torch.int16))
 
 
 def test_row_stride_and_rejects_bad_shapes():
     print("[case] nf4_gemm strides and errors", flush=True)
     _ops.load()
     d, dev, w16 = _layer()
-    parts, w, rows, k = _slice(d, dev, w16, 4, 2)
-    base = torch.randn(300, k + 64).half().cuda()
-    x = base[:, 32:32 + k]  # row stride k + 64
+    parts, w, rows, cols = _slice(d, dev, w16, 4, 2)
+    base = torch.randn(300, cols + 64).half().cuda()
+    x = base[:, 32:32 + cols]  # row stride cols + 64
     out = torch.empty(300, 2 * rows, dtype=torch.float16, device="cuda")[:, rows:]
-    torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], dev["code"], parts["absmax2"],
-                            parts["offset2"], rows, 64, 256, out)
+    _gemm(x, parts, dev["code"], rows, cols, False, out=out)
     ref = x.float() @ w.float().t()
     torch.testing.assert_close(out.float(), ref, rtol=2 ** -10,
                                atol=2 ** -11 * float(ref.abs().max()))
-    with pytest.raises(ValueError):
+    ws = torch.empty(0, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):  # block size
         torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], dev["code"],
-                                parts["absmax2"], parts["offset2"], rows, 128, 256, out)
+                                parts["absmax2"], parts["offset2"], rows, cols, False, 128, 256,
+                                out, ws)
+    dy = torch.randn(300, rows).half().cuda()
+    dx = torch.empty(300, cols, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):  # the gate|up input gradient splits K: no workspace given
+        torch.ops.talm.nf4_gemm(dy, parts["packed"], parts["absmax8"], dev["code"],
+                                parts["absmax2"], parts["offset2"], rows, cols, True, 64, 256,
+                                dx, ws)
