@@ -374,28 +374,37 @@ int talm_lora_adamw(const int64_t* table, int32_t n_tensors, int64_t max_numel, 
                     uint16_t* out, void* stream);
 
 /*
- * A product on a weight W [rows, cols] held in the layer group's NF4 form, dequantized inside the
- * GEMM (never written out): packed [rows * cols / 2] (two weights per byte, high nibble first),
- * absmax8 [rows * cols / 64] (the second-level code index of each 64-weight block along a row),
- * code f32 [256], absmax2 / offset2 f32 [rows * cols / 16384] (one per 256 blocks), all starting
- * at the weight's first element (which must start a 16384-weight group).
+ * The decoded absmax of NF4 blocks: out[b] = fl32(fl32(code[absmax8[b]] * absmax2[b / qblock2])
+ * + offset2[b / qblock2]) for b < n_blocks, the scale talm_nf4_group_dequant multiplies block b's
+ * levels by (solution/qgroup.py:82-83, decoded once instead of per element; the frozen base
+ * weights need it once). For talm_nf4_gemm.
+ */
+int talm_nf4_block_scales(const uint8_t* absmax8, const float* code, const float* absmax2,
+                          const float* offset2, int64_t n_blocks, int32_t qblock2, float* out,
+                          void* stream);
+
+/*
+ * A product on a weight W [rows, cols] held in NF4 form, dequantized inside the GEMM (never
+ * written out): packed [rows * cols / 2] (two weights per byte, high nibble first) and scale
+ * f32 [rows * cols / 64] (each 64-weight block's decoded absmax, talm_nf4_block_scales), both
+ * starting at the weight's first element.
  *   transpose == 0: out [n_tokens, rows] = x [n_tokens, cols] W^T  (a projection's forward)
  *   transpose != 0: out [n_tokens, cols] = x [n_tokens, rows] W    (its input gradient)
  * x and out fp16 with row strides ldx / ldo (multiples of 8). The fp16 weights are bit-identical
- * to talm_nf4_group_dequant's; fp32 accumulation. blocksize 64 and blocksize2 256 only; cols a
- * multiple of 64, rows a multiple of 8 (64 with transpose); x / packed / out 16-byte aligned.
- * When the output has too few tiles to fill the chip the reduction is split: the workspace
- * (talm_nf4_gemm_workspace bytes, 0 when none is needed, -1 for an unsupported shape) holds the
- * fp32 partials, summed in a fixed order (deterministic). Replaces the dequantization of the
- * layer's weights plus the projection GEMM on them (solution/qgroup.py:72-99, :346-355;
- * GroupLinear's forward and input gradient) for a projection it serves.
+ * to talm_nf4_group_dequant's; fp32 accumulation. blocksize 64 only; cols a multiple of 64, rows
+ * a multiple of 8 (64 with transpose), rows * cols whole 16384-weight groups below 2^31;
+ * x / packed / out 16-byte aligned. When the output has too few tiles to fill the chip the
+ * reduction is split: the workspace (talm_nf4_gemm_workspace bytes, 0 when none is needed, -1
+ * for an unsupported shape) holds the fp32 partials, summed in a fixed order (deterministic).
+ * Replaces the dequantization of the layer's weights plus the projection GEMM on them
+ * (solution/qgroup.py:72-99, :346-355; GroupLinear's forward and input gradient) for a
+ * projection it serves.
  */
 int64_t talm_nf4_gemm_workspace(int64_t n_tokens, int64_t rows, int64_t cols, int32_t transpose);
 int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_t* packed,
-                  const uint8_t* absmax8, const float* code, const float* absmax2,
-                  const float* offset2, int64_t rows, int64_t cols, int32_t transpose,
-                  int32_t blocksize, int32_t blocksize2, uint16_t* out, int64_t ldo,
-                  void* workspace, int64_t workspace_bytes, void* stream);
+                  const float* scale, int64_t rows, int64_t cols, int32_t transpose,
+                  int32_t blocksize, uint16_t* out, int64_t ldo, void* workspace,
+                  int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

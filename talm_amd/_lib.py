@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -55,8 +55,8 @@ SIGNATURES = {
                       _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
     "talm_lora_mirror": [_P, _I32, _I64, _P, _P],
     "talm_lora_adamw": [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _P, _P, _P, _P, _P, _P],
-    "talm_nf4_gemm": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _P, _I64,
-                      _P, _I64, _P],
+    "talm_nf4_gemm": [_P, _I64, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _I64, _P, _I64, _P],
+    "talm_nf4_block_scales": [_P, _P, _P, _P, _I64, _I32, _P, _P],
     "talm_gemm_splitk": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
 }
 

@@ -239,6 +239,19 @@ int log2_exact(int64_t v) {
   return s;
 }
 
+// scale[b] = block_scale(code[absmax8[b]], absmax2[b / qblock2], offset2[b / qblock2]): the
+// double-quantized absmax of every block decoded once (the values dequant_word multiplies by).
+// Grid (blocks of one second-level block / 256 threads, second-level blocks): no division.
+__global__ __launch_bounds__(kThreads) void nf4_block_scales_kernel(
+    const uint8_t* __restrict__ absmax8, const float* __restrict__ code,
+    const float* __restrict__ absmax2, const float* __restrict__ offset2, int64_t n_blocks,
+    uint32_t qblock2, float* __restrict__ out) {
+  const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+  const int64_t b2 = blockIdx.y, b = b2 * qblock2 + i;
+  if (i >= qblock2 || b >= n_blocks) return;
+  out[b] = block_scale(code[absmax8[b]], absmax2[b2], offset2[b2]);
+}
+
 }  // namespace
 }  // namespace talm
 
@@ -279,6 +292,25 @@ TALM_API int talm_nf4_group_dequant(const uint8_t* packed, const uint8_t* absmax
                      absmax2, offset2, reinterpret_cast<uint4*>(out), n_words, qshift - 3,
                      static_cast<uint32_t>(qblock2), log2_exact(qblock2));
   return check_launch("nf4_group_dequant");
+}
+
+TALM_API int talm_nf4_block_scales(const uint8_t* absmax8, const float* code,
+                                   const float* absmax2, const float* offset2, int64_t n_blocks,
+                                   int32_t qblock2, float* out, void* stream) {
+  if (n_blocks < 0 || qblock2 < 1)
+    return fail(TALM_EINVAL, "nf4_block_scales: n_blocks %lld, qblock2 %d", (long long)n_blocks,
+                qblock2);
+  if (n_blocks == 0) return ok();
+  if (!absmax8 || !code || !absmax2 || !offset2 || !out)
+    return fail(TALM_EINVAL, "nf4_block_scales: null pointer");
+  const int64_t groups = (n_blocks + qblock2 - 1) / qblock2;
+  if (groups > 65535) return fail(TALM_EINVAL, "nf4_block_scales: too many second-level blocks");
+  hipLaunchKernelGGL(nf4_block_scales_kernel,
+                     dim3(static_cast<unsigned>((qblock2 + kThreads - 1) / kThreads),
+                          static_cast<unsigned>(groups)),
+                     dim3(kThreads), 0, as_stream(stream), absmax8, code, absmax2, offset2,
+                     n_blocks, static_cast<uint32_t>(qblock2), out);
+  return check_launch("nf4_block_scales");
 }
 
 TALM_API int talm_nf4_group_dequant_t(const uint8_t* packed, const uint8_t* absmax8,

@@ -630,11 +630,30 @@ void lora_adamw(const Tensor& table, int64_t n_tensors, int64_t max_numel, doubl
 // ------------------------------------------------------------------------------------------
 // Products on the NF4 form of W [rows, cols] (dequantized inside the GEMM): out = x W^T
 // (transpose false: x [N, cols], out [N, rows]) or out = x W (transpose true: x [N, rows],
-// out [N, cols]); the workspace holds split-K partials (talm_nf4_gemm_workspace bytes).
+// out [N, cols]); scale holds the blocks' decoded absmax (nf4_block_scales), the workspace the
+// split-K partials (talm_nf4_gemm_workspace bytes).
 // ------------------------------------------------------------------------------------------
-void nf4_gemm(const Tensor& x, const Tensor& packed, const Tensor& absmax8, const Tensor& code,
-              const Tensor& absmax2, const Tensor& offset2, int64_t rows, int64_t cols,
-              bool transpose, int64_t blocksize, int64_t blocksize2, const Tensor& out,
+void nf4_block_scales(const Tensor& absmax8, const Tensor& code, const Tensor& absmax2,
+                      const Tensor& offset2, int64_t qblock2, const Tensor& out) {
+  for (const Tensor* t : {&absmax8, &code, &absmax2, &offset2, &out})
+    require(t->is_cuda() && t->is_contiguous() && t->device() == out.device(),
+            "nf4_block_scales: operands contiguous on one device");
+  require(absmax8.scalar_type() == at::kByte && code.scalar_type() == at::kFloat &&
+              absmax2.scalar_type() == at::kFloat && offset2.scalar_type() == at::kFloat &&
+              out.scalar_type() == at::kFloat,
+          "nf4_block_scales: absmax8 uint8, code / absmax2 / offset2 / out float32");
+  const int64_t n = out.numel();
+  require(qblock2 > 0 && absmax8.numel() >= n && code.numel() >= 256 &&
+              absmax2.numel() >= (n + qblock2 - 1) / qblock2 && offset2.numel() >= absmax2.numel(),
+          "nf4_block_scales: the inputs do not cover out's blocks");
+  check(talm_nf4_block_scales(as<uint8_t>(absmax8), as<float>(code), as<float>(absmax2),
+                              as<float>(offset2), n, static_cast<int32_t>(qblock2),
+                              as<float>(out), stream_of(out)),
+        "nf4_block_scales");
+}
+
+void nf4_gemm(const Tensor& x, const Tensor& packed, const Tensor& scale, int64_t rows,
+              int64_t cols, bool transpose, int64_t blocksize, const Tensor& out,
               const Tensor& workspace) {
   require_fp16(x, "x");
   require_fp16(out, "out");
@@ -644,23 +663,17 @@ void nf4_gemm(const Tensor& x, const Tensor& packed, const Tensor& absmax8, cons
           "nf4_gemm: x [N, K], out [N, n_out] with unit column stride (K, n_out = cols, rows, "
           "or rows, cols with transpose)");
   const int64_t n = x.size(0);
-  for (const Tensor* t : {&packed, &absmax8, &code, &absmax2, &offset2})
+  for (const Tensor* t : {&packed, &scale, &workspace})
     require(t->is_cuda() && t->is_contiguous() && t->device() == x.device(),
-            "nf4_gemm: packed, absmax8, code, absmax2, offset2 contiguous on x's device");
-  require(packed.scalar_type() == at::kByte && absmax8.scalar_type() == at::kByte &&
-              code.scalar_type() == at::kFloat && absmax2.scalar_type() == at::kFloat &&
-              offset2.scalar_type() == at::kFloat,
-          "nf4_gemm: packed / absmax8 uint8, code / absmax2 / offset2 float32");
-  require(cols % 64 == 0 && packed.numel() >= rows * cols / 2 &&
-              absmax8.numel() >= rows * cols / 64 && code.numel() >= 256 &&
-              absmax2.numel() >= rows * cols / 16384 && offset2.numel() >= rows * cols / 16384,
-          "nf4_gemm: the NF4 buffers do not cover [rows, cols]");
-  require(workspace.is_cuda() && workspace.is_contiguous() && workspace.device() == x.device(),
-          "nf4_gemm: workspace contiguous on x's device");
-  check(talm_nf4_gemm(as<uint16_t>(x), x.stride(0), n, as<uint8_t>(packed), as<uint8_t>(absmax8),
-                      as<float>(code), as<float>(absmax2), as<float>(offset2), rows, cols,
-                      transpose ? 1 : 0, static_cast<int32_t>(blocksize),
-                      static_cast<int32_t>(blocksize2), as<uint16_t>(out), out.stride(0),
+            "nf4_gemm: packed, scale and workspace contiguous on x's device");
+  require(packed.scalar_type() == at::kByte && scale.scalar_type() == at::kFloat,
+          "nf4_gemm: packed uint8, scale float32");
+  require(blocksize > 0 && packed.numel() >= rows * cols / 2 &&
+              scale.numel() >= rows * cols / blocksize,
+          "nf4_gemm: packed / scale do not cover [rows, cols]");
+  check(talm_nf4_gemm(as<uint16_t>(x), x.stride(0), n, as<uint8_t>(packed), as<float>(scale),
+                      rows, cols, transpose ? 1 : 0, static_cast<int32_t>(blocksize),
+                      as<uint16_t>(out), out.stride(0),
                       workspace.numel() ? workspace.data_ptr() : nullptr,
                       workspace.numel() * workspace.element_size(), stream_of(x)),
         "nf4_gemm");
@@ -1070,9 +1083,10 @@ TORCH_LIBRARY(talm, m) {
   m.def("gemm_lib_version() -> int", &gemm_lib_version);
   m.def("gemm_tune(Tensor a, int trans_a, Tensor b, int trans_b, Tensor(a!) d, int m, int n, "
         "int k, int lda, int ldb, int ldd, int reps) -> Tensor");
-  m.def("nf4_gemm(Tensor x, Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
-        "Tensor offset2, int rows, int cols, bool transpose, int blocksize, int blocksize2, "
-        "Tensor(a!) out, Tensor(b!) workspace) -> ()");
+  m.def("nf4_gemm(Tensor x, Tensor packed, Tensor scale, int rows, int cols, bool transpose, "
+        "int blocksize, Tensor(a!) out, Tensor(b!) workspace) -> ()");
+  m.def("nf4_block_scales(Tensor absmax8, Tensor code, Tensor absmax2, Tensor offset2, "
+        "int qblock2, Tensor(a!) out) -> ()");
   m.def("lora_adamw(Tensor table, int n_tensors, int max_numel, float lr, float beta1, "
         "float beta2, float eps, float weight_decay, Tensor step_in, Tensor(a!) step_out, "
         "Tensor? grad_scale, Tensor? found_inf, Tensor(b!) out) -> ()");
@@ -1103,5 +1117,6 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("lora_mirror", &lora_mirror);
   m.impl("gemm_tune", &gemm_tune);
   m.impl("nf4_gemm", &nf4_gemm);
+  m.impl("nf4_block_scales", &nf4_block_scales);
   m.impl("lora_adamw", &lora_adamw);
 }

@@ -37,9 +37,13 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
 using W4Shape = TileShape<256, 256, 64, 2, 2, 4>;
+constexpr int kW4ASlots = 3, kW4BSlots = 2;         // A two steps ahead, B one
+constexpr int kW4ABytes = W4Shape::kAChunks * 16;  // 32 KiB of activations per step
+constexpr int kW4BBytes = W4Shape::kBChunks * 16;  // 32 KiB of fp16 weights per step
+constexpr int kW4Ring = kW4ASlots * kW4ABytes + kW4BSlots * kW4BBytes;
 constexpr int kW4ZS = W4Shape::kBN + 8;  // staged fp16 output row stride (halfs)
-constexpr int kW4Lds = W4Shape::kRing > W4Shape::kBM * kW4ZS * 2 ? W4Shape::kRing
-                                                                 : W4Shape::kBM * kW4ZS * 2;
+constexpr int kW4Lds = kW4Ring > W4Shape::kBM * kW4ZS * 2 ? kW4Ring : W4Shape::kBM * kW4ZS * 2;
+static_assert(kW4Lds <= 160 * 1024, "LDS per CU");
 static_assert(W4Shape::kThreads == 512, "the B mapping assumes 512 threads");
 
 struct W4Args {
@@ -48,10 +52,7 @@ struct W4Args {
   int M, N, K;             // out [M, N], reduction K
   int w_cols;              // W's row length (the NF4 blocks run along it)
   const uint8_t* packed;   // W [rows][w_cols], two weights per byte, high nibble first
-  const uint8_t* absmax8;  // [rows * w_cols / 64]
-  const float* code;       // [256]
-  const float* absmax2;    // [rows * w_cols / 16384]
-  const float* offset2;
+  const float* scale;      // [rows * w_cols / 64]: each 64-weight block's decoded absmax
   uint16_t* out;           // [M][ldo] when parts == 1
   int64_t ldo;
   float* part;             // [parts][M][N] when parts > 1
@@ -122,15 +123,13 @@ __device__ __forceinline__ void w4_dequant_word(uint32_t word, const Nf4Table& t
 template <bool kNN>
 __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a) {
   using S = W4Shape;
-  // one LDS object (the ring / output staging, then the code table): with several,
-  // the compiler tags their accesses with alias scopes and then waits for the ring's
-  // direct-to-LDS loads before every LDS access of the same object
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kW4Lds + 256 * 4];
-  float* const s_code = reinterpret_cast<float*>(smem + kW4Lds);
+  // one LDS object (A ring, B ring; the output staging afterwards): with several, the compiler
+  // tags their accesses with alias scopes and then waits for the ring's direct-to-LDS loads
+  // before every LDS access of the same object
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[kW4Lds];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
-  if (tid < 256) s_code[tid] = a.code[tid];
 
   // row tiles vary fastest, then column tiles, then K parts: tiles in flight on one XCD share
   // the codes of their column tile and K part in its L2
@@ -159,21 +158,11 @@ __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a)
     e_step = static_cast<uint32_t>(S::kBK) * a.w_cols;
   }
   u32x4 bw[2];
-  uint32_t bcode[2];
-  float ba2[2], bo2[2];
-  auto b_load = [&](int r, int kt) {
+  float bscale[2];
+  auto b_load = [&](int r, int kt) {  // two loads: the codes and their block's scale
     const uint32_t e = e0 + e_step * static_cast<uint32_t>(min(kt, nk - 1));
     bw[r] = *reinterpret_cast<const u32x4*>(a.packed + (e >> 1));
-    bcode[r] = a.absmax8[e >> 6];
-    ba2[r] = a.absmax2[e >> 14];
-    bo2[r] = a.offset2[e >> 14];
-  };
-  auto b_table = [&](int r) { return nf4_table(block_scale(s_code[bcode[r]], ba2[r], bo2[r])); };
-  auto b_store = [&](int r, unsigned char* bs) {
-    const Nf4Table table = b_table(r);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      w4_dequant_word<kNN>(bw[r][j], table, reinterpret_cast<uint4*>(bs), tid, j);
+    bscale[r] = a.scale[e >> 6];
   };
 
   Acc<S> acc;
@@ -184,37 +173,45 @@ __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  constexpr int kABytes = S::kAChunks * 16;
-  __syncthreads();  // the code table
-  // Step kt computes slot kt % 2 while A(kt + 1) and the codes of step kt + 2 load and the codes
-  // of step kt + 1 (register set (kt + 1) % 2, loaded a step earlier) are dequantized into the
-  // other slot. Every load of a step is waited for at the next step's top (vmcnt 0), so the
-  // order in which the compiler issues them does not matter. Past the last step the codes loads
-  // and the dequantization still run (B reads the last step's codes into the retired slot).
-  b_load(0, 0);
-  b_load(1, 1);
+  unsigned char* const b_ring = smem + kW4ASlots * kW4ABytes;
+  // Step kt computes A slot kt % 3 and B slot kt % 2 while A(kt + 2) and the codes of step
+  // kt + 2 load and the codes of step kt + 1 (register set (kt + 1) % 2, loaded in the step
+  // before) are dequantized into B slot (kt + 1) % 2. Vector-memory issue order: A(0), codes(0),
+  // A(1), codes(1), then per step A(kt + 2), codes(kt + 2); at step kt's top A(kt) is complete once
+  // at most A(kt + 1) and codes(kt + 1) (6 loads) remain in flight (the codes of step kt were
+  // waited for by the step before, which dequantized them). A is issued past the last step too
+  // (its k window reads zeros into a retired slot), so the count holds to the end.
   la.issue(smem, 0, wave);
-  b_store(0, smem + kABytes);
-  auto step = [&](int kt, int h) {  // step kt = kb + h in slot h
-    unsigned char* const cur = smem + h * S::kStageBytes;
-    unsigned char* const nxt = smem + (h ^ 1) * S::kStageBytes;
-    wait_vmcnt<0>();
-    lds_barrier();  // slot h complete (A landed, B stored); every wavefront is done with slot h ^ 1
-    // (issued behind a branch, as in the other ring kernels: the compiler then adds no wait for
-    // it before this step's LDS reads of the other slot)
-    if (kt + 1 < nk) la.issue(nxt, (kt + 1) * S::kBK, wave);
-    b_load(h, kt + 2);  // set h held the codes of step kt, stored in the step before
-    const Nf4Table table = b_table(h ^ 1);
-    w4_mma<kNN>(reinterpret_cast<const uint4*>(cur), cur + kABytes, acc, lane, wm, wn, [&](int ks) {
-      w4_dequant_word<kNN>(bw[h ^ 1][ks], table, reinterpret_cast<uint4*>(nxt + kABytes), tid, ks);
-    });
-  };
-  int kb = 0;
-  for (; kb + 2 <= nk; kb += 2) {
-    step(kb, 0);
-    step(kb + 1, 1);
+  b_load(0, 0);
+  la.issue(smem + kW4ABytes, S::kBK, wave);
+  b_load(1, 1);
+  {
+    const Nf4Table table = nf4_table(bscale[0]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w4_dequant_word<kNN>(bw[0][j], table, reinterpret_cast<uint4*>(b_ring), tid, j);
   }
-  if (kb < nk) step(kb, 0);
+  auto step = [&](int kt, int h) {  // h = kt % 6: slots and register sets are constants
+    wait_vmcnt<6>();
+    lds_barrier();  // A(kt) landed, B(kt) stored; every wavefront is done with step kt - 1
+    la.issue(smem + ((h + 2) % kW4ASlots) * kW4ABytes, (kt + 2) * S::kBK, wave);
+    b_load(h & 1, kt + 2);  // set h % 2 held the codes of step kt, dequantized in the step before
+    // the loads stay here, a step ahead of their use (the scheduler would sink them to their
+    // first use to shorten the registers' lives)
+    __builtin_amdgcn_sched_barrier(0);
+    const Nf4Table table = nf4_table(bscale[(h + 1) & 1]);
+    uint4* const b_next = reinterpret_cast<uint4*>(b_ring + ((h + 1) & 1) * kW4BBytes);
+    w4_mma<kNN>(reinterpret_cast<const uint4*>(smem + (h % kW4ASlots) * kW4ABytes),
+                b_ring + (h & 1) * kW4BBytes, acc, lane, wm, wn,
+                [&](int ks) { w4_dequant_word<kNN>(bw[(h + 1) & 1][ks], table, b_next, tid, ks); });
+  };
+  for (int kb = 0; kb < nk; kb += 6) {
+#pragma unroll
+    for (int h = 0; h < 6; ++h) {
+      if (kb + h >= nk) break;
+      step(kb + h, h);
+    }
+  }
   __syncthreads();  // every wavefront is done with the ring (and every load has landed)
 
   if (a.parts > 1) {
@@ -282,15 +279,13 @@ TALM_API int64_t talm_nf4_gemm_workspace(int64_t n_tokens, int64_t rows, int64_t
 }
 
 TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_t* packed,
-                           const uint8_t* absmax8, const float* code, const float* absmax2,
-                           const float* offset2, int64_t rows, int64_t cols, int32_t transpose,
-                           int32_t blocksize, int32_t blocksize2, uint16_t* out, int64_t ldo,
-                           void* workspace, int64_t workspace_bytes, void* stream) {
+                           const float* scale, int64_t rows, int64_t cols, int32_t transpose,
+                           int32_t blocksize, uint16_t* out, int64_t ldo, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
   using S = W4Shape;
   const bool nn = transpose != 0;
-  if (blocksize != 64 || blocksize2 != 256)
-    return fail(TALM_EINVAL, "nf4_gemm: blocksizes %d / %d (64 / 256 supported)", blocksize,
-                blocksize2);
+  if (blocksize != 64)
+    return fail(TALM_EINVAL, "nf4_gemm: blocksize %d (64 supported)", blocksize);
   const int64_t n = nn ? cols : rows, k = nn ? rows : cols;
   if (!w4_shape_ok(nn, n_tokens, rows, cols) || ldx < k || ldx % 8 || ldo < n || ldo % 8 ||
       !(S::kBM * ldx * 2 < (int64_t{1} << 31)))
@@ -301,10 +296,9 @@ TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, con
                 (long long)n_tokens, (long long)rows, (long long)cols, nn ? "dy W" : "x W^T",
                 (long long)ldx, (long long)ldo, nn ? 64 : 8);
   if (n_tokens == 0) return ok();
-  if (!x || !packed || !absmax8 || !code || !absmax2 || !offset2 || !out)
-    return fail(TALM_EINVAL, "nf4_gemm: null pointer");
-  if (!aligned(x, 16) || !aligned(packed, 16) || !aligned(out, 16))
-    return fail(TALM_EINVAL, "nf4_gemm: x, packed and out must be 16-byte aligned");
+  if (!x || !packed || !scale || !out) return fail(TALM_EINVAL, "nf4_gemm: null pointer");
+  if (!aligned(x, 16) || !aligned(packed, 16) || !aligned(out, 16) || !aligned(scale, 4))
+    return fail(TALM_EINVAL, "nf4_gemm: x, packed and out must be 16-byte aligned, scale 4-byte");
   const SplitPlan p = w4_plan(n_tokens, n, k);
   if (p.parts > 1) {
     const int64_t need = static_cast<int64_t>(p.parts) * n_tokens * n * 4;
@@ -316,7 +310,7 @@ TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, con
   a.a = x; a.lda = ldx;
   a.M = static_cast<int>(n_tokens); a.N = static_cast<int>(n); a.K = static_cast<int>(k);
   a.w_cols = static_cast<int>(cols);
-  a.packed = packed; a.absmax8 = absmax8; a.code = code; a.absmax2 = absmax2; a.offset2 = offset2;
+  a.packed = packed; a.scale = scale;
   a.out = out; a.ldo = ldo;
   a.part = static_cast<float*>(workspace);
   a.steps_per_part = p.steps_per_part;

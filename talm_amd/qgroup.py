@@ -149,6 +149,7 @@ class LayerGroup:
             .expand((seg.stop - seg.start) // span2) for s, seg in zip(states, segments)])
         self.modules = [weakref.ref(m) for m in modules]
         self._bias_spans = {}
+        self._scales = None
         self.t_layout = self._transposed_layout()
 
     # -- shapes ----------------------------------------------------------------------------------
@@ -262,18 +263,29 @@ class LayerGroup:
                 and segs[0].start % (64 * 256) == 0 and next(iter(cols)) % 64 == 0
                 and rows % 64 == 0 and "qgroup" not in DISABLED)
 
+    def block_scales(self):
+        """Every block's decoded absmax, fp32 [numel / qblock] (one launch, made once: the base
+        weights are frozen; 2.9 MB per Qwen2.5-1.5B layer)."""
+        if self._scales is None:
+            scales = torch.empty(self.numel // self.qblock, dtype=torch.float32,
+                                 device=self.device)
+            torch.ops.talm.nf4_block_scales(self.absmax8, self.code, self.absmax2, self.offset2,
+                                            self.qblock2, scales)
+            self._scales = scales
+        return self._scales
+
     def nf4_gemm(self, x, first, last, transpose, out):
         """out = x W^T (transpose False: the forward) or x W (True: the input gradient) with W the
         [sum of out, in] rows of projections first .. last - 1 read as NF4 codes and dequantized
         inside the GEMM (the same fp16 weights as `span`)."""
         segs = self.segments[first:last]
         rows, cols = sum(seg.shape[0] for seg in segs), segs[0].shape[1]
-        lo, span2 = segs[0].start, self.qblock * self.qblock2
+        lo = segs[0].start
+        scales = self.block_scales()
         ws = torch.empty(_ops.nf4_gemm_workspace_bytes(x.shape[0], rows, cols, transpose),
                          dtype=torch.uint8, device=x.device)
-        torch.ops.talm.nf4_gemm(x, self.packed[lo // 2:], self.absmax8[lo // self.qblock:],
-                                self.code, self.absmax2[lo // span2:], self.offset2[lo // span2:],
-                                rows, cols, transpose, self.qblock, self.qblock2, out, ws)
+        torch.ops.talm.nf4_gemm(x, self.packed[lo // 2:], scales[lo // self.qblock:], rows, cols,
+                                transpose, self.qblock, out, ws)
 
     def dequantize_one(self, idx):
         return self.dequantize(idx, idx + 1).view(self.segments[idx].shape)

@@ -111,7 +111,7 @@ def _losses(trainer, batches):
     return [float(trainer.step(b)) for b in batches]
 
 
-@pytest.mark.parametrize("where", ["fused_head", "qgroup", "addnorm"])
+@pytest.mark.parametrize("where", ["fused_head", "qgroup", "addnorm", "w4a16"])
 def test_failure_inside_the_step_keeps_the_loss_curve(inject, where):
     """A launch failing mid-step: the step's loss stays on the eager path's curve (the
     component's original code computes the rest), the component is off afterwards."""
@@ -123,8 +123,12 @@ def test_failure_inside_the_step_keeps_the_loss_curve(inject, where):
         inject.fail(fused_head, "fused_head_loss")
     elif where == "qgroup":    # the layer's weights come from the per-projection dequant
         inject.fail(qgroup, "launch", on_call=2)
-    else:                      # the add + norm of the second layer runs as add, then norm
+    elif where == "addnorm":   # the add + norm of the second layer runs as add, then norm
         inject.fail(rmsnorm, "launch", on_call=3)
+    else:                      # the gate|up input gradient on the NF4 codes fails in the
+        # backward: that layer's transposed buffer is made again with gate|up in it
+        assert qgroup.W4_BLOCKS
+        inject.fail(qgroup.LayerGroup, "nf4_gemm", on_call=2)
     losses = _losses(trainer, batches)
     print(f"[eager] {eager}\n[{where}] {losses}", flush=True)
     for a, b in zip(losses, eager):

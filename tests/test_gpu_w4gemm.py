@@ -1,5 +1,6 @@
 """talm_nf4_gemm (products on the NF4 form of a weight W [rows, cols], dequantized inside the
-GEMM) on the config-1 layer's packed buffers, in both forms: the forward x W^T and the input
+GEMM from its codes and its blocks' absmax decoded by talm_nf4_block_scales) on the config-1
+layer's packed buffers, in both forms: the forward x W^T and the input
 gradient dy W. With x the identity the output is W^T (forward) or W (input gradient), which must
 equal the grouped dequant kernel's fp16 weights bit for bit (that kernel is pinned to the oracle
 in test_gpu_kernels.py); on random x the output is within one fp16 rounding of the fp32 product
@@ -25,6 +26,9 @@ def _layer():
     w16 = torch.empty(n, dtype=torch.float16, device="cuda")
     torch.ops.talm.nf4_group_dequant(dev["packed"], dev["absmax8"], dev["code"], dev["absmax2"],
                                      dev["offset2"], w16, 64, 256)
+    dev["scale"] = torch.empty(n // 64, dtype=torch.float32, device="cuda")
+    torch.ops.talm.nf4_block_scales(dev["absmax8"], dev["code"], dev["absmax2"], dev["offset2"],
+                                    256, dev["scale"])
     return d, dev, w16
 
 
@@ -34,19 +38,17 @@ def _slice(d, dev, w16, first, count):
     rows = sum(shapes[i][0] for i in range(first, first + count))
     cols = shapes[first][1]
     assert e0 % 16384 == 0
-    parts = dict(packed=dev["packed"][e0 // 2:], absmax8=dev["absmax8"][e0 // 64:],
-                 absmax2=dev["absmax2"][e0 // 16384:], offset2=dev["offset2"][e0 // 16384:])
+    parts = dict(packed=dev["packed"][e0 // 2:], scale=dev["scale"][e0 // 64:])
     return parts, w16[e0:e0 + rows * cols].view(rows, cols), rows, cols
 
 
-def _gemm(x, parts, code, rows, cols, transpose, out=None):
+def _gemm(x, parts, rows, cols, transpose, out=None):
     n_out = cols if transpose else rows
     if out is None:
         out = torch.full((x.shape[0], n_out), float("nan"), dtype=torch.float16, device="cuda")
     ws = torch.empty(_ops.nf4_gemm_workspace_bytes(x.shape[0], rows, cols, transpose),
                      dtype=torch.uint8, device="cuda")
-    torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], code, parts["absmax2"],
-                            parts["offset2"], rows, cols, transpose, 64, 256, out, ws)
+    torch.ops.talm.nf4_gemm(x, parts["packed"], parts["scale"], rows, cols, transpose, 64, out, ws)
     return out
 
 
@@ -59,7 +61,7 @@ def test_identity_input_gives_the_dequantized_weights(name, first, count, transp
     parts, w, rows, cols = _slice(d, dev, w16, first, count)
     k = rows if transpose else cols
     eye = torch.eye(k, dtype=torch.float16, device="cuda")
-    out = _gemm(eye, parts, dev["code"], rows, cols, transpose)
+    out = _gemm(eye, parts, rows, cols, transpose)
     # every output is 1 * w plus exact zeros: the weight's value exactly (a weight of -0, from a
     # negative block scale times the 0 level, sums to +0 with the other zero products)
     want = w if transpose else w.t().contiguous()
@@ -78,11 +80,11 @@ def test_matches_fp32_product_of_dequantized_weights(name, first, count, n_tok, 
     g = torch.Generator().manual_seed(n_tok)
     k = rows if transpose else cols
     x = torch.randn(n_tok, k, generator=g).half().cuda()
-    out = _gemm(x, parts, dev["code"], rows, cols, transpose)
+    out = _gemm(x, parts, rows, cols, transpose)
     ref = x.float() @ (w.float() if transpose else w.float().t())
     torch.testing.assert_close(out.float(), ref, rtol=2 ** -10,
                                atol=2 ** -11 * float(ref.abs().max()))
-    again = _gemm(x, parts, dev["code"], rows, cols, transpose)
+    again = _gemm(x, parts, rows, cols, transpose)
     assert torch.equal(again.view(torch.int16), out.view(torch.int16))
 
 
@@ -94,18 +96,14 @@ def test_row_stride_and_rejects_bad_shapes():
     base = torch.randn(300, cols + 64).half().cuda()
     x = base[:, 32:32 + cols]  # row stride cols + 64
     out = torch.empty(300, 2 * rows, dtype=torch.float16, device="cuda")[:, rows:]
-    _gemm(x, parts, dev["code"], rows, cols, False, out=out)
+    _gemm(x, parts, rows, cols, False, out=out)
     ref = x.float() @ w.float().t()
     torch.testing.assert_close(out.float(), ref, rtol=2 ** -10,
                                atol=2 ** -11 * float(ref.abs().max()))
     ws = torch.empty(0, dtype=torch.uint8, device="cuda")
     with pytest.raises(ValueError):  # block size
-        torch.ops.talm.nf4_gemm(x, parts["packed"], parts["absmax8"], dev["code"],
-                                parts["absmax2"], parts["offset2"], rows, cols, False, 128, 256,
-                                out, ws)
+        torch.ops.talm.nf4_gemm(x, parts["packed"], parts["scale"], rows, cols, False, 128, out, ws)
     dy = torch.randn(300, rows).half().cuda()
     dx = torch.empty(300, cols, dtype=torch.float16, device="cuda")
     with pytest.raises(ValueError):  # the gate|up input gradient splits K: no workspace given
-        torch.ops.talm.nf4_gemm(dy, parts["packed"], parts["absmax8"], dev["code"],
-                                parts["absmax2"], parts["offset2"], rows, cols, True, 64, 256,
-                                dx, ws)
+        torch.ops.talm.nf4_gemm(dy, parts["packed"], parts["scale"], rows, cols, True, 64, dx, ws)
