@@ -174,6 +174,33 @@ def kernel_suite(args, only):
                sets=k)
         del sets, outs
 
+    if want("nf4_gemm"):
+        # the W4A16 dequant-GEMM on config 1's layer as the step runs it: the MLP's gate|up input
+        # gradient dx = [dgate | dup] [W_gate; W_up] read as NF4 codes, at a step's token count
+        from talm_amd import _ops
+
+        d = workloads.nf4_layer()
+        t = {key: d[key].to(dev) for key in ("packed", "absmax8", "code", "absmax2", "offset2")}
+        scale = torch.empty(d["n"] // 64, dtype=torch.float32, device=dev)
+        torch.ops.talm.nf4_block_scales(t["absmax8"], t["code"], t["absmax2"], t["offset2"], 256,
+                                        scale)
+        shapes = d["shapes"]
+        e0 = sum(a * b for a, b in shapes[:4])  # gate's first weight
+        rows, cols, n_tok = shapes[4][0] + shapes[5][0], shapes[4][1], 1312
+        dy = torch.randn(n_tok, rows, generator=torch.Generator().manual_seed(5)).half().to(dev)
+        dx = torch.empty(n_tok, cols, dtype=torch.float16, device=dev)
+        ws = torch.empty(_ops.nf4_gemm_workspace_bytes(n_tok, rows, cols, True),
+                         dtype=torch.uint8, device=dev)
+        packed, sc = t["packed"][e0 // 2:], scale[e0 // 64:]
+
+        def fn(i):
+            torch.ops.talm.nf4_gemm(dy, packed, sc, rows, cols, True, 64, dx, ws)
+
+        record("nf4_gemm_gate_up_dx", timed(fn, 1), flops=2.0 * n_tok * rows * cols,
+               config=f"gate|up input gradient of the config-1 layer on its NF4 codes, "
+                      f"{n_tok} tokens")
+        del t, scale, dy, dx, ws
+
     d2 = workloads.norm_rope() if any(want(x) for x in ("addnorm_fwd", "addnorm_bwd", "rope",
                                                          "stacked", "attn")) else None
     # config 2's shapes, and (with "stacked") the 28 layers' rows in one launch: the per-launch

@@ -60,9 +60,15 @@ struct W4Args {
 };
 
 // The "nn" B tile: [64 k rows][256 columns] fp16, 32 chunks of 16 bytes per row, chunk c of row r
-// at position c ^ 4 (r & 3). A transposing read of one 32 x 16 fragment touches 4 consecutive rows
-// x 4 adjacent chunks per 32-lane phase: positions 4 ((c0 / 4) ^ t) + u, 16 distinct banks groups.
-__device__ __forceinline__ int nn_pos(int row, int chunk) { return row * 32 + (chunk ^ ((row & 3) << 2)); }
+// at position c ^ (4 (r & 3) + (c / 16 + 2 (r & 1)) % 4) (an XOR of the low four bits, so a
+// bijection on each row). gfx950's LDS serves 16 lanes of a 16-byte access, or 32 of an 8-byte
+// one, per phase over 64 four-byte banks: 16 chunk positions mod 16. The dequantization's
+// 16-byte stores (two rows, chunks 4 cc + j of cc = 0..7 per phase) and the transposing 8-byte
+// fragment reads (4 consecutive rows x 4 adjacent chunks per phase) both meet 16 distinct
+// positions mod 16 (the plain c ^ 4 (r & 3) made the stores a 4-way conflict).
+__device__ __forceinline__ int nn_pos(int row, int chunk) {
+  return row * 32 + (chunk ^ ((((chunk >> 4) + 2 * (row & 1)) & 3) | ((row & 3) << 2)));
+}
 
 // One step of the wavefront's 128 x 64 block: per 16-deep slice ks its fragments, its MFMAs, then
 // extra(ks) (the dequantization of the next stage, interleaved so that its VALU work issues
@@ -145,7 +151,9 @@ __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a)
   la.init(a.a + static_cast<int64_t>(m0) * a.lda + k0, a.lda, a.M - m0, nk * S::kBK, wave, lane);
 
   // B: this thread's 16 bytes of codes per step. "nt": weight row n0 + tid / 2 (clamped: the
-  // columns of rows past N are not stored), k half tid % 2. "nn": weight row k0 + 64 kt + tid / 8
+  // columns of rows past N are not stored), k half tid % 2 (a row's 32 bytes of codes in two
+  // adjacent lanes: storing 16 rows' halves per phase is a 2-way LDS bank conflict, and one
+  // row per lane with the halves 256 threads apart measured slower). "nn": weight row k0 + 64 kt + tid / 8
   // (below K: K is a multiple of 64), 32 columns n0 + 32 (tid % 8) (clamped to the last 32 of the
   // row: columns past N are not stored). e0 is the first weight's element index at step 0, e_step
   // the advance per step (rows * cols < 2^31).
