@@ -48,9 +48,10 @@ MEASURED_TRAFFIC = {
     "rope_inplace": 10.1e6,
     "swiglu_fwd": 110.1e6,
     "swiglu_bwd": 183.5e6,
-    "attn_fwd": 14.2e6,
-    "attn_bwd": 56.0e6,  # its three dispatches: dot, the dQ / dK / dV kernel, the reduction
-    "head_ce_fwd_bwd": 4583e6,
+    "attn_fwd": 14.1e6,
+    "attn_bwd": 56.1e6,  # its three dispatches: dot, the dQ / dK / dV kernel, the reduction
+    "nf4_gemm_gate_up_dx": 227.8e6,  # the dequant-GEMM and the reduction of its K parts
+    "head_ce_fwd_bwd": 4587e6,
 }
 
 
