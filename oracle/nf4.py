@@ -71,14 +71,20 @@ def group_dequant(packed, absmax8, code, absmax2, offset2, qblock=64, qblock2=25
     return out
 
 
+def block_scales_np(absmax8, code, absmax2, offset2, qblock2=256):
+    """The decoded absmax of every block, fl32(fl32(code[absmax8] * absmax2) + offset2)
+    (solution/qgroup.py:82-83): what `group_dequant` multiplies block r's levels by."""
+    absmax8 = np.asarray(absmax8)
+    block2 = np.arange(absmax8.size) // qblock2
+    prod = np.asarray(code, np.float32)[absmax8] * np.asarray(absmax2, np.float32)[block2]
+    return (prod + np.asarray(offset2, np.float32)[block2]).astype(np.float32)
+
+
 def group_dequant_np(packed, absmax8, code, absmax2, offset2, qblock=64, qblock2=256):
     """numpy twin of `group_dequant` (float32 ops round one at a time; numpy's float16 cast is
     IEEE round-to-nearest-even)."""
     packed = np.asarray(packed, dtype=np.uint8)
-    rows = np.arange(absmax8.size)
-    block2 = rows // qblock2
-    prod = np.asarray(code, np.float32)[absmax8] * np.asarray(absmax2, np.float32)[block2]
-    scale = (prod + np.asarray(offset2, np.float32)[block2]).astype(np.float32)
+    scale = block_scales_np(absmax8, code, absmax2, offset2, qblock2)
     scale = np.repeat(scale, qblock // 2)
     first = NF4_LEVELS[packed >> 4] * scale
     second = NF4_LEVELS[packed & 15] * scale

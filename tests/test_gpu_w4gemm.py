@@ -52,6 +52,21 @@ def _gemm(x, parts, rows, cols, transpose, out=None):
     return out
 
 
+def test_block_scales_match_the_oracle():
+    """talm_nf4_block_scales: every block's decoded absmax of the config-1 layer, bit for bit the
+    oracle's (the scale the group dequant multiplies the levels by)."""
+    from oracle import nf4 as onf4
+
+    print("[case] nf4_block_scales config-1 layer", flush=True)
+    _ops.load()
+    d, dev, _w16 = _layer()
+    want = onf4.block_scales_np(d["absmax8"].numpy(), d["code"].numpy(), d["absmax2"].numpy(),
+                                d["offset2"].numpy())
+    got = dev["scale"].cpu().numpy()
+    assert got.shape == want.shape
+    assert (got.view("uint32") == want.view("uint32")).all()
+
+
 @pytest.mark.parametrize("transpose", [False, True], ids=["xWt", "dyW"])
 @pytest.mark.parametrize("name,first,count", SLICES)
 def test_identity_input_gives_the_dequantized_weights(name, first, count, transpose):
@@ -107,3 +122,4 @@ def test_row_stride_and_rejects_bad_shapes():
     dx = torch.empty(300, cols, dtype=torch.float16, device="cuda")
     with pytest.raises(ValueError):  # the gate|up input gradient splits K: no workspace given
         torch.ops.talm.nf4_gemm(dy, parts["packed"], parts["scale"], rows, cols, True, 64, dx, ws)
+
