@@ -42,6 +42,15 @@ def patch_qwen2_mlp_inplace():
     """Qwen2MLP.forward as one FusedMLP node on a packed layer group (fused_mlp.py), else through
     the in-place-backward node when gate and up are separate fresh tensors of the same dtype
     (solution/swiglu_inplace.py:50-77)."""
+    install_mlp_forward()
+    ON.add("swiglu_inplace")
+
+
+def install_mlp_forward():
+    """The one Qwen2MLP.forward wrapper of this package. Which node takes a call depends on
+    what is installed (engaged.ON): the FusedMLP node (in save-up mode when mlp_save_up.py is
+    installed and the call records autograd), else, with the in-place patch, the in-place
+    SwiGLU node, else the forward found at install time."""
     from transformers.models.qwen2 import modeling_qwen2
 
     from .patches import _in_chain
@@ -59,6 +68,8 @@ def patch_qwen2_mlp_inplace():
         y = fused_mlp_forward(self, x)
         if y is not None:
             return y
+        if "swiglu_inplace" not in ON:
+            return previous(self, x)
         gate, up = self.gate_proj(x), self.up_proj(x)
         if gate.dtype != up.dtype or gate.data_ptr() == up.data_ptr():
             FELL_BACK["swiglu_inplace"] += 1
@@ -69,4 +80,3 @@ def patch_qwen2_mlp_inplace():
     forward._solution_inplace = True
     forward._previous = previous
     cls.forward = forward
-    ON.add("swiglu_inplace")

@@ -137,6 +137,32 @@ def test_switch_leaves_its_part_out(clean_apply, monkeypatch, switch):
     assert kept <= on, (switch, on)
 
 
+def test_save_up_mode_shares_the_one_mlp_wrapper(clean_apply, monkeypatch):
+    """SOLUTION_MLP_SAVE_UP=1 switches the MLP node's save-up mode on without a second wrapper of
+    Qwen2MLP.forward, also when the in-place MLP patch itself is switched off."""
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from talm_amd import mlp_save_up
+
+    original = modeling_qwen2.Qwen2MLP.forward
+    monkeypatch.setenv("SOLUTION_MLP_SAVE_UP", "1")
+    on = set(patches.apply())
+    assert {"mlp_save_up", "swiglu_inplace"} <= on
+    forward = modeling_qwen2.Qwen2MLP.forward
+    assert forward._previous is original
+    patches.unapply()
+    assert modeling_qwen2.Qwen2MLP.forward is original and "mlp_save_up" not in engaged.ON
+    monkeypatch.setenv("SOLUTION_DISABLE_SWIGLU_INPLACE", "1")
+    on = set(patches.apply())
+    assert "mlp_save_up" in on and "swiglu_inplace" not in on
+    assert modeling_qwen2.Qwen2MLP.forward._previous is original
+    # a call that records no autograd is not the save-up mode's
+    import torch
+
+    x = torch.zeros(2, 8)
+    assert mlp_save_up.save_up_group(object(), x) is None
+
+
 def test_solution_package_is_the_drop_in_name():
     import solution
     import solution.patches
