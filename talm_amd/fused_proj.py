@@ -38,9 +38,12 @@ COUNTS = {"attn": 0, "attn_fallback": 0}
 # id(parameter) -> (parameter, fp32 buffer of its shape). A q|k|v node then writes the weight's
 # gradient into its buffer, overwriting it (every adapter weight gets exactly one contribution
 # per backward), and returns None for that input, so autograd adds nothing into .grad and the
-# buffer needs no clearing first. GRAD_WRITTEN collects the ids written, for the caller to check.
+# buffer needs no clearing first. GRAD_WRITTEN collects the ids written, for the caller to check;
+# GRAD_TWICE the ids written more than once (two nodes feeding one weight: the second write would
+# drop the first contribution, so the caller must not rely on direct delivery).
 GRAD_INTO = {}
 GRAD_WRITTEN = set()
+GRAD_TWICE = set()
 
 
 def _grad_targets(params):
@@ -63,6 +66,8 @@ def _deliver(lora_grads, params):
     for i, (g, buf) in enumerate(zip(lora_grads, _grad_targets(params))):
         if g is None or buf is None:
             continue
+        if id(params[i]) in GRAD_WRITTEN:
+            GRAD_TWICE.add(id(params[i]))
         if g is not buf:
             buf.copy_(g)
         GRAD_WRITTEN.add(id(params[i]))

@@ -16,10 +16,14 @@ it. `GraphedTrainer` captures the forward and backward of the step once per buck
 - the LoRA gradients live in one set of buffers shared by every graph, so 97 buckets hold one
   gradient set, not 97. The q|k|v nodes write each adapter weight's gradient straight into its
   buffer (`fused_proj.GRAD_INTO`: one contribution per weight and backward, so the buffers need
-  no clearing and autograd adds nothing: about 230 fill and add launches fewer per step). If
-  some adapter's gradient does not come from such a node, the bucket is captured again the
-  general way: the graph zeroes the buffers (fill kernels) and the backward accumulates into
-  them. They are handed to the parameters after each replay.
+  no clearing and autograd adds nothing: about 230 fill and add launches fewer per step). That
+  holds only if those nodes are a weight's ONLY contribution. The capture watches for any other:
+  a weight no node wrote, a weight two nodes wrote (the second write would drop the first), or
+  autograd accumulating into a weight's buffer (another path to the weight, such as a penalty
+  term on it in the loss: it would add onto the buffer's stale contents). On any of them the
+  bucket, and every later one, is captured again the general way: the graph zeroes the buffers
+  (fill kernels) and the backward accumulates into them. They are handed to the parameters after
+  each replay.
 
 The optimizer tail stays eager: GradScaler unscale and update, clipping, `AdapterAdamW` and the
 learning-rate schedule. It is about ten launches, and their host cost overlaps the graph's GPU
@@ -106,9 +110,17 @@ class GraphedTrainer:
             p.grad = g
         graph = torch.cuda.CUDAGraph()
         direct = self.direct_grads
+        accumulated, hooks = set(), []
         if direct:
             fused_proj.GRAD_INTO.update((id(p), (p, g)) for p, g in zip(t.params, self.grads))
             fused_proj.GRAD_WRITTEN.clear()
+            fused_proj.GRAD_TWICE.clear()
+            # host-side callbacks (they record, they launch nothing): autograd is about to
+            # accumulate a gradient into a parameter's .grad, i.e. some contribution did not
+            # come through direct delivery (a node that delivered directly hands autograd an
+            # undefined gradient, which reaches the hook as None)
+            hooks = [p.register_hook(lambda g, i=id(p): None if g is None else accumulated.add(i))
+                     for p in t.params]
         try:
             # the pad sequence is shorter than one bucket step (a full bucket when no token is
             # real)
@@ -122,11 +134,18 @@ class GraphedTrainer:
                     t.scaler.scale(out.loss).backward()
         finally:
             fused_proj.GRAD_INTO.clear()
+            for h in hooks:
+                h.remove()
         if self.pool is None:
             self.pool = graph.pool()
-        if direct and any(id(p) not in fused_proj.GRAD_WRITTEN for p in t.params):
-            # some gradient went through autograd into an uncleared buffer: capture this bucket
-            # (and every later one) the general way
+        if direct and (any(id(p) not in fused_proj.GRAD_WRITTEN for p in t.params)
+                       or fused_proj.GRAD_TWICE or accumulated):
+            # some gradient went through autograd into an uncleared buffer, or one weight got two
+            # direct writes: capture this bucket (and every later one) the general way. The
+            # discarded graph is the only user of the memory pool when no other graph was kept:
+            # the pool then goes with it, and the next capture starts a new one
+            if not self.graphs:
+                self.pool = None
             del graph, out
             self.direct_grads = False
             for p, g in zip(t.params, held):

@@ -53,13 +53,26 @@ def _metrics():
                                          m.argmax)]
 
 
-def _run(mode, monkeypatch, bucket=64):
+def _penalize(model, weight, coeff=1e-2):
+    """The loss plus coeff * |weight|^2 (a second autograd path to one LoRA weight, beside the
+    q|k|v node's gradient), through a forward hook on the causal LM."""
+    def hook(_module, _args, _kwargs, output):
+        output.loss = output.loss + coeff * weight.float().square().sum()
+        return output
+
+    return model.register_forward_hook(hook, with_kwargs=True)
+
+
+def _run(mode, monkeypatch, bucket=64, penalty=False):
     """mode: "graph" (GraphedTrainer), "static" (eager steps under the same fixed-shape packing)
     or "eager" (the patched step with host-list packing). Returns (losses, LoRA weights,
-    (replays, buckets) or None, per-step metrics of patches.LAST_STEP)."""
+    (replays, buckets, direct gradient delivery) or None, per-step metrics of
+    patches.LAST_STEP). penalty: a weight-norm term on one adapter weight in the loss."""
     steps = len(LENGTHS)
     model = _model()
     trainer = qlora_model.Trainer(model, steps=steps, fused_adapters=True)
+    if penalty:
+        _penalize(model, trainer.params[1])
     patches.apply()
     monkeypatch.setattr(fused_head, "VOCAB_CHUNK", 384)
     gt = GraphedTrainer(trainer, bucket=bucket, warm_steps=WARM) if mode == "graph" else None
@@ -117,3 +130,21 @@ def test_graphed_step_matches_eager_loss_curve(monkeypatch):
     print(f"[graph] losses {losses}\n[eager] losses {ref_losses}", flush=True)
     for a, b in zip(losses, ref_losses):
         assert abs(a - b) <= 5e-3 * abs(b), (losses, ref_losses)
+
+
+def test_graphed_step_with_a_second_gradient_path_captures_the_general_way(monkeypatch):
+    """A penalty on one LoRA weight in the loss reaches that weight through autograd as well as
+    through the q|k|v node. Direct delivery would drop or stale-add that term, so the capture
+    must notice it and fall back to zeroing and accumulating; the graphed run is then
+    bit-identical to the eager fixed-shape run with the same penalty."""
+    print("[case] graphed step vs eager fixed-shape step with a penalty on one LoRA weight",
+          flush=True)
+    ref_losses, ref_weights, _, _ = _run("static", monkeypatch, 16, penalty=True)
+    losses, weights, (replays, _buckets, direct), _ = _run("graph", monkeypatch, 16,
+                                                            penalty=True)
+    print(f"[graph] losses {losses}\n[static] losses {ref_losses}", flush=True)
+    assert replays == len(LENGTHS) - WARM
+    assert not direct, "the capture kept direct delivery although autograd also fed a weight"
+    assert losses == ref_losses
+    for w, r in zip(weights, ref_weights):
+        assert torch.equal(w, r), (w - r).abs().max().item()

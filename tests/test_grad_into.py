@@ -32,3 +32,17 @@ def test_stale_entry_at_a_reused_id_is_ignored(monkeypatch):
     g = torch.ones(2)
     assert fused_proj._deliver([g], [p]) == [g]
     assert torch.equal(buf, torch.zeros(2)) and not fused_proj.GRAD_WRITTEN
+
+
+def test_second_write_of_one_weight_is_flagged(monkeypatch):
+    """Two nodes feeding one weight: the second direct write would drop the first contribution,
+    so the weight lands in GRAD_TWICE (the graphed step then captures the general way)."""
+    p = torch.zeros(3)
+    buf = torch.zeros(3)
+    monkeypatch.setattr(fused_proj, "GRAD_INTO", {id(p): (p, buf)})
+    monkeypatch.setattr(fused_proj, "GRAD_WRITTEN", set())
+    monkeypatch.setattr(fused_proj, "GRAD_TWICE", set())
+    fused_proj._deliver([torch.ones(3)], [p])
+    assert not fused_proj.GRAD_TWICE
+    fused_proj._deliver([torch.full((3,), 2.0)], [p])
+    assert fused_proj.GRAD_TWICE == {id(p)}
