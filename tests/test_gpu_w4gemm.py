@@ -1,13 +1,20 @@
 """talm_nf4_gemm (products on the NF4 form of a weight W [rows, cols], dequantized inside the
 GEMM from its codes and its blocks' absmax decoded by talm_nf4_block_scales) on the config-1
-layer's packed buffers, in both forms: the forward x W^T and the input
-gradient dy W. With x the identity the output is W^T (forward) or W (input gradient), which must
-equal the grouped dequant kernel's fp16 weights bit for bit (that kernel is pinned to the oracle
-in test_gpu_kernels.py); on random x the output is within one fp16 rounding of the fp32 product
-of those weights, for the q|k|v, o, gate|up and down slices of the layer, ragged token counts and
-the K-split shapes (down forward, gate|up input gradient). A second call on the same buffers is
+layer's packed buffers, in both forms: the forward x W^T and the input gradient dy W.
+
+The expected weights are the C oracle's (oracle.nf4.group_dequant, solution/qgroup.py:72-91),
+computed on the CPU from the same bytes. With x the identity the output is W^T (forward) or W
+(input gradient), which must equal the oracle's fp16 weights bit for bit; on random x the output
+is within one fp16 rounding of the fp32 product of those weights, for the q|k|v, o, gate|up and
+down slices of the layer, ragged token counts and the K-split shapes (down forward, gate|up input
+gradient). Two more weights cover the tiles the config-1 layer never reaches: W [520, 2048]
+(x W^T with 520 output columns: a 256-row weight tile cut at 8 rows) and W [512, 2112] (dy W
+with 2112 output columns: a 256-column tile cut at 64). A second call on the same buffers is
 bit-identical (the split-K partials are summed in a fixed order)."""
 
+import functools
+
+import numpy as np
 import pytest
 import torch
 
@@ -17,15 +24,26 @@ pytestmark = pytest.mark.gpu
 
 # (name, first projection, projections): slices of the packed layer (q, k, v, o, gate, up, down)
 SLICES = [("q|k|v", 0, 3), ("o", 3, 1), ("gate|up", 4, 2), ("down", 6, 1)]
+# weights whose row / column counts are not multiples of the 256-wide tiles (whole 16384-weight
+# groups each): (520 rows, 2048 columns) for x W^T, (512, 2112) for dy W
+RAGGED_SHAPES = ((520, 2048), (512, 2112))
+RAGGED = [("rows520", 0, 1, False), ("cols2112", 1, 1, True)]
 
 
-def _layer():
-    d = workloads.nf4_layer()
+@functools.lru_cache(maxsize=2)
+def _layer(shapes=workloads.LAYER_SHAPES):
+    """(host buffers, device buffers, expected fp16 weights on the device): the weights are the C
+    oracle's, bit patterns computed on the CPU from the bytes the GPU receives."""
+    from oracle import nf4 as onf4
+
+    _ops.load()
+    d = workloads.nf4_layer(shapes=shapes)
     dev = {k: v.cuda() for k, v in d.items() if torch.is_tensor(v)}
     n = d["n"]
-    w16 = torch.empty(n, dtype=torch.float16, device="cuda")
-    torch.ops.talm.nf4_group_dequant(dev["packed"], dev["absmax8"], dev["code"], dev["absmax2"],
-                                     dev["offset2"], w16, 64, 256)
+    bits = onf4.group_dequant(d["packed"].numpy(), d["absmax8"].numpy(), d["code"].numpy(),
+                              d["absmax2"].numpy(), d["offset2"].numpy(), 64, 256)
+    w16 = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.float16).cuda()
+    assert w16.numel() == n
     dev["scale"] = torch.empty(n // 64, dtype=torch.float32, device="cuda")
     torch.ops.talm.nf4_block_scales(dev["absmax8"], dev["code"], dev["absmax2"], dev["offset2"],
                                     256, dev["scale"])
@@ -58,7 +76,6 @@ def test_block_scales_match_the_oracle():
     from oracle import nf4 as onf4
 
     print("[case] nf4_block_scales config-1 layer", flush=True)
-    _ops.load()
     d, dev, _w16 = _layer()
     want = onf4.block_scales_np(d["absmax8"].numpy(), d["code"].numpy(), d["absmax2"].numpy(),
                                 d["offset2"].numpy())
@@ -71,9 +88,11 @@ def test_block_scales_match_the_oracle():
 @pytest.mark.parametrize("name,first,count", SLICES)
 def test_identity_input_gives_the_dequantized_weights(name, first, count, transpose):
     print(f"[case] nf4_gemm identity {name} transpose={transpose}", flush=True)
-    _ops.load()
     d, dev, w16 = _layer()
-    parts, w, rows, cols = _slice(d, dev, w16, first, count)
+    _check_identity(*_slice(d, dev, w16, first, count), transpose)
+
+
+def _check_identity(parts, w, rows, cols, transpose):
     k = rows if transpose else cols
     eye = torch.eye(k, dtype=torch.float16, device="cuda")
     out = _gemm(eye, parts, rows, cols, transpose)
@@ -89,9 +108,11 @@ def test_identity_input_gives_the_dequantized_weights(name, first, count, transp
 @pytest.mark.parametrize("n_tok", [1, 37, 333, 1367])
 def test_matches_fp32_product_of_dequantized_weights(name, first, count, n_tok, transpose):
     print(f"[case] nf4_gemm {name} tokens={n_tok} transpose={transpose}", flush=True)
-    _ops.load()
     d, dev, w16 = _layer()
-    parts, w, rows, cols = _slice(d, dev, w16, first, count)
+    _check_product(*_slice(d, dev, w16, first, count), transpose, n_tok)
+
+
+def _check_product(parts, w, rows, cols, transpose, n_tok):
     g = torch.Generator().manual_seed(n_tok)
     k = rows if transpose else cols
     x = torch.randn(n_tok, k, generator=g).half().cuda()
@@ -103,9 +124,23 @@ def test_matches_fp32_product_of_dequantized_weights(name, first, count, n_tok, 
     assert torch.equal(again.view(torch.int16), out.view(torch.int16))
 
 
+@pytest.mark.parametrize("name,first,count,transpose", RAGGED)
+def test_ragged_weight_tiles_identity(name, first, count, transpose):
+    print(f"[case] nf4_gemm identity ragged {name} transpose={transpose}", flush=True)
+    d, dev, w16 = _layer(RAGGED_SHAPES)
+    _check_identity(*_slice(d, dev, w16, first, count), transpose)
+
+
+@pytest.mark.parametrize("n_tok", [5, 300, 1301])
+@pytest.mark.parametrize("name,first,count,transpose", RAGGED)
+def test_ragged_weight_tiles_product(name, first, count, transpose, n_tok):
+    print(f"[case] nf4_gemm ragged {name} tokens={n_tok} transpose={transpose}", flush=True)
+    d, dev, w16 = _layer(RAGGED_SHAPES)
+    _check_product(*_slice(d, dev, w16, first, count), transpose, n_tok)
+
+
 def test_row_stride_and_rejects_bad_shapes():
     print("[case] nf4_gemm strides and errors", flush=True)
-    _ops.load()
     d, dev, w16 = _layer()
     parts, w, rows, cols = _slice(d, dev, w16, 4, 2)
     base = torch.randn(300, cols + 64).half().cuda()
