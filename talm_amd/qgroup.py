@@ -4,8 +4,11 @@ kernel launch (talm_nf4_group_dequant, talm_amd/csrc/nf4.hip).
 What stays as in the reference (solution/qgroup.py): the launch site `launch(...)` with its
 signature (:94-99), the packing of q, k, v, o, gate, up, down into contiguous packed / absmax8 /
 absmax2 buffers with the modules' parameters turned into views of them (no memory duplicated,
-:148-160), `GroupLinear` (y = x W^T + b, dx = dy W) and `span` (adjacent projections as one
-[sum of out, in] view, for the q|k|v and gate|up GEMMs).
+:148-160), `GroupLinear` (y = x W^T + b, dx = dy W), `span` (adjacent projections as one [sum of out, in]
+view, for the q|k|v and gate|up GEMMs) and `weight` (one projection). The reference's callers
+name the pass first (`span("fwd", first, last)`, `weight("bwd", idx)`, :213, :310) and report
+backward uses (`expected_bwd += 1`, :536); both forms are accepted here, and the pass name and
+the counter are ignored, since nothing is counted (below).
 
 What this build does its own way is the lifetime of the fp16 weights. The reference keeps a
 cache per pass and counts uses (the forward's seven, the backward's expected uses reported by
@@ -151,6 +154,9 @@ class LayerGroup:
         self._bias_spans = {}
         self._scales = None
         self.t_layout = self._transposed_layout()
+        # the reference's count of backward uses (solution/qgroup.py:179, :536): callers written
+        # for it may add to it; nothing here reads it
+        self.expected_bwd = 0
 
     # -- shapes ----------------------------------------------------------------------------------
     @property
@@ -202,6 +208,10 @@ class LayerGroup:
         if "w4a16" in DISABLED:
             return ()
         return tuple(b for b in W4_BLOCKS if self.w4_ok(b[0], b[-1] + 1))
+
+    def dequantize_all(self):
+        """fp16 [numel] of all seven projections (the reference's name, :194)."""
+        return self.dequantize()
 
     def dequantize_t(self, skip=()):
         """The layer's W^T blocks (one launch): block b at blocks[b][0], [in, width] row-major;
@@ -309,10 +319,12 @@ class LayerGroup:
         self.resident()
 
     # -- views -------------------------------------------------------------------------------------
-    def span(self, first, last):
-        """fp16 [sum of out, in] of the adjacent projections first .. last - 1 as one view of the
-        resident buffer; None once "qgroup" is off or when dequantization fails (state.py), and
-        the caller then takes them one at a time with `weight`."""
+    def span(self, *args):
+        """span(first, last) or span(which, first, last) (the reference's form; `which`, "fwd"
+        or "bwd", is ignored): fp16 [sum of out, in] of the adjacent projections first .. last - 1
+        as one view of the resident buffer; None once "qgroup" is off or when dequantization
+        fails (state.py), and the caller then takes them one at a time with `weight`."""
+        first, last = _pass_args(args, 2, "span")
         if "qgroup" in DISABLED:
             return None
         try:
@@ -325,9 +337,11 @@ class LayerGroup:
         rows = sum(seg.shape[0] for seg in segs)
         return buf[segs[0].start:segs[-1].stop].view(rows, segs[0].shape[1])
 
-    def weight(self, idx):
-        """fp16 [out, in] of projection `idx` (the per-projection dequantization once "qgroup"
-        is off: the same values)."""
+    def weight(self, *args):
+        """weight(idx) or weight(which, idx) (the reference's form, `which` ignored): fp16
+        [out, in] of projection `idx` (the per-projection dequantization once "qgroup" is off:
+        the same values)."""
+        (idx,) = _pass_args(args, 1, "weight")
         view = self.span(idx, idx + 1)
         return view if view is not None else self.reference_weight(idx)
 
@@ -350,6 +364,17 @@ class LayerGroup:
                     torch.zeros(seg.shape[0], dtype=torch.float16, device=self.device)
                     for seg in segs])
         return self._bias_spans[key]
+
+
+def _pass_args(args, count, what):
+    """The `count` projection indices of a call that may name the pass first ("fwd" / "bwd", the
+    reference's signature)."""
+    if len(args) == count + 1 and args[0] in ("fwd", "bwd"):
+        args = args[1:]
+    if len(args) != count or not all(isinstance(a, int) for a in args):
+        raise TypeError(f"LayerGroup.{what}: expected {count} projection index(es), optionally "
+                        f"after 'fwd' / 'bwd', got {args!r}")
+    return args
 
 
 def _rows(t):
