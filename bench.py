@@ -304,6 +304,59 @@ def kernel_suite(args, only):
         record("attn_fwd", timed(fwd, 1), flops=2 * unit, config=cfg)
         record("attn_bwd", timed(bwd, 1), flops=5 * unit, config=cfg)
 
+    if want("qkv"):
+        # the fused q|k|v projection with the q and v LoRA adapters (r 16, scaling 2) and the
+        # rotary embedding in place, as the step's attention block runs it (fused_proj.py):
+        # forward = lora_down (t = x [A_q; A_v]^T) + proj_ext ([x | s t] [W | B]^T + b, RoPE);
+        # backward = qkv_bwd_prep (RoPE-back, concatenation) + lora_down (u = s dy B) +
+        # proj_ext (dX = [dcat | u] [W^T | A^T]^T) + lora_wgrad (dA = u^T x, dB = s dy^T t).
+        # Algorithmic FLOPs: forward 2 N H (n_out + 32) + 2 N 16 (n_q + n_v); backward
+        # 2 N (n_out + 32) H + 2 N 16 (n_q + n_v) (u) + 2 N 32 H (dA) + 2 N 16 (n_q + n_v) (dB)
+        from talm_amd import fused_proj
+
+        hdim, sizes, r = 1536, (1536, 256, 256), 16
+        bounds = [0, 1536, 1792, 2048]
+        n_out, n_qv = bounds[-1], sizes[0] + sizes[2]
+        adapters = [(0, 2.0, 0.0), (2, 2.0, 0.0)]
+        n_cfg2 = workloads.norm_rope()["n"] if d2 is None else d2["n"]
+        for n in (n_cfg2, 1312):
+            g = torch.Generator().manual_seed(17)
+            x2 = torch.randn(n, hdim, generator=g).half().to(dev)
+            w = (0.02 * torch.randn(n_out, hdim, generator=g)).half().to(dev)
+            w_t = w.t().contiguous()
+            bias = (0.02 * torch.randn(n_out, generator=g)).half().to(dev)
+            halves = [((0.02 * torch.randn(r, hdim, generator=g)).half().to(dev),
+                       (0.02 * torch.randn(sizes[seg], r, generator=g)).half().to(dev))
+                      for seg, _s, _p in adapters]
+            a_t = torch.cat([a for a, _b in halves], 0).t().contiguous()
+            cos, sin = (t_.to(dev) for t_ in workloads.rope_cos_sin(torch.arange(n) % 512))
+            state = {}
+
+            def fwd(i):
+                state["out"], state["t"] = fused_proj._mfma_forward(
+                    x2, w, bias, bounds, adapters, halves, (cos, sin))
+
+            fwd(0)
+            dqkv = (0.1 * torch.randn(n, n_out, generator=g)).half().to(dev)
+            grads = (dqkv[:, :1536], dqkv[:, 1536:1792], dqkv[:, 1792:])
+            t = state["t"]
+            rest = [t[:, :16], halves[0][0], halves[0][1], t[:, 16:], halves[1][0], halves[1][1]]
+            outs = [torch.empty(r, hdim, dtype=torch.float32, device=dev),
+                    torch.empty(sizes[0], r, dtype=torch.float32, device=dev),
+                    torch.empty(r, hdim, dtype=torch.float32, device=dev),
+                    torch.empty(sizes[2], r, dtype=torch.float32, device=dev)]
+
+            def bwd(i):
+                fused_proj._mfma_backward_core(grads, x2, rest, cos, sin, None, sizes, adapters,
+                                               True, [True] * 4, a_t, outs, w_t)
+
+            cfg = (f"q|k|v + LoRA r16 on q, v + RoPE, N={n} H=1536 (q 1536, k 256, v 256)")
+            f_fwd = 2.0 * n * hdim * (n_out + 2 * r) + 2.0 * n * r * n_qv
+            f_bwd = 2.0 * n * (n_out + 2 * r) * hdim + 4.0 * n * r * n_qv + 2.0 * n * 2 * r * hdim
+            record(f"qkv_lora_fwd_n{n}", timed(fwd, 1), flops=f_fwd, config=cfg)
+            record(f"qkv_lora_bwd_n{n}", timed(bwd, 1), flops=f_bwd, config=cfg)
+            del x2, w, w_t, dqkv, state, outs
+
     if want("swiglu_fwd") or want("swiglu_bwd"):
         d3 = workloads.swiglu_inputs()
         n = d3["gate"].numel()
