@@ -126,6 +126,10 @@ class Trainer:
             self.opt, lambda i: 0.5 * (1.0 + math.cos(math.pi * min(i, steps) / steps)))
         self.scaler = torch.amp.GradScaler("cuda")
         self.max_grad_norm = max_grad_norm
+        # called as grad_hook(trainer, total_norm) after unscaling and clipping (total_norm: the
+        # gradients' norm before clipping), before the optimizer step (where the reference's
+        # parity test records the step's LoRA gradients)
+        self.grad_hook = None
 
     def step(self, batch, next_batch=None):
         """One optimizer step; returns the loss tensor (not synchronized). With `next_batch`, the
@@ -146,7 +150,9 @@ class Trainer:
         """After the backward: unscale, clip, the optimizer step, the scale update, the
         schedule, and the gradients released."""
         self.scaler.unscale_(self.opt)
-        torch.nn.utils.clip_grad_norm_(self.params, self.max_grad_norm)
+        norm = torch.nn.utils.clip_grad_norm_(self.params, self.max_grad_norm)
+        if self.grad_hook is not None:
+            self.grad_hook(self, norm)
         self.scaler.step(self.opt)
         self.scaler.update()
         self.sched.step()

@@ -3,10 +3,26 @@ MLP 8960, 12 query / 2 KV heads of 128, vocabulary 151936, tied embeddings, NF4 
 base, LoRA r16 / alpha 32 on q and v) trained on B4 x S512 right-padded batches (lengths uniform
 in [128, 512]) with AdamW, fp16 autocast and a GradScaler — once through the unpatched eager path
 (transformers + the 4-bit / LoRA layers' own forwards, the padded batch, full logits), once
-through `import solution; solution.apply()` (the reference's entry point): the 64-step loss
-curve of the graph-replayed step (what bench.py times) and a 16-step curve of the eagerly
-packed patched step. Bars (the north star): every step within 0.5% of the eager path, the first
-step within 1e-3."""
+through `import solution; solution.apply()` (the reference's entry point): the 64-step run of the
+graph-replayed step (what bench.py times) and a 16-step run of the eagerly packed patched step.
+
+Bars. On a random-init model fed uniform random tokens the loss sits near ln V at every step and
+LoRA B starts at zero, so a loss-curve bar alone could not see a wrong adapter gradient. The
+runs are therefore also compared where the reference's whole-solution test compares them
+(solution/test_parity.py:958-985):
+- every step's loss within 1e-3 relative of the unpatched run (the north star's 0.5% curve bar
+  is implied; measured gaps are about 2e-5);
+- the LoRA gradients the optimizer receives (unscaled, clipped) at steps 0 and 2 (the first graph
+  replay: steps 0 and 1 are the eager warm-up). Every dB within 1e-2 relative L2 (the
+  reference's bar). dA is exactly zero at step 0 in both runs (B = 0). Later dA = (s dy B)^T x
+  is formed through a B that is still small, and it differs between the runs far more than dB
+  does (measured at step 2: 8.1e-2, where dB differs by 6.7e-3): it is held to the reference's bar
+  for what it produces, the adapter updates, 1e-1 relative L2 (the reference's own solution
+  measured 3% on its updates after 4 steps with its loss within 1e-5,
+  solution/test_parity.py:962-966);
+- each adapter's update after all the steps (final minus initial weights) within 1e-1 relative
+  L2 of the unpatched run's update.
+"""
 
 import pytest
 import torch
@@ -17,18 +33,31 @@ pytestmark = pytest.mark.gpu
 
 STEPS = 64
 SEED_DATA = 7
+GRAD_STEPS = (0, 2)
 
 
 def _curve(mode, steps):
-    """Per-step losses of `steps` optimizer steps. mode: "eager" (unpatched), "graph"
-    (solution.apply() + GraphedTrainer, 16-token buckets) or "patched" (solution.apply(), the
-    eager patched step with host-list packing)."""
+    """(per-step losses, engaged counters, {step: LoRA gradients}, initial adapters, final
+    adapters) of `steps` optimizer steps. mode: "eager" (unpatched), "graph" (solution.apply()
+    + GraphedTrainer, 16-token buckets) or "patched" (solution.apply(), the eager patched step
+    with host-list packing). Tensors are float64 CPU copies in parameter order."""
     import solution
 
     torch.cuda.empty_cache()
     model = qlora_model.build_model(seed=1)
     vocab = model.config.vocab_size
     trainer = qlora_model.Trainer(model, steps=STEPS, fused_adapters=mode != "eager")
+    start = [p.detach().double().cpu() for p in trainer.params]
+    grads, done = {}, [0]
+
+    def record(t, norm):
+        if done[0] in GRAD_STEPS:
+            # the GradScaler's scale of this step and the clipping factor applied to the grads
+            scale = float(t.scaler.get_scale())
+            clip = min(1.0, t.max_grad_norm / (float(norm) + 1e-6))
+            grads[done[0]] = ([p.grad.detach().double().cpu() for p in t.params], scale, clip)
+
+    trainer.grad_hook = record
     runner, graphed = trainer, None
     if mode != "eager":
         solution.apply()
@@ -43,6 +72,7 @@ def _curve(mode, steps):
         for i in range(steps):
             loss = runner.step(batches[i], batches[i + 1] if i + 1 < steps else None)
             losses.append(float(loss))
+            done[0] += 1
             if i % 16 == 15:
                 print(f"[config5 {mode}] step {i + 1}: loss {losses[-1]:.5f}", flush=True)
         ran = dict(engaged.RAN)
@@ -51,38 +81,76 @@ def _curve(mode, steps):
             graphed.close()
         if mode != "eager":
             solution.unapply()
+    final = [p.detach().double().cpu() for p in trainer.params]
     del model, trainer, runner
     torch.cuda.empty_cache()
-    return losses, ran
+    return losses, ran, grads, start, final
 
 
 @pytest.fixture(scope="module")
-def eager_curve():
+def eager_run():
     print("[case] config 5 full size: unpatched eager, 64 steps", flush=True)
-    losses, ran = _curve("eager", STEPS)
-    assert ran.get("fused_head", 0) == 0
-    return losses
+    run = _curve("eager", STEPS)
+    assert run[1].get("fused_head", 0) == 0
+    return run
 
 
-def _assert_on_curve(losses, eager, what):
-    print(f"[{what}] {losses}\n[eager] {eager[:len(losses)]}", flush=True)
-    assert abs(losses[0] - eager[0]) <= 1e-3 * abs(eager[0]), (what, losses[0], eager[0])
-    gaps = [abs(a - b) / abs(b) for a, b in zip(losses, eager)]
+def _rel_l2(x, y):
+    return float((x - y).norm() / y.norm().clamp_min(1e-30))
+
+
+def _assert_on_run(run, eager, what):
+    losses, _ran, grads, start, final = run
+    e_losses, _, e_grads, e_start, e_final = eager
+    print(f"[{what}] {losses}\n[eager] {e_losses[:len(losses)]}", flush=True)
+    gaps = [abs(a - b) / abs(b) for a, b in zip(losses, e_losses)]
     worst = max(range(len(gaps)), key=gaps.__getitem__)
-    print(f"[{what}] max relative gap {gaps[worst]:.2e} at step {worst}", flush=True)
-    assert gaps[worst] <= 5e-3, (what, worst, losses[worst], eager[worst])
+    print(f"[{what}] max relative loss gap {gaps[worst]:.2e} at step {worst}", flush=True)
+    assert gaps[worst] <= 1e-3, (what, worst, losses[worst], e_losses[worst])
+    for a, b in zip(start, e_start):
+        assert torch.equal(a, b), f"{what}: the runs start from different adapters"
+    for step in GRAD_STEPS:
+        if step >= len(losses):
+            continue
+        (ours, _, _), (ref, e_scale, e_clip) = grads[step], e_grads[step]
+        finite = [bool(torch.isfinite(g).all()) for g in ref]
+        assert [bool(torch.isfinite(g).all()) for g in ours] == finite, (what, step)
+        worst = {"A": 0.0, "B": 0.0}
+        zero = []
+        for g, r, ok in zip(ours, ref, finite):
+            if not ok:
+                continue
+            if r.norm() == 0:
+                zero.append(float(g.abs().max()))
+                continue
+            kind = "A" if r.shape[0] == 16 else "B"  # lora_A [16, in], lora_B [out, 16]
+            worst[kind] = max(worst[kind], _rel_l2(g, r))
+        print(f"[{what}] step {step}: LoRA gradients, max relative L2: dA {worst['A']:.2e}, "
+              f"dB {worst['B']:.2e} (loss scale {e_scale:g}, clip {e_clip:.3g}; "
+              f"{len(zero)} exactly zero in the unpatched run)", flush=True)
+        assert worst["B"] <= 1e-2, (what, step, worst)
+        assert worst["A"] <= 1e-1, (what, step, worst)
+        # B = 0 at step 0 makes dA exactly zero in the unpatched run: it must be here too
+        assert all(z == 0.0 for z in zero), (what, step, max(zero))
+        if step == 0:
+            assert len(zero) == len(ref) // 2, (what, len(zero))
+    if len(losses) == len(e_losses):
+        errs = [_rel_l2(f - s, ef - es) for f, s, ef, es in zip(final, start, e_final, e_start)]
+        print(f"[{what}] adapter updates after {len(losses)} steps: max relative L2 "
+              f"{max(errs):.2e}", flush=True)
+        assert max(errs) <= 1e-1, (what, max(errs))
 
 
-def test_graphed_step_matches_eager_curve_64_steps(eager_curve):
+def test_graphed_step_matches_eager_run_64_steps(eager_run):
     print("[case] config 5 full size: solution.apply() + graph replay, 64 steps", flush=True)
-    losses, ran = _curve("graph", STEPS)
+    run = _curve("graph", STEPS)
     for name in ("attn_kernel", "qkv_mfma", "fused_mlp", "adapter_adamw"):
-        assert ran.get(name, 0) > 0, (name, ran)
-    _assert_on_curve(losses, eager_curve, "graph")
+        assert run[1].get(name, 0) > 0, (name, run[1])
+    _assert_on_run(run, eager_run, "graph")
 
 
-def test_eager_patched_step_matches_eager_curve_16_steps(eager_curve):
+def test_eager_patched_step_matches_eager_run_16_steps(eager_run):
     print("[case] config 5 full size: solution.apply(), eager patched step, 16 steps", flush=True)
-    losses, ran = _curve("patched", 16)
-    assert ran.get("fused_head", 0) == 16 and ran.get("unpad", 0) == 16, ran
-    _assert_on_curve(losses, eager_curve, "patched")
+    run = _curve("patched", 16)
+    assert run[1].get("fused_head", 0) == 16 and run[1].get("unpad", 0) == 16, run[1]
+    _assert_on_run(run, eager_run, "patched")
