@@ -133,27 +133,63 @@ def kernel_suite(args, only):
         del src, dst
 
     if want("ceilings"):
-        # what PyTorch's own elementwise kernels reach on the traffic mixes of the bandwidth
-        # kernels (same byte counts, cold buffers rotated like theirs): the practical HBM
-        # ceiling of each mix on this box, next to the 8 TB/s peak
+        # this build's own streaming probes (talm_amd/csrc/bench/stream.hip, libtalm_bench.so) on
+        # the read / write mixes of the bandwidth-bound kernels, at their byte counts, cold
+        # buffers rotated like theirs: 16-byte accesses, 64 items per wavefront and iteration,
+        # ordinary or non-temporal loads / stores, several grid sizes; the best of each mix is
+        # what this chip sustains for it (the ceiling the kernels are compared with)
+        import ctypes
+
+        from talm_amd import build as tbuild
+
+        blib = ctypes.CDLL(str(tbuild.BENCH_LIB))
+        blib.talm_bench_stream.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 6 + [
+            ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
         n_nf4 = 46792704
-        cases = [
-            ("ceiling_fill_0r1w", "write-only fill, 93.6 MB (the NF4 output)", 2 * n_nf4,
-             lambda: {"d": torch.empty(n_nf4, dtype=torch.float16, device=dev)},
-             lambda t: t["d"].fill_(1.0)),
-            ("ceiling_copy_1r1w", "copy of 36.7 MB", 4 * 2048 * 8960,
-             lambda: {"s": torch.ones(2048, 8960, dtype=torch.float16, device=dev),
-                      "d": torch.empty(2048, 8960, dtype=torch.float16, device=dev)},
-             lambda t: t["d"].copy_(t["s"])),
-            ("ceiling_add_2r1w", "c = a + b on [2048, 8960] fp16 (the SwiGLU forward mix)",
-             6 * 2048 * 8960,
-             lambda: {k: torch.ones(2048, 8960, dtype=torch.float16, device=dev) for k in "abc"},
-             lambda t: torch.add(t["a"], t["b"], out=t["c"])),
+        mixes = [  # name, what, reads, writes, write items per read item, items
+            ("ceiling_fill_0r1w", "write-only, 93.6 MB (the NF4 output)", 0, 1, 1,
+             2 * n_nf4 // 16),
+            ("ceiling_nf4_1r4w", "23.4 MB read, 93.6 MB written (the grouped NF4 dequant's mix)",
+             1, 1, 4, n_nf4 // 2 // 16),
+            ("ceiling_copy_1r1w", "copy of 36.7 MB", 1, 1, 1, 2048 * 8960 * 2 // 16),
+            ("ceiling_2r1w", "2 x 36.7 MB read, 36.7 MB written (the SwiGLU forward's mix)",
+             2, 1, 1, 2048 * 8960 * 2 // 16),
+            ("ceiling_3r2w", "3 x 36.7 MB read, 2 x 36.7 MB written (the SwiGLU backward's mix)",
+             3, 2, 1, 2048 * 8960 * 2 // 16),
+            ("ceiling_2r3w", "2 x 100 MB read, 3 x 100 MB written (the 28-layer stacked "
+             "add+RMSNorm forward's mix)", 2, 3, 1, 32676 * 1536 * 2 // 16),
         ]
-        for name, what, nbytes, make, op in cases:
+        for name, what, nr, nw, wr, items in mixes:
+            items -= items % 128
+            nbytes = 16 * items * (nr + nw * wr)
             k = rotation(nbytes)
-            sets = [make() for _ in range(k)]
-            record(name, timed(lambda i: op(sets[i]), k), bytes_=nbytes, config=what, sets=k)
+            sets = [([torch.ones(items * 8, dtype=torch.int16, device=dev) for _ in range(nr)],
+                     [torch.empty(items * 8 * wr, dtype=torch.int16, device=dev)
+                      for _ in range(nw)]) for _ in range(k)]
+            best, by_kind = None, {}
+            for nt in (0, 1):
+                for grid in (0, 1024, 2048, 4096):
+                    def op(i, nt=nt, grid=grid):
+                        srcs, dsts = sets[i]
+                        ptrs = [t.data_ptr() for t in srcs] + [None] * (3 - nr)
+                        outs = [t.data_ptr() for t in dsts] + [None] * (3 - nw)
+                        stream = torch.cuda.current_stream().cuda_stream
+                        st = blib.talm_bench_stream(nr, nw, wr, nt, *ptrs, *outs, items, grid,
+                                                    stream)
+                        if st != 0:
+                            raise RuntimeError(f"talm_bench_stream {name}: status {st}")
+
+                    timing = timed(op, k)
+                    if best is None or timing[0] < best[0][0]:
+                        best = (timing, nt, grid)
+                    kind = "non-temporal" if nt else "plain"
+                    if kind not in by_kind or timing[0] < by_kind[kind][0]:
+                        by_kind[kind] = (timing[0], grid)
+            (timing, nt, grid) = best
+            fracs = ", ".join(f"{kind} {nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS:.3f} (grid "
+                              f"{g or 'one-shot'})" for kind, (ms, g) in by_kind.items())
+            record(name, timing, bytes_=nbytes, sets=k,
+                   config=f"{what}; best of plain / non-temporal accesses x 4 grids: {fracs}")
             del sets
 
     if want("nf4_group"):

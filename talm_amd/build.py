@@ -20,6 +20,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtalm.so"
 OPS_LIB = PKG / "libtalm_torch.so"
+BENCH_LIB = PKG / "libtalm_bench.so"  # bench.py's streaming probes (csrc/bench/), not the product
 INCLUDE = PKG.parent / "include"
 ARCH = "gfx950"
 
@@ -67,7 +68,20 @@ def build(verbose=False):
         raise RuntimeError(f"link of libtalm.so failed:\n{proc.stdout}{proc.stderr}")
     os.replace(tmp, LIB)
     build_ops()
+    build_bench()
     return LIB
+
+
+def build_bench():
+    """Compile csrc/bench/*.hip into libtalm_bench.so (bench.py's HBM streaming probes)."""
+    sources = sorted((CSRC / "bench").glob("*.hip"))
+    tmp = BENCH_LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-shared", *map(str, sources), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build of libtalm_bench.so failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, BENCH_LIB)
+    return BENCH_LIB
 
 
 def build_ops():
