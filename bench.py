@@ -202,13 +202,17 @@ def kernel_suite(args, only):
                                                   "offset2")} for _ in range(k)]
         outs = [torch.empty(d["n"], dtype=torch.float16, device=dev) for _ in range(k)]
 
-        def fn(i):
-            t = sets[i]
-            qgroup.launch(t["packed"], t["absmax8"], t["code"], t["absmax2"], t["offset2"],
-                          None, outs[i], n_rows, 64, 256)
+        for name, streaming in (("nf4_group_dequant", False),
+                                ("nf4_group_dequant_streaming", True)):
+            def fn(i, streaming=streaming):
+                t = sets[i]
+                qgroup.launch(t["packed"], t["absmax8"], t["code"], t["absmax2"], t["offset2"],
+                              None, outs[i], n_rows, 64, 256, streaming=streaming)
 
-        record("nf4_group_dequant", timed(fn, k), bytes_=algo, config="1: Qwen2.5-1.5B layer",
-               sets=k)
+            record(name, timed(fn, k), bytes_=algo, sets=k,
+                   config="1: Qwen2.5-1.5B layer, " + (
+                       "non-temporal stores (talm_nf4_group_dequant_streaming)" if streaming else
+                       "ordinary stores (the training step's: its GEMMs read the layer next)"))
         del sets, outs
 
     if want("nf4_gemm"):

@@ -56,6 +56,19 @@ int talm_nf4_group_dequant(const uint8_t* packed, const uint8_t* absmax8, const 
                            int64_t n_rows, int32_t qblock, int32_t qblock2, void* stream);
 
 /*
+ * talm_nf4_group_dequant with non-temporal stores: the same arguments and the same values, bit
+ * for bit, for an output that is not read again soon (a layer dequantized ahead of its use, or
+ * on its own), so that it does not displace the last-level cache's contents. The training step
+ * uses talm_nf4_group_dequant instead: its GEMMs read the layer right after it is written, from
+ * the last-level cache the ordinary stores fill. Replaces the same reference launch
+ * (solution/qgroup.py:72-99); the reference has one store kind.
+ */
+int talm_nf4_group_dequant_streaming(const uint8_t* packed, const uint8_t* absmax8,
+                                     const float* code, const float* absmax2,
+                                     const float* offset2, uint16_t* out, int64_t n_rows,
+                                     int32_t qblock, int32_t qblock2, void* stream);
+
+/*
  * The same grouped dequantization written transposed, for the backward's input-gradient GEMMs
  * (dX = dY W reads W^T as the k-contiguous operand). No counterpart of its own in the reference,
  * whose backward multiplies by the row-major weight of qgroup.launch (solution/qgroup.py:72-99,

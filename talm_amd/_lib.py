@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -23,6 +23,7 @@ _F32 = ctypes.c_float
 # Every exported entry point with its argument types (all return int status).
 SIGNATURES = {
     "talm_nf4_group_dequant": [_P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P],
+    "talm_nf4_group_dequant_streaming": [_P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P],
     "talm_nf4_group_dequant_t": [_P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _I64, _P],
     "talm_nf4_dequant": [_P, _P, _P, _I64, _I32, _P],
     "talm_rmsnorm": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32, _F32, _I32, _I32,

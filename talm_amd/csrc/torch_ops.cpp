@@ -77,9 +77,9 @@ bool same_shape(const Tensor& t, int64_t rows, int64_t cols) {
 
 // ------------------------------------------------------------------------------------------
 
-void nf4_group_dequant(const Tensor& packed, const Tensor& absmax8, const Tensor& code,
-                       const Tensor& absmax2, const Tensor& offset2, const Tensor& out,
-                       int64_t qblock, int64_t qblock2) {
+void nf4_group_dequant_impl(const Tensor& packed, const Tensor& absmax8, const Tensor& code,
+                            const Tensor& absmax2, const Tensor& offset2, const Tensor& out,
+                            int64_t qblock, int64_t qblock2, bool streaming) {
   require(packed.scalar_type() == at::kByte && absmax8.scalar_type() == at::kByte,
           "packed/absmax8: uint8");
   require(code.scalar_type() == at::kFloat && absmax2.scalar_type() == at::kFloat &&
@@ -94,11 +94,23 @@ void nf4_group_dequant(const Tensor& packed, const Tensor& absmax8, const Tensor
           "packed / out sizes do not match n_rows * qblock");
   require(absmax2.numel() * qblock2 >= n_rows && offset2.numel() == absmax2.numel(),
           "absmax2 / offset2 do not cover every block");
-  check(talm_nf4_group_dequant(as<uint8_t>(packed), as<uint8_t>(absmax8), as<float>(code),
-                               as<float>(absmax2), as<float>(offset2), as<uint16_t>(out), n_rows,
-                               static_cast<int32_t>(qblock), static_cast<int32_t>(qblock2),
-                               stream_of(out)),
-        "nf4_group_dequant");
+  auto entry = streaming ? talm_nf4_group_dequant_streaming : talm_nf4_group_dequant;
+  check(entry(as<uint8_t>(packed), as<uint8_t>(absmax8), as<float>(code), as<float>(absmax2),
+              as<float>(offset2), as<uint16_t>(out), n_rows, static_cast<int32_t>(qblock),
+              static_cast<int32_t>(qblock2), stream_of(out)),
+        streaming ? "nf4_group_dequant_streaming" : "nf4_group_dequant");
+}
+
+void nf4_group_dequant(const Tensor& packed, const Tensor& absmax8, const Tensor& code,
+                       const Tensor& absmax2, const Tensor& offset2, const Tensor& out,
+                       int64_t qblock, int64_t qblock2) {
+  nf4_group_dequant_impl(packed, absmax8, code, absmax2, offset2, out, qblock, qblock2, false);
+}
+
+void nf4_group_dequant_streaming(const Tensor& packed, const Tensor& absmax8, const Tensor& code,
+                                 const Tensor& absmax2, const Tensor& offset2, const Tensor& out,
+                                 int64_t qblock, int64_t qblock2) {
+  nf4_group_dequant_impl(packed, absmax8, code, absmax2, offset2, out, qblock, qblock2, true);
 }
 
 // W^T of projections of a packed layer: segs holds (start, rows, cols, dst, ld) per projection.
@@ -1041,6 +1053,8 @@ Tensor gemm_tune(const Tensor& a, int64_t trans_a, const Tensor& b, int64_t tran
 TORCH_LIBRARY(talm, m) {
   m.def("nf4_group_dequant(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
         "Tensor offset2, Tensor(a!) out, int qblock, int qblock2) -> ()");
+  m.def("nf4_group_dequant_streaming(Tensor packed, Tensor absmax8, Tensor code, "
+        "Tensor absmax2, Tensor offset2, Tensor(a!) out, int qblock, int qblock2) -> ()");
   m.def("nf4_group_dequant_t(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
         "Tensor offset2, int[] segs, Tensor(a!) out, int qblock, int qblock2) -> ()");
   m.def("nf4_dequant(Tensor packed, Tensor absmax, Tensor(a!) out, int blocksize) -> ()");
@@ -1094,6 +1108,7 @@ TORCH_LIBRARY(talm, m) {
 
 TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("nf4_group_dequant", &nf4_group_dequant);
+  m.impl("nf4_group_dequant_streaming", &nf4_group_dequant_streaming);
   m.impl("nf4_group_dequant_t", &nf4_group_dequant_t);
   m.impl("gemm_splitk", &gemm_splitk);
   m.impl("nf4_dequant", &nf4_dequant);

@@ -69,14 +69,19 @@ T_BLOCKS = ((0, 1, 2), (3,), (4, 5), (6,))
 W4_BLOCKS = ((4, 5),) if os.environ.get("SOLUTION_DISABLE_W4A16") != "1" else ()
 
 
-def launch(packed, absmax8, code, absmax2, offset2, levels, out, n_rows, qblock, qblock2):
+def launch(packed, absmax8, code, absmax2, offset2, levels, out, n_rows, qblock, qblock2,
+           streaming=False):
     """The one launch site of the grouped kernel: `out` is the contiguous fp16 output of
     `n_rows` absmax blocks of `qblock` weights (solution/qgroup.py:94-99). `levels` is accepted
-    for the reference's signature; the kernel holds the NF4 table itself."""
+    for the reference's signature; the kernel holds the NF4 table itself. `streaming`: write with
+    non-temporal stores (talm_nf4_group_dequant_streaming, the same values) for an output that
+    is not read again soon; the layer group's own dequantization, read by the GEMMs right
+    after, keeps the ordinary stores."""
     del levels
-    torch.ops.talm.nf4_group_dequant(packed[:n_rows * qblock // 2], absmax8[:n_rows], code,
-                                     absmax2, offset2, out.view(-1)[:n_rows * qblock],
-                                     int(qblock), int(qblock2))
+    op = torch.ops.talm.nf4_group_dequant_streaming if streaming \
+        else torch.ops.talm.nf4_group_dequant
+    op(packed[:n_rows * qblock // 2], absmax8[:n_rows], code, absmax2, offset2,
+       out.view(-1)[:n_rows * qblock], int(qblock), int(qblock2))
 
 
 def release():

@@ -97,8 +97,9 @@ def test_nf4_kernels_have_no_fused_multiply_add():
         text = asm.read_text()
     bodies = re.findall(r"^(_Z\w*nf4_\w+_kernel\w*):[^\n]*\n(.*?)^\.Lfunc_end", text,
                         flags=re.S | re.M)
-    # group (chunks x 2, words, transposed x 2), per-projection (words, bytes), block scales
-    assert len(bodies) == 8
+    # group (chunks x 4: two second-level layouts x two store kinds; words; transposed x 2),
+    # per-projection (words, bytes), block scales
+    assert len(bodies) == 10
     for name, body in bodies:
         if "block_scales" not in name:
             assert "v_cvt_pk_f16_f32" in body or "v_cvt_f16_f32" in body, name

@@ -26,10 +26,13 @@ def _case(msg):
 
 # ----------------------------------------------------------------------------------- NF4 -----
 
-def test_nf4_group_dequant_config1_bit_exact():
+@pytest.mark.parametrize("streaming", [False, True], ids=["cached", "streaming"])
+def test_nf4_group_dequant_config1_bit_exact(streaming):
     """Config 1: one Qwen2.5-1.5B layer (46,792,704 weights) in one launch, bit for bit the
-    oracle (solution/qgroup.py:72-91); every projection slice launched alone too."""
-    _case("nf4 group config1")
+    oracle (solution/qgroup.py:72-91); every projection slice launched alone too. Both store
+    kinds (the step's ordinary stores and the streaming entry point's non-temporal ones); the
+    persistent grid walks about two tiles per wavefront here."""
+    _case(f"nf4 group config1 streaming={streaming}")
     d = workloads.nf4_layer()
     ref = nf4_oracle.group_dequant(d["packed"].numpy(), d["absmax8"].numpy(), d["code"].numpy(),
                                    d["absmax2"].numpy(), d["offset2"].numpy())
@@ -37,7 +40,7 @@ def test_nf4_group_dequant_config1_bit_exact():
     n_rows = d["absmax8"].numel()
     out = torch.full((d["n"],), float("nan"), dtype=torch.float16, device=DEV)
     qgroup.launch(t["packed"], t["absmax8"], t["code"], t["absmax2"], t["offset2"], None, out,
-                  n_rows, 64, 256)
+                  n_rows, 64, 256, streaming=streaming)
     got = f16_bits(out)
     assert got.shape == ref.shape
     bad = np.flatnonzero(got != ref)
@@ -48,7 +51,7 @@ def test_nf4_group_dequant_config1_bit_exact():
         r0, b0 = start // 64, start // (64 * 256)
         one = torch.empty(n, dtype=torch.float16, device=DEV)
         qgroup.launch(t["packed"][start // 2:], t["absmax8"][r0:], t["code"], t["absmax2"][b0:],
-                      t["offset2"][b0:], None, one, n // 64, 64, 256)
+                      t["offset2"][b0:], None, one, n // 64, 64, 256, streaming=streaming)
         assert np.array_equal(f16_bits(one), ref[start:start + n]), (rows, cols)
         start += n
 
@@ -116,14 +119,17 @@ def test_nf4_group_dequant_transposed_partial_tiles(rows, cols):
     assert np.all(np.isnan(rest[:, :o_off])) and np.all(np.isnan(rest[:, o_off + rows:]))
 
 
+@pytest.mark.parametrize("streaming", [False, True], ids=["cached", "streaming"])
 @pytest.mark.parametrize("n_rows,qblock,qblock2,shift", [
     (256, 64, 256, 0), (1, 8, 1, 0), (37, 128, 5, 0), (1000, 64, 3, 0), (2, 4096, 1, 0),
-    (33, 32, 7, 0), (1000, 64, 256, 4), (77, 16, 3, 0)])
-def test_nf4_group_dequant_edge_shapes(n_rows, qblock, qblock2, shift):
+    (33, 32, 7, 0), (1000, 64, 256, 4), (77, 16, 3, 0), (400001, 64, 256, 0)])
+def test_nf4_group_dequant_edge_shapes(n_rows, qblock, qblock2, shift, streaming):
     """Partial last workgroup and wavefront, odd second-level blocks, blocks of 8 to 4096
     weights (16-byte chunks of codes from 32 up, 8-weight words below), codes that start 4
-    bytes past a 16-byte boundary (`shift`: the word path); subnormal-producing scales."""
-    _case(f"nf4 group rows={n_rows} qblock={qblock} qblock2={qblock2} shift={shift}")
+    bytes past a 16-byte boundary (`shift`: the word path); subnormal-producing scales; 400001
+    blocks: more tiles than the persistent grid's wavefronts, the last tile holding 2 chunks."""
+    _case(f"nf4 group rows={n_rows} qblock={qblock} qblock2={qblock2} shift={shift} "
+          f"streaming={streaming}")
     g = torch.Generator().manual_seed(n_rows + qblock)
     n = n_rows * qblock
     n2 = -(-n_rows // qblock2)
@@ -137,8 +143,10 @@ def test_nf4_group_dequant_edge_shapes(n_rows, qblock, qblock2, shift):
     out = torch.empty(n, dtype=torch.float16, device=DEV)
     dev_packed = torch.empty(n // 2 + shift, dtype=torch.uint8, device=DEV)[shift:]
     dev_packed.copy_(packed)
-    torch.ops.talm.nf4_group_dequant(dev_packed, absmax8.to(DEV), code.to(DEV),
-                                     absmax2.to(DEV), offset2.to(DEV), out, qblock, qblock2)
+    op = torch.ops.talm.nf4_group_dequant_streaming if streaming \
+        else torch.ops.talm.nf4_group_dequant
+    op(dev_packed, absmax8.to(DEV), code.to(DEV), absmax2.to(DEV), offset2.to(DEV), out, qblock,
+       qblock2)
     assert np.array_equal(f16_bits(out), ref)
 
 
