@@ -14,6 +14,12 @@ constexpr int kThreads = 256;            // four rows per workgroup
 constexpr int kRowsPerBlock = kThreads / kWave;
 constexpr int kMaxChunks = 8;            // vector path: rows up to 8 * 8 * 64 = 4096 columns
 
+// Row operands are read with the non-temporal hint (each is read once; on gfx950 hinted loads
+// stream from HBM faster, as measured on the SwiGLU kernels' mixes); the weight, which every row
+// reads, and all stores stay ordinary.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <typename T>
 struct IO;
 
@@ -22,6 +28,12 @@ struct IO<float> {
   static __device__ __forceinline__ void load8(const float* p, float* v) {
     const float4 a = reinterpret_cast<const float4*>(p)[0];
     const float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void load8_nt(const float* p, float* v) {
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + 1);
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
   }
@@ -37,6 +49,11 @@ template <>
 struct IO<uint16_t> {
   static __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
     const uint4 a = *reinterpret_cast<const uint4*>(p);
+    v[0] = lo_f(a.x); v[1] = hi_f(a.x); v[2] = lo_f(a.y); v[3] = hi_f(a.y);
+    v[4] = lo_f(a.z); v[5] = hi_f(a.z); v[6] = lo_f(a.w); v[7] = hi_f(a.w);
+  }
+  static __device__ __forceinline__ void load8_nt(const uint16_t* p, float* v) {
+    const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     v[0] = lo_f(a.x); v[1] = hi_f(a.x); v[2] = lo_f(a.y); v[3] = hi_f(a.y);
     v[4] = lo_f(a.z); v[5] = hi_f(a.z); v[6] = lo_f(a.w); v[7] = hi_f(a.w);
   }
@@ -68,11 +85,11 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const XT* __restrict__ a
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int c = min(lane + kWave * i, n_chunks - 1);
-    IO<XT>::load8(a + at + 8 * c, x[i]);
+    IO<XT>::load8_nt(a + at + 8 * c, x[i]);
     IO<WT>::load8(w + 8 * c, wv[i]);
     if constexpr (ADD) {
       float pv[8];
-      IO<OT>::load8(p + at + 8 * c, pv);
+      IO<OT>::load8_nt(p + at + 8 * c, pv);
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[i][e] += pv[e];
     }
@@ -126,10 +143,10 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(XT* __restrict__ a, OT* 
   for (int i = 0; i < NC; ++i) {
     const int c = min(lane + kWave * i, n_chunks - 1);
     float wv[8];
-    IO<OT>::load8(h + at + 8 * c, g[i]);
-    IO<OT>::load8(xhat + at + 8 * c, xh[i]);
+    IO<OT>::load8_nt(h + at + 8 * c, g[i]);
+    IO<OT>::load8_nt(xhat + at + 8 * c, xh[i]);
     IO<WT>::load8(w + 8 * c, wv);
-    if constexpr (ADD) IO<XT>::load8(q + at + 8 * c, ds[i]);
+    if constexpr (ADD) IO<XT>::load8_nt(q + at + 8 * c, ds[i]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) g[i][e] *= wv[e];
   }

@@ -63,8 +63,13 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const uint16_t* q, const
   const bool bwd = backward != 0;
   if constexpr (VEC) {
     const int d = 8 * c;
-    const uint4 a = *reinterpret_cast<const uint4*>(src + d);
-    const uint4 b = *reinterpret_cast<const uint4*>(src + g.half + d);
+    // q / k with the non-temporal hint (read once, then written in place); cos / sin, which the
+    // token's 14 heads share, ordinary
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 av = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + d));
+    const u32x4 bv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + g.half + d));
+    const uint4 a = make_uint4(av.x, av.y, av.z, av.w);
+    const uint4 b = make_uint4(bv.x, bv.y, bv.z, bv.w);
     float c1[8], c2[8], s1[8], s2[8];
     load8f(cs + d, c1);
     load8f(cs + g.half + d, c2);
