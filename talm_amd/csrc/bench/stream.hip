@@ -1,7 +1,8 @@
 // Streaming probes for bench.py (not part of libtalm.so): the HBM rate this chip reaches for the
 // read / write mixes of the bandwidth-bound kernels, written the way those kernels are (16-byte
 // accesses, 64 consecutive 16-byte items per wavefront and iteration, two iterations in flight),
-// with ordinary or non-temporal loads and stores. Each mix moves R reads and W * WR writes of 16
+// with ordinary or non-temporal loads and stores (both ordinary, both non-temporal, or
+// non-temporal loads with ordinary stores: the kind the package's bandwidth kernels use). Each mix moves R reads and W * WR writes of 16
 // bytes per item:
 //   (0, 1, 1)  fill                          (1, 1, 1)  copy
 //   (1, 1, 4)  the grouped NF4 dequant's mix (a 16-byte read, 64 bytes written)
@@ -35,7 +36,7 @@ struct StreamArgs {
   int64_t n;  // items (16 bytes of each read stream)
 };
 
-template <int R, int W, int WR, bool kNt>
+template <int R, int W, int WR, bool kNtLoad, bool kNtStore>
 __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
       u32x4 x = {static_cast<uint32_t>(i), 1u, 2u, 3u};
       if (i < a.n) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) x ^= ld<kNt>(a.src[r] + i);
+        for (int r = 0; r < R; ++r) x ^= ld<kNtLoad>(a.src[r] + i);
       }
       v[u] = x;
     }
@@ -60,29 +61,32 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
       for (int w = 0; w < W; ++w)
 #pragma unroll
         for (int j = 0; j < WR; ++j)
-          st<kNt>(a.dst[w] + i0 * WR + j * 64 + lane, v[u] ^ static_cast<uint32_t>(j + w));
+          st<kNtStore>(a.dst[w] + i0 * WR + j * 64 + lane, v[u] ^ static_cast<uint32_t>(j + w));
     }
   }
 }
 
+// nt: 0 ordinary loads and stores, 1 both non-temporal, 2 non-temporal loads, ordinary stores
 template <int R, int W, int WR>
-void launch(const StreamArgs& a, bool nt, int grid, hipStream_t s) {
-  if (nt)
-    hipLaunchKernelGGL((stream_kernel<R, W, WR, true>), dim3(grid), dim3(256), 0, s, a);
+void launch(const StreamArgs& a, int nt, int grid, hipStream_t s) {
+  if (nt == 1)
+    hipLaunchKernelGGL((stream_kernel<R, W, WR, true, true>), dim3(grid), dim3(256), 0, s, a);
+  else if (nt == 2)
+    hipLaunchKernelGGL((stream_kernel<R, W, WR, true, false>), dim3(grid), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL((stream_kernel<R, W, WR, false>), dim3(grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((stream_kernel<R, W, WR, false, false>), dim3(grid), dim3(256), 0, s, a);
 }
 
 }  // namespace
 
-// Runs one mix over n_items 16-byte items (a multiple of 128; every pointer 16-byte aligned, the
+// Runs one mix (nt: the access kinds, see launch) over n_items 16-byte items (a multiple of 128; every pointer 16-byte aligned, the
 // read streams n_items * 16 bytes each, the write streams n_items * 16 * wr bytes each). grid 0:
 // one 128-item group per wavefront (no grid-stride loop). Returns 0, 1 for an unsupported mix or
 // bad arguments, 2 for a launch error.
 TALM_BENCH_API int talm_bench_stream(int reads, int writes, int wr, int nt, const void* s0,
                                      const void* s1, const void* s2, void* d0, void* d1, void* d2,
                                      int64_t n_items, int grid, void* stream) {
-  if (n_items <= 0 || n_items % 128 || grid < 0) return 1;
+  if (n_items <= 0 || n_items % 128 || grid < 0 || nt < 0 || nt > 2) return 1;
   StreamArgs a{};
   const void* src[3] = {s0, s1, s2};
   void* dst[3] = {d0, d1, d2};
@@ -98,7 +102,7 @@ TALM_BENCH_API int talm_bench_stream(int reads, int writes, int wr, int nt, cons
   const int64_t groups = n_items / 128;  // 128 items per wavefront and iteration
   const int g = grid > 0 ? grid : static_cast<int>((groups + 3) / 4);
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const bool t = nt != 0;
+  const int t = nt;
   if (reads == 0 && writes == 1 && wr == 1) launch<0, 1, 1>(a, t, g, s);
   else if (reads == 1 && writes == 1 && wr == 1) launch<1, 1, 1>(a, t, g, s);
   else if (reads == 1 && writes == 1 && wr == 4) launch<1, 1, 4>(a, t, g, s);
