@@ -356,6 +356,30 @@ int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head
                   void* stream);
 
 /*
+ * talm_attn_bwd with the rotary embedding's backward folded into its outputs: q and k are the
+ * rotated projections the forward attended over, and dq / dk come out as the gradients of the
+ * projections BEFORE the rotation, each 128-wide head rotated back on its (d, d + 64) pairs:
+ * dx1 = dy1 c1 + dy2 s2, dx2 = dy2 c2 - dy1 s1 with c / s the token's cos / sin rows (f32
+ * [n_tokens] rows of cs_stride >= 128 elements, a multiple of 4; 16-byte aligned), in fp32
+ * before the one rounding to fp16. dv as talm_attn_bwd. Replaces the attention backward
+ * followed by the rotary backward of q and k (solution/unpad.py:199-294, solution/rope.py:
+ * 145-157).
+ */
+int talm_attn_bwd_rope(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                       const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                       const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                       const uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                       const uint16_t* dout, int64_t do_stride_tok, int64_t do_stride_head,
+                       const float* lse, const int32_t* cu_seqlens, int32_t n_seqs,
+                       int32_t max_seqlen, int64_t n_tokens, int32_t n_q_heads,
+                       int32_t n_kv_heads, int32_t head_dim, float scale, const float* cos,
+                       const float* sin, int64_t cs_stride, uint16_t* dq, int64_t dq_stride_tok,
+                       int64_t dq_stride_head, uint16_t* dk, int64_t dk_stride_tok,
+                       int64_t dk_stride_head, uint16_t* dv, int64_t dv_stride_tok,
+                       int64_t dv_stride_head, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/*
  * fp16 copies of the LoRA adapters' fp32 weights, every adapter in one launch. `table` (device
  * memory, int64, 8-byte aligned) holds 9 entries per tensor: the fp32 weight's address (a
  * row-major contiguous [rows, cols] matrix), its element count, its column count, the element

@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -54,6 +54,9 @@ SIGNATURES = {
     "talm_attn_bwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
                       _I64, _P, _P, _I32, _I32, _I64, _I32, _I32, _I32, _F32, _P, _I64, _I64, _P,
                       _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
+    "talm_attn_bwd_rope": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P,
+                           _I64, _I64, _P, _P, _I32, _I32, _I64, _I32, _I32, _I32, _F32, _P, _P,
+                           _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
     "talm_lora_mirror": [_P, _I32, _I64, _P, _P],
     "talm_lora_adamw": [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _P, _P, _P, _P, _P, _P],
     "talm_nf4_gemm": [_P, _I64, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _I64, _P, _I64, _P],

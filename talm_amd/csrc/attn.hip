@@ -400,7 +400,31 @@ struct BwdArgs {
   int64_t dk_tok, dk_head;
   uint16_t* dv;
   int64_t dv_tok, dv_head;
+  // the rotary embedding's backward folded into the outputs (null: none): cos / sin fp32
+  // [n_tokens][cs_tok], and every 128-wide head of dq and dk is rotated back on its (d, d + 64)
+  // pairs: dx1 = dy1 c1 + dy2 s2, dx2 = dy2 c2 - dy1 s1 (solution/rope.py:145-157)
+  const float* cos;
+  const float* sin;
+  int64_t cs_tok;
 };
+
+// The rotary embedding's backward on one (d, d + 64) pair of four columns each: x = dy at
+// columns d .. d + 3, y at d + 64 .. d + 67, of the token whose cos / sin rows are cr / sr.
+__device__ __forceinline__ void rope_back4(float (&x)[4], float (&y)[4], const float* cr,
+                                          const float* sr, int d) {
+  const float4 c1 = *reinterpret_cast<const float4*>(cr + d);
+  const float4 c2 = *reinterpret_cast<const float4*>(cr + d + kD / 2);
+  const float4 s1 = *reinterpret_cast<const float4*>(sr + d);
+  const float4 s2 = *reinterpret_cast<const float4*>(sr + d + kD / 2);
+  const float cc1[4] = {c1.x, c1.y, c1.z, c1.w}, cc2[4] = {c2.x, c2.y, c2.z, c2.w};
+  const float ss1[4] = {s1.x, s1.y, s1.z, s1.w}, ss2[4] = {s2.x, s2.y, s2.z, s2.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = x[e], b = y[e];
+    x[e] = a * cc1[e] + b * ss2[e];
+    y[e] = b * cc2[e] - a * ss1[e];
+  }
+}
 
 // Dd[h][t] = sum_d dO[t][h][d] * O[t][h][d]: 16 lanes per (token, head), 8 columns each.
 __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(BwdArgs a) {
@@ -565,14 +589,43 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
 
   __syncthreads();  // every wavefront is done with the ring: it becomes the output staging
   uint16_t* os = reinterpret_cast<uint16_t*>(smem) + wave * 32 * kKS;
+  // dQ = scale * the accumulated sum; rows d = 32 j + 8 g + 4 hh + e of block j pair with the
+  // same (g, e) of block j + 2 (d + 64): with cos / sin the rotary backward is applied in fp32
+  // here, before the one rounding to fp16 (row qr: rows past the sequence are not stored)
+  float dqv[kD / 32][16];
+#pragma unroll
+  for (int j = 0; j < kD / 32; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) dqv[j][v] = acc[j][v] * a.scale;
+  if (a.cos) {
+    const float* cr = a.cos + static_cast<int64_t>(s0 + qr) * a.cs_tok;
+    const float* sr = a.sin + static_cast<int64_t>(s0 + qr) * a.cs_tok;
+#pragma unroll
+    for (int j = 0; j < kD / 64; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float x[4], y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[e] = dqv[j][4 * g + e];
+          y[e] = dqv[j + 2][4 * g + e];
+        }
+        rope_back4(x, y, cr, sr, 32 * j + 8 * g + 4 * hh);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dqv[j][4 * g + e] = x[e];
+          dqv[j + 2][4 * g + e] = y[e];
+        }
+      }
+  }
 #pragma unroll
   for (int j = 0; j < kD / 32; ++j)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * j + 8 * g + 4 * hh;
       uint2 w;
-      w.x = pack2(acc[j][4 * g] * a.scale, acc[j][4 * g + 1] * a.scale);
-      w.y = pack2(acc[j][4 * g + 2] * a.scale, acc[j][4 * g + 3] * a.scale);
+      w.x = pack2(dqv[j][4 * g], dqv[j][4 * g + 1]);
+      w.y = pack2(dqv[j][4 * g + 2], dqv[j][4 * g + 3]);
       *reinterpret_cast<uint2*>(&os[l32 * kKS + d0]) = w;
     }
   // the wavefront reads back its own staging rows: its LDS writes complete first
@@ -768,28 +821,46 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_kernel(BwdArgs a) {
     attn_bwd_dkdv<W>(a, rank, smem);
 }
 
-// dK / dV fp16 [token][kv head][d] = sum over the KV head's query heads, in head order.
-__global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // 4 columns each
-  const int64_t total = a.n_tokens * a.n_kv_heads * (kD / 4);
-  if (idx >= total) return;
-  const int c4 = static_cast<int>(idx % (kD / 4));
-  const int64_t tk = idx / (kD / 4);
-  const int kvh = static_cast<int>(tk % a.n_kv_heads);
-  const int64_t t = tk / a.n_kv_heads;
-  float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+// dK / dV fp16 [token][kv head][d] = sum over the KV head's query heads, in head order. A
+// thread takes 4 columns d and, with the rotary backward (a.cos), also their partners d + 64:
+// dK's pairs are rotated back in fp32 before the rounding.
+__device__ __forceinline__ void sum_heads4(const BwdArgs& a, int kvh, int64_t t, int d,
+                                           float (&k)[4], float (&v)[4]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) k[e] = v[e] = 0.f;
   for (int g = 0; g < a.group; ++g) {
     const int h = kvh * a.group + g;
-    const int64_t off = (static_cast<int64_t>(h) * a.n_tokens + t) * kD + 4 * c4;
+    const int64_t off = (static_cast<int64_t>(h) * a.n_tokens + t) * kD + d;
     const float4 xk = *reinterpret_cast<const float4*>(a.dk_part + off);
     const float4 xv = *reinterpret_cast<const float4*>(a.dv_part + off);
-    sk.x += xk.x; sk.y += xk.y; sk.z += xk.z; sk.w += xk.w;
-    sv.x += xv.x; sv.y += xv.y; sv.z += xv.z; sv.w += xv.w;
+    k[0] += xk.x; k[1] += xk.y; k[2] += xk.z; k[3] += xk.w;
+    v[0] += xv.x; v[1] += xv.y; v[2] += xv.z; v[3] += xv.w;
   }
-  *reinterpret_cast<uint2*>(a.dk + t * a.dk_tok + kvh * a.dk_head + 4 * c4) =
-      make_uint2(pack2(sk.x, sk.y), pack2(sk.z, sk.w));
-  *reinterpret_cast<uint2*>(a.dv + t * a.dv_tok + kvh * a.dv_head + 4 * c4) =
-      make_uint2(pack2(sv.x, sv.y), pack2(sv.z, sv.w));
+}
+
+template <bool kRope>
+__global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
+  constexpr int kGroups = kRope ? kD / 8 : kD / 4;  // threads per (token, KV head)
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = a.n_tokens * a.n_kv_heads * kGroups;
+  if (idx >= total) return;
+  const int c4 = static_cast<int>(idx % kGroups);
+  const int64_t tk = idx / kGroups;
+  const int kvh = static_cast<int>(tk % a.n_kv_heads);
+  const int64_t t = tk / a.n_kv_heads;
+  uint16_t* dk = a.dk + t * a.dk_tok + kvh * a.dk_head;
+  uint16_t* dv = a.dv + t * a.dv_tok + kvh * a.dv_head;
+  float k1[4], v1[4];
+  sum_heads4(a, kvh, t, 4 * c4, k1, v1);
+  if constexpr (kRope) {
+    float k2[4], v2[4];
+    sum_heads4(a, kvh, t, 4 * c4 + kD / 2, k2, v2);
+    rope_back4(k1, k2, a.cos + t * a.cs_tok, a.sin + t * a.cs_tok, 4 * c4);
+    *reinterpret_cast<uint2*>(dk + 4 * c4 + kD / 2) = make_uint2(pack2(k2[0], k2[1]), pack2(k2[2], k2[3]));
+    *reinterpret_cast<uint2*>(dv + 4 * c4 + kD / 2) = make_uint2(pack2(v2[0], v2[1]), pack2(v2[2], v2[3]));
+  }
+  *reinterpret_cast<uint2*>(dk + 4 * c4) = make_uint2(pack2(k1[0], k1[1]), pack2(k1[2], k1[3]));
+  *reinterpret_cast<uint2*>(dv + 4 * c4) = make_uint2(pack2(v1[0], v1[1]), pack2(v1[2], v1[3]));
 }
 
 }  // namespace
@@ -854,18 +925,22 @@ TALM_API int64_t talm_attn_bwd_workspace(int64_t n_tokens, int32_t n_q_heads) {
   return dd + 2 * n_tokens * n_q_heads * kD * 4;
 }
 
-TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
-                           const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
-                           const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
-                           const uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
-                           const uint16_t* dout, int64_t do_stride_tok, int64_t do_stride_head,
-                           const float* lse, const int32_t* cu_seqlens, int32_t n_seqs,
-                           int32_t max_seqlen, int64_t n_tokens, int32_t n_q_heads,
-                           int32_t n_kv_heads, int32_t head_dim, float scale, uint16_t* dq,
-                           int64_t dq_stride_tok, int64_t dq_stride_head, uint16_t* dk,
-                           int64_t dk_stride_tok, int64_t dk_stride_head, uint16_t* dv,
-                           int64_t dv_stride_tok, int64_t dv_stride_head, void* workspace,
-                           int64_t workspace_bytes, void* stream) {
+namespace talm {
+namespace {
+
+int attn_bwd_impl(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                  const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                  const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                  const uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                  const uint16_t* dout, int64_t do_stride_tok, int64_t do_stride_head,
+                  const float* lse, const int32_t* cu_seqlens, int32_t n_seqs,
+                  int32_t max_seqlen, int64_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads,
+                  int32_t head_dim, float scale, const float* cos, const float* sin,
+                  int64_t cs_stride, uint16_t* dq, int64_t dq_stride_tok,
+                  int64_t dq_stride_head, uint16_t* dk, int64_t dk_stride_tok,
+                  int64_t dk_stride_head, uint16_t* dv, int64_t dv_stride_tok,
+                  int64_t dv_stride_head, void* workspace, int64_t workspace_bytes,
+                  void* stream) {
   if (head_dim != kD)
     return fail(TALM_EINVAL, "attn_bwd: head_dim %d (only %d)", head_dim, kD);
   if (n_seqs < 0 || max_seqlen < 0 || n_tokens < 0 || n_q_heads < 1 || n_kv_heads < 1 ||
@@ -887,9 +962,15 @@ TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
   if (workspace_bytes < need)
     return fail(TALM_EINVAL, "attn_bwd: workspace of %lld bytes, %lld needed",
                 (long long)workspace_bytes, (long long)need);
+  const bool rope = cos != nullptr || sin != nullptr;
+  if (rope && (cs_stride < kD || cs_stride % 4 || cs_stride >= (int64_t{1} << 24)))
+    return fail(TALM_EINVAL, "attn_bwd: cos / sin row stride %lld (at least %d, a multiple of 4)",
+                (long long)cs_stride, kD);
   if (n_seqs == 0 || max_seqlen == 0 || n_tokens == 0) return ok();
   if (!q || !k || !v || !out || !dout || !lse || !cu_seqlens || !dq || !dk || !dv || !workspace)
     return fail(TALM_EINVAL, "attn_bwd: null pointer");
+  if (rope && (!cos || !sin || !aligned(cos, 16) || !aligned(sin, 16)))
+    return fail(TALM_EINVAL, "attn_bwd: cos and sin both given, 16-byte aligned");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) ||
       !aligned(dout, 16) || !aligned(dq, 16) || !aligned(dk, 8) || !aligned(dv, 8) ||
       !aligned(workspace, 256))
@@ -913,6 +994,7 @@ TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
   a.dq = dq; a.dq_tok = dq_stride_tok; a.dq_head = dq_stride_head;
   a.dk = dk; a.dk_tok = dk_stride_tok; a.dk_head = dk_stride_head;
   a.dv = dv; a.dv_tok = dv_stride_tok; a.dv_head = dv_stride_head;
+  a.cos = rope ? cos : nullptr; a.sin = rope ? sin : nullptr; a.cs_tok = cs_stride;
   const hipStream_t s = as_stream(stream);
   const int64_t rows = n_tokens * n_q_heads;
   hipLaunchKernelGGL(attn_bwd_dot_kernel, dim3(static_cast<unsigned>((rows * 16 + 255) / 256)),
@@ -920,8 +1002,58 @@ TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
   const dim3 grid(static_cast<unsigned>(n_q_heads), static_cast<unsigned>(n_seqs),
                   static_cast<unsigned>(2 * a.n_tiles));
   hipLaunchKernelGGL((attn_bwd_kernel<W>), grid, dim3(64 * W), 0, s, a);
-  const int64_t red = n_tokens * n_kv_heads * (kD / 4);
-  hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3(static_cast<unsigned>((red + 255) / 256)),
-                     dim3(256), 0, s, a);
+  const int64_t red = n_tokens * n_kv_heads * (rope ? kD / 8 : kD / 4);
+  if (rope)
+    hipLaunchKernelGGL(attn_bwd_reduce_kernel<true>, dim3(static_cast<unsigned>((red + 255) / 256)),
+                       dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(attn_bwd_reduce_kernel<false>, dim3(static_cast<unsigned>((red + 255) / 256)),
+                       dim3(256), 0, s, a);
   return check_launch("attn_bwd");
+}
+
+}  // namespace
+}  // namespace talm
+
+TALM_API int talm_attn_bwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                           const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                           const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                           const uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                           const uint16_t* dout, int64_t do_stride_tok, int64_t do_stride_head,
+                           const float* lse, const int32_t* cu_seqlens, int32_t n_seqs,
+                           int32_t max_seqlen, int64_t n_tokens, int32_t n_q_heads,
+                           int32_t n_kv_heads, int32_t head_dim, float scale, uint16_t* dq,
+                           int64_t dq_stride_tok, int64_t dq_stride_head, uint16_t* dk,
+                           int64_t dk_stride_tok, int64_t dk_stride_head, uint16_t* dv,
+                           int64_t dv_stride_tok, int64_t dv_stride_head, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  return attn_bwd_impl(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, v,
+                       v_stride_tok, v_stride_head, out, o_stride_tok, o_stride_head, dout,
+                       do_stride_tok, do_stride_head, lse, cu_seqlens, n_seqs, max_seqlen,
+                       n_tokens, n_q_heads, n_kv_heads, head_dim, scale, nullptr, nullptr, 0, dq,
+                       dq_stride_tok, dq_stride_head, dk, dk_stride_tok, dk_stride_head, dv,
+                       dv_stride_tok, dv_stride_head, workspace, workspace_bytes, stream);
+}
+
+TALM_API int talm_attn_bwd_rope(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                const uint16_t* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                const uint16_t* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                const uint16_t* out, int64_t o_stride_tok, int64_t o_stride_head,
+                                const uint16_t* dout, int64_t do_stride_tok,
+                                int64_t do_stride_head, const float* lse,
+                                const int32_t* cu_seqlens, int32_t n_seqs, int32_t max_seqlen,
+                                int64_t n_tokens, int32_t n_q_heads, int32_t n_kv_heads,
+                                int32_t head_dim, float scale, const float* cos, const float* sin,
+                                int64_t cs_stride, uint16_t* dq, int64_t dq_stride_tok,
+                                int64_t dq_stride_head, uint16_t* dk, int64_t dk_stride_tok,
+                                int64_t dk_stride_head, uint16_t* dv, int64_t dv_stride_tok,
+                                int64_t dv_stride_head, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  if (!cos || !sin) return fail(TALM_EINVAL, "attn_bwd_rope: cos and sin are required");
+  return attn_bwd_impl(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, v,
+                       v_stride_tok, v_stride_head, out, o_stride_tok, o_stride_head, dout,
+                       do_stride_tok, do_stride_head, lse, cu_seqlens, n_seqs, max_seqlen,
+                       n_tokens, n_q_heads, n_kv_heads, head_dim, scale, cos, sin, cs_stride, dq,
+                       dq_stride_tok, dq_stride_head, dk, dk_stride_tok, dk_stride_head, dv,
+                       dv_stride_tok, dv_stride_head, workspace, workspace_bytes, stream);
 }

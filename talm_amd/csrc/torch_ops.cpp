@@ -563,10 +563,12 @@ void attn_fwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& c
         "attn_fwd");
 }
 
-void attn_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out,
-              const Tensor& dout, const Tensor& lse, const Tensor& cu, int64_t max_seqlen,
-              double scale, const Tensor& dq, const Tensor& dk, const Tensor& dv,
-              const Tensor& workspace) {
+// The attention backward; with cos / sin (fp32 [N, >= 128], one row stride) q and k are the
+// rotated projections and dq / dk come out rotated back (the rotary backward folded in).
+void attn_bwd_any(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out,
+                  const Tensor& dout, const Tensor& lse, const Tensor& cu, int64_t max_seqlen,
+                  double scale, const OptTensor& cos, const OptTensor& sin, const Tensor& dq,
+                  const Tensor& dk, const Tensor& dv, const Tensor& workspace) {
   require(q.dim() == 3 && k.dim() == 3, "attn: q [N, Hq, 128], k / v [N, Hkv, 128]");
   const int64_t n = q.size(0), hq = q.size(1), hkv = k.size(1);
   attn_heads(q, "q", n, hq);
@@ -582,18 +584,49 @@ void attn_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& o
               same_shape(lse, hq, n),
           "attn_bwd: lse float32 [Hq, N]");
   require(workspace.is_cuda() && workspace.is_contiguous(), "attn_bwd: workspace");
-  check(talm_attn_bwd(as<uint16_t>(q), q.stride(0), q.stride(1), as<uint16_t>(k), k.stride(0),
-                      k.stride(1), as<uint16_t>(v), v.stride(0), v.stride(1), as<uint16_t>(out),
-                      out.stride(0), out.stride(1), as<uint16_t>(dout), dout.stride(0),
-                      dout.stride(1), as<float>(lse), as<int32_t>(cu),
-                      static_cast<int32_t>(cu.numel() - 1), static_cast<int32_t>(max_seqlen), n,
-                      static_cast<int32_t>(hq), static_cast<int32_t>(hkv), 128,
-                      static_cast<float>(scale), as<uint16_t>(dq), dq.stride(0), dq.stride(1),
-                      as<uint16_t>(dk), dk.stride(0), dk.stride(1), as<uint16_t>(dv),
-                      dv.stride(0), dv.stride(1), workspace.data_ptr(),
-                      workspace.numel() * static_cast<int64_t>(workspace.element_size()),
-                      stream_of(q)),
-        "attn_bwd");
+  const int64_t ws_bytes = workspace.numel() * static_cast<int64_t>(workspace.element_size());
+  if (!cos.has_value()) {
+    check(talm_attn_bwd(as<uint16_t>(q), q.stride(0), q.stride(1), as<uint16_t>(k), k.stride(0),
+                        k.stride(1), as<uint16_t>(v), v.stride(0), v.stride(1), as<uint16_t>(out),
+                        out.stride(0), out.stride(1), as<uint16_t>(dout), dout.stride(0),
+                        dout.stride(1), as<float>(lse), as<int32_t>(cu),
+                        static_cast<int32_t>(cu.numel() - 1), static_cast<int32_t>(max_seqlen), n,
+                        static_cast<int32_t>(hq), static_cast<int32_t>(hkv), 128,
+                        static_cast<float>(scale), as<uint16_t>(dq), dq.stride(0), dq.stride(1),
+                        as<uint16_t>(dk), dk.stride(0), dk.stride(1), as<uint16_t>(dv),
+                        dv.stride(0), dv.stride(1), workspace.data_ptr(), ws_bytes,
+                        stream_of(q)),
+          "attn_bwd");
+    return;
+  }
+  cos_sin_rows(cos, sin, n, "attn_bwd_rope: cos/sin fp32 [N, >= 128] with one row stride");
+  check(talm_attn_bwd_rope(as<uint16_t>(q), q.stride(0), q.stride(1), as<uint16_t>(k),
+                           k.stride(0), k.stride(1), as<uint16_t>(v), v.stride(0), v.stride(1),
+                           as<uint16_t>(out), out.stride(0), out.stride(1), as<uint16_t>(dout),
+                           dout.stride(0), dout.stride(1), as<float>(lse), as<int32_t>(cu),
+                           static_cast<int32_t>(cu.numel() - 1),
+                           static_cast<int32_t>(max_seqlen), n, static_cast<int32_t>(hq),
+                           static_cast<int32_t>(hkv), 128, static_cast<float>(scale),
+                           as<float>(cos), as<float>(sin), cos->stride(0), as<uint16_t>(dq),
+                           dq.stride(0), dq.stride(1), as<uint16_t>(dk), dk.stride(0),
+                           dk.stride(1), as<uint16_t>(dv), dv.stride(0), dv.stride(1),
+                           workspace.data_ptr(), ws_bytes, stream_of(q)),
+        "attn_bwd_rope");
+}
+
+void attn_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out,
+              const Tensor& dout, const Tensor& lse, const Tensor& cu, int64_t max_seqlen,
+              double scale, const Tensor& dq, const Tensor& dk, const Tensor& dv,
+              const Tensor& workspace) {
+  attn_bwd_any(q, k, v, out, dout, lse, cu, max_seqlen, scale, std::nullopt, std::nullopt, dq,
+               dk, dv, workspace);
+}
+
+void attn_bwd_rope(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& out,
+                   const Tensor& dout, const Tensor& lse, const Tensor& cu, int64_t max_seqlen,
+                   double scale, const Tensor& cos, const Tensor& sin, const Tensor& dq,
+                   const Tensor& dk, const Tensor& dv, const Tensor& workspace) {
+  attn_bwd_any(q, k, v, out, dout, lse, cu, max_seqlen, scale, cos, sin, dq, dk, dv, workspace);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1092,6 +1125,9 @@ TORCH_LIBRARY(talm, m) {
   m.def("attn_bwd(Tensor q, Tensor k, Tensor v, Tensor out, Tensor dout, Tensor lse, "
         "Tensor cu_seqlens, int max_seqlen, float scale, Tensor(a!) dq, Tensor(b!) dk, "
         "Tensor(c!) dv, Tensor(d!) workspace) -> ()");
+  m.def("attn_bwd_rope(Tensor q, Tensor k, Tensor v, Tensor out, Tensor dout, Tensor lse, "
+        "Tensor cu_seqlens, int max_seqlen, float scale, Tensor cos, Tensor sin, Tensor(a!) dq, "
+        "Tensor(b!) dk, Tensor(c!) dv, Tensor(d!) workspace) -> ()");
   m.def("lora_mirror(Tensor table, int n_tensors, int max_numel, Tensor(a!) out) -> ()");
   m.def("gemm_algo_table(Tensor rows) -> ()", &gemm_algo_table);
   m.def("gemm_lib_version() -> int", &gemm_lib_version);
@@ -1129,6 +1165,7 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("gemm_ex", &gemm_ex);
   m.impl("attn_fwd", &attn_fwd);
   m.impl("attn_bwd", &attn_bwd);
+  m.impl("attn_bwd_rope", &attn_bwd_rope);
   m.impl("lora_mirror", &lora_mirror);
   m.impl("gemm_tune", &gemm_tune);
   m.impl("nf4_gemm", &nf4_gemm);

@@ -457,7 +457,10 @@ class AttentionBlock(torch.autograd.Function):
     (torch.ops.talm.attn_fwd / attn_bwd) and o_proj on the layer group's weight
     (solution/fused_proj.py:88-218 and :382-445, solution/unpad.py:199-294, solution/qgroup.py:
     346-355). One node instead of FusedProjections + VarlenAttention + GroupLinear and the view
-    nodes between them: the step is bound by the host's launch rate. Same kernels, same values."""
+    nodes between them: the step is bound by the host's launch rate. Same kernels, same values,
+    except that the backward rotates dq / dk back inside the attention backward
+    (torch.ops.talm.attn_bwd_rope) from the fp32 sums, one fp16 rounding instead of two, and
+    hands the projections' backward that output as it is (no separate rotary pass)."""
 
     @staticmethod
     def forward(ctx, x, group, adapters, rope, head_dim, n_heads, n_kv, cu, max_len, scale,
@@ -538,10 +541,18 @@ class AttentionBlock(torch.autograd.Function):
         dv = dqkv[:, bounds[2]:]
         ws = torch.empty(_ops.attn_bwd_workspace_bytes(n_tok, nh), dtype=torch.uint8,
                          device=x2.device)
-        torch.ops.talm.attn_bwd(q, k, v, o, d_o.view(n_tok, nh, hd), lse, cu, ctx.max_len,
-                                ctx.scale, dq.view(n_tok, nh, hd), dk.view(n_tok, nkv, hd),
-                                dv.view(n_tok, nkv, hd), ws)
-        del ws, d_o
+        views = (dq.view(n_tok, nh, hd), dk.view(n_tok, nkv, hd), dv.view(n_tok, nkv, hd), ws)
+        if _rope_rows(cos, sin):
+            # the rotary backward in the attention backward's epilogues: dqkv is the q|k|v
+            # gradient before the rotation, the operand of the projections' backward as it is
+            torch.ops.talm.attn_bwd_rope(q, k, v, o, d_o.view(n_tok, nh, hd), lse, cu,
+                                         ctx.max_len, ctx.scale, cos, sin, *views)
+            grads = (dqkv,)
+        else:
+            torch.ops.talm.attn_bwd(q, k, v, o, d_o.view(n_tok, nh, hd), lse, cu, ctx.max_len,
+                                    ctx.scale, *views)
+            grads = (dq, dk, dv)
+        del ws, d_o, views
         weight = weight_t = None
         if ctx.needs_input_grad[0]:
             weight_t = group.span_t(Q, V + 1)
@@ -550,7 +561,7 @@ class AttentionBlock(torch.autograd.Function):
                 if weight is None:
                     weight = torch.cat([group.weight(i) for i in (Q, K, V)], 0)
         wanted = [ctx.needs_input_grad[10 + i] for i in range(2 * len(ctx.adapters))]
-        dx, lora_grads = _mfma_backward_core((dq, dk, dv), x2, rest, cos, sin, weight,
+        dx, lora_grads = _mfma_backward_core(grads, x2, rest, cos, sin, weight,
                                              ctx.sizes, ctx.adapters, True, wanted, ctx.a_t,
                                              _grad_targets(ctx.lora_params), weight_t)
         RAN["attn_kernel_bwd"] += 1
@@ -558,6 +569,15 @@ class AttentionBlock(torch.autograd.Function):
         dx = None if dx is None else dx.view(ctx.x_shape)
         return (dx, None, None, None, None, None, None, None, None, None,
                 *_deliver(lora_grads, ctx.lora_params))
+
+
+def _rope_rows(cos, sin):
+    """cos / sin in the row layout the attention backward's fused rotation reads: fp32 [N, >= 128]
+    of one row stride, a multiple of 4 elements, 16-byte aligned."""
+    return all(t.dim() == 2 and t.dtype == torch.float32 and t.stride(1) == 1
+               and t.shape[1] >= 128 and t.stride(0) >= 128 and t.stride(0) % 4 == 0
+               and t.data_ptr() % 16 == 0
+               for t in (cos, sin)) and cos.stride(0) == sin.stride(0)
 
 
 _HOOK_DICTS = ("_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks")

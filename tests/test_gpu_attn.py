@@ -1,6 +1,6 @@
-"""Variable-length causal GQA attention (torch.ops.talm.attn_fwd / attn_bwd) against per-row
-causal SDPA in fp32 on the CPU (solution/unpad.py:121-134): output, log-sum-exp and the
-gradients of q, k, v. fp16 operands, fp32 statistics, fp16 P and dS in the MFMA products: the
+"""Variable-length causal GQA attention (torch.ops.talm.attn_fwd / attn_bwd / attn_bwd_rope)
+against per-row causal SDPA in fp32 on the CPU (solution/unpad.py:121-134): output, log-sum-exp
+and the gradients of q, k, v. fp16 operands, fp32 statistics, fp16 P and dS in the MFMA products: the
 tolerances are stated per tensor relative to its largest reference magnitude."""
 
 import math
@@ -85,6 +85,79 @@ def _run(lengths, strided, seed):
 def test_attention_matches_per_row_causal_sdpa(lengths, strided, seed):
     print(f"[case] attention lengths={lengths} strided={strided} seed={seed}", flush=True)
     _run(lengths, strided, seed)
+
+
+def _rotate_back(dy, cos, sin):
+    """The gradient of x -> x cos + rotate_half(x) sin (transformers' apply_rotary_pos_emb on one
+    [N, H, 128] tensor, fp32 CPU) at dy, by autograd: the rotary backward the fused kernel folds
+    in, derived from the forward rather than restated."""
+    x = torch.zeros_like(dy, requires_grad=True)
+    half = x.shape[-1] // 2
+    rotated = torch.cat((-x[..., half:], x[..., :half]), -1)
+    (x * cos[:, None, :] + rotated * sin[:, None, :]).backward(dy)
+    return x.grad
+
+
+@pytest.mark.parametrize("lengths,seed", [
+    ([300, 128, 512, 257], 4),          # config-5-like packed batch
+    ([1, 17, 64, 65, 129], 5),          # single-token and tile-boundary sequences
+])
+def test_attention_backward_with_the_rotary_backward_folded_in(lengths, seed):
+    """attn_bwd_rope: dq / dk rotated back in the kernel's epilogues equal the reference's
+    attention gradients pushed through the rotary embedding's backward. cos / sin are independent
+    random rows (not the model's tables, whose two halves are equal) so that a swapped half or
+    a cos read in place of a sin fails, and their rows are strided (160 of which 128 are read).
+    The outputs are column views of one [N, q + k + v] buffer, as in the attention block."""
+    import talm_amd._ops  # noqa: F401
+    from talm_amd import _ops
+
+    print(f"[case] attention+rope backward lengths={lengths} seed={seed}", flush=True)
+    g = torch.Generator("cpu").manual_seed(seed)
+    n = sum(lengths)
+    qkv = torch.randn(n, (HQ + 2 * HKV) * D, generator=g).half().cuda()
+    q = qkv[:, :HQ * D].view(n, HQ, D)
+    k = qkv[:, HQ * D:(HQ + HKV) * D].view(n, HKV, D)
+    v = qkv[:, (HQ + HKV) * D:].view(n, HKV, D)
+    dout = torch.randn(n, HQ, D, generator=g).half().cuda()
+    cs = torch.rand(2, n, 160, generator=g) * 2 - 1
+    cos, sin = cs[0].cuda()[:, :D], cs[1].cuda()[:, :D]
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32).cuda()
+    scale = 1.0 / math.sqrt(D)
+    out = torch.empty(n, HQ, D, dtype=torch.float16, device="cuda")
+    lse = torch.empty(HQ, n, dtype=torch.float32, device="cuda")
+    torch.ops.talm.attn_fwd(q, k, v, cu, max(lengths), scale, out, lse)
+    grads = torch.full_like(qkv, float("nan"))
+    dq = grads[:, :HQ * D].view(n, HQ, D)
+    dk = grads[:, HQ * D:(HQ + HKV) * D].view(n, HKV, D)
+    dv = grads[:, (HQ + HKV) * D:].view(n, HKV, D)
+    ws = torch.empty(_ops.attn_bwd_workspace_bytes(n, HQ), dtype=torch.uint8, device="cuda")
+    torch.ops.talm.attn_bwd_rope(q, k, v, out, dout, lse, cu, max(lengths), scale, cos, sin, dq,
+                                 dk, dv, ws)
+    torch.cuda.synchronize()
+    _r_out, _r_lse, r_dq, r_dk, r_dv = _reference(q, k, v, lengths, scale, dout)
+    c, s_ = cos.cpu(), sin.cpu()
+    assert not grads.isnan().any(), "a gradient element was not written"
+    _close("dq (rotated back)", dq, _rotate_back(r_dq, c, s_), 4e-3)
+    _close("dk (rotated back)", dk, _rotate_back(r_dk, c, s_), 4e-3)
+    _close("dv", dv, r_dv, 4e-3)
+
+
+def test_attention_rope_backward_rejects_bad_tables():
+    import talm_amd._ops  # noqa: F401
+    from talm_amd import _ops
+
+    n = 8
+    q = torch.zeros(n, HQ, D, dtype=torch.float16, device="cuda")
+    k = torch.zeros(n, HKV, D, dtype=torch.float16, device="cuda")
+    cu = torch.tensor([0, n], dtype=torch.int32, device="cuda")
+    lse = torch.zeros(HQ, n, device="cuda")
+    ws = torch.empty(_ops.attn_bwd_workspace_bytes(n, HQ), dtype=torch.uint8, device="cuda")
+    narrow = torch.zeros(n, 64, device="cuda")                    # fewer than 128 columns
+    with pytest.raises(ValueError):
+        torch.ops.talm.attn_bwd_rope(q, k, k, q, q, lse, cu, n, 0.125, narrow, narrow, q, k, k, ws)
+    odd = torch.zeros(n, 131, device="cuda")[:, :128]             # row stride not a multiple of 4
+    with pytest.raises(ValueError):
+        torch.ops.talm.attn_bwd_rope(q, k, k, q, q, lse, cu, n, 0.125, odd, odd, q, k, k, ws)
 
 
 def test_attention_rejects_bad_shapes():

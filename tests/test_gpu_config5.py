@@ -61,7 +61,7 @@ def _curve(mode, steps):
     runner, graphed = trainer, None
     if mode != "eager":
         solution.apply()
-        engaged.reset()
+    engaged.reset()  # counters of this run only (earlier tests in the process leave theirs)
     if mode == "graph":
         from talm_amd.step_graph import GraphedTrainer
 
