@@ -27,99 +27,106 @@ constexpr int kMaxAdapters = 2;
 
 // ------------------------------------------------------------------------------------------
 // t[r][16 g + i] = fp16(sum_k x[r][k] A_g[i][k]); ts = fp16(scaling_g * the same fp32 sum).
-// One workgroup per 16 tokens, wavefront w takes the 32-deep k-steps w, w + 8, ..., issuing the
-// loads of kDownBatch steps before their MFMAs (steps past the reduction read zeros).
+// One workgroup per 16 tokens, wavefront w takes the 32-deep k-steps w, w + 8, ... of the
+// workgroup's chunk list, issuing the loads of up to kDownBatch steps before their MFMAs.
 // ------------------------------------------------------------------------------------------
 // Adapter g reduces over x's columns [xcol_g, xcol_g + k_g) against A_g [16][k_g] (the forward:
 // both over all of x; the backward: u = dy_seg B_g over each adapter's own output columns).
 // With `a_kmajor` the A_g are given as [k_g][16] (the backward passes B_g as it is stored):
 // each lane then gathers its 8 k-consecutive values with 2-byte loads.
-__device__ __forceinline__ half8_t gather_kmajor(const uint16_t* a, int k, int n) {
-  half8_t v;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = __builtin_bit_cast(_Float16, a[(k + e) * 16 + n]);
-  return v;
-}
-
 constexpr int kDownWaves = 8;
 constexpr int kDownBatch = 8;
 
-// One adapter's 16 x 16 block of one wavefront: sum over its k-steps of x[16 rows] A^T. A k-step
-// at or past klen reads x as zeros (out-of-range buffer offset) and A at a clamped, in-range k.
-template <bool KMAJOR>
-__device__ __forceinline__ f32x4 down_block(__amdgpu_buffer_rsrc_t rx, uint32_t xoff,
-                                            __amdgpu_buffer_rsrc_t ra, uint32_t aoff,
-                                            const uint16_t* a, int klen, int row, int kq, int wave) {
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int kb = wave * 32; kb < klen; kb += 32 * kDownWaves * kDownBatch) {
-    half8_t xa[kDownBatch], wa[kDownBatch];
-    uint32_t g[KMAJOR ? kDownBatch : 1][8];  // k-major A: the 8 gathered halfs of each step
+// How a workgroup walks its reduction: the 32-deep k-steps of adapter 0 ([0, n0)) then those of
+// adapter 1 ([n0, n0 + n1)) form ONE list of chunks, dealt to the wavefronts round-robin, so the
+// loads of both adapters are in flight together (one memory round trip, not one per adapter).
+// kDownShared (the forward: both adapters over the same x columns and depth): a chunk is one x
+// load for both adapters' MFMAs. kDownKmajor (the backward's B_g given as [k][16]): each lane
+// gathers its 8 k-consecutive A values with 2-byte loads.
+enum DownMode { kDownSplit = 0, kDownKmajor = 1, kDownShared = 2 };
+
+template <int kMode>
+__global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int n_tokens, int k0len, int k1len, int xcol0,
+    int xcol1, const uint16_t* __restrict__ a0, const uint16_t* __restrict__ a1, int n_adapters,
+    float s0, float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts, int64_t ldt) {
+  constexpr bool kKmajor = kMode == kDownKmajor, kShared = kMode == kDownShared;
+  __shared__ float red[kDownWaves][kMaxAdapters][16][16 + 1];
+  const int m0 = blockIdx.x * 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = lane & 15, kq = 8 * (lane >> 4);
+  const uint16_t* xr = x + static_cast<int64_t>(m0) * ldx;
+  const __amdgpu_buffer_rsrc_t rx0 = buffer_rsrc(xr + xcol0);
+  const __amdgpu_buffer_rsrc_t rx1 = buffer_rsrc(xr + xcol1);
+  const __amdgpu_buffer_rsrc_t ra0 = buffer_rsrc(a0);
+  const __amdgpu_buffer_rsrc_t ra1 = buffer_rsrc(a1);
+  const uint32_t xoff = m0 + row < n_tokens ? static_cast<uint32_t>((row * ldx + kq) * 2) : kOob;
+  const uint32_t aoff0 = static_cast<uint32_t>((row * k0len + kq) * 2);
+  const uint32_t aoff1 = static_cast<uint32_t>((row * k1len + kq) * 2);
+  const int n0 = k0len >> 5, n1 = n_adapters > 1 ? k1len >> 5 : 0;
+  const int chunks = kShared ? n0 : n0 + n1;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  for (int base = wave; base < chunks; base += kDownWaves * kDownBatch) {
+    // slot j of the pass is chunk base + 8 j; a slot past the list loads through an offset
+    // beyond every buffer (the load returns 0 and fetches nothing) and its MFMA adds zeros.
+    // Every load is unconditional: branches between them would make the compiler wait on
+    // earlier loads inside the chain.
+    half8_t xa[kDownBatch], wa[kDownBatch], wb[kShared ? kDownBatch : 1];
+    uint16_t g[kKmajor ? kDownBatch : 1][8];
 #pragma unroll
     for (int j = 0; j < kDownBatch; ++j) {
-      const int k = kb + 32 * kDownWaves * j;
-      const bool in = k < klen;
-      const uint32_t kbytes = static_cast<uint32_t>(k * 2);
-      xa[j] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, in ? xoff + kbytes : kOob, 0, 0));
-      if constexpr (KMAJOR) {
-        const uint16_t* ak = a + (min(k, klen - 32) + kq) * 16 + row;
+      const int c = base + kDownWaves * j;
+      const bool live = c < chunks, second = !kShared && c >= n0;
+      const uint32_t kbytes = static_cast<uint32_t>((second ? c - n0 : c) * 64);
+      xa[j] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              second ? rx1 : rx0, live ? xoff + kbytes : kOob, 0, 0));
+      if constexpr (kKmajor) {
+        // A_g [k][16]: element (k, i) at byte 32 k + 2 i; this lane's k = kbytes / 2 + kq + e
+        const uint32_t at = kbytes * 16 + static_cast<uint32_t>((kq * 16 + row) * 2);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) g[j][e] = ak[e * 16];
+        for (int e = 0; e < 8; ++e)
+          g[j][e] = __builtin_amdgcn_raw_buffer_load_b16(second ? ra1 : ra0,
+                                                         live ? at + 32 * e : kOob, 0, 0);
       } else {
-        wa[j] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra, in ? aoff + kbytes : kOob, 0, 0));
+        wa[j] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                second ? ra1 : ra0,
+                                                live ? (second ? aoff1 : aoff0) + kbytes : kOob, 0, 0));
       }
+      if constexpr (kShared)
+        wb[j] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                ra1, live ? aoff1 + kbytes : kOob, 0, 0));
     }
-    // every load of the batch is issued before the first use: the empty statements take the
-    // loaded registers, so the compiler waits for the batch here and not load by load
+    // the empty statements take the loaded registers, so the compiler waits for the whole pass
+    // here and not load by load
 #pragma unroll
     for (int j = 0; j < kDownBatch; ++j) {
       asm volatile("" : "+v"(xa[j]));
-      if constexpr (KMAJOR) {
+      if constexpr (kKmajor) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(g[j][e]));
       } else {
         asm volatile("" : "+v"(wa[j]));
       }
+      if constexpr (kShared) asm volatile("" : "+v"(wb[j]));
     }
-    if constexpr (KMAJOR) {
 #pragma unroll
-      for (int j = 0; j < kDownBatch; ++j) {
+    for (int j = 0; j < kDownBatch; ++j) {
+      if constexpr (kKmajor) {
         uint4 w;
-        w.x = g[j][0] | (g[j][1] << 16); w.y = g[j][2] | (g[j][3] << 16);
-        w.z = g[j][4] | (g[j][5] << 16); w.w = g[j][6] | (g[j][7] << 16);
+        w.x = g[j][0] | (uint32_t{g[j][1]} << 16); w.y = g[j][2] | (uint32_t{g[j][3]} << 16);
+        w.z = g[j][4] | (uint32_t{g[j][5]} << 16); w.w = g[j][6] | (uint32_t{g[j][7]} << 16);
         wa[j] = __builtin_bit_cast(half8_t, w);
       }
+      if constexpr (kShared) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wa[j], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wb[j], acc1, 0, 0, 0);
+      } else if (base + kDownWaves * j >= n0) {
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wa[j], acc1, 0, 0, 0);
+      } else {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wa[j], acc0, 0, 0, 0);
+      }
     }
-#pragma unroll
-    for (int j = 0; j < kDownBatch; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], wa[j], acc, 0, 0, 0);
-  }
-  return acc;
-}
-
-__global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, int n_tokens, int k0len, int k1len, int xcol0,
-    int xcol1, const uint16_t* __restrict__ a0, const uint16_t* __restrict__ a1, int n_adapters,
-    int a_kmajor, float s0, float s1, uint16_t* __restrict__ t, uint16_t* __restrict__ ts,
-    int64_t ldt) {
-  __shared__ float red[kDownWaves][kMaxAdapters][16][16 + 1];
-  const int m0 = blockIdx.x * 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = lane & 15, kq = 8 * (lane >> 4);
-  const uint16_t* xr = x + static_cast<int64_t>(m0) * ldx;
-  const __amdgpu_buffer_rsrc_t rx0 = buffer_rsrc(xr + xcol0);
-  const __amdgpu_buffer_rsrc_t rx1 = buffer_rsrc(xr + (n_adapters > 1 ? xcol1 : xcol0));
-  const __amdgpu_buffer_rsrc_t ra0 = buffer_rsrc(a0);
-  const __amdgpu_buffer_rsrc_t ra1 = buffer_rsrc(n_adapters > 1 ? a1 : a0);
-  const uint32_t xoff = m0 + row < n_tokens ? static_cast<uint32_t>((row * ldx + kq) * 2) : kOob;
-  const uint32_t aoff0 = static_cast<uint32_t>((row * k0len + kq) * 2);
-  const uint32_t aoff1 = static_cast<uint32_t>((row * k1len + kq) * 2);
-  const uint16_t* a1s = n_adapters > 1 ? a1 : a0;
-  f32x4 acc0, acc1 = {0.f, 0.f, 0.f, 0.f};
-  if (a_kmajor) {
-    acc0 = down_block<true>(rx0, xoff, ra0, aoff0, a0, k0len, row, kq, wave);
-    if (n_adapters > 1) acc1 = down_block<true>(rx1, xoff, ra1, aoff1, a1s, k1len, row, kq, wave);
-  } else {
-    acc0 = down_block<false>(rx0, xoff, ra0, aoff0, a0, k0len, row, kq, wave);
-    if (n_adapters > 1) acc1 = down_block<false>(rx1, xoff, ra1, aoff1, a1s, k1len, row, kq, wave);
   }
   // accumulator element v of lane l: token 4 * (l / 16) + v, rank l % 16
 #pragma unroll
@@ -130,14 +137,14 @@ __global__ __launch_bounds__(64 * kDownWaves) void lora_down_kernel(
   __syncthreads();
   const int tid = threadIdx.x;
   for (int e = tid; e < n_adapters * 256; e += 64 * kDownWaves) {
-    const int g = e >> 8, r = (e >> 4) & 15, i = e & 15;
+    const int g_ = e >> 8, r = (e >> 4) & 15, i = e & 15;
     if (m0 + r >= n_tokens) continue;
     float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kDownWaves; ++w) sum += red[w][g][r][i];
-    const int64_t at = static_cast<int64_t>(m0 + r) * ldt + g * kRank + i;
+    for (int w = 0; w < kDownWaves; ++w) sum += red[w][g_][r][i];
+    const int64_t at = static_cast<int64_t>(m0 + r) * ldt + g_ * kRank + i;
     t[at] = f2h(sum);
-    ts[at] = f2h((g == 0 ? s0 : s1) * sum);
+    ts[at] = f2h((g_ == 0 ? s0 : s1) * sum);
   }
 }
 
@@ -573,12 +580,23 @@ TALM_API int talm_lora_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, in
   if (!x || !a0 || (two && !a1) || !t || !ts) return fail(TALM_EINVAL, "lora_down: null pointer");
   if (!aligned(x, 16) || !aligned(a0, 16) || (two && !aligned(a1, 16)))
     return fail(TALM_EINVAL, "lora_down: x and the A matrices must be 16-byte aligned");
-  hipLaunchKernelGGL(lora_down_kernel, dim3(static_cast<unsigned>((n_tokens + 15) / 16)),
-                     dim3(64 * kDownWaves),
-                     0, as_stream(stream), x, ldx, static_cast<int>(n_tokens), static_cast<int>(k0),
-                     static_cast<int>(two ? k1 : k0), static_cast<int>(xcol0),
-                     static_cast<int>(two ? xcol1 : xcol0), a0, a1, n_adapters, a_kmajor ? 1 : 0,
-                     scaling0, scaling1, t, ts, ldt);
+  const int mode = a_kmajor ? kDownKmajor
+                   : two && xcol0 == xcol1 && k0 == k1 ? kDownShared : kDownSplit;
+  const dim3 grid(static_cast<unsigned>((n_tokens + 15) / 16)), block(64 * kDownWaves);
+  const uint16_t* a1s = two ? a1 : a0;
+  const int k1s = static_cast<int>(two ? k1 : k0), x1s = static_cast<int>(two ? xcol1 : xcol0);
+#define TALM_LORA_DOWN(M)                                                                     \
+  hipLaunchKernelGGL(lora_down_kernel<M>, grid, block, 0, as_stream(stream), x, ldx,          \
+                     static_cast<int>(n_tokens), static_cast<int>(k0), k1s,                   \
+                     static_cast<int>(xcol0), x1s, a0, a1s, n_adapters, scaling0, scaling1, t, \
+                     ts, ldt)
+  if (mode == kDownKmajor)
+    TALM_LORA_DOWN(kDownKmajor);
+  else if (mode == kDownShared)
+    TALM_LORA_DOWN(kDownShared);
+  else
+    TALM_LORA_DOWN(kDownSplit);
+#undef TALM_LORA_DOWN
   return check_launch("lora_down");
 }
 

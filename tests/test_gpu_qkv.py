@@ -151,21 +151,25 @@ def test_qkv_bwd_prep_matches_rope_backward(n, q, k, v, rope):
     assert torch.all(err <= 2.0 ** -10 * ref.abs() + 2.0 ** -24), float(err.max())
 
 
-def test_lora_down_backward_form_matches_fp32():
+@pytest.mark.parametrize("n,width,segs", [
+    (700, 2048, [(0, 1536), (1792, 2048)]),   # Qwen2.5-1.5B q|k|v: 48 + 8 k-steps of 32
+    (333, 2800, [(0, 2560), (2688, 2784)]),   # 80 + 3 k-steps: two passes, a mid-pass switch
+])
+def test_lora_down_backward_form_matches_fp32(n, width, segs):
     """u = (scaling dy) B per adapter over its own output columns: adapter 0 reduces columns
-    [0, 1536), adapter 1 columns [1792, 2048) of one [N, 2048] gradient."""
-    _case("lora_down backward form")
-    n = 700
-    g = torch.Generator().manual_seed(11)
-    dcat = torch.randn(n, 2048, generator=g).half().to(DEV)
-    b = [(torch.randn(1536, 16, generator=g) * 0.05).half().to(DEV),
-         (torch.randn(256, 16, generator=g) * 0.05).half().to(DEV)]
+    [lo0, hi0), adapter 1 columns [lo1, hi1) of one [N, width] gradient."""
+    _case(f"lora_down backward form n={n} segs={segs}")
+    g = torch.Generator().manual_seed(11 + n)
+    dcat = torch.randn(n, width, generator=g).half().to(DEV)
+    b = [(torch.randn(hi - lo, 16, generator=g) * 0.05).half().to(DEV) for lo, hi in segs]
     t = torch.empty(n, 32, dtype=torch.float16, device=DEV)
     u = torch.empty_like(t)
+    (lo0, hi0), (lo1, hi1) = segs
     for kmajor in (0, 1):  # B_g transposed to [16, seg], or read as stored [seg, 16]
         bs = [bb.t().contiguous() for bb in b] if not kmajor else b
-        torch.ops.talm.lora_down(dcat, bs[0], bs[1], 1536, 256, 0, 1792, kmajor, 2.0, 2.0, t, u)
-        for k, (lo, hi) in enumerate([(0, 1536), (1792, 2048)]):
+        torch.ops.talm.lora_down(dcat, bs[0], bs[1], hi0 - lo0, hi1 - lo1, lo0, lo1, kmajor, 2.0,
+                                 2.0, t, u)
+        for k, (lo, hi) in enumerate(segs):
             ref = 2.0 * (dcat[:, lo:hi].float() @ b[k].float())
             got = u[:, 16 * k:16 * (k + 1)].float()
             assert torch.all((got - ref).abs() <= 2.0 ** -10 * ref.abs() + 1e-5 * (hi - lo)), k
