@@ -117,7 +117,8 @@ int talm_nf4_dequant(const uint8_t* packed, const float* absmax, uint16_t* out, 
  * backward == 0: x = a (+ p when add); writes q = x (when add), h = w * xhat, xhat = x * rstd,
  *                rstd = rsqrt(mean(x^2) + eps).
  * backward != 0: reads dy = h, xhat, rstd; dx = rstd * (g - xhat * mean(g * xhat)), g = dy * w;
- *                with add, dx += q and dx is also written to p; dx is written to a.
+ *                with add, dx += q and dx is also written to p; dx is written to a. A NULL q
+ *                with add stands for ds = 0 (the sum's gradient is not used).
  * p and q are ignored (may be NULL) when add == 0.
  */
 int talm_rmsnorm(void* a, void* q, void* h, void* xhat, void* p, const void* weight, float* rstd,
@@ -442,6 +443,53 @@ int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_
                   const float* scale, int64_t rows, int64_t cols, int32_t transpose,
                   int32_t blocksize, uint16_t* out, int64_t ldo, void* workspace,
                   int64_t workspace_bytes, void* stream);
+
+/*
+ * The packed causal-LM step's per-step glue (each one launch of one workgroup for the batch
+ * work). int64 tensors are contiguous; the batch is right-padded [batch, seq] (row-major).
+ *
+ * talm_pack_rows: the batch packed into exactly n_tokens rows (a step captured in a HIP graph).
+ * Row b holds len_b = sum_t mask[b][t] real tokens (clamped to [0, seq]); they go to flat rows
+ * [cu[b], cu[b+1]) with cu[0] = 0, cu[k] = min(len_0 + .. + len_{k-1}, n_tokens), and flat rows
+ * [cu[batch], n_tokens) form one more sequence (cu[batch+1] = n_tokens, int32 [batch + 2]) that
+ * reads the pad slot batch * seq. Per flat row j of row r at position p: src[j] = r * seq + p
+ * (batch * seq for the pad sequence), ids[j] = input_ids at src (0 for the pad sequence),
+ * positions[j] = p, targets[j] = labels[r][p + 1] (-100 at a row's last position and in the
+ * pad sequence). batch <= 8192. Replaces the label shift and packing of the fused forward
+ * (solution/patches.py:173-260 with solution/unpad.py:66-92's gather), restated for a fixed row
+ * count.
+ *
+ * talm_row_stats: stats int64 [batch + 2] = the row lengths sum_t mask[b][t], then the number of
+ * labelled positions among each row's first length positions and among all positions (position
+ * t of row b is labelled when t + 1 < seq and labels[b][t + 1] >= 0). Replaces the one host
+ * copy's device side of solution/unpad.py:66-92.
+ *
+ * talm_head_loss: loss f32 [1] = sum_i token_loss[i] / denom with denom f32 [1] = max(#i with
+ * targets[i] >= 0, 1) (mode 0), *num_items (mode 1, device f32) or num_items_value (mode 2);
+ * correct_bool[i] = correct[i] != 0 (bytes 0 / 1). Replaces the loss and denominator of the
+ * fused head (solution/fused_head.py:272-277, :386).
+ *
+ * talm_scatter_rows: full_loss, full_entropy f32 [out_len] zeroed, then full[src[i]] = the row's
+ * value (src outside [0, out_len) skipped; rows sharing a slot leave one of their values);
+ * stats int64 [2] = (#i with correct[i] != 0 (bytes), #i with targets[i] >= 0). Replaces the scatter of
+ * the per-token outputs and the step's metric sums (solution/patches.py:244-253).
+ *
+ * talm_scale_rows: out[i] = fp16(fp32(g[i]) * s), s = *grad_loss / *denom (0 when *denom is 0),
+ * fp16 [n], 16-byte aligned. Replaces the head's backward (solution/fused_head.py:280-287).
+ */
+int talm_pack_rows(const int64_t* input_ids, const int64_t* mask, const int64_t* labels,
+                   int32_t batch, int32_t seq, int64_t n_tokens, int64_t* ids, int64_t* positions,
+                   int32_t* cu_seqlens, int64_t* targets, int64_t* src, void* stream);
+int talm_row_stats(const int64_t* mask, const int64_t* labels, int32_t batch, int32_t seq,
+                   int64_t* stats, void* stream);
+int talm_head_loss(const float* token_loss, const int32_t* correct, const int64_t* targets,
+                   int64_t n, const float* num_items, float num_items_value, int32_t mode,
+                   float* loss, float* denom, uint8_t* correct_bool, void* stream);
+int talm_scatter_rows(const float* token_loss, const float* entropy, const uint8_t* correct,
+                      const int64_t* targets, const int64_t* src, int64_t n, int64_t out_len,
+                      float* full_loss, float* full_entropy, int64_t* stats, void* stream);
+int talm_scale_rows(const uint16_t* g, int64_t n, const float* grad_loss, const float* denom,
+                    uint16_t* out, void* stream);
 
 #ifdef __cplusplus
 }

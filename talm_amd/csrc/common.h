@@ -32,6 +32,15 @@ __device__ __forceinline__ uint16_t f2h(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 
+// The fp32 product, materialized: the empty asm keeps the backend from folding "multiply, then
+// convert to fp16" into one v_fma_mix (a single rounding of the exact product, and -0 turned
+// into +0 by its zero addend), where the result must be rounded to fp32 first.
+__device__ __forceinline__ float mul_f32(float a, float b) {
+  float p = a * b;
+  asm("" : "+v"(p));
+  return p;
+}
+
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
 }

@@ -22,14 +22,6 @@ __constant__ float kNF4Levels[16] = {
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
-// The fp32 product, materialized: the empty asm keeps the backend from folding "multiply, then
-// convert to fp16" into one v_fma_mix (a single rounding of the exact product).
-__device__ __forceinline__ float mul_f32(float a, float b) {
-  float p = a * b;
-  asm("" : "+v"(p));
-  return p;
-}
-
 // Eight weights of one packed word (4 bytes, high nibble first) scaled and packed to 4 x 2 fp16.
 __device__ __forceinline__ uint4 dequant_word(uint32_t word, float scale, const float* levels) {
   uint32_t out[4];

@@ -123,7 +123,8 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const XT* __restrict__ a
   }
 }
 
-// Backward, vector path. g = dy * w; dx = rstd * (g - xhat * mean(g * xhat)) (+ ds -> p).
+// Backward, vector path. g = dy * w; dx = rstd * (g - xhat * mean(g * xhat)) (+ ds -> p; no q:
+// ds = 0).
 // Loads first, as in the forward.
 template <typename XT, typename OT, typename WT, bool ADD, int NC>
 __global__ __launch_bounds__(kThreads) void rms_bwd_vec(XT* __restrict__ a, OT* __restrict__ p,
@@ -146,7 +147,14 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(XT* __restrict__ a, OT* 
     IO<OT>::load8_nt(h + at + 8 * c, g[i]);
     IO<OT>::load8_nt(xhat + at + 8 * c, xh[i]);
     IO<WT>::load8(w + 8 * c, wv);
-    if constexpr (ADD) IO<XT>::load8_nt(q + at + 8 * c, ds[i]);
+    if constexpr (ADD) {
+      if (q) {
+        IO<XT>::load8_nt(q + at + 8 * c, ds[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ds[i][e] = 0.f;  // no sum gradient: ds = 0
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) g[i][e] *= wv[e];
   }
@@ -229,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_any(XT* __restrict__ a, OT* 
     const float g = IO<OT>::load1(h + at + j) * IO<WT>::load1(w + j);
     float dx = r * (g - IO<OT>::load1(xhat + at + j) * cmean);
     if constexpr (ADD) {
-      dx += IO<XT>::load1(q + at + j);
+      if (q) dx += IO<XT>::load1(q + at + j);
       IO<OT>::store1(p + at + j, dx);
     }
     IO<XT>::store1(a + at + j, dx);
@@ -315,7 +323,7 @@ TALM_API int talm_rmsnorm(void* a, void* q, void* h, void* xhat, void* p, const 
   if (n_rows < 0 || n_cols < 1 || n_cols > (1 << 24))
     return fail(TALM_EINVAL, "rmsnorm: bad shape [%lld, %lld]", (long long)n_rows, (long long)n_cols);
   if (n_rows == 0) return ok();
-  if (!a || !h || !xhat || !weight || !rstd || (add && (!p || !q)))
+  if (!a || !h || !xhat || !weight || !rstd || (add && (!p || (!q && !backward))))
     return fail(TALM_EINVAL, "rmsnorm: null pointer");
   const bool vec = n_cols % 8 == 0 && n_cols <= kMaxChunks * 8 * kWave && aligned(a, 16) &&
                    aligned(h, 16) && aligned(xhat, 16) && aligned(weight, 16) &&

@@ -184,13 +184,14 @@ void rmsnorm(const Tensor& a, const OptTensor& q, const Tensor& h, const Tensor&
   require(xhat.dim() == 2, "rmsnorm: [N, H] operands must be contiguous CUDA tensors of one shape");
   const int64_t n_rows = xhat.size(0), n_cols = xhat.size(1);
   const bool add = p.has_value();
-  require(!add || q.has_value(), "rmsnorm: p and q go together");
+  require(!add || backward || q.has_value(), "rmsnorm: p and q go together in the forward");
   auto ok = [&](const Tensor& t) {
     return t.is_cuda() && t.is_contiguous() && same_shape(t, n_rows, n_cols);
   };
-  require(ok(a) && ok(h) && ok(xhat) && (!add || (ok(*p) && ok(*q))),
+  require(ok(a) && ok(h) && ok(xhat) && (!add || (ok(*p) && (!q.has_value() || ok(*q)))),
           "rmsnorm: [N, H] operands must be contiguous CUDA tensors of one shape");
-  require(!add || a.scalar_type() == q->scalar_type(), "rmsnorm: q has a's dtype");
+  require(!add || !q.has_value() || a.scalar_type() == q->scalar_type(),
+          "rmsnorm: q has a's dtype");
   require(h.scalar_type() == xhat.scalar_type() && (!add || p->scalar_type() == h.scalar_type()),
           "rmsnorm: h, xhat and p share the output dtype");
   require(weight.is_contiguous() && weight.numel() == n_cols, "rmsnorm: weight [H]");
@@ -1081,7 +1082,134 @@ Tensor gemm_tune(const Tensor& a, int64_t trans_a, const Tensor& b, int64_t tran
   return result;
 }
 
+// ------------------------------------------------------------------------------------------
+// The packed causal-LM step's per-step glue: batch packing, row statistics, the head's loss and
+// metrics, the head backward's scaling (csrc/pack.hip).
+
+void i64_cuda(const Tensor& t, const char* name) {
+  TORCH_CHECK_VALUE(t.is_cuda() && t.scalar_type() == at::kLong && t.is_contiguous(), name,
+                    " must be a contiguous CUDA int64 tensor");
+}
+
+void f32_cuda(const Tensor& t, const char* name) {
+  TORCH_CHECK_VALUE(t.is_cuda() && t.scalar_type() == at::kFloat && t.is_contiguous(), name,
+                    " must be a contiguous CUDA float32 tensor");
+}
+
+// input_ids, mask, labels int64 [B, T] (right-padded) -> ids, positions, targets, src int64
+// [n_tokens] and cu int32 [B + 2].
+void pack_rows(const Tensor& input_ids, const Tensor& mask, const Tensor& labels,
+               int64_t n_tokens, const Tensor& ids, const Tensor& positions, const Tensor& cu,
+               const Tensor& targets, const Tensor& src) {
+  i64_cuda(input_ids, "input_ids");
+  i64_cuda(mask, "mask");
+  i64_cuda(labels, "labels");
+  require(mask.dim() == 2 && input_ids.sizes() == mask.sizes() && labels.sizes() == mask.sizes(),
+          "pack_rows: input_ids, mask and labels [B, T]");
+  const int64_t b = mask.size(0), t = mask.size(1);
+  for (const auto& [v, name] : {std::pair<const Tensor*, const char*>{&ids, "ids"},
+                                {&positions, "positions"}, {&targets, "targets"}, {&src, "src"}}) {
+    i64_cuda(*v, name);
+    TORCH_CHECK_VALUE(v->numel() == n_tokens, "pack_rows: ", name, " holds n_tokens values");
+  }
+  require(cu.is_cuda() && cu.scalar_type() == at::kInt && cu.is_contiguous() &&
+              cu.numel() == b + 2,
+          "pack_rows: cu int32 [B + 2]");
+  require(b <= INT32_MAX && t <= INT32_MAX, "pack_rows: batch and row length fit int32");
+  check(talm_pack_rows(as<int64_t>(input_ids), as<int64_t>(mask), as<int64_t>(labels),
+                       static_cast<int32_t>(b), static_cast<int32_t>(t), n_tokens, as<int64_t>(ids),
+                       as<int64_t>(positions), as<int32_t>(cu), as<int64_t>(targets),
+                       as<int64_t>(src), stream_of(mask)),
+        "pack_rows");
+}
+
+// mask, labels int64 [B, T] -> stats int64 [B + 2].
+void row_stats(const Tensor& mask, const Tensor& labels, const Tensor& stats) {
+  i64_cuda(mask, "mask");
+  i64_cuda(labels, "labels");
+  i64_cuda(stats, "stats");
+  require(mask.dim() == 2 && labels.sizes() == mask.sizes() && stats.numel() == mask.size(0) + 2,
+          "row_stats: mask, labels [B, T], stats [B + 2]");
+  require(mask.size(0) <= INT32_MAX && mask.size(1) <= INT32_MAX,
+          "row_stats: batch and row length fit int32");
+  check(talm_row_stats(as<int64_t>(mask), as<int64_t>(labels), static_cast<int32_t>(mask.size(0)),
+                       static_cast<int32_t>(mask.size(1)), as<int64_t>(stats), stream_of(mask)),
+        "row_stats");
+}
+
+// token_loss f32 [N], correct int32 [N], targets int64 [N] -> loss, denom f32 [] and
+// correct_bool bool [N]. mode 0: denom = max(#labelled, 1); 1: num_items (f32 []); 2: value.
+void head_loss(const Tensor& token_loss, const Tensor& correct, const Tensor& targets,
+               const OptTensor& num_items, double num_items_value, int64_t mode,
+               const Tensor& loss, const Tensor& denom, const Tensor& correct_bool) {
+  f32_cuda(token_loss, "token_loss");
+  i64_cuda(targets, "targets");
+  const int64_t n = token_loss.numel();
+  require(correct.is_cuda() && correct.scalar_type() == at::kInt && correct.is_contiguous() &&
+              correct.numel() == n && targets.numel() == n,
+          "head_loss: correct int32 [N], targets [N]");
+  require(correct_bool.is_cuda() && correct_bool.scalar_type() == at::kBool &&
+              correct_bool.is_contiguous() && correct_bool.numel() == n,
+          "head_loss: correct_bool bool [N]");
+  f32_cuda(loss, "loss");
+  f32_cuda(denom, "denom");
+  require(loss.numel() == 1 && denom.numel() == 1, "head_loss: loss and denom hold one value");
+  require(mode >= 0 && mode <= 2 && (mode != 1 || num_items.has_value()), "head_loss: mode");
+  if (num_items.has_value()) {
+    f32_cuda(*num_items, "num_items");
+    require(num_items->numel() == 1, "head_loss: num_items holds one value");
+  }
+  check(talm_head_loss(as<float>(token_loss), as<int32_t>(correct), as<int64_t>(targets), n,
+                       as<float>(num_items), static_cast<float>(num_items_value),
+                       static_cast<int32_t>(mode), as<float>(loss), as<float>(denom),
+                       static_cast<uint8_t*>(correct_bool.data_ptr()), stream_of(token_loss)),
+        "head_loss");
+}
+
+// token_loss, entropy f32 [N], correct bool [N], targets, src int64 [N] -> full_loss,
+// full_entropy f32 [L] and stats int64 [2].
+void scatter_rows(const Tensor& token_loss, const Tensor& entropy, const Tensor& correct,
+                  const Tensor& targets, const Tensor& src, const Tensor& full_loss,
+                  const Tensor& full_entropy, const Tensor& stats) {
+  f32_cuda(token_loss, "token_loss");
+  f32_cuda(entropy, "entropy");
+  f32_cuda(full_loss, "full_loss");
+  f32_cuda(full_entropy, "full_entropy");
+  i64_cuda(targets, "targets");
+  i64_cuda(src, "src");
+  i64_cuda(stats, "stats");
+  const int64_t n = token_loss.numel();
+  require(entropy.numel() == n && targets.numel() == n && src.numel() == n &&
+              correct.is_cuda() && correct.scalar_type() == at::kBool &&
+              correct.is_contiguous() && correct.numel() == n,
+          "scatter_rows: entropy, correct (bool), targets and src [N]");
+  require(full_entropy.numel() == full_loss.numel() && stats.numel() == 2,
+          "scatter_rows: full_loss, full_entropy [L], stats [2]");
+  check(talm_scatter_rows(as<float>(token_loss), as<float>(entropy),
+                          static_cast<const uint8_t*>(correct.data_ptr()),
+                          as<int64_t>(targets), as<int64_t>(src), n, full_loss.numel(),
+                          as<float>(full_loss), as<float>(full_entropy), as<int64_t>(stats),
+                          stream_of(token_loss)),
+        "scatter_rows");
+}
+
+// out = fp16(fp32(g) * (denom != 0 ? grad_loss / denom : 0)); g, out fp16 of one size.
+void scale_rows(const Tensor& g, const Tensor& grad_loss, const Tensor& denom, const Tensor& out) {
+  require_fp16(g, "g");
+  require_fp16(out, "out");
+  require(g.is_contiguous() && out.is_contiguous() && g.numel() == out.numel(),
+          "scale_rows: g and out contiguous, of one size");
+  f32_cuda(grad_loss, "grad_loss");
+  f32_cuda(denom, "denom");
+  require(grad_loss.numel() == 1 && denom.numel() == 1,
+          "scale_rows: grad_loss and denom hold one value");
+  check(talm_scale_rows(as<uint16_t>(g), g.numel(), as<float>(grad_loss), as<float>(denom),
+                        as<uint16_t>(out), stream_of(g)),
+        "scale_rows");
+}
+
 }  // namespace
+
 
 TORCH_LIBRARY(talm, m) {
   m.def("nf4_group_dequant(Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
@@ -1129,6 +1257,15 @@ TORCH_LIBRARY(talm, m) {
         "Tensor cu_seqlens, int max_seqlen, float scale, Tensor cos, Tensor sin, Tensor(a!) dq, "
         "Tensor(b!) dk, Tensor(c!) dv, Tensor(d!) workspace) -> ()");
   m.def("lora_mirror(Tensor table, int n_tensors, int max_numel, Tensor(a!) out) -> ()");
+  m.def("pack_rows(Tensor input_ids, Tensor mask, Tensor labels, int n_tokens, Tensor(a!) ids, "
+        "Tensor(b!) positions, Tensor(c!) cu, Tensor(d!) targets, Tensor(e!) src) -> ()");
+  m.def("row_stats(Tensor mask, Tensor labels, Tensor(a!) stats) -> ()");
+  m.def("head_loss(Tensor token_loss, Tensor correct, Tensor targets, Tensor? num_items, "
+        "float num_items_value, int mode, Tensor(a!) loss, Tensor(b!) denom, "
+        "Tensor(c!) correct_bool) -> ()");
+  m.def("scatter_rows(Tensor token_loss, Tensor entropy, Tensor correct, Tensor targets, "
+        "Tensor src, Tensor(a!) full_loss, Tensor(b!) full_entropy, Tensor(c!) stats) -> ()");
+  m.def("scale_rows(Tensor g, Tensor grad_loss, Tensor denom, Tensor(a!) out) -> ()");
   m.def("gemm_algo_table(Tensor rows) -> ()", &gemm_algo_table);
   m.def("gemm_lib_version() -> int", &gemm_lib_version);
   m.def("gemm_tune(Tensor a, int trans_a, Tensor b, int trans_b, Tensor(a!) d, int m, int n, "
@@ -1171,4 +1308,9 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("nf4_gemm", &nf4_gemm);
   m.impl("nf4_block_scales", &nf4_block_scales);
   m.impl("lora_adamw", &lora_adamw);
+  m.impl("pack_rows", &pack_rows);
+  m.impl("row_stats", &row_stats);
+  m.impl("head_loss", &head_loss);
+  m.impl("scatter_rows", &scatter_rows);
+  m.impl("scale_rows", &scale_rows);
 }

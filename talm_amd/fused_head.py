@@ -126,10 +126,47 @@ def _denominator(num_items, labelled_count):
     return torch.tensor(float(num_items), device=labelled_count.device)
 
 
+def _loss(token_loss, correct, targets, num_items):
+    """(loss, denom, correct as bool): loss = sum(token_loss) / denom with `_denominator`'s denom
+    (solution/fused_head.py:272-277, :386), one launch (talm_head_loss) when the operands suit it;
+    `correct` is the head's int32 per-row flag."""
+    if (token_loss.is_cuda and token_loss.dtype == torch.float32 and token_loss.is_contiguous()
+            and correct.dtype == torch.int32 and correct.is_contiguous()
+            and targets.dtype == torch.int64 and targets.is_contiguous()
+            and (not torch.is_tensor(num_items) or num_items.numel() == 1)):
+        device = token_loss.device
+        mode, value, items = 0, 0.0, None
+        if torch.is_tensor(num_items):
+            mode, items = 1, num_items.to(device=device, dtype=torch.float32).reshape(())
+        elif num_items is not None:
+            mode, value = 2, float(num_items)
+        loss = torch.empty((), dtype=torch.float32, device=device)
+        denom = torch.empty_like(loss)
+        correct_bool = torch.empty(correct.shape, dtype=torch.bool, device=device)
+        torch.ops.talm.head_loss(token_loss, correct, targets, items, value, mode, loss, denom,
+                                 correct_bool)
+        return loss, denom, correct_bool
+    denom = _denominator(num_items, (targets >= 0).sum())
+    return token_loss.sum() / denom, denom, correct.to(torch.bool)
+
+
 def _head_backward(ctx, grad_loss):
+    """dH = grad_loss / denom * the saved gradient (0 when denom is 0), in the forward's dtype
+    (solution/fused_head.py:280-287); one launch (talm_scale_rows) for fp16."""
+    if grad_loss is None:  # the loss was not used (grads are not materialized)
+        return None
     (grad_hidden,) = ctx.saved_tensors
-    scale = grad_loss.to(torch.float32) / ctx.denom
-    scale = torch.where(ctx.denom != 0, scale, 0.0)
+    denom = ctx.denom
+    if (ctx.out_dtype == torch.float16 and grad_hidden.dtype == torch.float16
+            and grad_hidden.is_contiguous() and grad_hidden.data_ptr() % 16 == 0
+            and grad_loss.dtype == torch.float32 and grad_loss.numel() == 1
+            and denom.dtype == torch.float32 and denom.numel() == 1
+            and grad_loss.device == denom.device == grad_hidden.device):
+        out = torch.empty_like(grad_hidden)
+        torch.ops.talm.scale_rows(grad_hidden, grad_loss.reshape(()).contiguous(), denom, out)
+        return out
+    scale = grad_loss.to(torch.float32) / denom
+    scale = torch.where(denom != 0, scale, 0.0)
     return (grad_hidden.to(torch.float32) * scale).to(ctx.out_dtype)
 
 
@@ -160,22 +197,23 @@ class FusedHeadLossVocab(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden, weight, targets, num_items, vocab_chunk, need_grad, n_labelled):
+        # the per-token outputs are not differentiable: no zero gradients made up for them
+        ctx.set_materialize_grads(False)
         n_tokens = hidden.shape[0]
         h16 = hidden.detach().to(torch.float16)
         if h16.stride(1) != 1 or h16.stride(0) % 8 or h16.data_ptr() % 16:
             h16 = h16.contiguous()
         w16, wt = head_weights(weight, need_transpose=bool(need_grad))
         targets = targets.to(device=hidden.device, dtype=torch.int64).contiguous()
-        labelled = targets >= 0
         n_grad, dest, rows_targets = 0, None, targets
         if need_grad and n_tokens > 0:
             if n_labelled is None:
-                n_labelled = int(labelled.sum())
+                n_labelled = int((targets >= 0).sum())
             n_grad = int(n_labelled)
             if not COMPACT and 0 < n_grad < n_tokens:
                 raise ValueError("the MI355X head accumulates labelled-first rows only")
             if 0 < n_grad < n_tokens:
-                dest, src = labelled_first(labelled, n_grad)
+                dest, src = labelled_first(targets >= 0, n_grad)
                 h16 = h16.index_select(0, src)
                 rows_targets = targets.index_select(0, src)
                 RAN["compact"] += 1
@@ -189,9 +227,7 @@ class FusedHeadLossVocab(torch.autograd.Function):
             correct = correct.index_select(0, dest)
             best_idx = best_idx.index_select(0, dest)
             grad_hidden = grad_hidden.index_select(0, dest)
-        denom = _denominator(num_items, labelled.sum())
-        loss = token_loss.sum() / denom
-        correct = correct.to(torch.bool)
+        loss, denom, correct = _loss(token_loss, correct, targets, num_items)
         ctx.denom = denom
         ctx.out_dtype = hidden.dtype
         if need_grad:

@@ -99,7 +99,6 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
     kwargs.pop("return_dict", None)
     num_items = kwargs.pop("num_items_in_batch", None)
     batch, seq = labels.shape
-    shift = torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:].reshape(-1)
     unpad = ("unpad" not in DISABLED and _unpad["enabled"] and input_ids is not None
              and inputs_embeds is None and position_ids is None and past_key_values is None
              and isinstance(attention_mask, torch.Tensor) and attention_mask.dim() == 2
@@ -111,8 +110,9 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
     if n_static is not None:
         if not unpad:
             raise ValueError("fixed-shape packing needs a right-padded [B, T] batch with a mask")
-        return _static_forward(self, input_ids, attention_mask, labels, shift, n_static,
-                               num_items, kwargs, output_cls, stage)
+        return _static_forward(self, input_ids, attention_mask, labels, n_static, num_items,
+                               kwargs, output_cls, stage)
+    shift = torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:].reshape(-1)
     if unpad:
         try:
             idx, positions, bounds, lengths, counts = unpad_batch(
@@ -155,21 +155,45 @@ def _fused_forward(self, input_ids, attention_mask, position_ids, past_key_value
         hidden.reshape(-1, size), self.lm_head.weight, shift, num_items, n_labelled=n_labelled,
         return_argmax=True)
     if unpad:
-        full_loss = token_loss.new_zeros(batch * seq)
-        full_entropy = token_entropy.new_zeros(batch * seq)
-        full_loss[idx] = token_loss
-        full_entropy[idx] = token_entropy
-        token_loss, token_entropy = full_loss, full_entropy
+        token_loss, token_entropy, n_correct, n_targets = scatter_metrics(
+            token_loss, token_entropy, correct, shift, idx, batch * seq)
+    else:
+        n_correct, n_targets = correct.sum(), (shift >= 0).sum()
     LAST_STEP.clear()
     LAST_STEP.append(SimpleNamespace(
         token_entropy=token_entropy.view(batch, seq), token_loss=token_loss.view(batch, seq),
-        correct=correct.sum(), labelled=(shift >= 0).sum(), argmax=argmax))
+        correct=n_correct, labelled=n_targets, argmax=argmax))
     return output_cls(loss=loss, logits=None, past_key_values=None,
                       hidden_states=outputs.hidden_states, attentions=outputs.attentions)
 
 
-def _static_forward(self, input_ids, mask, labels, shift, n_tokens, num_items, kwargs,
-                    output_cls, stage):
+def scatter_metrics(token_loss, token_entropy, correct, targets, src, out_len):
+    """The per-token loss and entropy of the packed rows back to `out_len` batch slots (zero
+    where no row lands; row i lands on slot src[i]) and the step's metric sums: (full loss, full
+    entropy, #correct, #targets >= 0) (solution/patches.py:244-253). One launch
+    (talm_scatter_rows) when the operands suit it."""
+    import torch
+
+    if (token_loss.is_cuda and token_loss.dtype == torch.float32 and token_loss.is_contiguous()
+            and token_entropy.dtype == torch.float32 and token_entropy.is_contiguous()
+            and correct.dtype == torch.bool and correct.is_contiguous()
+            and targets.dtype == torch.int64 and targets.is_contiguous()
+            and src.dtype == torch.int64 and src.is_contiguous()):
+        full_loss = torch.empty(out_len, dtype=torch.float32, device=token_loss.device)
+        full_entropy = torch.empty_like(full_loss)
+        stats = torch.empty(2, dtype=torch.int64, device=token_loss.device)
+        torch.ops.talm.scatter_rows(token_loss, token_entropy, correct, targets, src, full_loss,
+                                    full_entropy, stats)
+        return full_loss, full_entropy, stats[0], stats[1]
+    full_loss = token_loss.new_zeros(out_len)
+    full_entropy = token_entropy.new_zeros(out_len)
+    full_loss.index_copy_(0, src, token_loss)
+    full_entropy.index_copy_(0, src, token_entropy)
+    return full_loss, full_entropy, correct.sum(), (targets >= 0).sum()
+
+
+def _static_forward(self, input_ids, mask, labels, n_tokens, num_items, kwargs, output_cls,
+                    stage):
     """`_fused_forward` with the fixed-shape packing of `unpad.static_tokens` (a step captured in
     a HIP graph): the batch is packed into `n_tokens` rows on the device, the pad rows form their
     own sequence labelled -100, and the head takes every row as a gradient row (an ignored row's
@@ -179,13 +203,11 @@ def _static_forward(self, input_ids, mask, labels, shift, n_tokens, num_items, k
     from .engaged import RAN
     from .fused_head import fused_head_loss
     from .rmsnorm import link_next_norms
-    from .unpad import rows_context_static, static_max_len, unpad_static
-
-    import torch
+    from .unpad import pack_static, rows_context_static, static_max_len
 
     batch, seq = labels.shape
-    src, positions, cu, rows_targets = unpad_static(mask, shift.to(mask.device), n_tokens)
-    ids = torch.cat((input_ids.reshape(-1), input_ids.new_zeros(1))).index_select(0, src)
+    ids, positions, cu, rows_targets, src = pack_static(input_ids.to(mask.device), mask,
+                                                        labels.to(mask.device), n_tokens)
     RAN["fused_head"] += 1
     RAN["unpad"] += 1
     link_next_norms(self.model)
@@ -200,15 +222,13 @@ def _static_forward(self, input_ids, mask, labels, shift, n_tokens, num_items, k
         hidden.reshape(-1, hidden.shape[-1]), self.lm_head.weight, rows_targets, num_items,
         return_argmax=True, grad_all_rows=True)
     # back to [B, T]: the pad rows all land on one extra slot, dropped
-    full_loss = token_loss.new_zeros(batch * seq + 1)
-    full_entropy = token_entropy.new_zeros(batch * seq + 1)
-    full_loss.index_copy_(0, src, token_loss)
-    full_entropy.index_copy_(0, src, token_entropy)
+    full_loss, full_entropy, n_correct, n_targets = scatter_metrics(
+        token_loss, token_entropy, correct, rows_targets, src, batch * seq + 1)
     LAST_STEP.clear()
     LAST_STEP.append(SimpleNamespace(
         token_entropy=full_entropy[:-1].view(batch, seq),
-        token_loss=full_loss[:-1].view(batch, seq), correct=correct.sum(),
-        labelled=(rows_targets >= 0).sum(), argmax=argmax))
+        token_loss=full_loss[:-1].view(batch, seq), correct=n_correct, labelled=n_targets,
+        argmax=argmax))
     return output_cls(loss=loss, logits=None, past_key_values=None,
                       hidden_states=outputs.hidden_states, attentions=outputs.attentions)
 

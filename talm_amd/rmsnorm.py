@@ -39,7 +39,8 @@ _HANDOVER = "_talm_next_normed"  # attribute of a residual sum: (norm module, it
 def launch(a, weight, h, xhat, rstd, eps, backward, p=None, q=None):
     """The one launch site of the kernel (solution/rmsnorm.py:103-118): a, h, xhat (and p, q)
     are contiguous [N, H]; forward reads a (+ p) and writes h, xhat, rstd (and q = a + p);
-    backward reads h (= dy), xhat, rstd (and q = ds) and writes a (= dx) (and p = dx)."""
+    backward reads h (= dy), xhat, rstd (and q = ds; None: ds = 0) and writes a (= dx) (and
+    p = dx)."""
     torch.ops.talm.rmsnorm(a, q, h, xhat, p, weight, rstd, float(eps), int(backward))
 
 
@@ -92,10 +93,9 @@ class NormNode(torch.autograd.Function):
             return ds, ds.to(ctx.branch_dtype), None, None, None
         component = "addnorm" if add else "rmsnorm"
         dys = _flat(dy, xhat.dtype)
-        dss = None
-        if add:
-            dss = torch.zeros(xhat.shape, dtype=ctx.x_dtype, device=dy.device) if ds is None \
-                else _flat(ds, ctx.x_dtype)
+        # no gradient of the sum (the final norm: only its output is used): the kernel takes
+        # ds = 0 without a zero-filled operand
+        dss = _flat(ds, ctx.x_dtype) if add and ds is not None else None
         if component not in DISABLED:
             try:
                 dx = torch.empty(xhat.shape, dtype=ctx.x_dtype, device=dy.device)
@@ -115,7 +115,8 @@ class NormNode(torch.autograd.Function):
         dx32 = _dx_torch(dys, xhat, weight, rstd)
         if not add:
             return NormNode._grads(ctx, dx32.to(ctx.x_dtype), None)
-        dx32 = dx32 + dss.float()
+        if dss is not None:
+            dx32 = dx32 + dss.float()
         return NormNode._grads(ctx, dx32.to(ctx.x_dtype), dx32.to(ctx.branch_dtype))
 
     @staticmethod

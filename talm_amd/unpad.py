@@ -61,6 +61,13 @@ def _row_values(attention_mask, targets=None):
     return torch.cat((lengths, torch.stack(((lab & prefix).sum(), lab.sum()))))
 
 
+def _int64_rows(*tensors):
+    """The [B, T] batch tensors suit the packing kernels: contiguous int64 on one GPU."""
+    first = tensors[0]
+    return all(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous() and t.dim() == 2
+               and t.shape == first.shape and t.device == first.device for t in tensors)
+
+
 def _batch_key(attention_mask, labels):
     return (attention_mask.data_ptr(), attention_mask._version, tuple(attention_mask.shape),
             labels.data_ptr(), labels._version, tuple(labels.shape))
@@ -74,8 +81,14 @@ def prefetch(attention_mask, labels):
     if not (attention_mask.is_cuda and attention_mask.dim() == 2 and labels.dim() == 2
             and tuple(labels.shape) == tuple(attention_mask.shape)):
         return
-    shift = torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:].reshape(-1)
-    values = _row_values(attention_mask, shift.to(attention_mask.device))
+    if _int64_rows(attention_mask, labels):
+        # one launch (talm_row_stats) for the lengths and both labelled counts
+        values = torch.empty(attention_mask.shape[0] + 2, dtype=torch.int64,
+                             device=attention_mask.device)
+        torch.ops.talm.row_stats(attention_mask, labels, values)
+    else:
+        shift = torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:].reshape(-1)
+        values = _row_values(attention_mask, shift.to(attention_mask.device))
     host = torch.empty(values.shape, dtype=torch.int64, pin_memory=True)
     host.copy_(values, non_blocking=True)
     event = torch.cuda.Event()
@@ -182,6 +195,29 @@ def unpad_static(attention_mask, targets, n_tokens):
     src = torch.where(row < batch, row * seq + pos, batch * seq)
     ext = torch.cat((targets.reshape(-1), targets.new_full((1,), -100)))
     return src, pos.to(torch.int64)[None], cu, ext.index_select(0, src)
+
+
+def pack_static(input_ids, attention_mask, labels, n_tokens):
+    """`unpad_static` from the unshifted batch, with the ids gathered: (ids [n_tokens], positions
+    [1, n_tokens], cu_seqlens int32 [B + 2], targets [n_tokens], src [n_tokens]). One launch
+    (talm_pack_rows) for contiguous int64 batch tensors; the same values as shifting the labels
+    and composing `unpad_static` with the id gather otherwise. Row lengths are clamped to the
+    row width (a mask whose row sums exceed it is not a right-padded mask)."""
+    n_tokens = int(n_tokens)
+    if _int64_rows(input_ids, attention_mask, labels):
+        device = attention_mask.device
+        ids, positions, targets, src = (torch.empty(n_tokens, dtype=torch.int64, device=device)
+                                        for _ in range(4))
+        cu = torch.empty(attention_mask.shape[0] + 2, dtype=torch.int32, device=device)
+        torch.ops.talm.pack_rows(input_ids, attention_mask, labels, n_tokens, ids, positions, cu,
+                                 targets, src)
+        RAN["pack_rows"] += 1
+        return ids, positions[None], cu, targets, src
+    shift = torch.nn.functional.pad(labels, (0, 1), value=-100)[:, 1:].reshape(-1)
+    src, positions, cu, targets = unpad_static(attention_mask, shift.to(attention_mask.device),
+                                               n_tokens)
+    ids = torch.cat((input_ids.reshape(-1), input_ids.new_zeros(1))).index_select(0, src)
+    return ids, positions, cu, targets, src
 
 
 @contextlib.contextmanager

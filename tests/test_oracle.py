@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import codebook, head, nf4, norm, rope, swiglu
+from oracle import codebook, head, nf4, norm, pack, rope, swiglu
 from talm_amd import quant
 
 
@@ -372,3 +372,73 @@ def test_torch_cpu_dequant_equals_the_group_oracle():
                             state.state2.code.numpy(), state.state2.absmax.numpy(),
                             np.full(n_blk2, float(state.offset), np.float32))
     assert np.array_equal(ours.view(torch.int16).numpy().view(np.uint16).reshape(-1), ref)
+
+
+# ---------------------------------------------------------------------------- batch packing -----
+
+def _batch(seed, batch, seq, lengths=None, vocab=1000):
+    rng = np.random.default_rng(seed)
+    if lengths is None:
+        lengths = rng.integers(0, seq + 1, batch)
+    mask = (np.arange(seq)[None] < np.asarray(lengths)[:, None]).astype(np.int64)
+    ids = rng.integers(0, vocab, (batch, seq))
+    labels = np.where(mask == 1, ids, -100)
+    labels[rng.random((batch, seq)) < 0.2] = -100  # some real tokens unlabelled
+    return ids, mask, labels
+
+
+def test_pack_rows_known_answer():
+    """A 3 x 4 batch worked by hand: rows of 2, 0 and 3 tokens packed into 7 rows."""
+    ids = np.array([[11, 12, 0, 0], [21, 22, 23, 24], [31, 32, 33, 0]])
+    mask = np.array([[1, 1, 0, 0], [0, 0, 0, 0], [1, 1, 1, 0]])
+    labels = np.array([[11, 12, -100, -100], [-100] * 4, [31, -100, 33, -100]])
+    got = pack.pack_rows(ids, mask, labels, 7)
+    expect = ([11, 12, 31, 32, 33, 0, 0],          # ids (0 in the pad sequence)
+              [0, 1, 0, 1, 2, 0, 1],               # positions (the pad sequence restarts)
+              [0, 2, 2, 5, 7],                     # cu_seqlens (row 1 empty)
+              [12, -100, -100, 33, -100, -100, -100],  # labels[b][p + 1], -100 at the row end
+              [0, 1, 8, 9, 10, 12, 12])            # src (the pad slot is 3 * 4)
+    for g, e in zip(got, expect):
+        assert g.tolist() == e
+    assert pack.row_stats(mask, labels).tolist() == [2, 0, 3, 2, 2]
+
+
+@pytest.mark.parametrize("batch,seq,seed", [(4, 512, 0), (1, 1, 1), (7, 33, 2), (3, 64, 3)])
+def test_pack_rows_equals_the_reference_packing_and_the_torch_form(batch, seq, seed):
+    """The fixed-shape packing's real rows are the reference's `unpad_batch` gather (ids, labels
+    shifted then gathered, positions); its offsets, pad sequence and truncation equal
+    unpad.unpad_static's matrix-and-search formulation run on the CPU, at n_tokens above, at and
+    below the real token count."""
+    from talm_amd import unpad
+
+    ids, mask, labels = _batch(seed, batch, seq)
+    idx, positions, lengths, _counts = pack.unpad_batch(mask, labels)
+    total = len(idx)
+    shift = pack.shift_labels(labels)
+    for n_tokens in sorted({max(total, 1), total + 5, max(total // 2, 1), total + 16}):
+        got_ids, got_pos, cu, targets, src = pack.pack_rows(ids, mask, labels, n_tokens)
+        keep = min(total, n_tokens)
+        assert np.array_equal(src[:keep], idx[:keep])
+        assert np.array_equal(got_pos[:keep], positions[:keep])
+        assert np.array_equal(got_ids[:keep], ids.reshape(-1)[idx[:keep]])
+        assert np.array_equal(targets[:keep], shift[idx[:keep]])
+        assert np.all(src[keep:] == batch * seq) and np.all(targets[keep:] == -100)
+        t_src, t_pos, t_cu, t_targets = unpad.unpad_static(
+            torch.from_numpy(mask), torch.from_numpy(shift), n_tokens)
+        assert np.array_equal(t_src.numpy(), src) and np.array_equal(t_cu.numpy(), cu)
+        assert np.array_equal(t_pos[0].numpy(), got_pos)
+        assert np.array_equal(t_targets.numpy(), targets)
+        assert cu[-1] == n_tokens and np.all(np.diff(cu) >= 0)
+
+
+def test_row_stats_and_scatter_equal_the_torch_forms():
+    from talm_amd import unpad
+
+    ids, mask, labels = _batch(5, 6, 40)
+    shift = pack.shift_labels(labels)
+    expect = unpad._row_values(torch.from_numpy(mask), torch.from_numpy(shift))
+    assert pack.row_stats(mask, labels).tolist() == expect.tolist()
+    idx, _pos, _l, _c = pack.unpad_batch(mask, labels)
+    values = np.random.default_rng(6).standard_normal(len(idx)).astype(np.float32)
+    full = torch.zeros(6 * 40).index_copy_(0, torch.from_numpy(idx), torch.from_numpy(values))
+    assert np.array_equal(pack.scatter(values, idx, 6 * 40), full.numpy())
