@@ -99,6 +99,16 @@ int64_t talm_gemm_splitk_workspace(int64_t m, int64_t n, int64_t k);
 int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                      uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k, void* workspace,
                      int64_t workspace_bytes, void* stream);
+/*
+ * The same product leaving its fp32 partials [parts][m][n] in `partials` (no reduction, no fp16
+ * output), for a caller whose next launch sums them (talm_splitk_add_rmsnorm,
+ * talm_splitk_rmsnorm_bwd); talm_gemm_splitk_parts gives the part count (-1 for an unsupported
+ * shape), partials_bytes >= parts * m * n * 4.
+ */
+int64_t talm_gemm_splitk_parts(int64_t m, int64_t n, int64_t k);
+int talm_gemm_splitk_partials(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                              int64_t m, int64_t n, int64_t k, float* partials,
+                              int64_t partials_bytes, void* stream);
 
 /*
  * Per-projection NF4 dequantization with an fp32 absmax per block (bitsandbytes'
@@ -124,6 +134,28 @@ int talm_nf4_dequant(const uint8_t* packed, const float* absmax, uint16_t* out, 
 int talm_rmsnorm(void* a, void* q, void* h, void* xhat, void* p, const void* weight, float* rstd,
                  int64_t n_rows, int64_t n_cols, int32_t x_dtype, int32_t out_dtype,
                  int32_t w_dtype, float eps, int32_t backward, int32_t add, void* stream);
+
+/*
+ * talm_rmsnorm's residual-add forward and backward with the branch (forward) or dy (backward)
+ * given as a split-K product's fp32 partials [parts][n_rows][n_cols] (talm_gemm_splitk_partials,
+ * talm_nf4_gemm_partials): the partials are summed in part order and rounded to fp16, exactly the
+ * values the product's own reduction would write, and the norm then runs as talm_rmsnorm does on
+ * them (bit-identical to the two launches). x fp32, outputs fp16, weight w_dtype (f32 / f16);
+ * n_cols a multiple of 8, at most 2048; 16-byte aligned rows.
+ *   talm_splitk_add_rmsnorm: x = resid + branch -> sum_out, h = w * xhat, xhat, rstd.
+ *   talm_splitk_rmsnorm_bwd: dx = rstd (g - xhat mean(g xhat)) (+ ds; NULL: 0), g = dy * w, to dx
+ *                            (fp32) and dbranch (fp16).
+ * No counterpart of its own: they fuse the K-part reduction of the MLP's long products with the
+ * residual add and RMSNorm that follow (solution/rmsnorm.py:335-404) or precede them.
+ */
+int talm_splitk_add_rmsnorm(const float* partials, int32_t parts, const float* resid,
+                            const void* weight, int32_t w_dtype, float eps, int64_t n_rows,
+                            int64_t n_cols, float* sum_out, uint16_t* h, uint16_t* xhat,
+                            float* rstd, void* stream);
+int talm_splitk_rmsnorm_bwd(const float* partials, int32_t parts, const uint16_t* xhat,
+                            const float* rstd, const void* weight, int32_t w_dtype, const float* ds,
+                            int64_t n_rows, int64_t n_cols, float* dx, uint16_t* dbranch,
+                            void* stream);
 
 /*
  * Rotary position embedding of q and k, forward or backward, fp16 with fp32 math.
@@ -443,6 +475,17 @@ int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_
                   const float* scale, int64_t rows, int64_t cols, int32_t transpose,
                   int32_t blocksize, uint16_t* out, int64_t ldo, void* workspace,
                   int64_t workspace_bytes, void* stream);
+/*
+ * talm_nf4_gemm leaving fp32 partials [parts][n_tokens][n] (n = rows, or cols with transpose)
+ * in `partials`, also when the plan has one part (talm_nf4_gemm_parts; -1 for an unsupported
+ * shape); partials_bytes >= parts * n_tokens * n * 4. For the same callers as
+ * talm_gemm_splitk_partials.
+ */
+int64_t talm_nf4_gemm_parts(int64_t n_tokens, int64_t rows, int64_t cols, int32_t transpose);
+int talm_nf4_gemm_partials(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_t* packed,
+                           const float* scale, int64_t rows, int64_t cols, int32_t transpose,
+                           int32_t blocksize, float* partials, int64_t partials_bytes,
+                           void* stream);
 
 /*
  * The packed causal-LM step's per-step glue (each one launch of one workgroup for the batch

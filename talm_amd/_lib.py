@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -67,6 +67,10 @@ SIGNATURES = {
     "talm_nf4_gemm": [_P, _I64, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _I64, _P, _I64, _P],
     "talm_nf4_block_scales": [_P, _P, _P, _P, _I64, _I32, _P, _P],
     "talm_gemm_splitk": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "talm_gemm_splitk_partials": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "talm_nf4_gemm_partials": [_P, _I64, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _I64, _P],
+    "talm_splitk_add_rmsnorm": [_P, _I32, _P, _P, _I32, _F32, _I64, _I64, _P, _P, _P, _P, _P],
+    "talm_splitk_rmsnorm_bwd": [_P, _I32, _P, _P, _P, _I32, _P, _I64, _I64, _P, _P, _P],
 }
 
 # Entry points that return a size instead of a status.
@@ -76,6 +80,8 @@ SIZE_FUNCTIONS = {
     "talm_attn_bwd_workspace": [_I64, _I32],
     "talm_gemm_splitk_workspace": [_I64, _I64, _I64],
     "talm_nf4_gemm_workspace": [_I64, _I64, _I64, _I32],
+    "talm_gemm_splitk_parts": [_I64, _I64, _I64],
+    "talm_nf4_gemm_parts": [_I64, _I64, _I64, _I32],
 }
 
 _lock = threading.Lock()

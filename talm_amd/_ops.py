@@ -24,7 +24,8 @@ OPS = ("nf4_group_dequant", "nf4_group_dequant_streaming", "nf4_dequant", "rmsno
        "head_weight_t", "head_ce", "lora_down", "qkv_lora_fwd", "qkv_bwd_prep", "qkv_lora_bwd_dx",
        "lora_wgrad", "gemm", "gemm_ex", "attn_fwd", "attn_bwd", "attn_bwd_rope", "lora_mirror",
        "lora_adamw", "nf4_gemm", "nf4_block_scales", "nf4_group_dequant_t", "gemm_splitk",
-       "pack_rows", "row_stats", "head_loss", "scatter_rows", "scale_rows")
+       "pack_rows", "row_stats", "head_loss", "scatter_rows", "scale_rows",
+       "gemm_splitk_partials", "nf4_gemm_partials", "splitk_add_rmsnorm", "splitk_rmsnorm_bwd")
 
 _load_lock = threading.Lock()
 _loaded = False
@@ -88,3 +89,19 @@ def nf4_gemm_workspace_bytes(n_tokens, rows, cols, transpose):
     if size < 0:
         raise ValueError(f"nf4_gemm: unsupported shape tokens={n_tokens} W=[{rows}, {cols}]")
     return size
+
+
+def gemm_splitk_parts(m, n, k):
+    """K parts of the split-K GEMM's plan for [m, k] x [n, k]^T (its partials: parts x m x n)."""
+    parts = _lib.lib().talm_gemm_splitk_parts(m, n, k)
+    if parts < 1:
+        raise ValueError(f"gemm_splitk: unsupported shape m={m} n={n} k={k}")
+    return int(parts)
+
+
+def nf4_gemm_parts(n_tokens, rows, cols, transpose):
+    """K parts of the W4A16 GEMM's plan (its partials: parts x n_tokens x out columns)."""
+    parts = _lib.lib().talm_nf4_gemm_parts(n_tokens, rows, cols, 1 if transpose else 0)
+    if parts < 1:
+        raise ValueError(f"nf4_gemm: unsupported shape tokens={n_tokens} W=[{rows}, {cols}]")
+    return int(parts)

@@ -86,24 +86,28 @@ TALM_API int64_t talm_gemm_splitk_workspace(int64_t m, int64_t n, int64_t k) {
   return static_cast<int64_t>(plan_split(m, n, k, SplitShape::kBM, SplitShape::kBN, SplitShape::kBK).parts) * m * n * 4;
 }
 
-TALM_API int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                              uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
-                              void* workspace, int64_t workspace_bytes, void* stream) {
-  if (!splitk_shape_ok(m, n, k) || lda < k || ldb < k || ldo < n || lda % 8 || ldb % 8 ||
-      ldo % 8 || lda > (1 << 22) || ldb > (1 << 22))
+namespace talm {
+namespace {
+
+// out == nullptr: the fp32 partials stay in the workspace for the caller's next launch.
+int splitk_impl(const char* what, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k, void* workspace,
+                int64_t workspace_bytes, hipStream_t s) {
+  if (!splitk_shape_ok(m, n, k) || lda < k || ldb < k || (out && (ldo < n || ldo % 8)) ||
+      lda % 8 || ldb % 8 || lda > (1 << 22) || ldb > (1 << 22))
     return fail(TALM_EINVAL,
-                "gemm_splitk: bad shape (m %lld, n %lld, k %lld, lda %lld, ldb %lld, ldo %lld): "
+                "%s: bad shape (m %lld, n %lld, k %lld, lda %lld, ldb %lld, ldo %lld): "
                 "n, k and the strides multiples of 8, strides at least k (a, b) and n (out), "
                 "a / b strides below 2^22",
-                (long long)m, (long long)n, (long long)k, (long long)lda, (long long)ldb,
+                what, (long long)m, (long long)n, (long long)k, (long long)lda, (long long)ldb,
                 (long long)ldo);
-  if (!a || !b || !out || !workspace) return fail(TALM_EINVAL, "gemm_splitk: null pointer");
+  if (!a || !b || !workspace) return fail(TALM_EINVAL, "%s: null pointer", what);
   if (!aligned(a, 16) || !aligned(b, 16) || !aligned(out, 16) || !aligned(workspace, 16))
-    return fail(TALM_EINVAL, "gemm_splitk: operands and workspace must be 16-byte aligned");
+    return fail(TALM_EINVAL, "%s: operands and workspace must be 16-byte aligned", what);
   const SplitPlan p = plan_split(m, n, k, SplitShape::kBM, SplitShape::kBN, SplitShape::kBK);
   const int64_t need = static_cast<int64_t>(p.parts) * m * n * 4;
   if (workspace_bytes < need)
-    return fail(TALM_EINVAL, "gemm_splitk: workspace of %lld bytes, %lld needed",
+    return fail(TALM_EINVAL, "%s: workspace of %lld bytes, %lld needed", what,
                 (long long)workspace_bytes, (long long)need);
   SplitArgs args{};
   args.A = a; args.lda = lda; args.B = b; args.ldb = ldb;
@@ -112,9 +116,31 @@ TALM_API int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b,
   args.steps_per_part = p.steps_per_part;
   args.n_mtiles = p.n_mtiles; args.n_ntiles = p.n_ntiles;
   args.n_tiles = p.n_mtiles * p.n_ntiles * p.parts;
-  const hipStream_t s = as_stream(stream);
   hipLaunchKernelGGL((gemm_splitk_kernel<SplitShape>), dim3(static_cast<unsigned>(args.n_tiles)),
                      dim3(SplitShape::kThreads), 0, s, args);
-  launch_splitk_reduce(static_cast<const float*>(workspace), p.parts, m, n, out, ldo, s);
-  return check_launch("gemm_splitk");
+  if (out) launch_splitk_reduce(static_cast<const float*>(workspace), p.parts, m, n, out, ldo, s);
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace talm
+
+TALM_API int talm_gemm_splitk(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                              uint16_t* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                              void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!out) return fail(TALM_EINVAL, "gemm_splitk: null pointer");
+  return splitk_impl("gemm_splitk", a, lda, b, ldb, out, ldo, m, n, k, workspace,
+                     workspace_bytes, as_stream(stream));
+}
+
+TALM_API int64_t talm_gemm_splitk_parts(int64_t m, int64_t n, int64_t k) {
+  if (!splitk_shape_ok(m, n, k)) return -1;
+  return plan_split(m, n, k, SplitShape::kBM, SplitShape::kBN, SplitShape::kBK).parts;
+}
+
+TALM_API int talm_gemm_splitk_partials(const uint16_t* a, int64_t lda, const uint16_t* b,
+                                       int64_t ldb, int64_t m, int64_t n, int64_t k,
+                                       float* partials, int64_t partials_bytes, void* stream) {
+  return splitk_impl("gemm_splitk_partials", a, lda, b, ldb, nullptr, 0, m, n, k, partials,
+                     partials_bytes, as_stream(stream));
 }

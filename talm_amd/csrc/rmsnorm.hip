@@ -341,3 +341,223 @@ TALM_API int talm_rmsnorm(void* a, void* q, void* h, void* xhat, void* p, const 
     dispatch_w<uint16_t, float>(w_dtype, ad, a, q, h, xhat, p, weight, rstd, n_rows, cols, eps, bwd, vec, s);
   return check_launch("rmsnorm");
 }
+
+namespace talm {
+namespace {
+
+// The split-K forms: the branch (forward) or dy (backward) of a row given as a split-K GEMM's
+// fp32 K-part partials [parts][n_rows][n_cols], summed in part order from +0 and rounded to
+// fp16 (the values splitk_reduce_kernel would write for the vector kernels to read back), for
+// XT fp32 (the residual stream) and OT fp16 (autocast). One workgroup per row and one 8-column
+// chunk per thread (chunk 64 w + l in lane l of wavefront w), so there are as many threads in
+// flight as in the plain reduction. The row's reduction is folded in the vector kernels' order
+// (lane l accumulates chunks l, l + 64, ... in turn: wavefront w continues the fold of w - 1,
+// handed over through LDS), then the same butterfly: the results are those of the reduction
+// followed by the vector kernel, bit for bit.
+template <int NW>
+__device__ __forceinline__ float fold_row(float f, const float (&x)[8], const float (&y)[8],
+                                          bool live, float* handoff) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    if (wave == w) {
+      if (w > 0) f = handoff[lane];
+      if (live)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f += x[e] * y[e];
+      if (w < NW - 1) handoff[lane] = f;
+    }
+    if (w < NW - 1) __syncthreads();
+  }
+  return f;  // the lane's whole fold in the last wavefront
+}
+
+__device__ __forceinline__ void part_sum8(const float* __restrict__ part, int parts, int64_t mn,
+                                          int64_t at, float (&v)[8]) {
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < parts; k0 += 8) {
+    float t[8][8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      IO<float>::load8_nt(part + static_cast<int64_t>(min(k0 + kk, parts - 1)) * mn + at, t[kk]);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bool live = k0 + kk < parts;  // a part past the last adds +0
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[e] += live ? t[kk][e] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = h2f(f2h(s[e]));
+}
+
+template <typename WT, int NW>
+__global__ __launch_bounds__(64 * NW) void rms_fwd_parts(
+    const float* __restrict__ part, int parts, const float* __restrict__ a,
+    const WT* __restrict__ w, float* __restrict__ q, uint16_t* __restrict__ h,
+    uint16_t* __restrict__ xhat, float* __restrict__ rstd, int64_t n_rows, int n_cols,
+    float eps) {
+  __shared__ float handoff[kWave];
+  __shared__ float r_shared;
+  const int64_t row = blockIdx.x;
+  const int n_chunks = n_cols / 8;
+  const int c = static_cast<int>(threadIdx.x), cc = min(c, n_chunks - 1);
+  const bool live = c < n_chunks;
+  const int64_t at = row * n_cols + 8 * cc;
+  float x[8], wv[8], pv[8];
+  IO<float>::load8_nt(a + at, x);
+  IO<WT>::load8(w + 8 * cc, wv);
+  part_sum8(part, parts, n_rows * n_cols, at, pv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] += pv[e];
+  if (live) IO<float>::store8(q + at, x);
+  float ss = fold_row<NW>(0.f, x, x, live, handoff);
+  if ((threadIdx.x >> 6) == NW - 1) {
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) {
+      const float r = rsqrtf(ss / static_cast<float>(n_cols) + eps);
+      rstd[row] = r;
+      r_shared = r;
+    }
+  }
+  __syncthreads();
+  const float r = r_shared;
+  if (live) {
+    float xh[8], y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xh[e] = x[e] * r;
+      y[e] = wv[e] * xh[e];
+    }
+    IO<uint16_t>::store8(h + at, y);
+    IO<uint16_t>::store8(xhat + at, xh);
+  }
+}
+
+template <typename WT, int NW>
+__global__ __launch_bounds__(64 * NW) void rms_bwd_parts(
+    const float* __restrict__ part, int parts, const uint16_t* __restrict__ xhat,
+    const WT* __restrict__ w, const float* __restrict__ rstd, const float* __restrict__ ds,
+    float* __restrict__ dx, uint16_t* __restrict__ dbranch, int64_t n_rows, int n_cols) {
+  __shared__ float handoff[kWave];
+  __shared__ float m_shared;
+  const int64_t row = blockIdx.x;
+  const int n_chunks = n_cols / 8;
+  const int c = static_cast<int>(threadIdx.x), cc = min(c, n_chunks - 1);
+  const bool live = c < n_chunks;
+  const int64_t at = row * n_cols + 8 * cc;
+  float xh[8], wv[8], dsv[8], g[8];
+  IO<uint16_t>::load8_nt(xhat + at, xh);
+  IO<WT>::load8(w + 8 * cc, wv);
+  if (ds) {
+    IO<float>::load8_nt(ds + at, dsv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dsv[e] = 0.f;  // no sum gradient: ds = 0
+  }
+  part_sum8(part, parts, n_rows * n_cols, at, g);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g[e] *= wv[e];
+  float dot = fold_row<NW>(0.f, g, xh, live, handoff);
+  if ((threadIdx.x >> 6) == NW - 1) {
+    dot = wave_sum(dot);
+    if ((threadIdx.x & 63) == 0) m_shared = dot / static_cast<float>(n_cols);
+  }
+  __syncthreads();
+  const float cmean = m_shared, r = rstd[row];
+  if (live) {
+    float d[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = r * (g[e] - xh[e] * cmean);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] += dsv[e];
+    IO<uint16_t>::store8(dbranch + at, d);
+    IO<float>::store8(dx + at, d);
+  }
+}
+
+template <typename WT, bool BWD>
+void launch_parts(const float* part, int parts, const float* resid, const float* ds,
+                  const uint16_t* xhat_in, const void* weight, int64_t n_rows, int n_cols,
+                  float eps, float* x_out, uint16_t* h, uint16_t* xhat, float* rstd,
+                  hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(n_rows));
+  const WT* w = static_cast<const WT*>(weight);
+  const int nw = (n_cols / 8 + kWave - 1) / kWave;
+  switch (nw) {
+#define TALM_RMS_PARTS(NW)                                                                  \
+  case NW:                                                                                  \
+    if constexpr (BWD)                                                                      \
+      hipLaunchKernelGGL((rms_bwd_parts<WT, NW>), grid, dim3(64 * NW), 0, s, part, parts,   \
+                         xhat_in, w, rstd, ds, x_out, h, n_rows, n_cols);                   \
+    else                                                                                    \
+      hipLaunchKernelGGL((rms_fwd_parts<WT, NW>), grid, dim3(64 * NW), 0, s, part, parts,   \
+                         resid, w, x_out, h, xhat, rstd, n_rows, n_cols, eps);              \
+    break;
+    TALM_RMS_PARTS(1) TALM_RMS_PARTS(2) TALM_RMS_PARTS(3) TALM_RMS_PARTS(4)
+#undef TALM_RMS_PARTS
+  }
+}
+
+int check_parts(const char* what, const float* part, int32_t parts, int64_t n_rows,
+                int64_t n_cols, int32_t w_dtype, const void* weight) {
+  if (w_dtype != TALM_F32 && w_dtype != TALM_F16)
+    return fail(TALM_EINVAL, "%s: unsupported weight dtype code %d", what, w_dtype);
+  if (parts < 1 || parts > 4096 || n_rows < 0 || n_cols < 8 || n_cols % 8 || n_cols > 2048 ||
+      n_rows * n_cols > (int64_t{1} << 40))
+    return fail(TALM_EINVAL,
+                "%s: bad shape (parts %d, rows %lld, columns %lld): columns a multiple of 8, at "
+                "most 2048",
+                what, parts, (long long)n_rows, (long long)n_cols);
+  if (n_rows > 0 && (!part || !weight)) return fail(TALM_EINVAL, "%s: null pointer", what);
+  if (!aligned(part, 16) || !aligned(weight, 16))
+    return fail(TALM_EINVAL, "%s: partials and weight must be 16-byte aligned", what);
+  return TALM_OK;
+}
+
+}  // namespace
+}  // namespace talm
+
+TALM_API int talm_splitk_add_rmsnorm(const float* partials, int32_t parts, const float* resid,
+                                     const void* weight, int32_t w_dtype, float eps,
+                                     int64_t n_rows, int64_t n_cols, float* sum_out,
+                                     uint16_t* h, uint16_t* xhat, float* rstd, void* stream) {
+  if (check_parts("splitk_add_rmsnorm", partials, parts, n_rows, n_cols, w_dtype, weight))
+    return TALM_EINVAL;
+  if (n_rows == 0) return ok();
+  if (!resid || !sum_out || !h || !xhat || !rstd)
+    return fail(TALM_EINVAL, "splitk_add_rmsnorm: null pointer");
+  if (!aligned(resid, 16) || !aligned(sum_out, 16) || !aligned(h, 16) || !aligned(xhat, 16))
+    return fail(TALM_EINVAL, "splitk_add_rmsnorm: row operands must be 16-byte aligned");
+  const hipStream_t s = as_stream(stream);
+  if (w_dtype == TALM_F32)
+    launch_parts<float, false>(partials, parts, resid, nullptr, nullptr, weight, n_rows,
+                               static_cast<int>(n_cols), eps, sum_out, h, xhat, rstd, s);
+  else
+    launch_parts<uint16_t, false>(partials, parts, resid, nullptr, nullptr, weight, n_rows,
+                                  static_cast<int>(n_cols), eps, sum_out, h, xhat, rstd, s);
+  return check_launch("splitk_add_rmsnorm");
+}
+
+TALM_API int talm_splitk_rmsnorm_bwd(const float* partials, int32_t parts, const uint16_t* xhat,
+                                     const float* rstd, const void* weight, int32_t w_dtype,
+                                     const float* ds, int64_t n_rows, int64_t n_cols, float* dx,
+                                     uint16_t* dbranch, void* stream) {
+  if (check_parts("splitk_rmsnorm_bwd", partials, parts, n_rows, n_cols, w_dtype, weight))
+    return TALM_EINVAL;
+  if (n_rows == 0) return ok();
+  if (!xhat || !rstd || !dx || !dbranch)
+    return fail(TALM_EINVAL, "splitk_rmsnorm_bwd: null pointer");
+  if (!aligned(xhat, 16) || !aligned(dx, 16) || !aligned(dbranch, 16) || !aligned(ds, 16))
+    return fail(TALM_EINVAL, "splitk_rmsnorm_bwd: row operands must be 16-byte aligned");
+  const hipStream_t s = as_stream(stream);
+  if (w_dtype == TALM_F32)
+    launch_parts<float, true>(partials, parts, nullptr, ds, xhat, weight, n_rows,
+                              static_cast<int>(n_cols), 0.f, dx, dbranch, nullptr,
+                              const_cast<float*>(rstd), s);
+  else
+    launch_parts<uint16_t, true>(partials, parts, nullptr, ds, xhat, weight, n_rows,
+                                 static_cast<int>(n_cols), 0.f, dx, dbranch, nullptr,
+                                 const_cast<float*>(rstd), s);
+  return check_launch("splitk_rmsnorm_bwd");
+}

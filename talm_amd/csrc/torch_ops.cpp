@@ -725,6 +725,105 @@ void nf4_gemm(const Tensor& x, const Tensor& packed, const Tensor& scale, int64_
         "nf4_gemm");
 }
 
+// The MLP's long products leaving their fp32 K-part partials for the fused norm launches
+// below: partials float32 [parts, m, n] (parts from talm_gemm_splitk_parts / talm_nf4_gemm_parts).
+void gemm_splitk_partials(const Tensor& a, const Tensor& b, const Tensor& partials) {
+  require_fp16(a, "a");
+  require_fp16(b, "b");
+  require(a.dim() == 2 && b.dim() == 2 && a.stride(1) == 1 && b.stride(1) == 1,
+          "gemm_splitk_partials: a [m, k], b [n, k] with unit column stride");
+  const int64_t m = a.size(0), k = a.size(1), n = b.size(0);
+  require(b.size(1) == k, "gemm_splitk_partials: a [m, k], b [n, k]");
+  require(partials.is_cuda() && partials.scalar_type() == at::kFloat &&
+              partials.is_contiguous() && partials.device() == a.device() &&
+              partials.numel() == talm_gemm_splitk_parts(m, n, k) * m * n,
+          "gemm_splitk_partials: partials float32 [parts, m, n]");
+  check(talm_gemm_splitk_partials(as<uint16_t>(a), a.stride(0), as<uint16_t>(b), b.stride(0), m,
+                                  n, k, as<float>(partials), partials.numel() * 4, stream_of(a)),
+        "gemm_splitk_partials");
+}
+
+void nf4_gemm_partials(const Tensor& x, const Tensor& packed, const Tensor& scale, int64_t rows,
+                       int64_t cols, bool transpose, int64_t blocksize, const Tensor& partials) {
+  require_fp16(x, "x");
+  const int64_t k = transpose ? rows : cols, n_out = transpose ? cols : rows;
+  require(x.dim() == 2 && x.stride(1) == 1 && x.size(1) == k,
+          "nf4_gemm_partials: x [N, K] with unit column stride");
+  const int64_t n = x.size(0);
+  for (const Tensor* t : {&packed, &scale})
+    require(t->is_cuda() && t->is_contiguous() && t->device() == x.device(),
+            "nf4_gemm_partials: packed and scale contiguous on x's device");
+  require(packed.scalar_type() == at::kByte && scale.scalar_type() == at::kFloat,
+          "nf4_gemm_partials: packed uint8, scale float32");
+  require(blocksize > 0 && packed.numel() >= rows * cols / 2 &&
+              scale.numel() >= rows * cols / blocksize,
+          "nf4_gemm_partials: packed / scale do not cover [rows, cols]");
+  require(partials.is_cuda() && partials.scalar_type() == at::kFloat &&
+              partials.is_contiguous() && partials.device() == x.device() &&
+              partials.numel() == talm_nf4_gemm_parts(n, rows, cols, transpose ? 1 : 0) * n * n_out,
+          "nf4_gemm_partials: partials float32 [parts, N, n_out]");
+  check(talm_nf4_gemm_partials(as<uint16_t>(x), x.stride(0), n, as<uint8_t>(packed),
+                               as<float>(scale), rows, cols, transpose ? 1 : 0,
+                               static_cast<int32_t>(blocksize), as<float>(partials),
+                               partials.numel() * 4, stream_of(x)),
+        "nf4_gemm_partials");
+}
+
+// partials float32 [parts, N, H]; resid, sum_out float32 [N, H]; h, xhat fp16 [N, H]; rstd [N].
+void splitk_add_rmsnorm(const Tensor& partials, const Tensor& resid, const Tensor& weight,
+                        double eps, const Tensor& sum_out, const Tensor& h, const Tensor& xhat,
+                        const Tensor& rstd) {
+  require(partials.is_cuda() && partials.scalar_type() == at::kFloat && partials.dim() == 3 &&
+              partials.is_contiguous(),
+          "splitk_add_rmsnorm: partials float32 [parts, N, H]");
+  const int64_t n = partials.size(1), hd = partials.size(2);
+  for (const Tensor* t : {&resid, &sum_out})
+    require(t->is_cuda() && t->scalar_type() == at::kFloat && t->is_contiguous() &&
+                same_shape(*t, n, hd),
+            "splitk_add_rmsnorm: resid and sum_out float32 [N, H]");
+  for (const Tensor* t : {&h, &xhat})
+    require(t->is_cuda() && t->scalar_type() == at::kHalf && t->is_contiguous() &&
+                same_shape(*t, n, hd),
+            "splitk_add_rmsnorm: h and xhat float16 [N, H]");
+  require(weight.is_contiguous() && weight.numel() == hd, "splitk_add_rmsnorm: weight [H]");
+  require(rstd.scalar_type() == at::kFloat && rstd.is_contiguous() && rstd.numel() == n,
+          "splitk_add_rmsnorm: rstd float32 [N]");
+  check(talm_splitk_add_rmsnorm(as<float>(partials), static_cast<int32_t>(partials.size(0)),
+                                as<float>(resid), weight.data_ptr(),
+                                dtype_code(weight.scalar_type()), static_cast<float>(eps), n, hd,
+                                as<float>(sum_out), as<uint16_t>(h), as<uint16_t>(xhat),
+                                as<float>(rstd), stream_of(resid)),
+        "splitk_add_rmsnorm");
+}
+
+// partials float32 [parts, N, H] (dy); xhat fp16 [N, H]; rstd [N]; ds float32 [N, H] or None;
+// dx float32, dbranch fp16 [N, H].
+void splitk_rmsnorm_bwd(const Tensor& partials, const Tensor& xhat, const Tensor& rstd,
+                        const Tensor& weight, const OptTensor& ds, const Tensor& dx,
+                        const Tensor& dbranch) {
+  require(partials.is_cuda() && partials.scalar_type() == at::kFloat && partials.dim() == 3 &&
+              partials.is_contiguous(),
+          "splitk_rmsnorm_bwd: partials float32 [parts, N, H]");
+  const int64_t n = partials.size(1), hd = partials.size(2);
+  require(dx.is_cuda() && dx.scalar_type() == at::kFloat && dx.is_contiguous() &&
+              same_shape(dx, n, hd) &&
+              (!ds.has_value() || (ds->is_cuda() && ds->scalar_type() == at::kFloat &&
+                                   ds->is_contiguous() && same_shape(*ds, n, hd))),
+          "splitk_rmsnorm_bwd: dx (and ds) float32 [N, H]");
+  for (const Tensor* t : {&xhat, &dbranch})
+    require(t->is_cuda() && t->scalar_type() == at::kHalf && t->is_contiguous() &&
+                same_shape(*t, n, hd),
+            "splitk_rmsnorm_bwd: xhat and dbranch float16 [N, H]");
+  require(weight.is_contiguous() && weight.numel() == hd, "splitk_rmsnorm_bwd: weight [H]");
+  require(rstd.scalar_type() == at::kFloat && rstd.is_contiguous() && rstd.numel() == n,
+          "splitk_rmsnorm_bwd: rstd float32 [N]");
+  check(talm_splitk_rmsnorm_bwd(as<float>(partials), static_cast<int32_t>(partials.size(0)),
+                                as<uint16_t>(xhat), as<float>(rstd), weight.data_ptr(),
+                                dtype_code(weight.scalar_type()), as<float>(ds), n, hd,
+                                as<float>(dx), as<uint16_t>(dbranch), stream_of(dx)),
+        "splitk_rmsnorm_bwd");
+}
+
 // ------------------------------------------------------------------------------------------
 // Plain fp16 GEMMs on hipBLASLt with cached plans.
 // ------------------------------------------------------------------------------------------
@@ -1266,6 +1365,13 @@ TORCH_LIBRARY(talm, m) {
   m.def("scatter_rows(Tensor token_loss, Tensor entropy, Tensor correct, Tensor targets, "
         "Tensor src, Tensor(a!) full_loss, Tensor(b!) full_entropy, Tensor(c!) stats) -> ()");
   m.def("scale_rows(Tensor g, Tensor grad_loss, Tensor denom, Tensor(a!) out) -> ()");
+  m.def("gemm_splitk_partials(Tensor a, Tensor b, Tensor(a!) partials) -> ()");
+  m.def("nf4_gemm_partials(Tensor x, Tensor packed, Tensor scale, int rows, int cols, "
+        "bool transpose, int blocksize, Tensor(a!) partials) -> ()");
+  m.def("splitk_add_rmsnorm(Tensor partials, Tensor resid, Tensor weight, float eps, "
+        "Tensor(a!) sum_out, Tensor(b!) h, Tensor(c!) xhat, Tensor(d!) rstd) -> ()");
+  m.def("splitk_rmsnorm_bwd(Tensor partials, Tensor xhat, Tensor rstd, Tensor weight, "
+        "Tensor? ds, Tensor(a!) dx, Tensor(b!) dbranch) -> ()");
   m.def("gemm_algo_table(Tensor rows) -> ()", &gemm_algo_table);
   m.def("gemm_lib_version() -> int", &gemm_lib_version);
   m.def("gemm_tune(Tensor a, int trans_a, Tensor b, int trans_b, Tensor(a!) d, int m, int n, "
@@ -1313,4 +1419,8 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("head_loss", &head_loss);
   m.impl("scatter_rows", &scatter_rows);
   m.impl("scale_rows", &scale_rows);
+  m.impl("gemm_splitk_partials", &gemm_splitk_partials);
+  m.impl("nf4_gemm_partials", &nf4_gemm_partials);
+  m.impl("splitk_add_rmsnorm", &splitk_add_rmsnorm);
+  m.impl("splitk_rmsnorm_bwd", &splitk_rmsnorm_bwd);
 }

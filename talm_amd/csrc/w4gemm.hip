@@ -55,8 +55,9 @@ struct W4Args {
   const float* scale;      // [rows * w_cols / 64]: each 64-weight block's decoded absmax
   uint16_t* out;           // [M][ldo] when parts == 1
   int64_t ldo;
-  float* part;             // [parts][M][N] when parts > 1
+  float* part;             // [parts][M][N] when parts > 1 or partial_out
   int steps_per_part, n_mtiles, n_ntiles, n_tiles, parts;
+  int partial_out;         // fp32 partials even for one part (the caller sums them)
 };
 
 // The "nn" B tile: [64 k rows][256 columns] fp16, 32 chunks of 16 bytes per row, chunk c of row r
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(W4Shape::kThreads, 1) void w4_gemm_kernel(W4Args a)
   }
   __syncthreads();  // every wavefront is done with the ring (and every load has landed)
 
-  if (a.parts > 1) {
+  if (a.parts > 1 || a.partial_out) {
     float* P = a.part + static_cast<int64_t>(kp) * a.M * a.N;
 #pragma unroll
     for (int i = 0; i < S::kFragM; ++i)
@@ -286,33 +287,38 @@ TALM_API int64_t talm_nf4_gemm_workspace(int64_t n_tokens, int64_t rows, int64_t
   return p.parts > 1 ? static_cast<int64_t>(p.parts) * n_tokens * n * 4 : 0;
 }
 
-TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_t* packed,
-                           const float* scale, int64_t rows, int64_t cols, int32_t transpose,
-                           int32_t blocksize, uint16_t* out, int64_t ldo, void* workspace,
-                           int64_t workspace_bytes, void* stream) {
+namespace talm {
+namespace {
+
+// out == nullptr: fp32 partials [parts][n_tokens][n] in the workspace (also for one part), left
+// for the caller's next launch to sum.
+int nf4_gemm_impl(const char* what, const uint16_t* x, int64_t ldx, int64_t n_tokens,
+                  const uint8_t* packed, const float* scale, int64_t rows, int64_t cols,
+                  int32_t transpose, int32_t blocksize, uint16_t* out, int64_t ldo,
+                  void* workspace, int64_t workspace_bytes, hipStream_t s) {
   using S = W4Shape;
   const bool nn = transpose != 0;
   if (blocksize != 64)
-    return fail(TALM_EINVAL, "nf4_gemm: blocksize %d (64 supported)", blocksize);
+    return fail(TALM_EINVAL, "%s: blocksize %d (64 supported)", what, blocksize);
   const int64_t n = nn ? cols : rows, k = nn ? rows : cols;
-  if (!w4_shape_ok(nn, n_tokens, rows, cols) || ldx < k || ldx % 8 || ldo < n || ldo % 8 ||
-      !(S::kBM * ldx * 2 < (int64_t{1} << 31)))
+  if (!w4_shape_ok(nn, n_tokens, rows, cols) || ldx < k || ldx % 8 ||
+      (out && (ldo < n || ldo % 8)) || !(S::kBM * ldx * 2 < (int64_t{1} << 31)))
     return fail(TALM_EINVAL,
-                "nf4_gemm: bad shape (tokens %lld, W [%lld, %lld], %s, ldx %lld, ldo %lld): W's "
+                "%s: bad shape (tokens %lld, W [%lld, %lld], %s, ldx %lld, ldo %lld): W's "
                 "row length a multiple of 64, its rows a multiple of %d, whole 16384-weight "
                 "groups, strides multiples of 8 covering the rows",
-                (long long)n_tokens, (long long)rows, (long long)cols, nn ? "dy W" : "x W^T",
-                (long long)ldx, (long long)ldo, nn ? 64 : 8);
+                what, (long long)n_tokens, (long long)rows, (long long)cols,
+                nn ? "dy W" : "x W^T", (long long)ldx, (long long)ldo, nn ? 64 : 8);
   if (n_tokens == 0) return ok();
-  if (!x || !packed || !scale || !out) return fail(TALM_EINVAL, "nf4_gemm: null pointer");
+  if (!x || !packed || !scale) return fail(TALM_EINVAL, "%s: null pointer", what);
   if (!aligned(x, 16) || !aligned(packed, 16) || !aligned(out, 16) || !aligned(scale, 4))
-    return fail(TALM_EINVAL, "nf4_gemm: x, packed and out must be 16-byte aligned, scale 4-byte");
+    return fail(TALM_EINVAL, "%s: x, packed and out must be 16-byte aligned, scale 4-byte", what);
   const SplitPlan p = w4_plan(n_tokens, n, k);
-  if (p.parts > 1) {
+  if (p.parts > 1 || !out) {
     const int64_t need = static_cast<int64_t>(p.parts) * n_tokens * n * 4;
     if (!workspace || workspace_bytes < need || !aligned(workspace, 16))
-      return fail(TALM_EINVAL, "nf4_gemm: workspace of %lld bytes, %lld needed (16-byte aligned)",
-                  (long long)workspace_bytes, (long long)need);
+      return fail(TALM_EINVAL, "%s: workspace of %lld bytes, %lld needed (16-byte aligned)",
+                  what, (long long)workspace_bytes, (long long)need);
   }
   W4Args a{};
   a.a = x; a.lda = ldx;
@@ -324,14 +330,42 @@ TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, con
   a.steps_per_part = p.steps_per_part;
   a.n_mtiles = p.n_mtiles; a.n_ntiles = p.n_ntiles; a.parts = p.parts;
   a.n_tiles = p.n_mtiles * p.n_ntiles * p.parts;
-  const hipStream_t s = as_stream(stream);
+  a.partial_out = out ? 0 : 1;
   if (nn)
     hipLaunchKernelGGL(w4_gemm_kernel<true>, dim3(static_cast<unsigned>(a.n_tiles)),
                        dim3(S::kThreads), 0, s, a);
   else
     hipLaunchKernelGGL(w4_gemm_kernel<false>, dim3(static_cast<unsigned>(a.n_tiles)),
                        dim3(S::kThreads), 0, s, a);
-  if (p.parts > 1)
+  if (out && p.parts > 1)
     launch_splitk_reduce(static_cast<const float*>(workspace), p.parts, n_tokens, n, out, ldo, s);
-  return check_launch("nf4_gemm");
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace talm
+
+TALM_API int talm_nf4_gemm(const uint16_t* x, int64_t ldx, int64_t n_tokens, const uint8_t* packed,
+                           const float* scale, int64_t rows, int64_t cols, int32_t transpose,
+                           int32_t blocksize, uint16_t* out, int64_t ldo, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  if (!out && n_tokens > 0) return fail(TALM_EINVAL, "nf4_gemm: null pointer");
+  return nf4_gemm_impl("nf4_gemm", x, ldx, n_tokens, packed, scale, rows, cols, transpose,
+                       blocksize, out, ldo, workspace, workspace_bytes, as_stream(stream));
+}
+
+TALM_API int64_t talm_nf4_gemm_parts(int64_t n_tokens, int64_t rows, int64_t cols,
+                                     int32_t transpose) {
+  const bool nn = transpose != 0;
+  if (!w4_shape_ok(nn, n_tokens, rows, cols)) return -1;
+  return w4_plan(n_tokens, nn ? cols : rows, nn ? rows : cols).parts;
+}
+
+TALM_API int talm_nf4_gemm_partials(const uint16_t* x, int64_t ldx, int64_t n_tokens,
+                                    const uint8_t* packed, const float* scale, int64_t rows,
+                                    int64_t cols, int32_t transpose, int32_t blocksize,
+                                    float* partials, int64_t partials_bytes, void* stream) {
+  return nf4_gemm_impl("nf4_gemm_partials", x, ldx, n_tokens, packed, scale, rows, cols,
+                       transpose, blocksize, nullptr, 0, partials, partials_bytes,
+                       as_stream(stream));
 }

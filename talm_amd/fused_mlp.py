@@ -133,31 +133,39 @@ class FusedMLP(torch.autograd.Function):
             torch.ops.talm.swiglu_bwd_rows(dact, gate, up, gate, up)
         del dact
         dx = torch.empty(n_tok, hidden, dtype=torch.float16, device=dy.device)
-        if (GATE, UP) in group.w4_blocks():
-            # dx = [dgate | dup] [W_gate; W_up] with the weights read as NF4 codes (the
-            # transposed buffer leaves them out)
-            try:
-                group.nf4_gemm(gu, GATE, DOWN, True, dx)
-                RAN["w4a16"] += 1
-                return dx.view(ctx.x_shape), None, None
-            except Exception as exc:  # noqa: BLE001 - state.py convention
-                if not fallback("w4a16", exc):
-                    raise
-        w_gu_t = group.span_t(GATE, DOWN)
-        w_gu = None if w_gu_t is not None else group.span(GATE, DOWN)
-        if w_gu_t is not None:
-            # dx = [dgate | dup] [W_gate; W_up] = gu ([W_gate; W_up]^T)^T: one GEMM
-            _linear(gu, w_gu_t, dx)
-        elif w_gu is not None:
-            # dx = [dgate | dup] [W_gate; W_up]: one GEMM with the reduction over both halves
-            torch.ops.talm.gemm(gu, w_gu, None, 0, dx)
-        else:  # "qgroup" is off: the projections' own weights
-            w_gate, w_up = group.weight(GATE), group.weight(UP)
-            torch.ops.talm.gemm(gate, w_gate, None, 0, dx)
-            # dx += dup W_up in the column-major BLAS form: dx^T [H x N] += W_up^T [H x I] dup^T
-            torch.ops.talm.gemm_ex(w_up, 0, up, 0, dx, hidden, n_tok, inter, hidden, 2 * inter,
-                                   hidden, 1)
+        input_grad(group, gu, dx)
         return dx.view(ctx.x_shape), None, None
+
+
+def input_grad(group, gu, dx):
+    """dx = [dgate | dup] [W_gate; W_up] (fp16 [N, H]) from gu holding dgate | dup: on the NF4
+    codes while the layer group serves gate|up that way (the transposed buffer leaves them out),
+    else one GEMM on the transposed or the row-major weight, else ("qgroup" off) the
+    projections' own weights."""
+    n_tok, hidden, inter = gu.shape[0], dx.shape[1], gu.shape[1] // 2
+    if (GATE, UP) in group.w4_blocks():
+        try:
+            group.nf4_gemm(gu, GATE, DOWN, True, dx)
+            RAN["w4a16"] += 1
+            return
+        except Exception as exc:  # noqa: BLE001 - state.py convention
+            if not fallback("w4a16", exc):
+                raise
+    w_gu_t = group.span_t(GATE, DOWN)
+    w_gu = None if w_gu_t is not None else group.span(GATE, DOWN)
+    if w_gu_t is not None:
+        # dx = [dgate | dup] [W_gate; W_up] = gu ([W_gate; W_up]^T)^T: one GEMM
+        _linear(gu, w_gu_t, dx)
+    elif w_gu is not None:
+        # dx = [dgate | dup] [W_gate; W_up]: one GEMM with the reduction over both halves
+        torch.ops.talm.gemm(gu, w_gu, None, 0, dx)
+    else:  # "qgroup" is off: the projections' own weights
+        gate, up = gu[:, :inter], gu[:, inter:]
+        w_gate, w_up = group.weight(GATE), group.weight(UP)
+        torch.ops.talm.gemm(gate, w_gate, None, 0, dx)
+        # dx += dup W_up in the column-major BLAS form: dx^T [H x N] += W_up^T [H x I] dup^T
+        torch.ops.talm.gemm_ex(w_up, 0, up, 0, dx, hidden, n_tok, inter, hidden, 2 * inter,
+                               hidden, 1)
 
 
 def _recompute_gate(group, x2, gate):

@@ -289,18 +289,29 @@ class LayerGroup:
             self._scales = scales
         return self._scales
 
-    def nf4_gemm(self, x, first, last, transpose, out):
+    def nf4_gemm(self, x, first, last, transpose, out, partials=None):
         """out = x W^T (transpose False: the forward) or x W (True: the input gradient) with W the
         [sum of out, in] rows of projections first .. last - 1 read as NF4 codes and dequantized
-        inside the GEMM (the same fp16 weights as `span`)."""
+        inside the GEMM (the same fp16 weights as `span`). With `partials` (fp32 [parts, N, n],
+        `nf4_gemm_parts`) the product's K-part partials are left there instead (out unused)."""
         segs = self.segments[first:last]
         rows, cols = sum(seg.shape[0] for seg in segs), segs[0].shape[1]
         lo = segs[0].start
         scales = self.block_scales()
+        if partials is not None:
+            torch.ops.talm.nf4_gemm_partials(x, self.packed[lo // 2:], scales[lo // self.qblock:],
+                                             rows, cols, transpose, self.qblock, partials)
+            return
         ws = torch.empty(_ops.nf4_gemm_workspace_bytes(x.shape[0], rows, cols, transpose),
                          dtype=torch.uint8, device=x.device)
         torch.ops.talm.nf4_gemm(x, self.packed[lo // 2:], scales[lo // self.qblock:], rows, cols,
                                 transpose, self.qblock, out, ws)
+
+    def nf4_gemm_parts(self, n_tokens, first, last, transpose):
+        """The K-part count of `nf4_gemm`'s plan for n_tokens rows of x."""
+        segs = self.segments[first:last]
+        rows, cols = sum(seg.shape[0] for seg in segs), segs[0].shape[1]
+        return _ops.nf4_gemm_parts(n_tokens, rows, cols, transpose)
 
     def dequantize_one(self, idx):
         return self.dequantize(idx, idx + 1).view(self.segments[idx].shape)

@@ -261,6 +261,17 @@ def _layer_forward(layer, x, attn_kwargs):
     # stage 1: input norm (handed over by the previous layer when it could), attention, and the
     # attention's residual add with the post-attention norm in one launch
     h, _ = layer.self_attn(hidden_states=layer.input_layernorm(x), **attn_kwargs)
+    link = layer.__dict__.get("_talm_next_norm")
+    follower = None if link is None else link()
+    if follower is not None:
+        # stages 1 (the add and norm) to 3 as one node (mlp_block.py) when it applies
+        from .mlp_block import mlp_block
+
+        block = mlp_block(layer, x, h, follower)
+        if block is not None:
+            total, normed_next = block
+            setattr(total, _HANDOVER, (follower, normed_next))
+            return total
     fused = _sum_and_norm(x, h, layer.post_attention_layernorm)
     if fused is None:
         FELL_BACK["addnorm"] += 1
@@ -271,8 +282,6 @@ def _layer_forward(layer, x, attn_kwargs):
     # stage 2: the MLP
     h = layer.mlp(normed)
     # stage 3: the MLP's residual add, with the next norm when there is one to hand over to
-    link = layer.__dict__.get("_talm_next_norm")
-    follower = None if link is None else link()
     fused = None if follower is None else _sum_and_norm(stream, h, follower)
     if fused is None:
         FELL_BACK["addnorm"] += 1

@@ -158,3 +158,28 @@ def test_row_stride_and_rejects_bad_shapes():
     with pytest.raises(ValueError):  # the gate|up input gradient splits K: no workspace given
         torch.ops.talm.nf4_gemm(dy, parts["packed"], parts["scale"], rows, cols, True, 64, dx, ws)
 
+
+
+@pytest.mark.parametrize("name,first,count,transpose,n_tok", [
+    ("gate|up dy W", 4, 2, True, 1312),   # the MLP block's backward form (7 parts)
+    ("down x W^T", 6, 1, False, 1312),
+    ("o x W^T", 3, 1, False, 300),        # one part: partials written all the same
+])
+def test_partials_sum_to_the_product(name, first, count, transpose, n_tok):
+    """talm_nf4_gemm_partials: its fp32 partials, summed in part order and rounded, are the
+    product talm_nf4_gemm writes, bit for bit."""
+    print(f"[case] nf4_gemm_partials {name} tokens={n_tok}", flush=True)
+    d, dev, w16 = _layer()
+    parts, _w, rows, cols = _slice(d, dev, w16, first, count)
+    k = rows if transpose else cols
+    x = (torch.randn(n_tok, k, generator=torch.Generator().manual_seed(n_tok)) * 0.5).half().cuda()
+    want = _gemm(x, parts, rows, cols, transpose)
+    n_parts = _ops.nf4_gemm_parts(n_tok, rows, cols, transpose)
+    part = torch.full((n_parts, n_tok, cols if transpose else rows), float("nan"),
+                      device="cuda")
+    torch.ops.talm.nf4_gemm_partials(x, parts["packed"], parts["scale"], rows, cols, transpose,
+                                     64, part)
+    total = part[0].clone()
+    for p in range(1, n_parts):
+        total += part[p]
+    assert torch.equal(total.half().view(torch.int16), want.view(torch.int16))
