@@ -175,6 +175,17 @@ int talm_rope(const uint16_t* q, const uint16_t* k, const float* cos, const floa
               int64_t cs_stride_tok, int32_t backward, void* stream);
 
 /*
+ * The rotary tables of transformers' rotary embedding (Qwen2RotaryEmbedding.forward, default
+ * and statically scaled types): for token t and j < half, angle = fl32(inv_freq[j] *
+ * fl32(positions[t])), cos[t][j] = cos[t][j + half] = fl32(cosf(angle) * scaling), sin likewise;
+ * positions int64 [n_tokens], cos / sin f32 [n_tokens, 2 half] row-major. One launch instead of
+ * the position cast, the K = 1 product, the concatenation and the four elementwise ops; the
+ * tables feed the rotation the reference fuses (solution/rope.py:64-134).
+ */
+int talm_rope_table(const int64_t* positions, int64_t n_tokens, const float* inv_freq,
+                    int32_t half, float scaling, float* cos, float* sin, void* stream);
+
+/*
  * SwiGLU forward: out = silu(gate) * up in fp32, written as fp16. n elements, contiguous.
  * Replaces example_swiglu_fwd_kernel (solution/swiglu.py:23-30); `out` may alias `gate`
  * (the save-up node, solution/mlp_save_up.py:63).

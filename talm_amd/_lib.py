@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -58,6 +58,7 @@ SIGNATURES = {
                            _I64, _I64, _P, _P, _I32, _I32, _I64, _I32, _I32, _I32, _F32, _P, _P,
                            _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
     "talm_lora_mirror": [_P, _I32, _I64, _P, _P],
+    "talm_rope_table": [_P, _I64, _P, _I32, _F32, _P, _P, _P],
     "talm_pack_rows": [_P, _P, _P, _I32, _I32, _I64, _P, _P, _P, _P, _P, _P],
     "talm_row_stats": [_P, _P, _I32, _I32, _P, _P],
     "talm_head_loss": [_P, _P, _P, _I64, _P, _F32, _I32, _P, _P, _P, _P],

@@ -25,7 +25,8 @@ OPS = ("nf4_group_dequant", "nf4_group_dequant_streaming", "nf4_dequant", "rmsno
        "lora_wgrad", "gemm", "gemm_ex", "attn_fwd", "attn_bwd", "attn_bwd_rope", "lora_mirror",
        "lora_adamw", "nf4_gemm", "nf4_block_scales", "nf4_group_dequant_t", "gemm_splitk",
        "pack_rows", "row_stats", "head_loss", "scatter_rows", "scale_rows",
-       "gemm_splitk_partials", "nf4_gemm_partials", "splitk_add_rmsnorm", "splitk_rmsnorm_bwd")
+       "gemm_splitk_partials", "nf4_gemm_partials", "splitk_add_rmsnorm", "splitk_rmsnorm_bwd",
+       "rope_table")
 
 _load_lock = threading.Lock()
 _loaded = False

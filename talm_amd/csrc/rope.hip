@@ -99,10 +99,45 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(const uint16_t* q, const
   }
 }
 
+// The rotary tables themselves, as transformers' rotary embedding computes them for the default
+// (and statically scaled) types: angle = inv_freq[j] * float(position) in fp32 (its K = 1
+// product), cos / sin of it (the same libm calls) times the attention scaling, written to
+// columns j and j + half of the token's row. One thread per (token, j).
+__global__ __launch_bounds__(kThreads) void rope_table_kernel(
+    const int64_t* __restrict__ pos, int64_t n, const float* __restrict__ inv_freq, int half,
+    float scaling, float* __restrict__ cos_out, float* __restrict__ sin_out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n * half) return;
+  const int64_t t = i / half;
+  const int j = static_cast<int>(i - t * half);
+  const float angle = mul_f32(inv_freq[j], static_cast<float>(pos[t]));
+  const float c = mul_f32(cosf(angle), scaling), sn = mul_f32(sinf(angle), scaling);
+  float* crow = cos_out + t * 2 * half;
+  float* srow = sin_out + t * 2 * half;
+  crow[j] = c;
+  crow[j + half] = c;
+  srow[j] = sn;
+  srow[j + half] = sn;
+}
+
 }  // namespace
 }  // namespace talm
 
 using namespace talm;
+
+TALM_API int talm_rope_table(const int64_t* positions, int64_t n_tokens, const float* inv_freq,
+                             int32_t half, float scaling, float* cos, float* sin, void* stream) {
+  if (n_tokens < 0 || half < 1 || half > 4096 || n_tokens * half >= (int64_t{1} << 40))
+    return fail(TALM_EINVAL, "rope_table: bad shape tokens=%lld half=%d", (long long)n_tokens,
+                half);
+  if (n_tokens == 0) return ok();
+  if (!positions || !inv_freq || !cos || !sin) return fail(TALM_EINVAL, "rope_table: null pointer");
+  const int64_t blocks = (n_tokens * half + kThreads - 1) / kThreads;
+  if (blocks > 0x7fffffff) return fail(TALM_EINVAL, "rope_table: too many tokens");
+  hipLaunchKernelGGL(rope_table_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                     as_stream(stream), positions, n_tokens, inv_freq, half, scaling, cos, sin);
+  return check_launch("rope_table");
+}
 
 TALM_API int talm_rope(const uint16_t* q, const uint16_t* k, const float* cos, const float* sin,
                        uint16_t* out_q, uint16_t* out_k, int64_t n_tokens, int32_t n_q_heads,

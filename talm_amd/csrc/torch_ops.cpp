@@ -1181,6 +1181,26 @@ Tensor gemm_tune(const Tensor& a, int64_t trans_a, const Tensor& b, int64_t tran
   return result;
 }
 
+// positions int64 [N] (contiguous), inv_freq float32 [half] -> cos, sin float32 [N, 2 half].
+void rope_table(const Tensor& positions, const Tensor& inv_freq, double scaling,
+                const Tensor& cos, const Tensor& sin) {
+  require(positions.is_cuda() && positions.scalar_type() == at::kLong &&
+              positions.is_contiguous(),
+          "rope_table: positions contiguous CUDA int64");
+  require(inv_freq.is_cuda() && inv_freq.scalar_type() == at::kFloat && inv_freq.is_contiguous() &&
+              inv_freq.dim() == 1,
+          "rope_table: inv_freq float32 [half]");
+  const int64_t n = positions.numel(), half = inv_freq.numel();
+  for (const Tensor* t : {&cos, &sin})
+    require(t->is_cuda() && t->scalar_type() == at::kFloat && t->is_contiguous() &&
+                t->numel() == n * 2 * half,
+            "rope_table: cos, sin float32 [N, 2 half]");
+  check(talm_rope_table(as<int64_t>(positions), n, as<float>(inv_freq),
+                        static_cast<int32_t>(half), static_cast<float>(scaling), as<float>(cos),
+                        as<float>(sin), stream_of(cos)),
+        "rope_table");
+}
+
 // ------------------------------------------------------------------------------------------
 // The packed causal-LM step's per-step glue: batch packing, row statistics, the head's loss and
 // metrics, the head backward's scaling (csrc/pack.hip).
@@ -1365,6 +1385,8 @@ TORCH_LIBRARY(talm, m) {
   m.def("scatter_rows(Tensor token_loss, Tensor entropy, Tensor correct, Tensor targets, "
         "Tensor src, Tensor(a!) full_loss, Tensor(b!) full_entropy, Tensor(c!) stats) -> ()");
   m.def("scale_rows(Tensor g, Tensor grad_loss, Tensor denom, Tensor(a!) out) -> ()");
+  m.def("rope_table(Tensor positions, Tensor inv_freq, float scaling, Tensor(a!) cos, "
+        "Tensor(b!) sin) -> ()");
   m.def("gemm_splitk_partials(Tensor a, Tensor b, Tensor(a!) partials) -> ()");
   m.def("nf4_gemm_partials(Tensor x, Tensor packed, Tensor scale, int rows, int cols, "
         "bool transpose, int blocksize, Tensor(a!) partials) -> ()");
@@ -1419,6 +1441,7 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("head_loss", &head_loss);
   m.impl("scatter_rows", &scatter_rows);
   m.impl("scale_rows", &scale_rows);
+  m.impl("rope_table", &rope_table);
   m.impl("gemm_splitk_partials", &gemm_splitk_partials);
   m.impl("nf4_gemm_partials", &nf4_gemm_partials);
   m.impl("splitk_add_rmsnorm", &splitk_add_rmsnorm);

@@ -5,7 +5,7 @@ time, each installed once (`_in_chain`, :119-129) under `state.installing`, each
 the original code outside the exact situation it was written for. Installed here:
 
 - RMSNorm and the residual adds folded into the norms (rmsnorm.py);
-- RoPE (rope.py);
+- RoPE and its tables (rope.py);
 - SwiGLU with the in-place backward (swiglu.py, swiglu_inplace.py), or the save-up MLP
   (mlp_save_up.py, opt-in SOLUTION_MLP_SAVE_UP=1);
 - grouped NF4 dequantization of the 4-bit projections (qgroup.py), the LoRA node (lora.py) and
@@ -311,9 +311,10 @@ def apply():
                 patch_qwen2_add_norm()
     if not _off("ROPE"):
         with installing("rope"):
-            from .rope import patch_qwen2_rope
+            from .rope import patch_qwen2_rope, patch_qwen2_rotary_tables
 
             patch_qwen2_rope()
+            patch_qwen2_rotary_tables()
     if not _off("GROUP"):
         with installing("qgroup"):
             from .qgroup import patch_group_dequant
@@ -360,7 +361,8 @@ def unapply():
 
     for cls in (modeling_qwen2.Qwen2RMSNorm, modeling_qwen2.Qwen2DecoderLayer,
                 modeling_qwen2.Qwen2MLP, modeling_qwen2.Qwen2Attention,
-                modeling_qwen2.Qwen2ForCausalLM, Linear4bit, LoraLinear):
+                modeling_qwen2.Qwen2ForCausalLM, modeling_qwen2.Qwen2RotaryEmbedding,
+                Linear4bit, LoraLinear):
         cls.forward = _root(cls.forward)
     forward = modeling_qwen2.Qwen2Model.forward
     if getattr(forward, "_solution_link_norms", False):

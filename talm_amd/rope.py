@@ -127,3 +127,60 @@ def patch_qwen2_rope():
     apply_rotary_pos_emb._solution_rope = True
     apply_rotary_pos_emb._original = original
     modeling_qwen2.apply_rotary_pos_emb = apply_rotary_pos_emb
+
+
+def _table_applies(module, x, position_ids):
+    """transformers' rotary embedding of a default or statically scaled type (its inverse
+    frequencies fixed: no dynamic update) on fp32 inputs with int64 positions on one GPU."""
+    rope_type = getattr(module, "rope_type", "default")
+    inv_freq = getattr(module, "inv_freq", None)
+    return (isinstance(rope_type, str) and "dynamic" not in rope_type and rope_type != "longrope"
+            and torch.is_tensor(inv_freq) and inv_freq.is_cuda and inv_freq.dim() == 1
+            and inv_freq.dtype == torch.float32 and x.is_cuda and x.dtype == torch.float32
+            and torch.is_tensor(position_ids) and position_ids.dtype == torch.int64
+            and position_ids.dim() == 2 and position_ids.device == inv_freq.device
+            and x.device == inv_freq.device)
+
+
+def rope_tables(module, position_ids):
+    """(cos, sin) float32 [B, T, 2 half] of the rotary embedding in one launch
+    (talm_rope_table): the same products, libm calls and scaling as its forward."""
+    inv_freq = module.inv_freq.contiguous()
+    half = inv_freq.numel()
+    b, t = position_ids.shape
+    cos = torch.empty(b, t, 2 * half, dtype=torch.float32, device=inv_freq.device)
+    sin = torch.empty_like(cos)
+    torch.ops.talm.rope_table(position_ids.contiguous(), inv_freq,
+                              float(getattr(module, "attention_scaling", 1.0)), cos, sin)
+    return cos, sin
+
+
+def patch_qwen2_rotary_tables():
+    """`Qwen2RotaryEmbedding.forward` through `rope_tables` when `_table_applies`; the original
+    forward otherwise."""
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from .patches import _in_chain
+
+    cls = modeling_qwen2.Qwen2RotaryEmbedding
+    original = cls.forward
+    ON.add("rope_table")
+    if _in_chain(original, "_solution_rope_table"):
+        return
+
+    @torch.no_grad()
+    def forward(self, x, position_ids):
+        if "rope_table" not in DISABLED and _table_applies(self, x, position_ids):
+            try:
+                out = rope_tables(self, position_ids)
+                RAN["rope_table"] += 1
+                return out
+            except Exception as exc:  # noqa: BLE001 - state.py convention
+                if not fallback("rope_table", exc):
+                    raise
+        FELL_BACK["rope_table"] += 1
+        return original(self, x, position_ids)
+
+    forward._solution_rope_table = True
+    forward._original = original
+    cls.forward = forward

@@ -432,3 +432,28 @@ def test_swiglu_tails(n):
     swiglu.swiglu_fwd(big[1:], big[1:], o2)
     b = to_np(big[1:])
     assert_rel(o2, swiglu_oracle.forward(b, b, np.float64, np.float64), rtol=1e-3, what="view")
+
+
+@pytest.mark.parametrize("theta,layout", [(1e6, "packed"), (10000.0, "rows")])
+def test_rotary_tables_equal_transformers(theta, layout):
+    """talm_rope_table: cos / sin of transformers' Qwen2RotaryEmbedding.forward (default type)
+    for packed positions (rows restarting at 0, a pad sequence) and for padded rows, bit for bit
+    (the same fp32 products, the same libm cos / sin, the same scaling)."""
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from talm_amd import patches, qlora_model, rope
+
+    print(f"[case] rotary tables theta={theta} {layout}", flush=True)
+    config = qlora_model.qwen2_config(rope_theta=theta)
+    module = modeling_qwen2.Qwen2RotaryEmbedding(config).cuda()
+    if layout == "packed":
+        pos = torch.cat([torch.arange(n) for n in (300, 128, 512, 257, 16)])[None]
+    else:
+        pos = torch.arange(512).repeat(4, 1)
+    pos = pos.cuda()
+    x = torch.empty(1, dtype=torch.float32, device="cuda")
+    original = patches._root(modeling_qwen2.Qwen2RotaryEmbedding.forward)
+    want_cos, want_sin = original(module, x, pos)
+    got_cos, got_sin = rope.rope_tables(module, pos)
+    assert got_cos.shape == want_cos.shape and got_cos.dtype == want_cos.dtype
+    assert torch.equal(got_cos, want_cos) and torch.equal(got_sin, want_sin)
