@@ -455,6 +455,28 @@ int talm_lora_adamw(const int64_t* table, int32_t n_tensors, int64_t max_numel, 
                     uint16_t* out, void* stream);
 
 /*
+ * GradScaler.unscale_ + clip_grad_norm_ + the AdamW step without rewriting the gradients:
+ * talm_lora_grad_norm computes, over every gradient of the table (entry column 6), u =
+ * fl32(g * inv_scale) with inv_scale = fl32(1 / (double) *scale) (unscale_'s reciprocal) and
+ * writes stats f32 [4] = {found_inf (1 when any u or the norm is not finite), inv_scale,
+ * min(max_norm / (norm + 1e-6), 1) (NaN kept), norm = sqrt(sum of u^2)}: two launches, the
+ * workgroup sums added in a fixed order (talm_lora_grad_norm_workspace bytes of workspace).
+ * talm_lora_adamw_clipped is talm_lora_adamw with each gradient taken as fl32(fl32(g *
+ * grad_mul[0]) * grad_mul[1]) (pass stats + 1: the unscaled, then clipped value the two in-place
+ * ops would leave) and found_inf = stats. Replaces the unscale, norm and clip launches before the
+ * optimizer step (solution/lora.py:57-137's optimizer, under the trainer's GradScaler and
+ * gradient clipping).
+ */
+int64_t talm_lora_grad_norm_workspace(int32_t n_tensors, int64_t max_numel);
+int talm_lora_grad_norm(const int64_t* table, int32_t n_tensors, int64_t max_numel,
+                        const float* scale, float max_norm, void* workspace,
+                        int64_t workspace_bytes, float* stats, void* stream);
+int talm_lora_adamw_clipped(const int64_t* table, int32_t n_tensors, int64_t max_numel, float lr,
+                            float beta1, float beta2, float eps, float weight_decay,
+                            const float* step_in, float* step_out, const float* found_inf,
+                            const float* grad_mul, uint16_t* out, void* stream);
+
+/*
  * The decoded absmax of NF4 blocks: out[b] = fl32(fl32(code[absmax8[b]] * absmax2[b / qblock2])
  * + offset2[b / qblock2]) for b < n_blocks, the scale talm_nf4_group_dequant multiplies block b's
  * levels by (solution/qgroup.py:82-83, decoded once instead of per element; the frozen base

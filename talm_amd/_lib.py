@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -65,6 +65,9 @@ SIGNATURES = {
     "talm_scatter_rows": [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P],
     "talm_scale_rows": [_P, _I64, _P, _P, _P, _P],
     "talm_lora_adamw": [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _P, _P, _P, _P, _P, _P],
+    "talm_lora_grad_norm": [_P, _I32, _I64, _P, _F32, _P, _I64, _P, _P],
+    "talm_lora_adamw_clipped": [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _P, _P, _P, _P, _P,
+                                _P],
     "talm_nf4_gemm": [_P, _I64, _I64, _P, _P, _I64, _I64, _I32, _I32, _P, _I64, _P, _I64, _P],
     "talm_nf4_block_scales": [_P, _P, _P, _P, _I64, _I32, _P, _P],
     "talm_gemm_splitk": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
@@ -82,6 +85,7 @@ SIZE_FUNCTIONS = {
     "talm_gemm_splitk_workspace": [_I64, _I64, _I64],
     "talm_nf4_gemm_workspace": [_I64, _I64, _I64, _I32],
     "talm_gemm_splitk_parts": [_I64, _I64, _I64],
+    "talm_lora_grad_norm_workspace": [_I32, _I64],
     "talm_nf4_gemm_parts": [_I64, _I64, _I64, _I32],
 }
 

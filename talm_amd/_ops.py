@@ -26,7 +26,7 @@ OPS = ("nf4_group_dequant", "nf4_group_dequant_streaming", "nf4_dequant", "rmsno
        "lora_adamw", "nf4_gemm", "nf4_block_scales", "nf4_group_dequant_t", "gemm_splitk",
        "pack_rows", "row_stats", "head_loss", "scatter_rows", "scale_rows",
        "gemm_splitk_partials", "nf4_gemm_partials", "splitk_add_rmsnorm", "splitk_rmsnorm_bwd",
-       "rope_table")
+       "rope_table", "lora_grad_norm", "lora_adamw_clipped")
 
 _load_lock = threading.Lock()
 _loaded = False
@@ -106,3 +106,9 @@ def nf4_gemm_parts(n_tokens, rows, cols, transpose):
     if parts < 1:
         raise ValueError(f"nf4_gemm: unsupported shape tokens={n_tokens} W=[{rows}, {cols}]")
     return int(parts)
+
+
+def lora_grad_norm_workspace_bytes(n_tensors, max_numel):
+    size = _lib.lib().talm_lora_grad_norm_workspace(n_tensors, max_numel)
+    _require(size >= 0, "lora_grad_norm: unsupported table")
+    return int(size)

@@ -258,6 +258,36 @@ class AdapterAdamW(torch.optim.Optimizer):
         st["event"][i] = event
         return st["dev"][i]
 
+    def _group_launch_args(self, gi, group, params, buffer):
+        """(table, n, max_numel, step_in, step_out, buffer) of one group's launch: the device
+        table of its tensors (weight, sizes, copy offsets, gradient, moments) and the step
+        counters; the adapters' copy layout is built on first use."""
+        copies = self.copies
+        device = params[0].device
+        if copies.layout is None or not copies._alive():
+            copies._build_layout(device)
+        if buffer is None:
+            buffer = copies.reusable(device)
+        steps = self._state(group, params, device)
+        rows = []
+        for p, (h, t, ld) in zip(params, copies.entries(params)):
+            g = p.grad
+            if g.dtype != torch.float32 or not g.is_contiguous() or g.shape != p.shape:
+                raise ValueError("AdapterAdamW: gradients must be contiguous fp32")
+            st = self.state[p]
+            rows.append([p.data_ptr(), p.numel(), p.shape[1], h, t, ld, g.data_ptr(),
+                         st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr()])
+        table = self._table(gi, rows, device)
+        flip = group["_talm_flip"]
+        return (table, len(params), max(p.numel() for p in params), steps[flip:flip + 1],
+                steps[1 - flip:2 - flip], buffer)
+
+    def _after_group(self, group, params, step_out):
+        group["_talm_flip"] = 1 - group["_talm_flip"]
+        for p in params:
+            self.state[p]["step"] = step_out
+        RAN["adapter_adamw"] += 1
+
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
@@ -274,32 +304,61 @@ class AdapterAdamW(torch.optim.Optimizer):
             params = [p for p in group["params"] if p.grad is not None]
             if not params:
                 continue
-            device = params[0].device
-            if copies.layout is None or not copies._alive():
-                copies._build_layout(device)
-            if buffer is None:
-                buffer = copies.reusable(device)
-            steps = self._state(group, params, device)
-            rows = []
-            for p, (h, t, ld) in zip(params, copies.entries(params)):
-                g = p.grad
-                if g.dtype != torch.float32 or not g.is_contiguous() or g.shape != p.shape:
-                    raise ValueError("AdapterAdamW: gradients must be contiguous fp32")
-                st = self.state[p]
-                rows.append([p.data_ptr(), p.numel(), p.shape[1], h, t, ld, g.data_ptr(),
-                             st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr()])
-                covered.add(id(p))
-            table = self._table(gi, rows, device)
-            flip = group["_talm_flip"]
+            table, n, max_numel, step_in, step_out, buffer = self._group_launch_args(
+                gi, group, params, buffer)
+            covered.update(id(p) for p in params)
             beta1, beta2 = group["betas"]
-            torch.ops.talm.lora_adamw(table, len(params), max(p.numel() for p in params),
-                                      float(group["lr"]), beta1, beta2, group["eps"],
-                                      group["weight_decay"], steps[flip:flip + 1],
-                                      steps[1 - flip:2 - flip], grad_scale, found_inf, buffer)
-            group["_talm_flip"] = 1 - flip
-            for p in params:
-                self.state[p]["step"] = steps[1 - flip:2 - flip]
-            RAN["adapter_adamw"] += 1
+            torch.ops.talm.lora_adamw(table, n, max_numel, float(group["lr"]), beta1, beta2,
+                                      group["eps"], group["weight_decay"], step_in, step_out,
+                                      grad_scale, found_inf, buffer)
+            self._after_group(group, params, step_out)
         if buffer is not None and registered and registered <= covered:
             copies.adopt(buffer, self)
         return loss
+
+    @torch.no_grad()
+    def fused_tail(self, scaler, max_norm):
+        """`scaler.unscale_(self)`, `clip_grad_norm_(params, max_norm)` and `scaler.step(self)`
+        in three launches (talm_lora_grad_norm, talm_lora_adamw_clipped): the gradients are not
+        rewritten, the step reads them unscaled and clipped as those calls would leave them, and
+        is skipped when one is not finite. The scaler is left as `scaler.step` leaves it (this
+        step's inf flag recorded, ready for `scaler.update()`). Returns the gradients' total
+        norm (a device scalar), or None when it does not apply (one parameter group, every
+        parameter with a gradient, an enabled scaler that has scaled this step's loss and not
+        yet unscaled): the caller then runs the three calls."""
+        from torch.amp.grad_scaler import OptState
+
+        if len(self.param_groups) != 1 or not scaler.is_enabled():
+            return None
+        scale = getattr(scaler, "_scale", None)
+        states = getattr(scaler, "_per_optimizer_states", None)
+        if scale is None or states is None or states[id(self)]["stage"] is not OptState.READY:
+            return None
+        group = self.param_groups[0]
+        params = list(group["params"])
+        if not params or any(p.grad is None for p in params):
+            return None
+        copies = self.copies
+        registered = {id(ref()) for ref in copies.params if ref() is not None}
+        table, n, max_numel, step_in, step_out, buffer = self._group_launch_args(
+            0, group, params, None)
+        device = params[0].device
+        ws = torch.empty(_ops.lora_grad_norm_workspace_bytes(n, max_numel), dtype=torch.uint8,
+                         device=device)
+        stats = torch.empty(4, dtype=torch.float32, device=device)
+        torch.ops.talm.lora_grad_norm(table, n, max_numel, scale.reshape(1), float(max_norm), ws,
+                                      stats)
+        beta1, beta2 = group["betas"]
+        torch.ops.talm.lora_adamw_clipped(table, n, max_numel, float(group["lr"]), beta1, beta2,
+                                          group["eps"], group["weight_decay"], step_in, step_out,
+                                          stats[0:1], stats[1:3], buffer)
+        self._after_group(group, params, step_out)
+        if registered and registered <= {id(p) for p in params}:
+            copies.adopt(buffer, self)
+            copies.adopted_by = None  # what the step's post hook (`invalidate`) would leave
+        self._opt_called = True  # an optimizer step ran (the schedule's order check)
+        state = states[id(self)]
+        state["found_inf_per_device"] = {device: stats[0:1]}
+        state["stage"] = OptState.STEPPED
+        RAN["fused_tail"] += 1
+        return stats[3]

@@ -673,6 +673,50 @@ void lora_adamw(const Tensor& table, int64_t n_tensors, int64_t max_numel, doubl
         "lora_adamw");
 }
 
+// stats float32 [4] = {found_inf, inv_scale, clip coefficient, norm} of the table's gradients.
+void lora_grad_norm(const Tensor& table, int64_t n_tensors, int64_t max_numel, const Tensor& scale,
+                    double max_norm, const Tensor& workspace, const Tensor& stats) {
+  require(table.is_cuda() && table.scalar_type() == at::kLong && table.is_contiguous() &&
+              table.numel() >= n_tensors * 9,
+          "lora_grad_norm: table int64 [n_tensors, 9]");
+  for (const Tensor* t : {&scale, &stats})
+    require(t->is_cuda() && t->scalar_type() == at::kFloat && t->is_contiguous() &&
+                t->device() == table.device(),
+            "lora_grad_norm: scale and stats float32 on the table's device");
+  require(scale.numel() == 1 && stats.numel() == 4, "lora_grad_norm: scale [1], stats [4]");
+  require(workspace.is_cuda() && workspace.is_contiguous() && workspace.device() == table.device(),
+          "lora_grad_norm: workspace");
+  check(talm_lora_grad_norm(as<int64_t>(table), static_cast<int32_t>(n_tensors), max_numel,
+                            as<float>(scale), static_cast<float>(max_norm), workspace.data_ptr(),
+                            workspace.numel() * static_cast<int64_t>(workspace.element_size()),
+                            as<float>(stats), stream_of(stats)),
+        "lora_grad_norm");
+}
+
+// lora_adamw with the gradients unscaled and clipped by grad_mul = stats[1:3] and skipped on
+// found_inf = stats[0:1] (lora_grad_norm's outputs).
+void lora_adamw_clipped(const Tensor& table, int64_t n_tensors, int64_t max_numel, double lr,
+                        double beta1, double beta2, double eps, double weight_decay,
+                        const Tensor& step_in, const Tensor& step_out, const Tensor& found_inf,
+                        const Tensor& grad_mul, const Tensor& out) {
+  adapter_table(table, n_tensors, out, "lora_adamw_clipped");
+  for (const Tensor* t : {&step_in, &step_out, &found_inf, &grad_mul})
+    require(t->is_cuda() && t->scalar_type() == at::kFloat && t->is_contiguous() &&
+                t->device() == out.device(),
+            "lora_adamw_clipped: counters, inf flag and multipliers float32 on the copies' "
+            "device");
+  require(step_in.numel() == 1 && step_out.numel() == 1 && found_inf.numel() == 1 &&
+              grad_mul.numel() == 2 && step_in.data_ptr() != step_out.data_ptr(),
+          "lora_adamw_clipped: step counters [1] (distinct), found_inf [1], grad_mul [2]");
+  check(talm_lora_adamw_clipped(as<int64_t>(table), static_cast<int32_t>(n_tensors), max_numel,
+                                static_cast<float>(lr), static_cast<float>(beta1),
+                                static_cast<float>(beta2), static_cast<float>(eps),
+                                static_cast<float>(weight_decay), as<float>(step_in),
+                                as<float>(step_out), as<float>(found_inf), as<float>(grad_mul),
+                                as<uint16_t>(out), stream_of(out)),
+        "lora_adamw_clipped");
+}
+
 // ------------------------------------------------------------------------------------------
 // Products on the NF4 form of W [rows, cols] (dequantized inside the GEMM): out = x W^T
 // (transpose false: x [N, cols], out [N, rows]) or out = x W (transpose true: x [N, rows],
@@ -1385,6 +1429,11 @@ TORCH_LIBRARY(talm, m) {
   m.def("scatter_rows(Tensor token_loss, Tensor entropy, Tensor correct, Tensor targets, "
         "Tensor src, Tensor(a!) full_loss, Tensor(b!) full_entropy, Tensor(c!) stats) -> ()");
   m.def("scale_rows(Tensor g, Tensor grad_loss, Tensor denom, Tensor(a!) out) -> ()");
+  m.def("lora_grad_norm(Tensor table, int n_tensors, int max_numel, Tensor scale, "
+        "float max_norm, Tensor(a!) workspace, Tensor(b!) stats) -> ()");
+  m.def("lora_adamw_clipped(Tensor table, int n_tensors, int max_numel, float lr, float beta1, "
+        "float beta2, float eps, float weight_decay, Tensor step_in, Tensor(a!) step_out, "
+        "Tensor found_inf, Tensor grad_mul, Tensor(b!) out) -> ()");
   m.def("rope_table(Tensor positions, Tensor inv_freq, float scaling, Tensor(a!) cos, "
         "Tensor(b!) sin) -> ()");
   m.def("gemm_splitk_partials(Tensor a, Tensor b, Tensor(a!) partials) -> ()");
@@ -1442,6 +1491,8 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("scatter_rows", &scatter_rows);
   m.impl("scale_rows", &scale_rows);
   m.impl("rope_table", &rope_table);
+  m.impl("lora_grad_norm", &lora_grad_norm);
+  m.impl("lora_adamw_clipped", &lora_adamw_clipped);
   m.impl("gemm_splitk_partials", &gemm_splitk_partials);
   m.impl("nf4_gemm_partials", &nf4_gemm_partials);
   m.impl("splitk_add_rmsnorm", &splitk_add_rmsnorm);

@@ -19,6 +19,7 @@ uniform over the vocabulary, every real token labelled.
 """
 
 import math
+import os
 
 import torch
 import torch.nn as nn
@@ -31,6 +32,8 @@ QWEN25_15B = dict(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
                   max_position_embeddings=32768, rope_theta=1e6, rms_norm_eps=1e-6,
                   tie_word_embeddings=True, hidden_act="silu", attention_dropout=0.0,
                   initializer_range=0.02, use_sliding_window=False)
+
+FUSED_TAIL = os.environ.get("SOLUTION_DISABLE_FUSED_TAIL") != "1"
 
 PROJECTIONS = (("self_attn", "q_proj"), ("self_attn", "k_proj"), ("self_attn", "v_proj"),
                ("self_attn", "o_proj"), ("mlp", "gate_proj"), ("mlp", "up_proj"),
@@ -148,12 +151,20 @@ class Trainer:
 
     def optimizer_tail(self):
         """After the backward: unscale, clip, the optimizer step, the scale update, the
-        schedule, and the gradients released."""
-        self.scaler.unscale_(self.opt)
-        norm = torch.nn.utils.clip_grad_norm_(self.params, self.max_grad_norm)
-        if self.grad_hook is not None:
-            self.grad_hook(self, norm)
-        self.scaler.step(self.opt)
+        schedule, and the gradients released. With this package's optimizer and no grad_hook
+        (which reads the unscaled, clipped gradients) the first three run as
+        `AdapterAdamW.fused_tail`: three launches instead of about fifteen, the same values up
+        to the order in which the norm's squares are summed."""
+        norm = None
+        fused = getattr(self.opt, "fused_tail", None)
+        if fused is not None and self.grad_hook is None and FUSED_TAIL:
+            norm = fused(self.scaler, self.max_grad_norm)
+        if norm is None:
+            self.scaler.unscale_(self.opt)
+            norm = torch.nn.utils.clip_grad_norm_(self.params, self.max_grad_norm)
+            if self.grad_hook is not None:
+                self.grad_hook(self, norm)
+            self.scaler.step(self.opt)
         self.scaler.update()
         self.sched.step()
         self.opt.zero_grad(set_to_none=True)

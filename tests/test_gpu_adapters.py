@@ -118,3 +118,51 @@ def test_copies_registry_refreshes_after_inplace_change():
     assert torch.equal(second[0], first[0])  # an earlier copy is never overwritten
     t = copies.pair_t(tuple(ws))
     assert torch.equal(t, torch.cat(ws, 0).t().to(torch.float16))
+
+
+@pytest.mark.parametrize("case", ["clipped", "unclipped", "inf"])
+def test_fused_tail_matches_unscale_clip_step(case):
+    """AdapterAdamW.fused_tail (talm_lora_grad_norm + talm_lora_adamw_clipped) against
+    GradScaler.unscale_ + clip_grad_norm_ + GradScaler.step + update on the same scaled
+    gradients: the same total norm (to the norm's summation order), the same weights and moments
+    after the step, the same scale after the update; with an inf gradient no weight moves and
+    the scale backs off in both."""
+    print(f"[case] fused optimizer tail: {case}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    shapes = [(16, 1536), (1536, 16), (16, 1536), (256, 16)]
+    size = {"clipped": 1.0, "unclipped": 1e-4, "inf": 1.0}[case]
+    grads = [torch.randn(*s, generator=g).mul(size).cuda() for s in shapes]
+    if case == "inf":
+        grads[2][3, 7] = float("inf")
+    runs = []
+    for fused in (False, True):
+        params = [torch.randn(*s, generator=torch.Generator().manual_seed(4 + i)).mul(0.05)
+                  .cuda().requires_grad_() for i, s in enumerate(shapes)]
+        opt = adapters.AdapterAdamW(params, lr=1e-3, weight_decay=0.01,
+                                    copies=adapters.AdapterCopies())
+        scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 16)
+        scaler.scale(torch.ones((), device="cuda"))  # the scale tensor exists, as after a step
+        for p, gr in zip(params, grads):
+            p.grad = gr * scaler.get_scale()
+        if fused:
+            norm = opt.fused_tail(scaler, 1.0)
+            assert norm is not None
+        else:
+            scaler.unscale_(opt)
+            norm = torch.nn.utils.clip_grad_norm_(params, 1.0)
+            scaler.step(opt)
+        scaler.update()
+        runs.append((norm, [p.detach().clone() for p in params],
+                     [opt.state[p]["exp_avg_sq"].clone() for p in params], scaler.get_scale()))
+    (n0, w0, v0, s0), (n1, w1, v1, s1) = runs
+    assert s0 == s1
+    if case == "inf":
+        assert not torch.isfinite(n1) or not torch.isfinite(n0)
+        for a, b in zip(w0, w1):
+            assert torch.equal(a, b)
+        return
+    assert abs(float(n1) - float(n0)) <= 1e-6 * float(n0)
+    for a, b in zip(w0, w1):
+        torch.testing.assert_close(b, a, rtol=1e-6, atol=1e-9)
+    for a, b in zip(v0, v1):
+        torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-20)
