@@ -101,6 +101,8 @@ class MlpBlock(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, h, group, norm1, norm2, stage):
+        # an unused output (the last layer's sum) gets no made-up zero gradient
+        ctx.set_materialize_grads(False)
         shape, hidden = x.shape, x.shape[-1]
         x2, h2 = _flat(x, torch.float32), _flat(h, torch.float16)
         n_tok, dev = x2.shape[0], x.device

@@ -145,9 +145,20 @@ class Trainer:
         with torch.autocast("cuda", dtype=torch.float16):
             out = self.model(**batch)
         loss = out.loss
-        self.scaler.scale(loss).backward()
+        self.backward(loss)
         self.optimizer_tail()
         return loss.detach()
+
+    def backward(self, loss):
+        """`scaler.scale(loss).backward()`: the backward seeded with the scale itself once the
+        scaler holds it (the same gradients: d(loss * scale) / d(loss) = scale exactly), without
+        the multiply, the ones seed and the multiply's backward."""
+        scale = getattr(self.scaler, "_scale", None)
+        if self.scaler.is_enabled() and torch.is_tensor(scale) and scale.numel() == 1 \
+                and scale.device == loss.device and loss.dim() == 0:
+            torch.autograd.backward(loss, scale.reshape(()).to(loss.dtype))
+        else:
+            self.scaler.scale(loss).backward()
 
     def optimizer_tail(self):
         """After the backward: unscale, clip, the optimizer step, the scale update, the

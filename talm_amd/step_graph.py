@@ -131,7 +131,7 @@ class GraphedTrainer:
                             g.zero_()
                     with torch.autocast("cuda", dtype=torch.float16):
                         out = t.model(**self.static)
-                    t.scaler.scale(out.loss).backward()
+                    t.backward(out.loss)
         finally:
             fused_proj.GRAD_INTO.clear()
             for h in hooks:
