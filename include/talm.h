@@ -365,8 +365,8 @@ int talm_lora_wgrad_noalloc(const uint16_t* x, int64_t ldx, const uint16_t* dy, 
  * sequence; query head h reads KV head h / (n_q_heads / n_kv_heads). q f16 [n_tokens, n_q_heads,
  * head_dim], k / v f16 [n_tokens, n_kv_heads, head_dim] at element strides (token, head), unit
  * column stride; out likewise [n_tokens, n_q_heads, head_dim]; lse f32 [n_q_heads, n_tokens] =
- * log sum_j exp(scale q.k_j) per row. head_dim 128; strides multiples of 8; max_seqlen >= the
- * longest sequence. Replaces the reference's per-KV-head memory-efficient attention launches
+ * log sum_j exp(scale q.k_j) per row. head_dim 128; strides multiples of 8, the token strides of
+ * k, v and out below 2^23 elements; max_seqlen >= the longest sequence. Replaces the reference's per-KV-head memory-efficient attention launches
  * (solution/unpad.py:199-294) with per-row causal SDPA semantics (solution/unpad.py:121-134).
  */
 int talm_attn_fwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -379,10 +379,11 @@ int talm_attn_fwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head
 
 /*
  * Its backward: dq f16 [n_tokens, n_q_heads, head_dim], dk / dv f16 [n_tokens, n_kv_heads,
- * head_dim] (any strides as above) from q, k, v, the forward's out and lse, and dout. dk / dv of
+ * head_dim] (any strides as above; the token strides of q, k, v, dout and dq below 2^23
+ * elements) from q, k, v, the forward's out and lse, and dout. dk / dv of
  * a KV head sum its query heads' contributions in head order (deterministic). `workspace`
  * (256-byte aligned) holds talm_attn_bwd_workspace(n_tokens, n_q_heads) bytes: rowsum(dout *
- * out) and fp32 dk / dv partials per query head. Replaces the backward of the same launches
+ * out), lse in base-2 units and fp32 dk / dv partials per query head. Replaces the backward of the same launches
  * (solution/unpad.py:199-294).
  */
 int64_t talm_attn_bwd_workspace(int64_t n_tokens, int32_t n_q_heads);

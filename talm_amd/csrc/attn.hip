@@ -127,6 +127,17 @@ __device__ __forceinline__ void lgkm_wait8(half4_t (&r)[8]) {
                  "+v"(r[6]), "+v"(r[7]));
 }
 
+// 16 bytes stored at byte offset `off` of the range that starts at `base`. A row past the
+// sequence gets off = kOob, past the descriptor's range, and the hardware drops the store: the
+// epilogues issue all their LDS reads and then all their stores, with no branch per row (a branch
+// holding a read and its store made each read wait for the one before).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t store_rsrc(void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+}
+
 // One [64][128] tile from global rows base[r * ld + c] (r < rows_valid, else zeros) into `dst`
 // with direct-to-LDS 16-byte loads: block b (rows 4 b .. 4 b + 3) by wavefront b % W.
 template <int W>
@@ -237,11 +248,16 @@ __global__ __launch_bounds__(64 * W * S) void attn_fwd_kernel(FwdArgs a) {
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) st[b][v] = 0.f;
+      // the block's 8 operand reads issued before its MFMAs
+      half8_t ka[kD / 16];
 #pragma unroll
       for (int s = 0; s < kD / 16; ++s)
-        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            __builtin_bit_cast(half8_t, k16[tile_chunk(32 * b + l32, 2 * s + hh)]), qf[s], st[b],
-            0, 0, 0);
+        ka[s] = __builtin_bit_cast(half8_t, k16[tile_chunk(32 * b + l32, 2 * s + hh)]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s)
+        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[s], qf[s], st[b], 0, 0, 0);
     }
     // causal / length mask only on a tile that reaches past the first query row of the
     // workgroup or past the sequence: a real (uniform) branch; the empty volatile asm keeps the
@@ -361,13 +377,19 @@ __global__ __launch_bounds__(64 * W * S) void attn_fwd_kernel(FwdArgs a) {
   // the wavefront reads back its own staging rows (the other groups have exited: no workgroup
   // barrier): its LDS writes complete first, and the compiler keeps the order
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  constexpr int kOut = (32 * kD / 8) / 64;  // 16-byte chunks per lane
+  u32x4 ov[kOut];
 #pragma unroll
-  for (int it = 0; it < (32 * kD / 8) / 64; ++it) {
+  for (int it = 0; it < kOut; ++it) {
     const int cc16 = it * 64 + lane, r = cc16 / (kD / 8), cc = cc16 % (kD / 8);
-    const int row = q0 + r;
-    if (row < len)
-      *reinterpret_cast<u32x4*>(a.out + static_cast<int64_t>(s0 + row) * a.o_tok + head * a.o_head + 8 * cc) =
-          *reinterpret_cast<const u32x4*>(&os[r * kKS + 8 * cc]);
+    ov[it] = *reinterpret_cast<const u32x4*>(&os[r * kKS + 8 * cc]);
+  }
+  const __amdgpu_buffer_rsrc_t ors =
+      store_rsrc(a.out + static_cast<int64_t>(s0 + q0) * a.o_tok + head * a.o_head);
+#pragma unroll
+  for (int it = 0; it < kOut; ++it) {
+    const int cc16 = it * 64 + lane, r = cc16 / (kD / 8), cc = cc16 % (kD / 8);
+    store16(ors, q0 + r < len ? static_cast<uint32_t>((r * a.o_tok + 8 * cc) * 2) : kOob, ov[it]);
   }
 }
 
@@ -392,6 +414,7 @@ struct BwdArgs {
   float scale, scale_log2;
   int64_t n_tokens;
   float* dd;           // [Hq, n_tokens]: rowsum(dO * O)
+  float* lse2;         // [Hq, n_tokens]: lse in base-2 units (lse * log2 e)
   float* dk_part;      // [Hq, n_tokens, D] fp32
   float* dv_part;      // [Hq, n_tokens, D] fp32
   uint16_t* dq;
@@ -426,7 +449,8 @@ __device__ __forceinline__ void rope_back4(float (&x)[4], float (&y)[4], const f
   }
 }
 
-// Dd[h][t] = sum_d dO[t][h][d] * O[t][h][d]: 16 lanes per (token, head), 8 columns each.
+// Dd[h][t] = sum_d dO[t][h][d] * O[t][h][d] and lse2[h][t] = lse[h][t] log2 e (the exponent offset
+// both backward bodies subtract): 16 lanes per (token, head), 8 columns each.
 __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(BwdArgs a) {
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;  // t * Hq + h
   const int sub = threadIdx.x & 15;
@@ -441,7 +465,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(BwdArgs a) {
               lo_f(x.w) * lo_f(y.w) + hi_f(x.w) * hi_f(y.w);
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
-  if (sub == 0 && row < rows) a.dd[static_cast<int64_t>(h) * a.n_tokens + t] = acc;
+  if (sub == 0 && row < rows) {
+    const int64_t i = static_cast<int64_t>(h) * a.n_tokens + t;
+    a.dd[i] = acc;
+    a.lse2[i] = a.lse[i] * 1.44269504088896341f;
+  }
 }
 
 // The dQ and dK / dV bodies below stream their tiles with the forward's direct-to-LDS loads into
@@ -498,7 +526,7 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
       df[s] = *reinterpret_cast<const half8_t*>(dp + 16 * s);
     }
   }
-  const float lse2 = a.lse[static_cast<int64_t>(head) * a.n_tokens + s0 + qr] * 1.44269504088896341f;
+  const float lse2 = a.lse2[static_cast<int64_t>(head) * a.n_tokens + s0 + qr];
   const float ddr = a.dd[static_cast<int64_t>(head) * a.n_tokens + s0 + qr];
   const int wq0 = q0 + 32 * wave;  // the wavefront's first query row
 
@@ -531,14 +559,19 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) st[b][v] = dpt[b][v] = 0.f;
+      // the block's 16 operand reads issued before its MFMAs
+      half8_t ka[kD / 16], va[kD / 16];
 #pragma unroll
       for (int s = 0; s < kD / 16; ++s) {
-        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            __builtin_bit_cast(half8_t, k16[tile_chunk(32 * b + l32, 2 * s + hh)]), qf[s], st[b],
-            0, 0, 0);
-        dpt[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            __builtin_bit_cast(half8_t, v16[tile_chunk(32 * b + l32, 2 * s + hh)]), df[s],
-            dpt[b], 0, 0, 0);
+        ka[s] = __builtin_bit_cast(half8_t, k16[tile_chunk(32 * b + l32, 2 * s + hh)]);
+        va[s] = __builtin_bit_cast(half8_t, v16[tile_chunk(32 * b + l32, 2 * s + hh)]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s) {
+        st[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[s], qf[s], st[b], 0, 0, 0);
+        dpt[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[s], df[s], dpt[b], 0, 0, 0);
       }
     }
     // K^T operands of the first 16-key group, read while the scores are turned into dS^T
@@ -630,13 +663,19 @@ __device__ __forceinline__ void attn_bwd_dq(const BwdArgs& a, int tile, unsigned
     }
   // the wavefront reads back its own staging rows: its LDS writes complete first
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  constexpr int kOut = (32 * kD / 8) / 64;  // 16-byte chunks per lane
+  u32x4 ov[kOut];
 #pragma unroll
-  for (int it = 0; it < (32 * kD / 8) / 64; ++it) {
+  for (int it = 0; it < kOut; ++it) {
     const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
-    const int row = q0 + 32 * wave + r;
-    if (row < len)
-      *reinterpret_cast<u32x4*>(a.dq + static_cast<int64_t>(s0 + row) * a.dq_tok + head * a.dq_head + 8 * cc) =
-          *reinterpret_cast<const u32x4*>(&os[r * kKS + 8 * cc]);
+    ov[it] = *reinterpret_cast<const u32x4*>(&os[r * kKS + 8 * cc]);
+  }
+  const __amdgpu_buffer_rsrc_t ors =
+      store_rsrc(a.dq + static_cast<int64_t>(s0 + wq0) * a.dq_tok + head * a.dq_head);
+#pragma unroll
+  for (int it = 0; it < kOut; ++it) {
+    const int c = it * 64 + lane, r = c / (kD / 8), cc = c % (kD / 8);
+    store16(ors, wq0 + r < len ? static_cast<uint32_t>((r * a.dq_tok + 8 * cc) * 2) : kOob, ov[it]);
   }
 }
 
@@ -674,7 +713,7 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
   const uint16_t* qbase = a.q + static_cast<int64_t>(s0) * a.q_tok + head * a.q_head;
   const uint16_t* dbase = a.dout + static_cast<int64_t>(s0) * a.do_tok + head * a.do_head;
   const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(a.lse + static_cast<int64_t>(head) * a.n_tokens + s0), 0, len * 4, 0x00020000);
+      a.lse2 + static_cast<int64_t>(head) * a.n_tokens + s0, 0, len * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t drs = __builtin_amdgcn_make_buffer_rsrc(
       a.dd + static_cast<int64_t>(head) * a.n_tokens + s0, 0, len * 4, 0x00020000);
   auto issue = [&](int qt, int slot) {
@@ -712,14 +751,20 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
     for (int blk = 0; blk < 2; ++blk) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) sc[blk][v] = dp[blk][v] = 0.f;
+      // the block's 16 operand reads issued before its MFMAs (one LDS round trip, not one per
+      // MFMA pair)
+      half8_t qa[kD / 16], da[kD / 16];
 #pragma unroll
       for (int s = 0; s < kD / 16; ++s) {
-        sc[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            __builtin_bit_cast(half8_t, q16[tile_chunk(32 * blk + l32, 2 * s + hh)]), kf[s],
-            sc[blk], 0, 0, 0);
-        dp[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-            __builtin_bit_cast(half8_t, d16[tile_chunk(32 * blk + l32, 2 * s + hh)]), vf[s],
-            dp[blk], 0, 0, 0);
+        qa[s] = __builtin_bit_cast(half8_t, q16[tile_chunk(32 * blk + l32, 2 * s + hh)]);
+        da[s] = __builtin_bit_cast(half8_t, d16[tile_chunk(32 * blk + l32, 2 * s + hh)]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the 16 LDS reads first
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // then the 16 MFMAs
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s) {
+        sc[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa[s], kf[s], sc[blk], 0, 0, 0);
+        dp[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(da[s], vf[s], dp[blk], 0, 0, 0);
       }
     }
     // dO^T and Q^T operands of the first 16-row group, read while P and dS are formed
@@ -732,8 +777,10 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
       }
     };
     read_t(0, 0);
-    // P and dS, 0 where masked (query row < key or past the sequence, key past the sequence);
-    // the rows' lse and Dd come from the slot with untracked reads as well
+    // P and dS, 0 where masked (query row < key or past the sequence, key past the sequence: only
+    // on a tile with a row before the wavefront's last key or reaching past the sequence, a
+    // uniform branch); the rows' lse and Dd come from the slot with untracked reads as well
+    const bool edge = r0 < wk0 + 31 || r0 + kRowsT > len || wk0 + 32 > len;
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
       f32x4_t l4[4], d4[4];
@@ -744,17 +791,29 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
       }
       lgkm_wait_f4(l4);
       lgkm_wait_f4(d4);
+      if (edge) {
+        asm volatile("");
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+        for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = 4 * g + e, q = r0 + 32 * blk + 8 * g + 4 * hh + e;
-          const bool valid = q >= key && q < len && key < len;
-          const float p =
-              valid ? exp2_(sc[blk][v] * a.scale_log2 - l4[g][e] * 1.44269504088896341f) : 0.f;
-          sc[blk][v] = p;
-          dp[blk][v] = p * (dp[blk][v] - d4[g][e]);
-        }
+          for (int e = 0; e < 4; ++e) {
+            const int v = 4 * g + e, q = r0 + 32 * blk + 8 * g + 4 * hh + e;
+            const bool valid = q >= key && q < len && key < len;
+            const float p = valid ? exp2_(sc[blk][v] * a.scale_log2 - l4[g][e]) : 0.f;
+            sc[blk][v] = p;
+            dp[blk][v] = p * (dp[blk][v] - d4[g][e]);
+          }
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int v = 4 * g + e;
+            const float p = exp2_(sc[blk][v] * a.scale_log2 - l4[g][e]);
+            sc[blk][v] = p;
+            dp[blk][v] = p * (dp[blk][v] - d4[g][e]);
+          }
+      }
     }
     // dV^T[d][key] += dO^T[d][q] P[q][key];  dK^T[d][key] += Q^T[d][q] dS[q][key]
 #pragma unroll
@@ -784,22 +843,42 @@ __device__ __forceinline__ void attn_bwd_dkdv(const BwdArgs& a, int tile, unsign
   };
   ring2(n_qt, issue, body);
 
-  // fp32 partials [head][token][d]: lane = key column, rows d = 32 j + 8 (v / 4) + 4 hh + v % 4
-  if (key < len) {
-    float* pk = a.dk_part + (static_cast<int64_t>(head) * a.n_tokens + s0 + key) * kD;
-    float* pv = a.dv_part + (static_cast<int64_t>(head) * a.n_tokens + s0 + key) * kD;
+  // fp32 partials [head][token][d]. A lane holds its key's column of the accumulators (rows
+  // d = 32 j + 8 (v / 4) + 4 hh + v % 4): stored as they are, every store instruction would touch
+  // 64 rows 16 bytes each. Each wavefront stages its 32 keys x 128 columns in its own part of the
+  // ring instead (rows of 132 floats: the 16 lanes of a write phase meet 16 distinct bank groups)
+  // and stores whole rows, two per instruction.
+  __syncthreads();  // every wavefront is done with the ring
+  constexpr int kStageLd = kD + 4;
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * kStageLd;
+  auto store_rows = [&](const f32x16 (&acc)[kD / 32], float mul, float* part) {
 #pragma unroll
     for (int j = 0; j < kD / 32; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * j + 8 * g + 4 * hh;
-        *reinterpret_cast<float4*>(pk + d0) = make_float4(
-            dka[j][4 * g] * a.scale, dka[j][4 * g + 1] * a.scale, dka[j][4 * g + 2] * a.scale,
-            dka[j][4 * g + 3] * a.scale);
-        *reinterpret_cast<float4*>(pv + d0) =
-            make_float4(dva[j][4 * g], dva[j][4 * g + 1], dva[j][4 * g + 2], dva[j][4 * g + 3]);
-      }
-  }
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(&stage[l32 * kStageLd + 32 * j + 8 * g + 4 * hh]) =
+            make_float4(acc[j][4 * g] * mul, acc[j][4 * g + 1] * mul, acc[j][4 * g + 2] * mul,
+                        acc[j][4 * g + 3] * mul);
+    // the wavefront reads back its own rows: its LDS writes complete first
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    u32x4 x[16];
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int r = 2 * it + (lane >> 5), c = lane & 31;
+      x[it] = *reinterpret_cast<const u32x4*>(&stage[r * kStageLd + 4 * c]);
+    }
+    const __amdgpu_buffer_rsrc_t prs =
+        store_rsrc(part + (static_cast<int64_t>(head) * a.n_tokens + s0 + wk0) * kD);
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int r = 2 * it + (lane >> 5), c = lane & 31;
+      store16(prs, wk0 + r < len ? static_cast<uint32_t>((r * kD + 4 * c) * 4) : kOob, x[it]);
+    }
+    // the next call overwrites the rows: every read above has returned first
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  store_rows(dka, a.scale, a.dk_part);
+  store_rows(dva, 1.f, a.dv_part);
 }
 
 // dQ and the dK / dV partials in one launch: they read the same inputs and write disjoint
@@ -885,8 +964,9 @@ TALM_API int talm_attn_fwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
                     v_stride_head, o_stride_tok, o_stride_head})
     if (s < 0 || s % 8)
       return fail(TALM_EINVAL, "attn_fwd: strides must be non-negative multiples of 8 elements");
-  if (k_stride_tok >= (int64_t{1} << 23) || v_stride_tok >= (int64_t{1} << 23))
-    return fail(TALM_EINVAL, "attn_fwd: k / v token strides must be below 2^23 elements");
+  if (k_stride_tok >= (int64_t{1} << 23) || v_stride_tok >= (int64_t{1} << 23) ||
+      o_stride_tok >= (int64_t{1} << 23))
+    return fail(TALM_EINVAL, "attn_fwd: k / v / out token strides must be below 2^23 elements");
   if (n_seqs == 0 || max_seqlen == 0 || n_tokens == 0) return ok();
   if (!q || !k || !v || !cu_seqlens || !out || !lse) return fail(TALM_EINVAL, "attn_fwd: null pointer");
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
@@ -920,9 +1000,10 @@ TALM_API int talm_attn_fwd(const uint16_t* q, int64_t q_stride_tok, int64_t q_st
 
 TALM_API int64_t talm_attn_bwd_workspace(int64_t n_tokens, int32_t n_q_heads) {
   if (n_tokens < 0 || n_q_heads < 1) return -1;
-  // Dd [Hq, N] f32, then the dK and dV partials [Hq, N, D] f32 each (256-byte aligned parts)
+  // Dd and lse2 [Hq, N] f32, then the dK and dV partials [Hq, N, D] f32 each (256-byte aligned
+  // parts)
   const int64_t dd = (n_tokens * n_q_heads * 4 + 255) / 256 * 256;
-  return dd + 2 * n_tokens * n_q_heads * kD * 4;
+  return 2 * dd + 2 * n_tokens * n_q_heads * kD * 4;
 }
 
 namespace talm {
@@ -954,8 +1035,9 @@ int attn_bwd_impl(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head
     if (s < 0 || s % 8)
       return fail(TALM_EINVAL, "attn_bwd: strides must be non-negative multiples of 8 elements");
   if (q_stride_tok >= (int64_t{1} << 23) || k_stride_tok >= (int64_t{1} << 23) ||
-      v_stride_tok >= (int64_t{1} << 23) || do_stride_tok >= (int64_t{1} << 23))
-    return fail(TALM_EINVAL, "attn_bwd: q / k / v / dout token strides must be below 2^23 elements");
+      v_stride_tok >= (int64_t{1} << 23) || do_stride_tok >= (int64_t{1} << 23) ||
+      dq_stride_tok >= (int64_t{1} << 23))
+    return fail(TALM_EINVAL, "attn_bwd: q / k / v / dout / dq token strides must be below 2^23 elements");
   if (n_seqs > 65535 || (max_seqlen + 127) / 128 > 32767)
     return fail(TALM_EINVAL, "attn_bwd: at most 65535 sequences of at most 4194176 tokens");
   const int64_t need = talm_attn_bwd_workspace(n_tokens, n_q_heads);
@@ -988,8 +1070,10 @@ int attn_bwd_impl(const uint16_t* q, int64_t q_stride_tok, int64_t q_stride_head
   a.scale = scale; a.scale_log2 = scale * 1.44269504088896341f;
   a.n_tokens = n_tokens;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const int64_t dd_bytes = (n_tokens * n_q_heads * 4 + 255) / 256 * 256;
   a.dd = reinterpret_cast<float*>(ws);
-  a.dk_part = reinterpret_cast<float*>(ws + (n_tokens * n_q_heads * 4 + 255) / 256 * 256);
+  a.lse2 = reinterpret_cast<float*>(ws + dd_bytes);
+  a.dk_part = reinterpret_cast<float*>(ws + 2 * dd_bytes);
   a.dv_part = a.dk_part + n_tokens * n_q_heads * kD;
   a.dq = dq; a.dq_tok = dq_stride_tok; a.dq_head = dq_stride_head;
   a.dk = dk; a.dk_tok = dk_stride_tok; a.dk_head = dk_stride_head;
