@@ -298,6 +298,24 @@ int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t 
                       void* stream);
 
 /*
+ * talm_qkv_lora_fwd with the adapters' down-projection inside the same GEMM: A_g f16 [16, hidden]
+ * (row stride lda) for adapter g; every output tile of an adapter's columns accumulates
+ * t = x A_g^T over its rows during the main product and adds fp16(scaling_g t) B_g^T after it (in
+ * fp32, before the bias and the one rounding). t f16 [n_tokens, 16 * n_adapters] (row stride ldt,
+ * adapter g in columns 16 g ..) is written for the backward. Replaces the same reference code as
+ * talm_qkv_lora_fwd together with the adapters' down projection x A^T (solution/lora.py:
+ * 151-231, solution/fused_proj.py:118-140), in one launch instead of talm_lora_down + it.
+ */
+int talm_qkv_lora_fwd_down(const uint16_t* x, int64_t ldx, int64_t n_tokens, int64_t hidden,
+                           const uint16_t* weight, int64_t ldw, int64_t n_out, const uint16_t* bias,
+                           int32_t n_adapters, const uint16_t* a0, const uint16_t* a1, int64_t lda,
+                           float scaling0, float scaling1, const uint16_t* b0, int64_t seg0_begin,
+                           int64_t seg0_end, const uint16_t* b1, int64_t seg1_begin,
+                           int64_t seg1_end, const float* cos, const float* sin, int64_t cs_stride,
+                           int64_t rope_cols, uint16_t* t, int64_t ldt, uint16_t* out, int64_t ldo,
+                           void* stream);
+
+/*
  * The q|k|v node's backward operand: dcat f16 [n_tokens, q + k + v] (row stride ldc) =
  * [rope_back(dq) | rope_back(dk) | dv] with dx1 = dy1 c1 + dy2 s2, dx2 = dy2 c2 - dy1 s1 on the
  * (j, j + 64) pairs of each 128-column head (no rotation when cos is NULL). Replaces the

@@ -21,7 +21,7 @@ from . import _lib
 OPS_PATH = Path(__file__).resolve().parent / "libtalm_torch.so"
 OPS = ("nf4_group_dequant", "nf4_group_dequant_streaming", "nf4_dequant", "rmsnorm", "rope",
        "swiglu_fwd", "swiglu_bwd", "swiglu_fwd_rows", "swiglu_bwd_rows",
-       "head_weight_t", "head_ce", "lora_down", "qkv_lora_fwd", "qkv_bwd_prep", "qkv_lora_bwd_dx",
+       "head_weight_t", "head_ce", "lora_down", "qkv_lora_fwd", "qkv_lora_fwd_down", "qkv_bwd_prep", "qkv_lora_bwd_dx",
        "lora_wgrad", "gemm", "gemm_ex", "attn_fwd", "attn_bwd", "attn_bwd_rope", "lora_mirror",
        "lora_adamw", "nf4_gemm", "nf4_block_scales", "nf4_group_dequant_t", "gemm_splitk",
        "pack_rows", "row_stats", "head_loss", "scatter_rows", "scale_rows",

@@ -516,6 +516,7 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
 template <int BK, int FRAGS, int SLOTS>
 struct TileScale {
   static_assert(FRAGS == 2 || FRAGS == 4, "two or four 32-row A fragments per wavefront");
+  static constexpr int kLoads = 1;
   using Word = typename std::conditional<FRAGS == 4, uint2, uint32_t>::type;
   const uint16_t* base;  // &scale[scale_index(r0 + lane % 32, 0, blocks)]
   int64_t tile_stride;   // blocks * 128
@@ -531,6 +532,7 @@ struct TileScale {
     const uint16_t h = static_cast<uint16_t>((i & 1) ? w >> 16 : w & 0xffffu);
     return a * __builtin_bit_cast(_Float16, h);
   }
+  __device__ __forceinline__ void after(const unsigned char*, int, int) {}
 };
 struct GradArgs {
   const uint16_t* Z;

@@ -149,15 +149,19 @@ struct Loader {
 template <class S>
 using Acc = f32x16[S::kFragM][S::kFragN];
 
-// Scaling of the A fragments between their LDS read and the MFMAs, per ring step. The default
-// leaves them as read; a scaling hook loads step kt's factors into its register set `slot` (the
-// step's ring slot) in prefetch(kt, slot), issued right before step kt's DMA group so that the
-// wait for that group covers them too, and multiplies fragment i of the wavefront by them in
-// apply(a, i, slot). The ring is unrolled by its depth, so `slot` is a compile-time index and no
-// register is copied (a copy of a loaded register would wait for its load).
+// A per-step hook of the ring. The default does nothing; a hook loads step kt's own operands
+// (kLoads vector-memory operations per thread) into its register set `slot` (the step's ring
+// slot) in prefetch(kt, slot), issued right before step kt's DMA group so that the wait for that
+// group covers them too. apply(a, i, slot) may scale fragment i of the wavefront's A fragments
+// between their LDS read and the MFMAs; after(stage, slot, kt) runs once the step's MFMAs are
+// issued, with the step's stage still in LDS (more MFMAs on the same A block). The ring is
+// unrolled by its depth, so `slot` is a compile-time index and no register is copied (a copy of a
+// loaded register would wait for its load).
 struct NoScale {
+  static constexpr int kLoads = 0;
   __device__ __forceinline__ void prefetch(int, int) {}
   __device__ __forceinline__ half8_t apply(half8_t a, int, int) const { return a; }
+  __device__ __forceinline__ void after(const unsigned char*, int, int) {}
 };
 
 // One step of the wavefront's block: BK / 16 x (kFragM A + kFragN B fragments, their MFMAs).
@@ -203,14 +207,15 @@ __device__ __forceinline__ void wait_groups(int later) {
 // kt + STAGES - 2 stay in flight), one barrier makes every wavefront's data visible and retires
 // the slot read in step kt - 1, which then receives step kt + STAGES - 1. With a scaling hook,
 // step kt's factors are loaded right before its group and every step issues a full group (past
-// nk the loaders read zeros into a retired slot) and one factor load (clamped to the last step,
+// nk the loaders read zeros into a retired slot) and the hook's loads (clamped to the last step,
 // step 0 when nk is 0), so every wait counts whole groups. The step loop is unrolled by STAGES: slot indices and LDS
 // offsets are compile-time constants.
 template <class S, class Issue, class Scale = NoScale>
 __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& issue, Acc<S>& acc,
                                           int lane, int wave, Scale&& scale = Scale()) {
-  constexpr bool kScaled = !std::is_same<std::decay_t<Scale>, NoScale>::value;
-  constexpr int kGroup = Loader<S, S::kBM>::kPer + Loader<S, S::kBN>::kPer + (kScaled ? 1 : 0);
+  constexpr int kHookLoads = std::decay_t<Scale>::kLoads;
+  constexpr bool kScaled = kHookLoads > 0;
+  constexpr int kGroup = Loader<S, S::kBM>::kPer + Loader<S, S::kBN>::kPer + kHookLoads;
   constexpr int kSt = S::kStages;
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 #pragma unroll
@@ -242,6 +247,7 @@ __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& i
       mma_step<S>(reinterpret_cast<const uint4*>(st),
                   reinterpret_cast<const uint4*>(st + S::kAChunks * 16), acc, lane, wm, wn, scale,
                   i);
+      scale.after(st, i, kt);
     }
   }
   __syncthreads();  // every wavefront is done with the ring before the caller reuses the LDS

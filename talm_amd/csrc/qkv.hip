@@ -228,13 +228,79 @@ struct QkvArgs {
   uint16_t* out;          // [n_tokens][ldo]
   int64_t ldo;
   int n_mtiles, n_ntiles;
+  // proj_ext_kernel<true>: the adapters' down-projection inside the GEMM (ts unused): A_g
+  // [16][lda] fp16, t = x A_g^T written to t_out [n_tokens][ldt_out] (adapter g's 16 columns from
+  // 16 g) by the first column tile of the segment
+  const uint16_t* adown[kMaxAdapters];
+  int64_t lda;
+  float scaling[kMaxAdapters];
+  uint16_t* t_out;
+  int64_t ldt_out;
+};
+
+// The forward's LoRA down-projection inside the q|k|v GEMM (proj_ext_kernel<true>): each ring
+// step of the main product also accumulates t = x A_g^T over the tile's 64 rows, wavefront w
+// taking rows 16 w .. 16 w + 15 with two v_mfma_f32_16x16x32_f16 per 64-deep step. Their A
+// operand is the x block already in the step's stage; their B operand is the adapter's 16 x 64
+// slice of A_g, which the workgroup streams into a three-slot ring of its own beside the tile
+// ring (2 KiB per step: each wavefront one direct-to-LDS load of four rows, its lanes past 32
+// masked off), issued and waited with the step's stage. Slice row r holds chunk c at position
+// c ^ (r / 2): the 16 lanes of a read phase (rows 0 .. 15, one chunk) meet 16 bank groups.
+constexpr int kDownSlice = kRank * 64 * 2;  // bytes of one step's A_g slice
+
+template <class S>
+struct DownHook {
+  static constexpr int kLoads = 1;
+  __amdgpu_buffer_rsrc_t ra;
+  unsigned char* ring;  // kStages slices of kDownSlice bytes
+  uint32_t off;         // this lane's global byte offset at step 0 (lanes below 32)
+  int klim;             // k below which A_g is read: the hidden size, 0 outside the adapters
+  int kc;               // this lane's k inside a step (lanes below 32)
+  int dst;              // this wavefront's 512 bytes of a slice
+  int row;              // the lane's x row in the stage: 16 wave + lane % 16
+  int lane;
+  bool live;            // the tile is in an adapter's columns
+  f32x4 t;
+  __device__ __forceinline__ void prefetch(int kt, int slot) {
+    const int k = kt * S::kBK + kc;
+    // one compare, no branch around the address: a select between two offsets
+    const uint32_t o = k < klim ? off + static_cast<uint32_t>(kt * S::kBK * 2) : kOob;
+    if (lane < 32) dma16(ra, ring + slot * kDownSlice + dst, o);
+  }
+  __device__ __forceinline__ half8_t apply(half8_t a, int, int) const { return a; }
+  __device__ __forceinline__ void after(const unsigned char* st, int slot, int) {
+    if (!live) return;  // uniform over the workgroup
+    const uint4* As = reinterpret_cast<const uint4*>(st);
+    const uint4* Bs = reinterpret_cast<const uint4*>(ring + slot * kDownSlice);
+    const int r = lane & 15;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 4 * h + (lane >> 4);
+      t = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, As[swz<S::kCpr>(row, c)]),
+                                                  __builtin_bit_cast(half8_t, Bs[r * 8 + (c ^ (r >> 1))]),
+                                                  t, 0, 0, 0);
+    }
+  }
 };
 
 // out = x w^T (+ the extra step on the tile's segment) (+ bias), optionally rotated: the forward
 // (extra step = the adapter term) and the backward dX (extra step = u A over all columns).
+// kDown: the forward with the adapters' t = x A_g^T computed by the tile itself during the main
+// product (DownHook) and the adapter term added after it as ts B_g^T (ts = fp16(scaling t),
+// two v_mfma_f32_32x32x16_f16 per wavefront, K = the rank 16), in place of the extra step.
+constexpr int kTsOff = 32 * 1024;  // ts [64][kTsLd] in the ring after the main product
+constexpr int kTsLd = 24;          // 48-byte rows: a 16-lane phase of 16-byte reads meets 16 bank groups
+static_assert(kTsOff >= QkvShape::kBM * kQZS * 2 && kTsOff + QkvShape::kBM * kTsLd * 2 <= QkvShape::kRing,
+              "ts beside the staged tile");
+
+template <bool kDown>
 __global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void proj_ext_kernel(QkvArgs a) {
   using S = QkvShape;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing];
+  static_assert(S::kFragM == 1 && S::kWaveM == 32 && S::kWaves == 4 && S::kBM == 64 &&
+                    S::kBK == 64 && S::kCpr == 8,
+                "the down-projection hook assumes four wavefronts on 64 rows, 64-deep steps");
+  // the tile ring, then (kDown) the adapter slices' ring
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[S::kRing + (kDown ? S::kStages * kDownSlice : 0)];
   const uint32_t tile = xcd_tile(blockIdx.x, static_cast<uint32_t>(a.n_mtiles * a.n_ntiles));
   const int ntile = static_cast<int>(tile / a.n_mtiles), mtile = static_cast<int>(tile % a.n_mtiles);
   const int m0 = mtile * S::kBM, n0 = ntile * S::kBN;
@@ -261,13 +327,72 @@ __global__ __launch_bounds__(QkvShape::kThreads, QkvShape::kPerCu) void proj_ext
           bg + static_cast<int64_t>(n0 - sb) * ldb - lo, ldb, se - n0, lo, hi, wave, lane);
   const int nk1 = (a.hidden + S::kBK - 1) / S::kBK;
   Acc<S> acc;
-  ring_gemm<S>(
-      smem, nk1 + (g >= 0 ? (hi + S::kBK - 1) / S::kBK : 0),
-      [&](unsigned char* slot, int kt) {
-        la.issue(slot, kt, wave);
-        lb.issue(slot + S::kAChunks * 16, kt, wave);
-      },
-      acc, lane, wave);
+  if constexpr (!kDown) {
+    ring_gemm<S>(
+        smem, nk1 + (g >= 0 ? (hi + S::kBK - 1) / S::kBK : 0),
+        [&](unsigned char* slot, int kt) {
+          la.issue(slot, kt, wave);
+          lb.issue(slot + S::kAChunks * 16, kt, wave);
+        },
+        acc, lane, wave);
+  } else {
+    // the adapter's B rows for this wavefront's two 32-column blocks (B_g [segment][16]: lane
+    // gets output column n0 + 64 wn + 32 j + lane % 32, k-slots 8 (lane / 32) .. + 7), loaded
+    // now so that they have landed when the product ends
+    half8_t bfr[S::kFragN];
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(bg);
+#pragma unroll
+    for (int j = 0; j < S::kFragN; ++j) {
+      const int col = n0 + wn * S::kWaveN + 32 * j + (lane & 31);
+      bfr[j] = __builtin_bit_cast(
+          half8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                       rb, g >= 0 && col < se ? static_cast<uint32_t>(((col - sb) * kRank + 8 * (lane >> 5)) * 2) : kOob,
+                       0, 0));
+    }
+    DownHook<S> hook;
+    hook.ra = buffer_rsrc(g1 ? a.adown[1] : a.adown[0]);
+    {
+      // lane l < 32 of wavefront w fills slice row 4 w + l / 8, position l % 8: the global chunk
+      // the swizzle puts there
+      const int r = 4 * wave + (lane >> 3) % 4, c = (lane & 7) ^ (r >> 1);
+      hook.off = static_cast<uint32_t>((r * a.lda + 8 * c) * 2);
+      hook.kc = 8 * c;
+    }
+    hook.ring = smem + S::kRing;
+    hook.dst = wave * 512;
+    hook.lane = lane;
+    hook.klim = g >= 0 ? a.hidden : 0;
+    hook.row = 16 * wave + (lane & 15);
+    hook.live = g >= 0;
+    hook.t = f32x4{0.f, 0.f, 0.f, 0.f};
+    ring_gemm<S>(
+        smem, nk1,
+        [&](unsigned char* slot, int kt) {
+          la.issue(slot, kt, wave);
+          lb.issue(slot + S::kAChunks * 16, kt, wave);
+        },
+        acc, lane, wave, hook);
+    // ts = fp16(scaling t) into LDS for the adapter term; t itself, which the backward keeps, to
+    // t_out from the segment's first column tile (lane: rank lane % 16, rows 4 (lane / 16) + v)
+    uint16_t* tsl = reinterpret_cast<uint16_t*>(smem + kTsOff);
+    if (g >= 0) {
+      const float sg = g1 ? a.scaling[1] : a.scaling[0];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int r = 16 * wave + 4 * (lane >> 4) + v;
+        tsl[r * kTsLd + (lane & 15)] = f2h(sg * hook.t[v]);
+        if (n0 == sb && m0 + r < a.n_tokens)
+          a.t_out[static_cast<int64_t>(m0 + r) * a.ldt_out + kRank * g + (lane & 15)] = f2h(hook.t[v]);
+      }
+    }
+    __syncthreads();  // every wavefront's ts rows are in LDS
+    if (g >= 0) {
+      const half8_t tsa = *reinterpret_cast<const half8_t*>(&tsl[(wm * S::kWaveM + (lane & 31)) * kTsLd + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int j = 0; j < S::kFragN; ++j)
+        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(tsa, bfr[j], acc[0][j], 0, 0, 0);
+    }
+  }
 
   // Epilogue: + bias, fp16, staged in LDS ([kBM][kQZS] halfs)
   uint16_t* Zs = reinterpret_cast<uint16_t*>(smem);
@@ -621,7 +746,15 @@ void launch_proj(QkvArgs& a, hipStream_t stream) {
   using S = QkvShape;
   a.n_mtiles = (a.n_tokens + S::kBM - 1) / S::kBM;
   a.n_ntiles = (a.n_out + S::kBN - 1) / S::kBN;
-  hipLaunchKernelGGL(proj_ext_kernel, dim3(static_cast<unsigned>(a.n_mtiles * a.n_ntiles)),
+  hipLaunchKernelGGL(proj_ext_kernel<false>, dim3(static_cast<unsigned>(a.n_mtiles * a.n_ntiles)),
+                     dim3(S::kThreads), 0, stream, a);
+}
+
+void launch_proj_down(QkvArgs& a, hipStream_t stream) {
+  using S = QkvShape;
+  a.n_mtiles = (a.n_tokens + S::kBM - 1) / S::kBM;
+  a.n_ntiles = (a.n_out + S::kBN - 1) / S::kBN;
+  hipLaunchKernelGGL(proj_ext_kernel<true>, dim3(static_cast<unsigned>(a.n_mtiles * a.n_ntiles)),
                      dim3(S::kThreads), 0, stream, a);
 }
 
@@ -678,6 +811,64 @@ TALM_API int talm_qkv_lora_fwd(const uint16_t* x, int64_t ldx, int64_t n_tokens,
   a.out = out; a.ldo = ldo;
   launch_proj(a, as_stream(stream));
   return check_launch("qkv_lora_fwd");
+}
+
+TALM_API int talm_qkv_lora_fwd_down(const uint16_t* x, int64_t ldx, int64_t n_tokens,
+                                    int64_t hidden, const uint16_t* weight, int64_t ldw,
+                                    int64_t n_out, const uint16_t* bias, int32_t n_adapters,
+                                    const uint16_t* a0, const uint16_t* a1, int64_t lda,
+                                    float scaling0, float scaling1, const uint16_t* b0,
+                                    int64_t seg0_begin, int64_t seg0_end, const uint16_t* b1,
+                                    int64_t seg1_begin, int64_t seg1_end, const float* cos,
+                                    const float* sin, int64_t cs_stride, int64_t rope_cols,
+                                    uint16_t* t, int64_t ldt, uint16_t* out, int64_t ldo,
+                                    void* stream) {
+  using S = QkvShape;
+  if (check_proj("qkv_lora_fwd_down", ldx, n_tokens, hidden, ldw, n_out, ldo)) return TALM_EINVAL;
+  if (n_adapters < 0 || n_adapters > kMaxAdapters)
+    return fail(TALM_EINVAL, "qkv_lora_fwd_down: %d adapters (0-2)", n_adapters);
+  const int64_t begins[2] = {seg0_begin, seg1_begin}, ends[2] = {seg0_end, seg1_end};
+  for (int g = 0; g < n_adapters; ++g)
+    if (begins[g] < 0 || ends[g] <= begins[g] || ends[g] > n_out || begins[g] % S::kBN ||
+        (ends[g] % S::kBN && ends[g] != n_out))
+      return fail(TALM_EINVAL,
+                  "qkv_lora_fwd_down: adapter %d columns [%lld, %lld) must be whole %d-column "
+                  "tiles of [0, %lld)",
+                  g, (long long)begins[g], (long long)ends[g], S::kBN, (long long)n_out);
+  if (n_adapters > 1 && ends[0] > begins[1] && ends[1] > begins[0])
+    return fail(TALM_EINVAL, "qkv_lora_fwd_down: the adapters' columns overlap");
+  if (n_adapters > 0 && (ldt < kRank * n_adapters || lda < hidden || lda % 8 || !fits32(16, lda)))
+    return fail(TALM_EINVAL, "qkv_lora_fwd_down: ldt %lld < %d or A row stride %lld",
+                (long long)ldt, kRank * n_adapters, (long long)lda);
+  if (cos && (rope_cols < 0 || rope_cols % 128 || rope_cols > n_out || cs_stride < 128))
+    return fail(TALM_EINVAL,
+                "qkv_lora_fwd_down: rotary columns %lld must be whole 128-column heads of the "
+                "output (cos/sin row stride %lld >= 128)",
+                (long long)rope_cols, (long long)cs_stride);
+  if (n_tokens == 0) return ok();
+  if (!x || !weight || !out || (n_adapters > 0 && (!a0 || !b0 || !t)) ||
+      (n_adapters > 1 && (!a1 || !b1)) || (cos && !sin))
+    return fail(TALM_EINVAL, "qkv_lora_fwd_down: null pointer");
+  if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(out, 16) || (a0 && !aligned(a0, 16)) ||
+      (a1 && !aligned(a1, 16)) || (b0 && !aligned(b0, 16)) || (b1 && !aligned(b1, 16)))
+    return fail(TALM_EINVAL, "qkv_lora_fwd_down: x, weight, out, A and B must be 16-byte aligned");
+  QkvArgs a{};
+  a.x = x; a.ldx = ldx; a.n_tokens = static_cast<int>(n_tokens); a.hidden = static_cast<int>(hidden);
+  a.w = weight; a.ldw = ldw; a.n_out = static_cast<int>(n_out); a.bias = bias;
+  a.n_segs = n_adapters;
+  a.b[0] = b0; a.b[1] = b1;
+  for (int g = 0; g < 2; ++g) {
+    a.ldb[g] = kRank;
+    a.seg_begin[g] = static_cast<int>(begins[g]);
+    a.seg_end[g] = static_cast<int>(ends[g]);
+  }
+  a.adown[0] = a0; a.adown[1] = a1; a.lda = lda;
+  a.scaling[0] = scaling0; a.scaling[1] = scaling1;
+  a.t_out = t; a.ldt_out = ldt;
+  a.cos = cos; a.sin = sin; a.cs_stride = cs_stride; a.rope_cols = static_cast<int>(rope_cols);
+  a.out = out; a.ldo = ldo;
+  launch_proj_down(a, as_stream(stream));
+  return check_launch("qkv_lora_fwd_down");
 }
 
 TALM_API int talm_qkv_bwd_prep(const uint16_t* dq, int64_t ldq, const uint16_t* dk, int64_t ldk,

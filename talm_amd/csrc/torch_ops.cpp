@@ -426,6 +426,59 @@ void qkv_lora_fwd(const Tensor& x, const Tensor& weight, const OptTensor& bias,
         "qkv_lora_fwd");
 }
 
+// qkv_lora_fwd with the adapters' t = x A_g^T computed inside the same GEMM: A_g fp16 [16, H]
+// contiguous, t [N, 16 * adapters] written for the backward.
+void qkv_lora_fwd_down(const Tensor& x, const Tensor& weight, const OptTensor& bias,
+                       const OptTensor& a0, const OptTensor& a1, double scaling0, double scaling1,
+                       const OptTensor& b0, int64_t seg0_begin, int64_t seg0_end,
+                       const OptTensor& b1, int64_t seg1_begin, int64_t seg1_end,
+                       const OptTensor& cos, const OptTensor& sin, int64_t rope_cols,
+                       const OptTensor& t, const Tensor& out) {
+  require_fp16(x, "x");
+  require_fp16(weight, "weight");
+  require_fp16(out, "out");
+  require(x.dim() == 2 && weight.dim() == 2,
+          "qkv_lora_fwd_down: x [N, H], weight [n_out, H], out [N, n_out], unit column strides");
+  const int64_t n = x.size(0), size = x.size(1), n_out = weight.size(0);
+  require(x.stride(1) == 1 && weight.stride(1) == 1 && out.dim() == 2 && out.stride(1) == 1 &&
+              weight.size(1) == size && same_shape(out, n, n_out),
+          "qkv_lora_fwd_down: x [N, H], weight [n_out, H], out [N, n_out], unit column strides");
+  if (bias.has_value()) {
+    require_fp16(*bias, "bias");
+    require(bias->is_contiguous() && bias->numel() == n_out, "qkv_lora_fwd_down: bias [n_out]");
+  }
+  int n_adapters = 0;
+  const OptTensor* as_[2] = {&a0, &a1};
+  const OptTensor* bs_[2] = {&b0, &b1};
+  for (int g = 0; g < 2; ++g) {
+    if (!bs_[g]->has_value()) continue;
+    require(g == n_adapters && as_[g]->has_value(),
+            "qkv_lora_fwd_down: adapters in order, each with its A and B");
+    ++n_adapters;
+    require_fp16(**bs_[g], "lora B");
+    require((*bs_[g])->is_contiguous() && (*bs_[g])->dim() == 2 && (*bs_[g])->size(1) == 16,
+            "qkv_lora_fwd_down: B [segment, 16]");
+    require_fp16(**as_[g], "lora A");
+    require((*as_[g])->is_contiguous() && same_shape(**as_[g], 16, size),
+            "qkv_lora_fwd_down: A [16, H] contiguous");
+  }
+  if (n_adapters) {
+    TORCH_CHECK_VALUE(t.has_value(), "t must be a CUDA float16 tensor");
+    require_fp16(*t, "t");
+    require(t->dim() == 2 && t->stride(1) == 1 && t->size(0) == n && t->size(1) >= 16 * n_adapters,
+            "qkv_lora_fwd_down: t [N, 16 * adapters]");
+  }
+  cos_sin_rows(cos, sin, n, "qkv_lora_fwd_down: cos/sin fp32 [N, >= 128] with one row stride");
+  check(talm_qkv_lora_fwd_down(
+            as<uint16_t>(x), x.stride(0), n, size, as<uint16_t>(weight), weight.stride(0), n_out,
+            as<uint16_t>(bias), n_adapters, as<uint16_t>(a0), as<uint16_t>(a1), size,
+            static_cast<float>(scaling0), static_cast<float>(scaling1), as<uint16_t>(b0),
+            seg0_begin, seg0_end, as<uint16_t>(b1), seg1_begin, seg1_end, as<float>(cos),
+            as<float>(sin), cos.has_value() ? cos->stride(0) : 0, rope_cols, as<uint16_t>(t),
+            t.has_value() ? t->stride(0) : 0, as<uint16_t>(out), out.stride(0), stream_of(x)),
+        "qkv_lora_fwd_down");
+}
+
 // dcat [N, q + k + v] = [rope_back(dq) | rope_back(dk) | dv] (cos/sin fp32 [N, >= 128], or None
 // for no rotation); every operand fp16 with unit column stride.
 void qkv_bwd_prep(const Tensor& dq, const Tensor& dk, const Tensor& dv, const OptTensor& cos,
@@ -1401,6 +1454,10 @@ TORCH_LIBRARY(talm, m) {
   m.def("qkv_lora_fwd(Tensor x, Tensor weight, Tensor? bias, Tensor? ts, Tensor? b0, "
         "int seg0_begin, int seg0_end, Tensor? b1, int seg1_begin, int seg1_end, Tensor? cos, "
         "Tensor? sin, int rope_cols, Tensor(a!) out) -> ()");
+  m.def("qkv_lora_fwd_down(Tensor x, Tensor weight, Tensor? bias, Tensor? a0, Tensor? a1, "
+        "float scaling0, float scaling1, Tensor? b0, int seg0_begin, int seg0_end, Tensor? b1, "
+        "int seg1_begin, int seg1_end, Tensor? cos, Tensor? sin, int rope_cols, Tensor(a!)? t, "
+        "Tensor(b!) out) -> ()");
   m.def("qkv_bwd_prep(Tensor dq, Tensor dk, Tensor dv, Tensor? cos, Tensor? sin, "
         "Tensor(a!) dcat) -> ()");
   m.def("qkv_lora_bwd_dx(Tensor dcat, Tensor weight_t, Tensor? u, Tensor? a_t, "
@@ -1472,6 +1529,7 @@ TORCH_LIBRARY_IMPL(talm, CUDA, m) {
   m.impl("head_ce", &head_ce);
   m.impl("lora_down", &lora_down);
   m.impl("qkv_lora_fwd", &qkv_lora_fwd);
+  m.impl("qkv_lora_fwd_down", &qkv_lora_fwd_down);
   m.impl("qkv_bwd_prep", &qkv_bwd_prep);
   m.impl("qkv_lora_bwd_dx", &qkv_lora_bwd_dx);
   m.impl("lora_wgrad", &lora_wgrad);

@@ -7,10 +7,12 @@ added with PEFT's ops in PEFT's order (lora.py), v is returned as a fresh tensor
 views. Backward: dX = [dq|dk|dv] [Wq; Wk; Wv] in one GEMM (K = 2048) plus the adapters' input
 gradients, and the adapters' weight gradients.
 
-On MI355X the forward runs as two launches when it can (`_mfma_ok`): talm_lora_down (t = x A^T
-of both adapters) and talm_qkv_lora_fwd, one fp16 MFMA GEMM [x | s t] [W | B]^T + b that also
-rotates q and k in its epilogue (qkv.hip); otherwise the ops below. SOLUTION_DISABLE_QKV_MFMA=1
-keeps the ops.
+On MI355X the forward runs as one launch when it can (`_mfma_ok`): talm_qkv_lora_fwd_down, an
+fp16 MFMA GEMM x W^T + b whose adapter tiles also accumulate t = x A^T during the product and add
+s t B^T after it, and which rotates q and k in its epilogue (qkv.hip); with
+SOLUTION_QKV_SEPARATE_DOWN=1 the two launches it replaces, talm_lora_down (t) and
+talm_qkv_lora_fwd ([x | s t] [W | B]^T + b); otherwise the ops below.
+SOLUTION_DISABLE_QKV_MFMA=1 keeps the ops.
 
 MI355X addition: with `rope=(cos, sin)` the node also applies the rotary embedding to q and k IN
 PLACE on its own output (the rope kernel reads each rotation pair before writing it), and in the
@@ -32,6 +34,7 @@ from .state import DISABLED, fallback
 
 Q, K, V, O, GATE, UP, DOWN = range(7)
 QKV_MFMA = os.environ.get("SOLUTION_DISABLE_QKV_MFMA") != "1"
+QKV_FUSED_DOWN = os.environ.get("SOLUTION_QKV_SEPARATE_DOWN") != "1"
 COUNTS = {"attn": 0, "attn_fallback": 0}
 
 # Adapter weight gradients written straight into buffers that a caller owns (the graphed step):
@@ -292,21 +295,29 @@ def _mfma_forward(x2, weight, bias, bounds, adapters, halves, rope):
     adapters' t = x A^T ([N, 16 per adapter], what the backward keeps)."""
     n, n_out = x2.shape[0], bounds[-1]
     t = ts = None
+    a1 = halves[1][0] if len(adapters) > 1 else None
+    s1 = adapters[1][1] if len(adapters) > 1 else 0.0
     if adapters:
         t = torch.empty(n, 16 * len(adapters), dtype=torch.float16, device=x2.device)
-        ts = torch.empty_like(t)
-        a1 = halves[1][0] if len(adapters) > 1 else None
-        s1 = adapters[1][1] if len(adapters) > 1 else 0.0
-        size = x2.shape[1]
-        torch.ops.talm.lora_down(x2, halves[0][0], a1, size, size, 0, 0, 0, adapters[0][1], s1,
-                                 t, ts)
     segs = [(bounds[seg], bounds[seg + 1]) for seg, _s, _p in adapters] + [(0, 0)] * 2
     bs = [b16 for _a, b16 in halves] + [None] * 2
     cos, sin = rope if rope is not None else (None, None)
     out = torch.empty(n, n_out, dtype=torch.float16, device=x2.device)
+    rope_cols = bounds[2] if rope is not None else 0
+    if QKV_FUSED_DOWN:
+        a0 = halves[0][0] if adapters else None
+        s0 = adapters[0][1] if adapters else 0.0
+        torch.ops.talm.qkv_lora_fwd_down(x2, weight, bias, a0, a1, s0, s1, bs[0], segs[0][0],
+                                         segs[0][1], bs[1], segs[1][0], segs[1][1], cos, sin,
+                                         rope_cols, t, out)
+        return out, t
+    if adapters:
+        ts = torch.empty_like(t)
+        size = x2.shape[1]
+        torch.ops.talm.lora_down(x2, halves[0][0], a1, size, size, 0, 0, 0, adapters[0][1], s1,
+                                 t, ts)
     torch.ops.talm.qkv_lora_fwd(x2, weight, bias, ts, bs[0], segs[0][0], segs[0][1], bs[1],
-                                segs[1][0], segs[1][1], cos, sin,
-                                bounds[2] if rope is not None else 0, out)
+                                segs[1][0], segs[1][1], cos, sin, rope_cols, out)
     return out, t
 
 

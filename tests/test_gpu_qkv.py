@@ -110,6 +110,59 @@ def test_qkv_lora_fwd_matches_fp32(n, size, n_out, segs, rope_cols, with_bias):
     assert torch.all(err <= 2e-3 * ref.abs() + 2e-3 * scale), float(err.max())
 
 
+@pytest.mark.parametrize("n,size,n_out,segs,rope_cols,with_bias", [
+    (1130, 1536, 2048, [(0, 1536), (1792, 2048)], 1792, True),   # Qwen2.5-1.5B q|k|v
+    (1312, 1536, 2048, [(0, 1536), (1792, 2048)], 1792, True),   # a config-5 token count
+    (1130, 1536, 2048, [], 1792, True),                          # no adapters
+    (257, 512, 1024, [(0, 512), (768, 1024)], 768, False),       # test_gpu_step's layer, no bias
+    (37, 256, 1000, [(0, 256), (896, 1000)], 0, True),           # ragged n_out, no rotation
+    (1, 64, 384, [(128, 256)], 256, True),                       # one token, one adapter
+    (65, 96, 256, [(128, 256), (0, 128)], 128, True),            # H not a multiple of 64
+])
+def test_qkv_lora_fwd_down_matches_fp32(n, size, n_out, segs, rope_cols, with_bias):
+    """The one-launch forward (talm_qkv_lora_fwd_down): t = x A^T from the tiles' own product
+    within one fp16 rounding of the fp32 sum, and the projection against the same fp32 reference
+    as the two-launch forward."""
+    _case(f"qkv_lora_fwd_down n={n} H={size} n_out={n_out} segs={segs} rope={rope_cols}")
+    x, w, bias, a, b = _inputs(n, size, n_out, segs, seed=n + n_out + 7)
+    bias = bias if with_bias else None
+    scalings = [2.0, 0.75]
+    t = torch.full((n, 16 * len(segs)), float("nan"), dtype=torch.float16,
+                   device=DEV) if segs else None
+    cos, sin = _rope_tables(n) if rope_cols else (None, None)
+    out = torch.empty(n, n_out, dtype=torch.float16, device=DEV)
+    pad = segs + [(0, 0)] * 2
+    bs = b + [None] * 2
+    as_ = a + [None] * 2
+    torch.ops.talm.qkv_lora_fwd_down(x, w, bias, as_[0], as_[1], scalings[0], scalings[1], bs[0],
+                                     pad[0][0], pad[0][1], bs[1], pad[1][0], pad[1][1], cos, sin,
+                                     rope_cols, t, out)
+    ref = x.float() @ w.float().t()
+    if bias is not None:
+        ref += bias.float()
+    for g, (lo, hi) in enumerate(segs):
+        t_ref = x.float() @ a[g].float().t()
+        tg = t[:, 16 * g:16 * (g + 1)].float()
+        assert torch.all((tg - t_ref).abs() <= 2.0 ** -10 * t_ref.abs() + 1e-6 * size), g
+        ref[:, lo:hi] += scalings[g] * (t_ref @ b[g].float().t())
+    ref = ref.half().float()
+    if rope_cols:
+        ref = _rotate(ref, cos, sin, rope_cols)
+    got = out.float()
+    scale = ref.abs().max()
+    err = (got - ref).abs()
+    assert torch.all(err <= 2e-3 * ref.abs() + 2e-3 * scale), float(err.max())
+    if segs:  # the two-launch forward on the same inputs: the same values up to t's rounding
+        t2 = torch.empty(n, 16 * len(segs), dtype=torch.float16, device=DEV)
+        ts2 = torch.empty_like(t2)
+        torch.ops.talm.lora_down(x, a[0], a[1] if len(segs) > 1 else None, size, size, 0, 0, 0,
+                                 scalings[0], scalings[1], t2, ts2)
+        out2 = torch.empty_like(out)
+        torch.ops.talm.qkv_lora_fwd(x, w, bias, ts2, bs[0], pad[0][0], pad[0][1], bs[1],
+                                    pad[1][0], pad[1][1], cos, sin, rope_cols, out2)
+        assert torch.all((out.float() - out2.float()).abs() <= 2e-3 * out2.float().abs() + 1e-3 * scale)
+
+
 def test_qkv_lora_fwd_rejects_misaligned_adapter_columns():
     _case("qkv_lora_fwd rejects")
     x, w, bias, a, b = _inputs(8, 64, 512, [(64, 192)], seed=1)
