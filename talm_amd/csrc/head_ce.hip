@@ -435,14 +435,29 @@ struct MergeArgs {
   int32_t* correct;
 };
 
-__global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (row >= a.n_rows) return;
+// One wavefront per row. With slices of at most 64 tiles (vchunk <= 8192) a lane holds one tile of
+// each slice, and every load the row needs (the group's tiles, the running statistics, the
+// target's logit) is issued before the first reduction: one memory round trip per row instead
+// of two per slice. Wider slices take the tiles in lane-strided loops. Same merges in the same
+// order either way.
+template <bool kOne>
+__device__ __forceinline__ void merge_row(const MergeArgs& a, int row, int lane) {
+  constexpr int kMaxSlices = 8;
+  const int n = a.n_rows;
+  const float4* prow = a.part + static_cast<int64_t>(row) * a.parts_per_row;
+  const int tiles_per_slice = a.vchunk / kTile;
+  float4 p[kMaxSlices];
+  if constexpr (kOne) {
+#pragma unroll
+    for (int c = 0; c < kMaxSlices; ++c) {
+      const int tiles = c < a.n_slices ? (a.slice_cols[c] + kTile - 1) / kTile : 0;
+      p[c] = lane < tiles ? prow[c * tiles_per_slice + lane] : make_float4(-INFINITY, 0.f, 0.f, 0.f);
+    }
+  }
   const int64_t target = a.targets[row];
   const bool labelled = target >= 0;
+  const float zt_new = a.ztarget[row];  // meaningful only when the target is in this group
   float* run = a.run;
-  const int n = a.n_rows;
   float m, s, t, best, zt;
   int bidx;
   if (a.first_slice) {
@@ -451,13 +466,17 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
     m = run[row]; s = run[n + row]; t = run[2 * n + row]; best = run[3 * n + row];
     zt = run[4 * n + row]; bidx = __float_as_int(run[5 * n + row]);
   }
-  for (int c = 0; c < a.n_slices; ++c) {
+  auto slice = [&](int c) {
     const int tiles = (a.slice_cols[c] + kTile - 1) / kTile;
-    const int tile0 = c * (a.vchunk / kTile);
+    const int tile0 = c * tiles_per_slice;
     Stat acc{-INFINITY, 0.f, 0.f, 0x7fffffff};
-    for (int tt = lane; tt < tiles; tt += kWave) {
-      const float4 p = a.part[static_cast<int64_t>(row) * a.parts_per_row + tile0 + tt];
-      acc = merge(acc, Stat{p.x, p.y, p.z, __float_as_int(p.w)});
+    if constexpr (kOne) {
+      if (lane < tiles) acc = merge(acc, Stat{p[c].x, p[c].y, p[c].z, __float_as_int(p[c].w)});
+    } else {
+      for (int tt = lane; tt < tiles; tt += kWave) {
+        const float4 q = prow[tile0 + tt];
+        acc = merge(acc, Stat{q.x, q.y, q.z, __float_as_int(q.w)});
+      }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc = merge(acc, shfl_stat(acc, off));
@@ -474,20 +493,33 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
       bidx = acc.idx;
     }
     const int64_t rel = target - a.slice_col0[c];
-    if (labelled && rel >= 0 && rel < a.slice_cols[c]) zt = a.ztarget[row];
+    if (labelled && rel >= 0 && rel < a.slice_cols[c]) zt = zt_new;
     if (row < a.n_grad) {
       // P_t = fp16(e^{z - m_t}) of each tile becomes the reference's fp16(e^{z - m_c})
       // (solution/fused_head.py:178-182) through e^{m_t - m_c}, applied by head_grad
-      for (int tt = lane; tt < tiles; tt += kWave) {
-        const float mt = a.part[static_cast<int64_t>(row) * a.parts_per_row + tile0 + tt].x;
-        const float f = mt == -INFINITY ? 0.f : __expf(mt - m);
-        a.scale[scale_index(row, tile0 + tt, a.scale_blocks)] = f2h(f);
+      if constexpr (kOne) {
+        if (lane < tiles) {
+          const float mt = p[c].x;
+          a.scale[scale_index(row, tile0 + lane, a.scale_blocks)] = f2h(mt == -INFINITY ? 0.f : __expf(mt - m));
+        }
+      } else {
+        for (int tt = lane; tt < tiles; tt += kWave) {
+          const float mt = prow[tile0 + tt].x;
+          a.scale[scale_index(row, tile0 + tt, a.scale_blocks)] = f2h(mt == -INFINITY ? 0.f : __expf(mt - m));
+        }
       }
     }
     if (lane == 0) {
       a.alpha[static_cast<int64_t>(c) * n + row] =
           (a.first_slice && c == 0) || m_old == -INFINITY ? 0.f : __expf(m_old - m);
     }
+  };
+  if constexpr (kOne) {
+#pragma unroll
+    for (int c = 0; c < kMaxSlices; ++c)
+      if (c < a.n_slices) slice(c);
+  } else {
+    for (int c = 0; c < a.n_slices; ++c) slice(c);
   }
   if (lane != 0) return;
   run[row] = m; run[n + row] = s; run[2 * n + row] = t; run[3 * n + row] = best;
@@ -500,6 +532,14 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
     a.best_idx[row] = bidx;
     a.correct[row] = (labelled && static_cast<int64_t>(bidx) == target) ? 1 : 0;
   }
+}
+
+__global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (row >= a.n_rows) return;
+  if (a.vchunk <= kTile * kWave) merge_row<true>(a, row, lane);
+  else merge_row<false>(a, row, lane);
 }
 
 // ------------------------------------------------------------------------------------------
