@@ -13,16 +13,18 @@
 //                 P_t = fp16(e^{z - m_t}) to the group's buffer (the only copy of the logits
 //                 that reaches global memory).
 //   head_merge    one wavefront per row folds the tiles of each slice, in column order, into the
-//                 running statistics exactly as the reference's per-slice update, recording the
-//                 slice's running max m_c and rescale e^{m_old - m_c}, and for labelled rows the
-//                 per-tile factors fp16(e^{m_t - m_c}); after the last slice it writes token
-//                 loss, entropy, argmax and correctness.
-//   head_grad     Y_c = P_c W_c for every slice of the group side by side, against the
-//                 transposed weight W^T [hidden, vocab] so that both operands are k-contiguous;
-//                 P_c = fp16(P_t e^{m_t - m_c}), the reference's fp16(e^{z - m_c}) up to one
-//                 more fp16 rounding, is formed on the A fragments between LDS and the MFMAs.
-//   head_combine  acc = e^{m_old - m_c} acc + Y_c in slice order (the reference's rescale then
-//                 add), and after the last slice dH = acc / s - W16[target] in fp16.
+//                 running statistics exactly as the reference's per-slice update; for labelled
+//                 rows it writes the per-tile factors fp16(e^{m_t - m_G}) against the running max
+//                 m_G after the group and the accumulator's rescale e^{m_prev - m_G}; after the
+//                 last slice it writes token loss, entropy, argmax and correctness.
+//   head_grad     Y = P W over the group's columns, cut into K parts that fill the chip, against
+//                 the transposed weight W^T [hidden, vocab] so that both operands are
+//                 k-contiguous; P = fp16(P_t e^{m_t - m_G}) is formed on the A fragments between
+//                 LDS and the MFMAs. The reference's per-slice rescales e^{m_old - m_c} of its
+//                 accumulator telescope over a group into e^{m_c - m_G}, so this is its
+//                 accumulator update up to one more fp16 rounding of P.
+//   head_combine  acc = e^{m_prev - m_G} acc + the parts' sum, and after the last group
+//                 dH = acc / s - W16[target] in fp16.
 // The full [N, V] logits never exist: one group of slices (group * vchunk columns) at a time.
 //
 // Both GEMMs run the tile core of mfma_tile.h (v_mfma_f32_32x32x16_f16, operands streamed by
@@ -428,7 +430,7 @@ struct MergeArgs {
   int first_slice;         // this group holds the first slice of the vocabulary
   int last_slice;          // this group holds the last slice
   float* run;              // [6][n_rows]: m, s, t, best, zt, best_idx (as int bits)
-  float* alpha;            // [n_slices][n_rows]: e^{m_old - m} of each slice (0 for the first)
+  float* alpha;            // [n_rows]: e^{m_prev - m_G}, the accumulator's rescale for this group
   float* token_loss;
   float* entropy;
   int32_t* best_idx;
@@ -481,7 +483,6 @@ __device__ __forceinline__ void merge_row(const MergeArgs& a, int row, int lane)
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc = merge(acc, shfl_stat(acc, off));
     // the slice into the running statistics (solution/fused_head.py:136-153)
-    const float m_old = m;
     const float m_new = fmaxf(m, acc.m);
     const float e_old = m == -INFINITY ? 0.f : __expf(m - m_new);
     const float e_new = acc.m == -INFINITY ? 0.f : __expf(acc.m - m_new);
@@ -494,9 +495,25 @@ __device__ __forceinline__ void merge_row(const MergeArgs& a, int row, int lane)
     }
     const int64_t rel = target - a.slice_col0[c];
     if (labelled && rel >= 0 && rel < a.slice_cols[c]) zt = zt_new;
-    if (row < a.n_grad) {
-      // P_t = fp16(e^{z - m_t}) of each tile becomes the reference's fp16(e^{z - m_c})
-      // (solution/fused_head.py:178-182) through e^{m_t - m_c}, applied by head_grad
+  };
+  const float m_prev = m;  // the running maximum before this group
+  if constexpr (kOne) {
+#pragma unroll
+    for (int c = 0; c < kMaxSlices; ++c)
+      if (c < a.n_slices) slice(c);
+  } else {
+    for (int c = 0; c < a.n_slices; ++c) slice(c);
+  }
+  // The reference adds fp16(e^{z - m_c}) W_c into its fp32 accumulator after rescaling it by
+  // e^{m_old - m_c} at every slice (solution/fused_head.py:170-182); the rescales of one group's
+  // slices telescope, so the group's contribution is sum_c e^{m_c - m_G} fp16(e^{z - m_c}) W_c with
+  // m_G the running maximum after the group. Here each tile's P_t = fp16(e^{z - m_t}) is scaled by
+  // fp16(e^{m_t - m_G}) in head_grad (one more fp16 rounding than the reference's P, as before),
+  // so the group's columns form one plain reduction that head_grad may cut anywhere, and
+  // head_combine rescales the accumulator once per group by e^{m_prev - m_G}.
+  auto factors = [&](int c) {
+      const int tiles = (a.slice_cols[c] + kTile - 1) / kTile;
+      const int tile0 = c * tiles_per_slice;
       if constexpr (kOne) {
         if (lane < tiles) {
           const float mt = p[c].x;
@@ -508,19 +525,18 @@ __device__ __forceinline__ void merge_row(const MergeArgs& a, int row, int lane)
           a.scale[scale_index(row, tile0 + tt, a.scale_blocks)] = f2h(mt == -INFINITY ? 0.f : __expf(mt - m));
         }
       }
-    }
-    if (lane == 0) {
-      a.alpha[static_cast<int64_t>(c) * n + row] =
-          (a.first_slice && c == 0) || m_old == -INFINITY ? 0.f : __expf(m_old - m);
-    }
   };
-  if constexpr (kOne) {
+  if (row < a.n_grad) {
+    if constexpr (kOne) {
 #pragma unroll
-    for (int c = 0; c < kMaxSlices; ++c)
-      if (c < a.n_slices) slice(c);
-  } else {
-    for (int c = 0; c < a.n_slices; ++c) slice(c);
+      for (int c = 0; c < kMaxSlices; ++c)
+        if (c < a.n_slices) factors(c);
+    } else {
+      for (int c = 0; c < a.n_slices; ++c) factors(c);
+    }
   }
+  if (lane == 0)
+    a.alpha[row] = a.first_slice || m_prev == -INFINITY ? 0.f : __expf(m_prev - m);
   if (lane != 0) return;
   run[row] = m; run[n + row] = s; run[2 * n + row] = t; run[3 * n + row] = best;
   run[4 * n + row] = zt; run[5 * n + row] = __int_as_float(bidx);
@@ -543,9 +559,12 @@ __global__ __launch_bounds__(kThreads) void head_merge_kernel(MergeArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// GEMM2: Y_c[r][h] = sum_j P_c[r][zc + j] W^T[h][col0 + zc + j] over slice c's columns (zc = c *
-// vchunk inside the group), for the first n_grad rows (the labelled rows, put first by the
-// caller); P_c = fp16(P_t e^{m_t - m_c}) from head_logits' P_t and head_merge's factors.
+// GEMM2: Y_p[r][h] = sum_j P[r][j] W^T[h][col0 + j] over part p of the group's columns (a range of
+// whole 64-column steps; the group's slices lie side by side in P and in W^T), for the first
+// n_grad rows (the labelled rows, put first by the caller); P = fp16(P_t e^{m_t - m_G}) from
+// head_logits' P_t and head_merge's factors. The group's K steps are cut into `parts` equal
+// ranges so that (row tiles x hidden tiles x parts) workgroups fill the chip whatever the
+// number of labelled rows.
 // ------------------------------------------------------------------------------------------
 
 // The A-fragment hook of head_grad: ring step kt covers columns [zc + kt BK, + BK) of one 128-column
@@ -582,12 +601,12 @@ struct GradArgs {
   int col0;               // the group's first vocabulary column
   int n_grad;
   int hidden;
-  int vchunk;
-  int slice_cols[8];
-  int ksplit;             // parts of each slice's columns, each with its own partial
+  int group_cols;         // the group's columns
+  int parts;              // K ranges of the group's columns, each with its own partial
+  int steps_per_part;     // 64-column steps per part (the last part may have fewer or none)
   const uint16_t* scale;  // per-(row, tile) factors of head_merge, see scale_index
   int scale_blocks;
-  float* Y;               // [n_slices * ksplit][n_grad][hidden] fp32
+  float* Y;               // [parts][n_grad][hidden] fp32
   int n_mtiles, n_ntiles, n_tiles;
 };
 
@@ -601,14 +620,11 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
   const int ntile = static_cast<int>(tile % a.n_ntiles);
   const int rest = static_cast<int>(tile / a.n_ntiles);
   const int mtile = rest % a.n_mtiles, piece = rest / a.n_mtiles;
-  const int slice = piece / a.ksplit, kpart = piece % a.ksplit;
   const int m0 = mtile * kBM, n0 = ntile * kBN;
-  const int cols = a.slice_cols[slice];
-  // this part's columns of the slice, in whole steps
-  const int span = (cols + a.ksplit - 1) / a.ksplit;
-  const int per = (span + S::kBK - 1) / S::kBK * S::kBK;
-  const int k0 = min(kpart * per, cols), kn = min(cols - k0, per);
-  const int zc = slice * a.vchunk + k0;
+  // this part's columns of the group, in whole steps (BK divides 128: a step lies in one tile)
+  static_assert(kTile % S::kBK == 0, "a ring step inside one statistics tile");
+  const int per = a.steps_per_part * S::kBK;
+  const int zc = min(piece * per, a.group_cols), kn = min(a.group_cols - zc, per);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
@@ -645,20 +661,20 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
 }
 
 // ------------------------------------------------------------------------------------------
-// acc = e^{m_old - m_c} acc + Y_c in slice order; after the last slice dH = acc / s - W[target].
-// One thread per 4 hidden columns of one row.
+// acc = e^{m_prev - m_G} acc + sum_p Y_p (parts in order); after the last group dH = acc / s -
+// W[target]. One thread per 4 hidden columns of one row.
 // ------------------------------------------------------------------------------------------
 struct CombineArgs {
   float* acc;              // [n_grad][hidden]
-  const float* Y;          // [n_slices * ksplit][n_grad][hidden]: ksplit partials per slice
-  const float* alpha;      // [n_slices][n_rows]
+  const float* Y;          // [parts][n_grad][hidden]
+  const float* alpha;      // [n_rows]: e^{m_prev - m_G}
   const float* run;        // running statistics (s at [n_rows + row])
   const int64_t* targets;
   const uint16_t* W;       // full weight (row = vocabulary column)
   int64_t ldw;
   int64_t vocab;
   uint16_t* grad;          // [n_rows][hidden] fp16 (written after the last slice)
-  int n_rows, n_grad, hidden, n_slices, ksplit, first_slice, last_slice;
+  int n_rows, n_grad, hidden, parts, first_slice, last_slice;
 };
 
 __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
@@ -672,20 +688,16 @@ __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
     return;
   }
   const int64_t at = static_cast<int64_t>(row) * a.hidden + col;
-  float4 v = a.first_slice ? make_float4(0.f, 0.f, 0.f, 0.f) : *reinterpret_cast<const float4*>(a.acc + at);
-  for (int c = 0; c < a.n_slices; ++c) {
-    const float al = a.alpha[static_cast<int64_t>(c) * a.n_rows + row];
-    float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int p = 0; p < a.ksplit; ++p) {
-      const float4 yp = *reinterpret_cast<const float4*>(
-          a.Y + static_cast<int64_t>(c * a.ksplit + p) * a.n_grad * a.hidden + at);
-      y.x += yp.x; y.y += yp.y; y.z += yp.z; y.w += yp.w;
-    }
-    if (a.first_slice && c == 0) {
-      v = y;
-    } else {
-      v.x = v.x * al + y.x; v.y = v.y * al + y.y; v.z = v.z * al + y.z; v.w = v.w * al + y.w;
-    }
+  float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int p = 0; p < a.parts; ++p) {
+    const float4 yp = *reinterpret_cast<const float4*>(a.Y + static_cast<int64_t>(p) * a.n_grad * a.hidden + at);
+    y.x += yp.x; y.y += yp.y; y.z += yp.z; y.w += yp.w;
+  }
+  float4 v = y;
+  if (!a.first_slice) {
+    const float al = a.alpha[row];
+    const float4 o = *reinterpret_cast<const float4*>(a.acc + at);
+    v.x = o.x * al + y.x; v.y = o.y * al + y.y; v.z = o.z * al + y.z; v.w = o.w * al + y.w;
   }
   if (!a.last_slice) {
     *reinterpret_cast<float4*>(a.acc + at) = v;
@@ -748,38 +760,41 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 constexpr int kCus = 256;  // MI355X compute units
 
-// Fraction of the launch's workgroup slots that hold work, over the rounds it takes.
-double fill(int64_t blocks, int per_cu) {
-  const int64_t slots = static_cast<int64_t>(kCus) * per_cu;
-  const int64_t rounds = (blocks + slots - 1) / slots;
-  return rounds ? static_cast<double>(blocks) / static_cast<double>(rounds * slots) : 0.0;
-}
+// The gradient GEMM's output [n_grad, hidden] is small against its reduction (a group's columns):
+// the group's K steps are cut into `parts` ranges, each with its own fp32 partial (summed by
+// head_combine), so that the launch fills the chip. The plan minimizes a time model: rounds of
+// workgroups x steps per part x a step's time (GradWide: 1.7 us per 64-deep step of a 256 x 256
+// tile with every CU busy; GradNarrow, two 256 x 128 workgroups per CU: 1.0 us per 32-deep
+// step, measured), plus each part's partial written and read back at 5 TB/s.
+constexpr double kWideStepUs = 1.7, kNarrowStepUs = 1.0, kPartialBytesPerUs = 5e6;
+constexpr int kMaxParts = 16;
 
-// GradWide moves a third fewer bytes per FLOP (~20% faster per tile); pick it unless the launch
-// fills the chip clearly worse with it.
-constexpr double kWideGain = 1.2;
-
-// The gradient GEMM's output [n_grad, hidden] per slice is small: besides the shape, each slice's
-// columns may be split into `ksplit` parts (each its own fp32 partial, summed by head_combine) so
-// the launch fills the chip. Each extra part costs a little partial traffic.
 struct GradPlan {
   bool wide;
-  int ksplit;
+  int parts;           // parts holding work
+  int steps_per_part;  // ring steps of the shape's depth per part
 };
 
-GradPlan plan_grad(int64_t n_grad, int64_t hidden, int ns) {
+GradPlan plan_grad(int64_t n_grad, int64_t hidden, int64_t group_cols) {
   const int64_t mt = (n_grad + kBM - 1) / kBM;
-  GradPlan best{true, 1};
-  double best_score = -1.0;
+  GradPlan best{true, 1, static_cast<int>((group_cols + GradWide::kBK - 1) / GradWide::kBK)};
+  double best_t = 1e300;
   for (int wide = 1; wide >= 0; --wide) {
     const int bn = wide ? GradWide::kBN : GradNarrow::kBN;
-    for (int ks = 1; ks <= 4; ++ks) {
-      const int64_t blocks = mt * ((hidden + bn - 1) / bn) * ns * ks;
-      const double score = (wide ? kWideGain : 1.0) * (1.0 - 0.03 * (ks - 1)) *
-                           fill(blocks, wide ? GradWide::kPerCu : GradNarrow::kPerCu);
-      if (score > best_score + 1e-9) {
-        best_score = score;
-        best = GradPlan{wide != 0, ks};
+    const int bk = wide ? GradWide::kBK : GradNarrow::kBK;
+    const int per_cu = wide ? GradWide::kPerCu : GradNarrow::kPerCu;
+    const int64_t total = std::max<int64_t>(1, (group_cols + bk - 1) / bk);
+    for (int64_t p = 1; p <= std::min<int64_t>(kMaxParts, total); ++p) {
+      const int64_t steps = (total + p - 1) / p;
+      const int64_t parts = (total + steps - 1) / steps;
+      const int64_t blocks = mt * ((hidden + bn - 1) / bn) * parts;
+      const int64_t slots = static_cast<int64_t>(kCus) * per_cu;
+      const int64_t rounds = (blocks + slots - 1) / slots;
+      const double t = static_cast<double>(rounds * steps) * (wide ? kWideStepUs : kNarrowStepUs) +
+                       static_cast<double>(parts * n_grad * hidden) * 8.0 / kPartialBytesPerUs;
+      if (t < best_t - 1e-9) {
+        best_t = t;
+        best = GradPlan{wide != 0, static_cast<int>(parts), static_cast<int>(steps)};
       }
     }
   }
@@ -798,11 +813,11 @@ Layout layout(int64_t n_rows, int64_t hidden, int64_t vocab, int64_t vchunk, int
   Layout l{};
   l.ldz = align_up(static_cast<size_t>(group * vchunk), 8);
   l.parts_per_row = static_cast<int>(group * vchunk / kTile);
-  // fp32 partials for the largest group: a full one, or the last (narrower) one
+  // fp32 partials for the group with the most parts: a full one, or the last (narrower) one
   const int64_t slices = (vocab + vchunk - 1) / vchunk;
-  const int last = static_cast<int>(slices - (slices - 1) / group * group);
-  const int64_t pieces = n_grad > 0 ? std::max<int64_t>(group * plan_grad(n_grad, hidden, group).ksplit,
-                                                        last * plan_grad(n_grad, hidden, last).ksplit)
+  const int64_t last_cols = vocab - (slices - 1) / group * group * vchunk;
+  const int64_t pieces = n_grad > 0 ? std::max<int64_t>(plan_grad(n_grad, hidden, group * vchunk).parts,
+                                                        plan_grad(n_grad, hidden, last_cols).parts)
                                     : 0;
   l.scale_blocks = static_cast<int>((n_grad + kBM - 1) / kBM * 2);
   size_t off = 0;
@@ -811,7 +826,7 @@ Layout layout(int64_t n_rows, int64_t hidden, int64_t vocab, int64_t vchunk, int
   l.scale = off;  off = align_up(off + static_cast<size_t>(l.parts_per_row) * l.scale_blocks * 128 * 2, 256);
   l.run = off;    off = align_up(off + static_cast<size_t>(n_rows) * 6 * 4, 256);
   l.ztarget = off; off = align_up(off + static_cast<size_t>(n_rows) * 4, 256);
-  l.alpha = off;  off = align_up(off + static_cast<size_t>(group) * n_rows * 4, 256);
+  l.alpha = off;  off = align_up(off + static_cast<size_t>(n_rows) * 4, 256);
   l.y = off;      off = align_up(off + static_cast<size_t>(pieces) * n_grad * hidden * 4, 256);
   l.acc = off;    off = align_up(off + static_cast<size_t>(n_grad) * hidden * 4, 256);
   l.total = off;
@@ -940,16 +955,16 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
       GradArgs ga{};
       ga.Z = Z; ga.ldz = l.ldz; ga.WT = weight_t; ga.ldwt = ldwt; ga.col0 = static_cast<int>(col0);
       ga.n_grad = static_cast<int>(n_grad); ga.hidden = static_cast<int>(hidden);
-      ga.vchunk = static_cast<int>(vchunk);
-      for (int c = 0; c < ns; ++c) ga.slice_cols[c] = ma.slice_cols[c];
+      ga.group_cols = static_cast<int>(gcols);
       ga.scale = scale; ga.scale_blocks = l.scale_blocks;
       ga.Y = Y;
-      const GradPlan gp = plan_grad(n_grad, hidden, ns);
+      const GradPlan gp = plan_grad(n_grad, hidden, gcols);
       const int bn = gp.wide ? GradWide::kBN : GradNarrow::kBN;
-      ga.ksplit = gp.ksplit;
+      ga.parts = gp.parts;
+      ga.steps_per_part = gp.steps_per_part;
       ga.n_mtiles = static_cast<int>((n_grad + kBM - 1) / kBM);
       ga.n_ntiles = static_cast<int>((hidden + bn - 1) / bn);
-      ga.n_tiles = ga.n_mtiles * ga.n_ntiles * ns * gp.ksplit;
+      ga.n_tiles = ga.n_mtiles * ga.n_ntiles * gp.parts;
       if (gp.wide)
         hipLaunchKernelGGL((head_grad_kernel<GradWide>), dim3(static_cast<unsigned>(ga.n_tiles)),
                            dim3(GradWide::kThreads), 0, s, ga);
@@ -960,7 +975,7 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
       ca.acc = accbuf; ca.Y = Y; ca.alpha = alpha; ca.run = run; ca.targets = targets;
       ca.W = weight; ca.ldw = ldw; ca.vocab = vocab; ca.grad = grad_hidden; ca.n_rows = rows;
       ca.n_grad = static_cast<int>(n_grad); ca.hidden = static_cast<int>(hidden);
-      ca.n_slices = ns; ca.ksplit = gp.ksplit;
+      ca.parts = gp.parts;
       ca.first_slice = ma.first_slice; ca.last_slice = ma.last_slice;
       const int64_t work = (ca.last_slice ? n_rows : n_grad) * (hidden / 4);
       hipLaunchKernelGGL(head_combine_kernel, dim3(static_cast<unsigned>((work + kThreads - 1) / kThreads)),

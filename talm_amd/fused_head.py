@@ -11,8 +11,10 @@ saved dH (:280-287).
 On MI355X the whole slice loop is ONE call of talm_head_ce (talm_amd/csrc/head_ce.hip): both
 GEMMs are hand-written fp16 MFMA kernels whose epilogue / prologue do the statistics and the
 e^{z - m} weights, so a slice's logits are written once (fp16) and read once, and the per-slice
-accumulator GEMM, which the reference leaves to cuBLAS, fills the chip by running `GROUP` slices
-side by side (each with its own partial, combined in slice order by the reference's recurrence).
+accumulator GEMM, which the reference leaves to cuBLAS, runs once per group of `GROUP` slices:
+the reference's per-slice rescales of the accumulator telescope over a group, so the group's
+columns form one reduction, cut into as many K parts as fill the chip (fp32 partials summed in
+part order, then one rescale of the accumulator per group).
 
 As in the reference (:25-35, `labelled_first` :290-299), with the gradient on the rows are put
 labelled-first, so the accumulator covers the labelled rows only; the statistics of every row are
