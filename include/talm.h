@@ -225,12 +225,9 @@ int64_t talm_head_ce_workspace(int64_t n_rows, int64_t hidden, int64_t vocab, in
                                int64_t n_grad, int32_t group);
 
 /*
- * The transposed head weight the gradient GEMM of talm_head_ce reads:
- * weight_t[h][v] = weight[v][h] for v < vocab, 0 for vocab <= v < ldwt (row stride ldwt >= vocab,
- * a multiple of 8). The reference has no counterpart: its accumulator GEMM hands cuBLAS the
- * weight slice as is (solution/fused_head.py:178-182); here both GEMM operands are streamed
- * k-contiguous, so the frozen weight's transpose is built once per weight version by the caller
- * (talm_amd.fused_head keeps it) and reused by every call.
+ * A weight's transpose: weight_t[h][v] = weight[v][h] for v < vocab, 0 for vocab <= v < ldwt (row
+ * stride ldwt >= vocab, a multiple of 8); 64 x 64 blocks through LDS. Used for the q|k|v layer's
+ * W^T of talm_qkv_lora_bwd_dx when no transposed dequantization of the layer is at hand.
  */
 int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t vocab, int64_t hidden,
                        uint16_t* weight_t, int64_t ldwt, void* stream);
@@ -246,8 +243,8 @@ int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t vocab, int64
  *   rows: every labelled row must be among them (the caller orders rows labelled-first,
  *   solution/fused_head.py:290-299, or passes n_grad = n_rows); an ignored row among them
  *   costs gradient work and gets a zero gradient.
- *   weight_t: talm_head_weight_t of the same weight (row stride ldwt); required when the
- *   gradient is requested (n_grad > 0 and grad_hidden not NULL), ignored otherwise.
+ *   The gradient GEMM reads the weight's rows as they lie (no transposed copy); with the
+ *   gradient, group * vchunk * ldw * 2 stays below 2^31.
  * Writes per row: token_loss f32 (log s + m - z_target, 0 unlabelled), entropy f32
  * (lse - t / s), best_idx i32 (first argmax of the fp16 logits), correct i32 (labelled and
  * best_idx == target); and, when grad_hidden is not NULL, grad_hidden f16 [n_rows, hidden]
@@ -256,7 +253,7 @@ int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t vocab, int64
  * `workspace` (256-byte aligned) holds talm_head_ce_workspace(...) bytes.
  */
 int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* weight, int64_t ldw,
-                 const uint16_t* weight_t, int64_t ldwt, const int64_t* targets, int64_t n_rows,
+                 const int64_t* targets, int64_t n_rows,
                  int64_t hidden, int64_t vocab, int64_t vchunk, int64_t n_grad, int32_t group,
                  float* token_loss, float* entropy, int32_t* best_idx, int32_t* correct,
                  uint16_t* grad_hidden, void* workspace, int64_t workspace_bytes, void* stream);

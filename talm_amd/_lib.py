@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libtalm.so"
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 TALM_OK, TALM_EINVAL, TALM_EHIP = 0, 1, 2
 TALM_F32, TALM_F16 = 0, 1
@@ -50,7 +50,7 @@ SIGNATURES = {
     "talm_qkv_lora_fwd_down": [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I32, _P, _P, _I64, _F32,
                                _F32, _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64,
                                _P, _I64, _P],
-    "talm_head_ce": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P,
+    "talm_head_ce": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P,
                      _P, _P, _P, _P, _I64, _P],
     "talm_attn_fwd": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I32, _I32, _I64, _I32,
                       _I32, _I32, _F32, _P, _I64, _I64, _P, _P],

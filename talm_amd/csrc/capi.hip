@@ -46,4 +46,4 @@ int device_cus() {
 
 TALM_API const char* talm_last_error(void) { return g_error; }
 
-TALM_API int talm_abi_version(void) { return 19; }
+TALM_API int talm_abi_version(void) { return 20; }

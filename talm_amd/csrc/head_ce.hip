@@ -52,12 +52,11 @@ constexpr int kTile = 128;           // statistics granule (columns)
 using LogitsShape = TileShape<256, 256, 64, 2, 2, 4>;
 static_assert(LogitsShape::kWaveM == 128 && LogitsShape::kFragM == 4,
               "one statistics tile of 4 x 32 rows per wavefront");
-// head_grad: 256 (labelled rows) x BN (hidden) tiles, wavefronts of 64 x 128 (two A fragments,
-// each scaled between LDS and the MFMAs). Narrow runs two 256-thread workgroups per CU with a
-// three-stage ring of 32-deep steps; Wide one 512-thread workgroup that moves a third fewer bytes
-// per FLOP.
-using GradNarrow = TileShape<256, 128, 32, 3, 4, 1>;
-using GradWide = TileShape<256, 256, 64, 2, 4, 2>;
+// head_grad: 256 (labelled rows) x 256 (hidden) tiles, 64-deep steps through a two-slot ring,
+// eight wavefronts of 64 x 128 (two A fragments, each scaled between LDS and the MFMAs). The B
+// operand is the weight's rows as they lie ([64 vocabulary entries][256 hidden columns] per
+// stage), transposed by the fragment reads: no transposed copy of the weight.
+using GradShape = TileShape<256, 256, 64, 2, 4, 2>;
 constexpr int kBM = 256;
 
 struct Stat {
@@ -596,8 +595,9 @@ struct TileScale {
 struct GradArgs {
   const uint16_t* Z;
   int64_t ldz;
-  const uint16_t* WT;     // transposed weight [hidden][ldwt], columns past the vocabulary zero
-  int64_t ldwt;
+  const uint16_t* W;      // the weight [vocab][ldw]: the B operand's rows as they lie (nn stages)
+  int64_t ldw;
+  int vocab;
   int col0;               // the group's first vocabulary column
   int n_grad;
   int hidden;
@@ -630,20 +630,22 @@ __global__ __launch_bounds__(S::kThreads, S::kPerCu) void head_grad_kernel(GradA
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 
   Loader<S, kBM> la;
-  Loader<S, kBN> lb;
+  LoaderNN<S> lb;
   la.init(a.Z + static_cast<int64_t>(m0) * a.ldz + zc, a.ldz, a.n_grad - m0, kn, wave, lane);
-  lb.init(a.WT + static_cast<int64_t>(n0) * a.ldwt + a.col0 + zc, a.ldwt, a.hidden - n0, kn,
-          wave, lane);
+  // W's rows col0 + zc .. (the part's vocabulary entries, none past the vocabulary), columns
+  // n0 .. n0 + 255 of the hidden dimension, transposed by the fragment reads
+  lb.init(a.W + static_cast<int64_t>(a.col0 + zc) * a.ldw + n0, a.ldw,
+          min(kn, a.vocab - a.col0 - zc), a.hidden - n0, wave, lane);
   TileScale<S::kBK, S::kFragM, S::kStages> sc;
   sc.base = a.scale + scale_index(m0 + wm * S::kWaveM + (lane & 31), 0, a.scale_blocks);
   sc.tile_stride = static_cast<int64_t>(a.scale_blocks) * 128;
   sc.zc = kn > 0 ? zc : 0;  // an empty part (zc may be the group's end) still loads in range
   Acc<S> acc;
-  ring_gemm<S>(
+  ring_gemm<S, true>(
       smem, (kn + S::kBK - 1) / S::kBK,
       [&](unsigned char* slot, int kt) {
         la.issue(slot, kt * S::kBK, wave);
-        lb.issue(slot + S::kAChunks * 16, kt * S::kBK, wave);
+        lb.issue(slot + S::kAChunks * 16, kt, wave);
       },
       acc, lane, wave, sc);
 
@@ -719,8 +721,8 @@ __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// WT[h][v] = W[v][h] for v < vocab, 0 for vocab <= v < ldwt: the k-contiguous B operand of
-// head_grad. 64 x 64 blocks through LDS, 16-byte loads and stores.
+// WT[h][v] = W[v][h] for v < vocab, 0 for vocab <= v < ldwt (talm_head_weight_t). 64 x 64 blocks
+// through LDS, 16-byte loads and stores.
 // ------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void weight_t_kernel(const uint16_t* __restrict__ W,
                                                             int64_t ldw, int vocab, int hidden,
@@ -763,39 +765,31 @@ constexpr int kCus = 256;  // MI355X compute units
 // The gradient GEMM's output [n_grad, hidden] is small against its reduction (a group's columns):
 // the group's K steps are cut into `parts` ranges, each with its own fp32 partial (summed by
 // head_combine), so that the launch fills the chip. The plan minimizes a time model: rounds of
-// workgroups x steps per part x a step's time (GradWide: 1.7 us per 64-deep step of a 256 x 256
-// tile with every CU busy; GradNarrow, two 256 x 128 workgroups per CU: 1.0 us per 32-deep
-// step, measured), plus each part's partial written and read back at 5 TB/s.
-constexpr double kWideStepUs = 1.7, kNarrowStepUs = 1.0, kPartialBytesPerUs = 5e6;
+// workgroups x steps per part x a 64-deep step's time with every CU busy (1.7 us, measured),
+// plus each part's partial written and read back at 5 TB/s.
+constexpr double kStepUs = 1.7, kPartialBytesPerUs = 5e6;
 constexpr int kMaxParts = 16;
 
 struct GradPlan {
-  bool wide;
   int parts;           // parts holding work
-  int steps_per_part;  // ring steps of the shape's depth per part
+  int steps_per_part;  // 64-deep ring steps per part
 };
 
 GradPlan plan_grad(int64_t n_grad, int64_t hidden, int64_t group_cols) {
-  const int64_t mt = (n_grad + kBM - 1) / kBM;
-  GradPlan best{true, 1, static_cast<int>((group_cols + GradWide::kBK - 1) / GradWide::kBK)};
+  using S = GradShape;
+  const int64_t tiles = (n_grad + S::kBM - 1) / S::kBM * ((hidden + S::kBN - 1) / S::kBN);
+  const int64_t total = std::max<int64_t>(1, (group_cols + S::kBK - 1) / S::kBK);
+  GradPlan best{1, static_cast<int>(total)};
   double best_t = 1e300;
-  for (int wide = 1; wide >= 0; --wide) {
-    const int bn = wide ? GradWide::kBN : GradNarrow::kBN;
-    const int bk = wide ? GradWide::kBK : GradNarrow::kBK;
-    const int per_cu = wide ? GradWide::kPerCu : GradNarrow::kPerCu;
-    const int64_t total = std::max<int64_t>(1, (group_cols + bk - 1) / bk);
-    for (int64_t p = 1; p <= std::min<int64_t>(kMaxParts, total); ++p) {
-      const int64_t steps = (total + p - 1) / p;
-      const int64_t parts = (total + steps - 1) / steps;
-      const int64_t blocks = mt * ((hidden + bn - 1) / bn) * parts;
-      const int64_t slots = static_cast<int64_t>(kCus) * per_cu;
-      const int64_t rounds = (blocks + slots - 1) / slots;
-      const double t = static_cast<double>(rounds * steps) * (wide ? kWideStepUs : kNarrowStepUs) +
-                       static_cast<double>(parts * n_grad * hidden) * 8.0 / kPartialBytesPerUs;
-      if (t < best_t - 1e-9) {
-        best_t = t;
-        best = GradPlan{wide != 0, static_cast<int>(parts), static_cast<int>(steps)};
-      }
+  for (int64_t p = 1; p <= std::min<int64_t>(kMaxParts, total); ++p) {
+    const int64_t steps = (total + p - 1) / p;
+    const int64_t parts = (total + steps - 1) / steps;
+    const int64_t rounds = (tiles * parts + kCus - 1) / kCus;
+    const double t = static_cast<double>(rounds * steps) * kStepUs +
+                     static_cast<double>(parts * n_grad * hidden) * 8.0 / kPartialBytesPerUs;
+    if (t < best_t - 1e-9) {
+      best_t = t;
+      best = GradPlan{static_cast<int>(parts), static_cast<int>(steps)};
     }
   }
   return best;
@@ -866,8 +860,7 @@ TALM_API int talm_head_weight_t(const uint16_t* weight, int64_t ldw, int64_t voc
 }
 
 TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint16_t* weight,
-                          int64_t ldw, const uint16_t* weight_t, int64_t ldwt,
-                          const int64_t* targets, int64_t n_rows, int64_t hidden,
+                          int64_t ldw, const int64_t* targets, int64_t n_rows, int64_t hidden,
                           int64_t vocab, int64_t vchunk, int64_t n_grad, int32_t group,
                           float* token_loss, float* entropy, int32_t* best_idx, int32_t* correct,
                           uint16_t* grad_hidden, void* workspace, int64_t workspace_bytes,
@@ -885,16 +878,13 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
       ldw >= (1 << 22))
     return fail(TALM_EINVAL, "head_ce: sizes beyond 32-bit indexing (row strides below 2^22)");
   const bool with_grad = n_grad > 0 && grad_hidden;
-  if (with_grad && (ldwt < vocab || ldwt % 8 || ldwt >= (1 << 22)))
-    return fail(TALM_EINVAL, "head_ce: weight_t row stride %lld: at least vocab (%lld), a "
-                             "multiple of 8", (long long)ldwt, (long long)vocab);
   if (n_rows == 0) return ok();
   if (!hidden_states || !weight || !targets || !token_loss || !entropy || !best_idx || !correct ||
-      !workspace || (n_grad > 0 && !grad_hidden) || (with_grad && !weight_t))
+      !workspace || (n_grad > 0 && !grad_hidden))
     return fail(TALM_EINVAL, "head_ce: null pointer");
   if (!aligned(hidden_states, 16) || !aligned(weight, 16) || !aligned(workspace, 256) ||
-      (grad_hidden && !aligned(grad_hidden, 16)) || (with_grad && !aligned(weight_t, 16)))
-    return fail(TALM_EINVAL, "head_ce: hidden states, weight, weight_t and dH must be 16-byte "
+      (grad_hidden && !aligned(grad_hidden, 16)))
+    return fail(TALM_EINVAL, "head_ce: hidden states, weight and dH must be 16-byte "
                              "aligned, the workspace 256-byte aligned");
   const int64_t slices = (vocab + vchunk - 1) / vchunk;
   const int g = static_cast<int>(slices < group ? slices : group);
@@ -902,6 +892,9 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
   if (l.ldz >= (1 << 22))
     return fail(TALM_EINVAL, "head_ce: group * vchunk = %lld columns per step, below 2^22 needed",
                 (long long)l.ldz);
+  if (with_grad && static_cast<int64_t>(g) * vchunk * ldw * 2 >= (int64_t{1} << 31))
+    return fail(TALM_EINVAL, "head_ce: a group's weight rows (%lld x %lld halfs) beyond 2^31 bytes",
+                (long long)(g * vchunk), (long long)ldw);
   if (workspace_bytes < static_cast<int64_t>(l.total))
     return fail(TALM_EINVAL, "head_ce: workspace of %lld bytes, %zu needed",
                 (long long)workspace_bytes, l.total);
@@ -953,24 +946,21 @@ TALM_API int talm_head_ce(const uint16_t* hidden_states, int64_t ldh, const uint
                        0, s, ma);
     if (n_grad > 0 && grad_hidden) {
       GradArgs ga{};
-      ga.Z = Z; ga.ldz = l.ldz; ga.WT = weight_t; ga.ldwt = ldwt; ga.col0 = static_cast<int>(col0);
+      ga.Z = Z; ga.ldz = l.ldz; ga.W = weight; ga.ldw = ldw; ga.vocab = static_cast<int>(vocab);
+      ga.col0 = static_cast<int>(col0);
       ga.n_grad = static_cast<int>(n_grad); ga.hidden = static_cast<int>(hidden);
       ga.group_cols = static_cast<int>(gcols);
       ga.scale = scale; ga.scale_blocks = l.scale_blocks;
       ga.Y = Y;
       const GradPlan gp = plan_grad(n_grad, hidden, gcols);
-      const int bn = gp.wide ? GradWide::kBN : GradNarrow::kBN;
+      constexpr int bn = GradShape::kBN;
       ga.parts = gp.parts;
       ga.steps_per_part = gp.steps_per_part;
       ga.n_mtiles = static_cast<int>((n_grad + kBM - 1) / kBM);
       ga.n_ntiles = static_cast<int>((hidden + bn - 1) / bn);
       ga.n_tiles = ga.n_mtiles * ga.n_ntiles * gp.parts;
-      if (gp.wide)
-        hipLaunchKernelGGL((head_grad_kernel<GradWide>), dim3(static_cast<unsigned>(ga.n_tiles)),
-                           dim3(GradWide::kThreads), 0, s, ga);
-      else
-        hipLaunchKernelGGL((head_grad_kernel<GradNarrow>), dim3(static_cast<unsigned>(ga.n_tiles)),
-                           dim3(GradNarrow::kThreads), 0, s, ga);
+      hipLaunchKernelGGL((head_grad_kernel<GradShape>), dim3(static_cast<unsigned>(ga.n_tiles)),
+                         dim3(GradShape::kThreads), 0, s, ga);
       CombineArgs ca{};
       ca.acc = accbuf; ca.Y = Y; ca.alpha = alpha; ca.run = run; ca.targets = targets;
       ca.W = weight; ca.ldw = ldw; ca.vocab = vocab; ca.grad = grad_hidden; ca.n_rows = rows;

@@ -19,6 +19,8 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
 constexpr int kXcds = 8;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every range: the load returns 0
@@ -146,8 +148,82 @@ struct Loader {
   }
 };
 
+// An "nn" B stage: [BK k rows][256 n columns] fp16 (the operand's rows as they lie in memory, n
+// contiguous), 32 chunks of 16 bytes per row, chunk c of row r at position
+// c ^ (4 (r & 3) + (c / 16 + 2 (r & 1)) % 4) (an XOR of the low four bits, so a bijection on each
+// row that keeps bit 4). gfx950's LDS serves 16 lanes of a 16-byte access, or 32 of an 8-byte
+// one, per phase over 64 four-byte banks: 16 chunk positions mod 16. 16-byte stores of two rows
+// (chunks 4 cc + j of cc = 0..7 per phase) and the transposing 8-byte fragment reads (4
+// consecutive rows x 4 adjacent chunks per phase) both meet 16 distinct positions mod 16.
+__device__ __forceinline__ int nn_key(int row, int chunk) {
+  return (((chunk >> 4) + 2 * (row & 1)) & 3) | ((row & 3) << 2);
+}
+__device__ __forceinline__ int nn_pos(int row, int chunk) { return row * 32 + (chunk ^ nn_key(row, chunk)); }
+
+// The B operand of v_mfma_f32_32x32x16_f16 for the 32 columns [col0, col0 + 32) and k-slice ks of
+// an nn stage, read with the transposing ds_read_b64_tr_b16: lane (g = lane / 16, i = lane % 16)
+// points at row 16 ks + 8 (g / 2) + i / 4 (and 4 rows on), columns col .. col + 3 with col =
+// col0 + 16 (g % 2) + 4 (i % 4), and receives k-slots 8 (g / 2) + 0..3 (+ 4..7) of column
+// col0 + lane % 32.
+__device__ __forceinline__ half8_t nn_b_fragment(const unsigned char* Bs, int ks, int col0, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int row = ks * 16 + 8 * (g >> 1) + (i >> 2);
+  const int col = col0 + 16 * (g & 1) + 4 * (i & 3);
+  const unsigned char* p0 = Bs + nn_pos(row, col >> 3) * 16 + (col & 7) * 2;
+  const unsigned char* p1 = Bs + nn_pos(row + 4, col >> 3) * 16 + (col & 7) * 2;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p0));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p1));
+  return __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// An nn operand streamed into nn stages: rows [kt BK, kt BK + BK) of the matrix at `base` (row
+// stride `ld` halfs, n contiguous), its 256 columns from `base` on. A wavefront's 1 KiB DMA block
+// b covers stage positions [64 b, 64 b + 64), i.e. rows 2 b and 2 b + 1, so lane l loads the
+// global chunk that the swizzle puts at position l % 32 of row 2 b + l / 32. Rows at or past
+// `rows_valid` and chunks at or past `cols_valid` columns read as zeros (out-of-range offsets),
+// so the operand may end inside a step. rows_valid * ld * 2 stays below 2^31.
+template <class S>
+struct LoaderNN {
+  static_assert(S::kBN == 256, "32 chunks per stage row");
+  static constexpr int kPer = S::kBK * 32 / S::kThreads;  // DMA instructions per step
+  static_assert(kPer * S::kThreads == S::kBK * 32, "whole 1 KiB blocks per wavefront");
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off[kPer];
+  int row[kPer];
+  int rows_valid;
+  uint32_t step_bytes;
+  __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, int rows_valid_,
+                                       int cols_valid, int wave, int lane) {
+    rsrc = buffer_rsrc(base);
+    rows_valid = rows_valid_;
+    step_bytes = static_cast<uint32_t>(S::kBK * ld * 2);
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int r = 2 * (p * S::kWaves + wave) + lane / 32, pos = lane % 32;
+      const int c = pos ^ nn_key(r, pos);
+      row[p] = r;
+      off[p] = c * 8 < cols_valid ? static_cast<uint32_t>((r * ld + c * 8) * 2) : kOob;
+    }
+  }
+  __device__ __forceinline__ void issue(unsigned char* dst, int kt, int wave) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const uint32_t v = kt * S::kBK + row[p] < rows_valid && off[p] != kOob
+                             ? off[p] + static_cast<uint32_t>(kt) * step_bytes : kOob;
+      dma16(rsrc, dst + (p * S::kWaves + wave) * 1024, v);
+    }
+  }
+};
+
 template <class S>
 using Acc = f32x16[S::kFragM][S::kFragN];
+
+// DMA instructions per thread and step of the B operand, k-contiguous or nn stages.
+template <class S, bool kBnn>
+constexpr int b_dma_per_step() {
+  if constexpr (kBnn) return LoaderNN<S>::kPer;
+  else return Loader<S, S::kBN>::kPer;
+}
 
 // A per-step hook of the ring. The default does nothing; a hook loads step kt's own operands
 // (kLoads vector-memory operations per thread) into its register set `slot` (the step's ring
@@ -165,7 +241,7 @@ struct NoScale {
 };
 
 // One step of the wavefront's block: BK / 16 x (kFragM A + kFragN B fragments, their MFMAs).
-template <class S, class Scale = NoScale>
+template <class S, class Scale = NoScale, bool kBnn = false>
 __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uint4* __restrict__ Bs,
                                          Acc<S>& acc, int lane, int wm, int wn,
                                          const Scale& scale = Scale(), int slot = 0) {
@@ -179,9 +255,13 @@ __device__ __forceinline__ void mma_step(const uint4* __restrict__ As, const uin
       a[ks][i] = scale.apply(__builtin_bit_cast(
           half8_t, As[swz<S::kCpr>(wm * S::kWaveM + i * 32 + (lane & 31), kc)]), i, slot);
 #pragma unroll
-    for (int j = 0; j < S::kFragN; ++j)
-      b[ks][j] = __builtin_bit_cast(
-          half8_t, Bs[swz<S::kCpr>(wn * S::kWaveN + j * 32 + (lane & 31), kc)]);
+    for (int j = 0; j < S::kFragN; ++j) {
+      if constexpr (kBnn)
+        b[ks][j] = nn_b_fragment(reinterpret_cast<const unsigned char*>(Bs), ks, wn * S::kWaveN + j * 32, lane);
+      else
+        b[ks][j] = __builtin_bit_cast(
+            half8_t, Bs[swz<S::kCpr>(wn * S::kWaveN + j * 32 + (lane & 31), kc)]);
+    }
   }
 #pragma unroll
   for (int ks = 0; ks < kSteps; ++ks)
@@ -210,12 +290,13 @@ __device__ __forceinline__ void wait_groups(int later) {
 // nk the loaders read zeros into a retired slot) and the hook's loads (clamped to the last step,
 // step 0 when nk is 0), so every wait counts whole groups. The step loop is unrolled by STAGES: slot indices and LDS
 // offsets are compile-time constants.
-template <class S, class Issue, class Scale = NoScale>
+template <class S, bool kBnn = false, class Issue, class Scale = NoScale>
 __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& issue, Acc<S>& acc,
                                           int lane, int wave, Scale&& scale = Scale()) {
   constexpr int kHookLoads = std::decay_t<Scale>::kLoads;
   constexpr bool kScaled = kHookLoads > 0;
-  constexpr int kGroup = Loader<S, S::kBM>::kPer + Loader<S, S::kBN>::kPer + kHookLoads;
+  constexpr int kBPer = b_dma_per_step<S, kBnn>();
+  constexpr int kGroup = Loader<S, S::kBM>::kPer + kBPer + kHookLoads;
   constexpr int kSt = S::kStages;
   const int wm = wave / S::kWavesN, wn = wave % S::kWavesN;
 #pragma unroll
@@ -244,7 +325,7 @@ __device__ __forceinline__ void ring_gemm(unsigned char* smem, int nk, Issue&& i
       lds_barrier();
       if (kScaled || kt + kSt - 1 < nk) issue_step((i + kSt - 1) % kSt, kt + kSt - 1);
       const unsigned char* st = smem + i * S::kStageBytes;
-      mma_step<S>(reinterpret_cast<const uint4*>(st),
+      mma_step<S, std::decay_t<Scale>, kBnn>(reinterpret_cast<const uint4*>(st),
                   reinterpret_cast<const uint4*>(st + S::kAChunks * 16), acc, lane, wm, wn, scale,
                   i);
       scale.after(st, i, kt);

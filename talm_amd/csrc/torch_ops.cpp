@@ -294,11 +294,9 @@ void head_weight_t(const Tensor& weight, const Tensor& weight_t) {
         "head_weight_t");
 }
 
-// hidden fp16 [N, H] (unit column stride), weight fp16 [V, H] (unit column stride), weight_t its
-// head_weight_t transpose (needed with the gradient), targets int64 [N] with rows [0, n_grad)
-// exactly the labelled ones.
-void head_ce(const Tensor& hidden, const Tensor& weight, const OptTensor& weight_t,
-             const Tensor& targets, int64_t vchunk, int64_t n_grad, int64_t group,
+// hidden fp16 [N, H] (unit column stride), weight fp16 [V, H] (unit column stride), targets
+// int64 [N] with rows [0, n_grad) exactly the labelled ones.
+void head_ce(const Tensor& hidden, const Tensor& weight, const Tensor& targets, int64_t vchunk, int64_t n_grad, int64_t group,
              const Tensor& token_loss, const Tensor& entropy, const Tensor& best_idx,
              const Tensor& correct, const OptTensor& grad_hidden, const Tensor& workspace) {
   require_fp16(hidden, "hidden");
@@ -308,12 +306,6 @@ void head_ce(const Tensor& hidden, const Tensor& weight, const OptTensor& weight
   const int64_t n_rows = hidden.size(0), size = hidden.size(1), vocab = weight.size(0);
   require(hidden.stride(1) == 1 && weight.stride(1) == 1 && weight.size(1) == size,
           "head_ce: hidden [N, H] and weight [V, H] with unit column stride");
-  if (weight_t.has_value()) {
-    require_fp16(*weight_t, "weight_t");
-    require(weight_t->dim() == 2 && weight_t->stride(1) == 1 && weight_t->size(0) == size &&
-                weight_t->size(1) >= vocab,
-            "head_ce: weight_t [H, >= V], unit column stride");
-  }
   require(targets.scalar_type() == at::kLong && targets.is_contiguous() &&
               targets.numel() == n_rows,
           "head_ce: targets int64 [N]");
@@ -328,8 +320,7 @@ void head_ce(const Tensor& hidden, const Tensor& weight, const OptTensor& weight
   }
   require(workspace.is_cuda() && workspace.is_contiguous(), "head_ce: workspace");
   check(talm_head_ce(as<uint16_t>(hidden), hidden.stride(0), as<uint16_t>(weight),
-                     weight.stride(0), as<uint16_t>(weight_t),
-                     weight_t.has_value() ? weight_t->stride(0) : 0, as<int64_t>(targets),
+                     weight.stride(0), as<int64_t>(targets),
                      n_rows, size, vocab, vchunk, n_grad, static_cast<int32_t>(group),
                      as<float>(token_loss), as<float>(entropy), as<int32_t>(best_idx),
                      as<int32_t>(correct), as<uint16_t>(grad_hidden), workspace.data_ptr(),
@@ -1446,7 +1437,7 @@ TORCH_LIBRARY(talm, m) {
   m.def("swiglu_bwd_rows(Tensor grad, Tensor gate, Tensor up, Tensor(a!) dgate, "
         "Tensor(b!) dup) -> ()");
   m.def("head_weight_t(Tensor weight, Tensor(a!) weight_t) -> ()");
-  m.def("head_ce(Tensor hidden, Tensor weight, Tensor? weight_t, Tensor targets, int vchunk, "
+  m.def("head_ce(Tensor hidden, Tensor weight, Tensor targets, int vchunk, "
         "int n_grad, int group, Tensor(a!) token_loss, Tensor(b!) entropy, Tensor(c!) best_idx, "
         "Tensor(d!) correct, Tensor(e!)? grad_hidden, Tensor(f!) workspace) -> ()");
   m.def("lora_down(Tensor x, Tensor a0, Tensor? a1, int k0, int k1, int xcol0, int xcol1, "

@@ -33,8 +33,6 @@ namespace talm {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
 
 using W4Shape = TileShape<256, 256, 64, 2, 2, 4>;
 constexpr int kW4ASlots = 3, kW4BSlots = 2;         // A two steps ahead, B one
@@ -60,17 +58,6 @@ struct W4Args {
   int partial_out;         // fp32 partials even for one part (the caller sums them)
 };
 
-// The "nn" B tile: [64 k rows][256 columns] fp16, 32 chunks of 16 bytes per row, chunk c of row r
-// at position c ^ (4 (r & 3) + (c / 16 + 2 (r & 1)) % 4) (an XOR of the low four bits, so a
-// bijection on each row). gfx950's LDS serves 16 lanes of a 16-byte access, or 32 of an 8-byte
-// one, per phase over 64 four-byte banks: 16 chunk positions mod 16. The dequantization's
-// 16-byte stores (two rows, chunks 4 cc + j of cc = 0..7 per phase) and the transposing 8-byte
-// fragment reads (4 consecutive rows x 4 adjacent chunks per phase) both meet 16 distinct
-// positions mod 16 (the plain c ^ 4 (r & 3) made the stores a 4-way conflict).
-__device__ __forceinline__ int nn_pos(int row, int chunk) {
-  return row * 32 + (chunk ^ ((((chunk >> 4) + 2 * (row & 1)) & 3) | ((row & 3) << 2)));
-}
-
 // One step of the wavefront's 128 x 64 block: per 16-deep slice ks its fragments, its MFMAs, then
 // extra(ks) (the dequantization of the next stage, interleaved so that its VALU work issues
 // while the slice's MFMAs run).
@@ -92,17 +79,7 @@ __device__ __forceinline__ void w4_mma(const uint4* __restrict__ As, const unsig
         b[j] = __builtin_bit_cast(
             half8_t, reinterpret_cast<const uint4*>(Bs)[swz<S::kCpr>(wn * S::kWaveN + j * 32 + (lane & 31), kc)]);
       } else {
-        // lane (g = lane / 16, i = lane % 16) points at row 16 ks + 8 (g / 2) + i / 4 (+ 4),
-        // columns col .. col + 3 with col = the fragment's 16 (g % 2) + 4 (i % 4): it receives
-        // k-slots 8 (g / 2) + 0..3 (+ 4..7) of column n = lane % 32
-        const int g = lane >> 4, i = lane & 15;
-        const int row = ks * 16 + 8 * (g >> 1) + (i >> 2);
-        const int col = wn * S::kWaveN + j * 32 + 16 * (g & 1) + 4 * (i & 3);
-        const unsigned char* p0 = Bs + nn_pos(row, col >> 3) * 16 + (col & 7) * 2;
-        const unsigned char* p1 = Bs + nn_pos(row + 4, col >> 3) * 16 + (col & 7) * 2;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p0));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p1));
-        b[j] = __builtin_bit_cast(half8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        b[j] = nn_b_fragment(Bs, ks, wn * S::kWaveN + j * 32, lane);
       }
     }
 #pragma unroll

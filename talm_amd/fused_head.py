@@ -46,12 +46,11 @@ def _slice_width(vocab_chunk, vocab):
 
 
 def head_ce(h16, w16, targets, vocab_chunk=VOCAB_CHUNK, n_grad=None, need_grad=True,
-            group=GROUP, weight_t=None):
+            group=GROUP):
     """One talm_head_ce call. h16 fp16 [N, H], w16 fp16 [V, H] (unit column strides), targets
     int64 [N]. With `need_grad`, rows [0, n_grad) are the gradient rows: every labelled row must
     be among them (labelled-first order; n_grad defaults to counting them, one host sync), and an
-    ignored row among them gets a zero gradient and `weight_t` is w16's transpose from
-    `head_weights` (built here when not given). Returns per-row token_loss, entropy, best_idx
+    ignored row among them gets a zero gradient. Returns per-row token_loss, entropy, best_idx
     (int32), correct (int32) and grad (fp16 [N, H] or None)."""
     n, size = h16.shape
     vocab = w16.shape[0]
@@ -69,24 +68,11 @@ def head_ce(h16, w16, targets, vocab_chunk=VOCAB_CHUNK, n_grad=None, need_grad=T
     }
     if n == 0:
         return out
-    if need_grad and n_grad > 0 and weight_t is None:
-        weight_t = transpose_weight(w16)
     nbytes = _ops.head_ce_workspace_bytes(n, size, vocab, vchunk, n_grad, group)
     workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    torch.ops.talm.head_ce(h16, w16, weight_t if need_grad else None, targets, vchunk, n_grad,
-                           group, out["token_loss"], out["entropy"], out["best_idx"],
+    torch.ops.talm.head_ce(h16, w16, targets, vchunk, n_grad, group, out["token_loss"], out["entropy"], out["best_idx"],
                            out["correct"], out["grad"], workspace)
     return out
-
-
-def transpose_weight(w16):
-    """w16 fp16 [V, H] -> [H, ldwt] with ldwt = V rounded up to 64 and columns [V, ldwt) zero:
-    the k-contiguous operand of the head's gradient GEMM."""
-    vocab, size = w16.shape
-    ldwt = -(-vocab // 64) * 64
-    wt = torch.empty(size, ldwt, dtype=torch.float16, device=w16.device)
-    torch.ops.talm.head_weight_t(w16, wt)
-    return wt
 
 
 def transpose_weight_exact(w):
@@ -100,24 +86,19 @@ def transpose_weight_exact(w):
 _HEAD_WEIGHTS = {}
 
 
-def head_weights(weight, need_transpose=True):
-    """(w16, w16^T) of the frozen output weight: w16 its fp16 [V, H] view (or one converted copy)
-    and, with `need_transpose`, the transposed copy the gradient GEMM reads (else None). Both are
-    kept for the weight object at its current version (data pointer, version counter, layout) and
-    rebuilt when any of these changes: the tied embedding of the QLoRA model is frozen, so they
-    are built once (the transpose is 2 bytes per weight element of extra HBM)."""
+def head_weights(weight):
+    """w16, the frozen output weight's fp16 [V, H] view (or one converted copy), kept for the
+    weight object at its current version (data pointer, version counter, layout) and rebuilt when
+    any of these changes: the tied embedding of the QLoRA model is frozen, so a converted copy is
+    made once. Both GEMMs of the head read it as it lies (no transposed copy)."""
     w = weight.detach()
     key = (w.data_ptr(), w._version, w.dtype, tuple(w.shape), tuple(w.stride()), str(w.device))
     hit = _HEAD_WEIGHTS.get("head")
     if hit is not None and hit[0]() is weight and hit[1] == key:
-        if hit[3] is not None or not need_transpose:
-            return hit[2], hit[3]
-        w16 = hit[2]
-    else:
-        w16 = _fp16_weight(weight)
-    wt = transpose_weight(w16) if need_transpose else None
-    _HEAD_WEIGHTS["head"] = (weakref.ref(weight), key, w16, wt)
-    return w16, wt
+        return hit[2]
+    w16 = _fp16_weight(weight)
+    _HEAD_WEIGHTS["head"] = (weakref.ref(weight), key, w16)
+    return w16
 
 
 def _denominator(num_items, labelled_count):
@@ -205,7 +186,7 @@ class FusedHeadLossVocab(torch.autograd.Function):
         h16 = hidden.detach().to(torch.float16)
         if h16.stride(1) != 1 or h16.stride(0) % 8 or h16.data_ptr() % 16:
             h16 = h16.contiguous()
-        w16, wt = head_weights(weight, need_transpose=bool(need_grad))
+        w16 = head_weights(weight)
         targets = targets.to(device=hidden.device, dtype=torch.int64).contiguous()
         n_grad, dest, rows_targets = 0, None, targets
         if need_grad and n_tokens > 0:
@@ -219,7 +200,7 @@ class FusedHeadLossVocab(torch.autograd.Function):
                 h16 = h16.index_select(0, src)
                 rows_targets = targets.index_select(0, src)
                 RAN["compact"] += 1
-        out = head_ce(h16, w16, rows_targets, vocab_chunk, n_grad, need_grad, weight_t=wt)
+        out = head_ce(h16, w16, rows_targets, vocab_chunk, n_grad, need_grad)
         RAN["head"] += 1
         token_loss, entropy = out["token_loss"], out["entropy"]
         correct, best_idx, grad_hidden = out["correct"], out["best_idx"], out["grad"]

@@ -56,11 +56,11 @@ def test_argument_rejection_needs_no_gpu():
     assert lib.talm_head_weight_t(None, 64, 100, 64, None, 96, None) == _lib.TALM_EINVAL
     assert b"ldwt" in lib.talm_last_error()
     assert lib.talm_head_weight_t(None, 64, 100, 64, None, 100, None) == _lib.TALM_EINVAL
-    # the gradient needs the transposed weight: a NULL weight_t is rejected before any launch
-    ws, out = 1 << 8, 1 << 12  # fake, aligned addresses: never dereferenced on rejection
-    status = lib.talm_head_ce(out, 64, out, 64, None, 0, out, 4, 64, 1000, 256, 2, 1, out, out,
+    # the head rejects a workspace that is not 256-byte aligned before any launch
+    ws, out = 1 << 4, 1 << 12  # fake addresses: never dereferenced on rejection
+    status = lib.talm_head_ce(out, 64, out, 64, out, 4, 64, 1000, 256, 2, 1, out, out,
                               out, out, out, ws, 1 << 30, None)
-    assert status == _lib.TALM_EINVAL and b"weight_t" in lib.talm_last_error()
+    assert status == _lib.TALM_EINVAL and b"256-byte" in lib.talm_last_error()
 
 
 def test_custom_ops_are_registered_for_the_gpu_only():

@@ -189,17 +189,19 @@ def test_head_config4_full_size_every_row():
 
 
 def test_head_weight_transpose_and_cache():
-    """talm_head_weight_t: exact transpose with zero columns past the vocabulary; the cached
-    transpose is reused for the same weight version and rebuilt after an in-place update."""
+    """talm_head_weight_t: exact transpose with zero columns past the vocabulary. head_weights:
+    the fp16 copy of an fp32 output weight is made once per weight version and rebuilt after an
+    in-place update; an fp16 weight is used as it lies."""
     _case("head weight_t + cache")
     w = torch.randn(1003, 136, device=DEV).half()
-    wt = fused_head.transpose_weight(w)
-    assert tuple(wt.shape) == (136, 1024)
+    wt = torch.empty(136, 1024, dtype=torch.float16, device=DEV)
+    torch.ops.talm.head_weight_t(w, wt)
     assert torch.equal(wt[:, :1003], w.t())
     assert bool(torch.all(wt[:, 1003:] == 0))
-    _, wt_a = fused_head.head_weights(w)
-    _, wt_b = fused_head.head_weights(w)
-    assert wt_a is wt_b
-    w.mul_(2)
-    _, wt_c = fused_head.head_weights(w)
-    assert wt_c is not wt_a and torch.equal(wt_c[:, :1003], w.t())
+    assert fused_head.head_weights(w).data_ptr() == w.data_ptr()
+    w32 = torch.randn(1003, 136, device=DEV)
+    a = fused_head.head_weights(w32)
+    assert fused_head.head_weights(w32) is a and torch.equal(a, w32.half())
+    w32.mul_(2)
+    c = fused_head.head_weights(w32)
+    assert c is not a and torch.equal(c, w32.half())
