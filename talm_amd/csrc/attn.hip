@@ -903,17 +903,40 @@ __global__ __launch_bounds__(64 * W, 1) void attn_bwd_kernel(BwdArgs a) {
 // dK / dV fp16 [token][kv head][d] = sum over the KV head's query heads, in head order. A
 // thread takes 4 columns d and, with the rotary backward (a.cos), also their partners d + 64:
 // dK's pairs are rotated back in fp32 before the rounding.
-__device__ __forceinline__ void sum_heads4(const BwdArgs& a, int kvh, int64_t t, int d,
-                                           float (&k)[4], float (&v)[4]) {
+// dK / dV partials of the KV head's query heads at columns d_c .. d_c + 3 (c < C), summed in head
+// order; every load of eight heads is in flight before their adds.
+template <int C>
+__device__ __forceinline__ void sum_heads4(const BwdArgs& a, int kvh, int64_t t, const int (&d)[C],
+                                           float (&k)[C][4], float (&v)[C][4]) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) k[e] = v[e] = 0.f;
-  for (int g = 0; g < a.group; ++g) {
-    const int h = kvh * a.group + g;
-    const int64_t off = (static_cast<int64_t>(h) * a.n_tokens + t) * kD + d;
-    const float4 xk = *reinterpret_cast<const float4*>(a.dk_part + off);
-    const float4 xv = *reinterpret_cast<const float4*>(a.dv_part + off);
-    k[0] += xk.x; k[1] += xk.y; k[2] += xk.z; k[3] += xk.w;
-    v[0] += xv.x; v[1] += xv.y; v[2] += xv.z; v[3] += xv.w;
+  for (int c = 0; c < C; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) k[c][e] = v[c][e] = 0.f;
+  const int64_t head_stride = a.n_tokens * kD;
+  const int64_t off0 = (static_cast<int64_t>(kvh) * a.group * a.n_tokens + t) * kD;
+  for (int g0 = 0; g0 < a.group; g0 += 8) {
+    float4 xk[8][C], xv[8][C];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int64_t off = off0 + (g0 + j < a.group ? g0 + j : 0) * head_stride + d[c];
+        xk[j][c] = *reinterpret_cast<const float4*>(a.dk_part + off);
+        xv[j][c] = *reinterpret_cast<const float4*>(a.dv_part + off);
+      }
+    // selects, not a branch: a branch between the loads and the adds would let the compiler sink
+    // each load to its add, one round trip per head (heads past the group add +0)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool in = g0 + j < a.group;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        k[c][0] += in ? xk[j][c].x : 0.f; k[c][1] += in ? xk[j][c].y : 0.f;
+        k[c][2] += in ? xk[j][c].z : 0.f; k[c][3] += in ? xk[j][c].w : 0.f;
+        v[c][0] += in ? xv[j][c].x : 0.f; v[c][1] += in ? xv[j][c].y : 0.f;
+        v[c][2] += in ? xv[j][c].z : 0.f; v[c][3] += in ? xv[j][c].w : 0.f;
+      }
+    }
   }
 }
 
@@ -929,11 +952,17 @@ __global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(BwdArgs a) {
   const int64_t t = tk / a.n_kv_heads;
   uint16_t* dk = a.dk + t * a.dk_tok + kvh * a.dk_head;
   uint16_t* dv = a.dv + t * a.dv_tok + kvh * a.dv_head;
-  float k1[4], v1[4];
-  sum_heads4(a, kvh, t, 4 * c4, k1, v1);
+  constexpr int C = kRope ? 2 : 1;  // with the rotary backward: the (d, d + 64) column pairs
+  int d[C];
+  d[0] = 4 * c4;
+  if constexpr (kRope) d[C - 1] = 4 * c4 + kD / 2;
+  float kk[C][4], vv[C][4];
+  sum_heads4<C>(a, kvh, t, d, kk, vv);
+  float(&k1)[4] = kk[0];
+  float(&v1)[4] = vv[0];
   if constexpr (kRope) {
-    float k2[4], v2[4];
-    sum_heads4(a, kvh, t, 4 * c4 + kD / 2, k2, v2);
+    float(&k2)[4] = kk[C - 1];
+    float(&v2)[4] = vv[C - 1];
     rope_back4(k1, k2, a.cos + t * a.cs_tok, a.sin + t * a.cs_tok, 4 * c4);
     *reinterpret_cast<uint2*>(dk + 4 * c4 + kD / 2) = make_uint2(pack2(k2[0], k2[1]), pack2(k2[2], k2[3]));
     *reinterpret_cast<uint2*>(dv + 4 * c4 + kD / 2) = make_uint2(pack2(v2[0], v2[1]), pack2(v2[2], v2[3]));

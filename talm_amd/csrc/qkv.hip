@@ -560,8 +560,19 @@ __global__ __launch_bounds__(256) void lora_wgrad_reduce_kernel(WgradArgs a) {
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (e >= static_cast<int64_t>(a.cols) * 32) return;
   const int c = static_cast<int>(e >> 5), i = static_cast<int>(e & 31);
+  // the chunks in order; eight loads in flight before their adds (one memory round trip per
+  // eight chunks instead of one per chunk; selects, not a branch, so that no load is sunk to its
+  // add; chunks past the last add +0)
+  const float* pc = a.part + static_cast<int64_t>(c) * 32 + i;
+  const int64_t chunk_stride = static_cast<int64_t>(a.cols) * 32;
   float sum = 0.f;
-  for (int k = 0; k < a.chunks; ++k) sum += a.part[(static_cast<int64_t>(k) * a.cols + c) * 32 + i];
+  for (int k0 = 0; k0 < a.chunks; k0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = pc[min(k0 + j, a.chunks - 1) * chunk_stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += k0 + j < a.chunks ? v[j] : 0.f;
+  }
   if (c < a.hidden) {
     const int g = i >> 4;
     if (g < a.n_adapters) (g ? a.da[1] : a.da[0])[static_cast<int64_t>(i & 15) * a.hidden + c] = sum;
@@ -605,12 +616,20 @@ __global__ __launch_bounds__(256) void lora_wgrad_mfma_kernel(WgradArgs a) {
   const int c0 = blockIdx.x * kWmCols;
   const int tid = threadIdx.x;
   const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
-  // the column values: item = (8-column group, token pair); rows past the batch are clamped to
-  // its last row for the load and zeroed
-  for (int it = tid; it < (kWmCols / 8) * kPairs; it += 256) {
-    const int p = it % kPairs, g = it / kPairs;
+  // Every global load of the workgroup is issued before the first LDS store (one memory round
+  // trip): the column values, item = (8-column group, token pair), then u^T and t^T, item =
+  // (which, 8-column group of 32, token pair). Rows past the batch are clamped to its last row
+  // for the load and zeroed; columns of a missing adapter are zero.
+  constexpr int kXItems = (kWmCols / 8) * kPairs / 256;  // 4 per thread
+  constexpr int kMItems = 2 * 4 * kPairs / 256;          // 2 per thread
+  static_assert(kXItems * 256 == (kWmCols / 8) * kPairs && kMItems * 256 == 2 * 4 * kPairs,
+                "whole items per thread");
+  uint4 xa[kXItems], xb[kXItems], ma[kMItems], mb[kMItems];
+#pragma unroll
+  for (int q = 0; q < kXItems; ++q) {
+    const int it = q * 256 + tid, p = it % kPairs, g = it / kPairs;
     const int c = c0 + 8 * g;
-    uint4 va = zero, vb = zero;
+    xa[q] = xb[q] = zero;
     if (c < a.cols) {
       const uint16_t* src;
       int64_t ld;
@@ -623,31 +642,34 @@ __global__ __launch_bounds__(256) void lora_wgrad_mfma_kernel(WgradArgs a) {
         ld = a.ldy;
       }
       const int ra = min(2 * p, rn - 1), rb = min(2 * p + 1, rn - 1);
-      va = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + ra) * ld);
-      vb = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + rb) * ld);
-      if (2 * p >= rn) va = zero;
-      if (2 * p + 1 >= rn) vb = zero;
+      xa[q] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + ra) * ld);
+      xb[q] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + rb) * ld);
     }
-    put_pair_columns(xs, 8 * g, p, va, vb);
   }
-  // u^T and t^T: item = (which, 8-column group of 32, token pair); columns of a missing adapter
-  // are zero
   const bool need_u = c0 < a.hidden, need_t = c0 + kWmCols > a.hidden;
   const int rank = kRank * a.n_adapters;
-  for (int it = tid; it < 2 * 4 * kPairs; it += 256) {
-    const int p = it % kPairs, q = (it / kPairs) % 4, which = it / (4 * kPairs);
-    if (which ? !need_t : !need_u) continue;
-    uint4 va = zero, vb = zero;
-    if (8 * q < rank) {
-      const uint16_t* src = (which ? a.t : a.u) + 8 * q;
+#pragma unroll
+  for (int q = 0; q < kMItems; ++q) {
+    const int it = q * 256 + tid, p = it % kPairs, gq = (it / kPairs) % 4, which = it / (4 * kPairs);
+    ma[q] = mb[q] = zero;
+    if ((which ? need_t : need_u) && 8 * gq < rank) {
+      const uint16_t* src = (which ? a.t : a.u) + 8 * gq;
       const int64_t ld = which ? a.ldt : a.ldu;
       const int ra = min(2 * p, rn - 1), rb = min(2 * p + 1, rn - 1);
-      va = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + ra) * ld);
-      vb = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + rb) * ld);
-      if (2 * p >= rn) va = zero;
-      if (2 * p + 1 >= rn) vb = zero;
+      ma[q] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + ra) * ld);
+      mb[q] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(r0 + rb) * ld);
     }
-    put_pair_columns(ms[which], 8 * q, p, va, vb);
+  }
+#pragma unroll
+  for (int q = 0; q < kXItems; ++q) {
+    const int it = q * 256 + tid, p = it % kPairs, g = it / kPairs;
+    put_pair_columns(xs, 8 * g, p, 2 * p < rn ? xa[q] : zero, 2 * p + 1 < rn ? xb[q] : zero);
+  }
+#pragma unroll
+  for (int q = 0; q < kMItems; ++q) {
+    const int it = q * 256 + tid, p = it % kPairs, gq = (it / kPairs) % 4, which = it / (4 * kPairs);
+    if (which ? !need_t : !need_u) continue;
+    put_pair_columns(ms[which], 8 * gq, p, 2 * p < rn ? ma[q] : zero, 2 * p + 1 < rn ? mb[q] : zero);
   }
   __syncthreads();
   const int wave = tid >> 6, lane = tid & 63;
