@@ -690,23 +690,43 @@ __global__ __launch_bounds__(kThreads) void head_combine_kernel(CombineArgs a) {
     return;
   }
   const int64_t at = static_cast<int64_t>(row) * a.hidden + col;
+  // the row's other inputs are loaded beside the parts (one memory round trip; the weight row
+  // of the target follows)
+  float al = 0.f, s = 1.f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  int64_t tgt = -1;
+  if (!a.first_slice) {
+    al = a.alpha[row];
+    o = *reinterpret_cast<const float4*>(a.acc + at);
+  }
+  if (a.last_slice) {
+    s = a.run[a.n_rows + row];
+    tgt = a.targets[row];
+  }
+  // the parts in order, eight loads in flight before their adds (selects, not a branch, so that
+  // no load is sunk to its add; parts past the last add +0)
+  const int64_t part_stride = static_cast<int64_t>(a.n_grad) * a.hidden;
   float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int p = 0; p < a.parts; ++p) {
-    const float4 yp = *reinterpret_cast<const float4*>(a.Y + static_cast<int64_t>(p) * a.n_grad * a.hidden + at);
-    y.x += yp.x; y.y += yp.y; y.z += yp.z; y.w += yp.w;
+  for (int p0 = 0; p0 < a.parts; p0 += 8) {
+    float4 yp[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      yp[j] = *reinterpret_cast<const float4*>(a.Y + min(p0 + j, a.parts - 1) * part_stride + at);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool in = p0 + j < a.parts;
+      y.x += in ? yp[j].x : 0.f; y.y += in ? yp[j].y : 0.f;
+      y.z += in ? yp[j].z : 0.f; y.w += in ? yp[j].w : 0.f;
+    }
   }
   float4 v = y;
   if (!a.first_slice) {
-    const float al = a.alpha[row];
-    const float4 o = *reinterpret_cast<const float4*>(a.acc + at);
     v.x = o.x * al + y.x; v.y = o.y * al + y.y; v.z = o.z * al + y.z; v.w = o.w * al + y.w;
   }
   if (!a.last_slice) {
     *reinterpret_cast<float4*>(a.acc + at) = v;
     return;
   }
-  const float s = a.run[a.n_rows + row];
-  const int64_t tgt = a.targets[row];
   if (tgt < 0) {  // an ignored row among the gradient rows: zero gradient, as for the others
     *reinterpret_cast<uint2*>(a.grad + at) = make_uint2(0u, 0u);
     return;
