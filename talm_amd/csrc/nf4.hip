@@ -206,6 +206,23 @@ struct TSegs {
   int n_seg;
 };
 
+// Persistent: workgroup b (on XCD b % 8) walks tiles first, first + stride, ... of its XCD's
+// contiguous range, and the next tile's codes and scale inputs are loaded while the current one
+// is dequantized, transposed through LDS and stored.
+struct TTile {
+  int g, r0, c0;  // projection, first weight row, first column
+};
+
+__device__ __forceinline__ TTile t_tile(const TSegs& s, int tile) {
+  TTile t;
+  t.g = 0;
+  while (t.g + 1 < s.n_seg && tile >= s.tile0[t.g + 1]) ++t.g;
+  const int local = tile - s.tile0[t.g];
+  t.r0 = local / s.col_tiles[t.g] * kTRows;
+  t.c0 = local % s.col_tiles[t.g] * kTCols;
+  return t;
+}
+
 template <bool kPow2>
 __global__ __launch_bounds__(kThreads) void nf4_group_t_kernel(
     const uint8_t* __restrict__ packed, const uint8_t* __restrict__ absmax8,
@@ -217,60 +234,93 @@ __global__ __launch_bounds__(kThreads) void nf4_group_t_kernel(
   __shared__ __attribute__((aligned(16))) uint32_t s_t[kTCols * kTStride];
   s_code[threadIdx.x] = code[threadIdx.x];
   if (threadIdx.x < 16) s_levels[threadIdx.x] = kNF4Levels[threadIdx.x];
-  // workgroup b runs on XCD b % 8: each XCD takes one contiguous range of tiles, so the
-  // neighbouring tiles of a row band, which read the same cache lines of codes, share an L2
+  // each XCD one contiguous range of tiles, so the neighbouring tiles of a row band, which read
+  // the same cache lines of codes, share an L2
   const uint32_t n_tiles = static_cast<uint32_t>(s.tile0[s.n_seg]);
-  const uint32_t xcd = blockIdx.x % 8, per = n_tiles / 8, extra = n_tiles % 8;
-  const int tile = static_cast<int>(xcd * per + min(xcd, extra) + blockIdx.x / 8);
-  int g = 0;
-  while (g + 1 < s.n_seg && tile >= s.tile0[g + 1]) ++g;
-  const int local = tile - s.tile0[g];
-  const int r0 = local / s.col_tiles[g] * kTRows, c0 = local % s.col_tiles[g] * kTCols;
-  const int rows = s.rows[g], cols = s.cols[g];
+  uint32_t first = blockIdx.x, stride = gridDim.x, end = n_tiles;
+  if (gridDim.x % 8 == 0) {
+    const uint32_t x = blockIdx.x % 8, q = n_tiles / 8, r = n_tiles % 8;
+    const uint32_t start = x * q + min(x, r);
+    first = start + blockIdx.x / 8;
+    stride = gridDim.x / 8;
+    end = start + q + (x < r ? 1u : 0u);
+  }
+  __syncthreads();  // the tables in LDS
+  if (first >= end) return;  // the whole workgroup; no barrier follows
   const int p = threadIdx.x >> 3, ci = threadIdx.x & 7;
-  const bool col_ok = c0 + 32 * ci < cols;
-  const int cc = col_ok ? c0 + 32 * ci : c0;  // a column chunk past the end reads the first
   u32x4 w[2];
   uint32_t a8[2];
   float a2[2], o2[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {  // both rows' loads before any use (rows past the end clamped)
-    const int r = min(r0 + 2 * p + h, rows - 1);
-    const int64_t e = s.start[g] + static_cast<int64_t>(r) * cols + cc;
-    w[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + e / 2));
-    const int64_t blk = e >> qblock_shift;
-    const int64_t blk2 = kPow2 ? (blk >> qblock2_shift)
-                               : static_cast<int64_t>(static_cast<uint32_t>(blk) / qblock2);
-    a8[h] = absmax8[blk];
-    a2[h] = absmax2[blk2];
-    o2[h] = offset2[blk2];
-  }
-  __syncthreads();  // the tables in LDS
-  float scale[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) scale[h] = block_scale(s_code[a8[h]], a2[h], o2[h]);
-  uint32_t* col = s_t + (32 * ci) * kTStride + (p ^ (4 * ci));
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {  // word j / 8, byte (j % 8) / 2, high nibble first
-    uint32_t pair = 0;
+  // thread (p, ci)'s codes of tile `tt`: columns 32 ci .. of rows 2 p and 2 p + 1 (rows past the
+  // end clamped, a column chunk past the end reads the tile's first)
+  auto load = [&](const TTile& tt, u32x4 (&lw)[2], uint32_t (&la8)[2], float (&la2)[2],
+                  float (&lo2)[2]) {
+    const int rows = s.rows[tt.g], cols = s.cols[tt.g];
+    const int cc = tt.c0 + 32 * ci < cols ? tt.c0 + 32 * ci : tt.c0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint32_t word = w[h][j >> 3];
-      const uint32_t byte = (word >> (8 * ((j & 7) >> 1))) & 0xffu;
-      const uint32_t nib = (j & 1) ? (byte & 15u) : (byte >> 4);
-      pair |= static_cast<uint32_t>(f2h(mul_f32(s_levels[nib], scale[h]))) << (16 * h);
+      const int r = min(tt.r0 + 2 * p + h, rows - 1);
+      const int64_t e = s.start[tt.g] + static_cast<int64_t>(r) * cols + cc;
+      lw[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(packed + e / 2));
+      const int64_t blk = e >> qblock_shift;
+      const int64_t blk2 = kPow2 ? (blk >> qblock2_shift)
+                                 : static_cast<int64_t>(static_cast<uint32_t>(blk) / qblock2);
+      la8[h] = absmax8[blk];
+      la2[h] = absmax2[blk2];
+      lo2[h] = offset2[blk2];
     }
-    col[j * kTStride] = pair;
-  }
-  __syncthreads();
-  uint16_t* dst = out + s.dst[g];
+  };
+  TTile cur = t_tile(s, static_cast<int>(first));
+  load(cur, w, a8, a2, o2);
+  for (uint32_t tile = first;;) {
+    const uint32_t next = tile + stride;
+    const bool more = next < end;
+    TTile nxt = cur;
+    u32x4 nw[2] = {w[0], w[1]};
+    uint32_t na8[2] = {0u, 0u};
+    float na2[2] = {0.f, 0.f}, no2[2] = {0.f, 0.f};
+    if (more) {
+      nxt = t_tile(s, static_cast<int>(next));
+      load(nxt, nw, na8, na2, no2);
+    }
+    float scale[2];
 #pragma unroll
-  for (int k = 0; k < kTCols * (kTRows / 8) / kThreads; ++k) {
-    const int id = k * kThreads + threadIdx.x;
-    const int c = id >> 3, oc = id & 7;  // W^T row c0 + c: rows r0 + 8 oc .. + 7 of W
-    if (c0 + c < cols && r0 + 8 * oc < rows)
-      *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(c0 + c) * s.ld[g] + r0 + 8 * oc) =
-          *reinterpret_cast<const uint4*>(s_t + c * kTStride + ((4 * oc) ^ (4 * (c >> 5))));
+    for (int h = 0; h < 2; ++h) scale[h] = block_scale(s_code[a8[h]], a2[h], o2[h]);
+    uint32_t* col = s_t + (32 * ci) * kTStride + (p ^ (4 * ci));
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {  // word j / 8, byte (j % 8) / 2, high nibble first
+      uint32_t pair = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t word = w[h][j >> 3];
+        const uint32_t byte = (word >> (8 * ((j & 7) >> 1))) & 0xffu;
+        const uint32_t nib = (j & 1) ? (byte & 15u) : (byte >> 4);
+        pair |= static_cast<uint32_t>(f2h(mul_f32(s_levels[nib], scale[h]))) << (16 * h);
+      }
+      col[j * kTStride] = pair;
+    }
+    __syncthreads();
+    const int rows = s.rows[cur.g], cols = s.cols[cur.g];
+    uint16_t* dst = out + s.dst[cur.g];
+#pragma unroll
+    for (int k = 0; k < kTCols * (kTRows / 8) / kThreads; ++k) {
+      const int id = k * kThreads + threadIdx.x;
+      const int c = id >> 3, oc = id & 7;  // W^T row c0 + c: rows r0 + 8 oc .. + 7 of W
+      if (cur.c0 + c < cols && cur.r0 + 8 * oc < rows)
+        *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(cur.c0 + c) * s.ld[cur.g] + cur.r0 + 8 * oc) =
+            *reinterpret_cast<const uint4*>(s_t + c * kTStride + ((4 * oc) ^ (4 * (c >> 5))));
+    }
+    if (!more) break;
+    __syncthreads();  // every thread has read the tile before the next one is staged
+    tile = next;
+    cur = nxt;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      w[h] = nw[h];
+      a8[h] = na8[h];
+      a2[h] = na2[h];
+      o2[h] = no2[h];
+    }
   }
 }
 
@@ -427,7 +477,12 @@ TALM_API int talm_nf4_group_dequant_t(const uint8_t* packed, const uint8_t* absm
   t.tile0[n_seg] = static_cast<int32_t>(tiles);
   const int q2shift = log2_exact(qblock2);
   auto kernel = q2shift >= 0 ? nf4_group_t_kernel<true> : nf4_group_t_kernel<false>;
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+  // persistent workgroups, four per CU (a multiple of 8 in all), or one per tile; measured on the
+  // step's transposed layer (q|k|v, o, down): 14.5 us with one workgroup per tile, 20.2 / 15.1 /
+  // 13.4 / 12.5 / 14.3 / 14.3 us with 1 / 2 / 3 / 4 / 6 / 8 per CU
+  int64_t wgs = std::min<int64_t>(tiles, 4 * static_cast<int64_t>(device_cus()));
+  if (wgs >= 8) wgs -= wgs % 8;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0,
                      as_stream(stream), packed, absmax8, code, absmax2, offset2, out, t, qshift,
                      static_cast<uint32_t>(qblock2), q2shift);
   return check_launch("nf4_group_dequant_t");
