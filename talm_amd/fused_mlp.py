@@ -5,7 +5,7 @@ gate and up are adjacent projections of the layer buffer, so [W_gate; W_up] is o
 view, and their outputs are the two halves of one [N, 2I] buffer:
   forward   gu = x [W_gate; W_up]^T            (one GEMM: gu[:, :I] = gate, gu[:, I:] = up)
             act = silu(gu[:, :I]) * gu[:, I:]  (talm_swiglu_fwd_rows)
-            y = act W_down^T
+            y = act W_down^T                   (hipBLASLt)
   backward  dact = dy W_down
             dgate, dup over gu's halves        (talm_swiglu_bwd_rows, in place)
             dx = [dgate | dup] [W_gate; W_up]  (one GEMM reducing over 2I)
@@ -39,8 +39,8 @@ from .state import DISABLED, fallback
 
 GATE, UP, DOWN = 4, 5, 6
 ENABLED = os.environ.get("SOLUTION_DISABLE_FUSED_MLP") != "1"
-# the long-reduction products (K >= SPLITK_MIN_K: the down projection and the input gradient on
-# the transposed gate|up weight) on this package's split-K MFMA GEMM instead of hipBLASLt
+# the long-reduction input gradient on the transposed gate|up weight (K >= SPLITK_MIN_K), when it
+# does not run on the NF4 codes, on this package's split-K MFMA GEMM instead of hipBLASLt
 SPLITK = os.environ.get("SOLUTION_DISABLE_SPLITK") != "1"
 SPLITK_MIN_K = 4096
 
@@ -90,9 +90,11 @@ class FusedMLP(torch.autograd.Function):
             act = torch.empty(n_tok, inter, dtype=torch.float16, device=x.device)
             torch.ops.talm.swiglu_fwd_rows(gu[:, :inter], gu[:, inter:], act)
             ctx.save_for_backward(gu)
+        # the down projection on hipBLASLt: at ~1300 tokens its one fp16 output beats the split-K
+        # GEMM's seven fp32 K-part partials (56 MB written and read back)
         w_down = group.weight(DOWN)
         y = torch.empty(n_tok, hidden, dtype=torch.float16, device=x.device)
-        _linear(act, w_down, y)
+        torch.ops.talm.gemm(act, w_down, None, 1, y)
         del act, w_down
         ctx.group, ctx.x_shape, ctx.save_up = group, x.shape, bool(save_up)
         return y.view(*x.shape[:-1], hidden)

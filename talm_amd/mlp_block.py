@@ -3,17 +3,17 @@
 After the attention's output h, the decoder layer computes (the residual adds folded into the
 norms as in solution/rmsnorm.py:335-404, the MLP as solution/fused_proj.py:241-287's FusedMLP):
     s1 = x + h;   n1 = post_attention_norm(s1)              add + norm        (talm_rmsnorm)
-    y  = down(silu(gate(n1)) * up(n1))                      the MLP           (hipBLASLt, SwiGLU,
-                                                                                split-K GEMM)
+    y  = down(silu(gate(n1)) * up(n1))                      the MLP           (hipBLASLt, SwiGLU)
     s2 = s1 + y;  n2 = next_norm(s2)                        add + the next layer's input norm
-`MlpBlock` runs them as one node, and the down projection's split-K reduction goes into the next
-norm's launch: the GEMM leaves its fp32 K-part partials (talm_gemm_splitk_partials) and
-talm_splitk_add_rmsnorm sums them, rounds y to fp16 and runs the add + norm on the row. In the
-backward the gate|up input gradient's partials (on the NF4 codes, talm_nf4_gemm_partials, or the
-split-K GEMM on the transposed weight) are summed inside the post-attention norm's backward
-(talm_splitk_rmsnorm_bwd). One launch fewer per layer each way, and the same bits as the
-separate nodes: the partials are summed in the same order and rounded to fp16 before the norm
-reads them, as the products' own reduction does.
+`MlpBlock` runs them as one node. The down projection runs on hipBLASLt with one fp16 output
+that the next norm's add reads: at the step's ~1300 tokens that measured 0.07 ms per step faster
+(same box, three runs each) than this package's split-K GEMM with its seven fp32 K-part partials
+(56 MB written and read back) summed inside the next norm's launch. In the backward the gate|up
+input gradient's partials (on the NF4 codes, talm_nf4_gemm_partials, or the split-K GEMM on the
+transposed weight) are summed inside the post-attention norm's backward
+(talm_splitk_rmsnorm_bwd): one launch fewer, and the same bits as the separate nodes (the
+partials are summed in the same order and rounded to fp16 before the norm reads them, as the
+product's own reduction does).
 
 Graceful degradation (state.py): a launch failing in the forward turns its component off and the
 layer runs the separate nodes; in the backward each failed launch falls back as those nodes do
@@ -127,20 +127,19 @@ class MlpBlock(torch.autograd.Function):
         act = torch.empty(n_tok, inter, **half)
         torch.ops.talm.swiglu_fwd_rows(gu[:, :inter], gu[:, inter:], act)
         # y = act W_down^T as K-part partials, summed inside the next norm's launch
-        stage[0] = "splitk"
+        # y = act W_down^T (fp16), then s2 = s1 + y, n2 = norm2(s2)
         w_down = group.weight(DOWN)
-        part = torch.empty(_ops.gemm_splitk_parts(n_tok, hidden, inter), n_tok, hidden,
-                           dtype=torch.float32, device=dev)
-        torch.ops.talm.gemm_splitk_partials(act, w_down, part)
+        y = torch.empty(n_tok, hidden, **half)
+        torch.ops.talm.gemm(act, w_down, None, 1, y)
         del act, w_down
         stage[0] = "addnorm"
         s2 = torch.empty_like(x2)
         n2 = torch.empty(n_tok, hidden, **half)
         xhat2 = torch.empty_like(n2)
         rstd2 = torch.empty(n_tok, dtype=torch.float32, device=dev)
-        torch.ops.talm.splitk_add_rmsnorm(part, s1, norm2.weight, norm2.variance_epsilon, s2, n2,
-                                          xhat2, rstd2)
-        del part
+        _rms.launch(s1, norm2.weight, n2, xhat2, rstd2, norm2.variance_epsilon, backward=0, p=y,
+                    q=s2)
+        del y
         ctx.save_for_backward(xhat1, rstd1, gu, xhat2, rstd2, norm1.weight, norm2.weight)
         ctx.group, ctx.shape, ctx.h_dtype = group, shape, h.dtype
         return s2.view(shape), n2.view(shape)
@@ -200,8 +199,9 @@ def mlp_block(layer, x, h, follower):
     """(s2, n2) of the layer's MLP half as one `MlpBlock` node when it applies: x the fp32
     residual stream, h the attention's fp16 output of x's shape, both norms on the kernel with
     fp16 outputs, rows of at most MAX_WIDTH columns, the MLP a packed layer group in FusedMLP's
-    default mode (`fused_mlp.mlp_plan`) whose down projection takes the split-K GEMM; else None
-    (the caller runs the separate nodes)."""
+    default mode (`fused_mlp.mlp_plan`) whose gate|up input gradient can be left as K-part
+    partials (the NF4 dequant-GEMM, or the split-K GEMM); else None (the caller runs the separate
+    nodes)."""
     if not ENABLED or "mlp_block" in DISABLED or "addnorm" in DISABLED or "splitk" in DISABLED \
             or not fused_mlp.SPLITK:
         return None
@@ -230,5 +230,4 @@ def mlp_block(layer, x, h, follower):
     RAN["mlp_block"] += 1
     RAN["fused_mlp"] += 1
     RAN["addnorm"] += 2
-    RAN["splitk"] += 1
     return out
