@@ -49,9 +49,9 @@ MEASURED_TRAFFIC = {
     "swiglu_fwd": 110.1e6,
     "swiglu_bwd": 183.5e6,
     "attn_fwd": 14.1e6,
-    "attn_bwd": 56.1e6,  # its three dispatches: dot, the dQ / dK / dV kernel, the reduction
+    "attn_bwd": 56.9e6,  # its three dispatches: dot, the dQ / dK / dV kernel, the reduction
     "nf4_gemm_gate_up_dx": 227.8e6,  # the dequant-GEMM and the reduction of its K parts
-    "head_ce_fwd_bwd": 4569e6,
+    "head_ce_fwd_bwd": 4329e6,
     "nf4_group_dequant_streaming": 118.3e6,
     "qkv_lora_fwd_n1312": 54.1e6 + 5.2e6,   # proj_ext + lora_down
     "qkv_lora_bwd_n1312": 57.9e6 + 12.1e6 + 5.2e6 + 13.6e6 + 4.8e6,  # + prep, lora_down, wgrad
