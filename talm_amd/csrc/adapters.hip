@@ -94,17 +94,31 @@ __global__ __launch_bounds__(kThreads) void lora_adamw_kernel(const int64_t* __r
   const float bc2_sqrt = sqrtf(1.f - powf(a.beta2, t));
   const float step_size = a.lr / bc1;
   const float inv_scale = a.grad_scale ? 1.f / *a.grad_scale : 1.f;
+  // the multipliers in registers before any store (the stores below may alias them as far as
+  // the compiler knows, which would reload them after each element)
+  const float gm0 = a.grad_mul ? a.grad_mul[0] : 1.f, gm1 = a.grad_mul ? a.grad_mul[1] : 1.f;
+  // every element's loads first (indices past the tensor clamped to its last element, their
+  // results unused), then the updates: one memory round trip instead of one per element
+  float w0[kPerThread], g0[kPerThread], m0[kPerThread], v0[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const int64_t i = min(i0 + j, x.n - 1);
+    w0[j] = x.w[i];
+    g0[j] = x.g[i];
+    m0[j] = x.m[i];
+    v0[j] = x.v[i];
+  }
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {
     const int64_t i = i0 + j;
     if (i >= x.n) break;
-    float p = x.w[i];
+    float p = w0[j];
     if (!skip) {
-      float g = a.grad_scale ? x.g[i] * inv_scale : x.g[i];
-      if (a.grad_mul) g = mul_f32(mul_f32(g, a.grad_mul[0]), a.grad_mul[1]);
+      float g = a.grad_scale ? g0[j] * inv_scale : g0[j];
+      if (a.grad_mul) g = mul_f32(mul_f32(g, gm0), gm1);
       p -= a.lr * a.weight_decay * p;
-      const float m = a.beta1 * x.m[i] + (1.f - a.beta1) * g;
-      const float v = a.beta2 * x.v[i] + (1.f - a.beta2) * g * g;
+      const float m = a.beta1 * m0[j] + (1.f - a.beta1) * g;
+      const float v = a.beta2 * v0[j] + (1.f - a.beta2) * g * g;
       p -= step_size * m / (sqrtf(v) / bc2_sqrt + a.eps);
       x.m[i] = m;
       x.v[i] = v;
