@@ -171,6 +171,29 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {  // v_cvt_pk_f
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){lo, hi}, half2_t));
 }
 
+// The epilogue's LDS row accesses (the rare target-logit path) as assembly. A plain LDS access
+// here makes the compiler wait for every direct-to-LDS load in flight first (it cannot tell
+// that the next tile's first ring step lands in the other slot, where the rows are not), which
+// would drain the prefetch the persistent loop keeps in flight under this epilogue.
+// lds_store16: 16 bytes into the row. lds_u16_now: one fp16 read back and waited for in the same
+// block; both blocks are ordered ("memory" clobbers), and a wavefront's LDS operations complete
+// in order, so the read sees the stores.
+__device__ __forceinline__ void lds_store16(uint16_t* p, uint4 v) {
+  const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) uint16_t*)(p)));
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t d = {v.x, v.y, v.z, v.w};
+  asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(d) : "memory");
+}
+
+__device__ __forceinline__ uint16_t lds_u16_now(const uint16_t* p) {
+  const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const uint16_t*)(p)));
+  uint32_t r;
+  asm volatile("ds_read_u16 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
+  return static_cast<uint16_t>(r);
+}
+
 __device__ __forceinline__ void tile_stats(const uint32_t (&zp)[32], float mx, uint16_t* zs,
                                            int lane, int tok, int64_t target, int c0, int valid,
                                            const LogitsArgs& a) {
@@ -180,7 +203,7 @@ __device__ __forceinline__ void tile_stats(const uint32_t (&zp)[32], float mx, u
   if (__builtin_amdgcn_ballot_w64(hit)) {
 #pragma unroll
     for (int k = 0; k < 32; k += 4)
-      *reinterpret_cast<uint4*>(zs + 2 * k) = make_uint4(zp[k], zp[k + 1], zp[k + 2], zp[k + 3]);
+      lds_store16(zs + 2 * k, make_uint4(zp[k], zp[k + 1], zp[k + 2], zp[k + 3]));
   }
   auto zh = [&](int k) {  // row stat_row(k, h) as fp16
     return __builtin_bit_cast(half2_t, zp[k >> 1])[k & 1];
@@ -243,7 +266,7 @@ __device__ __forceinline__ void tile_stats(const uint32_t (&zp)[32], float mx, u
   tu += other_half(tu);
   const float t = fmaf(tu, 1.f / kLog2e, m * s);
   if (tok < a.n_rows && h == 0) put_part(a, tok, c0, m, s, t, idx);
-  if (hit) a.ztarget[tok] = h2f(zs[kt]);
+  if (hit) a.ztarget[tok] = h2f(lds_u16_now(zs + kt));
 }
 
 // One ring step of the logits kernel: for each 16-deep slice ks, the wavefront's 4 A and 2 B
@@ -324,6 +347,18 @@ __global__ __launch_bounds__(S::kThreads, 1) void head_logits_kernel(LogitsArgs 
     const int tt = static_cast<int>(tile % a.n_ttiles), vt = static_cast<int>(tile / a.n_ttiles);
     const int c0 = vt * S::kBM + wm * S::kWaveM;  // the wavefront's first column in the group
     const int valid = a.group_cols - c0;         // of its rows, those that are vocabulary
+    // the targets of the lane's two tokens, loaded before the K loop (whose first wait covers
+    // them): loaded in the epilogue, after the next tile's first ring step was issued, their
+    // wait would also wait for that step's loads (vector-memory loads complete in order), and
+    // the epilogue would not overlap the prefetch. Held as int32 (-1: none; a label past 2^31
+    // is past any vocabulary and can hit no column either).
+    int tgt[S::kFragN];
+#pragma unroll
+    for (int j = 0; j < S::kFragN; ++j) {
+      const int tok = tt * S::kBN + wn * S::kWaveN + j * 32 + (lane & 31);
+      const int64_t t = tok < a.n_rows ? a.targets[tok] : -1;
+      tgt[j] = t < 0 || t > 0x7fffffff ? -1 : static_cast<int>(t);
+    }
     // Accumulators start at 0, or at -65504 (fp16's lowest finite value) for rows past the group's
     // end: their weight rows read as zeros, so their logits stay -65504 exactly, and e^{z - m}
     // is 0 for them whenever a vocabulary logit of the tile exceeds -65400 (a tile whose logits
@@ -365,6 +400,10 @@ __global__ __launch_bounds__(S::kThreads, 1) void head_logits_kernel(LogitsArgs 
         logits_step<S>(smem + i * S::kStageBytes, fo, acc);
       }
     }
+    // the targets count as written here, where nothing else is in flight: their wait (if the
+    // loop's own did not cover them) is placed here and not after the next step's loads below
+    asm volatile("" : "+v"(tgt[0]), "+v"(tgt[1]));
+    static_assert(S::kFragN == 2, "two token columns per wavefront");
     // every wavefront has read the last step: slot 0 takes the next tile's first step, slot 1
     // serves the epilogue's rare paths (a 128-byte row per lane)
     lds_barrier();
@@ -393,8 +432,7 @@ __global__ __launch_bounds__(S::kThreads, 1) void head_logits_kernel(LogitsArgs 
 #pragma unroll
       for (int j = 0; j < S::kFragN; ++j) {
         const int tok = tt * S::kBN + wn * S::kWaveN + j * 32 + (lane & 31);
-        const int64_t target = tok < a.n_rows ? a.targets[tok] : -1;
-        tile_stats(zp[j], mx[j], zs, lane, tok, target, c0, valid, a);
+        tile_stats(zp[j], mx[j], zs, lane, tok, tgt[j], c0, valid, a);
       }
     }
     if (next >= end) break;

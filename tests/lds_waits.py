@@ -77,6 +77,44 @@ def violations(body):
     return found
 
 
+_VM = re.compile(r"vmcnt\((\d+)\)")
+
+
+def drained_prefetches(body):
+    """[(instruction index, LDS read, the wait before it)] where a vmcnt wait forces a
+    direct-to-LDS load (`buffer_load_* ... lds`) issued since the last `s_barrier` to complete
+    before an LDS read of the same window.
+
+    A ring keeps the next tile's direct-to-LDS loads in flight while the wavefront reads the
+    current tile; the waits it needs sit before the barrier that publishes a tile. A compiler
+    that cannot tell the slot being filled from the slot being read inserts a vmcnt wait right
+    before the reads instead, which waits for the prefetch too (the ring then runs one memory
+    round trip per tile). Vector-memory operations complete in order (on gfx9 vmcnt counts loads
+    and stores), so `s_waitcnt vmcnt(N)` completes all but the newest N: it drains the window's
+    first prefetch when N is below the number of vector-memory operations issued since it.
+    Linear scan: a barrier ends the window, labels do not."""
+    found = []
+    since_dma = None  # vector-memory operations issued since the window's first prefetch
+    drained = None
+    for i, ins in enumerate(_instructions(body)):
+        op = ins.split(None, 1)[0]
+        if op == "s_barrier":
+            since_dma = drained = None
+        elif op.startswith(("buffer_", "global_", "flat_")) and not op.startswith(
+                ("buffer_wbl2", "buffer_inv", "buffer_gl")):
+            if since_dma is None and op.startswith("buffer_load") and ins.rstrip().endswith(" lds"):
+                since_dma = 0
+            if since_dma is not None:
+                since_dma += 1
+        elif op == "s_waitcnt" and since_dma is not None:
+            m = _VM.search(ins)
+            if m is not None and int(m.group(1)) < since_dma:
+                drained = ins
+        elif op.startswith(("ds_read", "ds_load")) and drained is not None:
+            found.append((i, ins, drained))
+    return found
+
+
 def kernel_bodies(asm_text, pattern):
     """{symbol: body} of the kernels whose mangled names match `pattern`."""
     bodies = re.findall(r"^(_Z\w+):[^\n]*\n(.*?)^\.Lfunc_end", asm_text, flags=re.S | re.M)
