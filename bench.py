@@ -139,9 +139,10 @@ def kernel_suite(args, only):
         # this build's own streaming probes (talm_amd/csrc/bench/stream.hip, libtalm_bench.so) on
         # the read / write mixes of the bandwidth-bound kernels, at their byte counts, cold
         # buffers rotated like theirs: 16-byte accesses, 64 items per wavefront and iteration,
-        # ordinary accesses, non-temporal ones, or non-temporal loads with ordinary stores,
-        # several grid sizes; the best of each mix is what this chip sustains for it (the
-        # ceiling the kernels are compared with)
+        # ordinary accesses, non-temporal ones, non-temporal loads with ordinary stores, or
+        # non-temporal loads with buffer stores carrying the nt and sc1 cache-policy bits, several
+        # grid sizes; the best of each mix is what this chip sustains for it (the ceiling the
+        # kernels are compared with)
         import ctypes
 
         from talm_amd import build as tbuild
@@ -171,7 +172,7 @@ def kernel_suite(args, only):
                      [torch.empty(items * 8 * wr, dtype=torch.int16, device=dev)
                       for _ in range(nw)]) for _ in range(k)]
             best, by_kind = None, {}
-            for nt in (0, 1, 2):
+            for nt in (0, 1, 2, 6):
                 for grid in (0, 1024, 2048, 4096):
                     def op(i, nt=nt, grid=grid):
                         srcs, dsts = sets[i]
@@ -186,14 +187,15 @@ def kernel_suite(args, only):
                     timing = timed(op, k)
                     if best is None or timing[0] < best[0][0]:
                         best = (timing, nt, grid)
-                    kind = ("plain", "non-temporal", "non-temporal loads")[nt]
+                    kind = {0: "plain", 1: "non-temporal", 2: "non-temporal loads",
+                            6: "non-temporal loads, nt sc1 buffer stores"}[nt]
                     if kind not in by_kind or timing[0] < by_kind[kind][0]:
                         by_kind[kind] = (timing[0], grid)
             (timing, nt, grid) = best
             fracs = ", ".join(f"{kind} {nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS:.3f} (grid "
                               f"{g or 'one-shot'})" for kind, (ms, g) in by_kind.items())
             record(name, timing, bytes_=nbytes, sets=k,
-                   config=f"{what}; best of 3 access kinds x 4 grids: {fracs}")
+                   config=f"{what}; best of 4 access kinds x 4 grids: {fracs}")
             del sets
 
     if want("nf4_group"):

@@ -30,13 +30,22 @@ __device__ __forceinline__ void st(u32x4* p, u32x4 v) {
   else *p = v;
 }
 
+// 16 bytes stored with a buffer store carrying the cache-policy bits `kAux` (gfx950: 1 sc0,
+// 2 nt, 16 sc1) at byte offset `off` of the range that starts at `base`.
+template <int kAux>
+__device__ __forceinline__ void st_aux(void* base, int64_t item, u32x4 v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<uint32_t>(item * 16), 0, kAux);
+}
+
 struct StreamArgs {
   const u32x4* src[3];
   u32x4* dst[3];
   int64_t n;  // items (16 bytes of each read stream)
 };
 
-template <int R, int W, int WR, bool kNtLoad, bool kNtStore>
+// kAux >= 0: the stores are buffer stores with those cache-policy bits (kNtStore unused)
+template <int R, int W, int WR, bool kNtLoad, bool kNtStore, int kAux = -1>
 __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
@@ -61,14 +70,27 @@ __global__ __launch_bounds__(256) void stream_kernel(StreamArgs a) {
       for (int w = 0; w < W; ++w)
 #pragma unroll
         for (int j = 0; j < WR; ++j)
-          st<kNtStore>(a.dst[w] + i0 * WR + j * 64 + lane, v[u] ^ static_cast<uint32_t>(j + w));
+          if constexpr (kAux >= 0)
+            st_aux<kAux>(a.dst[w], i0 * WR + j * 64 + lane, v[u] ^ static_cast<uint32_t>(j + w));
+          else
+            st<kNtStore>(a.dst[w] + i0 * WR + j * 64 + lane, v[u] ^ static_cast<uint32_t>(j + w));
     }
   }
 }
 
-// nt: 0 ordinary loads and stores, 1 both non-temporal, 2 non-temporal loads, ordinary stores
+// nt: 0 ordinary loads and stores, 1 both non-temporal, 2 non-temporal loads, ordinary stores;
+// 3 .. 10 non-temporal loads and buffer stores with the cache-policy bits kStoreAux[nt - 3]
+constexpr int kStoreAux[8] = {0, 2, 16, 18, 1, 3, 17, 19};
 template <int R, int W, int WR>
 void launch(const StreamArgs& a, int nt, int grid, hipStream_t s) {
+#define TALM_AUX(I)                                                                            \
+  if (nt == 3 + I) {                                                                           \
+    hipLaunchKernelGGL((stream_kernel<R, W, WR, true, false, kStoreAux[I]>), dim3(grid),       \
+                       dim3(256), 0, s, a);                                                    \
+    return;                                                                                    \
+  }
+  TALM_AUX(0) TALM_AUX(1) TALM_AUX(2) TALM_AUX(3) TALM_AUX(4) TALM_AUX(5) TALM_AUX(6) TALM_AUX(7)
+#undef TALM_AUX
   if (nt == 1)
     hipLaunchKernelGGL((stream_kernel<R, W, WR, true, true>), dim3(grid), dim3(256), 0, s, a);
   else if (nt == 2)
@@ -86,7 +108,9 @@ void launch(const StreamArgs& a, int nt, int grid, hipStream_t s) {
 TALM_BENCH_API int talm_bench_stream(int reads, int writes, int wr, int nt, const void* s0,
                                      const void* s1, const void* s2, void* d0, void* d1, void* d2,
                                      int64_t n_items, int grid, void* stream) {
-  if (n_items <= 0 || n_items % 128 || grid < 0 || nt < 0 || nt > 2) return 1;
+  if (n_items <= 0 || n_items % 128 || grid < 0 || nt < 0 || nt > 10) return 1;
+  for (int w = 0; nt >= 3 && w < writes; ++w)
+    if (n_items * 16 * wr > 0x7fffffff) return 1;  // buffer-store offsets are 32-bit
   StreamArgs a{};
   const void* src[3] = {s0, s1, s2};
   void* dst[3] = {d0, d1, d2};
