@@ -12,14 +12,18 @@ the original code outside the exact situation it was written for. Installed here
   q|k|v as one projection node with the rotary embedding in place (fused_proj.py);
 - padding removal with per-row attention (unpad.py) and the fused LM head + cross-entropy of
   the causal LM (fused_head.py, `patch_qwen2_causal_lm` below);
-- the measured hipBLASLt solution table of the decoder's GEMMs (gemm_tuning.py).
+- the measured hipBLASLt solution table of the decoder's GEMMs (gemm_tuning.py);
+- when TRL is installed, `SFTTrainer.compute_loss` on the fused head, its entropy / token /
+  accuracy metrics taken from the head's per-token outputs (sft_loss.py).
 
 Switches: SOLUTION_DISABLE_<PART>=1 leaves a part out (RMSNORM, ADDNORM, ROPE, SWIGLU_INPLACE,
 GROUP, LORA, FUSED_PROJ, FUSED_HEAD, UNPAD, FUSED_MLP, ATTN_BLOCK, GEMM_TABLE), as in the
 reference (solution/__init__.py:51-84).
 """
 
+import importlib.util
 import os
+import sys
 
 from .engaged import ON
 from .state import DISABLED, fallback, installing
@@ -39,6 +43,16 @@ def _in_chain(fn, marker):
 
 def _off(name):
     return os.environ.get(f"SOLUTION_DISABLE_{name}") == "1"
+
+
+def _have_trl():
+    """Whether `trl` is imported or importable (without importing it)."""
+    if "trl" in sys.modules:
+        return True
+    try:
+        return importlib.util.find_spec("trl") is not None
+    except (ImportError, ValueError):
+        return False
 
 
 # ------------------------------------------------------------------ the fused causal LM -----
@@ -336,6 +350,12 @@ def apply():
 
             patch_sdpa_rows()
             patch_qwen2_causal_lm()
+        if _have_trl():
+            with installing("fused_head"):
+                from .sft_loss import patch_sft_compute_loss
+
+                patch_sft_compute_loss()
+                ON.add("sft_loss")
     return sorted(ON)
 
 
@@ -368,6 +388,9 @@ def unapply():
     if getattr(forward, "_solution_link_norms", False):
         modeling_qwen2.Qwen2Model.forward = forward.__wrapped__
     modeling_qwen2.apply_rotary_pos_emb = _root(modeling_qwen2.apply_rotary_pos_emb)
+    trl = sys.modules.get("trl")
+    if trl is not None and hasattr(trl, "SFTTrainer"):
+        trl.SFTTrainer.compute_loss = _root(trl.SFTTrainer.compute_loss)
     ALL_ATTENTION_FUNCTIONS["sdpa"] = _root(ALL_ATTENTION_FUNCTIONS["sdpa"])
     rmsnorm.LAYER_FORWARDS.clear()
     qgroup.release()
