@@ -116,13 +116,16 @@ def dequant_state_torch(packed, state):
     dequantize_4bit as the reference's tests restate it (`_nf4_manual`, solution/test_fuzz.py:
     860-868) after the double-quant absmax is rebuilt (code[absmax8] * absmax2 + offset, each
     rounded in fp32: solution/qgroup.py:12-14). Returns fp16 [out, in], bit-identical to
-    `group_dequant` on the same bytes (tests/test_oracle.py)."""
+    `group_dequant` on the same bytes (tests/test_oracle.py). Runs on the device of `packed` (the
+    GPU tests' unpatched baselines use it there, so that their 4-bit layers do not run this
+    build's kernels)."""
     import torch
 
+    dev = packed.device
     codes = packed.reshape(-1).to(torch.int64)
-    levels = torch.tensor(NF4_LEVELS, dtype=torch.float32)
+    levels = torch.tensor(NF4_LEVELS, dtype=torch.float32, device=dev)
     inner = state.state2
-    blk2 = torch.arange(state.absmax.numel()) // inner.blocksize
+    blk2 = torch.arange(state.absmax.numel(), device=dev) // inner.blocksize
     absmax = inner.code[state.absmax.to(torch.int64)] * inner.absmax[blk2] + state.offset
     vals = torch.stack((levels[codes >> 4], levels[codes & 15]), 1).reshape(-1)
     vals = vals * absmax.repeat_interleave(state.blocksize)[:vals.numel()]

@@ -22,6 +22,8 @@ runs are therefore also compared where the reference's whole-solution test compa
   solution/test_parity.py:962-966);
 - each adapter's update after all the steps (final minus initial weights) within 1e-1 relative
   L2 of the unpatched run's update.
+The unpatched run uses no kernel of this package: its 4-bit layers dequantize with the oracle's
+PyTorch restatement of bitsandbytes' dequantize_4bit.
 """
 
 import pytest
@@ -91,9 +93,20 @@ def _curve(mode, steps):
 
 @pytest.fixture(scope="module")
 def eager_run():
+    """The unpatched run, its 4-bit layers dequantizing with the oracle's PyTorch restatement of
+    bitsandbytes' dequantize_4bit (bit-identical to the C oracle, tests/test_oracle.py) instead
+    of this build's per-projection kernel: no HIP kernel of the package takes part in it."""
+    from oracle import nf4 as nf4_oracle
+    from talm_amd import nf4_linear
+
     print("[case] config 5 full size: unpatched eager, 64 steps", flush=True)
-    run = _curve("eager", STEPS)
-    assert run[1].get("fused_head", 0) == 0
+    kernel = nf4_linear.dequantize_4bit
+    nf4_linear.dequantize_4bit = nf4_oracle.dequant_state_torch
+    try:
+        run = _curve("eager", STEPS)
+    finally:
+        nf4_linear.dequantize_4bit = kernel
+    assert run[1].get("fused_head", 0) == 0 and run[1].get("nf4_dequant", 0) == 0
     return run
 
 

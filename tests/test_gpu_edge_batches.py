@@ -130,7 +130,14 @@ def test_patched_forward_matches_unpatched_on_edge_batches(monkeypatch, case, pa
     model = _model()
 
     patches.unapply()
-    ref, ref_grads = _step(model, ids, mask, labels, num_items)
+    # the unpatched baseline's 4-bit layers on the oracle's PyTorch dequantization (no kernel of
+    # this package in the reference run)
+    from oracle import nf4 as nf4_oracle
+    from talm_amd import nf4_linear
+
+    with monkeypatch.context() as m:
+        m.setattr(nf4_linear, "dequantize_4bit", nf4_oracle.dequant_state_torch)
+        ref, ref_grads = _step(model, ids, mask, labels, num_items)
     ref_loss, ref_entropy, ref_correct, n_labelled = _per_token(ref.logits.detach(), labels)
 
     monkeypatch.setenv("SOLUTION_DISABLE_GEMM_TABLE", "1")
