@@ -389,7 +389,8 @@ def unapply():
         modeling_qwen2.Qwen2Model.forward = forward.__wrapped__
     modeling_qwen2.apply_rotary_pos_emb = _root(modeling_qwen2.apply_rotary_pos_emb)
     trl = sys.modules.get("trl")
-    if trl is not None and hasattr(trl, "SFTTrainer"):
+    if trl is not None and hasattr(trl, "SFTTrainer") \
+            and _in_chain(trl.SFTTrainer.compute_loss, "_talm_sft_loss"):
         trl.SFTTrainer.compute_loss = _root(trl.SFTTrainer.compute_loss)
     ALL_ATTENTION_FUNCTIONS["sdpa"] = _root(ALL_ATTENTION_FUNCTIONS["sdpa"])
     rmsnorm.LAYER_FORWARDS.clear()
